@@ -1,0 +1,206 @@
+/*
+ * smegemm_gpu.h -- C ABI of the MI355X (gfx950) quantized-weight matmul
+ * library. It replaces the reference crate's FFI for this path
+ * (src/ffi.rs <-> csrc/sme_gemm_api.h) and the kernel dispatch in
+ * src/kernels/q4/matmul.rs and src/kernels/lowbit/matmul.rs.
+ *
+ * Conventions (the reference's, csrc/sme_gemm_api.h and ARCHITECTURE.md):
+ *   - f16 / bf16 values travel as uint16_t bit patterns.
+ *   - Every entry point returns int: 0 = done; non-zero = failed with the
+ *     output untouched (the reference's rc contract, src/kernels/q4/matmul.rs:85-90),
+ *     so the caller may fall back. Codes below say why.
+ *   - `ep == NULL` (or n_nodes == 0) means no epilogue. A trailing activation
+ *     is the last node with op EP_OP_ACT, as resolve_nodes builds it
+ *     (src/exec/scalar.rs:28-53).
+ *   - Host-pointer entry points (gemm_gpu_*) are synchronous, like the
+ *     reference: dst is fully written on return. Epilogue operand pointers
+ *     are host pointers there.
+ *   - Device-pointer entry points (smg_*_dev) are asynchronous on `stream`
+ *     (a hipStream_t, NULL = the null stream); lhs, dst and every epilogue
+ *     operand pointer are device pointers.
+ *   - Safe for concurrent callers on different host threads: each thread gets
+ *     its own stream and staging buffers for the host-pointer entry points.
+ *
+ * Weights live on the device behind an opaque handle (the "prepack"): the
+ * reference keeps them in Q4Weights / Q2Weights / Q1Weights / Packed<f16>,
+ * and a Rust binding keeps the handle there.
+ */
+#ifndef SMEGEMM_GPU_H
+#define SMEGEMM_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- return codes --------------------------------------------------------- */
+#define SMG_OK 0
+#define SMG_EINVAL -1  /* bad argument (e.g. block not a power of two); the reference's -1 */
+#define SMG_ENOMEM -2  /* device allocation failed */
+#define SMG_EHIP -3    /* a HIP runtime call or launch failed */
+#define SMG_ENODEV -4  /* no usable gfx950 device */
+#define SMG_EKIND -5   /* weight handle of the wrong kind for this entry point */
+
+/* ---- epilogue ABI: byte-identical to csrc/epilogue.h:136-236 -------------- */
+enum ep_act {
+    EP_ACT_NONE = 0, EP_ACT_RELU = 1, EP_ACT_GELU = 2, EP_ACT_SILU = 3, EP_ACT_TANH = 4,
+    EP_ACT_SIGMOID = 5, EP_ACT_LEAKY_RELU = 6, EP_ACT_RELU6 = 7, EP_ACT_HARDSIGMOID = 8,
+    EP_ACT_HARDSWISH = 9, EP_ACT_ABS = 10, EP_ACT_NEG = 11, EP_ACT_SQUARE = 12,
+    EP_ACT_SIGN = 13, EP_ACT_SQRT = 14, EP_ACT_SOFTSIGN = 15, EP_ACT_RECIP = 16,
+    EP_ACT_RSQRT = 17, EP_ACT_EXP = 18, EP_ACT_LOG = 19, EP_ACT_ELU = 20, EP_ACT_SELU = 21,
+    EP_ACT_SOFTPLUS = 22, EP_ACT_MISH = 23, EP_ACT_GELU_EXACT = 24
+};
+
+enum ep_op {
+    EP_OP_ADD_SCALAR = 0, EP_OP_MUL_SCALAR = 1, EP_OP_ADD_ROW = 2, EP_OP_MUL_ROW = 3,
+    EP_OP_ADD_COL = 4, EP_OP_MUL_COL = 5, EP_OP_ADD_TENSOR = 6, EP_OP_MUL_TENSOR = 7,
+    EP_OP_ACT = 8, EP_OP_MAX_SCALAR = 9, EP_OP_MIN_SCALAR = 10, EP_OP_SUB_SCALAR = 11,
+    EP_OP_SUB_ROW = 12, EP_OP_SUB_COL = 13, EP_OP_SUB_TENSOR = 14, EP_OP_DIV_SCALAR = 15,
+    EP_OP_DIV_ROW = 16, EP_OP_DIV_COL = 17, EP_OP_DIV_TENSOR = 18, EP_OP_MAX_ROW = 19,
+    EP_OP_MAX_COL = 20, EP_OP_MAX_TENSOR = 21, EP_OP_MIN_ROW = 22, EP_OP_MIN_COL = 23,
+    EP_OP_MIN_TENSOR = 24
+};
+
+/* One op-graph node (csrc/epilogue.h:214-221; Rust mirror src/epilogue/mod.rs:150). */
+typedef struct {
+    uint32_t op;     /* enum ep_op */
+    uint32_t aux;    /* enum ep_act for EP_OP_ACT */
+    float scalar;    /* *_SCALAR operand; alpha of LEAKY_RELU / ELU */
+    const void *ptr; /* ROW (m) / COL (n) / TENSOR (rows at stride ld) operand, f16 or bf16 */
+    size_t ld;       /* TENSOR row stride in elements; 0 = n */
+} EpNode;
+
+/* csrc/epilogue.h:233-236 */
+typedef struct {
+    uint32_t n_nodes;
+    const EpNode *nodes;
+} ep_desc16;
+
+/* Nodes one call carries to the device (by value, in the kernel arguments).
+ * Longer graphs return SMG_EINVAL. */
+#define SMG_MAX_EP_NODES 16
+
+/* ---- weight handles ------------------------------------------------------- */
+typedef struct smg_weights smg_weights;
+
+/* Q4: replaces Q4Weights::new / with_params (src/kernels/q4/weights.rs:50-123).
+ * Row-major input: weight idx = d*n + j is nibble idx%2 (low first) of byte
+ * idx/2, code = nib < 8 ? nib : nib - 16; scales[j*ceil(k/block) + d/block]
+ * (f16); mins the same shape or NULL (Q4Form::Scale). block: a power of two. */
+int smg_q4_create(const uint8_t *quants, const uint16_t *scales, const uint16_t *mins, size_t n,
+                  size_t k, size_t block, smg_weights **out);
+
+/* Q4 from the reference's band-major resident arrays -- exactly what src/ffi.rs
+ * passes to gemm_sme_f16f16_q4 (nibbles/scales/mins of Q4Weights,
+ * weights.rs:89-113): 128-column bands, 64 bytes per depth, scales [band][blk][128]. */
+int smg_q4_create_band(const uint8_t *nibbles, const uint16_t *scales, const uint16_t *mins,
+                       size_t n, size_t k, size_t block, smg_weights **out);
+
+/* Q2: replaces Q2Weights::new (src/kernels/lowbit/q2.rs:53-86). Row-major codes,
+ * weight idx = d*n + j at bits 2*(idx%4) of byte idx/4; scales[j*nbk + d/block];
+ * codebook: the 4 int8 values (Q2Params, lowbit/mod.rs:38-94).
+ * block: power of two in [16, 65536]. */
+int smg_q2_create(const uint8_t *codes, const uint16_t *scales, const int8_t *codebook,
+                  size_t n, size_t k, size_t block, smg_weights **out);
+/* Q2 from the band-major arrays src/ffi.rs passes (q2.rs:12-20,148-161). */
+int smg_q2_create_band(const uint8_t *codes, const uint16_t *scales, const int8_t *codebook,
+                       size_t n, size_t k, size_t block, smg_weights **out);
+
+/* Q1: replaces Q1Weights::new (src/kernels/lowbit/q1.rs:47-107). layout 0 =
+ * WeightLayout::OutIn (idx = j*k + d), 1 = InOut (idx = d*n + j); bit idx%8 of
+ * byte idx/8, set = +scale. */
+int smg_q1_create(const uint8_t *signs, const uint16_t *scales, int layout, size_t n, size_t k,
+                  size_t block, smg_weights **out);
+/* Q1 from the band-major arrays src/ffi.rs passes (q1.rs:186-201). */
+int smg_q1_create_band(const uint8_t *signs, const uint16_t *scales, size_t n, size_t k,
+                       size_t block, smg_weights **out);
+
+/* Dense Packed<f16> / Packed<bf16>: replaces prepack_f16 / prepack_bf16
+ * (src/kernels/f16.rs:212; bf16.rs:240) and gemm_sme_f16f16_packb
+ * (csrc/sme_gemm_api.h:94). B[l][j] = rhs[l*rhs_rs + j*rhs_cs] (k x n). */
+int smg_f16_prepack(const uint16_t *rhs, size_t n, size_t k, long rhs_rs, long rhs_cs,
+                    smg_weights **out);
+int smg_bf16_prepack(const uint16_t *rhs, size_t n, size_t k, long rhs_rs, long rhs_cs,
+                     smg_weights **out);
+
+/* Eager dequant of a Q4 handle to a dense handle on the device: replaces
+ * dequant_q4 / dequant_q4_with (f16: one RNE rounding of scale*code+min) and
+ * dequant_q4_bf16 / _with (bf16 through f32), src/kernels/q4/mod.rs:145-257. */
+int smg_q4_dequant(const smg_weights *q4, int to_bf16, smg_weights **out);
+
+/* A second device copy of a handle's weights (device-to-device; no host
+ * repack). Used to rotate benchmark weights past the 256 MB MALL. */
+int smg_weights_clone(const smg_weights *w, smg_weights **out);
+
+void smg_weights_destroy(smg_weights *w);
+/* n, k, block (0 for dense) and device bytes of a handle. */
+int smg_weights_info(const smg_weights *w, size_t *n, size_t *k, size_t *block, size_t *bytes);
+
+/* ---- host-pointer drop-ins (synchronous) ---------------------------------- */
+
+/* matmul_q4 / matmul_q4_ep: C = ep(A @ dequant(B)); replaces gemm_sme_f16f16_q4
+ * (csrc/sme_gemm_api.h:97-99). lhs m x k f16 row-major, dst m x n f16. */
+int gemm_gpu_f16f16_q4(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                       const ep_desc16 *ep);
+/* matmul_q4_bf16 / _ep; replaces gemm_sme_b16b16_q4 (csrc/sme_gemm_api.h:66-69). */
+int gemm_gpu_b16b16_q4(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                       const ep_desc16 *ep);
+/* matmul_q2 / _ep and matmul_q1 / _ep (int8 path, bit-exact with
+ * src/kernels/lowbit/matmul.rs:376-398); replace gemm_sme_f16_q2 / _q1
+ * (csrc/sme_gemm_api.h:208-213). The handle's kind selects Q2 or Q1. */
+int gemm_gpu_f16_q2(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                    const ep_desc16 *ep);
+int gemm_gpu_f16_q1(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                    const ep_desc16 *ep);
+/* matmul_q2_mopa / matmul_q1_mopa (+_ep): f16 weights scale*value rounded once,
+ * f16 activations, f32 accumulation; replace gemm_sme_f16f16_q2 / _q1
+ * (csrc/sme_gemm_api.h:110-115). */
+int gemm_gpu_f16f16_q2(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                       const ep_desc16 *ep);
+int gemm_gpu_f16f16_q1(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                       const ep_desc16 *ep);
+/* The dense packed GEMM behind Gemm::new(&a, &packed, m)...run(&mut c) and
+ * matmul_f16_packed: replaces gemm_sme_f16f16_run_packed
+ * (csrc/sme_gemm_api.h:120-123). C[i,j] at dst[i*dst_rs + j*dst_cs];
+ * A[i,l] at lhs[i*lhs_rs + l*lhs_cs]; dst = ep(beta * A@B) with read_dst == 0
+ * (the only form the reference's callers use, src/exec/macros.rs:131-150);
+ * alpha_bits is ignored under read_dst == 0. */
+int gemm_gpu_f16f16_run_packed(size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs,
+                               long dst_rs, int read_dst, const uint16_t *lhs, long lhs_cs,
+                               long lhs_rs, const smg_weights *b_pack, uint16_t alpha_bits,
+                               uint16_t beta_bits, const ep_desc16 *ep);
+int gemm_gpu_b16b16_run_packed(size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs,
+                               long dst_rs, int read_dst, const uint16_t *lhs, long lhs_cs,
+                               long lhs_rs, const smg_weights *b_pack, uint16_t alpha_bits,
+                               uint16_t beta_bits, const ep_desc16 *ep);
+/* Whether an m-row Q4 call runs the GEMV kernel (replaces
+ * gemm_sme_f16f16_q4_single, csrc/sme_gemm_api.h:107). */
+int gemm_gpu_f16f16_q4_single(size_t m, size_t n, size_t k);
+
+/* ---- device-pointer entry points (asynchronous on `stream`) --------------- */
+int smg_q4_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                      const ep_desc16 *ep, int bf16, void *stream);
+int smg_lowbit_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                          const ep_desc16 *ep, void *stream);
+int smg_lowbit_mopa_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                        const ep_desc16 *ep, void *stream);
+int smg_packed_matmul_dev(size_t m, const smg_weights *b_pack, uint16_t *dst, long dst_cs,
+                          long dst_rs, const uint16_t *lhs, long lhs_cs, long lhs_rs,
+                          uint16_t beta_bits, const ep_desc16 *ep, int bf16, void *stream);
+
+/* ---- runtime --------------------------------------------------------------- */
+/* 1 when a gfx950 device is present and this library's kernels load on it. */
+int smg_available(void);
+/* Text of the last error on the calling thread ("" if none). */
+const char *smg_last_error(void);
+/* Rows at or below which Q4 runs the GEMV kernel (the reference's
+ * Q4_GEMV_MAXR = 7 cut, csrc/gemm_f16f16_q4.h:129, moved to the GPU's own
+ * crossover). */
+size_t smg_q4_gemv_max_rows(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SMEGEMM_GPU_H */

@@ -1,0 +1,618 @@
+/*
+ * CPU oracle for the quantized-weight matmul path of electricapp/sme-gemm.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file restates, in plain C, the reference
+ * crate's portable (non-SME) Rust path, which is what every entry point runs
+ * off Apple silicon. Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it, and only as the checker. The product path
+ * (sme-gemm_amd/) never links or calls it.
+ *
+ * Build: `make -C oracle` (gcc, -ffp-contract=off: the Rust reference never
+ * contracts a*b+c into an fma unless it writes mul_add).
+ *
+ * Pinning (how each part is checked against something other than itself):
+ *   - f16/bf16 conversions: exhaustive / sampled comparison against numpy's
+ *     float16 (direct f32->f16 and f64->f16 RNE) and torch's bfloat16 RNE
+ *     (tests/test_oracle_pins.py).
+ *   - Q4 dequant: closed form over every nibble x a sweep of scales, and the
+ *     reference's own round-trip invariants (weights.rs:315,359,426).
+ *   - gemm_f16/bf16: brute force against an independent numpy f32 sequential
+ *     accumulation, plus closed forms (all-ones A -> column sums, k=0 -> 0).
+ *   - epilogue: per-op closed forms against numpy/math in f64.
+ *   - lowbit quantize_row/reference: numpy restatement on small shapes, the
+ *     f64 activation-rounding bound of tests/correctness/q2.rs:39-77, grid
+ *     recovery (q2.rs:228, q1.rs:279), and independence from m.
+ */
+#include <math.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* IEEE binary16 / bfloat16 conversions (the `half` 2.7.1 crate semantics).  */
+/* ------------------------------------------------------------------------ */
+
+static inline uint32_t f32_bits(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
+static inline float bits_f32(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
+static inline uint64_t f64_bits(double x) { uint64_t u; memcpy(&u, &x, 8); return u; }
+
+/* half::f16::to_f32 -- exact widening. */
+float or_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1f;
+    uint32_t man = h & 0x3ffu;
+    if (exp == 0x1f) {
+        /* inf / NaN: payload moves to the top of the f32 mantissa */
+        return bits_f32(sign | 0x7f800000u | (man << 13));
+    }
+    if (exp == 0) {
+        if (man == 0) return bits_f32(sign);
+        /* subnormal: value = man * 2^-24, exact in f32 */
+        float v = (float)man * 0x1p-24f;
+        return sign ? -v : v;
+    }
+    return bits_f32(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+/* Round a finite positive value given as an unbounded binary fraction
+ * (mantissa m with implicit exponent e: value = m * 2^e, m < 2^63) to f16
+ * bits with round-to-nearest-even. Shared by the f32 and f64 paths so both
+ * are a single rounding from the exact input. */
+static uint16_t round_to_f16(uint64_t m, int e) {
+    /* normalise m to have its top bit at position 62 */
+    if (m == 0) return 0;
+    int top = 63 - __builtin_clzll(m);
+    /* value = m * 2^e, leading bit weight 2^(top+e) */
+    int lead = top + e; /* unbiased exponent of the value */
+    if (lead > 15) return 0x7c00; /* overflow -> inf (RNE rounds >= 65520 up too) */
+    /* target quantum: normals have 10 fraction bits -> quantum 2^(lead-10);
+     * subnormals have fixed quantum 2^-24 */
+    int q = lead - 10;
+    if (q < -24) q = -24;
+    /* number of bits of m below the quantum */
+    int shift = q - e;
+    uint64_t r;
+    if (shift <= 0) {
+        r = m << (-shift); /* exact */
+    } else if (shift >= 64) {
+        r = 0; /* value < 2^-25 * ... -> rounds to 0 unless above half quantum */
+        /* value < quantum/2 ? m*2^e < 2^(q-1) holds when shift >= 64 since m < 2^63 */
+    } else {
+        uint64_t rem = m & ((1ull << shift) - 1);
+        uint64_t half = 1ull << (shift - 1);
+        r = m >> shift;
+        if (rem > half || (rem == half && (r & 1))) r++;
+    }
+    /* r is the count of quanta; rebuild the f16 */
+    if (q == -24) {
+        /* subnormal range (or rounded up into the first normal binade) */
+        return (uint16_t)r; /* r <= 0x400 -> 0x400 is the smallest normal: bits match */
+    }
+    /* normal: r in [2^10, 2^11] */
+    int biased = q + 10 + 15;
+    if (r == (1ull << 11)) { r >>= 1; biased++; }
+    if (biased >= 31) return 0x7c00;
+    return (uint16_t)((biased << 10) | (r & 0x3ff));
+}
+
+/* half::f16::from_f32 -- RNE; NaN keeps its top payload bits and is quieted. */
+uint16_t or_f32_to_f16(float x) {
+    uint32_t u = f32_bits(x);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    uint32_t exp = (u >> 23) & 0xff;
+    uint32_t man = u & 0x7fffffu;
+    if (exp == 0xff) {
+        if (man == 0) return sign | 0x7c00;
+        return sign | 0x7e00 | (uint16_t)(man >> 13);
+    }
+    uint64_t m;
+    int e;
+    if (exp == 0) { m = man; e = -149; }
+    else { m = man | 0x800000u; e = (int)exp - 150; }
+    return sign | round_to_f16(m, e);
+}
+
+/* half::f16::from_f64 -- one direct RNE rounding (not via f32). */
+uint16_t or_f64_to_f16(double x) {
+    uint64_t u = f64_bits(x);
+    uint16_t sign = (uint16_t)((u >> 48) & 0x8000u);
+    uint32_t exp = (uint32_t)((u >> 52) & 0x7ff);
+    uint64_t man = u & 0xfffffffffffffull;
+    if (exp == 0x7ff) {
+        if (man == 0) return sign | 0x7c00;
+        return sign | 0x7e00 | (uint16_t)(man >> 42);
+    }
+    uint64_t m;
+    int e;
+    if (exp == 0) { m = man; e = -1074; }
+    else { m = man | (1ull << 52); e = (int)exp - 1075; }
+    return sign | round_to_f16(m, e);
+}
+
+/* half::bf16::to_f32 -- exact. */
+float or_bf16_to_f32(uint16_t h) { return bits_f32((uint32_t)h << 16); }
+
+/* half::bf16::from_f32 -- RNE on the top 16 bits; NaN quieted. */
+uint16_t or_f32_to_bf16(float x) {
+    uint32_t u = f32_bits(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    uint32_t round_bit = 0x8000u;
+    if ((u & round_bit) != 0 && (u & (3u * round_bit - 1)) != 0)
+        return (uint16_t)((u >> 16) + 1);
+    return (uint16_t)(u >> 16);
+}
+
+/* Rust `f64 as f32`: RNE. C's (float) cast on x86-64 SSE is RNE. */
+static inline float f64_to_f32(double x) { return (float)x; }
+
+/* ------------------------------------------------------------------------ */
+/* Q4 row-major dequant: src/kernels/q4/mod.rs:193-224 (q4_rowmajor),        */
+/* weights.rs:232-259 (dequant_rows). w = f64(scale)*code (+ f64(min)),      */
+/* exact in f64, rounded once.                                               */
+/* ------------------------------------------------------------------------ */
+
+static inline int q4_code(const uint8_t *quants, size_t idx) {
+    uint8_t byte = quants[idx / 2];
+    int nib = (idx % 2 == 0) ? (byte & 0x0f) : (byte >> 4);
+    return nib - (nib < 8 ? 0 : 16); /* mod.rs:213-214 two's complement */
+}
+
+/* out: k x n row-major f16 bits. mins may be NULL (Q4Form::Scale). */
+void or_q4_dequant_f16(const uint8_t *quants, const uint16_t *scales, const uint16_t *mins,
+                       size_t n, size_t k, size_t block, uint16_t *out) {
+    size_t nbk = (k + block - 1) / block;
+    for (size_t d = 0; d < k; d++) {
+        for (size_t j = 0; j < n; j++) {
+            size_t idx = d * n + j;
+            size_t bi = j * nbk + d / block;
+            double w = (double)or_f16_to_f32(scales[bi]) * (double)q4_code(quants, idx);
+            if (mins) w += (double)or_f16_to_f32(mins[bi]);
+            out[idx] = or_f64_to_f16(w);
+        }
+    }
+}
+
+/* bf16 twin: mod.rs:250-256 / weights.rs:198-201 -- `bf16::from_f32(w as f32)`,
+ * i.e. f64 -> f32 (RNE) -> bf16 (RNE). */
+void or_q4_dequant_bf16(const uint8_t *quants, const uint16_t *scales, const uint16_t *mins,
+                        size_t n, size_t k, size_t block, uint16_t *out) {
+    size_t nbk = (k + block - 1) / block;
+    for (size_t d = 0; d < k; d++) {
+        for (size_t j = 0; j < n; j++) {
+            size_t idx = d * n + j;
+            size_t bi = j * nbk + d / block;
+            double w = (double)or_f16_to_f32(scales[bi]) * (double)q4_code(quants, idx);
+            if (mins) w += (double)or_f16_to_f32(mins[bi]);
+            out[idx] = or_f32_to_bf16(f64_to_f32(w));
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Dense half-precision reference GEMM: src/reference.rs:349-387 (f16) and   */
+/* :308-346 (bf16). ikj, f32 accumulator per row, K order, no contraction    */
+/* (each f16 x f16 / bf16 x bf16 product is exact in f32). Output            */
+/* c = to16(0 + beta*acc) (alpha = 0 as src/exec/macros.rs:188-203 passes).  */
+/* col_major selects C[i,j] at c[i + j*m] (Gemm::col_major_output).          */
+/* ------------------------------------------------------------------------ */
+
+static void gemm16(int is_bf16, size_t m, size_t n, size_t k, uint16_t *c, const uint16_t *a,
+                   const uint16_t *b, uint16_t beta_bits, int col_major, float *acc) {
+    float (*to32)(uint16_t) = is_bf16 ? or_bf16_to_f32 : or_f16_to_f32;
+    uint16_t (*to16)(float) = is_bf16 ? or_f32_to_bf16 : or_f32_to_f16;
+    float beta = to32(beta_bits);
+    for (size_t i = 0; i < m; i++) {
+        for (size_t j = 0; j < n; j++) acc[j] = 0.0f;
+        for (size_t l = 0; l < k; l++) {
+            float av = to32(a[i * k + l]);
+            const uint16_t *brow = b + l * n;
+            for (size_t j = 0; j < n; j++) {
+                float p = av * to32(brow[j]);
+                acc[j] = acc[j] + p;
+            }
+        }
+        for (size_t j = 0; j < n; j++) {
+            float v = 0.0f + beta * acc[j];
+            size_t idx = col_major ? (i + j * m) : (i * n + j);
+            c[idx] = to16(v);
+        }
+    }
+}
+
+/* acc: scratch of n floats */
+void or_gemm_f16(size_t m, size_t n, size_t k, uint16_t *c, const uint16_t *a, const uint16_t *b,
+                 uint16_t beta_bits, int col_major, float *acc) {
+    gemm16(0, m, n, k, c, a, b, beta_bits, col_major, acc);
+}
+void or_gemm_bf16(size_t m, size_t n, size_t k, uint16_t *c, const uint16_t *a, const uint16_t *b,
+                  uint16_t beta_bits, int col_major, float *acc) {
+    gemm16(1, m, n, k, c, a, b, beta_bits, col_major, acc);
+}
+
+/* Column range [j0, j1) of the same GEMM, for the threaded CPU baseline
+ * (identical per-output arithmetic: each output only depends on its column). */
+void or_gemm_f16_cols(size_t m, size_t n, size_t k, uint16_t *c, const uint16_t *a,
+                      const uint16_t *b, size_t j0, size_t j1, float *acc) {
+    for (size_t i = 0; i < m; i++) {
+        for (size_t j = j0; j < j1; j++) acc[j - j0] = 0.0f;
+        for (size_t l = 0; l < k; l++) {
+            float av = or_f16_to_f32(a[i * k + l]);
+            const uint16_t *brow = b + l * n;
+            for (size_t j = j0; j < j1; j++) acc[j - j0] = acc[j - j0] + av * or_f16_to_f32(brow[j]);
+        }
+        for (size_t j = j0; j < j1; j++) c[i * n + j] = or_f32_to_f16(0.0f + 1.0f * acc[j - j0]);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Epilogue: src/exec/scalar.rs:58-140 (ep_apply_cell / apply_ep_scalar) and */
+/* src/epilogue/mod.rs:40-110 (act_apply_f64_a, erf_approx).                 */
+/* ------------------------------------------------------------------------ */
+
+/* C mirror of the reference's EpNode (csrc/epilogue.h:214-221). */
+typedef struct {
+    uint32_t op;
+    uint32_t aux;
+    float scalar;
+    const void *ptr;
+    size_t ld;
+} OrEpNode;
+
+enum {
+    OP_ADD_SCALAR = 0, OP_MUL_SCALAR = 1, OP_ADD_ROW = 2, OP_MUL_ROW = 3, OP_ADD_COL = 4,
+    OP_MUL_COL = 5, OP_ADD_TENSOR = 6, OP_MUL_TENSOR = 7, OP_ACT = 8, OP_MAX_SCALAR = 9,
+    OP_MIN_SCALAR = 10, OP_SUB_SCALAR = 11, OP_SUB_ROW = 12, OP_SUB_COL = 13,
+    OP_SUB_TENSOR = 14, OP_DIV_SCALAR = 15, OP_DIV_ROW = 16, OP_DIV_COL = 17,
+    OP_DIV_TENSOR = 18, OP_MAX_ROW = 19, OP_MAX_COL = 20, OP_MAX_TENSOR = 21,
+    OP_MIN_ROW = 22, OP_MIN_COL = 23, OP_MIN_TENSOR = 24
+};
+
+/* erf via Abramowitz-Stegun 7.1.26 -- src/epilogue/mod.rs:86-95. */
+static double erf_approx(double x) {
+    double ax = fabs(x);
+    double t = 1.0 / (1.0 + 0.3275911 * ax);
+    double poly = ((((1.061405429 * t - 1.453152027) * t + 1.421413741) * t - 0.284496736) * t +
+                   0.254829592) *
+                  t;
+    double e = 1.0 - poly * exp(-ax * ax);
+    return x < 0.0 ? -e : e;
+}
+
+/* maxNum / minNum as IEEE 754-2019 maximumNumber / minimumNumber (a NaN
+ * operand yields the other operand; -0 < +0). Rust's f32::max / f64::max
+ * leave the sign of a zero result unspecified and glibc's fmax and LLVM's x86
+ * lowering disagree on it; this is the AArch64 FMAXNM / FMINNM result, the
+ * reference's native platform. */
+static inline double maxnumd(double x, double y) {
+    if (isnan(x)) return y;
+    if (isnan(y)) return x;
+    if (x == 0.0 && y == 0.0) return (signbit(x) && signbit(y)) ? -0.0 : 0.0;
+    return x > y ? x : y;
+}
+static inline float maxnumf(float x, float y) {
+    if (isnan(x)) return y;
+    if (isnan(y)) return x;
+    if (x == 0.0f && y == 0.0f) return (signbit(x) && signbit(y)) ? -0.0f : 0.0f;
+    return x > y ? x : y;
+}
+static inline float minnumf(float x, float y) {
+    if (isnan(x)) return y;
+    if (isnan(y)) return x;
+    if (x == 0.0f && y == 0.0f) return (signbit(x) || signbit(y)) ? -0.0f : 0.0f;
+    return x < y ? x : y;
+}
+
+/* Rust f64::clamp: NaN stays NaN. */
+static inline double clampd(double x, double lo, double hi) {
+    if (x < lo) x = lo;
+    if (x > hi) x = hi;
+    return x;
+}
+
+/* act_apply_f64_a -- src/epilogue/mod.rs:40-84. Operation order follows the
+ * Rust expressions left to right (no re-association, no contraction). */
+double or_act_f64(uint32_t kind, double x, double alpha) {
+    const double SELU_ALPHA = 1.6732632423543772;
+    const double SELU_LAMBDA = 1.0507009873554805;
+    switch (kind) {
+    case 1: return maxnumd(x, 0.0);
+    case 2: {
+        double inner = 0.7978845608028654 * (x + 0.044715 * x * x * x);
+        return 0.5 * x * (1.0 + tanh(inner));
+    }
+    case 3: return x / (1.0 + exp(-x));
+    case 4: return tanh(x);
+    case 5: return 1.0 / (1.0 + exp(-x));
+    case 6: return x >= 0.0 ? x : alpha * x;
+    case 7: return clampd(x, 0.0, 6.0);
+    case 8: return clampd(x / 6.0 + 0.5, 0.0, 1.0);
+    case 9: return x * clampd(x / 6.0 + 0.5, 0.0, 1.0);
+    case 10: return fabs(x);
+    case 11: return -x;
+    case 12: return x * x;
+    case 13: return x > 0.0 ? 1.0 : (x < 0.0 ? -1.0 : 0.0);
+    case 14: return sqrt(x);
+    case 15: return x / (1.0 + fabs(x));
+    case 16: return 1.0 / x;
+    case 17: return 1.0 / sqrt(x);
+    case 18: return exp(x);
+    case 19: return log(x);
+    case 20: return x >= 0.0 ? x : alpha * expm1(x);
+    case 21: return SELU_LAMBDA * (x >= 0.0 ? x : SELU_ALPHA * expm1(x));
+    case 22: return maxnumd(x, 0.0) + log1p(exp(-fabs(x)));
+    case 23: return x * tanh(maxnumd(x, 0.0) + log1p(exp(-fabs(x))));
+    case 24: return 0.5 * x * (1.0 + erf_approx(x * 0.70710678118654752440));
+    default: return x;
+    }
+}
+
+/* act_apply_f32_a: widen, evaluate in f64, narrow (RNE). */
+float or_act_f32(uint32_t kind, float x, float alpha) {
+    return f64_to_f32(or_act_f64(kind, (double)x, (double)alpha));
+}
+
+static inline int is_tensor_op(uint32_t op) {
+    return op == OP_ADD_TENSOR || op == OP_MUL_TENSOR || op == OP_SUB_TENSOR ||
+           op == OP_DIV_TENSOR || op == OP_MAX_TENSOR || op == OP_MIN_TENSOR;
+}
+
+/* ep_apply_cell -- src/exec/scalar.rs:58-123. `act` < 0 means no trailing
+ * activation; otherwise it is applied last with alpha 0 (scalar.rs:118-121).
+ * Operands are f16 or bf16 (is_bf16) and read as f32. */
+float or_ep_cell(const OrEpNode *nodes, size_t n_nodes, int act, int is_bf16, float x, size_t i,
+                 size_t j, size_t n) {
+    float (*to32)(uint16_t) = is_bf16 ? or_bf16_to_f32 : or_f16_to_f32;
+    for (size_t t = 0; t < n_nodes; t++) {
+        const OrEpNode *nd = &nodes[t];
+        const uint16_t *p = (const uint16_t *)nd->ptr;
+        size_t ld = nd->ld == 0 ? n : nd->ld;
+        float v = 0.0f;
+        if (is_tensor_op(nd->op)) v = to32(p[i * ld + j]);
+        switch (nd->op) {
+        case OP_ADD_SCALAR: x = x + nd->scalar; break;
+        case OP_MUL_SCALAR: x = x * nd->scalar; break;
+        case OP_ADD_ROW: x = x + to32(p[i]); break;
+        case OP_MUL_ROW: x = x * to32(p[i]); break;
+        case OP_ADD_COL: x = x + to32(p[j]); break;
+        case OP_MUL_COL: x = x * to32(p[j]); break;
+        case OP_ADD_TENSOR: x = x + v; break;
+        case OP_MUL_TENSOR: x = x * v; break;
+        case OP_ACT: x = or_act_f32(nd->aux, x, nd->scalar); break;
+        case OP_MAX_SCALAR: x = maxnumf(x, nd->scalar); break;
+        case OP_MIN_SCALAR: x = minnumf(x, nd->scalar); break;
+        case OP_SUB_SCALAR: x = x - nd->scalar; break;
+        case OP_DIV_SCALAR: x = x / nd->scalar; break;
+        case OP_SUB_ROW: x = x - to32(p[i]); break;
+        case OP_DIV_ROW: x = x / to32(p[i]); break;
+        case OP_MAX_ROW: x = maxnumf(x, to32(p[i])); break;
+        case OP_MIN_ROW: x = minnumf(x, to32(p[i])); break;
+        case OP_SUB_COL: x = x - to32(p[j]); break;
+        case OP_DIV_COL: x = x / to32(p[j]); break;
+        case OP_MAX_COL: x = maxnumf(x, to32(p[j])); break;
+        case OP_MIN_COL: x = minnumf(x, to32(p[j])); break;
+        case OP_SUB_TENSOR: x = x - v; break;
+        case OP_DIV_TENSOR: x = x / v; break;
+        case OP_MAX_TENSOR: x = maxnumf(x, v); break;
+        case OP_MIN_TENSOR: x = minnumf(x, v); break;
+        default: break;
+        }
+    }
+    if (act >= 0) x = or_act_f32((uint32_t)act, x, 0.0f);
+    return x;
+}
+
+/* apply_ep_scalar -- scalar.rs:125-140: c[idx] = to16(cell(to32(c[idx]))). */
+void or_apply_ep(uint16_t *c, size_t m, size_t n, size_t rs, size_t cs, const OrEpNode *nodes,
+                 size_t n_nodes, int act, int is_bf16) {
+    float (*to32)(uint16_t) = is_bf16 ? or_bf16_to_f32 : or_f16_to_f32;
+    uint16_t (*to16)(float) = is_bf16 ? or_f32_to_bf16 : or_f32_to_f16;
+    for (size_t i = 0; i < m; i++) {
+        for (size_t j = 0; j < n; j++) {
+            size_t idx = i * rs + j * cs;
+            float v = or_ep_cell(nodes, n_nodes, act, is_bf16, to32(c[idx]), i, j, n);
+            c[idx] = to16(v);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Low-bit path: src/kernels/lowbit/matmul.rs:354-398.                        */
+/* ------------------------------------------------------------------------ */
+
+/* quantize_row -- matmul.rs:354-371. q: k int8, s: ceil(k/block) f32. */
+void or_quantize_row(const uint16_t *a, size_t k, size_t block, int8_t *q, float *s) {
+    size_t nbk = (k + block - 1) / block;
+    for (size_t b = 0; b < nbk; b++) {
+        size_t d0 = b * block, d1 = d0 + block < k ? d0 + block : k;
+        float amax = 0.0f;
+        for (size_t d = d0; d < d1; d++) {
+            float x = fabsf(or_f16_to_f32(a[d]));
+            if (isnan(x) || isnan(amax)) amax = NAN;
+            else amax = fmaxf(amax, x);
+        }
+        float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+        s[b] = amax / 127.0f;
+        for (size_t d = d0; d < d1; d++) {
+            float v = or_f16_to_f32(a[d]) * inv;
+            float r = nearbyintf(v); /* round-ties-even under the default mode */
+            int8_t o;
+            if (isnan(r)) o = 0; /* Rust `as i8`: NaN -> 0, saturating */
+            else if (r >= 127.0f) o = 127;
+            else if (r <= -128.0f) o = -128;
+            else o = (int8_t)r;
+            q[d] = o;
+        }
+    }
+}
+
+/* Value lookups on the reference's public INPUT formats (the band-major
+ * repack is a bijection checked separately):
+ *   Q2: weight idx = d*n + j is bits 2*(idx%4) of byte idx/4 (q2.rs:43-47),
+ *       value = codebook[code] (matmul.rs:157-160).
+ *   Q1: weight idx (OutIn: j*k + d, InOut: d*n + j) is bit idx%8 of byte
+ *       idx/8 (q1.rs:35-41), value = +1 if set else -1 (matmul.rs:161-167).
+ *   scales[j*nbk + blk] (f16), read as f32. */
+static inline int lowbit_value(int kind, const uint8_t *codes, const int8_t *codebook,
+                               int layout_inout, size_t n, size_t k, size_t d, size_t j) {
+    if (kind == 2) {
+        size_t idx = d * n + j;
+        int code = (codes[idx / 4] >> (2 * (idx % 4))) & 3;
+        return codebook[code];
+    }
+    size_t idx = layout_inout ? d * n + j : j * k + d;
+    return ((codes[idx / 8] >> (idx % 8)) & 1) ? 1 : -1;
+}
+
+/* reference -- matmul.rs:376-398. kind 2 (Q2) or 1 (Q1). c: m x n f16 bits.
+ * scratch_q: k int8, scratch_s: nbk f32. Columns [j0, j1) only, so the
+ * threaded CPU baseline can split N with identical arithmetic. */
+void or_lowbit_reference_cols(int kind, const uint16_t *a, const uint8_t *codes,
+                              const uint16_t *scales, const int8_t *codebook, int layout_inout,
+                              size_t m, size_t n, size_t k, size_t block, uint16_t *c, size_t j0,
+                              size_t j1, int8_t *scratch_q, float *scratch_s) {
+    size_t nbk = (k + block - 1) / block;
+    for (size_t i = 0; i < m; i++) {
+        or_quantize_row(a + i * k, k, block, scratch_q, scratch_s);
+        for (size_t j = j0; j < j1; j++) {
+            float total = 0.0f;
+            for (size_t blk = 0; blk < nbk; blk++) {
+                size_t d0 = blk * block, d1 = d0 + block < k ? d0 + block : k;
+                int32_t sum = 0;
+                for (size_t d = d0; d < d1; d++)
+                    sum += (int32_t)scratch_q[d] *
+                           lowbit_value(kind, codes, codebook, layout_inout, n, k, d, j);
+                float f = (float)sum; /* i32 -> f32 RNE */
+                float sc = or_f16_to_f32(scales[j * nbk + blk]) * scratch_s[blk];
+                total = fmaf(f, sc, total);
+            }
+            c[i * n + j] = or_f32_to_f16(total);
+        }
+    }
+}
+
+void or_lowbit_reference(int kind, const uint16_t *a, const uint8_t *codes,
+                         const uint16_t *scales, const int8_t *codebook, int layout_inout,
+                         size_t m, size_t n, size_t k, size_t block, uint16_t *c,
+                         int8_t *scratch_q, float *scratch_s) {
+    or_lowbit_reference_cols(kind, a, codes, scales, codebook, layout_inout, m, n, k, block, c, 0,
+                             n, scratch_q, scratch_s);
+    if (k == 0)
+        for (size_t t = 0; t < m * n; t++) c[t] = 0;
+}
+
+/* Codes::dequant -- matmul.rs:178-197: the MOPA route's f16 weights,
+ * f16::from_f32(scale_f32 * value) (row-major k x n). */
+void or_lowbit_dequant_f16(int kind, const uint8_t *codes, const uint16_t *scales,
+                           const int8_t *codebook, int layout_inout, size_t n, size_t k,
+                           size_t block, uint16_t *out) {
+    size_t nbk = (k + block - 1) / block;
+    for (size_t d = 0; d < k; d++)
+        for (size_t j = 0; j < n; j++) {
+            float s = or_f16_to_f32(scales[j * nbk + d / block]);
+            int v = lowbit_value(kind, codes, codebook, layout_inout, n, k, d, j);
+            float w = kind == 2 ? s * (float)v : (v > 0 ? s : -s);
+            out[d * n + j] = or_f32_to_f16(w);
+        }
+}
+
+/* ------------------------------------------------------------------------ */
+/* The reference's band-major resident packs (the layouts src/ffi.rs hands   */
+/* to the kernels), so the GPU library's "upload from band-major" entry      */
+/* points can be checked: q4/weights.rs:89-113, lowbit/q2.rs:12-20,53-86,     */
+/* 148-161, lowbit/q1.rs:47-107,186-201.                                      */
+/* ------------------------------------------------------------------------ */
+
+size_t or_q4_band_sizes(size_t n, size_t k, size_t block, size_t *nib_len, size_t *sc_len) {
+    size_t nb = (n + 127) / 128, nbk = (k + block - 1) / block;
+    *nib_len = nb * k * 64;
+    *sc_len = nb * nbk * 128;
+    return nb;
+}
+
+void or_q4_pack_band(const uint8_t *quants, const uint16_t *scales, const uint16_t *mins,
+                     size_t n, size_t k, size_t block, uint8_t *nib, uint16_t *sc, uint16_t *mn) {
+    size_t nib_len, sc_len;
+    or_q4_band_sizes(n, k, block, &nib_len, &sc_len);
+    size_t nbk = (k + block - 1) / block;
+    size_t nib_per_band = k * 64, sc_per_band = nbk * 128;
+    memset(nib, 0, nib_len);
+    memset(sc, 0, sc_len * 2);
+    if (mn) memset(mn, 0, sc_len * 2);
+    for (size_t d = 0; d < k; d++)
+        for (size_t j = 0; j < n; j++) {
+            size_t idx = d * n + j;
+            uint8_t v = (idx % 2 == 0) ? (quants[idx / 2] & 0x0f) : (quants[idx / 2] >> 4);
+            size_t b = j / 128, cc = j % 128;
+            nib[b * nib_per_band + d * 64 + cc / 2] |= (uint8_t)(v << (4 * (cc % 2)));
+        }
+    for (size_t j = 0; j < n; j++) {
+        size_t b = j / 128, cc = j % 128;
+        for (size_t blk = 0; blk < nbk; blk++) {
+            sc[b * sc_per_band + blk * 128 + cc] = scales[j * nbk + blk];
+            if (mn && mins) mn[b * sc_per_band + blk * 128 + cc] = mins[j * nbk + blk];
+        }
+    }
+}
+
+static inline size_t lb_scale_index(size_t sc_per_band, size_t blk, size_t j) {
+    size_t cc = j % 64;
+    return (j / 64) * sc_per_band + blk * 64 + (cc / 32) * 32 + 2 * (cc % 16) + (cc % 32) / 16;
+}
+
+/* kind 2: band_bytes = pad16(k)*16; kind 1: pad16(k)*8. sc_per_band = nbk*64. */
+void or_lowbit_band_sizes(int kind, size_t n, size_t k, size_t block, size_t *codes_len,
+                          size_t *sc_len) {
+    size_t nb = (n + 63) / 64, kp = (k + 15) / 16 * 16, nbk = (k + block - 1) / block;
+    *codes_len = nb * kp * (kind == 2 ? 16 : 8);
+    *sc_len = nb * nbk * 64;
+}
+
+void or_lowbit_pack_band(int kind, const uint8_t *codes, const uint16_t *scales,
+                         int layout_inout, size_t n, size_t k, size_t block, uint8_t *packed,
+                         uint16_t *sc) {
+    size_t codes_len, sc_len;
+    or_lowbit_band_sizes(kind, n, k, block, &codes_len, &sc_len);
+    size_t kp = (k + 15) / 16 * 16, nbk = (k + block - 1) / block;
+    size_t band_bytes = kp * (kind == 2 ? 16 : 8), sc_per_band = nbk * 64;
+    memset(packed, 0, codes_len);
+    memset(sc, 0, sc_len * 2);
+    for (size_t d = 0; d < k; d++)
+        for (size_t j = 0; j < n; j++) {
+            if (kind == 2) {
+                size_t idx = d * n + j;
+                uint8_t code = (codes[idx / 4] >> (2 * (idx % 4))) & 3;
+                packed[(j / 64) * band_bytes + (d / 4) * 64 + j % 64] |=
+                    (uint8_t)(code << (2 * (d % 4)));
+            } else {
+                size_t idx = layout_inout ? d * n + j : j * k + d;
+                if ((codes[idx / 8] >> (idx % 8)) & 1) {
+                    size_t cc = j % 64;
+                    size_t byte = (j / 64) * band_bytes + (d / 4) * 32 + cc / 2;
+                    size_t bit = 4 * (cc % 2) + d % 4;
+                    packed[byte] |= (uint8_t)(1u << bit);
+                }
+            }
+        }
+    for (size_t j = 0; j < n; j++)
+        for (size_t blk = 0; blk < nbk; blk++)
+            sc[lb_scale_index(sc_per_band, blk, j)] = scales[j * nbk + blk];
+}
+
+/* ------------------------------------------------------------------------ */
+/* Array forms of the conversions, for the Python test harness.              */
+/* ------------------------------------------------------------------------ */
+void or_f32_to_f16_array(const float *x, uint16_t *y, size_t len) {
+    for (size_t i = 0; i < len; i++) y[i] = or_f32_to_f16(x[i]);
+}
+void or_f64_to_f16_array(const double *x, uint16_t *y, size_t len) {
+    for (size_t i = 0; i < len; i++) y[i] = or_f64_to_f16(x[i]);
+}
+void or_f16_to_f32_array(const uint16_t *x, float *y, size_t len) {
+    for (size_t i = 0; i < len; i++) y[i] = or_f16_to_f32(x[i]);
+}
+void or_f32_to_bf16_array(const float *x, uint16_t *y, size_t len) {
+    for (size_t i = 0; i < len; i++) y[i] = or_f32_to_bf16(x[i]);
+}
+void or_act_f32_array(uint32_t kind, const float *x, float *y, size_t len, float alpha) {
+    for (size_t i = 0; i < len; i++) y[i] = or_act_f32(kind, x[i], alpha);
+}

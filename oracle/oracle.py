@@ -1,0 +1,304 @@
+"""Python harness over the C oracle (``oracle.c`` -> ``liboracle.so``).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg, as the checker. Every function restates a
+piece of the reference crate's portable path; the C source cites file:line for
+each. Arrays of f16/bf16 values travel as ``np.uint16`` bit patterns.
+
+Epilogues are described as ``(nodes, act)``: ``nodes`` a list of
+``(op, aux, scalar, operand_or_None, ld)`` tuples in builder order (operand a
+``np.uint16`` array of f16/bf16 bits) and ``act`` the trailing activation kind
+or ``None`` -- the fields of the reference's ``Epilogue`` (src/epilogue/graph.rs:33).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+P = C.c_void_p
+SZ = C.c_size_t
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB):
+            build()
+        _lib = C.CDLL(_LIB)
+        L = _lib
+        L.or_f16_to_f32.restype = C.c_float
+        L.or_f16_to_f32.argtypes = [C.c_uint16]
+        L.or_f32_to_f16.restype = C.c_uint16
+        L.or_f32_to_f16.argtypes = [C.c_float]
+        L.or_f64_to_f16.restype = C.c_uint16
+        L.or_f64_to_f16.argtypes = [C.c_double]
+        L.or_f32_to_bf16.restype = C.c_uint16
+        L.or_f32_to_bf16.argtypes = [C.c_float]
+        L.or_act_f64.restype = C.c_double
+        L.or_act_f64.argtypes = [C.c_uint32, C.c_double, C.c_double]
+        L.or_act_f32.restype = C.c_float
+        L.or_act_f32.argtypes = [C.c_uint32, C.c_float, C.c_float]
+        for name in ("or_f32_to_f16_array", "or_f64_to_f16_array", "or_f16_to_f32_array",
+                     "or_f32_to_bf16_array"):
+            getattr(L, name).argtypes = [P, P, SZ]
+            getattr(L, name).restype = None
+        L.or_act_f32_array.argtypes = [C.c_uint32, P, P, SZ, C.c_float]
+        L.or_q4_dequant_f16.argtypes = [P, P, P, SZ, SZ, SZ, P]
+        L.or_q4_dequant_bf16.argtypes = [P, P, P, SZ, SZ, SZ, P]
+        L.or_gemm_f16.argtypes = [SZ, SZ, SZ, P, P, P, C.c_uint16, C.c_int, P]
+        L.or_gemm_bf16.argtypes = [SZ, SZ, SZ, P, P, P, C.c_uint16, C.c_int, P]
+        L.or_gemm_f16_cols.argtypes = [SZ, SZ, SZ, P, P, P, SZ, SZ, P]
+        L.or_apply_ep.argtypes = [P, SZ, SZ, SZ, SZ, P, SZ, C.c_int, C.c_int]
+        L.or_quantize_row.argtypes = [P, SZ, SZ, P, P]
+        L.or_lowbit_reference.argtypes = [C.c_int, P, P, P, P, C.c_int, SZ, SZ, SZ, SZ, P, P, P]
+        L.or_lowbit_reference_cols.argtypes = [C.c_int, P, P, P, P, C.c_int, SZ, SZ, SZ, SZ, P,
+                                               SZ, SZ, P, P]
+        L.or_lowbit_dequant_f16.argtypes = [C.c_int, P, P, P, C.c_int, SZ, SZ, SZ, P]
+        L.or_q4_band_sizes.argtypes = [SZ, SZ, SZ, C.POINTER(SZ), C.POINTER(SZ)]
+        L.or_q4_band_sizes.restype = SZ
+        L.or_q4_pack_band.argtypes = [P, P, P, SZ, SZ, SZ, P, P, P]
+        L.or_lowbit_band_sizes.argtypes = [C.c_int, SZ, SZ, SZ, C.POINTER(SZ), C.POINTER(SZ)]
+        L.or_lowbit_pack_band.argtypes = [C.c_int, P, P, C.c_int, SZ, SZ, SZ, P, P]
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(P)
+
+
+def _c(a, dtype):
+    return None if a is None else np.ascontiguousarray(a, dtype=dtype)
+
+
+# ---- conversions -----------------------------------------------------------
+
+def f32_to_f16(x) -> np.ndarray:
+    x = _c(np.asarray(x, np.float32).ravel(), np.float32)
+    y = np.empty(x.size, np.uint16)
+    lib().or_f32_to_f16_array(_p(x), _p(y), x.size)
+    return y
+
+
+def f64_to_f16(x) -> np.ndarray:
+    x = _c(np.asarray(x, np.float64).ravel(), np.float64)
+    y = np.empty(x.size, np.uint16)
+    lib().or_f64_to_f16_array(_p(x), _p(y), x.size)
+    return y
+
+
+def f16_to_f32(h) -> np.ndarray:
+    h = _c(np.asarray(h, np.uint16).ravel(), np.uint16)
+    y = np.empty(h.size, np.float32)
+    lib().or_f16_to_f32_array(_p(h), _p(y), h.size)
+    return y
+
+
+def f32_to_bf16(x) -> np.ndarray:
+    x = _c(np.asarray(x, np.float32).ravel(), np.float32)
+    y = np.empty(x.size, np.uint16)
+    lib().or_f32_to_bf16_array(_p(x), _p(y), x.size)
+    return y
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def act_f32(kind: int, x, alpha: float = 0.0) -> np.ndarray:
+    x = _c(np.asarray(x, np.float32).ravel(), np.float32)
+    y = np.empty_like(x)
+    lib().or_act_f32_array(kind, _p(x), _p(y), x.size, alpha)
+    return y
+
+
+# ---- Q4 --------------------------------------------------------------------
+
+def q4_dequant(quants, scales, mins, n, k, block, bf16=False) -> np.ndarray:
+    """Row-major k x n weights as the portable path multiplies them
+    (src/kernels/q4/mod.rs:193-224; weights.rs:190-259)."""
+    quants = _c(quants, np.uint8)
+    scales = _c(scales, np.uint16)
+    mins = _c(mins, np.uint16)
+    out = np.empty(k * n, np.uint16)
+    fn = lib().or_q4_dequant_bf16 if bf16 else lib().or_q4_dequant_f16
+    fn(_p(quants), _p(scales), _p(mins), n, k, block, _p(out))
+    return out
+
+
+def gemm16(a, b, m, n, k, beta_bits=None, col_major=False, bf16=False) -> np.ndarray:
+    """reference::gemm_f16 / gemm_bf16 (src/reference.rs:308-387) with
+    alpha = 0, as the packed fallback calls it (src/exec/macros.rs:188-203)."""
+    a = _c(a, np.uint16)
+    b = _c(b, np.uint16)
+    if beta_bits is None:
+        beta_bits = 0x3F80 if bf16 else 0x3C00
+    c = np.zeros(m * n, np.uint16)
+    acc = np.empty(max(n, 1), np.float32)
+    fn = lib().or_gemm_bf16 if bf16 else lib().or_gemm_f16
+    fn(m, n, k, _p(c), _p(a), _p(b), beta_bits, int(col_major), _p(acc))
+    return c
+
+
+class _EpNode(C.Structure):
+    _fields_ = [("op", C.c_uint32), ("aux", C.c_uint32), ("scalar", C.c_float),
+                ("ptr", C.c_void_p), ("ld", C.c_size_t)]
+
+
+def apply_ep(c, m, n, nodes, act, bf16=False, col_major=False) -> np.ndarray:
+    """apply_ep_scalar (src/exec/scalar.rs:125-140) on a copy of c."""
+    c = np.array(c, np.uint16, copy=True)
+    keep = []
+    arr = (_EpNode * max(len(nodes), 1))()
+    for t, (op, aux, scalar, operand, ld) in enumerate(nodes):
+        ptr = None
+        if operand is not None:
+            operand = _c(operand, np.uint16)
+            keep.append(operand)
+            ptr = operand.ctypes.data
+        arr[t] = _EpNode(op, aux, scalar, ptr, ld)
+    rs, cs = (1, m) if col_major else (n, 1)
+    lib().or_apply_ep(_p(c), m, n, rs, cs, C.cast(arr, P), len(nodes),
+                      -1 if act is None else int(act), int(bf16))
+    return c
+
+
+def _has_ep(nodes, act):
+    return len(nodes) > 0 or act is not None
+
+
+def packed_ep(a, b, m, n, k, nodes=(), act=None, beta_bits=None, col_major=False, bf16=False):
+    """f16/bf16_packed_ep_impl's portable branch (src/exec/macros.rs:188-206):
+    reference GEMM, then the scalar epilogue iff the graph is non-empty."""
+    c = gemm16(a, b, m, n, k, beta_bits, col_major, bf16)
+    if _has_ep(nodes, act):
+        c = apply_ep(c, m, n, list(nodes), act, bf16, col_major)
+    return c
+
+
+def matmul_q4_ep(a, quants, scales, mins, m, n, k, block, nodes=(), act=None, bf16=False):
+    """matmul_q4_ep / matmul_q4_bf16_ep off-Apple (src/kernels/q4/matmul.rs:91-102,
+    :258-270): dequant to row-major, then the dense packed path."""
+    if m == 0 or n == 0:
+        return np.zeros(m * n, np.uint16)
+    b = q4_dequant(quants, scales, mins, n, k, block, bf16)
+    return packed_ep(a, b, m, n, k, nodes, act, None, False, bf16)
+
+
+# ---- low-bit -----------------------------------------------------------------
+
+def quantize_row(a, k, block):
+    """quantize_row (src/kernels/lowbit/matmul.rs:354-371)."""
+    a = _c(a, np.uint16)
+    nbk = -(-k // block)
+    q = np.empty(max(k, 1), np.int8)
+    s = np.empty(max(nbk, 1), np.float32)
+    lib().or_quantize_row(_p(a), k, block, _p(q), _p(s))
+    return q[:k], s[:nbk]
+
+
+def lowbit_reference(kind, a, codes, scales, m, n, k, block, codebook=(-1, 0, 1, 0),
+                     inout=False, cols=None):
+    """reference (src/kernels/lowbit/matmul.rs:376-398) on the public input
+    formats: kind 2 = Q2 (q2.rs:43-47), kind 1 = Q1 (q1.rs:35-41)."""
+    a = _c(a, np.uint16)
+    codes = _c(codes, np.uint8)
+    scales = _c(scales, np.uint16)
+    cb = np.asarray(codebook, np.int8)
+    c = np.zeros(m * n, np.uint16)
+    q = np.empty(max(k, 1), np.int8)
+    s = np.empty(max(-(-k // block), 1), np.float32)
+    if cols is None:
+        lib().or_lowbit_reference(kind, _p(a), _p(codes), _p(scales), _p(cb), int(inout), m, n,
+                                  k, block, _p(c), _p(q), _p(s))
+    else:
+        lib().or_lowbit_reference_cols(kind, _p(a), _p(codes), _p(scales), _p(cb), int(inout),
+                                       m, n, k, block, _p(c), cols[0], cols[1], _p(q), _p(s))
+    return c
+
+
+def matmul_lowbit_ep(kind, a, codes, scales, m, n, k, block, nodes=(), act=None,
+                     codebook=(-1, 0, 1, 0), inout=False):
+    """lowbit_impl off-Apple (matmul.rs:326-337): reference, then apply_ep_scalar
+    (always called; the empty graph is the identity)."""
+    if m == 0 or n == 0:
+        return np.zeros(m * n, np.uint16)
+    c = lowbit_reference(kind, a, codes, scales, m, n, k, block, codebook, inout)
+    return apply_ep(c, m, n, list(nodes), act)
+
+
+def lowbit_dequant(kind, codes, scales, n, k, block, codebook=(-1, 0, 1, 0), inout=False):
+    """Codes::dequant (matmul.rs:178-197)."""
+    codes = _c(codes, np.uint8)
+    scales = _c(scales, np.uint16)
+    cb = np.asarray(codebook, np.int8)
+    out = np.empty(k * n, np.uint16)
+    lib().or_lowbit_dequant_f16(kind, _p(codes), _p(scales), _p(cb), int(inout), n, k, block,
+                                _p(out))
+    return out
+
+
+def matmul_lowbit_mopa_ep(kind, a, codes, scales, m, n, k, block, nodes=(), act=None,
+                          codebook=(-1, 0, 1, 0), inout=False):
+    """mopa_impl off-Apple (matmul.rs:339-350): eager dequant, dense f16 path."""
+    if m == 0 or n == 0:
+        return np.zeros(m * n, np.uint16)
+    b = lowbit_dequant(kind, codes, scales, n, k, block, codebook, inout)
+    return packed_ep(a, b, m, n, k, nodes, act)
+
+
+# ---- the reference's band-major resident packs ------------------------------
+
+def q4_pack_band(quants, scales, mins, n, k, block):
+    nl, sl = SZ(), SZ()
+    lib().or_q4_band_sizes(n, k, block, C.byref(nl), C.byref(sl))
+    nib = np.empty(nl.value, np.uint8)
+    sc = np.empty(sl.value, np.uint16)
+    mn = np.empty(sl.value, np.uint16) if mins is not None else None
+    lib().or_q4_pack_band(_p(_c(quants, np.uint8)), _p(_c(scales, np.uint16)),
+                          _p(_c(mins, np.uint16)), n, k, block, _p(nib), _p(sc), _p(mn))
+    return nib, sc, mn
+
+
+def lowbit_pack_band(kind, codes, scales, n, k, block, inout=False):
+    cl, sl = SZ(), SZ()
+    lib().or_lowbit_band_sizes(kind, n, k, block, C.byref(cl), C.byref(sl))
+    packed = np.empty(cl.value, np.uint8)
+    sc = np.empty(sl.value, np.uint16)
+    lib().or_lowbit_pack_band(kind, _p(_c(codes, np.uint8)), _p(_c(scales, np.uint16)),
+                              int(inout), n, k, block, _p(packed), _p(sc))
+    return packed, sc
+
+
+# ---- the reference's test-data generators -----------------------------------
+
+def lcg_bytes(seed: int, length: int) -> np.ndarray:
+    """`data`/`bytes`/`byte` of the reference tests
+    (src/kernels/lowbit/matmul.rs:409-417, tests/correctness/q4.rs:18-21):
+    s = s*6364136223846793005 + 1 (mod 2^64), byte = (s >> 40) as u8."""
+    out = np.empty(length, np.uint8)
+    s = seed & 0xFFFFFFFFFFFFFFFF
+    for i in range(length):
+        s = (s * 6364136223846793005 + 1) & 0xFFFFFFFFFFFFFFFF
+        out[i] = (s >> 40) & 0xFF
+    return out
+
+
+def lcg_fill(seed: int, length: int):
+    """`fill` of tests/correctness/main.rs:36-46: returns (f16 bits, new seed)."""
+    vals = np.empty(length, np.float32)
+    s = seed & 0xFFFFFFFFFFFFFFFF
+    for i in range(length):
+        s = (s * 6364136223846793005 + 1442695040888963407) & 0xFFFFFFFFFFFFFFFF
+        vals[i] = np.float32(s >> 40) / np.float32(1 << 24) - np.float32(0.5)
+    return f32_to_f16(vals), s

@@ -1,0 +1,737 @@
+// The C ABI (include/smegemm_gpu.h): weight handles, host-pointer drop-ins for
+// the reference's gemm_sme_* entry points, and device-pointer entry points.
+//
+// Error contract (the reference's, src/kernels/q4/matmul.rs:85-90): a non-zero
+// return leaves the caller's output untouched -- results are copied back to
+// the host only after the kernels and the stream have completed successfully.
+#include <pthread.h>
+
+#include <atomic>
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+
+using namespace smg;
+
+struct smg_weights {
+    WDev d;
+    int device;
+    size_t bytes;
+    std::vector<void *> allocs;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *what, hipError_t e = hipSuccess) {
+    g_err = what;
+    if (e != hipSuccess) {
+        g_err += ": ";
+        g_err += hipGetErrorString(e);
+    }
+    return code;
+}
+
+#define HIP_TRY(call, code)                                        \
+    do {                                                           \
+        hipError_t e_ = (call);                                    \
+        if (e_ != hipSuccess) return fail((code), #call, e_);      \
+    } while (0)
+
+bool is_pow2(size_t x) { return x != 0 && (x & (x - 1)) == 0; }
+size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// ---- device presence -------------------------------------------------------
+int g_avail = -1;
+pthread_once_t g_avail_once = PTHREAD_ONCE_INIT;
+void probe_avail() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        g_avail = 0;
+        return;
+    }
+    hipDeviceProp_t p;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess) {
+        g_avail = 0;
+        return;
+    }
+    g_avail = std::strncmp(p.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+// ---- per-thread stream + staging (the reference's thread_local scratch) ----
+struct Ctx {
+    hipStream_t stream = nullptr;
+    int device = -1;
+    void *buf = nullptr;
+    size_t cap = 0;
+    ~Ctx() {
+        if (buf) (void)hipFree(buf);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+thread_local Ctx g_ctx;
+
+int ctx_for(int device, size_t bytes, Ctx **out) {
+    Ctx &c = g_ctx;
+    HIP_TRY(hipSetDevice(device), SMG_EHIP);
+    if (c.device != device) {
+        if (c.buf) (void)hipFree(c.buf);
+        if (c.stream) (void)hipStreamDestroy(c.stream);
+        c.buf = nullptr;
+        c.cap = 0;
+        c.stream = nullptr;
+        HIP_TRY(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking), SMG_EHIP);
+        c.device = device;
+    }
+    if (bytes > c.cap) {
+        if (c.buf) (void)hipFree(c.buf);
+        c.buf = nullptr;
+        c.cap = 0;
+        size_t want = round_up(bytes, 1 << 20);
+        if (hipMalloc(&c.buf, want) != hipSuccess) return fail(SMG_ENOMEM, "staging hipMalloc");
+        c.cap = want;
+    }
+    *out = &c;
+    return SMG_OK;
+}
+
+bool trace_on() {
+    static int on = -1;
+    if (on < 0) {
+        const char *e = std::getenv("SMEGEMM_TRACE");
+        on = (e && *e && std::strcmp(e, "0") != 0) ? 1 : 0;
+    }
+    return on == 1;
+}
+
+// ---- epilogue marshalling --------------------------------------------------
+bool op_is_row(uint32_t op) {
+    return op == EP_OP_ADD_ROW || op == EP_OP_MUL_ROW || op == EP_OP_SUB_ROW ||
+           op == EP_OP_DIV_ROW || op == EP_OP_MAX_ROW || op == EP_OP_MIN_ROW;
+}
+bool op_is_col(uint32_t op) {
+    return op == EP_OP_ADD_COL || op == EP_OP_MUL_COL || op == EP_OP_SUB_COL ||
+           op == EP_OP_DIV_COL || op == EP_OP_MAX_COL || op == EP_OP_MIN_COL;
+}
+bool op_is_tensor(uint32_t op) {
+    return op == EP_OP_ADD_TENSOR || op == EP_OP_MUL_TENSOR || op == EP_OP_SUB_TENSOR ||
+           op == EP_OP_DIV_TENSOR || op == EP_OP_MAX_TENSOR || op == EP_OP_MIN_TENSOR;
+}
+// Elements a node's operand spans (0 for scalar / act nodes).
+size_t operand_elems(const EpNode &nd, size_t m, size_t n) {
+    if (op_is_row(nd.op)) return m;
+    if (op_is_col(nd.op)) return n;
+    if (op_is_tensor(nd.op)) {
+        size_t ld = nd.ld == 0 ? n : nd.ld;
+        return m == 0 ? 0 : (m - 1) * ld + n;
+    }
+    return 0;
+}
+
+int ep_args(const ep_desc16 *ep, EpArgs *out) {
+    std::memset(out, 0, sizeof(*out));
+    if (!ep || ep->n_nodes == 0) return SMG_OK;
+    if (ep->n_nodes > SMG_MAX_EP_NODES) return fail(SMG_EINVAL, "epilogue has too many nodes");
+    out->n_nodes = ep->n_nodes;
+    for (uint32_t i = 0; i < ep->n_nodes; i++) out->nodes[i] = ep->nodes[i];
+    return SMG_OK;
+}
+
+// ---- weight creation ---------------------------------------------------------
+int alloc_dev(smg_weights *w, size_t bytes, void **p) {
+    if (hipMalloc(p, bytes ? bytes : 16) != hipSuccess) return fail(SMG_ENOMEM, "weights hipMalloc");
+    w->allocs.push_back(*p);
+    w->bytes += bytes;
+    return SMG_OK;
+}
+
+void destroy(smg_weights *w) {
+    if (!w) return;
+    if (w->device >= 0) (void)hipSetDevice(w->device);
+    for (void *p : w->allocs) (void)hipFree(p);
+    delete w;
+}
+
+int upload(smg_weights *w, const void *host, size_t bytes, void **dev) {
+    int rc = alloc_dev(w, bytes, dev);
+    if (rc) return rc;
+    if (bytes) HIP_TRY(hipMemcpy(*dev, host, bytes, hipMemcpyHostToDevice), SMG_EHIP);
+    return SMG_OK;
+}
+
+smg_weights *new_weights(int kind, size_t n, size_t k, size_t block) {
+    smg_weights *w = new smg_weights();
+    std::memset(&w->d, 0, sizeof(w->d));
+    w->d.kind = kind;
+    w->d.n = n;
+    w->d.k = k;
+    w->d.block = block;
+    w->d.n_pad = round_up(n ? n : 1, 128);
+    w->bytes = 0;
+    (void)hipGetDevice(&w->device);
+    return w;
+}
+
+// Nibble accessors for the two Q4 input formats.
+struct Q4RowMajor {
+    const uint8_t *q;
+    size_t n;
+    uint8_t operator()(size_t d, size_t j) const {
+        size_t idx = d * n + j;
+        return idx % 2 == 0 ? (q[idx / 2] & 0x0f) : (q[idx / 2] >> 4);
+    }
+};
+struct Q4Band {  // q4/weights.rs:89-101 (128-column bands, 64 bytes a depth)
+    const uint8_t *q;
+    size_t k;
+    uint8_t operator()(size_t d, size_t j) const {
+        size_t b = j / 128, c = j % 128;
+        uint8_t byte = q[b * k * 64 + d * 64 + c / 2];
+        return (byte >> (4 * (c % 2))) & 0x0f;
+    }
+};
+
+template <class Get>
+int make_q4(Get get, const uint16_t *scales_rm, const uint16_t *mins_rm, const uint16_t *scales_band,
+            const uint16_t *mins_band, size_t n, size_t k, size_t block, smg_weights **out) {
+    if (!is_pow2(block)) return fail(SMG_EINVAL, "q4 block size must be a power of two");
+    smg_weights *w = new_weights(W_Q4, n, k, block);
+    WDev &d = w->d;
+    d.nchunks = (k + Q4_CHUNK - 1) / Q4_CHUNK;
+    const size_t nbk = (k + block - 1) / block;
+    d.sc_rows = std::max(nbk, (d.nchunks * Q4_CHUNK + block - 1) / block);
+    d.k_pad = round_up(k ? k : 1, 64);
+    std::vector<uint8_t> nib(d.nchunks * d.n_pad * 16, 0);
+    for (size_t dd = 0; dd < k; dd++) {
+        const size_t kc = dd / 32, x = dd % 32, wd = x / 8, e = (x % 8) / 2, h = x % 2;
+        const size_t bitpos = 16 * h + 4 * e;
+        const size_t byteoff = wd * 4 + bitpos / 8;
+        const int shift = bitpos % 8;
+        for (size_t j = 0; j < n; j++)
+            nib[(kc * d.n_pad + j) * 16 + byteoff] |= (uint8_t)(get(dd, j) << shift);
+    }
+    std::vector<uint16_t> sc(d.sc_rows * d.n_pad, 0), mn;
+    const bool affine = mins_rm || mins_band;
+    if (affine) mn.assign(d.sc_rows * d.n_pad, 0);
+    for (size_t j = 0; j < n; j++)
+        for (size_t b = 0; b < nbk; b++) {
+            size_t src;
+            if (scales_rm) {
+                src = j * nbk + b;
+                sc[b * d.n_pad + j] = scales_rm[src];
+                if (affine) mn[b * d.n_pad + j] = mins_rm[src];
+            } else {
+                src = (j / 128) * (nbk * 128) + b * 128 + j % 128;
+                sc[b * d.n_pad + j] = scales_band[src];
+                if (affine) mn[b * d.n_pad + j] = mins_band[src];
+            }
+        }
+    void *p;
+    int rc;
+    if ((rc = upload(w, nib.data(), nib.size(), &p))) { destroy(w); return rc; }
+    d.codes = (const uint8_t *)p;
+    if ((rc = upload(w, sc.data(), sc.size() * 2, &p))) { destroy(w); return rc; }
+    d.scales = (const uint16_t *)p;
+    if (affine) {
+        if ((rc = upload(w, mn.data(), mn.size() * 2, &p))) { destroy(w); return rc; }
+        d.mins = (const uint16_t *)p;
+    }
+    *out = w;
+    return SMG_OK;
+}
+
+// Low-bit value accessors (2-bit code or 1-bit sign at depth d, column j).
+struct Q2RowMajor {  // q2.rs:43-47
+    const uint8_t *q;
+    size_t n;
+    uint8_t operator()(size_t d, size_t j) const {
+        size_t idx = d * n + j;
+        return (q[idx / 4] >> (2 * (idx % 4))) & 3;
+    }
+};
+struct Q2Band {  // q2.rs:148-161
+    const uint8_t *q;
+    size_t band_bytes;
+    uint8_t operator()(size_t d, size_t j) const {
+        return (q[(j / 64) * band_bytes + (d / 4) * 64 + j % 64] >> (2 * (d % 4))) & 3;
+    }
+};
+struct Q1RowMajor {  // q1.rs:35-41
+    const uint8_t *q;
+    size_t n, k;
+    int inout;
+    uint8_t operator()(size_t d, size_t j) const {
+        size_t idx = inout ? d * n + j : j * k + d;
+        return (q[idx / 8] >> (idx % 8)) & 1;
+    }
+};
+struct Q1Band {  // q1.rs:186-201
+    const uint8_t *q;
+    size_t band_bytes;
+    uint8_t operator()(size_t d, size_t j) const {
+        size_t c = j % 64;
+        size_t byte = (j / 64) * band_bytes + (d / 4) * 32 + c / 2;
+        return (q[byte] >> (4 * (c % 2) + d % 4)) & 1;
+    }
+};
+
+size_t lb_scale_index(size_t sc_per_band, size_t blk, size_t j) {  // q2.rs:17-20
+    size_t c = j % 64;
+    return (j / 64) * sc_per_band + blk * 64 + (c / 32) * 32 + 2 * (c % 16) + (c % 32) / 16;
+}
+
+template <class Get>
+int make_lowbit(int kind, Get get, const uint16_t *scales, bool band_scales,
+                const int8_t *codebook, size_t n, size_t k, size_t block, smg_weights **out) {
+    if (!is_pow2(block) || block < 16 || block > 65536)
+        return fail(SMG_EINVAL, "low-bit block size must be a power of two from 16 to 65536");
+    smg_weights *w = new_weights(kind, n, k, block);
+    WDev &d = w->d;
+    const size_t ch = kind == W_Q2 ? Q2_CHUNK : Q1_CHUNK;
+    d.nchunks = (k + ch - 1) / ch;
+    const size_t nbk = (k + block - 1) / block;
+    d.sc_rows = std::max(nbk, (d.nchunks * ch + block - 1) / block);
+    d.k_pad = round_up(k ? k : 1, 64);
+    if (kind == W_Q2)
+        d.codebook = (uint32_t)(uint8_t)codebook[0] | ((uint32_t)(uint8_t)codebook[1] << 8) |
+                     ((uint32_t)(uint8_t)codebook[2] << 16) | ((uint32_t)(uint8_t)codebook[3] << 24);
+    std::vector<uint8_t> codes(d.nchunks * d.n_pad * 16, 0);
+    for (size_t dd = 0; dd < k; dd++) {
+        const size_t kc = dd / ch, x = dd % ch;
+        size_t bitpos;
+        if (kind == W_Q2) {
+            const size_t wd = x / 16, i = (x % 16) / 4, b = x % 4;
+            bitpos = wd * 32 + 8 * b + 2 * i;
+        } else {
+            const size_t wd = x / 32, i = (x % 32) / 4, b = x % 4;
+            bitpos = wd * 32 + 8 * b + i;
+        }
+        for (size_t j = 0; j < n; j++)
+            codes[(kc * d.n_pad + j) * 16 + bitpos / 8] |= (uint8_t)(get(dd, j) << (bitpos % 8));
+    }
+    std::vector<uint16_t> sc(d.sc_rows * d.n_pad, 0);
+    for (size_t j = 0; j < n; j++)
+        for (size_t b = 0; b < nbk; b++)
+            sc[b * d.n_pad + j] =
+                band_scales ? scales[lb_scale_index(nbk * 64, b, j)] : scales[j * nbk + b];
+    void *p;
+    int rc;
+    if ((rc = upload(w, codes.data(), codes.size(), &p))) { destroy(w); return rc; }
+    d.codes = (const uint8_t *)p;
+    if ((rc = upload(w, sc.data(), sc.size() * 2, &p))) { destroy(w); return rc; }
+    d.scales = (const uint16_t *)p;
+    *out = w;
+    return SMG_OK;
+}
+
+int make_dense(int kind, const uint16_t *rhs, size_t n, size_t k, long rs, long cs,
+               smg_weights **out) {
+    smg_weights *w = new_weights(kind, n, k, 0);
+    WDev &d = w->d;
+    d.k_pad = round_up(k ? k : 1, 64);
+    std::vector<uint16_t> buf(d.n_pad * d.k_pad, 0);
+    for (size_t j = 0; j < n; j++)
+        for (size_t l = 0; l < k; l++) buf[j * d.k_pad + l] = rhs[(long)l * rs + (long)j * cs];
+    void *p;
+    int rc = upload(w, buf.data(), buf.size() * 2, &p);
+    if (rc) { destroy(w); return rc; }
+    d.dense = (const uint16_t *)p;
+    *out = w;
+    return SMG_OK;
+}
+
+// ---- one host-pointer call ---------------------------------------------------
+// Stages lhs and epilogue operands, runs `launch` on the thread's stream, and
+// copies dst back only after everything succeeded.
+template <class Launch>
+int host_call(const char *name, int device, size_t m, size_t n, size_t k, uint16_t *dst,
+              size_t dst_elems, bool preload_dst, const uint16_t *lhs, size_t lhs_elems,
+              const ep_desc16 *ep, size_t extra_scratch, Launch launch) {
+    EpArgs ea;
+    int rc = ep_args(ep, &ea);
+    if (rc) return rc;
+    size_t op_elems[SMG_MAX_EP_NODES] = {0};
+    size_t total = round_up(lhs_elems * 2, 256) + round_up(dst_elems * 2, 256) +
+                   round_up(extra_scratch, 256);
+    for (uint32_t i = 0; i < ea.n_nodes; i++) {
+        op_elems[i] = ea.nodes[i].ptr ? operand_elems(ea.nodes[i], m, n) : 0;
+        total += round_up(op_elems[i] * 2, 256);
+    }
+    Ctx *c;
+    if ((rc = ctx_for(device, total, &c))) return rc;
+    uint8_t *p = (uint8_t *)c->buf;
+    uint16_t *d_lhs = (uint16_t *)p;
+    p += round_up(lhs_elems * 2, 256);
+    uint16_t *d_dst = (uint16_t *)p;
+    p += round_up(dst_elems * 2, 256);
+    void *scratch = p;
+    p += round_up(extra_scratch, 256);
+    for (uint32_t i = 0; i < ea.n_nodes; i++) {
+        if (!op_elems[i]) continue;
+        HIP_TRY(hipMemcpyAsync(p, ea.nodes[i].ptr, op_elems[i] * 2, hipMemcpyHostToDevice,
+                               c->stream), SMG_EHIP);
+        ea.nodes[i].ptr = p;
+        p += round_up(op_elems[i] * 2, 256);
+    }
+    if (lhs_elems)
+        HIP_TRY(hipMemcpyAsync(d_lhs, lhs, lhs_elems * 2, hipMemcpyHostToDevice, c->stream),
+                SMG_EHIP);
+    if (preload_dst && dst_elems)
+        HIP_TRY(hipMemcpyAsync(d_dst, dst, dst_elems * 2, hipMemcpyHostToDevice, c->stream),
+                SMG_EHIP);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    const bool tr = trace_on();
+    if (tr) {
+        (void)hipEventCreate(&e0);
+        (void)hipEventCreate(&e1);
+        (void)hipEventRecord(e0, c->stream);
+    }
+    hipError_t e = launch(d_dst, d_lhs, ea, scratch, c->stream);
+    if (e != hipSuccess) return fail(SMG_EHIP, name, e);
+    if (tr) (void)hipEventRecord(e1, c->stream);
+    HIP_TRY(hipStreamSynchronize(c->stream), SMG_EHIP);
+    if (tr) {
+        float ms = 0;
+        (void)hipEventElapsedTime(&ms, e0, e1);
+        std::fprintf(stderr, "[smegemm] %s %zux%zux%zu %.1f us\n", name, m, n, k, ms * 1e3);
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+    }
+    if (dst_elems)
+        HIP_TRY(hipMemcpy(dst, d_dst, dst_elems * 2, hipMemcpyDeviceToHost), SMG_EHIP);
+    return SMG_OK;
+}
+
+int check_kind(const smg_weights *w, int kind) {
+    if (!w) return fail(SMG_EINVAL, "null weights");
+    if (w->d.kind != kind) return fail(SMG_EKIND, "weight handle of another kind");
+    return SMG_OK;
+}
+
+// Q4 dispatch: GEMV up to Q4_GEMV_MAX_ROWS rows, MFMA GEMM above.
+hipError_t run_q4(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs, const EpArgs &ea,
+                  bool bf16, hipStream_t s) {
+    if (m <= Q4_GEMV_MAX_ROWS) return launch_q4_gemv(w, m, dst, lhs, ea, bf16, s);
+    return launch_gemm(w, m, dst, 1, (long)w.n, lhs, 1, (long)w.k, 1.0f, ea, bf16, s);
+}
+
+// k == 0: every output is the epilogue applied to +0 (reference GEMM of an
+// empty sum); the GEMV and GEMM kernels handle it (zero chunks, zero steps).
+
+float half_bits_to_float(uint16_t h, bool bf16) {
+    if (bf16) {
+        uint32_t u = (uint32_t)h << 16;
+        float f;
+        std::memcpy(&f, &u, 4);
+        return f;
+    }
+    // f16 -> f32 (exact)
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, exp = (h >> 10) & 0x1f, man = h & 0x3ffu, u;
+    if (exp == 0x1f) u = sign | 0x7f800000u | (man << 13);
+    else if (exp == 0) {
+        float v = (float)man * 5.9604644775390625e-08f;
+        return sign ? -v : v;
+    } else u = sign | ((exp + 112u) << 23) | (man << 13);
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+}  // namespace
+
+// ============================================================================
+extern "C" {
+
+int smg_available(void) {
+    pthread_once(&g_avail_once, probe_avail);
+    return g_avail;
+}
+
+const char *smg_last_error(void) { return g_err.c_str(); }
+
+size_t smg_q4_gemv_max_rows(void) { return Q4_GEMV_MAX_ROWS; }
+
+int smg_q4_create(const uint8_t *quants, const uint16_t *scales, const uint16_t *mins, size_t n,
+                  size_t k, size_t block, smg_weights **out) {
+    if (!smg_available()) return fail(SMG_ENODEV, "no gfx950 device");
+    return make_q4(Q4RowMajor{quants, n}, scales, mins, nullptr, nullptr, n, k, block, out);
+}
+
+int smg_q4_create_band(const uint8_t *nibbles, const uint16_t *scales, const uint16_t *mins,
+                       size_t n, size_t k, size_t block, smg_weights **out) {
+    if (!smg_available()) return fail(SMG_ENODEV, "no gfx950 device");
+    return make_q4(Q4Band{nibbles, k}, nullptr, nullptr, scales, mins, n, k, block, out);
+}
+
+int smg_q2_create(const uint8_t *codes, const uint16_t *scales, const int8_t *codebook, size_t n,
+                  size_t k, size_t block, smg_weights **out) {
+    if (!smg_available()) return fail(SMG_ENODEV, "no gfx950 device");
+    return make_lowbit(W_Q2, Q2RowMajor{codes, n}, scales, false, codebook, n, k, block, out);
+}
+
+int smg_q2_create_band(const uint8_t *codes, const uint16_t *scales, const int8_t *codebook,
+                       size_t n, size_t k, size_t block, smg_weights **out) {
+    if (!smg_available()) return fail(SMG_ENODEV, "no gfx950 device");
+    return make_lowbit(W_Q2, Q2Band{codes, round_up(k, 16) * 16}, scales, true, codebook, n, k,
+                       block, out);
+}
+
+int smg_q1_create(const uint8_t *signs, const uint16_t *scales, int layout, size_t n, size_t k,
+                  size_t block, smg_weights **out) {
+    if (!smg_available()) return fail(SMG_ENODEV, "no gfx950 device");
+    return make_lowbit(W_Q1, Q1RowMajor{signs, n, k, layout}, scales, false, nullptr, n, k, block,
+                       out);
+}
+
+int smg_q1_create_band(const uint8_t *signs, const uint16_t *scales, size_t n, size_t k,
+                       size_t block, smg_weights **out) {
+    if (!smg_available()) return fail(SMG_ENODEV, "no gfx950 device");
+    return make_lowbit(W_Q1, Q1Band{signs, round_up(k, 16) * 8}, scales, true, nullptr, n, k,
+                       block, out);
+}
+
+int smg_f16_prepack(const uint16_t *rhs, size_t n, size_t k, long rhs_rs, long rhs_cs,
+                    smg_weights **out) {
+    if (!smg_available()) return fail(SMG_ENODEV, "no gfx950 device");
+    return make_dense(W_F16, rhs, n, k, rhs_rs, rhs_cs, out);
+}
+
+int smg_bf16_prepack(const uint16_t *rhs, size_t n, size_t k, long rhs_rs, long rhs_cs,
+                     smg_weights **out) {
+    if (!smg_available()) return fail(SMG_ENODEV, "no gfx950 device");
+    return make_dense(W_BF16, rhs, n, k, rhs_rs, rhs_cs, out);
+}
+
+int smg_q4_dequant(const smg_weights *q4, int to_bf16, smg_weights **out) {
+    int rc = check_kind(q4, W_Q4);
+    if (rc) return rc;
+    HIP_TRY(hipSetDevice(q4->device), SMG_EHIP);
+    smg_weights *w = new_weights(to_bf16 ? W_BF16 : W_F16, q4->d.n, q4->d.k, 0);
+    w->d.k_pad = round_up(q4->d.k_pad, 32);
+    WDev src = q4->d;
+    src.k_pad = w->d.k_pad;
+    void *p;
+    if ((rc = alloc_dev(w, w->d.n_pad * w->d.k_pad * 2, &p))) { destroy(w); return rc; }
+    w->d.dense = (const uint16_t *)p;
+    hipError_t e = launch_q4_dequant_dense(src, (uint16_t *)p, to_bf16 != 0, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) { destroy(w); return fail(SMG_EHIP, "q4 dequant", e); }
+    *out = w;
+    return SMG_OK;
+}
+
+void smg_weights_destroy(smg_weights *w) { destroy(w); }
+
+int smg_weights_clone(const smg_weights *w, smg_weights **out) {
+    if (!w) return fail(SMG_EINVAL, "null weights");
+    HIP_TRY(hipSetDevice(w->device), SMG_EHIP);
+    smg_weights *c = new_weights(w->d.kind, w->d.n, w->d.k, w->d.block);
+    c->d = w->d;
+    struct Field {
+        const void *src;
+        size_t bytes;
+    };
+    const size_t code_bytes = w->d.nchunks * w->d.n_pad * 16;
+    const size_t sc_bytes = w->d.sc_rows * w->d.n_pad * 2;
+    const size_t dense_bytes = w->d.n_pad * w->d.k_pad * 2;
+    const Field f[4] = {{w->d.codes, code_bytes}, {w->d.scales, sc_bytes},
+                        {w->d.mins, sc_bytes}, {w->d.dense, dense_bytes}};
+    const void **dst[4] = {(const void **)&c->d.codes, (const void **)&c->d.scales,
+                           (const void **)&c->d.mins, (const void **)&c->d.dense};
+    for (int i = 0; i < 4; i++) {
+        if (!f[i].src) continue;
+        void *p;
+        int rc = alloc_dev(c, f[i].bytes, &p);
+        if (rc) { destroy(c); return rc; }
+        hipError_t e = hipMemcpy(p, f[i].src, f[i].bytes, hipMemcpyDeviceToDevice);
+        if (e != hipSuccess) { destroy(c); return fail(SMG_EHIP, "clone copy", e); }
+        *dst[i] = p;
+    }
+    *out = c;
+    return SMG_OK;
+}
+
+int smg_weights_info(const smg_weights *w, size_t *n, size_t *k, size_t *block, size_t *bytes) {
+    if (!w) return fail(SMG_EINVAL, "null weights");
+    if (n) *n = w->d.n;
+    if (k) *k = w->d.k;
+    if (block) *block = w->d.block;
+    if (bytes) *bytes = w->bytes;
+    return SMG_OK;
+}
+
+// ---- host-pointer drop-ins -------------------------------------------------
+
+static int q4_host(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                   const ep_desc16 *ep, bool bf16) {
+    int rc = check_kind(w, W_Q4);
+    if (rc) return rc;
+    const size_t n = w->d.n, k = w->d.k;
+    if (m == 0 || n == 0) return SMG_OK;  // q4/matmul.rs:43-44
+    const WDev d = w->d;
+    return host_call(bf16 ? "gemm_gpu_b16b16_q4" : "gemm_gpu_f16f16_q4", w->device, m, n, k, dst,
+                     m * n, false, lhs, m * k, ep, 0,
+                     [&](uint16_t *dd, const uint16_t *dl, const EpArgs &ea, void *, hipStream_t s) {
+                         return run_q4(d, m, dd, dl, ea, bf16, s);
+                     });
+}
+
+int gemm_gpu_f16f16_q4(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                       const ep_desc16 *ep) {
+    return q4_host(m, w, dst, lhs, ep, false);
+}
+
+int gemm_gpu_b16b16_q4(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                       const ep_desc16 *ep) {
+    return q4_host(m, w, dst, lhs, ep, true);
+}
+
+static int lowbit_host(int kind, bool mopa, size_t m, const smg_weights *w, uint16_t *dst,
+                       const uint16_t *lhs, const ep_desc16 *ep) {
+    int rc = check_kind(w, kind);
+    if (rc) return rc;
+    const size_t n = w->d.n, k = w->d.k;
+    if (m == 0 || n == 0) return SMG_OK;  // lowbit/matmul.rs:318-324
+    const WDev d = w->d;
+    const size_t scratch = mopa ? 0 : lowbit_scratch_bytes(d, m);
+    const char *name = mopa ? (kind == W_Q2 ? "gemm_gpu_f16f16_q2" : "gemm_gpu_f16f16_q1")
+                            : (kind == W_Q2 ? "gemm_gpu_f16_q2" : "gemm_gpu_f16_q1");
+    return host_call(name, w->device, m, n, k, dst, m * n, false, lhs, m * k, ep, scratch,
+                     [&](uint16_t *dd, const uint16_t *dl, const EpArgs &ea, void *sc, hipStream_t s) {
+                         if (mopa) return launch_gemm(d, m, dd, 1, (long)n, dl, 1, (long)k, 1.0f, ea, false, s);
+                         return launch_lowbit_gemv(d, m, dd, dl, ea, sc, s);
+                     });
+}
+
+int gemm_gpu_f16_q2(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                    const ep_desc16 *ep) {
+    return lowbit_host(W_Q2, false, m, w, dst, lhs, ep);
+}
+int gemm_gpu_f16_q1(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                    const ep_desc16 *ep) {
+    return lowbit_host(W_Q1, false, m, w, dst, lhs, ep);
+}
+int gemm_gpu_f16f16_q2(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                       const ep_desc16 *ep) {
+    return lowbit_host(W_Q2, true, m, w, dst, lhs, ep);
+}
+int gemm_gpu_f16f16_q1(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                       const ep_desc16 *ep) {
+    return lowbit_host(W_Q1, true, m, w, dst, lhs, ep);
+}
+
+static int packed_host(bool bf16, size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs,
+                       long dst_rs, int read_dst, const uint16_t *lhs, long lhs_cs, long lhs_rs,
+                       const smg_weights *b, uint16_t beta_bits, const ep_desc16 *ep) {
+    int rc = check_kind(b, bf16 ? W_BF16 : W_F16);
+    if (rc) return rc;
+    if (b->d.n != n || b->d.k != k) return fail(SMG_EINVAL, "packed weights shape mismatch");
+    if (read_dst) return fail(SMG_EINVAL, "read_dst != 0 is not supported");
+    if (m == 0 || n == 0) return SMG_OK;
+    if (dst_cs <= 0 || dst_rs <= 0 || lhs_cs <= 0 || lhs_rs <= 0)
+        return fail(SMG_EINVAL, "strides must be positive");
+    const size_t dst_elems = (m - 1) * (size_t)dst_rs + (n - 1) * (size_t)dst_cs + 1;
+    const size_t lhs_elems = k ? (m - 1) * (size_t)lhs_rs + (k - 1) * (size_t)lhs_cs + 1 : 0;
+    const bool dense_out = (dst_cs == 1 && (size_t)dst_rs == n) || (dst_rs == 1 && (size_t)dst_cs == m);
+    const float beta = half_bits_to_float(beta_bits, bf16);
+    const WDev d = b->d;
+    return host_call(bf16 ? "gemm_gpu_b16b16_run_packed" : "gemm_gpu_f16f16_run_packed", b->device,
+                     m, n, k, dst, dst_elems, !dense_out, lhs, lhs_elems, ep, 0,
+                     [&](uint16_t *dd, const uint16_t *dl, const EpArgs &ea, void *, hipStream_t s) {
+                         return launch_gemm(d, m, dd, dst_cs, dst_rs, dl, lhs_cs, lhs_rs, beta, ea, bf16, s);
+                     });
+}
+
+int gemm_gpu_f16f16_run_packed(size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs,
+                               long dst_rs, int read_dst, const uint16_t *lhs, long lhs_cs,
+                               long lhs_rs, const smg_weights *b_pack, uint16_t alpha_bits,
+                               uint16_t beta_bits, const ep_desc16 *ep) {
+    (void)alpha_bits;
+    return packed_host(false, m, n, k, dst, dst_cs, dst_rs, read_dst, lhs, lhs_cs, lhs_rs, b_pack,
+                       beta_bits, ep);
+}
+
+int gemm_gpu_b16b16_run_packed(size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs,
+                               long dst_rs, int read_dst, const uint16_t *lhs, long lhs_cs,
+                               long lhs_rs, const smg_weights *b_pack, uint16_t alpha_bits,
+                               uint16_t beta_bits, const ep_desc16 *ep) {
+    (void)alpha_bits;
+    return packed_host(true, m, n, k, dst, dst_cs, dst_rs, read_dst, lhs, lhs_cs, lhs_rs, b_pack,
+                       beta_bits, ep);
+}
+
+int gemm_gpu_f16f16_q4_single(size_t m, size_t n, size_t k) {
+    (void)n;
+    (void)k;
+    return m <= Q4_GEMV_MAX_ROWS ? 1 : 0;
+}
+
+// ---- device-pointer entry points -------------------------------------------
+
+int smg_q4_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                      const ep_desc16 *ep, int bf16, void *stream) {
+    int rc = check_kind(w, W_Q4);
+    if (rc) return rc;
+    if (m == 0 || w->d.n == 0) return SMG_OK;
+    EpArgs ea;
+    if ((rc = ep_args(ep, &ea))) return rc;
+    hipError_t e = run_q4(w->d, m, dst, lhs, ea, bf16 != 0, (hipStream_t)stream);
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_q4_matmul_dev", e);
+}
+
+int smg_lowbit_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                          const ep_desc16 *ep, void *stream) {
+    if (!w) return fail(SMG_EINVAL, "null weights");
+    if (w->d.kind != W_Q2 && w->d.kind != W_Q1) return fail(SMG_EKIND, "not low-bit weights");
+    if (m == 0 || w->d.n == 0) return SMG_OK;
+    EpArgs ea;
+    int rc = ep_args(ep, &ea);
+    if (rc) return rc;
+    const size_t sb = lowbit_scratch_bytes(w->d, m);
+    void *scratch = nullptr;
+    if (sb) {
+        // huge blocks (> in-kernel pass) need a staging buffer for the
+        // pre-quantized activations: the calling thread's own
+        Ctx *c;
+        if ((rc = ctx_for(w->device, sb, &c))) return rc;
+        scratch = c->buf;
+    }
+    hipError_t e = launch_lowbit_gemv(w->d, m, dst, lhs, ea, scratch, (hipStream_t)stream);
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_lowbit_matmul_dev", e);
+}
+
+int smg_lowbit_mopa_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                        const ep_desc16 *ep, void *stream) {
+    if (!w) return fail(SMG_EINVAL, "null weights");
+    if (w->d.kind != W_Q2 && w->d.kind != W_Q1) return fail(SMG_EKIND, "not low-bit weights");
+    if (m == 0 || w->d.n == 0) return SMG_OK;
+    EpArgs ea;
+    int rc = ep_args(ep, &ea);
+    if (rc) return rc;
+    hipError_t e = launch_gemm(w->d, m, dst, 1, (long)w->d.n, lhs, 1, (long)w->d.k, 1.0f, ea,
+                               false, (hipStream_t)stream);
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_lowbit_mopa_dev", e);
+}
+
+int smg_packed_matmul_dev(size_t m, const smg_weights *b, uint16_t *dst, long dst_cs, long dst_rs,
+                          const uint16_t *lhs, long lhs_cs, long lhs_rs, uint16_t beta_bits,
+                          const ep_desc16 *ep, int bf16, void *stream) {
+    int rc = check_kind(b, bf16 ? W_BF16 : W_F16);
+    if (rc) return rc;
+    if (m == 0 || b->d.n == 0) return SMG_OK;
+    EpArgs ea;
+    if ((rc = ep_args(ep, &ea))) return rc;
+    hipError_t e = launch_gemm(b->d, m, dst, dst_cs, dst_rs, lhs, lhs_cs, lhs_rs,
+                               half_bits_to_float(beta_bits, bf16 != 0), ea, bf16 != 0,
+                               (hipStream_t)stream);
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_packed_matmul_dev", e);
+}
+
+}  // extern "C"

@@ -1,0 +1,244 @@
+// Shared device-side pieces of the gfx950 quantized-matmul library: element
+// conversions, the fused op-graph epilogue, and the device weight layouts.
+//
+// Numerics follow the reference crate's portable path exactly where it is
+// integer or rounding work (src/kernels/lowbit/matmul.rs:354-398,
+// src/exec/scalar.rs:58-140, src/epilogue/mod.rs:40-110); every file of this
+// library is compiled with -ffp-contract=off so a*b+c is never fused unless
+// written as fmaf / fma.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/smegemm_gpu.h"
+
+namespace smg {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef short short2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef short short8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef int int4_t __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// f16 / bf16 <-> f32. f32 -> f16 is the hardware RNE convert; bf16 is RNE on
+// the top half-word, NaN quieted (the `half` crate's bf16::from_f32).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float((uint32_t)h << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    uint32_t lsb = (u >> 16) & 1u;
+    return (uint16_t)((u + 0x7fffu + lsb) >> 16);
+}
+template <bool BF16>
+__device__ __forceinline__ float to_f32(uint16_t h) {
+    return BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+template <bool BF16>
+__device__ __forceinline__ uint16_t from_f32(float x) {
+    return BF16 ? f32_to_bf16(x) : f32_to_f16(x);
+}
+
+// f64 -> f16 with a single RNE rounding (half::f16::from_f64): round to f32
+// with round-to-odd (f32 keeps 13 more bits than f16, so the later RNE step
+// cannot double-round), then the hardware f32 -> f16 RNE convert.
+__device__ __forceinline__ uint16_t f64_to_f16(double x) {
+    float f = (float)x;
+    double back = (double)f;
+    if (back != x && x == x) {
+        uint32_t u = __float_as_uint(f);
+        if (fabs(back) > fabs(x)) u -= 1u;  // step toward zero (same sign)
+        u |= 1u;
+        f = __uint_as_float(u);
+    }
+    return f32_to_f16(f);
+}
+
+// ---------------------------------------------------------------------------
+// Epilogue (src/exec/scalar.rs:58-140). The node list travels by value in the
+// kernel arguments; operand pointers are device pointers to T (f16/bf16).
+// ---------------------------------------------------------------------------
+struct EpArgs {
+    uint32_t n_nodes;
+    uint32_t pad;
+    EpNode nodes[SMG_MAX_EP_NODES];
+};
+
+// maxNum / minNum with IEEE 754-2019 maximumNumber / minimumNumber results: a
+// NaN operand yields the other operand and -0 < +0 (the AArch64 FMAXNM /
+// FMINNM answer; the sign of a zero max is otherwise unspecified by Rust).
+__device__ __forceinline__ double maxnumd(double x, double y) {
+    if (x != x) return y;
+    if (y != y) return x;
+    if (x == 0.0 && y == 0.0) return (signbit(x) && signbit(y)) ? -0.0 : 0.0;
+    return x > y ? x : y;
+}
+__device__ __forceinline__ float maxnumf(float x, float y) {
+    if (x != x) return y;
+    if (y != y) return x;
+    if (x == 0.0f && y == 0.0f) return (signbit(x) && signbit(y)) ? -0.0f : 0.0f;
+    return x > y ? x : y;
+}
+__device__ __forceinline__ float minnumf(float x, float y) {
+    if (x != x) return y;
+    if (y != y) return x;
+    if (x == 0.0f && y == 0.0f) return (signbit(x) || signbit(y)) ? -0.0f : 0.0f;
+    return x < y ? x : y;
+}
+
+__device__ __forceinline__ double clampd(double x, double lo, double hi) {
+    if (x < lo) x = lo;
+    if (x > hi) x = hi;
+    return x;
+}
+
+// act_apply_f64_a (src/epilogue/mod.rs:40-84), evaluated in f64 with the
+// same operation order as the Rust expressions.
+__device__ __noinline__ double act_f64(uint32_t kind, double x, double alpha) {
+    switch (kind) {
+    case 1: return maxnumd(x, 0.0);
+    case 2: {
+        double inner = 0.7978845608028654 * (x + 0.044715 * x * x * x);
+        return 0.5 * x * (1.0 + tanh(inner));
+    }
+    case 3: return x / (1.0 + exp(-x));
+    case 4: return tanh(x);
+    case 5: return 1.0 / (1.0 + exp(-x));
+    case 6: return x >= 0.0 ? x : alpha * x;
+    case 7: return clampd(x, 0.0, 6.0);
+    case 8: return clampd(x / 6.0 + 0.5, 0.0, 1.0);
+    case 9: return x * clampd(x / 6.0 + 0.5, 0.0, 1.0);
+    case 10: return fabs(x);
+    case 11: return -x;
+    case 12: return x * x;
+    case 13: return x > 0.0 ? 1.0 : (x < 0.0 ? -1.0 : 0.0);
+    case 14: return sqrt(x);
+    case 15: return x / (1.0 + fabs(x));
+    case 16: return 1.0 / x;
+    case 17: return 1.0 / sqrt(x);
+    case 18: return exp(x);
+    case 19: return log(x);
+    case 20: return x >= 0.0 ? x : alpha * expm1(x);
+    case 21: return 1.0507009873554805 * (x >= 0.0 ? x : 1.6732632423543772 * expm1(x));
+    case 22: return maxnumd(x, 0.0) + log1p(exp(-fabs(x)));
+    case 23: return x * tanh(maxnumd(x, 0.0) + log1p(exp(-fabs(x))));
+    case 24: {
+        // erf via Abramowitz-Stegun 7.1.26 (src/epilogue/mod.rs:86-95)
+        double xe = x * 0.70710678118654752440;
+        double ax = fabs(xe);
+        double t = 1.0 / (1.0 + 0.3275911 * ax);
+        double poly =
+            ((((1.061405429 * t - 1.453152027) * t + 1.421413741) * t - 0.284496736) * t +
+             0.254829592) *
+            t;
+        double e = 1.0 - poly * exp(-ax * ax);
+        double erfv = xe < 0.0 ? -e : e;
+        return 0.5 * x * (1.0 + erfv);
+    }
+    default: return x;
+    }
+}
+
+__device__ __forceinline__ float act_f32(uint32_t kind, float x, float alpha) {
+    return (float)act_f64(kind, (double)x, (double)alpha);
+}
+
+// One cell of the op-graph: x is the f32 value of the already-rounded GEMM
+// output; (i, j) its row and column; n the row length used when a TENSOR
+// node's ld is 0. Nodes apply in order (the trailing activation is the last
+// node, as resolve_nodes appends it: src/exec/scalar.rs:28-53).
+template <bool BF16>
+__device__ float ep_cell(const EpArgs &ep, float x, size_t i, size_t j, size_t n) {
+    for (uint32_t t = 0; t < ep.n_nodes; t++) {
+        const EpNode &nd = ep.nodes[t];
+        const uint16_t *p = (const uint16_t *)nd.ptr;
+        uint32_t op = nd.op;
+        float v = 0.0f;
+        // operand fetch by class: ROW ops read p[i], COL ops p[j], TENSOR p[i*ld+j]
+        switch (op) {
+        case EP_OP_ADD_ROW: case EP_OP_MUL_ROW: case EP_OP_SUB_ROW: case EP_OP_DIV_ROW:
+        case EP_OP_MAX_ROW: case EP_OP_MIN_ROW:
+            v = to_f32<BF16>(p[i]);
+            break;
+        case EP_OP_ADD_COL: case EP_OP_MUL_COL: case EP_OP_SUB_COL: case EP_OP_DIV_COL:
+        case EP_OP_MAX_COL: case EP_OP_MIN_COL:
+            v = to_f32<BF16>(p[j]);
+            break;
+        case EP_OP_ADD_TENSOR: case EP_OP_MUL_TENSOR: case EP_OP_SUB_TENSOR:
+        case EP_OP_DIV_TENSOR: case EP_OP_MAX_TENSOR: case EP_OP_MIN_TENSOR: {
+            size_t ld = nd.ld == 0 ? n : nd.ld;
+            v = to_f32<BF16>(p[i * ld + j]);
+            break;
+        }
+        default: v = nd.scalar; break;
+        }
+        switch (op) {
+        case EP_OP_ADD_SCALAR: case EP_OP_ADD_ROW: case EP_OP_ADD_COL: case EP_OP_ADD_TENSOR:
+            x = x + v; break;
+        case EP_OP_MUL_SCALAR: case EP_OP_MUL_ROW: case EP_OP_MUL_COL: case EP_OP_MUL_TENSOR:
+            x = x * v; break;
+        case EP_OP_SUB_SCALAR: case EP_OP_SUB_ROW: case EP_OP_SUB_COL: case EP_OP_SUB_TENSOR:
+            x = x - v; break;
+        case EP_OP_DIV_SCALAR: case EP_OP_DIV_ROW: case EP_OP_DIV_COL: case EP_OP_DIV_TENSOR:
+            x = __fdiv_rn(x, v); break;
+        case EP_OP_MAX_SCALAR: case EP_OP_MAX_ROW: case EP_OP_MAX_COL: case EP_OP_MAX_TENSOR:
+            x = maxnumf(x, v); break;
+        case EP_OP_MIN_SCALAR: case EP_OP_MIN_ROW: case EP_OP_MIN_COL: case EP_OP_MIN_TENSOR:
+            x = minnumf(x, v); break;
+        case EP_OP_ACT:
+            x = act_f32(nd.aux, x, nd.scalar); break;
+        default: break;
+        }
+    }
+    return x;
+}
+
+// Final store of one output: round the accumulator-derived value to T, then
+// (iff the graph is non-empty) run the graph in f32 on that rounded value and
+// round again -- "GEMM to T, then apply_ep_scalar" (src/exec/macros.rs:188-206).
+template <bool BF16>
+__device__ __forceinline__ uint16_t finish(const EpArgs &ep, float acc, size_t i, size_t j,
+                                           size_t n) {
+    uint16_t c = from_f32<BF16>(acc);
+    if (ep.n_nodes == 0) return c;
+    return from_f32<BF16>(ep_cell<BF16>(ep, to_f32<BF16>(c), i, j, n));
+}
+
+// ---------------------------------------------------------------------------
+// Device weight layouts (this library's own; the reference's band-major
+// arrays are repacked into these at upload).
+//
+// Q4 ("chunk-major"): K is cut into chunks of 32 depths (16 bytes). Chunk kc of
+// column j sits at byte (kc*n_pad + j)*16, so a wave reading consecutive
+// columns of one chunk reads one contiguous run. Inside a chunk, dword w
+// (depths 8w..8w+7) holds depth 8w+2e at bits 4e..4e+3 and depth 8w+2e+1 at
+// bits 16+4e..16+4e+3 (e = 0..3), so ((dword >> 4e) & 0x000F000F) yields the
+// consecutive pair (8w+2e, 8w+2e+1) in two half-words. The stored nibble is
+// the reference's nibble (code two's complement, q4/mod.rs:213-214).
+// Scales (and mins): row kb = d/block of an [n_sc_rows][n_pad] f16 array.
+//
+// Q2: chunks of 64 depths (16 bytes) at (kc*n_pad + j)*16; dword w holds
+// depths 16w..16w+15 with depth 16w+4i+b at byte b, bits 2i..2i+1, so
+// ((dword >> 2i) & 0x03030303) gives the codes of depths 16w+4i..+3 as bytes.
+// Q1: chunks of 128 depths; dword w holds depths 32w..32w+31 with depth
+// 32w+4i+b at byte b, bit i, so ((dword >> i) & 0x01010101) gives the sign
+// bits of depths 32w+4i..+3 as 0/1 bytes.
+// Low-bit scales: [nbk][n_pad] f16.
+// ---------------------------------------------------------------------------
+constexpr int Q4_CHUNK = 32;   // depths per 16-byte Q4 chunk
+constexpr int Q2_CHUNK = 64;   // depths per 16-byte Q2 chunk
+constexpr int Q1_CHUNK = 128;  // depths per 16-byte Q1 chunk
+
+}  // namespace smg

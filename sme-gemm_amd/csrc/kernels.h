@@ -1,0 +1,50 @@
+// Host-side launch interface between the C ABI (api.hip) and the kernel
+// translation units. Internal to the library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "common.cuh"
+
+namespace smg {
+
+enum WKind { W_Q4 = 4, W_Q2 = 2, W_Q1 = 1, W_F16 = 16, W_BF16 = 17 };
+
+// Device view of a weight set (layouts: common.cuh).
+struct WDev {
+    int kind;
+    size_t n, k, block;
+    size_t n_pad;     // columns padded to a multiple of 64
+    size_t nchunks;   // chunks along K (Q4: 32 depths, Q2: 64, Q1: 128)
+    size_t sc_rows;   // rows of the scale array
+    const uint8_t *codes;   // Q4 nibbles / Q2 codes / Q1 signs
+    const uint16_t *scales;
+    const uint16_t *mins;   // Q4 affine only
+    uint32_t codebook;      // Q2: the 4 int8 values, byte c = value of code c
+    const uint16_t *dense;  // F16/BF16: [n_pad][k_pad] (column j's K contiguous)
+    size_t k_pad;           // dense: K padded to a multiple of 64
+};
+
+// Rows at or below which the Q4 path runs the GEMV kernel.
+constexpr size_t Q4_GEMV_MAX_ROWS = 8;
+
+hipError_t launch_q4_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
+                          const EpArgs &ep, bool bf16, hipStream_t s);
+
+// Low-bit int8 path. scratch: device buffer of lowbit_scratch_bytes() bytes
+// (only used when the block is too large to quantize in-kernel).
+size_t lowbit_scratch_bytes(const WDev &w, size_t m);
+hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
+                              const EpArgs &ep, void *scratch, hipStream_t s);
+
+// MFMA GEMM over any weight kind (Q4 / Q2 / Q1 dequantized to f16/bf16 in LDS,
+// or dense), C[i,j] at dst[i*rs + j*cs] = ep(to16(beta * acc)).
+hipError_t launch_gemm(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,
+                       const uint16_t *lhs, long lhs_cs, long lhs_rs, float beta,
+                       const EpArgs &ep, bool bf16, hipStream_t s);
+
+// Device-side repacks / dequant.
+hipError_t launch_q4_dequant_dense(const WDev &q4, uint16_t *dense, bool to_bf16,
+                                   hipStream_t s);
+
+}  // namespace smg

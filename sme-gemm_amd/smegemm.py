@@ -1,0 +1,689 @@
+"""Python mirror of the reference crate's quantized-matmul API over the gfx950
+C ABI (``include/smegemm_gpu.h`` -> ``libsmegemm_gpu.so``).
+
+Names, argument meaning and panics follow the Rust API this path replaces:
+``Q4Params``/``Q4Weights``/``matmul_q4*`` (src/kernels/q4/), ``Q2Params``/
+``Q2Weights``/``Q1Weights``/``matmul_q{1,2}{,_ep,_mopa,_mopa_ep}``
+(src/kernels/lowbit/), ``Epilogue`` (src/epilogue/graph.rs), ``prepack_f16``/
+``Packed`` and the ``Gemm`` builder (src/exec/builder.rs). Length checks raise
+``ValueError`` where the Rust code panics.
+
+Arrays are f16/bf16 bit patterns (``np.uint16``) in host memory, or torch CUDA
+tensors (int16/float16/bfloat16) for the asynchronous device-pointer entry
+points, which run on torch's current stream. There is no CPU fallback: when the
+library or a gfx950 device is missing every call raises ``SmeGemmError``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIBPATH = os.path.join(_HERE, "libsmegemm_gpu.so")
+_lib = None
+
+P = C.c_void_p
+SZ = C.c_size_t
+
+Q4_BLOCK = 32          # src/kernels/q4/mod.rs:34
+Q2_BLOCK = 256         # src/kernels/lowbit/mod.rs:26
+Q2_TERNARY = (-1, 0, 1, 0)  # src/kernels/lowbit/mod.rs:30
+
+
+class SmeGemmError(RuntimeError):
+    pass
+
+
+def build() -> None:
+    """Compile the HIP library for gfx950 in-tree."""
+    subprocess.run(["make", "-s", "-C", _HERE, "-j8"], check=True)
+
+
+def lib() -> C.CDLL:
+    """The loaded C ABI. Raises if the library has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIBPATH):
+        raise SmeGemmError(f"{_LIBPATH} is not built (run make -C {_HERE})")
+    L = C.CDLL(_LIBPATH)
+    W = C.POINTER(C.c_void_p)
+    L.smg_available.restype = C.c_int
+    L.smg_last_error.restype = C.c_char_p
+    L.smg_q4_gemv_max_rows.restype = SZ
+    L.smg_q4_create.argtypes = [P, P, P, SZ, SZ, SZ, W]
+    L.smg_q4_create_band.argtypes = [P, P, P, SZ, SZ, SZ, W]
+    L.smg_q2_create.argtypes = [P, P, P, SZ, SZ, SZ, W]
+    L.smg_q2_create_band.argtypes = [P, P, P, SZ, SZ, SZ, W]
+    L.smg_q1_create.argtypes = [P, P, C.c_int, SZ, SZ, SZ, W]
+    L.smg_q1_create_band.argtypes = [P, P, SZ, SZ, SZ, W]
+    L.smg_f16_prepack.argtypes = [P, SZ, SZ, C.c_long, C.c_long, W]
+    L.smg_bf16_prepack.argtypes = [P, SZ, SZ, C.c_long, C.c_long, W]
+    L.smg_q4_dequant.argtypes = [P, C.c_int, W]
+    L.smg_weights_clone.argtypes = [P, W]
+    L.smg_weights_destroy.argtypes = [P]
+    L.smg_weights_destroy.restype = None
+    L.smg_weights_info.argtypes = [P, C.POINTER(SZ), C.POINTER(SZ), C.POINTER(SZ), C.POINTER(SZ)]
+    for name in ("gemm_gpu_f16f16_q4", "gemm_gpu_b16b16_q4", "gemm_gpu_f16_q2", "gemm_gpu_f16_q1",
+                 "gemm_gpu_f16f16_q2", "gemm_gpu_f16f16_q1"):
+        getattr(L, name).argtypes = [SZ, P, P, P, P]
+    for name in ("gemm_gpu_f16f16_run_packed", "gemm_gpu_b16b16_run_packed"):
+        getattr(L, name).argtypes = [SZ, SZ, SZ, P, C.c_long, C.c_long, C.c_int, P, C.c_long,
+                                     C.c_long, P, C.c_uint16, C.c_uint16, P]
+    L.gemm_gpu_f16f16_q4_single.argtypes = [SZ, SZ, SZ]
+    L.smg_q4_matmul_dev.argtypes = [SZ, P, P, P, P, C.c_int, P]
+    L.smg_lowbit_matmul_dev.argtypes = [SZ, P, P, P, P, P]
+    L.smg_lowbit_mopa_dev.argtypes = [SZ, P, P, P, P, P]
+    L.smg_packed_matmul_dev.argtypes = [SZ, P, P, C.c_long, C.c_long, P, C.c_long, C.c_long,
+                                        C.c_uint16, P, C.c_int, P]
+    _lib = L
+    return L
+
+
+def available() -> bool:
+    try:
+        return bool(lib().smg_available())
+    except (OSError, SmeGemmError):
+        return False
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise SmeGemmError(f"{what} failed (rc={rc}): {lib().smg_last_error().decode()}")
+
+
+def _require_device() -> None:
+    if not lib().smg_available():
+        raise SmeGemmError("no gfx950 device: the HIP path is required (there is no CPU fallback)")
+
+
+# ---- array plumbing ---------------------------------------------------------
+
+def _is_dev(x) -> bool:
+    return hasattr(x, "is_cuda") and x.is_cuda
+
+
+def _host16(x, n: int, what: str) -> np.ndarray:
+    a = np.ascontiguousarray(x)
+    if a.dtype != np.uint16:
+        if a.dtype == np.float16:
+            a = a.view(np.uint16)
+        else:
+            raise TypeError(f"{what}: expected uint16 bit patterns or float16")
+    if a.size != n:
+        raise ValueError(f"{what} has {a.size} elements, expected {n}")
+    return a
+
+
+def _ptr(a) -> int:
+    if _is_dev(a):
+        return a.data_ptr()
+    return a.ctypes.data
+
+
+def _stream() -> int:
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+# ---- epilogue ---------------------------------------------------------------
+
+EP_ACT = dict(relu=1, gelu=2, silu=3, tanh=4, sigmoid=5, leaky_relu=6, relu6=7, hardsigmoid=8,
+              hardswish=9, abs=10, neg=11, square=12, sign=13, sqrt=14, softsign=15, recip=16,
+              rsqrt=17, exp=18, log=19, elu=20, selu=21, softplus=22, mish=23, gelu_exact=24)
+EP_OP = dict(add_scalar=0, mul_scalar=1, add_row=2, mul_row=3, add_col=4, mul_col=5,
+             add_tensor=6, mul_tensor=7, act=8, max_scalar=9, min_scalar=10, sub_scalar=11,
+             sub_row=12, sub_col=13, sub_tensor=14, div_scalar=15, div_row=16, div_col=17,
+             div_tensor=18, max_row=19, max_col=20, max_tensor=21, min_row=22, min_col=23,
+             min_tensor=24)
+_ROW = {2, 3, 12, 16, 19, 22}
+_COL = {4, 5, 13, 17, 20, 23}
+_TENSOR = {6, 7, 14, 18, 21, 24}
+
+
+class EpNode(C.Structure):
+    """csrc/epilogue.h:214-221 (32 bytes)."""
+    _fields_ = [("op", C.c_uint32), ("aux", C.c_uint32), ("scalar", C.c_float),
+                ("ptr", C.c_void_p), ("ld", C.c_size_t)]
+
+
+class EpDesc16(C.Structure):
+    _fields_ = [("n_nodes", C.c_uint32), ("nodes", C.POINTER(EpNode))]
+
+
+def _bf16_round(x: float) -> float:
+    """f32 -> bf16 RNE -> f32 (NaN kept)."""
+    u = int(np.float32(x).view(np.uint32))
+    if (u & 0x7FFFFFFF) > 0x7F800000:
+        return float(np.float32(x))
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return float(np.uint32(u).view(np.float32))
+
+
+def _scalar_to_f32(v, bf16: bool) -> float:
+    """A scalar operand is stored as `v.ep_to_f32()` of a T (graph.rs:86-96):
+    pass either a float (rounded to T here) or T's bit pattern as an int."""
+    if isinstance(v, (np.uint16, int)) and not isinstance(v, bool):
+        if bf16:
+            return float(np.uint32(int(v) << 16).view(np.float32))
+        return float(np.uint16(v).view(np.float16))
+    return _bf16_round(v) if bf16 else float(np.float16(v))
+
+
+class Epilogue:
+    """The ordered op-graph builder (src/epilogue/graph.rs:33). Operands are
+    uint16 f16/bf16 bit arrays (host) or CUDA tensors (device calls).
+    Named activations (.relu/.gelu/.silu/.tanh/.sigmoid) set the trailing
+    activation, applied last; the others push in-order nodes."""
+
+    def __init__(self, bf16: bool = False):
+        self.bf16 = bf16  # element type T of the operands: f16 (default) or bf16
+        self.nodes = []   # (op, aux, scalar, operand, ld)
+        self.act = None
+
+    def _scalar(self, op, v):
+        self.nodes.append((op, 0, _scalar_to_f32(v, self.bf16), None, 0))
+        return self
+
+    def _vec(self, op, v, ld=0):
+        self.nodes.append((op, 0, 0.0, v, ld))
+        return self
+
+    def _push_act(self, kind, alpha=0.0):
+        self.nodes.append((8, kind, float(np.float32(alpha)), None, 0))
+        return self
+
+    # scalar / vector ops (graph.rs:103-331)
+    def add_scalar(self, v): return self._scalar(0, v)
+    def mul_scalar(self, v): return self._scalar(1, v)
+    def sub_scalar(self, v): return self._scalar(11, v)
+    def div_scalar(self, v): return self._scalar(15, v)
+    def max(self, lo): return self._scalar(9, lo)
+    def min(self, hi): return self._scalar(10, hi)
+    def clamp(self, lo, hi): return self.max(lo).min(hi)
+    def add_row(self, r): return self._vec(2, r)
+    def mul_row(self, r): return self._vec(3, r)
+    def sub_row(self, r): return self._vec(12, r)
+    def div_row(self, r): return self._vec(16, r)
+    def max_row(self, r): return self._vec(19, r)
+    def min_row(self, r): return self._vec(22, r)
+    def add_col(self, c): return self._vec(4, c)
+    def mul_col(self, c): return self._vec(5, c)
+    def sub_col(self, c): return self._vec(13, c)
+    def div_col(self, c): return self._vec(17, c)
+    def max_col(self, c): return self._vec(20, c)
+    def min_col(self, c): return self._vec(23, c)
+    def add_tensor(self, t, ld=0): return self._vec(6, t, ld)
+    def mul_tensor(self, t, ld=0): return self._vec(7, t, ld)
+    def sub_tensor(self, t, ld=0): return self._vec(14, t, ld)
+    def div_tensor(self, t, ld=0): return self._vec(18, t, ld)
+    def max_tensor(self, t, ld=0): return self._vec(21, t, ld)
+    def min_tensor(self, t, ld=0): return self._vec(24, t, ld)
+    add_tensor_strided = add_tensor
+    mul_tensor_strided = mul_tensor
+
+    # trailing activations (graph.rs:193-223)
+    def relu(self): self.act = 1; return self
+    def gelu(self): self.act = 2; return self
+    def silu(self): self.act = 3; return self
+    def tanh(self): self.act = 4; return self
+    def sigmoid(self): self.act = 5; return self
+
+    # in-order activation nodes (graph.rs:334-431)
+    def leaky_relu(self, alpha): return self._push_act(6, alpha)
+    def relu6(self): return self._push_act(7)
+    def hardsigmoid(self): return self._push_act(8)
+    def hardswish(self): return self._push_act(9)
+    def abs(self): return self._push_act(10)
+    def neg(self): return self._push_act(11)
+    def square(self): return self._push_act(12)
+    def sign(self): return self._push_act(13)
+    def sqrt(self): return self._push_act(14)
+    def softsign(self): return self._push_act(15)
+    def recip(self): return self._push_act(16)
+    def rsqrt(self): return self._push_act(17)
+    def exp(self): return self._push_act(18)
+    def log(self): return self._push_act(19)
+    def elu(self, alpha): return self._push_act(20, alpha)
+    def selu(self): return self._push_act(21)
+    def softplus(self): return self._push_act(22)
+    def mish(self): return self._push_act(23)
+    def gelu_exact(self): return self._push_act(24)
+
+    def is_empty(self) -> bool:
+        return not self.nodes and self.act is None
+
+    def validate(self, m: int, n: int) -> None:
+        """validate_ep (src/exec/guard.rs:112-147)."""
+        for op, _aux, _s, v, ld in self.nodes:
+            length = None if v is None else (v.numel() if _is_dev(v) else np.asarray(v).size)
+            if op in _ROW and length != m:
+                raise ValueError("row operand is per-M (length m)")
+            if op in _COL and length != n:
+                raise ValueError("col operand is per-N (length n)")
+            if op in _TENSOR:
+                eld = n if ld == 0 else ld
+                if eld < n:
+                    raise ValueError("tensor row stride must be >= n")
+                if m != 0 and length < (m - 1) * eld + n:
+                    raise ValueError("tensor must hold m*n elements (stride ld)")
+
+    def desc(self, n: int):
+        """resolve_nodes (src/exec/scalar.rs:28-53): tensor ld 0 -> n, the
+        trailing activation appended as a final ACT node. Returns
+        (EpDesc16 or None, keepalive)."""
+        nodes = []
+        keep = []
+        for op, aux, scalar, v, ld in self.nodes:
+            ptr = None
+            if v is not None:
+                if not _is_dev(v):
+                    v = np.ascontiguousarray(v).view(np.uint16) if np.asarray(v).dtype in (
+                        np.float16, np.uint16) else np.ascontiguousarray(v, dtype=np.uint16)
+                keep.append(v)
+                ptr = _ptr(v)
+            if op in _TENSOR and ld == 0:
+                ld = n
+            nodes.append(EpNode(op, aux, scalar, ptr, ld))
+        if self.act is not None:
+            nodes.append(EpNode(8, self.act, 0.0, None, 0))
+        if not nodes:
+            return None, keep
+        arr = (EpNode * len(nodes))(*nodes)
+        keep.append(arr)
+        d = EpDesc16(len(nodes), C.cast(arr, C.POINTER(EpNode)))
+        keep.append(d)
+        return d, keep
+
+
+def _ep_ptr(ep, n):
+    if ep is None:
+        return None, []
+    d, keep = ep.desc(n)
+    return (None if d is None else C.addressof(d)), keep
+
+
+# ---- weight handles -----------------------------------------------------------
+
+class _Handle:
+    def __init__(self, h: C.c_void_p, n: int, k: int):
+        self._h = h
+        self._n = n
+        self._k = k
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.smg_weights_destroy(h)
+            self._h = None
+
+    def n(self) -> int:
+        return self._n
+
+    def k(self) -> int:
+        return self._k
+
+    def clone(self):
+        """Another device copy of the same weights (device-to-device)."""
+        import copy
+        h = C.c_void_p()
+        _check(lib().smg_weights_clone(self._h, C.byref(h)), "smg_weights_clone")
+        c = copy.copy(self)
+        c._h = h
+        return c
+
+    def device_bytes(self) -> int:
+        b = SZ()
+        _check(lib().smg_weights_info(self._h, None, None, None, C.byref(b)), "smg_weights_info")
+        return b.value
+
+
+class Q4Params:
+    """src/kernels/q4/mod.rs:56-103."""
+
+    def __init__(self, block: int = Q4_BLOCK):
+        if block <= 0 or block & (block - 1):
+            raise ValueError(f"q4 block size must be a power of two, got {block}")
+        self._block = block
+        self._affine = False
+
+    def affine(self) -> "Q4Params":
+        p = Q4Params(self._block)
+        p._affine = True
+        return p
+
+    def block(self) -> int:
+        return self._block
+
+    def is_affine(self) -> bool:
+        return self._affine
+
+
+def _u8(x) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.uint8)
+
+
+class Q4Weights(_Handle):
+    """Q4 weights kept 4-bit resident on the device (src/kernels/q4/weights.rs:26)."""
+
+    def __init__(self, quants, scales, n: int, k: int, params: Q4Params | None = None,
+                 mins=None, _band=False):
+        p = params or Q4Params()
+        nbk = -(-k // p.block())
+        quants = _u8(quants)
+        scales = _host16(scales, (n * nbk) if not _band else scales.size, "scales")
+        if p.is_affine() != (mins is not None):
+            raise ValueError("Q4Form::Affine requires a mins array" if p.is_affine()
+                             else "Q4Form::Scale takes no mins array")
+        if mins is not None:
+            mins = _host16(mins, scales.size, "mins")
+        if not _band and quants.size != -(-(k * n) // 2):
+            raise ValueError("quants is ceil(k*n/2) bytes")
+        _require_device()
+        h = C.c_void_p()
+        fn = lib().smg_q4_create_band if _band else lib().smg_q4_create
+        _check(fn(_ptr(quants), _ptr(scales), None if mins is None else _ptr(mins), n, k,
+                  p.block(), C.byref(h)), "smg_q4_create")
+        super().__init__(h, n, k)
+        self._params = p
+
+    @classmethod
+    def new(cls, quants, scales, n, k):
+        return cls(quants, scales, n, k)
+
+    @classmethod
+    def with_params(cls, quants, scales, mins, n, k, p: Q4Params):
+        return cls(quants, scales, n, k, p, mins)
+
+    @classmethod
+    def from_band(cls, nibbles, scales, mins, n, k, p: Q4Params):
+        """From the reference's band-major resident arrays (what src/ffi.rs passes)."""
+        return cls(nibbles, scales, n, k, p, mins, _band=True)
+
+    def params(self) -> Q4Params:
+        return self._params
+
+
+class Q2Params:
+    """src/kernels/lowbit/mod.rs:38-94."""
+
+    def __init__(self, block: int = Q2_BLOCK):
+        if block & (block - 1) or not (16 <= block <= 1 << 16):
+            raise ValueError(f"q2 block size must be a power of two from 16 to 65536, got {block}")
+        self._block = block
+        self._codebook = tuple(Q2_TERNARY)
+
+    def with_codebook(self, values) -> "Q2Params":
+        p = Q2Params(self._block)
+        p._codebook = tuple(int(v) for v in values)
+        return p
+
+    def block(self) -> int:
+        return self._block
+
+    def codebook(self):
+        return self._codebook
+
+
+class WeightLayout:
+    OutIn = 0
+    InOut = 1
+
+
+class Q2Weights(_Handle):
+    """2-bit weights resident on the device (src/kernels/lowbit/q2.rs:31)."""
+
+    def __init__(self, codes, scales, n: int, k: int, p: Q2Params | None = None, _band=False):
+        p = p or Q2Params()
+        nbk = -(-k // p.block())
+        codes = _u8(codes)
+        if not _band and codes.size != -(-(k * n) // 4):
+            raise ValueError("codes is ceil(k*n/4) bytes")
+        scales = _host16(scales, (n * nbk) if not _band else scales.size, "scales")
+        cb = np.asarray(p.codebook(), np.int8)
+        _require_device()
+        h = C.c_void_p()
+        fn = lib().smg_q2_create_band if _band else lib().smg_q2_create
+        _check(fn(_ptr(codes), _ptr(scales), _ptr(cb), n, k, p.block(), C.byref(h)),
+               "smg_q2_create")
+        super().__init__(h, n, k)
+        self._params = p
+
+    @classmethod
+    def from_band(cls, codes, scales, n, k, p: Q2Params):
+        return cls(codes, scales, n, k, p, _band=True)
+
+    def params(self) -> Q2Params:
+        return self._params
+
+
+class Q1Weights(_Handle):
+    """1-bit weights resident on the device (src/kernels/lowbit/q1.rs:23)."""
+
+    def __init__(self, signs, scales, layout: int, n: int, k: int, block: int, _band=False):
+        if block & (block - 1) or not (16 <= block <= 1 << 16):
+            raise ValueError(f"q1 block size must be a power of two from 16 to 65536, got {block}")
+        nbk = -(-k // block)
+        signs = _u8(signs)
+        if not _band and signs.size != -(-(k * n) // 8):
+            raise ValueError("signs is ceil(k*n/8) bytes")
+        scales = _host16(scales, (n * nbk) if not _band else scales.size, "scales")
+        _require_device()
+        h = C.c_void_p()
+        if _band:
+            rc = lib().smg_q1_create_band(_ptr(signs), _ptr(scales), n, k, block, C.byref(h))
+        else:
+            rc = lib().smg_q1_create(_ptr(signs), _ptr(scales), int(layout), n, k, block,
+                                     C.byref(h))
+        _check(rc, "smg_q1_create")
+        super().__init__(h, n, k)
+        self._block = block
+
+    @classmethod
+    def from_band(cls, signs, scales, n, k, block):
+        return cls(signs, scales, 0, n, k, block, _band=True)
+
+    def block(self) -> int:
+        return self._block
+
+
+class Packed(_Handle):
+    """Packed<f16> / Packed<bf16> (src/element.rs:87) held on the device."""
+
+    def __init__(self, h, n, k, bf16):
+        super().__init__(h, n, k)
+        self.bf16 = bf16
+
+
+def prepack_f16(b, n: int, k: int) -> Packed:
+    """prepack_f16 (src/kernels/f16.rs:212): b is row-major k x n."""
+    b = _host16(b, k * n, "b")
+    _require_device()
+    h = C.c_void_p()
+    _check(lib().smg_f16_prepack(_ptr(b), n, k, n, 1, C.byref(h)), "smg_f16_prepack")
+    return Packed(h, n, k, False)
+
+
+def prepack_bf16(b, n: int, k: int) -> Packed:
+    b = _host16(b, k * n, "b")
+    _require_device()
+    h = C.c_void_p()
+    _check(lib().smg_bf16_prepack(_ptr(b), n, k, n, 1, C.byref(h)), "smg_bf16_prepack")
+    return Packed(h, n, k, True)
+
+
+def _dequant(w: Q4Weights, bf16: bool) -> Packed:
+    h = C.c_void_p()
+    _check(lib().smg_q4_dequant(w._h, int(bf16), C.byref(h)), "smg_q4_dequant")
+    return Packed(h, w.n(), w.k(), bf16)
+
+
+def dequant_q4(quants, scales, n, k) -> Packed:
+    """dequant_q4 (src/kernels/q4/mod.rs:145): eager dequant on the device."""
+    return _dequant(Q4Weights(quants, scales, n, k), False)
+
+
+def dequant_q4_with(quants, scales, mins, n, k, p: Q4Params) -> Packed:
+    return _dequant(Q4Weights(quants, scales, n, k, p, mins), False)
+
+
+def dequant_q4_bf16(quants, scales, n, k) -> Packed:
+    return _dequant(Q4Weights(quants, scales, n, k), True)
+
+
+def dequant_q4_bf16_with(quants, scales, mins, n, k, p: Q4Params) -> Packed:
+    return _dequant(Q4Weights(quants, scales, n, k, p, mins), True)
+
+
+# ---- matmuls --------------------------------------------------------------------
+
+def _run_host_or_dev(name_host, dev_fn, a, w, c, m, ep, extra_dev=()):
+    n, k = w.n(), w.k()
+    ep = ep or Epilogue()
+    if (_is_dev(a)) != (_is_dev(c)):
+        raise ValueError("a and c must both be host arrays or both device tensors")
+    if _is_dev(a):
+        if a.numel() != m * k:
+            raise ValueError("a is m*k")
+        if c.numel() != m * n:
+            raise ValueError("c is m*n")
+        ep.validate(m, n)
+        eptr, keep = _ep_ptr(ep, n)
+        _check(dev_fn(m, w._h, c.data_ptr(), a.data_ptr(), eptr, *extra_dev, _stream()), name_host)
+        return c
+    a = _host16(a, m * k, "a")
+    if not isinstance(c, np.ndarray) or c.dtype not in (np.uint16, np.float16) or c.size != m * n:
+        raise ValueError("c is m*n (uint16/float16 numpy array)")
+    if not c.flags["C_CONTIGUOUS"]:
+        raise ValueError("c must be contiguous")
+    ep.validate(m, n)
+    eptr, keep = _ep_ptr(ep, n)
+    _check(getattr(lib(), name_host)(m, w._h, c.ctypes.data, a.ctypes.data, eptr), name_host)
+    return c
+
+
+def matmul_q4_ep(a, w: Q4Weights, c, m: int, ep: Epilogue):
+    """src/kernels/q4/matmul.rs:21."""
+    return _run_host_or_dev("gemm_gpu_f16f16_q4", lambda *x: lib().smg_q4_matmul_dev(*x[:5], 0, x[5]),
+                            a, w, c, m, ep)
+
+
+def matmul_q4(a, w: Q4Weights, c, m: int):
+    return matmul_q4_ep(a, w, c, m, Epilogue())
+
+
+def matmul_q4_bf16_ep(a, w: Q4Weights, c, m: int, ep: Epilogue):
+    """src/kernels/q4/matmul.rs:187."""
+    return _run_host_or_dev("gemm_gpu_b16b16_q4", lambda *x: lib().smg_q4_matmul_dev(*x[:5], 1, x[5]),
+                            a, w, c, m, ep)
+
+
+def matmul_q4_bf16(a, w: Q4Weights, c, m: int):
+    return matmul_q4_bf16_ep(a, w, c, m, Epilogue())
+
+
+def matmul_q2_ep(a, w: Q2Weights, c, m: int, ep: Epilogue):
+    """src/kernels/lowbit/matmul.rs:48."""
+    return _run_host_or_dev("gemm_gpu_f16_q2", lib().smg_lowbit_matmul_dev, a, w, c, m, ep)
+
+
+def matmul_q2(a, w: Q2Weights, c, m: int):
+    return matmul_q2_ep(a, w, c, m, Epilogue())
+
+
+def matmul_q1_ep(a, w: Q1Weights, c, m: int, ep: Epilogue):
+    """src/kernels/lowbit/matmul.rs:79."""
+    return _run_host_or_dev("gemm_gpu_f16_q1", lib().smg_lowbit_matmul_dev, a, w, c, m, ep)
+
+
+def matmul_q1(a, w: Q1Weights, c, m: int):
+    return matmul_q1_ep(a, w, c, m, Epilogue())
+
+
+def matmul_q2_mopa_ep(a, w: Q2Weights, c, m: int, ep: Epilogue):
+    """src/kernels/lowbit/matmul.rs:107."""
+    return _run_host_or_dev("gemm_gpu_f16f16_q2", lib().smg_lowbit_mopa_dev, a, w, c, m, ep)
+
+
+def matmul_q2_mopa(a, w: Q2Weights, c, m: int):
+    return matmul_q2_mopa_ep(a, w, c, m, Epilogue())
+
+
+def matmul_q1_mopa_ep(a, w: Q1Weights, c, m: int, ep: Epilogue):
+    """src/kernels/lowbit/matmul.rs:131."""
+    return _run_host_or_dev("gemm_gpu_f16f16_q1", lib().smg_lowbit_mopa_dev, a, w, c, m, ep)
+
+
+def matmul_q1_mopa(a, w: Q1Weights, c, m: int):
+    return matmul_q1_mopa_ep(a, w, c, m, Epilogue())
+
+
+class Gemm:
+    """Gemm::new(&a, &packed, m) builder (src/exec/builder.rs:220-814) over a
+    device-resident Packed<f16>/<bf16>: row-major output, beta = 1 and no
+    epilogue until configured."""
+
+    def __init__(self, a, packed: Packed, m: int):
+        self.a = a
+        self.packed = packed
+        self.m = m
+        self._beta = 0x3F80 if packed.bf16 else 0x3C00
+        self.ep = Epilogue(packed.bf16)
+        self._col_major = False
+
+    def col_major_output(self) -> "Gemm":
+        self._col_major = True
+        return self
+
+    def beta(self, v) -> "Gemm":
+        if isinstance(v, (np.uint16,)) or (isinstance(v, int) and not isinstance(v, bool)):
+            self._beta = int(v)
+        elif self.packed.bf16:
+            self._beta = int(np.float32(_bf16_round(v)).view(np.uint32)) >> 16
+        else:
+            self._beta = int(np.float16(v).view(np.uint16))
+        return self
+
+    def __getattr__(self, name):
+        # every Epilogue builder method, chained on this Gemm
+        fn = getattr(self.ep, name)
+
+        def chain(*args):
+            fn(*args)
+            return self
+        return chain
+
+    def run(self, c):
+        m, n, k = self.m, self.packed.n(), self.packed.k()
+        dst_cs, dst_rs = (m, 1) if self._col_major else (1, n)
+        if _is_dev(self.a):
+            if self.a.numel() != m * k or c.numel() != m * n:
+                raise ValueError("a is m*k, c is m*n")
+            self.ep.validate(m, n)
+            eptr, keep = _ep_ptr(self.ep, n)
+            _check(lib().smg_packed_matmul_dev(m, self.packed._h, c.data_ptr(), dst_cs, dst_rs,
+                                               self.a.data_ptr(), 1, k, self._beta, eptr,
+                                               int(self.packed.bf16), _stream()),
+                   "smg_packed_matmul_dev")
+            return c
+        a = _host16(self.a, m * k, "a")
+        if c.size != m * n:
+            raise ValueError("c is m*n")
+        self.ep.validate(m, n)
+        eptr, keep = _ep_ptr(self.ep, n)
+        fn = lib().gemm_gpu_b16b16_run_packed if self.packed.bf16 else lib().gemm_gpu_f16f16_run_packed
+        _check(fn(m, n, k, c.ctypes.data, dst_cs, dst_rs, 0, a.ctypes.data, 1, k, self.packed._h,
+                  0, self._beta, eptr), "run_packed")
+        return c
+
+
+def matmul_f16_packed(a, packed: Packed, c, m: int):
+    """src/kernels/f16.rs:255."""
+    return Gemm(a, packed, m).run(c)
+
+
+def matmul_bf16_packed(a, packed: Packed, c, m: int):
+    return Gemm(a, packed, m).run(c)

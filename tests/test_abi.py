@@ -1,0 +1,123 @@
+"""The C ABI on any host: the library loads, exports every function
+include/smegemm_gpu.h declares, keeps the reference's EpNode layout, and the
+host-side mirror validates arguments as the Rust API panics. No GPU calls."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "smegemm_gpu.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"\b((?:smg|gemm_gpu)_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import smegemm
+    path = os.path.join(ROOT, "sme-gemm_amd", "libsmegemm_gpu.so")
+    if not os.path.exists(path):
+        smegemm.build()
+    return C.CDLL(path)
+
+
+def test_header_declares_the_drop_ins():
+    names = _declared_functions()
+    for must in ("gemm_gpu_f16f16_q4", "gemm_gpu_b16b16_q4", "gemm_gpu_f16_q2", "gemm_gpu_f16_q1",
+                 "gemm_gpu_f16f16_q2", "gemm_gpu_f16f16_q1", "gemm_gpu_f16f16_run_packed",
+                 "gemm_gpu_b16b16_run_packed", "gemm_gpu_f16f16_q4_single", "smg_q4_create",
+                 "smg_q4_create_band", "smg_q2_create", "smg_q1_create", "smg_f16_prepack"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in _declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_epnode_layout_matches_reference():
+    """csrc/epilogue.h:224-229: 32 bytes, op@0 aux@4 scalar@8 ptr@16 ld@24."""
+    import smegemm
+    E = smegemm.EpNode
+    assert C.sizeof(E) == 32
+    assert (E.op.offset, E.aux.offset, E.scalar.offset, E.ptr.offset, E.ld.offset) == \
+        (0, 4, 8, 16, 24)
+
+
+def test_enum_values_match_reference():
+    """ep_op / ep_act numbering (csrc/epilogue.h:136-199)."""
+    import smegemm
+    text = open(HEADER).read()
+    for name, val in smegemm.EP_OP.items():
+        if name == "act":
+            continue
+        assert re.search(rf"EP_OP_{name.upper()} = {val}\b", text), name
+    for name, val in smegemm.EP_ACT.items():
+        assert re.search(rf"EP_ACT_{name.upper()} = {val}\b", text), name
+
+
+def test_q4_gemv_single_cut(lib):
+    lib.gemm_gpu_f16f16_q4_single.argtypes = [C.c_size_t] * 3
+    assert lib.gemm_gpu_f16f16_q4_single(1, 4096, 4096) == 1
+    assert lib.gemm_gpu_f16f16_q4_single(8, 4096, 4096) == 1
+    assert lib.gemm_gpu_f16f16_q4_single(9, 4096, 4096) == 0
+
+
+def test_params_validation_mirrors_reference_panics():
+    import smegemm as smg
+    with pytest.raises(ValueError):
+        smg.Q4Params(24)  # q4/mod.rs:76-79
+    with pytest.raises(ValueError):
+        smg.Q2Params(8)   # lowbit/mod.rs:65-68
+    with pytest.raises(ValueError):
+        smg.Q2Params(1 << 17)
+    assert smg.Q2Params().block() == 256 and smg.Q2Params().codebook() == (-1, 0, 1, 0)
+    assert smg.Q4Params().block() == 32 and not smg.Q4Params().is_affine()
+    assert smg.Q4Params(64).affine().is_affine()
+
+
+def test_epilogue_resolve_nodes():
+    """resolve_nodes (src/exec/scalar.rs:28-53): tensor ld 0 -> n and the
+    trailing activation appended last with alpha 0."""
+    import smegemm as smg
+    col = np.zeros(10, np.uint16)
+    ten = np.zeros(30, np.uint16)
+    ep = smg.Epilogue().add_col(col).silu().add_tensor(ten).leaky_relu(0.5).mul_scalar(2.0)
+    d, keep = ep.desc(10)
+    nodes = [d.nodes[i] for i in range(d.n_nodes)]
+    assert [nd.op for nd in nodes] == [4, 6, 8, 1, 8]
+    assert nodes[1].ld == 10
+    assert (nodes[2].aux, nodes[2].scalar) == (6, 0.5)
+    assert nodes[3].scalar == 2.0
+    assert (nodes[4].aux, nodes[4].scalar) == (3, 0.0)
+    assert smg.Epilogue().desc(10)[0] is None
+
+
+def test_epilogue_validate_lengths():
+    """validate_ep (src/exec/guard.rs:112-147)."""
+    import smegemm as smg
+    with pytest.raises(ValueError):
+        smg.Epilogue().add_col(np.zeros(5, np.uint16)).validate(3, 6)
+    with pytest.raises(ValueError):
+        smg.Epilogue().add_row(np.zeros(5, np.uint16)).validate(3, 6)
+    with pytest.raises(ValueError):
+        smg.Epilogue().add_tensor(np.zeros(17, np.uint16)).validate(3, 6)
+    smg.Epilogue().add_tensor(np.zeros(20, np.uint16), 7).validate(3, 6)
+    with pytest.raises(ValueError):
+        smg.Epilogue().add_tensor(np.zeros(40, np.uint16), 5).validate(3, 6)
+
+
+def test_scalar_operands_round_through_the_element_type():
+    """Scalars are stored as T::ep_to_f32 (graph.rs:86-96)."""
+    import smegemm as smg
+    e = smg.Epilogue().add_scalar(0.1)
+    assert e.nodes[0][2] == float(np.float16(0.1))
+    e = smg.Epilogue(bf16=True).add_scalar(0.1)
+    assert e.nodes[0][2] == float(np.float32(0.10009765625))

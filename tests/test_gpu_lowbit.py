@@ -1,0 +1,212 @@
+"""2-bit / 1-bit int8 path on the GPU vs the oracle, bit for bit.
+
+Mirrors src/kernels/lowbit/matmul.rs:457 (kernels_match_reference_bits: 12
+shapes x 4 blocks x 3 codebooks, both Q1 layouts, the reference's own LCG
+data), tests/correctness/q2.rs:83 (fused epilogue == plain then applied) and
+the BASELINE config-2 / config-3 shapes. Integer quantization and i32 block
+sums are exact, so outputs must be identical bits.
+"""
+import numpy as np
+import pytest
+
+from conftest import f16_tol, max_rel
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 64, 256), (1, 65, 37), (1, 1, 1), (2, 200, 300), (3, 64, 16), (5, 130, 513),
+          (6, 192, 256), (7, 100, 64), (12, 70, 200), (1, 2048, 1024), (4, 1536, 512),
+          (9, 1024, 384)]
+BOOKS = [(-1, 0, 1, 0), (-2, -1, 1, 2), (-128, 127, 3, -7)]
+
+
+def _data(orc, seed, length):
+    return orc.lcg_bytes(seed, length)
+
+
+@pytest.mark.parametrize("si", range(len(SHAPES)))
+@pytest.mark.parametrize("bi,block", list(enumerate([16, 64, 128, 4096])))
+def test_kernels_match_reference_bits(smg, orc, si, bi, block):
+    """matmul.rs:457-500, with the same generators and parameters."""
+    m, n, k = SHAPES[si]
+    nbk = -(-k // block)
+    sbytes = _data(orc, si + 7, n * nbk)
+    scales = orc.f32_to_f16(sbytes.astype(np.float32) * np.float32(1e-3) - np.float32(0.1))
+    abytes = _data(orc, si + 99, m * k)
+    a = orc.f32_to_f16((abytes.astype(np.float32) - np.float32(128.0)) / np.float32(37.0))
+    book = BOOKS[(si + bi) % len(BOOKS)]
+    p = smg.Q2Params(block).with_codebook(book)
+    codes = _data(orc, si * 31 + bi, (k * n + 3) // 4)
+    q2 = smg.Q2Weights(codes, scales, n, k, p)
+    got = np.full(m * n, 0x4880, np.uint16)  # f16 9.0, as the reference pre-fills
+    smg.matmul_q2(a, q2, got, m)
+    want = orc.lowbit_reference(2, a, codes, scales, m, n, k, block, book)
+    assert np.array_equal(got, want), f"q2 {m}x{n}x{k} {block} {book}"
+    signs = _data(orc, si * 17 + bi, (k * n + 7) // 8)
+    for layout in (smg.WeightLayout.OutIn, smg.WeightLayout.InOut):
+        q1 = smg.Q1Weights(signs, scales, layout, n, k, block)
+        got = np.full(m * n, 0x4880, np.uint16)
+        smg.matmul_q1(a, q1, got, m)
+        want = orc.lowbit_reference(1, a, signs, scales, m, n, k, block,
+                                    inout=(layout == smg.WeightLayout.InOut))
+        assert np.array_equal(got, want), f"q1 {m}x{n}x{k} {block} layout {layout}"
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_config2_q2_ternary(smg, orc, m):
+    """K=4096, N=11008, block 128, ternary; bitwise."""
+    import workloads
+    n, k = 11008, 4096
+    a, codes, scales = workloads.q2_inputs(m, n, k, seed=0)
+    w = smg.Q2Weights(codes, scales, n, k, smg.Q2Params(128))
+    got = np.zeros(m * n, np.uint16)
+    smg.matmul_q2(a, w, got, m)
+    want = orc.lowbit_reference(2, a, codes, scales, m, n, k, 128)
+    assert np.array_equal(got, want)
+
+
+def test_config3_q1_add_col_silu(smg, orc):
+    """Q1 + add_col(bias) + silu, K=4096, N=14336; bitwise."""
+    import workloads
+    m, n, k = 1, 14336, 4096
+    a, signs, scales, bias = workloads.q1_inputs(m, n, k, seed=0)
+    w = smg.Q1Weights(signs, scales, smg.WeightLayout.OutIn, n, k, 128)
+    got = np.zeros(m * n, np.uint16)
+    smg.matmul_q1_ep(a, w, got, m, smg.Epilogue().add_col(bias).silu())
+    want = orc.matmul_lowbit_ep(1, a, signs, scales, m, n, k, 128, [(4, 0, 0.0, bias, 0)], 3)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 200, 300), (4, 1536, 512), (13, 70, 64)])
+def test_fused_epilogue_is_plain_then_applied(smg, orc, m, n, k):
+    """q2.rs:83-108: bias, row scale and trailing gelu == plain product then the
+    scalar graph (bitwise here: both sides are the reference's arithmetic)."""
+    rng = np.random.default_rng(m * 131 + n * 17 + k)
+    a, codes, scales = (orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32) * 0.5),
+                        rng.integers(0, 256, (k * n + 3) // 4, dtype=np.uint8),
+                        orc.f32_to_f16(rng.uniform(0.005, 0.03, n * -(-k // 256))
+                                       .astype(np.float32)))
+    bias = orc.f32_to_f16(rng.uniform(-0.5, 0.5, n).astype(np.float32))
+    rows = orc.f32_to_f16(rng.uniform(-0.5, 0.5, m).astype(np.float32))
+    w = smg.Q2Weights(codes, scales, n, k)
+    plain = np.zeros(m * n, np.uint16)
+    smg.matmul_q2(a, w, plain, m)
+    got = np.zeros(m * n, np.uint16)
+    smg.matmul_q2_ep(a, w, got, m, smg.Epilogue().add_col(bias).mul_row(rows).gelu())
+    want = orc.apply_ep(plain, m, n, [(4, 0, 0.0, bias, 0), (3, 0, 0.0, rows, 0)], 2)
+    assert np.array_equal(got, want)
+
+
+def test_m_independence_and_row_groups(smg, orc):
+    """Results depend only on the row and column (ARCHITECTURE.md:511-514):
+    row i of an m=20 call (three row groups) equals the m=1 call on row i."""
+    m, n, k = 20, 300, 700
+    rng = np.random.default_rng(3)
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    codes = rng.integers(0, 256, (k * n + 3) // 4, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.01, 0.05, n * -(-k // 64)).astype(np.float32))
+    w = smg.Q2Weights(codes, scales, n, k, smg.Q2Params(64))
+    full = np.zeros(m * n, np.uint16)
+    smg.matmul_q2(a, w, full, m)
+    for i in (0, 7, 8, 19):
+        one = np.zeros(n, np.uint16)
+        smg.matmul_q2(a[i * k:(i + 1) * k], w, one, 1)
+        assert np.array_equal(one, full[i * n:(i + 1) * n])
+
+
+@pytest.mark.parametrize("block,k,m", [(8192, 20000, 1), (65536, 70000, 2), (16384, 16384, 9)])
+def test_long_blocks_prequantized(smg, orc, block, k, m):
+    """Blocks longer than one in-kernel pass (quantized by the stand-alone
+    kernel first), including the maximum block 65536 and a partial last block."""
+    n = 96
+    rng = np.random.default_rng(block + k)
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    nbk = -(-k // block)
+    scales = orc.f32_to_f16(rng.uniform(0.01, 0.05, n * nbk).astype(np.float32))
+    codes = rng.integers(0, 256, (k * n + 3) // 4, dtype=np.uint8)
+    w = smg.Q2Weights(codes, scales, n, k, smg.Q2Params(block))
+    got = np.zeros(m * n, np.uint16)
+    smg.matmul_q2(a, w, got, m)
+    assert np.array_equal(got, orc.lowbit_reference(2, a, codes, scales, m, n, k, block))
+    signs = rng.integers(0, 256, (k * n + 7) // 8, dtype=np.uint8)
+    w1 = smg.Q1Weights(signs, scales, smg.WeightLayout.OutIn, n, k, block)
+    got1 = np.zeros(m * n, np.uint16)
+    smg.matmul_q1(a, w1, got1, m)
+    assert np.array_equal(got1, orc.lowbit_reference(1, a, signs, scales, m, n, k, block))
+
+
+def test_nan_and_inf_activations(smg, orc):
+    """A NaN in a block makes its amax NaN (matmul.rs:356-363) and an inf gives
+    inv = 0; both propagate exactly as the reference's fold does."""
+    m, n, k = 2, 64, 256
+    rng = np.random.default_rng(1)
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    a[5] = 0x7E00      # NaN in row 0, block 0
+    a[k + 200] = 0x7C00  # +inf in row 1, block 1 (block 128)
+    codes = rng.integers(0, 256, (k * n + 3) // 4, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.01, 0.05, n * 2).astype(np.float32))
+    w = smg.Q2Weights(codes, scales, n, k, smg.Q2Params(128))
+    got = np.zeros(m * n, np.uint16)
+    smg.matmul_q2(a, w, got, m)
+    want = orc.lowbit_reference(2, a, codes, scales, m, n, k, 128)
+    gnan = (got & 0x7C00) == 0x7C00
+    wnan = (want & 0x7C00) == 0x7C00
+    assert np.array_equal(gnan & ((got & 0x3FF) != 0), wnan & ((want & 0x3FF) != 0))
+    fin = ~wnan
+    assert np.array_equal(got[fin], want[fin])
+
+
+def test_band_major_upload_matches_row_major(smg, orc):
+    n, k, block = 130, 300, 64
+    rng = np.random.default_rng(2)
+    a = orc.f32_to_f16(rng.standard_normal(3 * k).astype(np.float32))
+    codes = rng.integers(0, 256, (k * n + 3) // 4, dtype=np.uint8)
+    nbk = -(-k // block)
+    scales = orc.f32_to_f16(rng.uniform(0.01, 0.05, n * nbk).astype(np.float32))
+    p = smg.Q2Params(block).with_codebook((-2, -1, 1, 2))
+    packed, sc = orc.lowbit_pack_band(2, codes, scales, n, k, block)
+    c1 = np.zeros(3 * n, np.uint16)
+    c2 = np.zeros(3 * n, np.uint16)
+    smg.matmul_q2(a, smg.Q2Weights(codes, scales, n, k, p), c1, 3)
+    smg.matmul_q2(a, smg.Q2Weights.from_band(packed, sc, n, k, p), c2, 3)
+    assert np.array_equal(c1, c2)
+    signs = rng.integers(0, 256, (k * n + 7) // 8, dtype=np.uint8)
+    packed1, sc1 = orc.lowbit_pack_band(1, signs, scales, n, k, block, inout=True)
+    d1 = np.zeros(3 * n, np.uint16)
+    d2 = np.zeros(3 * n, np.uint16)
+    smg.matmul_q1(a, smg.Q1Weights(signs, scales, smg.WeightLayout.InOut, n, k, block), d1, 3)
+    smg.matmul_q1(a, smg.Q1Weights.from_band(packed1, sc1, n, k, block), d2, 3)
+    assert np.array_equal(d1, d2)
+
+
+MOPA_SHAPES = [(8, 64, 256), (1, 65, 37), (3, 200, 301), (33, 130, 514), (40, 4200, 1030),
+               (200, 1000, 2048)]
+
+
+@pytest.mark.parametrize("si", range(len(MOPA_SHAPES)))
+@pytest.mark.parametrize("bi,block", list(enumerate([16, 128, 4096])))
+def test_mopa_matches_eager_dequant(smg, orc, si, bi, block):
+    """matmul.rs:527-567: the MOPA route against eager dequant + dense GEMM
+    (f32 accumulation here and in the oracle; tolerance on the sum order)."""
+    m, n, k = MOPA_SHAPES[si]
+    nbk = -(-k // block)
+    scales = orc.f32_to_f16(_data(orc, si + 3, n * nbk).astype(np.float32) * np.float32(1e-3)
+                            - np.float32(0.1))
+    a = orc.f32_to_f16((_data(orc, si + 77, m * k).astype(np.float32) - np.float32(128.0))
+                       / np.float32(61.0))
+    book = BOOKS[(si + bi) % len(BOOKS)]
+    codes = _data(orc, si * 13 + bi, (k * n + 3) // 4)
+    signs = _data(orc, si * 19 + bi, (k * n + 7) // 8)
+    bias = orc.f32_to_f16(np.arange(n, dtype=np.float32) * np.float32(0.01) - np.float32(1.0))
+    q2 = smg.Q2Weights(codes, scales, n, k, smg.Q2Params(block).with_codebook(book))
+    q1 = smg.Q1Weights(signs, scales, smg.WeightLayout.OutIn, n, k, block)
+    for ei in range(2):
+        ep = smg.Epilogue() if ei == 0 else smg.Epilogue().add_col(bias).silu()
+        nodes, act = ([], None) if ei == 0 else ([(4, 0, 0.0, bias, 0)], 3)
+        got = np.zeros(m * n, np.uint16)
+        smg.matmul_q2_mopa_ep(a, q2, got, m, ep)
+        want = orc.matmul_lowbit_mopa_ep(2, a, codes, scales, m, n, k, block, nodes, act, book)
+        assert max_rel(got, want) <= f16_tol(k), f"q2 mopa ep {ei}"
+        got = np.zeros(m * n, np.uint16)
+        smg.matmul_q1_mopa_ep(a, q1, got, m, ep)
+        want = orc.matmul_lowbit_mopa_ep(1, a, signs, scales, m, n, k, block, nodes, act)
+        assert max_rel(got, want) <= f16_tol(k), f"q1 mopa ep {ei}"

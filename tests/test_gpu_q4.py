@@ -1,0 +1,249 @@
+"""Q4 path on the GPU vs the CPU oracle (the reference's portable path).
+
+Mirrors tests/correctness/q4.rs (q4_resident :66, q4_blocks_and_affine :127,
+q4_fused_epilogue_matches_oracle :417), gemv.rs:229 (gemv_q4) and the
+BASELINE config-1 / config-4 shapes. Float outputs: max |g-w|/(1+|w|) against
+the oracle's rounded output within 2e-3*sqrt(K)/64 (f16) or 8x that (bf16);
+the empty epilogue is pinned bitwise to the plain call (q4.rs:508-513).
+"""
+import threading
+
+import numpy as np
+import pytest
+
+from conftest import bf16_tol, f16_tol, max_rel
+
+pytestmark = pytest.mark.gpu
+
+# (m, n, k): the reference's SIZES (tests/correctness/main.rs:80-91) + tails
+SIZES = [(1, 1, 1), (7, 5, 3), (31, 31, 31), (32, 32, 32), (33, 17, 9), (64, 96, 48),
+         (128, 64, 80), (40, 8, 7), (7, 50, 200), (96, 96, 256)]
+TAIL_SIZES = [(65, 257, 257), (33, 512, 257), (97, 300, 131), (7, 400, 800), (33, 161, 401)]
+
+
+def _lcg_q4(orc, seed, m, n, k, block):
+    """q4.rs:74-82 data: fill() activations, LCG bytes, scales 0.01+0.001*(i%5)."""
+    a, s = orc.lcg_fill(seed, m * k)
+    quants = orc.lcg_bytes(s, (k * n + 1) // 2)
+    nbk = -(-k // block)
+    scales = orc.f32_to_f16(np.float32(0.01) + np.float32(0.001) * (np.arange(n * nbk) % 5)
+                            .astype(np.float32))
+    return a, quants, scales
+
+
+@pytest.mark.parametrize("m,n,k", SIZES + TAIL_SIZES)
+def test_q4_resident_sizes(smg, orc, m, n, k):
+    seed = 0x4444_9999_DEAD_0001 ^ (m * 131 + n * 17 + k)
+    a, quants, scales = _lcg_q4(orc, seed, m, n, k, 32)
+    w = smg.Q4Weights(quants, scales, n, k)
+    c = np.zeros(m * n, np.uint16)
+    smg.matmul_q4(a, w, c, m)
+    want = orc.matmul_q4_ep(a, quants, scales, None, m, n, k, 32)
+    assert max_rel(c, want) <= f16_tol(k), f"{m}x{n}x{k}"
+
+
+GEMV_CASES = [(1, 33, 256), (1, 389, 1027), (1, 1100, 2051), (2, 100, 70), (3, 129, 1027),
+              (4, 4109, 4099), (5, 70, 513), (7, 1030, 2050)]
+
+
+@pytest.mark.parametrize("m,n,k", GEMV_CASES)
+@pytest.mark.parametrize("block", [16, 32, 64])
+@pytest.mark.parametrize("affine", [False, True])
+def test_gemv_q4_blocks_affine(smg, orc, m, n, k, block, affine):
+    """gemv.rs:229-300: ragged N and K, partial last block, both forms."""
+    rng = np.random.default_rng(n * 17 + k + block)
+    nbk = -(-k // block)
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(np.float32(0.01) + np.float32(0.001) * (np.arange(n * nbk) % 7))
+    mins = orc.f32_to_f16(np.float32(0.05) * (np.arange(n * nbk) % 5) - np.float32(0.1)) \
+        if affine else None
+    a = orc.f32_to_f16((np.arange(m * k) % 13).astype(np.float32) * np.float32(0.05)
+                       - np.float32(0.3))
+    p = smg.Q4Params(block).affine() if affine else smg.Q4Params(block)
+    w = smg.Q4Weights.with_params(quants, scales, mins, n, k, p)
+    c = np.zeros(m * n, np.uint16)
+    smg.matmul_q4(a, w, c, m)
+    want = orc.matmul_q4_ep(a, quants, scales, mins, m, n, k, block)
+    assert max_rel(c, want) <= f16_tol(k)
+
+
+@pytest.mark.parametrize("block", [1, 2, 16, 32, 64, 128])
+@pytest.mark.parametrize("m", [1, 6, 40])
+def test_q4_block_sizes_gemv_and_gemm(smg, orc, block, m):
+    """q4.rs:127: every power-of-two block (GEMV for m <= 8, MFMA above)."""
+    n, k = 70, 200
+    rng = np.random.default_rng(block * 100 + m)
+    nbk = -(-k // block)
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.005, 0.02, n * nbk).astype(np.float32))
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    w = smg.Q4Weights.with_params(quants, scales, None, n, k, smg.Q4Params(block))
+    c = np.zeros(m * n, np.uint16)
+    smg.matmul_q4(a, w, c, m)
+    want = orc.matmul_q4_ep(a, quants, scales, None, m, n, k, block)
+    assert max_rel(c, want) <= f16_tol(k)
+
+
+def test_config1_q4_gemv(smg, orc):
+    """m=1, K=N=4096, block 32, seed 0."""
+    import workloads
+    m, n, k = 1, 4096, 4096
+    a, quants, scales, _ = workloads.q4_inputs(m, n, k, seed=0)
+    w = smg.Q4Weights(quants, scales, n, k)
+    c = np.zeros(m * n, np.uint16)
+    smg.matmul_q4(a, w, c, m)
+    want = orc.matmul_q4_ep(a, quants, scales, None, m, n, k, 32)
+    assert max_rel(c, want) <= f16_tol(k)
+    # most outputs agree bit for bit (differences are f32 summation order only)
+    assert np.mean(c == want) > 0.99
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 96, 128), (65, 33, 256), (200, 520, 512), (1, 96, 128),
+                                   (5, 33, 256)])
+@pytest.mark.parametrize("affine", [False, True])
+def test_q4_fused_epilogue_matches_oracle(smg, orc, m, n, k, affine):
+    """q4.rs:417-515 cases 0..3; the empty graph equals matmul_q4 bitwise."""
+    nbk = -(-k // 32)
+    rng = np.random.default_rng(m * 131 + n * 17 + k)
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(np.float32(0.01) + np.float32(0.001) * (np.arange(n * nbk) % 7))
+    mins = orc.f32_to_f16(np.float32(0.05) * (np.arange(n * nbk) % 5) - np.float32(0.1)) \
+        if affine else None
+    a = orc.f32_to_f16((np.arange(m * k) % 13) * np.float32(0.05) - np.float32(0.3))
+    col = orc.f32_to_f16(np.float32(0.02) * np.arange(n, dtype=np.float32) - np.float32(0.4))
+    row = orc.f32_to_f16(np.float32(0.01) * np.arange(m, dtype=np.float32) - np.float32(0.2))
+    p = smg.Q4Params(32).affine() if affine else smg.Q4Params(32)
+    w = smg.Q4Weights.with_params(quants, scales, mins, n, k, p)
+    for case in range(4):
+        ep = smg.Epilogue()
+        nodes, act = [], None
+        if case >= 1:
+            ep = ep.add_col(col) if case < 3 else ep.add_row(row).add_col(col)
+            nodes = [(4, 0, 0.0, col, 0)] if case < 3 else [(2, 0, 0.0, row, 0), (4, 0, 0.0, col, 0)]
+        if case == 2:
+            ep = ep.relu()
+            act = 1
+        if case == 3:
+            ep = ep.gelu()
+            act = 2
+        got = np.zeros(m * n, np.uint16)
+        smg.matmul_q4_ep(a, w, got, m, ep)
+        want = orc.matmul_q4_ep(a, quants, scales, mins, m, n, k, 32, nodes, act)
+        assert max_rel(got, want) <= f16_tol(k), f"case {case}"
+        if case == 0:
+            plain = np.zeros(m * n, np.uint16)
+            smg.matmul_q4(a, w, plain, m)
+            assert np.array_equal(plain, got)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 96, 128), (3, 200, 300), (64, 96, 128), (33, 70, 257)])
+@pytest.mark.parametrize("affine", [False, True])
+def test_q4_bf16(smg, orc, m, n, k, affine):
+    """matmul_q4_bf16(_ep) vs the bf16 portable path (q4/matmul.rs:258-270)."""
+    nbk = -(-k // 32)
+    rng = np.random.default_rng(7 * m + n + k)
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.005, 0.02, n * nbk).astype(np.float32))
+    mins = orc.f32_to_f16(rng.uniform(-0.1, 0.1, n * nbk).astype(np.float32)) if affine else None
+    a = orc.f32_to_bf16(rng.standard_normal(m * k).astype(np.float32))
+    bias = orc.f32_to_bf16(rng.normal(0, 0.1, n).astype(np.float32))
+    p = smg.Q4Params(32).affine() if affine else smg.Q4Params(32)
+    w = smg.Q4Weights.with_params(quants, scales, mins, n, k, p)
+    got = np.zeros(m * n, np.uint16)
+    smg.matmul_q4_bf16_ep(a, w, got, m, smg.Epilogue().add_col(bias).silu())
+    want = orc.matmul_q4_ep(a, quants, scales, mins, m, n, k, 32, [(4, 0, 0.0, bias, 0)], 3,
+                            bf16=True)
+    assert max_rel(got, want, bf16=True) <= bf16_tol(k)
+
+
+@pytest.mark.parametrize("m", [1, 4, 20])
+@pytest.mark.parametrize("affine", [False, True])
+def test_q4_band_major_upload_matches_row_major(smg, orc, m, affine):
+    """The reference's band-major resident arrays (what src/ffi.rs passes) give
+    the same device weights as the public row-major input."""
+    n, k, block = 300, 160, 32
+    rng = np.random.default_rng(11)
+    nbk = -(-k // block)
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.005, 0.02, n * nbk).astype(np.float32))
+    mins = orc.f32_to_f16(rng.uniform(-0.1, 0.1, n * nbk).astype(np.float32)) if affine else None
+    p = smg.Q4Params(block).affine() if affine else smg.Q4Params(block)
+    nib, sc, mn = orc.q4_pack_band(quants, scales, mins, n, k, block)
+    w1 = smg.Q4Weights.with_params(quants, scales, mins, n, k, p)
+    w2 = smg.Q4Weights.from_band(nib, sc, mn, n, k, p)
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    c1 = np.zeros(m * n, np.uint16)
+    c2 = np.zeros(m * n, np.uint16)
+    smg.matmul_q4(a, w1, c1, m)
+    smg.matmul_q4(a, w2, c2, m)
+    assert np.array_equal(c1, c2)
+
+
+def test_q4_empty_shapes_leave_c_untouched(smg):
+    """m == 0 or n == 0 returns at once (q4/matmul.rs:43-44)."""
+    w = smg.Q4Weights(np.zeros(0, np.uint8), np.zeros(0, np.uint16), 0, 64)
+    c = np.zeros(0, np.uint16)
+    smg.matmul_q4(np.zeros(0, np.uint16), w, c, 0)
+    w2 = smg.Q4Weights(np.zeros(64 * 8 // 2, np.uint8), np.full(16, 0x3C00, np.uint16), 8, 64)
+    c2 = np.zeros(0, np.uint16)
+    smg.matmul_q4(np.zeros(0, np.uint16), w2, c2, 0)
+
+
+def test_q4_k_zero_gives_epilogue_of_zero(smg, orc):
+    """k == 0: the product is the empty sum (+0), then the op-graph."""
+    n = 40
+    w = smg.Q4Weights(np.zeros(0, np.uint8), np.zeros(0, np.uint16), n, 0)
+    bias = orc.f32_to_f16(np.linspace(-1, 1, n).astype(np.float32))
+    c = np.full(2 * n, 0x7777, np.uint16)
+    smg.matmul_q4_ep(np.zeros(0, np.uint16), w, c, 2, smg.Epilogue().add_col(bias))
+    assert np.array_equal(c, np.concatenate([bias, bias]))
+
+
+def test_q4_concurrent_callers_bit_identical(smg, orc):
+    """tests/concurrency.rs:130: concurrent callers get identical bits."""
+    m, n, k = 3, 1000, 1024
+    rng = np.random.default_rng(5)
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.005, 0.02, n * (k // 32)).astype(np.float32))
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    w = smg.Q4Weights(quants, scales, n, k)
+    ref = np.zeros(m * n, np.uint16)
+    smg.matmul_q4(a, w, ref, m)
+    outs = [np.zeros(m * n, np.uint16) for _ in range(8)]
+    errs = []
+
+    def run(i):
+        try:
+            for _ in range(5):
+                smg.matmul_q4(a, w, outs[i], m)
+        except Exception as e:  # noqa: BLE001
+            errs.append(e)
+
+    ts = [threading.Thread(target=run, args=(i,)) for i in range(8)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errs
+    for o in outs:
+        assert np.array_equal(o, ref)
+
+
+def test_q4_device_pointer_path_matches_host(smg, orc):
+    """smg_q4_matmul_dev (torch tensors on the current stream) == host path."""
+    import torch
+    m, n, k = 2, 512, 1024
+    rng = np.random.default_rng(9)
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.005, 0.02, n * (k // 32)).astype(np.float32))
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    bias = orc.f32_to_f16(rng.normal(0, 0.1, n).astype(np.float32))
+    w = smg.Q4Weights(quants, scales, n, k)
+    host = np.zeros(m * n, np.uint16)
+    smg.matmul_q4_ep(a, w, host, m, smg.Epilogue().add_col(bias).silu())
+    ad = torch.from_numpy(a.view(np.int16)).cuda()
+    bd = torch.from_numpy(bias.view(np.int16)).cuda()
+    cd = torch.zeros(m * n, dtype=torch.int16, device="cuda")
+    smg.matmul_q4_ep(ad, w, cd, m, smg.Epilogue().add_col(bd).silu())
+    torch.cuda.synchronize()
+    assert np.array_equal(cd.cpu().numpy().view(np.uint16), host)
