@@ -206,7 +206,8 @@ int make_q4(Get get, const uint16_t *scales_rm, const uint16_t *mins_rm, const u
     WDev &d = w->d;
     d.nchunks = (k + Q4_CHUNK - 1) / Q4_CHUNK;
     const size_t nbk = (k + block - 1) / block;
-    d.sc_rows = std::max(nbk, (d.nchunks * Q4_CHUNK + block - 1) / block);
+    // rows for every depth the kernels may touch: the GEMM steps K in 64s
+    d.sc_rows = std::max(nbk, (round_up(d.nchunks * Q4_CHUNK, 64) + block - 1) / block);
     d.k_pad = round_up(k ? k : 1, 64);
     std::vector<uint8_t> nib(d.nchunks * d.n_pad * 16, 0);
     for (size_t dd = 0; dd < k; dd++) {
@@ -215,7 +216,7 @@ int make_q4(Get get, const uint16_t *scales_rm, const uint16_t *mins_rm, const u
         const size_t byteoff = wd * 4 + bitpos / 8;
         const int shift = bitpos % 8;
         for (size_t j = 0; j < n; j++)
-            nib[(kc * d.n_pad + j) * 16 + byteoff] |= (uint8_t)(get(dd, j) << shift);
+            nib[(kc * d.n_pad + j) * 16 + byteoff] |= (uint8_t)((get(dd, j) ^ 8) << shift);
     }
     std::vector<uint16_t> sc(d.sc_rows * d.n_pad, 0), mn;
     const bool affine = mins_rm || mins_band;

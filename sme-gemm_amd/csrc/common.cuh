@@ -51,6 +51,40 @@ __device__ __forceinline__ uint16_t from_f32(float x) {
     return BF16 ? f32_to_bf16(x) : f32_to_f16(x);
 }
 
+// ---------------------------------------------------------------------------
+// Bounds-checked buffer loads. A raw buffer load whose offset lies past the
+// resource's byte count returns zero in hardware, so edge handling needs no
+// branch (a branch around a load makes the compiler wait on every load in
+// flight). Offsets are 32-bit: a resource spans < 2 GiB.
+// ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t OOB = 0x80000000u;  // an offset no resource reaches
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+__device__ __forceinline__ uint4 bload16(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint16_t bload2(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
+// 8 consecutive 16-bit elements A[row][d..d+8) of a row-major [rows][k] array
+// at `r` (zero outside rows x k). vec: k % 8 == 0, so rows are 16-byte aligned
+// and a group of 8 is either wholly inside or wholly outside.
+__device__ __forceinline__ uint4 load_row8(rsrc_t r, uint32_t row, uint32_t rows, uint32_t k,
+                                           uint32_t d, bool vec) {
+    if (vec) return bload16(r, (row < rows && d < k) ? (row * k + d) * 2u : OOB);
+    uint16_t e[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++)
+        e[q] = bload2(r, (row < rows && d + q < k) ? (row * k + d + q) * 2u : OOB);
+    return make_uint4(e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16),
+                      e[4] | ((uint32_t)e[5] << 16), e[6] | ((uint32_t)e[7] << 16));
+}
+
 // f64 -> f16 with a single RNE rounding (half::f16::from_f64): round to f32
 // with round-to-odd (f32 keeps 13 more bits than f16, so the later RNE step
 // cannot double-round), then the hardware f32 -> f16 RNE convert.

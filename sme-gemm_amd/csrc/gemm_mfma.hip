@@ -41,6 +41,8 @@ struct GemmArgs {
     uint32_t block_shift;
     uint32_t codebook;
     float beta;
+    uint32_t lhs_bytes;  // byte footprint of A (the buffer resource's range)
+    uint32_t vec_a;      // A rows 16-byte aligned, unit column stride, k % 8 == 0
 };
 
 template <bool BF16>
@@ -82,28 +84,32 @@ __device__ __forceinline__ void b_load(const GemmArgs &g, uint32_t col0, uint32_
     const uint32_t col = col0 + t % 128;
     const uint32_t d = k0 + (t / 128) * 32;  // first depth of the unit
     constexpr uint32_t CH = WK == W_Q4 ? 32 : WK == W_Q2 ? 64 : 128;
+    // Branch-free: a chunk past K loads the last chunk (a valid address) and
+    // its scale is forced to 0, so its weights are +-0.
     const uint32_t kc = d / CH;
+    const bool live = kc < g.nchunks;
+    const uint32_t kcc = live ? kc : g.nchunks - 1;
+    const uint8_t *base = g.codes + ((size_t)kcc * g.n_pad + col) * 16;
     r.raw[0] = make_uint4(0, 0, 0, 0);
+    if (WK == W_Q4) {
+        r.raw[0] = *(const uint4 *)base;
+    } else if (WK == W_Q2) {
+        const uint2 v = *(const uint2 *)(base + ((d % 64) / 32) * 8);
+        r.raw[0].x = v.x;
+        r.raw[0].y = v.y;
+    } else {
+        r.raw[0].x = *(const uint32_t *)(base + ((d % 128) / 32) * 4);
+    }
+    const uint32_t dc = kcc * CH + d % CH;
     r.s = 0;
     r.mn = 0;
-    if (kc < g.nchunks) {
-        const uint8_t *base = g.codes + ((size_t)kc * g.n_pad + col) * 16;
-        if (WK == W_Q4) {
-            r.raw[0] = *(const uint4 *)base;
-        } else if (WK == W_Q2) {
-            const uint2 v = *(const uint2 *)(base + ((d % 64) / 32) * 8);
-            r.raw[0].x = v.x;
-            r.raw[0].y = v.y;
-        } else {
-            r.raw[0].x = *(const uint32_t *)(base + ((d % 128) / 32) * 4);
-        }
-        if (WK == W_Q4 && (g.block_shift >= 5)) {
-            const uint32_t kb = d >> g.block_shift;
-            r.s = g.sc[(size_t)kb * g.n_pad + col];
-            if (g.mn) r.mn = g.mn[(size_t)kb * g.n_pad + col];
-        }
-        if (WK == W_Q2 || WK == W_Q1) {
-            if (g.block_shift >= 5) r.s = g.sc[(size_t)(d >> g.block_shift) * g.n_pad + col];
+    if (g.block_shift >= 5) {
+        const uint32_t kb = dc >> g.block_shift;
+        const uint16_t s = g.sc[(size_t)kb * g.n_pad + col];
+        r.s = live ? s : (uint16_t)0;
+        if (WK == W_Q4 && g.mn) {
+            const uint16_t mv = g.mn[(size_t)kb * g.n_pad + col];
+            r.mn = live ? mv : (uint16_t)0;
         }
     }
 }
@@ -130,7 +136,7 @@ __device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, uint32
         const bool fast = !BF16 && !AFFINE && g.block_shift >= 5;
 #pragma unroll
         for (int w = 0; w < 4; w++) {
-            const uint32_t q = words[w] ^ 0x88888888u;
+            const uint32_t q = words[w];  // stored nibbles are code + 8
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const uint32_t u = (q >> (4 * e)) & 0x000F000Fu;
@@ -220,23 +226,25 @@ __device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, uint32
 // ---- A-tile staging: 128 rows x 64 depths; thread t: row t/2, 32 depths ----
 __device__ __forceinline__ void a_load(const GemmArgs &g, uint32_t row0, uint32_t k0,
                                        uint4 (&ra)[4]) {
+    // buffer loads: out-of-range offsets read zero, no branches
     const int t = threadIdx.x;
     const uint32_t row = row0 + t / 2;
     const uint32_t d = k0 + (t % 2) * 32;
-    if (row >= g.m) {
+    const rsrc_t rs = make_rsrc(g.lhs, g.lhs_bytes);
+    if (g.vec_a) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) ra[q] = make_uint4(0, 0, 0, 0);
-        return;
-    }
-    const uint16_t *src = g.lhs + (size_t)row * g.lhs_rs + (size_t)d * g.lhs_cs;
-    if (g.lhs_cs == 1 && d + 32 <= g.k && ((((uintptr_t)src) & 15) == 0)) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) ra[q] = ((const uint4 *)src)[q];
+        for (int q = 0; q < 4; q++)
+            ra[q] = bload16(rs, (row < g.m && d + 8 * q < g.k)
+                                    ? (uint32_t)(row * g.lhs_rs + d + 8 * q) * 2u
+                                    : OOB);
         return;
     }
     uint16_t e[32];
 #pragma unroll
-    for (int q = 0; q < 32; q++) e[q] = (d + q < g.k) ? src[(size_t)q * g.lhs_cs] : (uint16_t)0;
+    for (int q = 0; q < 32; q++)
+        e[q] = bload2(rs, (row < g.m && d + q < g.k)
+                              ? (uint32_t)(row * g.lhs_rs + (d + q) * g.lhs_cs) * 2u
+                              : OOB);
 #pragma unroll
     for (int q = 0; q < 4; q++)
         ra[q] = make_uint4(e[8 * q] | ((uint32_t)e[8 * q + 1] << 16),
@@ -371,6 +379,11 @@ hipError_t launch_gemm(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long
     g.block_shift = w.block ? (uint32_t)__builtin_ctzll(w.block) : 0;
     g.codebook = w.codebook;
     g.beta = beta;
+    const size_t fp = (m && w.k) ? ((m - 1) * (size_t)lhs_rs + (w.k - 1) * (size_t)lhs_cs + 1) * 2 : 0;
+    if (fp >= ((size_t)1 << 31)) return hipErrorInvalidValue;  // one buffer resource spans < 2 GiB
+    g.lhs_bytes = (uint32_t)fp;
+    g.vec_a = (lhs_cs == 1 && lhs_rs % 8 == 0 && w.k % 8 == 0 &&
+               ((uintptr_t)lhs & 15) == 0) ? 1u : 0u;
     const bool affine = w.mins != nullptr;
     switch (w.kind) {
     case W_Q4:
@@ -402,7 +415,7 @@ __global__ void q4_dequant_kernel(WDev w, uint16_t *dense) {
     const uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
     const uint32_t shift = (uint32_t)__builtin_ctzll(w.block);
     for (int wd = 0; wd < 4; wd++) {
-        const uint32_t q = words[wd] ^ 0x88888888u;
+        const uint32_t q = words[wd];  // stored nibbles are code + 8
         for (int e = 0; e < 4; e++) {
             const uint32_t u = (q >> (4 * e)) & 0x000F000Fu;
             const int cs[2] = {(int)(u & 0xF) - 8, (int)(u >> 16) - 8};

@@ -65,19 +65,26 @@ __device__ void quantize_pass(const LbArgs &g, int mr, uint32_t row0, uint32_t p
     const uint32_t groups = 256 / G;
     const uint32_t t = threadIdx.x;
     const uint32_t gi = t / G, li = t % G;
+    const rsrc_t ar = make_rsrc(g.lhs, g.m * g.k * 2u);
+    const bool vec = (g.k & 7) == 0;
     for (uint32_t pr = gi; pr < ((npairs + groups - 1) / groups) * groups; pr += groups) {
         const bool live = pr < npairs;
         const uint32_t r = live ? pr / nb : 0, b = live ? pr % nb : 0;
         const uint32_t dstart = p0 + b * block + li * EL;
-        const uint16_t *src = g.lhs + (size_t)(row0 + r) * g.k;
+        // buffer loads: a dead pair (rows = 0) and depths past k read zero
+        const uint32_t row = row0 + r, rows = live ? g.m : 0u;
         // amax with NaN propagation (matmul.rs:356-363)
         float amax = 0.0f;
         bool nan = false;
-        for (uint32_t e = 0; e < EL; e++) {
-            uint32_t d = dstart + e;
-            float x = (live && d < p1) ? fabsf(f16_to_f32(src[d])) : 0.0f;
-            if (x != x) nan = true;
-            amax = fmaxf(amax, x);
+        for (uint32_t e0 = 0; e0 < EL; e0 += 8) {
+            const uint4 v = load_row8(ar, row, rows, g.k, dstart + e0, vec);
+            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float x = fabsf(f16_to_f32((uint16_t)(w4[e / 2] >> (16 * (e % 2)))));
+                nan = nan || (x != x);
+                amax = fmaxf(amax, x);
+            }
         }
         for (uint32_t off = G / 2; off > 0; off >>= 1) {
             amax = fmaxf(amax, __shfl_xor(amax, off, G));
@@ -87,18 +94,20 @@ __device__ void quantize_pass(const LbArgs &g, int mr, uint32_t row0, uint32_t p
         const float inv = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
         const float s = __fdiv_rn(amax, 127.0f);
         int32_t qs = 0;
-        for (uint32_t e0 = 0; e0 < EL; e0 += 4) {
-            uint32_t packed = 0;
+        for (uint32_t e0 = 0; e0 < EL; e0 += 8) {
+            const uint4 v = load_row8(ar, row, rows, g.k, dstart + e0, vec);
+            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+            uint32_t packed[2] = {0, 0};
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                uint32_t d = dstart + e0 + e;
-                float x = (live && d < p1) ? f16_to_f32(src[d]) : 0.0f;
-                float v = rintf(x * inv);
-                int qi = (v != v) ? 0 : (int)fminf(fmaxf(v, -128.0f), 127.0f);
+            for (int e = 0; e < 8; e++) {
+                const float x = f16_to_f32((uint16_t)(w4[e / 2] >> (16 * (e % 2))));
+                const float qv = rintf(x * inv);
+                const int qi = (qv != qv) ? 0 : (int)fminf(fmaxf(qv, -128.0f), 127.0f);
                 qs += qi;
-                packed |= ((uint32_t)(qi & 0xff)) << (8 * e);
+                packed[e / 4] |= ((uint32_t)(qi & 0xff)) << (8 * (e % 4));
             }
-            if (live) *(uint32_t *)(aq + (size_t)r * pd + (dstart - p0) + e0) = packed;
+            if (live)
+                *(uint2 *)(aq + (size_t)r * pd + (dstart - p0) + e0) = make_uint2(packed[0], packed[1]);
         }
         for (uint32_t off = G / 2; off > 0; off >>= 1) qs += __shfl_xor(qs, off, G);
         if (live && li == 0) {
@@ -144,12 +153,13 @@ __global__ void __launch_bounds__(256) lowbit_gemv_kernel(LbArgs g, EpArgs ep) {
         uint4 wq[CPT];
 #pragma unroll
         for (int q = 0; q < CPT; q++) {
-            uint32_t kcl = kl * cpt + q;
-            uint32_t kc = kc0 + kcl;
-            if (q < (int)cpt && kcl < chunks_per_pass && kc < g.nchunks)
-                wq[q] = *(const uint4 *)(g.codes + ((size_t)kc * g.n_pad + j) * 16);
-            else
-                wq[q] = make_uint4(0, 0, 0, 0);
+            // branch-free: a chunk this lane does not own loads a valid
+            // chunk (the last), and is never used
+            const uint32_t kcl = kl * cpt + q;
+            const uint32_t kc = kc0 + kcl;
+            const bool own = q < (int)cpt && kcl < chunks_per_pass && kc < g.nchunks;
+            const uint32_t kcc = own ? kc : g.nchunks - 1;
+            wq[q] = *(const uint4 *)(g.codes + ((size_t)kcc * g.n_pad + j) * 16);
         }
         // 2. activations for the pass; zero the block sums
         __syncthreads();
@@ -303,9 +313,11 @@ inline uint32_t ilog2(size_t x) { return (uint32_t)(63 - __builtin_clzll(x)); }
 // Depths per pass: a power of two holding whole blocks when it can, within
 // the LDS budgets for int8 activations (AQ_BYTES) and block sums (S_BYTES),
 // and at most CPT chunks per lane.
-inline size_t pass_depths(int kind, size_t block, int mr) {
+inline size_t pass_depths(int kind, size_t block, int mr, size_t k) {
     const size_t ch = kind == 2 ? 64 : 128;
     size_t pd = (size_t)KL * CPT * ch;
+    // no longer than K needs (fewer idle chunk slots per lane)
+    while (pd / 2 >= k && pd / 2 >= ch && pd / 2 >= block) pd >>= 1;
     while (pd * mr > AQ_BYTES) pd >>= 1;
     while (pd >= block && (pd / block) * mr * TN * 4 > S_BYTES) pd >>= 1;
     if (pd / block > 512) pd = 512 * block;
@@ -343,7 +355,7 @@ inline int rows_per_group(size_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 
 
 size_t lowbit_scratch_bytes(const WDev &w, size_t m) {
     const int mr = rows_per_group(m);
-    const size_t pd = pass_depths(w.kind, w.block, mr);
+    const size_t pd = pass_depths(w.kind, w.block, mr, w.k);
     if (pd >= w.block) return 0;
     const size_t nbk = (w.k + w.block - 1) / w.block;
     const size_t kq = nbk * w.block;
@@ -353,7 +365,7 @@ size_t lowbit_scratch_bytes(const WDev &w, size_t m) {
 hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
                               const EpArgs &ep, void *scratch, hipStream_t s) {
     const int mr = rows_per_group(m);
-    const size_t pd = pass_depths(w.kind, w.block, mr);
+    const size_t pd = pass_depths(w.kind, w.block, mr, w.k);
     const bool preq = pd < w.block;
     LbArgs g = {};
     g.codes = w.codes;

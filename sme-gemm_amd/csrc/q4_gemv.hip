@@ -9,22 +9,30 @@
 // f32 (split over K, so the sum order differs: tolerance-checked), the sum is
 // rounded to f16/bf16 and the op-graph runs on that rounded value.
 //
-// The call is HBM-bound (0.5625 B of weights per MAC at block 32). Each
-// workgroup owns 16 output columns and splits K over 16 lanes; every lane
-// issues all of its 16-byte weight loads for a 4096-depth pass before it
-// touches A, so a whole pass of the weight matrix is in flight at once. A
-// (<= 64 KB) is staged in LDS per pass and read with broadcast ds_read_b128.
+// The call is HBM-bound (0.5625 B of weights per MAC at block 32). Two kernels:
+//
+// q4_gemv_mfma (f16, scale-only, block >= 32 -- the decode configuration):
+//   a workgroup of 8 waves owns 16 output columns; wave w takes every 8th
+//   group of 4 chunks (128 depths). Lane (g = lane/16, c = lane%16) loads the
+//   16-byte chunk g of column c, so a wave load reads four contiguous 256-byte
+//   runs, and every lane issues all its weight loads before it waits. Each
+//   dword (8 depths) dequantizes to 8 f16 weights -- v_bfi_b32 puts the
+//   nibble under an f16 exponent, a packed subtract leaves the exact code, a
+//   packed multiply by the scale is the reference's single RNE rounding -- and
+//   feeds one v_mfma_f32_16x16x32_f16 as the A operand (16 columns x 32
+//   depths), with up to 16 activation rows as the B operand. The matrix core
+//   does the dot products, so VALU work is the dequant alone. The 8 waves'
+//   partial 16x16 tiles are summed through LDS in a fixed order.
+//
+// q4_gemv_kernel (every other variant: bf16, affine, block < 32): 16 columns x
+//   16 lanes along K per workgroup, weights rounded per value, dot products on
+//   VALU. All loads are branch-free (clamped address, then a select) so they
+//   stay in flight together.
 #include "kernels.h"
 
 namespace smg {
 
 namespace {
-
-constexpr int TN = 16;        // output columns per workgroup
-constexpr int KL = 16;        // lanes along K per column
-constexpr int P = 8;          // chunks per lane per pass
-constexpr int PASS_CH = KL * P;            // chunks per pass
-constexpr int PASS_D = PASS_CH * Q4_CHUNK; // depths per pass (4096)
 
 struct Q4GemvArgs {
     const uint8_t *nib;
@@ -36,30 +44,150 @@ struct Q4GemvArgs {
     uint32_t block_shift;  // log2(block)
 };
 
-// Two consecutive depths' weights as a packed pair of 16-bit values.
-// Generic form: any block size, affine or not, f16 or bf16 (the exact
-// reference roundings, computed per value).
+// ---------------------------------------------------------------------------
+// MFMA GEMV (fast path)
+// ---------------------------------------------------------------------------
+constexpr int MF_WAVES = 8;                  // waves per workgroup (K slices)
+constexpr int MF_U = 4;                      // steps (4 chunks each) in flight per lane
+constexpr int MF_SEG = 4096;                 // depths of A staged in LDS at a time
+constexpr int MF_SEG_CH = MF_SEG / Q4_CHUNK; // 128 chunks per segment
+
+// v_bfi_b32 (mask in an SGPR, both data operands in VGPRs): the compiler
+// otherwise splits the insert into an and + an or with literal constants.
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t x, uint32_t y) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(x), "v"(y));
+    return r;
+}
+
+// dword of 8 biased nibbles (code+8; depth 2e at bits 4e, depth 2e+1 at bits
+// 16+4e) -> 8 f16 weights f16_RNE(scale*code) in depth order.
+__device__ __forceinline__ uint4 deq8(uint32_t q, half2_t s2, uint32_t mag_lo, uint32_t mag_hi) {
+    const half2_t off_lo = {(_Float16)1032.0f, (_Float16)1032.0f};  // 0x6400|u = 1024+u
+    const half2_t off_hi = {(_Float16)72.0f, (_Float16)72.0f};      // 0x5400|u<<4 = 64+u
+    const uint32_t q8 = q >> 8;
+    // one v_bfi_b32 each: (mask & x) | (~mask & magic)
+    const uint32_t h0 = bfi(0x000F000Fu, q, mag_lo);
+    const uint32_t h1 = bfi(0x00F000F0u, q, mag_hi);
+    const uint32_t h2 = bfi(0x000F000Fu, q8, mag_lo);
+    const uint32_t h3 = bfi(0x00F000F0u, q8, mag_hi);
+    const half2_t w0 = (__builtin_bit_cast(half2_t, h0) - off_lo) * s2;
+    const half2_t w1 = (__builtin_bit_cast(half2_t, h1) - off_hi) * s2;
+    const half2_t w2 = (__builtin_bit_cast(half2_t, h2) - off_lo) * s2;
+    const half2_t w3 = (__builtin_bit_cast(half2_t, h3) - off_hi) * s2;
+    return make_uint4(__builtin_bit_cast(uint32_t, w0), __builtin_bit_cast(uint32_t, w1),
+                      __builtin_bit_cast(uint32_t, w2), __builtin_bit_cast(uint32_t, w3));
+}
+
+template <int MR>  // rows staged per segment (1, 2, 4, 8)
+__global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpArgs ep) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint16_t *a_lds = (uint16_t *)smem;          // [MR][MF_SEG]
+    float *red = (float *)smem;                   // reused: [MF_WAVES][16 cols][MR]
+
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int c = lane & 15, grp = lane >> 4;
+    const uint32_t col = blockIdx.x * 16 + c;     // < n_pad
+    // the bfi magics live in VGPRs (a VOP3 takes one scalar operand)
+    const uint32_t mag_lo = __builtin_amdgcn_readfirstlane(0x64006400u) | (uint32_t)(t >> 30);
+    const uint32_t mag_hi = __builtin_amdgcn_readfirstlane(0x54005400u) | (uint32_t)(t >> 30);
+
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    const uint32_t last = g.nchunks - 1;  // nchunks >= 1 here
+    const uint32_t nseg = (g.nchunks + MF_SEG_CH - 1) / MF_SEG_CH;
+    for (uint32_t seg = 0; seg < nseg; seg++) {
+        const uint32_t sc0 = seg * MF_SEG_CH;
+        // A[:, segment] first: vmcnt retires in issue order, so loads issued
+        // before the weights can be waited on while the weights stay in flight
+        const uint32_t d0 = sc0 * Q4_CHUNK;
+        const rsrc_t ar = make_rsrc(g.lhs, g.m * g.k * 2u);
+        const bool vec = (g.k & 7) == 0;
+        uint4 areg[MR];  // row r, depths d0 + 8t .. +8 (MF_SEG / 8 == 512 threads)
+#pragma unroll
+        for (int r = 0; r < MR; r++) areg[r] = load_row8(ar, r, g.m, g.k, d0 + 8 * t, vec);
+        // steps of this wave within the segment: chunks sc0 + 4*(wave + 8*u) + grp
+        uint4 wq[MF_U];
+        uint16_t sv[MF_U];
+#pragma unroll
+        for (int u = 0; u < MF_U; u++) {
+            const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
+            const uint32_t kcc = kc < last ? kc : last;  // clamped: always a valid load
+            wq[u] = *(const uint4 *)(g.nib + ((size_t)kcc * g.n_pad + col) * 16);
+            const uint16_t sl = g.sc[(size_t)((kcc * Q4_CHUNK) >> g.block_shift) * g.n_pad + col];
+            sv[u] = kc < g.nchunks ? sl : (uint16_t)0;  // a dead step's weights become 0
+        }
+        // stage A[:, segment] (rows < m, zero past k)
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < MR; r++) *(uint4 *)(a_lds + r * MF_SEG + 8 * t) = areg[r];
+        __syncthreads();
+        // dequant + MFMA: A operand = 16 columns x 32 depths of weights, B
+        // operand = 32 depths x 16 rows of activations (rows >= m are zero)
+        const int row = c;  // B-operand lane: activation row lane%16
+#pragma unroll
+        for (int u = 0; u < MF_U; u++) {
+            const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
+            const bool live = kc < g.nchunks;
+            const half2_t s2 = {__builtin_bit_cast(_Float16, sv[u]), __builtin_bit_cast(_Float16, sv[u])};
+            const uint32_t words[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
+            const uint32_t kcl = live ? kc - sc0 : 0;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                uint4 wa = deq8(words[w], s2, mag_lo, mag_hi);
+                uint4 ab = make_uint4(0, 0, 0, 0);
+                if (row < MR) {
+                    const uint4 v = *(const uint4 *)(a_lds + row * MF_SEG + kcl * Q4_CHUNK + w * 8);
+                    ab = live ? v : make_uint4(0, 0, 0, 0);
+                }
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wa),
+                                                             __builtin_bit_cast(half8_t, ab), acc,
+                                                             0, 0, 0);
+            }
+        }
+    }
+    // lane holds D[col = 4*grp + v][row = c] for v = 0..3
+    __syncthreads();
+    if (c < MR) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) red[(wave * 16 + 4 * grp + v) * MR + c] = acc[v];
+    }
+    __syncthreads();
+    if (t < 16 * MR) {
+        const int cc = t / MR, r = t % MR;
+        float total = 0.0f;
+#pragma unroll
+        for (int w = 0; w < MF_WAVES; w++) total = total + red[(w * 16 + cc) * MR + r];
+        const uint32_t j = blockIdx.x * 16 + cc;
+        if (r < (int)g.m && j < g.n) g.dst[(size_t)r * g.n + j] = finish<false>(ep, total, r, j, g.n);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Generic GEMV (bf16, affine, block < 32)
+// ---------------------------------------------------------------------------
+constexpr int TN = 16;        // output columns per workgroup
+constexpr int KL = 16;        // lanes along K per column
+constexpr int P = 8;          // chunks per lane per pass
+constexpr int PASS_CH = KL * P;            // chunks per pass
+constexpr int PASS_D = PASS_CH * Q4_CHUNK; // depths per pass (4096)
+
+// Two consecutive depths' weights as a packed pair of 16-bit values: the
+// exact reference roundings, computed per value.
 template <bool BF16, bool AFFINE>
 __device__ __forceinline__ uint32_t deq_pair_generic(int c0, int c1, uint16_t s0, uint16_t s1,
                                                      uint16_t m0, uint16_t m1) {
     uint16_t w0, w1;
     if (!AFFINE) {
         // scale*code is exact in f32 (11-bit x 4-bit), so one rounding to T
-        float v0 = f16_to_f32(s0) * (float)c0;
-        float v1 = f16_to_f32(s1) * (float)c1;
-        w0 = from_f32<BF16>(v0);
-        w1 = from_f32<BF16>(v1);
+        w0 = from_f32<BF16>(f16_to_f32(s0) * (float)c0);
+        w1 = from_f32<BF16>(f16_to_f32(s1) * (float)c1);
     } else {
         // scale*code + min is exact in f64 (q4/mod.rs:146-147)
-        double v0 = (double)f16_to_f32(s0) * (double)c0 + (double)f16_to_f32(m0);
-        double v1 = (double)f16_to_f32(s1) * (double)c1 + (double)f16_to_f32(m1);
-        if (BF16) {
-            w0 = f32_to_bf16((float)v0);
-            w1 = f32_to_bf16((float)v1);
-        } else {
-            w0 = f64_to_f16(v0);
-            w1 = f64_to_f16(v1);
-        }
+        const double v0 = (double)f16_to_f32(s0) * (double)c0 + (double)f16_to_f32(m0);
+        const double v1 = (double)f16_to_f32(s1) * (double)c1 + (double)f16_to_f32(m1);
+        w0 = BF16 ? f32_to_bf16((float)v0) : f64_to_f16(v0);
+        w1 = BF16 ? f32_to_bf16((float)v1) : f64_to_f16(v1);
     }
     return (uint32_t)w0 | ((uint32_t)w1 << 16);
 }
@@ -71,17 +199,13 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t w, float acc) {
                                       __builtin_bit_cast(half2_t, w), acc, false);
     } else {
         // bf16 x bf16 products are exact in f32; two separately rounded adds
-        float p0 = bf16_to_f32((uint16_t)a) * bf16_to_f32((uint16_t)w);
-        float p1 = bf16_to_f32((uint16_t)(a >> 16)) * bf16_to_f32((uint16_t)(w >> 16));
+        const float p0 = bf16_to_f32((uint16_t)a) * bf16_to_f32((uint16_t)w);
+        const float p1 = bf16_to_f32((uint16_t)(a >> 16)) * bf16_to_f32((uint16_t)(w >> 16));
         return (acc + p0) + p1;
     }
 }
 
-// FAST: f16, scale-only, block >= 32 (one scale per chunk): the nibble pair
-// (code+8 after the xor) becomes 1024+u in f16, minus 1032 gives the exact
-// code, and one packed f16 multiply by the scale is the reference's single
-// RNE rounding of scale*code.
-template <int M, bool BF16, bool AFFINE, bool FAST>
+template <int M, bool BF16, bool AFFINE>
 __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4GemvArgs g, EpArgs ep) {
     extern __shared__ __align__(16) uint8_t smem[];
     uint16_t *a_lds = (uint16_t *)smem;  // [M][PASS_D]
@@ -92,6 +216,7 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4GemvArgs g, EpArgs ep) {
     const int kl = t / TN;
     const uint32_t j = blockIdx.x * TN + c;  // < n_pad always
     const uint32_t block = 1u << g.block_shift;
+    const uint32_t last = g.nchunks - 1;
 
     float acc[M];
 #pragma unroll
@@ -100,98 +225,70 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4GemvArgs g, EpArgs ep) {
     const uint32_t npass = (g.nchunks + PASS_CH - 1) / PASS_CH;
     for (uint32_t pass = 0; pass < npass; pass++) {
         const uint32_t kc0 = pass * PASS_CH;
-        // 1. weight loads for the whole pass, issued before anything waits
+        // 0. A[:, pass] into registers first (vmcnt retires in issue order)
+        const uint32_t d0 = kc0 * Q4_CHUNK;
+        const rsrc_t ar = make_rsrc(g.lhs, g.m * g.k * 2u);
+        const bool vec = (g.k & 7) == 0;
+        uint4 areg[2 * M];  // element group t + 256*i: row (t + 256 i) / 512
+#pragma unroll
+        for (int i = 0; i < 2 * M; i++) {
+            const uint32_t idx = t + 256 * i;
+            areg[i] = load_row8(ar, idx / 512, g.m, g.k, d0 + (idx % 512) * 8, vec);
+        }
+        // 1. weight loads for the whole pass, branch-free so they overlap
         uint4 wq[P];
-        uint16_t sv[P];
-        uint16_t mv[P];
+        uint16_t sv[P], mv[P];
 #pragma unroll
         for (int p = 0; p < P; p++) {
-            uint32_t kc = kc0 + kl * P + p;
-            if (kc < g.nchunks) {
-                wq[p] = *(const uint4 *)(g.nib + ((size_t)kc * g.n_pad + j) * 16);
-                if (FAST || block >= Q4_CHUNK) {
-                    uint32_t kb = (kc * Q4_CHUNK) >> g.block_shift;
-                    sv[p] = g.sc[(size_t)kb * g.n_pad + j];
-                    if (AFFINE) mv[p] = g.mn[(size_t)kb * g.n_pad + j];
-                }
-            } else {
-                wq[p] = make_uint4(0, 0, 0, 0);
-                sv[p] = 0;
-                mv[p] = 0;
-            }
+            const uint32_t kc = kc0 + kl * P + p;
+            const uint32_t kcc = kc < last ? kc : last;
+            wq[p] = *(const uint4 *)(g.nib + ((size_t)kcc * g.n_pad + j) * 16);
+            const uint32_t kb = block >= Q4_CHUNK ? ((kcc * Q4_CHUNK) >> g.block_shift) : 0;
+            sv[p] = g.sc[(size_t)kb * g.n_pad + j];
+            mv[p] = AFFINE ? g.mn[(size_t)kb * g.n_pad + j] : (uint16_t)0;
         }
         // 2. stage A[:, pass] into LDS (zero beyond k)
         __syncthreads();
-        const uint32_t d0 = kc0 * Q4_CHUNK;
-        for (uint32_t idx = t; idx < (uint32_t)M * PASS_D / 8; idx += 256) {
-            uint32_t r = idx / (PASS_D / 8);
-            uint32_t x = (idx % (PASS_D / 8)) * 8;
-            uint32_t d = d0 + x;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (r < g.m) {
-                const uint16_t *src = g.lhs + (size_t)r * g.k + d;
-                if (d + 8 <= g.k && ((((uintptr_t)src) & 15) == 0)) {
-                    v = *(const uint4 *)src;
-                } else {
-                    uint16_t e[8];
 #pragma unroll
-                    for (int q = 0; q < 8; q++) e[q] = (d + q < g.k) ? src[q] : (uint16_t)0;
-                    v.x = e[0] | ((uint32_t)e[1] << 16);
-                    v.y = e[2] | ((uint32_t)e[3] << 16);
-                    v.z = e[4] | ((uint32_t)e[5] << 16);
-                    v.w = e[6] | ((uint32_t)e[7] << 16);
-                }
-            }
-            *(uint4 *)(a_lds + r * PASS_D + x) = v;
+        for (int i = 0; i < 2 * M; i++) {
+            const uint32_t idx = t + 256 * i;
+            *(uint4 *)(a_lds + (idx / 512) * PASS_D + (idx % 512) * 8) = areg[i];
         }
         __syncthreads();
         // 3. dequant + dot
 #pragma unroll
         for (int p = 0; p < P; p++) {
-            uint32_t kc = kc0 + kl * P + p;
+            const uint32_t kc = kc0 + kl * P + p;
             if (kc >= g.nchunks) break;
             const uint32_t kcl = kl * P + p;  // chunk within pass
-            uint32_t words[4] = {wq[p].x, wq[p].y, wq[p].z, wq[p].w};
+            const uint32_t words[4] = {wq[p].x, wq[p].y, wq[p].z, wq[p].w};
 #pragma unroll
             for (int w = 0; w < 4; w++) {
                 uint4 av[M];
 #pragma unroll
                 for (int r = 0; r < M; r++)
                     av[r] = *(const uint4 *)(a_lds + r * PASS_D + kcl * Q4_CHUNK + w * 8);
-                uint32_t q = words[w] ^ 0x88888888u;  // nibble -> code + 8
+                const uint32_t q = words[w];  // stored nibbles are code + 8
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    uint32_t u = (q >> (4 * e)) & 0x000F000Fu;
-                    uint32_t wpair;
-                    if (FAST) {
-                        half2_t h = __builtin_bit_cast(half2_t, u | 0x64006400u);
-                        const half2_t magic = {(_Float16)1032.0f, (_Float16)1032.0f};
-                        _Float16 s = __builtin_bit_cast(_Float16, sv[p]);
-                        half2_t s2 = {s, s};
-                        half2_t wv = (h - magic) * s2;
-                        wpair = __builtin_bit_cast(uint32_t, wv);
-                    } else {
-                        int c0 = (int)(u & 0xF) - 8;
-                        int c1 = (int)(u >> 16) - 8;
-                        uint32_t dp = kc * Q4_CHUNK + w * 8 + 2 * e;  // depth of c0
-                        uint16_t s0, s1, m0 = 0, m1 = 0;
-                        if (block >= Q4_CHUNK) {
-                            s0 = s1 = sv[p];
-                            if (AFFINE) m0 = m1 = mv[p];
-                        } else {
-                            uint32_t b0 = dp >> g.block_shift, b1 = (dp + 1) >> g.block_shift;
-                            s0 = g.sc[(size_t)b0 * g.n_pad + j];
-                            s1 = g.sc[(size_t)b1 * g.n_pad + j];
-                            if (AFFINE) {
-                                m0 = g.mn[(size_t)b0 * g.n_pad + j];
-                                m1 = g.mn[(size_t)b1 * g.n_pad + j];
-                            }
+                    const uint32_t u = (q >> (4 * e)) & 0x000F000Fu;
+                    const int c0 = (int)(u & 0xF) - 8;
+                    const int c1 = (int)(u >> 16) - 8;
+                    const uint32_t dp = kc * Q4_CHUNK + w * 8 + 2 * e;  // depth of c0
+                    uint16_t s0 = sv[p], s1 = sv[p], m0 = mv[p], m1 = mv[p];
+                    if (block < Q4_CHUNK) {
+                        const uint32_t b0 = dp >> g.block_shift, b1 = (dp + 1) >> g.block_shift;
+                        s0 = g.sc[(size_t)b0 * g.n_pad + j];
+                        s1 = g.sc[(size_t)b1 * g.n_pad + j];
+                        if (AFFINE) {
+                            m0 = g.mn[(size_t)b0 * g.n_pad + j];
+                            m1 = g.mn[(size_t)b1 * g.n_pad + j];
                         }
-                        wpair = deq_pair_generic<BF16, AFFINE>(c0, c1, s0, s1, m0, m1);
                     }
+                    const uint32_t wpair = deq_pair_generic<BF16, AFFINE>(c0, c1, s0, s1, m0, m1);
 #pragma unroll
                     for (int r = 0; r < M; r++) {
-                        uint32_t a2 = e == 0 ? av[r].x : e == 1 ? av[r].y : e == 2 ? av[r].z : av[r].w;
+                        const uint32_t a2 = e == 0 ? av[r].x : e == 1 ? av[r].y : e == 2 ? av[r].z : av[r].w;
                         acc[r] = dot2<BF16>(a2, wpair, acc[r]);
                     }
                 }
@@ -214,24 +311,32 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4GemvArgs g, EpArgs ep) {
     }
 }
 
-template <int M, bool BF16, bool AFFINE, bool FAST>
-hipError_t launch_m(const Q4GemvArgs &g, const EpArgs &ep, hipStream_t s) {
+template <int M, bool BF16, bool AFFINE>
+hipError_t launch_generic(const Q4GemvArgs &g, const EpArgs &ep, hipStream_t s) {
     size_t lds = (size_t)M * PASS_D * 2;
-    size_t red = (size_t)KL * M * TN * 4;
+    const size_t red = (size_t)KL * M * TN * 4;
     if (red > lds) lds = red;
-    dim3 grid(g.n_pad / TN);
-    hipLaunchKernelGGL((q4_gemv_kernel<M, BF16, AFFINE, FAST>), grid, dim3(256), lds, s, g, ep);
+    hipLaunchKernelGGL((q4_gemv_kernel<M, BF16, AFFINE>), dim3(g.n_pad / TN), dim3(256), lds, s,
+                       g, ep);
     return hipGetLastError();
 }
 
 template <int M>
 hipError_t launch_variant(const Q4GemvArgs &g, const EpArgs &ep, bool bf16, bool affine,
-                          bool big_block, hipStream_t s) {
-    if (!bf16 && !affine && big_block) return launch_m<M, false, false, true>(g, ep, s);
-    if (!bf16 && !affine) return launch_m<M, false, false, false>(g, ep, s);
-    if (!bf16) return launch_m<M, false, true, false>(g, ep, s);
-    if (!affine) return launch_m<M, true, false, false>(g, ep, s);
-    return launch_m<M, true, true, false>(g, ep, s);
+                          hipStream_t s) {
+    if (!bf16 && !affine) return launch_generic<M, false, false>(g, ep, s);
+    if (!bf16) return launch_generic<M, false, true>(g, ep, s);
+    if (!affine) return launch_generic<M, true, false>(g, ep, s);
+    return launch_generic<M, true, true>(g, ep, s);
+}
+
+template <int MR>
+hipError_t launch_mfma(const Q4GemvArgs &g, const EpArgs &ep, hipStream_t s) {
+    size_t lds = (size_t)MR * MF_SEG * 2;
+    const size_t red = (size_t)MF_WAVES * 16 * MR * 4;
+    if (red > lds) lds = red;
+    hipLaunchKernelGGL((q4_gemv_mfma<MR>), dim3(g.n_pad / 16), dim3(MF_WAVES * 64), lds, s, g, ep);
+    return hipGetLastError();
 }
 
 }  // namespace
@@ -251,11 +356,23 @@ hipError_t launch_q4_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t
     g.m = (uint32_t)m;
     g.block_shift = (uint32_t)__builtin_ctzll(w.block);
     const bool affine = w.mins != nullptr;
-    const bool big = w.block >= (size_t)Q4_CHUNK;
-    if (m <= 1) return launch_variant<1>(g, ep, bf16, affine, big, s);
-    if (m <= 2) return launch_variant<2>(g, ep, bf16, affine, big, s);
-    if (m <= 4) return launch_variant<4>(g, ep, bf16, affine, big, s);
-    return launch_variant<8>(g, ep, bf16, affine, big, s);
+    if ((size_t)m * w.k * 2 >= ((size_t)1 << 31)) return hipErrorInvalidValue;  // buffer range
+    if (w.nchunks == 0) {
+        // k == 0: every product is the empty sum; the generic kernel runs no
+        // pass and stores ep(+0)
+        if (m <= 1) return launch_generic<1, false, false>(g, ep, s);
+        return launch_generic<8, false, false>(g, ep, s);
+    }
+    if (!bf16 && !affine && w.block >= (size_t)Q4_CHUNK) {
+        if (m <= 1) return launch_mfma<1>(g, ep, s);
+        if (m <= 2) return launch_mfma<2>(g, ep, s);
+        if (m <= 4) return launch_mfma<4>(g, ep, s);
+        return launch_mfma<8>(g, ep, s);
+    }
+    if (m <= 1) return launch_variant<1>(g, ep, bf16, affine, s);
+    if (m <= 2) return launch_variant<2>(g, ep, bf16, affine, s);
+    if (m <= 4) return launch_variant<4>(g, ep, bf16, affine, s);
+    return launch_variant<8>(g, ep, bf16, affine, s);
 }
 
 }  // namespace smg

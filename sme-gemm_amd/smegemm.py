@@ -49,6 +49,14 @@ def lib() -> C.CDLL:
         return _lib
     if not os.path.exists(_LIBPATH):
         raise SmeGemmError(f"{_LIBPATH} is not built (run make -C {_HERE})")
+    # PyTorch-ROCm ships its own libamdhip64; loading torch first makes this
+    # library resolve to that same runtime, so one HIP runtime serves the
+    # process and torch streams / device pointers are valid here. (With two
+    # runtimes loaded, the second one to initialise sees no GPU.)
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = C.CDLL(_LIBPATH)
     W = C.POINTER(C.c_void_p)
     L.smg_available.restype = C.c_int

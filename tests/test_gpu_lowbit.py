@@ -199,14 +199,22 @@ def test_mopa_matches_eager_dequant(smg, orc, si, bi, block):
     bias = orc.f32_to_f16(np.arange(n, dtype=np.float32) * np.float32(0.01) - np.float32(1.0))
     q2 = smg.Q2Weights(codes, scales, n, k, smg.Q2Params(block).with_codebook(book))
     q1 = smg.Q1Weights(signs, scales, smg.WeightLayout.OutIn, n, k, block)
-    for ei in range(2):
-        ep = smg.Epilogue() if ei == 0 else smg.Epilogue().add_col(bias).silu()
-        nodes, act = ([], None) if ei == 0 else ([(4, 0, 0.0, bias, 0)], 3)
-        got = np.zeros(m * n, np.uint16)
-        smg.matmul_q2_mopa_ep(a, q2, got, m, ep)
-        want = orc.matmul_lowbit_mopa_ep(2, a, codes, scales, m, n, k, block, nodes, act, book)
-        assert max_rel(got, want) <= f16_tol(k), f"q2 mopa ep {ei}"
-        got = np.zeros(m * n, np.uint16)
-        smg.matmul_q1_mopa_ep(a, q1, got, m, ep)
-        want = orc.matmul_lowbit_mopa_ep(1, a, signs, scales, m, n, k, block, nodes, act)
-        assert max_rel(got, want) <= f16_tol(k), f"q1 mopa ep {ei}"
+    # plain product within tolerance of the oracle; the fused epilogue equals
+    # the scalar op-graph applied to the GPU's own plain product, bit for bit
+    # (as q2.rs:83 checks it): a 1-ulp flip of the rounded sum must not be
+    # amplified by add_col cancellation into a tolerance failure
+    ep = smg.Epilogue().add_col(bias).silu()
+    nodes, act = [(4, 0, 0.0, bias, 0)], 3
+    for kind, w, codes_ in ((2, q2, codes), (1, q1, signs)):
+        plain = np.zeros(m * n, np.uint16)
+        fused = np.zeros(m * n, np.uint16)
+        if kind == 2:
+            smg.matmul_q2_mopa(a, w, plain, m)
+            smg.matmul_q2_mopa_ep(a, w, fused, m, ep)
+            want = orc.matmul_lowbit_mopa_ep(2, a, codes_, scales, m, n, k, block, (), None, book)
+        else:
+            smg.matmul_q1_mopa(a, w, plain, m)
+            smg.matmul_q1_mopa_ep(a, w, fused, m, ep)
+            want = orc.matmul_lowbit_mopa_ep(1, a, codes_, scales, m, n, k, block)
+        assert max_rel(plain, want) <= f16_tol(k), f"q{kind} mopa plain"
+        assert np.array_equal(fused, orc.apply_ep(plain, m, n, nodes, act)), f"q{kind} mopa ep"
