@@ -295,27 +295,22 @@ int make_lowbit(int kind, Get get, const uint16_t *scales, bool band_scales,
         return fail(SMG_EINVAL, "low-bit block size must be a power of two from 16 to 65536");
     smg_weights *w = new_weights(kind, n, k, block);
     WDev &d = w->d;
-    const size_t ch = kind == W_Q2 ? Q2_CHUNK : Q1_CHUNK;
-    d.nchunks = (k + ch - 1) / ch;
+    const size_t grp = kind == W_Q2 ? Q2_GROUP : Q1_GROUP;
+    d.nchunks = (k + grp - 1) / grp;  // lane groups along K
     const size_t nbk = (k + block - 1) / block;
-    d.sc_rows = std::max(nbk, (d.nchunks * ch + block - 1) / block);
+    d.sc_rows = std::max(nbk, (d.nchunks * grp + block - 1) / block);
     d.k_pad = round_up(k ? k : 1, 64);
     if (kind == W_Q2)
         d.codebook = (uint32_t)(uint8_t)codebook[0] | ((uint32_t)(uint8_t)codebook[1] << 8) |
                      ((uint32_t)(uint8_t)codebook[2] << 16) | ((uint32_t)(uint8_t)codebook[3] << 24);
-    std::vector<uint8_t> codes(d.nchunks * d.n_pad * 16, 0);
+    std::vector<uint8_t> codes(d.nchunks * d.n_pad * 64, 0);
     for (size_t dd = 0; dd < k; dd++) {
-        const size_t kc = dd / ch, x = dd % ch;
-        size_t bitpos;
-        if (kind == W_Q2) {
-            const size_t wd = x / 16, i = (x % 16) / 4, b = x % 4;
-            bitpos = wd * 32 + 8 * b + 2 * i;
-        } else {
-            const size_t wd = x / 32, i = (x % 32) / 4, b = x % 4;
-            bitpos = wd * 32 + 8 * b + i;
+        const uint32_t bit = kind == W_Q2 ? lb_bit<2>(dd) : lb_bit<1>(dd);
+        for (size_t j = 0; j < n; j++) {
+            const size_t off = kind == W_Q2 ? lb_dword_offset<2>(dd, j, d.n_pad)
+                                            : lb_dword_offset<1>(dd, j, d.n_pad);
+            codes[off + bit / 8] |= (uint8_t)(get(dd, j) << (bit % 8));
         }
-        for (size_t j = 0; j < n; j++)
-            codes[(kc * d.n_pad + j) * 16 + bitpos / 8] |= (uint8_t)(get(dd, j) << (bitpos % 8));
     }
     std::vector<uint16_t> sc(d.sc_rows * d.n_pad, 0);
     for (size_t j = 0; j < n; j++)
@@ -539,7 +534,7 @@ int smg_weights_clone(const smg_weights *w, smg_weights **out) {
         const void *src;
         size_t bytes;
     };
-    const size_t code_bytes = w->d.nchunks * w->d.n_pad * 16;
+    const size_t code_bytes = w->d.nchunks * w->d.n_pad * (w->d.kind == W_Q4 ? 16 : 64);
     const size_t sc_bytes = w->d.sc_rows * w->d.n_pad * 2;
     const size_t dense_bytes = w->d.n_pad * w->d.k_pad * 2;
     const Field f[4] = {{w->d.codes, code_bytes}, {w->d.scales, sc_bytes},

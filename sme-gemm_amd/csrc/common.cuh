@@ -263,16 +263,40 @@ __device__ __forceinline__ uint16_t finish(const EpArgs &ep, float acc, size_t i
 // the reference's nibble (code two's complement, q4/mod.rs:213-214).
 // Scales (and mins): row kb = d/block of an [n_sc_rows][n_pad] f16 array.
 //
-// Q2: chunks of 64 depths (16 bytes) at (kc*n_pad + j)*16; dword w holds
-// depths 16w..16w+15 with depth 16w+4i+b at byte b, bits 2i..2i+1, so
-// ((dword >> 2i) & 0x03030303) gives the codes of depths 16w+4i..+3 as bytes.
-// Q1: chunks of 128 depths; dword w holds depths 32w..32w+31 with depth
-// 32w+4i+b at byte b, bit i, so ((dword >> i) & 0x01010101) gives the sign
-// bits of depths 32w+4i..+3 as 0/1 bytes.
-// Low-bit scales: [nbk][n_pad] f16.
+// Low-bit (Q2 / Q1) layouts are cut for v_mfma_i32_16x16x64_i8, whose A
+// operand gives each lane 16 depths of one column: K is split into 64-depth
+// slabs, a slab into four 16-depth quarters g. A "group" is the 16 bytes one
+// lane loads: quarter g of several consecutive slabs of one column. Group
+// (q, column j, quarter g) sits at byte ((q*n_pad + j)*4 + g)*16, so the four
+// quarters of a column are 64 contiguous bytes and 16 columns are 1 KB.
+// Q2: a group covers 4 slabs (256 depths); dword u is slab 4q+u, quarter g,
+//   depth 16g+4i+b of the slab at byte b, bits 2i..2i+1, so
+//   ((dword >> 2i) & 0x03030303) gives 4 consecutive depths' codes as bytes.
+// Q1: a group covers 8 slabs (512 depths); dword u holds slabs 8q+2u (bit i of
+//   byte b = depth 16g+4i+b, i < 4) and 8q+2u+1 (bit 4+i of byte b), so
+//   ((dword >> i) & 0x01010101) gives 4 consecutive sign bits as 0/1 bytes.
+// Low-bit scales: [sc_rows][n_pad] f16, row = block.
 // ---------------------------------------------------------------------------
-constexpr int Q4_CHUNK = 32;   // depths per 16-byte Q4 chunk
-constexpr int Q2_CHUNK = 64;   // depths per 16-byte Q2 chunk
-constexpr int Q1_CHUNK = 128;  // depths per 16-byte Q1 chunk
+constexpr int Q4_CHUNK = 32;    // depths per 16-byte Q4 chunk
+constexpr int LB_SLAB = 64;     // depths per MFMA K step
+constexpr int Q2_GROUP = 256;   // depths per 16-byte Q2 lane group
+constexpr int Q1_GROUP = 512;   // depths per 16-byte Q1 lane group
+
+// Byte offset of the dword holding (depth d, column j) in a low-bit layout,
+// and the bit of depth d inside that dword.
+template <int KIND>
+__host__ __device__ __forceinline__ size_t lb_dword_offset(size_t d, size_t j, size_t n_pad) {
+    const size_t grp = KIND == 2 ? Q2_GROUP : Q1_GROUP;
+    const size_t q = d / grp, slab = (d % grp) / LB_SLAB, g = (d % LB_SLAB) / 16;
+    const size_t u = KIND == 2 ? slab : slab / 2;
+    return ((q * n_pad + j) * 4 + g) * 16 + u * 4;
+}
+template <int KIND>
+__host__ __device__ __forceinline__ uint32_t lb_bit(size_t d) {
+    const uint32_t x = (uint32_t)(d % 16), i = x / 4, b = x % 4;
+    if (KIND == 2) return 8 * b + 2 * i;
+    const uint32_t h = (uint32_t)((d % Q1_GROUP) / LB_SLAB) % 2;
+    return 8 * b + 4 * h + i;
+}
 
 }  // namespace smg

@@ -83,24 +83,23 @@ __device__ __forceinline__ void b_load(const GemmArgs &g, uint32_t col0, uint32_
     }
     const uint32_t col = col0 + t % 128;
     const uint32_t d = k0 + (t / 128) * 32;  // first depth of the unit
-    constexpr uint32_t CH = WK == W_Q4 ? 32 : WK == W_Q2 ? 64 : 128;
+    constexpr uint32_t CH = WK == W_Q4 ? Q4_CHUNK : WK == W_Q2 ? Q2_GROUP : Q1_GROUP;
     // Branch-free: a chunk past K loads the last chunk (a valid address) and
-    // its scale is forced to 0, so its weights are +-0.
+    // its scale is forced to 0, so its weights are +-0. (Low-bit groups cover
+    // K in multiples of 256 depths, so only Q4 ever has a dead chunk.)
     const uint32_t kc = d / CH;
     const bool live = kc < g.nchunks;
     const uint32_t kcc = live ? kc : g.nchunks - 1;
-    const uint8_t *base = g.codes + ((size_t)kcc * g.n_pad + col) * 16;
+    const uint32_t dc = kcc * CH + d % CH;
     r.raw[0] = make_uint4(0, 0, 0, 0);
     if (WK == W_Q4) {
-        r.raw[0] = *(const uint4 *)base;
-    } else if (WK == W_Q2) {
-        const uint2 v = *(const uint2 *)(base + ((d % 64) / 32) * 8);
-        r.raw[0].x = v.x;
-        r.raw[0].y = v.y;
+        r.raw[0] = *(const uint4 *)(g.codes + ((size_t)kcc * g.n_pad + col) * 16);
     } else {
-        r.raw[0].x = *(const uint32_t *)(base + ((d % 128) / 32) * 4);
+        // quarters g and g+1 of the unit's slab: two dwords 16 bytes apart
+        const uint8_t *p = g.codes + lb_dword_offset<WK == W_Q2 ? 2 : 1>(dc, col, g.n_pad);
+        r.raw[0].x = *(const uint32_t *)p;
+        r.raw[0].y = *(const uint32_t *)(p + 16);
     }
-    const uint32_t dc = kcc * CH + d % CH;
     r.s = 0;
     r.mn = 0;
     if (g.block_shift >= 5) {
@@ -197,23 +196,28 @@ __device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, uint32
             }
         }
     } else {
-        // Q1: +scale for a set bit, -scale otherwise (exact)
-        const uint32_t word = r.raw[0].x;
+        // Q1: +scale for a set bit, -scale otherwise (exact). Each dword holds
+        // two slabs; this unit's slab is bit-half hs.
+        const uint32_t words[2] = {r.raw[0].x, r.raw[0].y};
+        const uint32_t hs = ((d0 % Q1_GROUP) / LB_SLAB) % 2;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t bits = (word >> i) & 0x01010101u;
-            uint16_t h[4];
+        for (int w = 0; w < 2; w++) {
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const uint32_t dp = d0 + 4 * i + b;
-                const uint16_t sb = g.block_shift >= 5
-                                        ? r.s
-                                        : g.sc[(size_t)(dp >> g.block_shift) * g.n_pad + col];
-                const uint32_t bit = (bits >> (8 * b)) & 1u;
-                h[b] = bit ? sb : (uint16_t)(sb ^ 0x8000u);
+            for (int i = 0; i < 4; i++) {
+                const uint32_t bits = (words[w] >> (4 * hs + i)) & 0x01010101u;
+                uint16_t h[4];
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const uint32_t dp = d0 + w * 16 + 4 * i + b;
+                    const uint16_t sb = g.block_shift >= 5
+                                            ? r.s
+                                            : g.sc[(size_t)(dp >> g.block_shift) * g.n_pad + col];
+                    const uint32_t bit = (bits >> (8 * b)) & 1u;
+                    h[b] = bit ? sb : (uint16_t)(sb ^ 0x8000u);
+                }
+                out[w * 8 + 2 * i] = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+                out[w * 8 + 2 * i + 1] = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
             }
-            out[2 * i] = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
-            out[2 * i + 1] = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
         }
     }
     // Q1/Q2 depth order inside out[]: depth 4i+b sits at half-word 4i+b, i.e.
