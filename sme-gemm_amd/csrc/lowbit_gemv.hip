@@ -53,8 +53,8 @@ template <int KIND, int MR>
 __global__ void __launch_bounds__(T) lowbit_gemv(LbArgs g, EpArgs ep) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t block = 1u << g.block_shift;
-    const uint32_t unit = block > (uint32_t)LB_SLAB ? block : (uint32_t)LB_SLAB;
-    const uint32_t nbs = g.seg_depths >> g.block_shift;  // block slots per segment
+    // block slots per segment (1 when blocks are longer than a segment)
+    const uint32_t nbs = g.seg_depths >= block ? g.seg_depths >> g.block_shift : 1;
     int32_t *S = (int32_t *)smem;                        // [nbs][16][MR]
     uint16_t *scl = (uint16_t *)(smem + (size_t)nbs * 16 * MR * 4);  // [nbs][16]
     float *sa = (float *)(scl + nbs * 16);               // [MR][nbs]
@@ -82,11 +82,16 @@ __global__ void __launch_bounds__(T) lowbit_gemv(LbArgs g, EpArgs ep) {
     for (uint32_t seg = 0; seg < nseg; seg++) {
         const uint32_t d0 = seg * g.seg_depths;
         const uint32_t dl = min(g.seg_depths, g.k - d0);
-        const uint32_t nu = (dl + unit - 1) / unit;  // units in the segment
-        // this wave's contiguous unit range
-        const uint32_t ua = (nu * wave) / WV, ub = (nu * (wave + 1)) / WV;
-        const uint32_t sa0 = d0 / LB_SLAB + ua * (unit / LB_SLAB);  // first slab (global)
-        const uint32_t ns = (ub - ua) * (unit / LB_SLAB);           // slabs of this wave
+        // blocks overlapping the segment; a block longer than a segment keeps
+        // its slot-0 partial sum from the segment before
+        const uint32_t b0 = d0 >> g.block_shift;
+        const uint32_t nb = ((d0 + dl - 1) >> g.block_shift) - b0 + 1;
+        const bool carry = (d0 & (block - 1)) != 0;
+        const bool block_done = ((d0 + dl) & (block - 1)) == 0 || d0 + dl == g.k;
+        // this wave's contiguous slab range
+        const uint32_t nslab = (dl + LB_SLAB - 1) / LB_SLAB;
+        const uint32_t sa0 = d0 / LB_SLAB + (nslab * wave) / WV;
+        const uint32_t ns = (nslab * (wave + 1)) / WV - (nslab * wave) / WV;  // <= MAXS
         // -- 1. loads: activations (B operand), weights (A operand), then the
         //       fold's scales; all in flight before anything waits
         uint4 qreg[MAXS];
@@ -101,69 +106,74 @@ __global__ void __launch_bounds__(T) lowbit_gemv(LbArgs g, EpArgs ep) {
             wreg[i] = *(const uint32_t *)(g.codes +
                                           lb_dword_offset<KIND>((size_t)sl * LB_SLAB + 16 * gq4, col, g.n_pad));
         }
-        const uint32_t b0 = d0 >> g.block_shift;
-        const uint32_t nb = (dl + block - 1) >> g.block_shift;  // real blocks in segment
         // scales of the 16 columns (32 bytes a block), activation scales, sums
         constexpr int RS = 4;  // up to 4 x 512 x 16 B = 32 KB of scale rows
         uint4 sreg[RS];
 #pragma unroll
         for (int r = 0; r < RS; r++) {
-            const uint32_t i = t + T * r, b = i / 2, half = i % 2;
-            sreg[r] = bload16(sr, b < nb ? ((b0 + b) * g.n_pad + col0) * 2u + half * 16u : OOB);
+            const uint32_t i = t + T * r, bb = i / 2, half = i % 2;
+            sreg[r] = bload16(sr, bb < nb ? ((b0 + bb) * g.n_pad + col0) * 2u + half * 16u : OOB);
         }
         float fsa[2];
         int32_t fas[2];
 #pragma unroll
         for (int r = 0; r < 2; r++) {
-            const uint32_t i = t + T * r, rr = i / nbs, b = i % nbs;
-            const bool ok = rr < mr && b < nb && i < MR * nbs;
+            const uint32_t i = t + T * r, rr = i / nbs, bb = i % nbs;
+            const bool ok = rr < mr && bb < nb && i < MR * nbs;
             fsa[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                fr, ok ? ((row0 + rr) * g.nbq + b0 + b) * 4u : OOB, 0, 0));
+                fr, ok ? ((row0 + rr) * g.nbq + b0 + bb) * 4u : OOB, 0, 0));
             fas[r] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(
-                ur, ok ? ((row0 + rr) * g.nbq + b0 + b) * 4u : OOB, 0, 0);
+                ur, ok ? ((row0 + rr) * g.nbq + b0 + bb) * 4u : OOB, 0, 0);
         }
-        // -- 2. block sums on the matrix cores
+        // zero the block sums (not a carried slot)
+        for (uint32_t i = t; i < nbs * 16 * MR; i += T)
+            if (!(carry && i < 16 * MR)) S[i] = 0;
+        __syncthreads();
+        // -- 2. block sums on the matrix cores; partial sums of a block split
+        //       between waves meet in LDS through integer atomics (exact)
         const uint32_t parts = block < (uint32_t)LB_SLAB ? LB_SLAB / block : 1;
         const uint32_t spb = block > (uint32_t)LB_SLAB ? block / LB_SLAB : 1;  // slabs per block
         int4_t acc = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < MAXS; i++) {
             if ((uint32_t)i < ns) {  // uniform
-            const uint32_t slab = sa0 + i;
-            int4_t wa;
-            if (KIND == 2) {
+                const uint32_t slab = sa0 + i;
+                int4_t wa;
+                if (KIND == 2) {
 #pragma unroll
-                for (int j = 0; j < 4; j++)
-                    wa[j] = (int)__builtin_amdgcn_perm(g.codebook, g.codebook,
-                                                       (wreg[i] >> (2 * j)) & 0x03030303u);
-            } else {
-                const uint32_t hs = 4 * (((slab * LB_SLAB) % Q1_GROUP) / LB_SLAB % 2);
+                    for (int j = 0; j < 4; j++)
+                        wa[j] = (int)__builtin_amdgcn_perm(g.codebook, g.codebook,
+                                                           (wreg[i] >> (2 * j)) & 0x03030303u);
+                } else {
+                    const uint32_t hs = 4 * (((slab * LB_SLAB) % Q1_GROUP) / LB_SLAB % 2);
 #pragma unroll
-                for (int j = 0; j < 4; j++) wa[j] = (int)((wreg[i] >> (hs + j)) & 0x01010101u);
-            }
-            const int4_t ab = __builtin_bit_cast(int4_t, qreg[i]);
-            for (uint32_t p = 0; p < parts; p++) {
-                int4_t abp = ab;
-                if (parts > 1 && (uint32_t)(16 * gq4) / block != p) abp = (int4_t){0, 0, 0, 0};
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, abp, acc, 0, 0, 0);
-                const bool ends = parts > 1 || ((i + 1) % spb) == 0;  // uniform
-                if (ends) {
-                    // block (within the segment) of this MFMA
-                    const uint32_t bl = ((slab * LB_SLAB + p * (parts > 1 ? block : 0)) >> g.block_shift) - b0;
-                    if ((uint32_t)c < mr) {
+                    for (int j = 0; j < 4; j++) wa[j] = (int)((wreg[i] >> (hs + j)) & 0x01010101u);
+                }
+                const int4_t ab = __builtin_bit_cast(int4_t, qreg[i]);
+                for (uint32_t p = 0; p < parts; p++) {
+                    int4_t abp = ab;
+                    if (parts > 1 && (uint32_t)(16 * gq4) / block != p) abp = (int4_t){0, 0, 0, 0};
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, abp, acc, 0, 0, 0);
+                    // flush at a block's end or at the end of this wave's range
+                    const bool flush = parts > 1 || ((slab + 1) % spb) == 0 || (uint32_t)i + 1 == ns;
+                    if (flush) {  // uniform
+                        const uint32_t bl =
+                            ((slab * LB_SLAB + p * (parts > 1 ? block : 0)) >> g.block_shift) - b0;
+                        if ((uint32_t)c < mr) {
 #pragma unroll
-                        for (int v = 0; v < 4; v++) S[(bl * 16 + 4 * gq4 + v) * MR + c] = acc[v];
+                            for (int v = 0; v < 4; v++)
+                                atomicAdd(&S[(bl * 16 + 4 * gq4 + v) * MR + c], acc[v]);
+                        }
+                        acc = (int4_t){0, 0, 0, 0};
                     }
-                    acc = (int4_t){0, 0, 0, 0};
                 }
             }
-            }
         }
-        // -- 3. stage the fold's operands, then fold in block order
+        // -- 3. stage the fold's operands, then fold the finished blocks in order
 #pragma unroll
         for (int r = 0; r < RS; r++) {
-            const uint32_t i = t + T * r, b = i / 2, half = i % 2;
-            if (b < nb) *(uint4 *)(scl + b * 16 + half * 8) = sreg[r];
+            const uint32_t i = t + T * r, bb = i / 2, half = i % 2;
+            if (bb < nb) *(uint4 *)(scl + bb * 16 + half * 8) = sreg[r];
         }
 #pragma unroll
         for (int r = 0; r < 2; r++) {
@@ -175,10 +185,12 @@ __global__ void __launch_bounds__(T) lowbit_gemv(LbArgs g, EpArgs ep) {
         }
         __syncthreads();
         if (folder) {
-            for (uint32_t b = 0; b < nb; b++) {
-                int32_t sum = S[(b * 16 + fc) * MR + frow];
-                if (KIND == 1) sum = 2 * sum - as[frow * nbs + b];
-                const float scv = f16_to_f32(scl[b * 16 + fc]) * sa[frow * nbs + b];
+            // the last block waits for its remaining depths when it continues
+            const uint32_t nfold = block_done ? nb : nb - 1;
+            for (uint32_t bb = 0; bb < nfold; bb++) {
+                int32_t sum = S[(bb * 16 + fc) * MR + frow];
+                if (KIND == 1) sum = 2 * sum - as[frow * nbs + bb];
+                const float scv = f16_to_f32(scl[bb * 16 + fc]) * sa[frow * nbs + bb];
                 total = fmaf((float)sum, scv, total);
             }
         }
@@ -258,19 +270,18 @@ Geo geometry(const WDev &w, size_t m) {
     if (ge.kq == 0) ge.kq = ge.unit;
     ge.nbq = ge.kq / w.block;
     const int mr = rows_per_group(m);
-    // a segment: at most MAXS slabs per wave, and its block sums fit S_BUDGET
+    // a segment: at most MAXS slabs per wave; its block sums fit S_BUDGET and
+    // its block scales the staging registers (blocks may be longer than it)
     size_t seg = (size_t)WV * MAXS * LB_SLAB;
-    while (seg > ge.unit && (seg / w.block) * 16 * mr * 4 > (size_t)S_BUDGET) seg /= 2;
-    if (seg < ge.unit) seg = ge.unit;
-    // a segment never holds more blocks than the scale staging covers
-    while (seg > ge.unit && seg / w.block > 4 * T / 2) seg /= 2;
+    while (seg > (size_t)LB_SLAB && (seg / w.block) * 16 * mr * 4 > (size_t)S_BUDGET) seg /= 2;
+    while (seg > (size_t)LB_SLAB && seg / w.block > 2 * (size_t)T / mr) seg /= 2;
     ge.seg = seg;
     return ge;
 }
 
 template <int KIND, int MR>
 hipError_t launch_t(const LbArgs &g, const EpArgs &ep, hipStream_t s) {
-    const size_t nbs = (size_t)g.seg_depths >> g.block_shift;
+    const size_t nbs = g.seg_depths >= (1u << g.block_shift) ? (size_t)g.seg_depths >> g.block_shift : 1;
     const size_t lds = nbs * 16 * MR * 4 + nbs * 16 * 2 + 2 * MR * nbs * 4;
     static bool attr = false;  // benign race: every setter writes the same value
     if (!attr) {
