@@ -140,7 +140,15 @@ int ep_args(const ep_desc16 *ep, EpArgs *out) {
     if (!ep || ep->n_nodes == 0) return SMG_OK;
     if (ep->n_nodes > SMG_MAX_EP_NODES) return fail(SMG_EINVAL, "epilogue has too many nodes");
     out->n_nodes = ep->n_nodes;
-    for (uint32_t i = 0; i < ep->n_nodes; i++) out->nodes[i] = ep->nodes[i];
+    for (uint32_t i = 0; i < ep->n_nodes; i++) {
+        const EpNode &nd = ep->nodes[i];
+        if (ep_family(nd.op) == EPF_NONE) return fail(SMG_EINVAL, "epilogue node has an unknown op");
+        if (nd.op == EP_OP_ACT && nd.aux > EP_ACT_GELU_EXACT)
+            return fail(SMG_EINVAL, "epilogue node has an unknown activation");
+        out->nodes[i] = nd;
+        out->fam[i] = (uint8_t)ep_family(nd.op);
+        out->cls[i] = (uint8_t)ep_class(nd.op);
+    }
     return SMG_OK;
 }
 

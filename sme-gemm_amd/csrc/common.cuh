@@ -108,6 +108,8 @@ struct EpArgs {
     uint32_t n_nodes;
     uint32_t pad;
     EpNode nodes[SMG_MAX_EP_NODES];
+    uint8_t fam[SMG_MAX_EP_NODES];  // ep_family(nodes[i].op), filled on the host
+    uint8_t cls[SMG_MAX_EP_NODES];  // ep_class(nodes[i].op)
 };
 
 // maxNum / minNum with IEEE 754-2019 maximumNumber / minimumNumber results: a
@@ -140,7 +142,7 @@ __device__ __forceinline__ double clampd(double x, double lo, double hi) {
 
 // act_apply_f64_a (src/epilogue/mod.rs:40-84), evaluated in f64 with the
 // same operation order as the Rust expressions.
-__device__ __noinline__ double act_f64(uint32_t kind, double x, double alpha) {
+__device__ __forceinline__ double act_f64_body(uint32_t kind, double x, double alpha) {
     switch (kind) {
     case 1: return maxnumd(x, 0.0);
     case 2: {
@@ -185,8 +187,95 @@ __device__ __noinline__ double act_f64(uint32_t kind, double x, double alpha) {
     }
 }
 
+// One out-of-line copy for per-cell use (GEMV stores).
+__device__ __noinline__ double act_f64(uint32_t kind, double x, double alpha) {
+    return act_f64_body(kind, x, alpha);
+}
+
 __device__ __forceinline__ float act_f32(uint32_t kind, float x, float alpha) {
     return (float)act_f64(kind, (double)x, (double)alpha);
+}
+
+// Eight cells at once (GEMM stores): one call per 8 cells, the kind switch
+// taken once and each case's f64 formula inlined for a constant kind.
+struct F8 {
+    float v[8];
+};
+__device__ __noinline__ F8 act8(uint32_t kind, F8 x, float alpha) {
+    const double a = (double)alpha;
+    switch (kind) {
+#define SMG_ACT8_CASE(K)                                                                  \
+    case K:                                                                               \
+        _Pragma("unroll") for (int e = 0; e < 8; e++)                                     \
+            x.v[e] = (float)act_f64_body(K, (double)x.v[e], a);                           \
+        break;
+        SMG_ACT8_CASE(1) SMG_ACT8_CASE(2) SMG_ACT8_CASE(3) SMG_ACT8_CASE(4) SMG_ACT8_CASE(5)
+        SMG_ACT8_CASE(6) SMG_ACT8_CASE(7) SMG_ACT8_CASE(8) SMG_ACT8_CASE(9) SMG_ACT8_CASE(10)
+        SMG_ACT8_CASE(11) SMG_ACT8_CASE(12) SMG_ACT8_CASE(13) SMG_ACT8_CASE(14)
+        SMG_ACT8_CASE(15) SMG_ACT8_CASE(16) SMG_ACT8_CASE(17) SMG_ACT8_CASE(18)
+        SMG_ACT8_CASE(19) SMG_ACT8_CASE(20) SMG_ACT8_CASE(21) SMG_ACT8_CASE(22)
+        SMG_ACT8_CASE(23) SMG_ACT8_CASE(24)
+#undef SMG_ACT8_CASE
+    default:
+        break;
+    }
+    return x;
+}
+
+// Operand class of an op-graph node: which operand element a cell reads.
+enum EpClass : uint32_t { EPC_SCALAR = 0, EPC_ROW = 1, EPC_COL = 2, EPC_TENSOR = 3 };
+// Arithmetic family of a node.
+enum EpFamily : uint32_t { EPF_ADD = 0, EPF_MUL, EPF_SUB, EPF_DIV, EPF_MAX, EPF_MIN, EPF_ACT, EPF_NONE };
+
+__host__ __device__ constexpr uint32_t ep_class(uint32_t op) {
+    switch (op) {
+    case EP_OP_ADD_ROW: case EP_OP_MUL_ROW: case EP_OP_SUB_ROW: case EP_OP_DIV_ROW:
+    case EP_OP_MAX_ROW: case EP_OP_MIN_ROW:
+        return EPC_ROW;
+    case EP_OP_ADD_COL: case EP_OP_MUL_COL: case EP_OP_SUB_COL: case EP_OP_DIV_COL:
+    case EP_OP_MAX_COL: case EP_OP_MIN_COL:
+        return EPC_COL;
+    case EP_OP_ADD_TENSOR: case EP_OP_MUL_TENSOR: case EP_OP_SUB_TENSOR:
+    case EP_OP_DIV_TENSOR: case EP_OP_MAX_TENSOR: case EP_OP_MIN_TENSOR:
+        return EPC_TENSOR;
+    default:
+        return EPC_SCALAR;  // scalar ops read nd.scalar; ACT reads nothing
+    }
+}
+
+__host__ __device__ constexpr uint32_t ep_family(uint32_t op) {
+    switch (op) {
+    case EP_OP_ADD_SCALAR: case EP_OP_ADD_ROW: case EP_OP_ADD_COL: case EP_OP_ADD_TENSOR:
+        return EPF_ADD;
+    case EP_OP_MUL_SCALAR: case EP_OP_MUL_ROW: case EP_OP_MUL_COL: case EP_OP_MUL_TENSOR:
+        return EPF_MUL;
+    case EP_OP_SUB_SCALAR: case EP_OP_SUB_ROW: case EP_OP_SUB_COL: case EP_OP_SUB_TENSOR:
+        return EPF_SUB;
+    case EP_OP_DIV_SCALAR: case EP_OP_DIV_ROW: case EP_OP_DIV_COL: case EP_OP_DIV_TENSOR:
+        return EPF_DIV;
+    case EP_OP_MAX_SCALAR: case EP_OP_MAX_ROW: case EP_OP_MAX_COL: case EP_OP_MAX_TENSOR:
+        return EPF_MAX;
+    case EP_OP_MIN_SCALAR: case EP_OP_MIN_ROW: case EP_OP_MIN_COL: case EP_OP_MIN_TENSOR:
+        return EPF_MIN;
+    case EP_OP_ACT:
+        return EPF_ACT;
+    default:
+        return EPF_NONE;
+    }
+}
+
+// One non-activation node applied to one value; v is the node's operand (f32
+// of the T element, or the scalar) (src/exec/scalar.rs:28-53).
+__device__ __forceinline__ float ep_arith(uint32_t fam, float x, float v) {
+    switch (fam) {
+    case EPF_ADD: return x + v;
+    case EPF_MUL: return x * v;
+    case EPF_SUB: return x - v;
+    case EPF_DIV: return __fdiv_rn(x, v);
+    case EPF_MAX: return maxnumf(x, v);
+    case EPF_MIN: return minnumf(x, v);
+    default: return x;
+    }
 }
 
 // One cell of the op-graph: x is the f32 value of the already-rounded GEMM
@@ -198,43 +287,14 @@ __device__ float ep_cell(const EpArgs &ep, float x, size_t i, size_t j, size_t n
     for (uint32_t t = 0; t < ep.n_nodes; t++) {
         const EpNode &nd = ep.nodes[t];
         const uint16_t *p = (const uint16_t *)nd.ptr;
-        uint32_t op = nd.op;
-        float v = 0.0f;
-        // operand fetch by class: ROW ops read p[i], COL ops p[j], TENSOR p[i*ld+j]
-        switch (op) {
-        case EP_OP_ADD_ROW: case EP_OP_MUL_ROW: case EP_OP_SUB_ROW: case EP_OP_DIV_ROW:
-        case EP_OP_MAX_ROW: case EP_OP_MIN_ROW:
-            v = to_f32<BF16>(p[i]);
-            break;
-        case EP_OP_ADD_COL: case EP_OP_MUL_COL: case EP_OP_SUB_COL: case EP_OP_DIV_COL:
-        case EP_OP_MAX_COL: case EP_OP_MIN_COL:
-            v = to_f32<BF16>(p[j]);
-            break;
-        case EP_OP_ADD_TENSOR: case EP_OP_MUL_TENSOR: case EP_OP_SUB_TENSOR:
-        case EP_OP_DIV_TENSOR: case EP_OP_MAX_TENSOR: case EP_OP_MIN_TENSOR: {
-            size_t ld = nd.ld == 0 ? n : nd.ld;
-            v = to_f32<BF16>(p[i * ld + j]);
-            break;
-        }
-        default: v = nd.scalar; break;
-        }
-        switch (op) {
-        case EP_OP_ADD_SCALAR: case EP_OP_ADD_ROW: case EP_OP_ADD_COL: case EP_OP_ADD_TENSOR:
-            x = x + v; break;
-        case EP_OP_MUL_SCALAR: case EP_OP_MUL_ROW: case EP_OP_MUL_COL: case EP_OP_MUL_TENSOR:
-            x = x * v; break;
-        case EP_OP_SUB_SCALAR: case EP_OP_SUB_ROW: case EP_OP_SUB_COL: case EP_OP_SUB_TENSOR:
-            x = x - v; break;
-        case EP_OP_DIV_SCALAR: case EP_OP_DIV_ROW: case EP_OP_DIV_COL: case EP_OP_DIV_TENSOR:
-            x = __fdiv_rn(x, v); break;
-        case EP_OP_MAX_SCALAR: case EP_OP_MAX_ROW: case EP_OP_MAX_COL: case EP_OP_MAX_TENSOR:
-            x = maxnumf(x, v); break;
-        case EP_OP_MIN_SCALAR: case EP_OP_MIN_ROW: case EP_OP_MIN_COL: case EP_OP_MIN_TENSOR:
-            x = minnumf(x, v); break;
-        case EP_OP_ACT:
-            x = act_f32(nd.aux, x, nd.scalar); break;
+        float v = nd.scalar;
+        switch (ep.cls[t]) {
+        case EPC_ROW: v = to_f32<BF16>(p[i]); break;
+        case EPC_COL: v = to_f32<BF16>(p[j]); break;
+        case EPC_TENSOR: v = to_f32<BF16>(p[i * (nd.ld == 0 ? n : nd.ld) + j]); break;
         default: break;
         }
+        x = ep.fam[t] == EPF_ACT ? act_f32(nd.aux, x, nd.scalar) : ep_arith(ep.fam[t], x, v);
     }
     return x;
 }

@@ -16,18 +16,20 @@
 // (src/reference.rs:349-387). The store rounds beta*acc to 16 bits and runs the
 // op-graph on that value (src/exec/macros.rs:188-206).
 //
-// Tiling: 128x128 output tile per 256-thread workgroup (2x2 waves of 64x64),
-// K steps of 64 depths, LDS double-buffered so the next tile's global loads
-// and dequant overlap the current tile's MFMAs.
+// Tiling: BM x 128 output tile (BM = 256 with 8 waves, or 128 with 4 waves),
+// every wave a 64 x 64 sub-tile, K in steps of 64 depths. Two register stages
+// and two LDS buffers: the global loads for step k+2 are issued while step k
+// multiplies, and step k+1 is dequantized into the other LDS buffer at the end
+// of step k, so each load has two steps of MFMA work to arrive behind. With
+// BM = 256 every Q4 weight is dequantized once per 256 output rows.
 #include "kernels.h"
 
 namespace smg {
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int LDS_STRIDE = BK + 8;  // halfs per LDS row (pad against bank conflicts)
-constexpr int TILE_HALFS = 128 * LDS_STRIDE;
+constexpr int BN = 128, BK = 64;
+constexpr int LDS_STRIDE = BK + 8;  // halfs per LDS row (pad: conflict-free fragment reads)
 
 struct GemmArgs {
     const uint16_t *lhs;
@@ -42,7 +44,6 @@ struct GemmArgs {
     uint32_t codebook;
     float beta;
     uint32_t lhs_bytes;  // byte footprint of A (the buffer resource's range)
-    uint32_t vec_a;      // A rows 16-byte aligned, unit column stride, k % 8 == 0
 };
 
 template <bool BF16>
@@ -57,105 +58,133 @@ __device__ __forceinline__ float4_t mfma(const uint4 &a, const uint4 &b, float4_
     }
 }
 
-// ---- B-tile staging: global -> registers (issued early) -> LDS (dequant) ----
-//
-// Each thread owns one "unit" of the 128-column x 64-depth B tile; the unit's
-// shape depends on the weight kind:
-//   Q4:    column t%128, 32 depths (one 16-byte chunk), chunk t/128 of the step
-//   Q2:    column t%128, 32 depths (8 bytes: half a chunk)
-//   Q1:    column t%128, 32 depths (4 bytes: a quarter chunk)
-//   dense: column t/2, 32 depths (64 bytes)
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t x, uint32_t y) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(x), "v"(y));
+    return r;
+}
+
+// ---- B tile: global -> registers (early) -> LDS (dequantized) ----------------
+// Thread t owns column t % 128 and UD consecutive depths (t / 128) * UD of the
+// 128-column x 64-depth tile; UD = 64 * 128 / threads (32 or 16).
+template <int UD>
 struct BRegs {
-    uint4 raw[4];
+    // dense: UD halfs; Q4 uses dwords 0..UD/8-1, low-bit dwords 0..UD/16-1.
+    // A vector type (not an array) so the register stages never go to scratch.
+    uint32_t __attribute__((ext_vector_type(UD / 2))) v;
     uint16_t s, mn;
+    uint32_t dc;  // first depth actually loaded (clamped into the weights)
+    bool live;    // false for a unit past K: its weights are forced to 0
 };
 
-template <int WK>
-__device__ __forceinline__ void b_load(const GemmArgs &g, uint32_t col0, uint32_t k0, BRegs &r) {
+template <int WK, int UD>
+__device__ __forceinline__ void b_load(const GemmArgs &g, uint32_t col0, uint32_t k0, BRegs<UD> &r) {
     const int t = threadIdx.x;
-    if (WK == W_F16 || WK == W_BF16) {
-        const uint32_t col = col0 + t / 2;
-        const uint32_t d = k0 + (t % 2) * 32;
-        const uint4 *p = (const uint4 *)(g.dense + (size_t)col * g.k_pad + d);
+    const uint32_t col = col0 + t % 128;
+    const uint32_t d = k0 + (t / 128) * UD;  // first depth of the unit
+    if constexpr (WK == W_F16 || WK == W_BF16) {
+        r.live = d < g.k_pad;
+        const uint4 *p = (const uint4 *)(g.dense + (size_t)col * g.k_pad + (r.live ? d : g.k_pad - UD));
 #pragma unroll
-        for (int q = 0; q < 4; q++) r.raw[q] = p[q];
+        for (int q = 0; q < UD / 8; q++) {
+            const uint4 x = p[q];
+            r.v[4 * q] = x.x;
+            r.v[4 * q + 1] = x.y;
+            r.v[4 * q + 2] = x.z;
+            r.v[4 * q + 3] = x.w;
+        }
         return;
     }
-    const uint32_t col = col0 + t % 128;
-    const uint32_t d = k0 + (t / 128) * 32;  // first depth of the unit
     constexpr uint32_t CH = WK == W_Q4 ? Q4_CHUNK : WK == W_Q2 ? Q2_GROUP : Q1_GROUP;
-    // Branch-free: a chunk past K loads the last chunk (a valid address) and
-    // its scale is forced to 0, so its weights are +-0. (Low-bit groups cover
-    // K in multiples of 256 depths, so only Q4 ever has a dead chunk.)
+    // Branch-free: a unit past K (a padding chunk, or a step issued past the
+    // last one) loads from the last chunk (a valid address) and its scale is
+    // forced to 0 in b_store, so its weights are +-0.
     const uint32_t kc = d / CH;
     const bool live = kc < g.nchunks;
     const uint32_t kcc = live ? kc : g.nchunks - 1;
     const uint32_t dc = kcc * CH + d % CH;
-    r.raw[0] = make_uint4(0, 0, 0, 0);
-    if (WK == W_Q4) {
-        r.raw[0] = *(const uint4 *)(g.codes + ((size_t)kcc * g.n_pad + col) * 16);
-    } else {
-        // quarters g and g+1 of the unit's slab: two dwords 16 bytes apart
-        const uint8_t *p = g.codes + lb_dword_offset<WK == W_Q2 ? 2 : 1>(dc, col, g.n_pad);
-        r.raw[0].x = *(const uint32_t *)p;
-        r.raw[0].y = *(const uint32_t *)(p + 16);
-    }
-    r.s = 0;
-    r.mn = 0;
-    if (g.block_shift >= 5) {
-        const uint32_t kb = dc >> g.block_shift;
-        const uint16_t s = g.sc[(size_t)kb * g.n_pad + col];
-        r.s = live ? s : (uint16_t)0;
-        if (WK == W_Q4 && g.mn) {
-            const uint16_t mv = g.mn[(size_t)kb * g.n_pad + col];
-            r.mn = live ? mv : (uint16_t)0;
+    if constexpr (WK == W_Q4) {
+        const uint8_t *p = g.codes + ((size_t)kcc * g.n_pad + col) * 16 + ((d % 32) / 8) * 4;
+        if constexpr (UD == 32) {
+            const uint4 x = *(const uint4 *)p;
+            r.v[0] = x.x;
+            r.v[1] = x.y;
+            r.v[2] = x.z;
+            r.v[3] = x.w;
+        } else {
+            const uint2 x = *(const uint2 *)p;
+            r.v[0] = x.x;
+            r.v[1] = x.y;
         }
+    } else {
+        // quarter(s) of the unit's slab: dwords 16 bytes apart
+        const uint8_t *p = g.codes + lb_dword_offset<WK == W_Q2 ? 2 : 1>(dc, col, g.n_pad);
+        r.v[0] = *(const uint32_t *)p;
+        if constexpr (UD == 32) r.v[1] = *(const uint32_t *)(p + 16);
     }
+    // Scale (and min) loads are unconditional so no wait is forced here: the
+    // values are only consumed (and masked by `live`) in b_store. When the
+    // block is shorter than the unit, b_store reads per-depth scales instead.
+    const size_t si = (size_t)(dc >> g.block_shift) * g.n_pad + col;
+    r.s = g.sc[si];
+    if constexpr (WK == W_Q4) r.mn = (g.mn ? g.mn : g.sc)[si];
+    r.live = live;
+    r.dc = dc;
 }
 
-// Write one unit into the LDS B tile (column-major: B_lds[col][depth]).
-template <int WK, bool BF16, bool AFFINE>
+template <int WK, bool BF16, bool AFFINE, int UD>
 __device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, uint32_t k0,
-                                        const BRegs &r, uint16_t *blds) {
+                                        const BRegs<UD> &r, uint16_t *blds) {
     const int t = threadIdx.x;
-    if (WK == W_F16 || WK == W_BF16) {
-        uint16_t *dstp = blds + (t / 2) * LDS_STRIDE + (t % 2) * 32;
+    const int cl = t % 128;
+    const int dl = (t / 128) * UD;
+    uint16_t *dstp = blds + cl * LDS_STRIDE + dl;
+    if constexpr (WK == W_F16 || WK == W_BF16) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) *(uint4 *)(dstp + q * 8) = r.raw[q];
+        for (int q = 0; q < UD / 8; q++)
+            *(uint4 *)(dstp + q * 8) = r.live ? make_uint4(r.v[4 * q], r.v[4 * q + 1], r.v[4 * q + 2], r.v[4 * q + 3])
+                                              : make_uint4(0, 0, 0, 0);
         return;
     }
-    const int cl = t % 128;
-    const int dl = (t / 128) * 32;
     const uint32_t col = col0 + cl;
-    const uint32_t d0 = k0 + dl;
-    uint16_t *dstp = blds + cl * LDS_STRIDE + dl;
-    uint32_t out[16];
-    if (WK == W_Q4) {
-        const uint32_t words[4] = {r.raw[0].x, r.raw[0].y, r.raw[0].z, r.raw[0].w};
-        const bool fast = !BF16 && !AFFINE && g.block_shift >= 5;
+    const uint32_t d0 = r.dc;  // per-depth scales are read at clamped depths
+    const bool per_depth = (1u << g.block_shift) < (uint32_t)UD;  // scale per depth
+    const uint16_t us = r.live ? r.s : (uint16_t)0;
+    const uint16_t um = r.live ? r.mn : (uint16_t)0;
+    uint32_t out[UD / 2];
+    if constexpr (WK == W_Q4) {
+        const uint32_t words[4] = {r.v[0], r.v[1], r.v[2], r.v[3]};
+        const bool fast = !BF16 && !AFFINE && !per_depth;
+        const uint32_t mag_lo = 0x64006400u, mag_hi = 0x54005400u;
 #pragma unroll
-        for (int w = 0; w < 4; w++) {
+        for (int w = 0; w < UD / 8; w++) {
             const uint32_t q = words[w];  // stored nibbles are code + 8
+            if (fast) {
+                // bfi puts the nibble under an f16 exponent; subtracting the
+                // bias leaves the exact code; one multiply rounds scale*code
+                const _Float16 s = __builtin_bit_cast(_Float16, us);
+                const half2_t s2 = {s, s};
+                const half2_t off_lo = {(_Float16)1032.0f, (_Float16)1032.0f};
+                const half2_t off_hi = {(_Float16)72.0f, (_Float16)72.0f};
+                const uint32_t q8 = q >> 8;
+                out[w * 4 + 0] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2_t, bfi(0x000F000Fu, q, mag_lo)) - off_lo) * s2);
+                out[w * 4 + 1] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2_t, bfi(0x00F000F0u, q, mag_hi)) - off_hi) * s2);
+                out[w * 4 + 2] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2_t, bfi(0x000F000Fu, q8, mag_lo)) - off_lo) * s2);
+                out[w * 4 + 3] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2_t, bfi(0x00F000F0u, q8, mag_hi)) - off_hi) * s2);
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t u = (q >> (4 * e)) & 0x000F000Fu;
-                if (fast) {
-                    half2_t h = __builtin_bit_cast(half2_t, u | 0x64006400u);
-                    const half2_t magic = {(_Float16)1032.0f, (_Float16)1032.0f};
-                    _Float16 s = __builtin_bit_cast(_Float16, r.s);
-                    half2_t s2 = {s, s};
-                    out[w * 4 + e] = __builtin_bit_cast(uint32_t, (h - magic) * s2);
-                } else {
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t u = (q >> (4 * e)) & 0x000F000Fu;
                     const int c0 = (int)(u & 0xF) - 8, c1 = (int)(u >> 16) - 8;
                     const uint32_t dp = d0 + w * 8 + 2 * e;
-                    uint16_t s0 = r.s, s1 = r.s, m0 = r.mn, m1 = r.mn;
-                    if (g.block_shift < 5) {
+                    uint16_t s0 = us, s1 = us, m0 = um, m1 = um;
+                    if (per_depth) {
                         const uint32_t b0 = dp >> g.block_shift, b1 = (dp + 1) >> g.block_shift;
-                        s0 = g.sc[(size_t)b0 * g.n_pad + col];
-                        s1 = g.sc[(size_t)b1 * g.n_pad + col];
+                        s0 = r.live ? g.sc[(size_t)b0 * g.n_pad + col] : (uint16_t)0;
+                        s1 = r.live ? g.sc[(size_t)b1 * g.n_pad + col] : (uint16_t)0;
                         if (AFFINE) {
-                            m0 = g.mn[(size_t)b0 * g.n_pad + col];
-                            m1 = g.mn[(size_t)b1 * g.n_pad + col];
+                            m0 = r.live ? g.mn[(size_t)b0 * g.n_pad + col] : (uint16_t)0;
+                            m1 = r.live ? g.mn[(size_t)b1 * g.n_pad + col] : (uint16_t)0;
                         }
                     }
                     uint16_t w0, w1;
@@ -172,11 +201,11 @@ __device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, uint32
                 }
             }
         }
-    } else if (WK == W_Q2) {
+    } else if constexpr (WK == W_Q2) {
         // f16(scale * codebook[code]): the product is exact in f32 (matmul.rs:185-187)
-        const uint32_t words[2] = {r.raw[0].x, r.raw[0].y};
+        const uint32_t words[2] = {r.v[0], r.v[1]};
 #pragma unroll
-        for (int w = 0; w < 2; w++) {
+        for (int w = 0; w < UD / 16; w++) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t sel = (words[w] >> (2 * i)) & 0x03030303u;
@@ -185,11 +214,8 @@ __device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, uint32
 #pragma unroll
                 for (int b = 0; b < 4; b++) {
                     const uint32_t dp = d0 + w * 16 + 4 * i + b;
-                    const uint16_t sb = g.block_shift >= 5
-                                            ? r.s
-                                            : g.sc[(size_t)(dp >> g.block_shift) * g.n_pad + col];
-                    const float v = (float)(int8_t)(vals >> (8 * b));
-                    h[b] = f32_to_f16(f16_to_f32(sb) * v);
+                    const uint16_t sb = per_depth ? (r.live ? g.sc[(size_t)(dp >> g.block_shift) * g.n_pad + col] : (uint16_t)0) : us;
+                    h[b] = f32_to_f16(f16_to_f32(sb) * (float)(int8_t)(vals >> (8 * b)));
                 }
                 out[w * 8 + 2 * i] = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
                 out[w * 8 + 2 * i + 1] = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
@@ -198,10 +224,10 @@ __device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, uint32
     } else {
         // Q1: +scale for a set bit, -scale otherwise (exact). Each dword holds
         // two slabs; this unit's slab is bit-half hs.
-        const uint32_t words[2] = {r.raw[0].x, r.raw[0].y};
+        const uint32_t words[2] = {r.v[0], r.v[1]};
         const uint32_t hs = ((d0 % Q1_GROUP) / LB_SLAB) % 2;
 #pragma unroll
-        for (int w = 0; w < 2; w++) {
+        for (int w = 0; w < UD / 16; w++) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t bits = (words[w] >> (4 * hs + i)) & 0x01010101u;
@@ -209,46 +235,40 @@ __device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, uint32
 #pragma unroll
                 for (int b = 0; b < 4; b++) {
                     const uint32_t dp = d0 + w * 16 + 4 * i + b;
-                    const uint16_t sb = g.block_shift >= 5
-                                            ? r.s
-                                            : g.sc[(size_t)(dp >> g.block_shift) * g.n_pad + col];
-                    const uint32_t bit = (bits >> (8 * b)) & 1u;
-                    h[b] = bit ? sb : (uint16_t)(sb ^ 0x8000u);
+                    const uint16_t sb = per_depth ? (r.live ? g.sc[(size_t)(dp >> g.block_shift) * g.n_pad + col] : (uint16_t)0) : us;
+                    h[b] = ((bits >> (8 * b)) & 1u) ? sb : (uint16_t)(sb ^ 0x8000u);
                 }
                 out[w * 8 + 2 * i] = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
                 out[w * 8 + 2 * i + 1] = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
             }
         }
     }
-    // Q1/Q2 depth order inside out[]: depth 4i+b sits at half-word 4i+b, i.e.
-    // natural order. Q4: depth 8w+2e+h at half-word 8w+2e+h, also natural.
+    // depth order inside out[]: natural (depth x at half-word x)
 #pragma unroll
-    for (int q = 0; q < 4; q++)
+    for (int q = 0; q < UD / 8; q++)
         *(uint4 *)(dstp + q * 8) = make_uint4(out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]);
 }
 
-// ---- A-tile staging: 128 rows x 64 depths; thread t: row t/2, 32 depths ----
-__device__ __forceinline__ void a_load(const GemmArgs &g, uint32_t row0, uint32_t k0,
-                                       uint4 (&ra)[4]) {
+// ---- A tile: BM rows x 64 depths; thread t: row t/2, 32 depths --------------
+template <bool VECA>
+__device__ __forceinline__ void a_load(const GemmArgs &g, uint32_t row0, uint32_t k0, uint4 (&ra)[4]) {
     // buffer loads: out-of-range offsets read zero, no branches
     const int t = threadIdx.x;
     const uint32_t row = row0 + t / 2;
     const uint32_t d = k0 + (t % 2) * 32;
     const rsrc_t rs = make_rsrc(g.lhs, g.lhs_bytes);
-    if (g.vec_a) {
+    if constexpr (VECA) {
 #pragma unroll
         for (int q = 0; q < 4; q++)
             ra[q] = bload16(rs, (row < g.m && d + 8 * q < g.k)
-                                    ? (uint32_t)(row * g.lhs_rs + d + 8 * q) * 2u
-                                    : OOB);
+                                    ? (uint32_t)(row * g.lhs_rs + d + 8 * q) * 2u : OOB);
         return;
     }
     uint16_t e[32];
 #pragma unroll
     for (int q = 0; q < 32; q++)
         e[q] = bload2(rs, (row < g.m && d + q < g.k)
-                              ? (uint32_t)(row * g.lhs_rs + (d + q) * g.lhs_cs) * 2u
-                              : OOB);
+                              ? (uint32_t)(row * g.lhs_rs + (d + q) * g.lhs_cs) * 2u : OOB);
 #pragma unroll
     for (int q = 0; q < 4; q++)
         ra[q] = make_uint4(e[8 * q] | ((uint32_t)e[8 * q + 1] << 16),
@@ -264,15 +284,43 @@ __device__ __forceinline__ void a_store(const uint4 (&ra)[4], uint16_t *alds) {
     for (int q = 0; q < 4; q++) *(uint4 *)(dstp + q * 8) = ra[q];
 }
 
-template <int WK, bool BF16, bool AFFINE>
-__global__ void __launch_bounds__(256) gemm_kernel(GemmArgs g, EpArgs ep) {
-    extern __shared__ __align__(16) uint16_t lds[];
-    // stage s: A at lds + 2*s*TILE, B at lds + (2*s+1)*TILE
+// One 64-depth step of a wave's 64 x 64 sub-tile from LDS.
+template <bool BF16, int BM>
+__device__ __forceinline__ void compute_step(const uint16_t *Al, int wm, int wn, int lr, int lk,
+                                             float4_t (&acc)[4][4]) {
+    const uint16_t *Bl = Al + BM * LDS_STRIDE;
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 32) {
+        uint4 af[4], bf[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            af[i] = *(const uint4 *)(Al + (wm * 64 + i * 16 + lr) * LDS_STRIDE + kk + lk);
+#pragma unroll
+        for (int jt = 0; jt < 4; jt++)
+            bf[jt] = *(const uint4 *)(Bl + (wn * 64 + jt * 16 + lr) * LDS_STRIDE + kk + lk);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int jt = 0; jt < 4; jt++) acc[i][jt] = mfma<BF16>(af[i], bf[jt], acc[i][jt]);
+    }
+}
 
-    // column-tile-major grid order: consecutive workgroups share a weight tile
+template <int BM>
+struct Tile {
+    static constexpr int THREADS = BM * 2;          // BM/64 x 2 waves
+    static constexpr int UD = 64 * 128 / THREADS;   // B depths per thread
+    static constexpr int STAGE = (BM + BN) * LDS_STRIDE;  // halfs per LDS stage
+};
+
+template <int WK, bool BF16, bool AFFINE, int BM, bool VECA>
+__global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
+    constexpr int UD = Tile<BM>::UD;
+    constexpr int STAGE = Tile<BM>::STAGE;
+    extern __shared__ __align__(16) uint16_t lds[];  // [2][A: BM rows | B: 128 rows] x LDS_STRIDE
+
+    // column-tile-major order: consecutive workgroups share a weight tile
     const uint32_t mtiles = (g.m + BM - 1) / BM;
-    const uint32_t tile = blockIdx.x;
-    const uint32_t tm = tile % mtiles, tn = tile / mtiles;
+    const uint32_t tm = blockIdx.x % mtiles, tn = blockIdx.x / mtiles;
     const uint32_t row0 = tm * BM, col0 = tn * BN;
 
     const int t = threadIdx.x;
@@ -286,76 +334,155 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs g, EpArgs ep) {
 #pragma unroll
         for (int jt = 0; jt < 4; jt++) acc[i][jt] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
-    const uint32_t ksteps = (g.k + BK - 1) / BK;
-    uint4 ra[4];
-    BRegs rb;
-    a_load(g, row0, 0, ra);
-    b_load<WK>(g, col0, 0, rb);
-    a_store(ra, lds);
-    b_store<WK, BF16, AFFINE>(g, col0, 0, rb, lds + TILE_HALFS);
+    uint4 ra0[4], ra1[4];
+    BRegs<UD> rb0, rb1;
+
+    // Every load is unconditional (steps past K read zeros, see b_load and
+    // a_load), so the compiler can count outstanding loads exactly and each
+    // wait retires only the step about to be stored. The step count is
+    // rounded up to even; an odd K-step count multiplies one zero step.
+    const uint32_t ksteps = (g.k + 2 * BK - 1) / (2 * BK) * 2;  // >= 2
+    a_load<VECA>(g, row0, 0, ra0);
+    b_load<WK, UD>(g, col0, 0, rb0);
+    a_load<VECA>(g, row0, BK, ra1);
+    b_load<WK, UD>(g, col0, BK, rb1);
+    a_store(ra0, lds);
+    b_store<WK, BF16, AFFINE, UD>(g, col0, 0, rb0, lds + BM * LDS_STRIDE);
     __syncthreads();
 
-    for (uint32_t ks = 0; ks < ksteps; ks++) {
-        const int cur = ks & 1;
-        const bool more = ks + 1 < ksteps;
-        if (more) {
-            a_load(g, row0, (ks + 1) * BK, ra);
-            b_load<WK>(g, col0, (ks + 1) * BK, rb);
-        }
-        const uint16_t *Al = lds + 2 * cur * TILE_HALFS;
-        const uint16_t *Bl = Al + TILE_HALFS;
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 32) {
-            uint4 af[4], bf[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                af[i] = *(const uint4 *)(Al + (wm * 64 + i * 16 + lr) * LDS_STRIDE + kk + lk);
-#pragma unroll
-            for (int jt = 0; jt < 4; jt++)
-                bf[jt] = *(const uint4 *)(Bl + (wn * 64 + jt * 16 + lr) * LDS_STRIDE + kk + lk);
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int jt = 0; jt < 4; jt++) acc[i][jt] = mfma<BF16>(af[i], bf[jt], acc[i][jt]);
-        }
-        if (more) {
-            uint16_t *An = lds + 2 * (cur ^ 1) * TILE_HALFS;
-            a_store(ra, An);
-            b_store<WK, BF16, AFFINE>(g, col0, (ks + 1) * BK, rb, An + TILE_HALFS);
-        }
+    for (uint32_t ks = 0; ks < ksteps; ks += 2) {
+        // even step ks: LDS buffer 0; step ks+2 loads into register stage 0
+        a_load<VECA>(g, row0, (ks + 2) * BK, ra0);
+        b_load<WK, UD>(g, col0, (ks + 2) * BK, rb0);
+        compute_step<BF16, BM>(lds, wm, wn, lr, lk, acc);
+        a_store(ra1, lds + STAGE);
+        b_store<WK, BF16, AFFINE, UD>(g, col0, (ks + 1) * BK, rb1, lds + STAGE + BM * LDS_STRIDE);
+        __syncthreads();
+        // odd step ks+1: LDS buffer 1; step ks+3 loads into register stage 1
+        a_load<VECA>(g, row0, (ks + 3) * BK, ra1);
+        b_load<WK, UD>(g, col0, (ks + 3) * BK, rb1);
+        compute_step<BF16, BM>(lds + STAGE, wm, wn, lr, lk, acc);
+        a_store(ra0, lds);
+        b_store<WK, BF16, AFFINE, UD>(g, col0, (ks + 2) * BK, rb0, lds + BM * LDS_STRIDE);
         __syncthreads();
     }
 
-    // store: lane holds D[4*(lane/16)+v][lane%16] of each 16x16 tile
+    // Round beta*acc to 16 bits into LDS (the loop's last barrier freed it),
+    // then store rows of 8 consecutive columns: 16-byte stores when the
+    // destination is row-major, and the op-graph on the rounded value
+    // (src/exec/macros.rs:188-206). A lane holds D[4*(lane/16)+v][lane%16] of
+    // each 16x16 MFMA tile.
+    constexpr int CS = BN + 8;  // halfs per staged row
+    static_assert(BM * CS <= 2 * STAGE, "staged tile exceeds the LDS buffers");
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int jt = 0; jt < 4; jt++)
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const uint32_t row = row0 + wm * 64 + i * 16 + (lane / 16) * 4 + v;
-                const uint32_t col = col0 + wn * 64 + jt * 16 + lr;
-                if (row < g.m && col < g.n) {
-                    const float x = 0.0f + g.beta * acc[i][jt][v];
-                    g.dst[(size_t)row * g.dst_rs + (size_t)col * g.dst_cs] =
-                        finish<BF16>(ep, x, row, col, g.n);
+            for (int v = 0; v < 4; v++)
+                lds[(wm * 64 + i * 16 + (lane / 16) * 4 + v) * CS + wn * 64 + jt * 16 + lr] =
+                    from_f32<BF16>(0.0f + g.beta * acc[i][jt][v]);
+    __syncthreads();
+    const bool plain = ep.n_nodes == 0;
+    // ROW / COL operand vectors are read once per tile into LDS (as f32), so
+    // the cell loop below touches global memory only for TENSOR operands.
+    float *colv = (float *)(lds + BM * CS);   // [node][BN]
+    float *rowv = colv + SMG_MAX_EP_NODES * BN;  // [node][BM]
+    static_assert(BM * CS * 2 + SMG_MAX_EP_NODES * (BN + BM) * 4 <= 2 * STAGE * 2,
+                  "epilogue operands exceed the LDS buffers");
+    for (uint32_t q = 0; q < ep.n_nodes; q++) {
+        const uint32_t cls = ep.cls[q];
+        const uint16_t *p = (const uint16_t *)ep.nodes[q].ptr;
+        if (cls == EPC_COL && t < BN)
+            colv[q * BN + t] = col0 + t < g.n ? to_f32<BF16>(p[col0 + t]) : 0.0f;
+        if (cls == EPC_ROW && t < BM)
+            rowv[q * BM + t] = row0 + t < g.m ? to_f32<BF16>(p[row0 + t]) : 0.0f;
+    }
+    __syncthreads();
+    for (int u = t; u < BM * (BN / 8); u += BM * 2) {
+        const int rl = u / (BN / 8), cl = (u % (BN / 8)) * 8;
+        const uint32_t row = row0 + rl, col = col0 + cl;
+        if (row >= g.m || col >= g.n) continue;
+        const uint32_t ne = g.n - col < 8 ? g.n - col : 8;  // cells of this row group
+        uint4 c8 = *(const uint4 *)(lds + rl * CS + cl);
+        if (!plain) {
+            uint32_t w4[4] = {c8.x, c8.y, c8.z, c8.w};
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = to_f32<BF16>((uint16_t)(w4[e / 2] >> (16 * (e % 2))));
+            for (uint32_t q = 0; q < ep.n_nodes; q++) {
+                const EpNode &nd = ep.nodes[q];
+                const uint32_t cls = ep.cls[q], fam = ep.fam[q];
+                if (fam == EPF_ACT) {
+                    F8 y;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) y.v[e] = x[e];
+                    y = act8(nd.aux, y, nd.scalar);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) x[e] = y.v[e];
+                    continue;
+                }
+                float v[8];
+                if (cls == EPC_TENSOR) {
+                    // the 8 loads are issued together, then consumed
+                    const uint16_t *p = (const uint16_t *)nd.ptr + (size_t)row * (nd.ld == 0 ? g.n : nd.ld) + col;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = (uint32_t)e < ne ? to_f32<BF16>(p[e]) : 0.0f;
+                } else if (cls == EPC_COL) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = colv[q * BN + cl + e];
+                } else {
+                    const float vs = cls == EPC_ROW ? rowv[q * BM + rl] : nd.scalar;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = vs;
+                }
+                switch (fam) {  // uniform: one branch per node, then 8 lanes of arithmetic
+#define SMG_EP_FAM(F)                                                           \
+    case F:                                                                     \
+        _Pragma("unroll") for (int e = 0; e < 8; e++) x[e] = ep_arith(F, x[e], v[e]); \
+        break;
+                    SMG_EP_FAM(EPF_ADD) SMG_EP_FAM(EPF_MUL) SMG_EP_FAM(EPF_SUB)
+                    SMG_EP_FAM(EPF_DIV) SMG_EP_FAM(EPF_MAX) SMG_EP_FAM(EPF_MIN)
+#undef SMG_EP_FAM
+                default: break;
                 }
             }
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                w4[e] = (uint32_t)from_f32<BF16>(x[2 * e]) | ((uint32_t)from_f32<BF16>(x[2 * e + 1]) << 16);
+            c8 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+        uint16_t *dp = g.dst + (size_t)row * g.dst_rs + (size_t)col * g.dst_cs;
+        if (g.dst_cs == 1 && ne == 8 && ((uintptr_t)dp & 15) == 0) {
+            *(uint4 *)dp = c8;
+            continue;
+        }
+        const uint32_t w4[4] = {c8.x, c8.y, c8.z, c8.w};
+        for (uint32_t e = 0; e < ne; e++) dp[(size_t)e * g.dst_cs] = (uint16_t)(w4[e / 2] >> (16 * (e % 2)));
+    }
 }
 
-template <int WK, bool BF16, bool AFFINE>
+template <int WK, bool BF16, bool AFFINE, int BM, bool VECA>
 hipError_t launch_t(const GemmArgs &g, const EpArgs &ep, hipStream_t s) {
-    const size_t lds = 4 * TILE_HALFS * 2;
+    const size_t lds = 2 * (size_t)Tile<BM>::STAGE * 2;
     static bool attr_set = false;  // benign race: every setter writes the same value
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)gemm_kernel<WK, BF16, AFFINE>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        const hipError_t e = hipFuncSetAttribute((const void *)gemm_kernel<WK, BF16, AFFINE, BM, VECA>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
     const uint32_t tiles = ((g.m + BM - 1) / BM) * ((g.n + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_kernel<WK, BF16, AFFINE>), dim3(tiles), dim3(256), lds, s, g, ep);
+    hipLaunchKernelGGL((gemm_kernel<WK, BF16, AFFINE, BM, VECA>), dim3(tiles), dim3(BM * 2), lds, s,
+                       g, ep);
     return hipGetLastError();
+}
+
+template <int WK, bool BF16, bool AFFINE>
+hipError_t launch_shape(const GemmArgs &g, const EpArgs &ep, bool vec_a, hipStream_t s) {
+    if (!vec_a) return launch_t<WK, BF16, AFFINE, 128, false>(g, ep, s);
+    if (g.m > 128) return launch_t<WK, BF16, AFFINE, 256, true>(g, ep, s);
+    return launch_t<WK, BF16, AFFINE, 128, true>(g, ep, s);
 }
 
 }  // namespace
@@ -386,17 +513,16 @@ hipError_t launch_gemm(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long
     const size_t fp = (m && w.k) ? ((m - 1) * (size_t)lhs_rs + (w.k - 1) * (size_t)lhs_cs + 1) * 2 : 0;
     if (fp >= ((size_t)1 << 31)) return hipErrorInvalidValue;  // one buffer resource spans < 2 GiB
     g.lhs_bytes = (uint32_t)fp;
-    g.vec_a = (lhs_cs == 1 && lhs_rs % 8 == 0 && w.k % 8 == 0 &&
-               ((uintptr_t)lhs & 15) == 0) ? 1u : 0u;
+    const bool vec_a = lhs_cs == 1 && lhs_rs % 8 == 0 && w.k % 8 == 0 && ((uintptr_t)lhs & 15) == 0;
     const bool affine = w.mins != nullptr;
     switch (w.kind) {
     case W_Q4:
-        if (bf16) return affine ? launch_t<W_Q4, true, true>(g, ep, s) : launch_t<W_Q4, true, false>(g, ep, s);
-        return affine ? launch_t<W_Q4, false, true>(g, ep, s) : launch_t<W_Q4, false, false>(g, ep, s);
-    case W_Q2: return launch_t<W_Q2, false, false>(g, ep, s);
-    case W_Q1: return launch_t<W_Q1, false, false>(g, ep, s);
-    case W_F16: return launch_t<W_F16, false, false>(g, ep, s);
-    case W_BF16: return launch_t<W_BF16, true, false>(g, ep, s);
+        if (bf16) return affine ? launch_shape<W_Q4, true, true>(g, ep, vec_a, s) : launch_shape<W_Q4, true, false>(g, ep, vec_a, s);
+        return affine ? launch_shape<W_Q4, false, true>(g, ep, vec_a, s) : launch_shape<W_Q4, false, false>(g, ep, vec_a, s);
+    case W_Q2: return launch_shape<W_Q2, false, false>(g, ep, vec_a, s);
+    case W_Q1: return launch_shape<W_Q1, false, false>(g, ep, vec_a, s);
+    case W_F16: return launch_shape<W_F16, false, false>(g, ep, vec_a, s);
+    case W_BF16: return launch_shape<W_BF16, true, false>(g, ep, vec_a, s);
     default: return hipErrorInvalidValue;
     }
 }
