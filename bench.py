@@ -9,13 +9,21 @@ bracketed by torch.cuda.synchronize().
 
 `roofline` covers the dominant kernel (the Q4 GEMV): achieved = algorithmic
 bytes per call / average kernel duration, the duration measured with HIP
-events recorded around each launch on the launch stream (an eager loop over the
-same rotating copies). `extra` reports configs 2-4 the same way (config 4
-against the f16 MFMA peak). `cpu_baseline` times the C restatement of the
-reference's portable path (oracle/) single-threaded on this host for a bounded
-sample of config-1 calls.
+events around the K graph-replayed calls on the stream they run on (so it
+includes the graph's inter-kernel gap, reported as `graph_gap_us` from a
+graph of near-empty kernels). `traffic` is the HBM bytes per launch read from
+the committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary in profiles/ (null if
+absent). `extra` reports configs 2-4 the same way (config 4 against the f16
+MFMA peak) plus a diagnostic per-launch event time (one event pair per eager
+launch, which adds the event overhead). `cpu_baseline` times the C restatement
+of the reference's portable path (oracle/) single-threaded on this host for a
+bounded sample of config-1 calls.
+
+--calib-copy first runs 16 device copies of 64 MiB (a kernel of known traffic)
+so that a rocprofv3 --pmc run of this script can scale its counters.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+                       [--calib-copy]
 """
 from __future__ import annotations
 
@@ -38,10 +46,26 @@ def _events(torch, n):
             for _ in range(n)]
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemv_mfma_config1_traffic.md")
+
+
+def committed_traffic():
+    """HBM bytes per launch of the config-1 GEMV from the committed PMC summary."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def time_calls(torch, calls, reps: int, warmup: int):
-    """Per-launch kernel time (us) with an event pair around each launch on the
-    current stream, and graph-replayed whole-job time (us per call).
-    `calls` is a list of zero-arg callables launching one call each."""
+    """Graph-replayed time per call (us; events around the whole replay on the
+    stream it runs on) and a diagnostic per-launch time (an event pair around
+    each eager launch). `calls` is a list of zero-arg callables launching one
+    call each."""
     s = torch.cuda.current_stream()
     for i in range(warmup):
         calls[i % len(calls)]()
@@ -73,8 +97,8 @@ def time_calls(torch, calls, reps: int, warmup: int):
     t1.record(s)
     torch.cuda.synchronize()
     whole = t0.elapsed_time(t1) * 1e3 / reps
-    return {"us_kernel_avg": per_launch, "us_kernel_min": durs[0],
-            "us_kernel_median": durs[len(durs) // 2], "us_per_call_graph": whole}
+    return {"us_kernel_avg": whole, "us_event_per_launch_avg": per_launch,
+            "us_event_per_launch_min": durs[0], "us_event_per_launch_median": durs[len(durs) // 2]}
 
 
 def main():
@@ -84,6 +108,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="config 1 only")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="16 x 64 MiB device copies first (PMC counter scale)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -102,6 +128,18 @@ def main():
     dev = torch.device("cuda:0")
     to_dev = lambda x: torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).to(dev)  # noqa
 
+    if args.calib_copy:
+        src = torch.ones(32 << 20, dtype=torch.int16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(16):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    # inter-kernel gap of a replayed graph: near-empty kernels (1-element fill)
+    tiny = torch.empty(1, dtype=torch.int16, device=dev)
+    gap = time_calls(torch, [lambda: tiny.fill_(1)], args.steps, 8)["us_kernel_avg"]
+
     def rotate(w, per_copy_bytes):
         copies = max(1, -(-(2 * MALL_BYTES + 64 * 2**20) // per_copy_bytes))
         return [w] + [w.clone() for _ in range(copies - 1)]
@@ -119,7 +157,7 @@ def main():
     hot = time_calls(torch, calls[:1], args.steps, args.warmup)
     t_kernel = cold["us_kernel_avg"]
     achieved = bytes1 / (t_kernel * 1e-6) / 1e9
-    value = bytes1 / (cold["us_per_call_graph"] * 1e-6) / 1e9
+    value = bytes1 / (cold["us_kernel_avg"] * 1e-6) / 1e9
 
     extra = {"config1_q4_gemv": {
         "bytes": bytes1, "weight_copies": len(ws), "cold": cold, "hot_mall": hot,
@@ -199,7 +237,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": cold["us_per_call_graph"] / 1e3,
+        "ms_per_step": cold["us_kernel_avg"] / 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -208,9 +246,10 @@ def main():
         "config": {"workload": "q4_gemv m=1 K=4096 N=4096 block=32, 64 rotating weight copies",
                    "m": 1, "k": 4096, "n": 4096, "block": 32},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": committed_traffic()},
         "cpu_baseline": cpu,
         "extra": extra,
+        "graph_gap_us": gap,
     }
     print(json.dumps(line))
 

@@ -42,6 +42,18 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float x) {
     uint32_t lsb = (u >> 16) & 1u;
     return (uint16_t)((u + 0x7fffu + lsb) >> 16);
 }
+// The hardware hands consecutive workgroups of a 1-D grid to the 8 XCDs in
+// turn (each XCD has its own L2). Renumber them so each XCD owns one
+// contiguous run of logical tiles: neighbouring tiles share cache lines
+// (e.g. the 128-byte line of 64 columns' scales), and those lines are then
+// fetched into one L2 instead of four. A bijection for any grid size.
+constexpr uint32_t N_XCD = 8;
+__device__ __forceinline__ uint32_t xcd_tile(uint32_t b, uint32_t grid) {
+    const uint32_t base = grid / N_XCD, rem = grid % N_XCD;
+    const uint32_t x = b % N_XCD, slot = b / N_XCD;
+    return (x < rem ? x * (base + 1) : rem * (base + 1) + (x - rem) * base) + slot;
+}
+
 template <bool BF16>
 __device__ __forceinline__ float to_f32(uint16_t h) {
     return BF16 ? bf16_to_f32(h) : f16_to_f32(h);

@@ -320,7 +320,8 @@ __global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
 
     // column-tile-major order: consecutive workgroups share a weight tile
     const uint32_t mtiles = (g.m + BM - 1) / BM;
-    const uint32_t tm = blockIdx.x % mtiles, tn = blockIdx.x / mtiles;
+    const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
+    const uint32_t tm = tile % mtiles, tn = tile / mtiles;
     const uint32_t row0 = tm * BM, col0 = tn * BN;
 
     const int t = threadIdx.x;

@@ -63,7 +63,7 @@ __global__ void __launch_bounds__(T) lowbit_gemv(LbArgs g, EpArgs ep) {
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int gq4 = lane >> 4, c = lane & 15;   // quarter; column (A) / row (B)
-    const uint32_t col0 = blockIdx.x * 16;
+    const uint32_t col0 = xcd_tile(blockIdx.x, gridDim.x) * 16;
     const uint32_t col = col0 + c;               // < n_pad
     const uint32_t row0 = blockIdx.y * MR;
     const uint32_t mr = min((uint32_t)MR, g.m - row0);

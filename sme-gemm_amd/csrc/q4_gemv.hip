@@ -88,7 +88,8 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int c = lane & 15, grp = lane >> 4;
-    const uint32_t col = blockIdx.x * 16 + c;     // < n_pad
+    const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
+    const uint32_t col = tile * 16 + c;           // < n_pad
     // the bfi magics live in VGPRs (a VOP3 takes one scalar operand)
     const uint32_t mag_lo = __builtin_amdgcn_readfirstlane(0x64006400u) | (uint32_t)(t >> 30);
     const uint32_t mag_hi = __builtin_amdgcn_readfirstlane(0x54005400u) | (uint32_t)(t >> 30);
@@ -158,7 +159,7 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
         float total = 0.0f;
 #pragma unroll
         for (int w = 0; w < MF_WAVES; w++) total = total + red[(w * 16 + cc) * MR + r];
-        const uint32_t j = blockIdx.x * 16 + cc;
+        const uint32_t j = tile * 16 + cc;
         if (r < (int)g.m && j < g.n) g.dst[(size_t)r * g.n + j] = finish<false>(ep, total, r, j, g.n);
     }
 }
@@ -214,7 +215,8 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4GemvArgs g, EpArgs ep) {
     const int t = threadIdx.x;
     const int c = t % TN;
     const int kl = t / TN;
-    const uint32_t j = blockIdx.x * TN + c;  // < n_pad always
+    const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
+    const uint32_t j = tile * TN + c;  // < n_pad always
     const uint32_t block = 1u << g.block_shift;
     const uint32_t last = g.nchunks - 1;
 
@@ -302,7 +304,7 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4GemvArgs g, EpArgs ep) {
     __syncthreads();
     if (t < M * TN) {
         const int r = t / TN, cc = t % TN;
-        const uint32_t jj = blockIdx.x * TN + cc;
+        const uint32_t jj = tile * TN + cc;
         float total = 0.0f;
 #pragma unroll
         for (int q = 0; q < KL; q++) total = total + red[(q * M + r) * TN + cc];
