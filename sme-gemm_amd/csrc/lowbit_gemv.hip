@@ -202,6 +202,328 @@ __global__ void __launch_bounds__(T) lowbit_gemv(LbArgs g, EpArgs ep) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Single-launch path (m <= 8, block <= 4096, K <= 8192, m*K <= 32 K): one
+// workgroup of 8 waves per 16-column tile, a straight-line program kept short
+// (each workgroup runs it once, so its instruction fetch is part of the
+// latency). Each workgroup quantizes the rows of A itself -- a few KB, read
+// from L2 -- so a call is one launch:
+//   1. loads: A, then the tile's code groups (a wave covers a contiguous K
+//      range in whole 16-byte groups: Q2 4 slabs, Q1 8), then its scale rows;
+//   2. quantize: thread t takes depths 8t..8t+7 (per 4096-depth pass) of every
+//      row; a block's amax and sum(q) are reduced over the block's lanes by
+//      shuffles, and through LDS over waves for blocks longer than 512;
+//   3. exact block sums on v_mfma_i32_16x16x64_i8, accumulated over a block's
+//      slabs inside one wave (a wave's K range holds whole blocks; shorter
+//      blocks take one masked product each), written to LDS per (row, column)
+//      with blocks contiguous;
+//   4. one lane per output folds its blocks in order with fmaf, reading four
+//      blocks' sums, scales and activation factors per LDS load, then the
+//      op-graph and the f16 store.
+// LDS rows are padded so these accesses do not collide on banks.
+// ---------------------------------------------------------------------------
+constexpr uint32_t QPASS = T * 8;  // depths quantized per pass (8 per thread)
+
+struct LtArgs {
+    const uint8_t *codes;
+    const uint16_t *sc;
+    const uint16_t *lhs;
+    uint16_t *dst;
+    uint32_t n, k, n_pad, m;
+    uint32_t block_shift;
+    uint32_t codebook;
+    uint32_t sc_rows;
+    uint32_t ngroups;      // 16-byte code groups per column
+    uint32_t kq;           // depths the waves cover (8 waves x NG groups)
+    uint32_t nbq;          // blocks in kq (a multiple of 4)
+    uint32_t codes_bytes;  // extent of the code array (buffer resource)
+};
+
+__device__ __forceinline__ float nanmax(float a, float b) {
+    return (a != a) ? a : ((b != b) ? b : fmaxf(a, b));
+}
+// Reductions over aligned groups of gl lanes (gl a power of two <= 64).
+__device__ __forceinline__ float group_max(float a, uint32_t gl) {
+    for (uint32_t off = 1; off < gl; off <<= 1) a = nanmax(a, __shfl_xor(a, (int)off));
+    return a;
+}
+__device__ __forceinline__ int32_t group_sum(int32_t a, uint32_t gl) {
+    for (uint32_t off = 1; off < gl; off <<= 1) a += __shfl_xor(a, (int)off);
+    return a;
+}
+
+// LDS: q [MR][kq + 16] i8 | s [MR][nbq] f32 | sum(q) [MR][nbq] i32 |
+//      block sums [MR][16][nbq + 4] i32 | scales [16][nbq + 4] f16 | wave partials
+size_t tile_lds_bytes(uint32_t kq, uint32_t nbq, int mr) {
+    return (size_t)mr * (kq + 16) + (size_t)mr * nbq * 8 + (size_t)mr * 16 * (nbq + 4) * 4 +
+           (size_t)16 * (nbq + 4) * 2 + (size_t)mr * WV * 8;
+}
+
+// SPB: slabs per block when fixed at compile time (2 = blocks of 128, the
+// usual decode format), 0 for any block (runtime block structure).
+template <int KIND, int MR, int NG, int SPB>
+__global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr uint32_t SPG = KIND == 2 ? 4 : 8;  // slabs per code group
+    constexpr int NSW = NG * (int)SPG;            // slabs per wave
+    constexpr int QP = (NSW * WV * LB_SLAB + QPASS - 1) / QPASS;  // A passes (<= 2)
+    const uint32_t block = 1u << g.block_shift;
+    const uint32_t nbq = g.nbq, kq = g.kq;
+    const uint32_t qs_ = kq + 16;   // q row stride (bytes)
+    const uint32_t bs = nbq + 4;    // block-sum / scale row stride (elements)
+    int8_t *ql = (int8_t *)smem;                        // [MR][qs_]
+    float *sa = (float *)(smem + MR * qs_);             // [MR][nbq]
+    int32_t *as = (int32_t *)(sa + MR * nbq);           // [MR][nbq]
+    int32_t *sb = as + MR * nbq;                        // [MR][16][bs]
+    uint16_t *scl = (uint16_t *)(sb + MR * 16 * bs);    // [16][bs]
+    float *wmax = (float *)(scl + 16 * bs);             // [MR][WV]
+    int32_t *wsum = (int32_t *)(wmax + MR * WV);        // [MR][WV]
+
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int gq4 = lane >> 4, c = lane & 15;
+    const uint32_t col0 = xcd_tile(blockIdx.x, gridDim.x) * 16;
+    const uint32_t mr = g.m;  // <= MR
+    const rsrc_t ar = make_rsrc(g.lhs, g.m * g.k * 2u);
+    const bool vec = (g.k & 7) == 0;
+
+    // -- 1. loads: A (waited on first), codes, scales
+    uint4 areg[QP][MR];
+#pragma unroll
+    for (int p = 0; p < QP; p++)
+#pragma unroll
+        for (int r = 0; r < MR; r++) areg[p][r] = load_row8(ar, r, g.m, g.k, p * QPASS + 8 * t, vec);
+    uint4 wreg[NG];
+    {
+        const rsrc_t cr = make_rsrc(g.codes, g.codes_bytes);
+#pragma unroll
+        for (int i = 0; i < NG; i++) {
+            const uint32_t grp = wave * NG + i;
+            wreg[i] = bload16(cr, grp < g.ngroups ? ((grp * g.n_pad + col0 + c) * 4 + gq4) * 16 : OOB);
+        }
+    }
+    uint4 sreg;
+    {
+        const rsrc_t sr = make_rsrc(g.sc, g.sc_rows * g.n_pad * 2u);
+        const uint32_t bb = t / 2;
+        sreg = bload16(sr, (bb < nbq && bb < g.sc_rows) ? (bb * g.n_pad + col0) * 2u + (t % 2) * 16u : OOB);
+    }
+
+    // -- 2. quantize A (quantize_row, src/kernels/lowbit/matmul.rs:354-371)
+    const uint32_t gl = block / 8 < 64u ? block / 8 : 64u;  // lanes of a block in a wave
+    const uint32_t wpb = block > 512u ? block / 512u : 1u;   // waves of a block
+#pragma unroll
+    for (int p = 0; p < QP; p++) {
+        const uint32_t d0 = p * QPASS + 8 * t;
+        float am[MR];
+#pragma unroll
+        for (int r = 0; r < MR; r++) {
+            const uint32_t wd[4] = {areg[p][r].x, areg[p][r].y, areg[p][r].z, areg[p][r].w};
+            float a = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) a = nanmax(a, fabsf(f16_to_f32((uint16_t)(wd[e / 2] >> (16 * (e % 2))))));
+            am[r] = group_max(a, gl);
+        }
+        if (wpb > 1) {  // blocks longer than a wave: combine the waves' maxima
+            if (p > 0) __syncthreads();
+            if (lane == 0)
+#pragma unroll
+                for (int r = 0; r < MR; r++) wmax[r * WV + wave] = am[r];
+            __syncthreads();
+            const uint32_t w0 = (wave / wpb) * wpb;
+#pragma unroll
+            for (int r = 0; r < MR; r++) {
+                float a = 0.0f;
+                for (uint32_t w = 0; w < wpb; w++) a = nanmax(a, wmax[r * WV + w0 + w]);
+                am[r] = a;
+            }
+        }
+        int32_t qs[MR];
+#pragma unroll
+        for (int r = 0; r < MR; r++) {
+            const uint32_t wd[4] = {areg[p][r].x, areg[p][r].y, areg[p][r].z, areg[p][r].w};
+            const float inv = am[r] > 0.0f ? __fdiv_rn(127.0f, am[r]) : 0.0f;
+            uint32_t qw0 = 0, qw1 = 0;
+            int32_t sum = 0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float v = rintf(f16_to_f32((uint16_t)(wd[e / 2] >> (16 * (e % 2)))) * inv);
+                const int qi = (v != v) ? 0 : (int)fminf(fmaxf(v, -128.0f), 127.0f);
+                if (e < 4) qw0 |= ((uint32_t)qi & 0xFFu) << (8 * e);
+                else qw1 |= ((uint32_t)qi & 0xFFu) << (8 * (e - 4));
+                sum += qi;
+            }
+            if (d0 < kq) *(uint2 *)(ql + r * qs_ + d0) = make_uint2(qw0, qw1);
+            qs[r] = KIND == 1 ? group_sum(sum, gl) : 0;
+        }
+        if (KIND == 1 && wpb > 1) {
+            if (lane == 0)
+#pragma unroll
+                for (int r = 0; r < MR; r++) wsum[r * WV + wave] = qs[r];
+            __syncthreads();
+            const uint32_t w0 = (wave / wpb) * wpb;
+#pragma unroll
+            for (int r = 0; r < MR; r++) {
+                int32_t sum = 0;
+                for (uint32_t w = 0; w < wpb; w++) sum += wsum[r * WV + w0 + w];
+                qs[r] = sum;
+            }
+        }
+        if ((uint32_t)lane % gl == 0 && (uint32_t)wave % wpb == 0 && d0 < kq) {
+            const uint32_t bb = d0 >> g.block_shift;
+#pragma unroll
+            for (int r = 0; r < MR; r++) {
+                sa[r * nbq + bb] = __fdiv_rn(am[r], 127.0f);
+                as[r * nbq + bb] = qs[r];
+            }
+        }
+    }
+    if ((uint32_t)t < 2 * nbq) {  // transpose: scale of (block t/2, column 8(t%2)+e)
+        const uint32_t sw[4] = {sreg.x, sreg.y, sreg.z, sreg.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) scl[(8 * (t % 2) + e) * bs + t / 2] = (uint16_t)(sw[e / 2] >> (16 * (e % 2)));
+    }
+    __syncthreads();
+
+    // -- 3. exact block sums on the matrix cores: A = 16 columns x 64 depths
+    //       of expanded codes, B = 64 depths x up to 16 rows of q
+    // lane (gq4, c) holds the sums of columns 4*gq4 + v, row c; rows m..MR-1
+    // of q are zero, so their sums are too
+    int32_t *dp = sb + (c * 16 + 4 * gq4) * bs;
+    auto expand = [&](int i) {
+        const uint4 wv = wreg[i / SPG];
+        const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+        int4_t wa;
+        if (KIND == 2) {
+            const uint32_t w = words[i % 4];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                wa[j] = (int)__builtin_amdgcn_perm(g.codebook, g.codebook, (w >> (2 * j)) & 0x03030303u);
+        } else {
+            const uint32_t w = words[(i % 8) / 2], hs = 4 * (i % 2);
+#pragma unroll
+            for (int j = 0; j < 4; j++) wa[j] = (int)((w >> (hs + j)) & 0x01010101u);
+        }
+        return wa;
+    };
+    auto qload = [&](int i) {
+        const uint32_t slab = wave * NSW + i;
+        const uint4 qb = c < MR ? *(const uint4 *)(ql + c * qs_ + slab * LB_SLAB + 16 * gq4)
+                                : make_uint4(0, 0, 0, 0);
+        return __builtin_bit_cast(int4_t, qb);
+    };
+    if constexpr (SPB > 0) {
+        // blocks of SPB slabs, whole inside this wave's range
+#pragma unroll
+        for (int b = 0; b < NSW / SPB; b++) {
+            int4_t acc = {0, 0, 0, 0};
+#pragma unroll
+            for (int u = 0; u < SPB; u++)
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(b * SPB + u), qload(b * SPB + u), acc, 0, 0, 0);
+            const uint32_t bb = wave * (NSW / SPB) + b;
+            if (c < MR && bb < nbq) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) dp[v * bs + bb] = acc[v];
+            }
+        }
+    } else {
+        const uint32_t parts = block < (uint32_t)LB_SLAB ? LB_SLAB / block : 1;
+        const uint32_t spb = block > (uint32_t)LB_SLAB ? block / LB_SLAB : 1;  // slabs per block
+        int4_t acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < NSW; i++) {
+            const uint32_t slab = wave * NSW + i;
+            const int4_t wa = expand(i), ab = qload(i);
+            if (parts == 1) {
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, ab, acc, 0, 0, 0);
+                if ((slab + 1) % spb == 0) {  // uniform: the block ends in this wave
+                    const uint32_t bb = slab / spb;
+                    if (c < MR && bb < nbq) {
+#pragma unroll
+                        for (int v = 0; v < 4; v++) dp[v * bs + bb] = acc[v];
+                    }
+                    acc = (int4_t){0, 0, 0, 0};
+                }
+            } else {
+                // blocks shorter than a slab: one masked product per block
+                for (uint32_t pp = 0; pp < parts; pp++) {
+                    const int4_t abp = (uint32_t)(16 * gq4) / block == pp ? ab : (int4_t){0, 0, 0, 0};
+                    const int4_t r4 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, abp, (int4_t){0, 0, 0, 0}, 0, 0, 0);
+                    const uint32_t bb = slab * parts + pp;
+                    if (c < MR && bb < nbq) {
+#pragma unroll
+                        for (int v = 0; v < 4; v++) dp[v * bs + bb] = r4[v];
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // -- 4. fold in block order (reference, matmul.rs:380-393): four blocks'
+    //       sums, scales and factors per LDS load
+    if (t < 16 * (int)mr) {
+        const int fc = t & 15, frow = t >> 4;
+        const int32_t *sp = sb + (frow * 16 + fc) * bs;
+        const uint16_t *cp = scl + fc * bs;
+        const float *ap = sa + frow * nbq;
+        const int32_t *qp = as + frow * nbq;
+        const uint32_t nb_live = (g.k + block - 1) >> g.block_shift;
+        float total = 0.0f;
+        for (uint32_t b0 = 0; b0 < nb_live; b0 += 4) {
+            const int4_t s4 = *(const int4_t *)(sp + b0);
+            const uint2 c4 = *(const uint2 *)(cp + b0);
+            const float4_t a4 = *(const float4_t *)(ap + b0);
+            int4_t q4 = {0, 0, 0, 0};
+            if (KIND == 1) q4 = *(const int4_t *)(qp + b0);
+            const uint16_t sc4[4] = {(uint16_t)c4.x, (uint16_t)(c4.x >> 16), (uint16_t)c4.y, (uint16_t)(c4.y >> 16)};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (b0 + u < nb_live) {
+                    const int32_t sum = KIND == 1 ? 2 * s4[u] - q4[u] : s4[u];
+                    total = fmaf((float)sum, f16_to_f32(sc4[u]) * a4[u], total);
+                }
+            }
+        }
+        const uint32_t j = col0 + fc;
+        if (j < g.n) g.dst[(size_t)frow * g.n + j] = finish<false>(ep, total, frow, j, g.n);
+    }
+}
+
+template <int KIND, int MR, int NG, int SPB>
+hipError_t launch_tile_t(const LtArgs &g, const EpArgs &ep, hipStream_t s) {
+    const size_t lds = tile_lds_bytes(g.kq, g.nbq, MR);
+    if (lds > 64 * 1024) {
+        static bool attr = false;  // benign race: every setter writes the same value
+        if (!attr) {
+            const hipError_t e = hipFuncSetAttribute((const void *)lowbit_tile<KIND, MR, NG, SPB>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     160 * 1024);
+            if (e != hipSuccess) return e;
+            attr = true;
+        }
+    }
+    hipLaunchKernelGGL((lowbit_tile<KIND, MR, NG, SPB>), dim3(g.n_pad / 16), dim3(T), lds, s, g, ep);
+    return hipGetLastError();
+}
+
+template <int KIND, int MR>
+hipError_t launch_tile_ng(const LtArgs &g, const EpArgs &ep, int ng, hipStream_t s) {
+    const bool b128 = g.block_shift == 7;
+    if (ng <= 1) return b128 ? launch_tile_t<KIND, MR, 1, 2>(g, ep, s) : launch_tile_t<KIND, MR, 1, 0>(g, ep, s);
+    if (ng <= 2 || KIND == 1)
+        return b128 ? launch_tile_t<KIND, MR, 2, 2>(g, ep, s) : launch_tile_t<KIND, MR, 2, 0>(g, ep, s);
+    constexpr int NG4 = KIND == 1 ? 2 : 4;
+    return b128 ? launch_tile_t<KIND, MR, NG4, 2>(g, ep, s) : launch_tile_t<KIND, MR, NG4, 0>(g, ep, s);
+}
+
+template <int KIND>
+hipError_t launch_tile(const LtArgs &g, const EpArgs &ep, int mr, int ng, hipStream_t s) {
+    if (mr <= 1) return launch_tile_ng<KIND, 1>(g, ep, ng, s);
+    if (mr <= 4) return launch_tile_ng<KIND, 4>(g, ep, ng, s);
+    return launch_tile_ng<KIND, 8>(g, ep, ng, s);
+}
+
 // One workgroup per (row, block): q for the block's depths (zero past k), the
 // block's s = amax/127 and sum(q). Blocks from k up to kq are all zero.
 __global__ void __launch_bounds__(256) lowbit_quant(const uint16_t *lhs, uint32_t k,
@@ -305,15 +627,73 @@ hipError_t launch_kind(const LbArgs &g, const EpArgs &ep, int mr, hipStream_t s)
     return launch_t<KIND, 16>(g, ep, s);
 }
 
+// The single-launch path's geometry: code groups per lane (NG), the depths
+// the waves cover and the blocks in them; it serves the decode shapes (up to
+// 8 rows, blocks up to one quantization pass, K up to 8192, A in LDS).
+struct TileGeo {
+    bool ok;
+    int ng;
+    uint32_t kq, nbq;
+};
+TileGeo tile_geometry(const WDev &w, size_t m) {
+    TileGeo sg = {false, 0, 0, 0};
+    if (m < 1 || m > 8 || w.block > QPASS || w.block < 16) return sg;
+    const int mr = m <= 1 ? 1 : m <= 4 ? 4 : 8;  // the row counts the kernel is built for
+    const size_t spg = w.kind == W_Q2 ? 4 : 8;
+    const size_t nslab = (w.k + LB_SLAB - 1) / LB_SLAB;
+    const size_t per_wave = (nslab + WV - 1) / WV;
+    const size_t ng_need = (per_wave + spg - 1) / spg;
+    if (ng_need > (w.kind == W_Q2 ? 4u : 2u)) return sg;  // K <= 8192
+    const int ng = ng_need <= 1 ? 1 : ng_need <= 2 ? 2 : 4;
+    const size_t kq = (size_t)WV * ng * spg * LB_SLAB;
+    if (kq < w.block || (size_t)mr * kq > 32768) return sg;
+    // a wave's K range must hold whole blocks (block sums stay in one wave)
+    if (w.block > (size_t)ng * spg * LB_SLAB) return sg;
+    const size_t nbq = (kq / w.block + 3) / 4 * 4;  // whole 16-byte runs of blocks
+    if (nbq > (size_t)T / 2 || tile_lds_bytes((uint32_t)kq, (uint32_t)nbq, mr) > 96 * 1024) return sg;
+    sg.ok = true;
+    sg.ng = ng;
+    sg.kq = (uint32_t)kq;
+    sg.nbq = (uint32_t)nbq;
+    return sg;
+}
+
 }  // namespace
 
 size_t lowbit_scratch_bytes(const WDev &w, size_t m) {
+    if (tile_geometry(w, m).ok) return 0;
     const Geo ge = geometry(w, m);
     return (m * ge.kq + 255) / 256 * 256 + m * ge.nbq * 8;
 }
 
 hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
                               const EpArgs &ep, void *scratch, hipStream_t s) {
+    const TileGeo sg = tile_geometry(w, m);
+    if (sg.ok) {
+        const size_t cb = w.nchunks * w.n_pad * 64;
+        if (m * w.k * 2 >= ((size_t)1 << 31) || w.sc_rows * w.n_pad * 2 >= ((size_t)1 << 31) ||
+            cb >= ((size_t)1 << 31))
+            return hipErrorInvalidValue;  // one buffer resource spans < 2 GiB
+        LtArgs f = {};
+        f.codes = w.codes;
+        f.sc = w.scales;
+        f.lhs = lhs;
+        f.dst = dst;
+        f.n = (uint32_t)w.n;
+        f.k = (uint32_t)w.k;
+        f.n_pad = (uint32_t)w.n_pad;
+        f.m = (uint32_t)m;
+        f.block_shift = ilog2(w.block);
+        f.codebook = w.codebook;
+        f.sc_rows = (uint32_t)w.sc_rows;
+        f.ngroups = (uint32_t)w.nchunks;
+        f.kq = sg.kq;
+        f.nbq = sg.nbq;
+        f.codes_bytes = (uint32_t)cb;
+        const int mr = m <= 1 ? 1 : m <= 4 ? 4 : 8;
+        if (w.kind == W_Q2) return launch_tile<2>(f, ep, mr, sg.ng, s);
+        return launch_tile<1>(f, ep, mr, sg.ng, s);
+    }
     const Geo ge = geometry(w, m);
     if (m * ge.kq >= ((size_t)1 << 31) || w.sc_rows * w.n_pad * 2 >= ((size_t)1 << 31))
         return hipErrorInvalidValue;  // one buffer resource spans < 2 GiB

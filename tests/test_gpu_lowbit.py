@@ -51,6 +51,31 @@ def test_kernels_match_reference_bits(smg, orc, si, bi, block):
         assert np.array_equal(got, want), f"q1 {m}x{n}x{k} {block} layout {layout}"
 
 
+@pytest.mark.parametrize("block", [32, 256, 512, 1024, 2048])
+@pytest.mark.parametrize("m,n,k", [(1, 300, 9000), (3, 129, 4096), (8, 64, 5000), (2, 40, 700),
+                                   (1, 20000, 512), (1, 300, 8000)])
+def test_single_launch_blocks_and_segments(smg, orc, block, m, n, k):
+    """The streaming path and its limits: blocks within a wave's K range and
+    blocks spanning waves (amax and sum(q) combined through LDS, block sums
+    through integer atomics), A quantized over several passes, more tiles per
+    workgroup than the ring holds (N = 20000), the widest K ranges per lane,
+    partial last blocks, and shapes past its limits (the two-kernel path)."""
+    nbk = -(-k // block)
+    rng = np.random.default_rng(block * 7 + m)
+    scales = orc.f32_to_f16(rng.uniform(0.01, 0.05, n * nbk).astype(np.float32))
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    codes = rng.integers(0, 256, (k * n + 3) // 4, dtype=np.uint8)
+    q2 = smg.Q2Weights(codes, scales, n, k, smg.Q2Params(block))
+    got = np.zeros(m * n, np.uint16)
+    smg.matmul_q2(a, q2, got, m)
+    assert np.array_equal(got, orc.lowbit_reference(2, a, codes, scales, m, n, k, block, (-1, 0, 1, 0)))
+    signs = rng.integers(0, 256, (k * n + 7) // 8, dtype=np.uint8)
+    q1 = smg.Q1Weights(signs, scales, smg.WeightLayout.InOut, n, k, block)
+    got = np.zeros(m * n, np.uint16)
+    smg.matmul_q1(a, q1, got, m)
+    assert np.array_equal(got, orc.lowbit_reference(1, a, signs, scales, m, n, k, block, inout=True))
+
+
 @pytest.mark.parametrize("m", [1, 8])
 def test_config2_q2_ternary(smg, orc, m):
     """K=4096, N=11008, block 128, ternary; bitwise."""
