@@ -311,6 +311,62 @@ __device__ float ep_cell(const EpArgs &ep, float x, size_t i, size_t j, size_t n
     return x;
 }
 
+// Operands of the first EP_PRE nodes of one cell, loaded ahead of time (raw
+// 16-bit elements; scalar nodes need none) so a kernel can issue these loads
+// with its other early loads instead of after its result is ready.
+constexpr int EP_PRE = 4;
+struct EpPre {
+    uint32_t raw[EP_PRE];
+};
+__device__ __forceinline__ EpPre ep_prefetch(const EpArgs &ep, size_t i, size_t j, size_t n) {
+    EpPre pre;
+#pragma unroll
+    for (int q = 0; q < EP_PRE; q++) {
+        pre.raw[q] = 0;
+        if ((uint32_t)q < ep.n_nodes) {
+            const EpNode &nd = ep.nodes[q];
+            const uint16_t *p = (const uint16_t *)nd.ptr;
+            switch (ep.cls[q]) {
+            case EPC_ROW: pre.raw[q] = p[i]; break;
+            case EPC_COL: pre.raw[q] = p[j]; break;
+            case EPC_TENSOR: pre.raw[q] = p[i * (nd.ld == 0 ? n : nd.ld) + j]; break;
+            default: break;
+            }
+        }
+    }
+    return pre;
+}
+
+// finish() with the first EP_PRE operands taken from ep_prefetch.
+template <bool BF16>
+__device__ __forceinline__ uint16_t finish_pre(const EpArgs &ep, const EpPre &pre, float acc, size_t i,
+                                               size_t j, size_t n) {
+    uint16_t c = from_f32<BF16>(acc);
+    if (ep.n_nodes == 0) return c;
+    float x = to_f32<BF16>(c);
+#pragma unroll
+    for (int q = 0; q < EP_PRE; q++) {
+        if ((uint32_t)q < ep.n_nodes) {
+            const EpNode &nd = ep.nodes[q];
+            const float v = ep.cls[q] == EPC_SCALAR ? nd.scalar : to_f32<BF16>((uint16_t)pre.raw[q]);
+            x = ep.fam[q] == EPF_ACT ? act_f32(nd.aux, x, nd.scalar) : ep_arith(ep.fam[q], x, v);
+        }
+    }
+    for (uint32_t q = EP_PRE; q < ep.n_nodes; q++) {
+        const EpNode &nd = ep.nodes[q];
+        const uint16_t *p = (const uint16_t *)nd.ptr;
+        float v = nd.scalar;
+        switch (ep.cls[q]) {
+        case EPC_ROW: v = to_f32<BF16>(p[i]); break;
+        case EPC_COL: v = to_f32<BF16>(p[j]); break;
+        case EPC_TENSOR: v = to_f32<BF16>(p[i * (nd.ld == 0 ? n : nd.ld) + j]); break;
+        default: break;
+        }
+        x = ep.fam[q] == EPF_ACT ? act_f32(nd.aux, x, nd.scalar) : ep_arith(ep.fam[q], x, v);
+    }
+    return from_f32<BF16>(x);
+}
+
 // Final store of one output: round the accumulator-derived value to T, then
 // (iff the graph is non-empty) run the graph in f32 on that rounded value and
 // round again -- "GEMM to T, then apply_ep_scalar" (src/exec/macros.rs:188-206).

@@ -237,12 +237,37 @@ struct LtArgs {
     uint32_t kq;           // depths the waves cover (8 waves x NG groups)
     uint32_t nbq;          // blocks in kq (a multiple of 4)
     uint32_t codes_bytes;  // extent of the code array (buffer resource)
+    uint32_t cg_shift;     // log2 of the 16-column groups per workgroup (CG)
 };
 
 __device__ __forceinline__ float nanmax(float a, float b) {
     return (a != a) ? a : ((b != b) ? b : fmaxf(a, b));
 }
-// Reductions over aligned groups of gl lanes (gl a power of two <= 64).
+// Reductions over aligned groups of gl lanes (gl a power of two <= 64): DPP
+// within 16-lane rows (quad swaps, then the half-row and row mirrors pair
+// each lane with one from the other half), cross-lane shuffles beyond.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t a, uint32_t gl) {
+    if (gl > 1) a = max(a, dpp<0xB1>(a));   // quad_perm [1,0,3,2]
+    if (gl > 2) a = max(a, dpp<0x4E>(a));   // quad_perm [2,3,0,1]
+    if (gl > 4) a = max(a, dpp<0x141>(a));  // row_half_mirror
+    if (gl > 8) a = max(a, dpp<0x140>(a));  // row_mirror
+    if (gl > 16) a = max(a, (uint32_t)__shfl_xor((int)a, 16));
+    if (gl > 32) a = max(a, (uint32_t)__shfl_xor((int)a, 32));
+    return a;
+}
+__device__ __forceinline__ int32_t group_sum_i32(int32_t a, uint32_t gl) {
+    if (gl > 1) a += (int32_t)dpp<0xB1>((uint32_t)a);
+    if (gl > 2) a += (int32_t)dpp<0x4E>((uint32_t)a);
+    if (gl > 4) a += (int32_t)dpp<0x141>((uint32_t)a);
+    if (gl > 8) a += (int32_t)dpp<0x140>((uint32_t)a);
+    if (gl > 16) a += __shfl_xor(a, 16);
+    if (gl > 32) a += __shfl_xor(a, 32);
+    return a;
+}
 __device__ __forceinline__ float group_max(float a, uint32_t gl) {
     for (uint32_t off = 1; off < gl; off <<= 1) a = nanmax(a, __shfl_xor(a, (int)off));
     return a;
@@ -253,10 +278,10 @@ __device__ __forceinline__ int32_t group_sum(int32_t a, uint32_t gl) {
 }
 
 // LDS: q [MR][kq + 16] i8 | s [MR][nbq] f32 | sum(q) [MR][nbq] i32 |
-//      block sums [MR][16][nbq + 4] i32 | scales [16][nbq + 4] f16 | wave partials
-size_t tile_lds_bytes(uint32_t kq, uint32_t nbq, int mr) {
-    return (size_t)mr * (kq + 16) + (size_t)mr * nbq * 8 + (size_t)mr * 16 * (nbq + 4) * 4 +
-           (size_t)16 * (nbq + 4) * 2 + (size_t)mr * WV * 8;
+//      block sums [MR][16 CG][nbq + 4] i32 | scales [16 CG][nbq + 4] f16 | wave partials
+size_t tile_lds_bytes(uint32_t kq, uint32_t nbq, int mr, uint32_t cg) {
+    return (size_t)mr * (kq + 16) + (size_t)mr * nbq * 8 + (size_t)mr * 16 * cg * (nbq + 4) * 4 +
+           (size_t)16 * cg * (nbq + 4) * 2 + (size_t)mr * WV * 8;
 }
 
 // SPB: slabs per block when fixed at compile time (2 = blocks of 128, the
@@ -266,24 +291,29 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr uint32_t SPG = KIND == 2 ? 4 : 8;  // slabs per code group
     constexpr int NSW = NG * (int)SPG;            // slabs per wave
-    constexpr int QP = (NSW * WV * LB_SLAB + QPASS - 1) / QPASS;  // A passes (<= 2)
+    constexpr int QP = 2;                         // A passes held in registers (K <= 8192)
     const uint32_t block = 1u << g.block_shift;
     const uint32_t nbq = g.nbq, kq = g.kq;
+    const uint32_t cg = 1u << g.cg_shift;         // 16-column groups in this workgroup
+    const uint32_t ncol = 16 * cg;
     const uint32_t qs_ = kq + 16;   // q row stride (bytes)
     const uint32_t bs = nbq + 4;    // block-sum / scale row stride (elements)
     int8_t *ql = (int8_t *)smem;                        // [MR][qs_]
     float *sa = (float *)(smem + MR * qs_);             // [MR][nbq]
     int32_t *as = (int32_t *)(sa + MR * nbq);           // [MR][nbq]
-    int32_t *sb = as + MR * nbq;                        // [MR][16][bs]
-    uint16_t *scl = (uint16_t *)(sb + MR * 16 * bs);    // [16][bs]
-    float *wmax = (float *)(scl + 16 * bs);             // [MR][WV]
+    int32_t *sb = as + MR * nbq;                        // [MR][ncol][bs]
+    uint16_t *scl = (uint16_t *)(sb + MR * ncol * bs);  // [ncol][bs]
+    float *wmax = (float *)(scl + ncol * bs);           // [MR][WV]
     int32_t *wsum = (int32_t *)(wmax + MR * WV);        // [MR][WV]
 
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int gq4 = lane >> 4, c = lane & 15;
-    const uint32_t col0 = xcd_tile(blockIdx.x, gridDim.x) * 16;
-    const uint32_t mr = g.m;  // <= MR
+    // wave -> (column group gi, K range kw): 8 / CG waves share a column group
+    const uint32_t wpg_shift = 3 - g.cg_shift;
+    const uint32_t gi = (uint32_t)wave >> wpg_shift, kw = (uint32_t)wave & ((1u << wpg_shift) - 1);
+    const uint32_t wg_col0 = xcd_tile(blockIdx.x, gridDim.x) * ncol;
+    const uint32_t col0 = wg_col0 + gi * 16;  // this wave's 16 columns
     const rsrc_t ar = make_rsrc(g.lhs, g.m * g.k * 2u);
     const bool vec = (g.k & 7) == 0;
 
@@ -292,21 +322,30 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
 #pragma unroll
     for (int p = 0; p < QP; p++)
 #pragma unroll
-        for (int r = 0; r < MR; r++) areg[p][r] = load_row8(ar, r, g.m, g.k, p * QPASS + 8 * t, vec);
+        for (int r = 0; r < MR; r++)
+            areg[p][r] = (uint32_t)p * QPASS < kq ? load_row8(ar, r, g.m, g.k, p * QPASS + 8 * t, vec)
+                                                  : make_uint4(0, 0, 0, 0);
+    // scale rows next (waited on before the first barrier), then the
+    // epilogue operands, then the codes: vmcnt retires in issue order, so
+    // the codes can still be in flight when the waits before them end
+    uint4 sreg;
+    {
+        const rsrc_t sr = make_rsrc(g.sc, g.sc_rows * g.n_pad * 2u);
+        const uint32_t bb = t >> (g.cg_shift + 1), piece = t & (2 * cg - 1);  // 8 columns a piece
+        sreg = bload16(sr, (bb < nbq && bb < g.sc_rows) ? (bb * g.n_pad + wg_col0 + piece * 8) * 2u : OOB);
+    }
+    const bool folder = (uint32_t)t < ncol * g.m;
+    const int fc = t & (ncol - 1), frow = t >> (4 + g.cg_shift);
+    EpPre pre = {};
+    if (folder && wg_col0 + fc < g.n) pre = ep_prefetch(ep, frow, wg_col0 + fc, g.n);
     uint4 wreg[NG];
     {
         const rsrc_t cr = make_rsrc(g.codes, g.codes_bytes);
 #pragma unroll
         for (int i = 0; i < NG; i++) {
-            const uint32_t grp = wave * NG + i;
+            const uint32_t grp = kw * NG + i;
             wreg[i] = bload16(cr, grp < g.ngroups ? ((grp * g.n_pad + col0 + c) * 4 + gq4) * 16 : OOB);
         }
-    }
-    uint4 sreg;
-    {
-        const rsrc_t sr = make_rsrc(g.sc, g.sc_rows * g.n_pad * 2u);
-        const uint32_t bb = t / 2;
-        sreg = bload16(sr, (bb < nbq && bb < g.sc_rows) ? (bb * g.n_pad + col0) * 2u + (t % 2) * 16u : OOB);
     }
 
     // -- 2. quantize A (quantize_row, src/kernels/lowbit/matmul.rs:354-371)
@@ -314,15 +353,19 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
     const uint32_t wpb = block > 512u ? block / 512u : 1u;   // waves of a block
 #pragma unroll
     for (int p = 0; p < QP; p++) {
+        if ((uint32_t)p * QPASS >= kq) break;  // uniform
         const uint32_t d0 = p * QPASS + 8 * t;
+        // |a| as f16 magnitude bits: their unsigned order is the numeric order,
+        // and every NaN pattern sorts above infinity, so an integer max is the
+        // reference's NaN-propagating amax
         float am[MR];
 #pragma unroll
         for (int r = 0; r < MR; r++) {
-            const uint32_t wd[4] = {areg[p][r].x, areg[p][r].y, areg[p][r].z, areg[p][r].w};
-            float a = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; e++) a = nanmax(a, fabsf(f16_to_f32((uint16_t)(wd[e / 2] >> (16 * (e % 2))))));
-            am[r] = group_max(a, gl);
+            const uint32_t w0 = areg[p][r].x & 0x7FFF7FFFu, w1 = areg[p][r].y & 0x7FFF7FFFu;
+            const uint32_t w2 = areg[p][r].z & 0x7FFF7FFFu, w3 = areg[p][r].w & 0x7FFF7FFFu;
+            const uint32_t lo = max(max(w0 & 0xFFFFu, w1 & 0xFFFFu), max(w2 & 0xFFFFu, w3 & 0xFFFFu));
+            const uint32_t hi = max(max(w0 >> 16, w1 >> 16), max(w2 >> 16, w3 >> 16));
+            am[r] = f16_to_f32((uint16_t)group_max_u32(max(lo, hi), gl));
         }
         if (wpb > 1) {  // blocks longer than a wave: combine the waves' maxima
             if (p > 0) __syncthreads();
@@ -354,7 +397,7 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
                 sum += qi;
             }
             if (d0 < kq) *(uint2 *)(ql + r * qs_ + d0) = make_uint2(qw0, qw1);
-            qs[r] = KIND == 1 ? group_sum(sum, gl) : 0;
+            qs[r] = KIND == 1 ? group_sum_i32(sum, gl) : 0;
         }
         if (KIND == 1 && wpb > 1) {
             if (lane == 0)
@@ -378,10 +421,11 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
             }
         }
     }
-    if ((uint32_t)t < 2 * nbq) {  // transpose: scale of (block t/2, column 8(t%2)+e)
+    if ((uint32_t)t < 2 * cg * nbq) {  // transpose: scale of (block bb, column 8 piece + e)
+        const uint32_t bb = t >> (g.cg_shift + 1), piece = t & (2 * cg - 1);
         const uint32_t sw[4] = {sreg.x, sreg.y, sreg.z, sreg.w};
 #pragma unroll
-        for (int e = 0; e < 8; e++) scl[(8 * (t % 2) + e) * bs + t / 2] = (uint16_t)(sw[e / 2] >> (16 * (e % 2)));
+        for (int e = 0; e < 8; e++) scl[(8 * piece + e) * bs + bb] = (uint16_t)(sw[e / 2] >> (16 * (e % 2)));
     }
     __syncthreads();
 
@@ -389,7 +433,7 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
     //       of expanded codes, B = 64 depths x up to 16 rows of q
     // lane (gq4, c) holds the sums of columns 4*gq4 + v, row c; rows m..MR-1
     // of q are zero, so their sums are too
-    int32_t *dp = sb + (c * 16 + 4 * gq4) * bs;
+    int32_t *dp = sb + (c * ncol + gi * 16 + 4 * gq4) * bs;
     auto expand = [&](int i) {
         const uint4 wv = wreg[i / SPG];
         const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
@@ -407,23 +451,31 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
         return wa;
     };
     auto qload = [&](int i) {
-        const uint32_t slab = wave * NSW + i;
+        const uint32_t slab = kw * NSW + i;
         const uint4 qb = c < MR ? *(const uint4 *)(ql + c * qs_ + slab * LB_SLAB + 16 * gq4)
                                 : make_uint4(0, 0, 0, 0);
         return __builtin_bit_cast(int4_t, qb);
     };
     if constexpr (SPB > 0) {
-        // blocks of SPB slabs, whole inside this wave's range
+        // blocks of SPB slabs, whole inside this wave's range; independent
+        // accumulators, written after the last product
+        constexpr int NBW = NSW / SPB;
+        int4_t acc[NBW];
 #pragma unroll
-        for (int b = 0; b < NSW / SPB; b++) {
-            int4_t acc = {0, 0, 0, 0};
+        for (int b = 0; b < NBW; b++) {
+            acc[b] = (int4_t){0, 0, 0, 0};
 #pragma unroll
             for (int u = 0; u < SPB; u++)
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(b * SPB + u), qload(b * SPB + u), acc, 0, 0, 0);
-            const uint32_t bb = wave * (NSW / SPB) + b;
-            if (c < MR && bb < nbq) {
+                acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(b * SPB + u), qload(b * SPB + u), acc[b], 0, 0, 0);
+        }
+        if (c < MR) {
 #pragma unroll
-                for (int v = 0; v < 4; v++) dp[v * bs + bb] = acc[v];
+            for (int b = 0; b < NBW; b++) {
+                const uint32_t bb = kw * NBW + b;
+                if (bb < nbq) {
+#pragma unroll
+                    for (int v = 0; v < 4; v++) dp[v * bs + bb] = acc[b][v];
+                }
             }
         }
     } else {
@@ -432,7 +484,7 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
         int4_t acc = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < NSW; i++) {
-            const uint32_t slab = wave * NSW + i;
+            const uint32_t slab = kw * NSW + i;
             const int4_t wa = expand(i), ab = qload(i);
             if (parts == 1) {
                 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, ab, acc, 0, 0, 0);
@@ -462,37 +514,47 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
 
     // -- 4. fold in block order (reference, matmul.rs:380-393): four blocks'
     //       sums, scales and factors per LDS load
-    if (t < 16 * (int)mr) {
-        const int fc = t & 15, frow = t >> 4;
-        const int32_t *sp = sb + (frow * 16 + fc) * bs;
+    if (folder) {
+        const int32_t *sp = sb + (frow * ncol + fc) * bs;
         const uint16_t *cp = scl + fc * bs;
         const float *ap = sa + frow * nbq;
         const int32_t *qp = as + frow * nbq;
         const uint32_t nb_live = (g.k + block - 1) >> g.block_shift;
         float total = 0.0f;
-        for (uint32_t b0 = 0; b0 < nb_live; b0 += 4) {
-            const int4_t s4 = *(const int4_t *)(sp + b0);
-            const uint2 c4 = *(const uint2 *)(cp + b0);
-            const float4_t a4 = *(const float4_t *)(ap + b0);
-            int4_t q4 = {0, 0, 0, 0};
-            if (KIND == 1) q4 = *(const int4_t *)(qp + b0);
-            const uint16_t sc4[4] = {(uint16_t)c4.x, (uint16_t)(c4.x >> 16), (uint16_t)c4.y, (uint16_t)(c4.y >> 16)};
+        for (uint32_t b0 = 0; b0 < nb_live; b0 += 16) {
+            // 16 blocks' operands in flight before the fma chain
+            int4_t s4[4], q4[4];
+            uint2 c4[4];
+            float4_t a4[4];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                if (b0 + u < nb_live) {
-                    const int32_t sum = KIND == 1 ? 2 * s4[u] - q4[u] : s4[u];
-                    total = fmaf((float)sum, f16_to_f32(sc4[u]) * a4[u], total);
+            for (int h = 0; h < 4; h++) {
+                const uint32_t bh = b0 + 4 * h < nbq ? b0 + 4 * h : 0;
+                s4[h] = *(const int4_t *)(sp + bh);
+                c4[h] = *(const uint2 *)(cp + bh);
+                a4[h] = *(const float4_t *)(ap + bh);
+                q4[h] = KIND == 1 ? *(const int4_t *)(qp + bh) : (int4_t){0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                const uint16_t sc4[4] = {(uint16_t)c4[h].x, (uint16_t)(c4[h].x >> 16), (uint16_t)c4[h].y,
+                                         (uint16_t)(c4[h].y >> 16)};
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    if (b0 + 4 * h + u < nb_live) {
+                        const int32_t sum = KIND == 1 ? 2 * s4[h][u] - q4[h][u] : s4[h][u];
+                        total = fmaf((float)sum, f16_to_f32(sc4[u]) * a4[h][u], total);
+                    }
                 }
             }
         }
-        const uint32_t j = col0 + fc;
-        if (j < g.n) g.dst[(size_t)frow * g.n + j] = finish<false>(ep, total, frow, j, g.n);
+        const uint32_t j = wg_col0 + fc;
+        if (j < g.n) g.dst[(size_t)frow * g.n + j] = finish_pre<false>(ep, pre, total, frow, j, g.n);
     }
 }
 
 template <int KIND, int MR, int NG, int SPB>
 hipError_t launch_tile_t(const LtArgs &g, const EpArgs &ep, hipStream_t s) {
-    const size_t lds = tile_lds_bytes(g.kq, g.nbq, MR);
+    const size_t lds = tile_lds_bytes(g.kq, g.nbq, MR, 1u << g.cg_shift);
     if (lds > 64 * 1024) {
         static bool attr = false;  // benign race: every setter writes the same value
         if (!attr) {
@@ -503,7 +565,8 @@ hipError_t launch_tile_t(const LtArgs &g, const EpArgs &ep, hipStream_t s) {
             attr = true;
         }
     }
-    hipLaunchKernelGGL((lowbit_tile<KIND, MR, NG, SPB>), dim3(g.n_pad / 16), dim3(T), lds, s, g, ep);
+    hipLaunchKernelGGL((lowbit_tile<KIND, MR, NG, SPB>), dim3(g.n_pad / (16u << g.cg_shift)), dim3(T), lds,
+                       s, g, ep);
     return hipGetLastError();
 }
 
@@ -511,10 +574,11 @@ template <int KIND, int MR>
 hipError_t launch_tile_ng(const LtArgs &g, const EpArgs &ep, int ng, hipStream_t s) {
     const bool b128 = g.block_shift == 7;
     if (ng <= 1) return b128 ? launch_tile_t<KIND, MR, 1, 2>(g, ep, s) : launch_tile_t<KIND, MR, 1, 0>(g, ep, s);
-    if (ng <= 2 || KIND == 1)
-        return b128 ? launch_tile_t<KIND, MR, 2, 2>(g, ep, s) : launch_tile_t<KIND, MR, 2, 0>(g, ep, s);
-    constexpr int NG4 = KIND == 1 ? 2 : 4;
-    return b128 ? launch_tile_t<KIND, MR, NG4, 2>(g, ep, s) : launch_tile_t<KIND, MR, NG4, 0>(g, ep, s);
+    if (ng <= 2) return b128 ? launch_tile_t<KIND, MR, 2, 2>(g, ep, s) : launch_tile_t<KIND, MR, 2, 0>(g, ep, s);
+    if (ng <= 4 || KIND == 1)
+        return b128 ? launch_tile_t<KIND, MR, 4, 2>(g, ep, s) : launch_tile_t<KIND, MR, 4, 0>(g, ep, s);
+    constexpr int NG8 = KIND == 1 ? 4 : 8;
+    return b128 ? launch_tile_t<KIND, MR, NG8, 2>(g, ep, s) : launch_tile_t<KIND, MR, NG8, 0>(g, ep, s);
 }
 
 template <int KIND>
@@ -633,29 +697,47 @@ hipError_t launch_kind(const LbArgs &g, const EpArgs &ep, int mr, hipStream_t s)
 struct TileGeo {
     bool ok;
     int ng;
-    uint32_t kq, nbq;
+    uint32_t kq, nbq, cg_shift;
 };
-TileGeo tile_geometry(const WDev &w, size_t m) {
-    TileGeo sg = {false, 0, 0, 0};
-    if (m < 1 || m > 8 || w.block > QPASS || w.block < 16) return sg;
+// Column groups per workgroup: enough that the grid is about one workgroup
+// per CU (the per-workgroup quantization of A and the fold are then paid once
+// per CU); a wave's K range grows with them.
+TileGeo tile_geometry_cg(const WDev &w, size_t m, uint32_t cg_shift) {
+    TileGeo sg = {false, 0, 0, 0, cg_shift};
     const int mr = m <= 1 ? 1 : m <= 4 ? 4 : 8;  // the row counts the kernel is built for
     const size_t spg = w.kind == W_Q2 ? 4 : 8;
+    const size_t wpg = (size_t)WV >> cg_shift;   // waves along K per column group
     const size_t nslab = (w.k + LB_SLAB - 1) / LB_SLAB;
-    const size_t per_wave = (nslab + WV - 1) / WV;
+    const size_t per_wave = (nslab + wpg - 1) / wpg;
     const size_t ng_need = (per_wave + spg - 1) / spg;
-    if (ng_need > (w.kind == W_Q2 ? 4u : 2u)) return sg;  // K <= 8192
-    const int ng = ng_need <= 1 ? 1 : ng_need <= 2 ? 2 : 4;
-    const size_t kq = (size_t)WV * ng * spg * LB_SLAB;
-    if (kq < w.block || (size_t)mr * kq > 32768) return sg;
+    const size_t ng_max = w.kind == W_Q2 ? 8 : 4;
+    if (ng_need > ng_max) return sg;
+    const int ng = ng_need <= 1 ? 1 : ng_need <= 2 ? 2 : ng_need <= 4 ? 4 : 8;
+    const size_t kq = wpg * ng * spg * LB_SLAB;
+    if (kq > 2 * QPASS || kq < w.block || (size_t)mr * kq > 32768) return sg;
     // a wave's K range must hold whole blocks (block sums stay in one wave)
     if (w.block > (size_t)ng * spg * LB_SLAB) return sg;
     const size_t nbq = (kq / w.block + 3) / 4 * 4;  // whole 16-byte runs of blocks
-    if (nbq > (size_t)T / 2 || tile_lds_bytes((uint32_t)kq, (uint32_t)nbq, mr) > 96 * 1024) return sg;
+    const size_t cg = (size_t)1 << cg_shift;
+    if (2 * cg * nbq > (size_t)T || tile_lds_bytes((uint32_t)kq, (uint32_t)nbq, mr, (uint32_t)cg) > 96 * 1024)
+        return sg;
     sg.ok = true;
     sg.ng = ng;
     sg.kq = (uint32_t)kq;
     sg.nbq = (uint32_t)nbq;
     return sg;
+}
+TileGeo tile_geometry(const WDev &w, size_t m) {
+    TileGeo none = {false, 0, 0, 0, 0};
+    if (m < 1 || m > 8 || w.block > QPASS || w.block < 16) return none;
+    const size_t tiles16 = w.n_pad / 16;
+    uint32_t want = 0;  // smallest CG with at most ~1.5 workgroups per CU (256 CUs)
+    while (want < 2 && (tiles16 >> want) > 384) want++;
+    for (int cs = (int)want; cs >= 0; cs--) {
+        const TileGeo g = tile_geometry_cg(w, m, (uint32_t)cs);
+        if (g.ok) return g;
+    }
+    return none;
 }
 
 }  // namespace
@@ -690,6 +772,7 @@ hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint
         f.kq = sg.kq;
         f.nbq = sg.nbq;
         f.codes_bytes = (uint32_t)cb;
+        f.cg_shift = sg.cg_shift;
         const int mr = m <= 1 ? 1 : m <= 4 ? 4 : 8;
         if (w.kind == W_Q2) return launch_tile<2>(f, ep, mr, sg.ng, s);
         return launch_tile<1>(f, ep, mr, sg.ng, s);
