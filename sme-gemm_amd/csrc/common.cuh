@@ -234,6 +234,71 @@ __device__ __noinline__ F8 act8(uint32_t kind, F8 x, float alpha) {
     return x;
 }
 
+// The same activations evaluated in f32 (device libm), for the f16/bf16 GEMM
+// stores, whose results are held to a tolerance rather than to the bits: the
+// value then rounds to 16 bits, so it differs from the f64 formula's only when
+// the two straddle a 16-bit rounding boundary (at most one 16-bit ulp).
+// Piecewise-linear kinds (relu, clamps, abs, neg, sign, leaky) are exact.
+__device__ __forceinline__ float clampf_(float x, float lo, float hi) {
+    if (x < lo) x = lo;
+    if (x > hi) x = hi;
+    return x;
+}
+__device__ __forceinline__ float act_f32_fast(uint32_t kind, float x, float a) {
+    switch (kind) {
+    case 1: return maxnumf(x, 0.0f);
+    case 2: return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x)));
+    case 3: return x / (1.0f + expf(-x));
+    case 4: return tanhf(x);
+    case 5: return 1.0f / (1.0f + expf(-x));
+    case 6: return x >= 0.0f ? x : a * x;
+    case 7: return clampf_(x, 0.0f, 6.0f);
+    case 8: return clampf_(x / 6.0f + 0.5f, 0.0f, 1.0f);
+    case 9: return x * clampf_(x / 6.0f + 0.5f, 0.0f, 1.0f);
+    case 10: return fabsf(x);
+    case 11: return -x;
+    case 12: return x * x;
+    case 13: return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
+    case 14: return sqrtf(x);
+    case 15: return x / (1.0f + fabsf(x));
+    case 16: return 1.0f / x;
+    case 17: return 1.0f / sqrtf(x);
+    case 18: return expf(x);
+    case 19: return logf(x);
+    case 20: return x >= 0.0f ? x : a * expm1f(x);
+    case 21: return 1.0507009873554805f * (x >= 0.0f ? x : 1.6732632423543772f * expm1f(x));
+    case 22: return maxnumf(x, 0.0f) + log1pf(expf(-fabsf(x)));
+    case 23: return x * tanhf(maxnumf(x, 0.0f) + log1pf(expf(-fabsf(x))));
+    case 24: {
+        const float xe = x * 0.70710678118654752440f, ax = fabsf(xe);
+        const float t = 1.0f / (1.0f + 0.3275911f * ax);
+        const float poly =
+            ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t + 0.254829592f) * t;
+        const float e = 1.0f - poly * expf(-ax * ax);
+        return 0.5f * x * (1.0f + (xe < 0.0f ? -e : e));
+    }
+    default: return x;
+    }
+}
+__device__ __noinline__ F8 act8_fast(uint32_t kind, F8 x, float alpha) {
+    switch (kind) {
+#define SMG_ACT8F_CASE(K)                                                                 \
+    case K:                                                                               \
+        _Pragma("unroll") for (int e = 0; e < 8; e++) x.v[e] = act_f32_fast(K, x.v[e], alpha); \
+        break;
+        SMG_ACT8F_CASE(1) SMG_ACT8F_CASE(2) SMG_ACT8F_CASE(3) SMG_ACT8F_CASE(4) SMG_ACT8F_CASE(5)
+        SMG_ACT8F_CASE(6) SMG_ACT8F_CASE(7) SMG_ACT8F_CASE(8) SMG_ACT8F_CASE(9) SMG_ACT8F_CASE(10)
+        SMG_ACT8F_CASE(11) SMG_ACT8F_CASE(12) SMG_ACT8F_CASE(13) SMG_ACT8F_CASE(14)
+        SMG_ACT8F_CASE(15) SMG_ACT8F_CASE(16) SMG_ACT8F_CASE(17) SMG_ACT8F_CASE(18)
+        SMG_ACT8F_CASE(19) SMG_ACT8F_CASE(20) SMG_ACT8F_CASE(21) SMG_ACT8F_CASE(22)
+        SMG_ACT8F_CASE(23) SMG_ACT8F_CASE(24)
+#undef SMG_ACT8F_CASE
+    default:
+        break;
+    }
+    return x;
+}
+
 // Operand class of an op-graph node: which operand element a cell reads.
 enum EpClass : uint32_t { EPC_SCALAR = 0, EPC_ROW = 1, EPC_COL = 2, EPC_TENSOR = 3 };
 // Arithmetic family of a node.

@@ -29,7 +29,11 @@ namespace smg {
 namespace {
 
 constexpr int BN = 128, BK = 64;
-constexpr int LDS_STRIDE = BK + 8;  // halfs per LDS row (pad: conflict-free fragment reads)
+constexpr int LDS_STRIDE = BK;  // halfs per LDS row: 8 chunks of 16 bytes, swizzled
+
+// 16-byte chunk c of LDS row r lives at chunk c ^ (r & 7) of that row, so the
+// rows a fragment read or a tile store touches together hit different banks.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * LDS_STRIDE + ((chunk ^ (row & 7)) << 3); }
 
 struct GemmArgs {
     const uint16_t *lhs;
@@ -132,23 +136,25 @@ __device__ __forceinline__ void b_load(const GemmArgs &g, uint32_t col0, uint32_
     r.dc = dc;
 }
 
-template <int WK, bool BF16, bool AFFINE, int UD>
+// PD: blocks shorter than a thread's UD depths, so scales vary per depth
+// (a separate instantiation keeps that rare path out of the common kernel).
+template <int WK, bool BF16, bool AFFINE, int UD, bool PD>
 __device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, uint32_t k0,
                                         const BRegs<UD> &r, uint16_t *blds) {
     const int t = threadIdx.x;
     const int cl = t % 128;
     const int dl = (t / 128) * UD;
-    uint16_t *dstp = blds + cl * LDS_STRIDE + dl;
     if constexpr (WK == W_F16 || WK == W_BF16) {
 #pragma unroll
         for (int q = 0; q < UD / 8; q++)
-            *(uint4 *)(dstp + q * 8) = r.live ? make_uint4(r.v[4 * q], r.v[4 * q + 1], r.v[4 * q + 2], r.v[4 * q + 3])
-                                              : make_uint4(0, 0, 0, 0);
+            *(uint4 *)(blds + swz(cl, dl / 8 + q)) =
+                r.live ? make_uint4(r.v[4 * q], r.v[4 * q + 1], r.v[4 * q + 2], r.v[4 * q + 3])
+                       : make_uint4(0, 0, 0, 0);
         return;
     }
     const uint32_t col = col0 + cl;
     const uint32_t d0 = r.dc;  // per-depth scales are read at clamped depths
-    const bool per_depth = (1u << g.block_shift) < (uint32_t)UD;  // scale per depth
+    constexpr bool per_depth = PD;  // scale per depth
     const uint16_t us = r.live ? r.s : (uint16_t)0;
     const uint16_t um = r.live ? r.mn : (uint16_t)0;
     uint32_t out[UD / 2];
@@ -246,7 +252,7 @@ __device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, uint32
     // depth order inside out[]: natural (depth x at half-word x)
 #pragma unroll
     for (int q = 0; q < UD / 8; q++)
-        *(uint4 *)(dstp + q * 8) = make_uint4(out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]);
+        *(uint4 *)(blds + swz(cl, dl / 8 + q)) = make_uint4(out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]);
 }
 
 // ---- A tile: BM rows x 64 depths; thread t: row t/2, 32 depths --------------
@@ -279,30 +285,29 @@ __device__ __forceinline__ void a_load(const GemmArgs &g, uint32_t row0, uint32_
 
 __device__ __forceinline__ void a_store(const uint4 (&ra)[4], uint16_t *alds) {
     const int t = threadIdx.x;
-    uint16_t *dstp = alds + (t / 2) * LDS_STRIDE + (t % 2) * 32;
 #pragma unroll
-    for (int q = 0; q < 4; q++) *(uint4 *)(dstp + q * 8) = ra[q];
+    for (int q = 0; q < 4; q++) *(uint4 *)(alds + swz(t / 2, (t % 2) * 4 + q)) = ra[q];
 }
 
-// One 64-depth step of a wave's 64 x 64 sub-tile from LDS.
-template <bool BF16, int BM>
-__device__ __forceinline__ void compute_step(const uint16_t *Al, int wm, int wn, int lr, int lk,
-                                             float4_t (&acc)[4][4]) {
-    const uint16_t *Bl = Al + BM * LDS_STRIDE;
+// One 32-depth half of a step's fragments (A: 4 row blocks, B: 4 column
+// blocks of the wave's 64 x 64 sub-tile), and its 16 products.
+template <int BM>
+__device__ __forceinline__ void read_half(const uint16_t *stage, int kk, int wm, int wn, int lane,
+                                          uint4 (&fa)[4], uint4 (&fb)[4]) {
+    const uint16_t *Bl = stage + BM * LDS_STRIDE;
+    const int lr = lane % 16, ch = kk / 8 + lane / 16;
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 32) {
-        uint4 af[4], bf[4];
+    for (int i = 0; i < 4; i++) fa[i] = *(const uint4 *)(stage + swz(wm * 64 + i * 16 + lr, ch));
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            af[i] = *(const uint4 *)(Al + (wm * 64 + i * 16 + lr) * LDS_STRIDE + kk + lk);
+    for (int jt = 0; jt < 4; jt++) fb[jt] = *(const uint4 *)(Bl + swz(wn * 64 + jt * 16 + lr, ch));
+}
+
+template <bool BF16>
+__device__ __forceinline__ void mma_half(const uint4 (&fa)[4], const uint4 (&fb)[4], float4_t (&acc)[4][4]) {
 #pragma unroll
-        for (int jt = 0; jt < 4; jt++)
-            bf[jt] = *(const uint4 *)(Bl + (wn * 64 + jt * 16 + lr) * LDS_STRIDE + kk + lk);
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int jt = 0; jt < 4; jt++) acc[i][jt] = mfma<BF16>(af[i], bf[jt], acc[i][jt]);
-    }
+        for (int jt = 0; jt < 4; jt++) acc[i][jt] = mfma<BF16>(fa[i], fb[jt], acc[i][jt]);
 }
 
 template <int BM>
@@ -310,13 +315,14 @@ struct Tile {
     static constexpr int THREADS = BM * 2;          // BM/64 x 2 waves
     static constexpr int UD = 64 * 128 / THREADS;   // B depths per thread
     static constexpr int STAGE = (BM + BN) * LDS_STRIDE;  // halfs per LDS stage
+    static constexpr int NSTAGE = 3;                // LDS ring
 };
 
-template <int WK, bool BF16, bool AFFINE, int BM, bool VECA>
+template <int WK, bool BF16, bool AFFINE, int BM, bool VECA, bool PD>
 __global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
     constexpr int UD = Tile<BM>::UD;
     constexpr int STAGE = Tile<BM>::STAGE;
-    extern __shared__ __align__(16) uint16_t lds[];  // [2][A: BM rows | B: 128 rows] x LDS_STRIDE
+    extern __shared__ __align__(16) uint16_t lds[];  // [3][A: BM rows | B: 128 rows] x 64, swizzled
 
     // column-tile-major order: consecutive workgroups share a weight tile
     const uint32_t mtiles = (g.m + BM - 1) / BM;
@@ -327,7 +333,7 @@ __global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
     const int t = threadIdx.x;
     const int lane = t % 64, wave = t / 64;
     const int wm = wave / 2, wn = wave % 2;
-    const int lr = lane % 16, lk = (lane / 16) * 8;
+    const int lr = lane % 16;
 
     float4_t acc[4][4];
 #pragma unroll
@@ -338,34 +344,59 @@ __global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
     uint4 ra0[4], ra1[4];
     BRegs<UD> rb0, rb1;
 
-    // Every load is unconditional (steps past K read zeros, see b_load and
-    // a_load), so the compiler can count outstanding loads exactly and each
-    // wait retires only the step about to be stored. The step count is
-    // rounded up to even; an odd K-step count multiplies one zero step.
+    // Pipeline, per 64-depth step k: the global loads of step k+3 are issued,
+    // step k+2 is dequantized into LDS stage (k+2)%3, and the fragments of
+    // step k+1 are read from stage (k+1)%3 -- published by the barrier that
+    // ended step k-1 -- while step k multiplies. Every load is unconditional
+    // (steps past K read zeros, see b_load and a_load), so the compiler counts
+    // outstanding loads exactly. The step count is rounded up to even (two
+    // register stages); an odd count multiplies one zero step.
     const uint32_t ksteps = (g.k + 2 * BK - 1) / (2 * BK) * 2;  // >= 2
     a_load<VECA>(g, row0, 0, ra0);
     b_load<WK, UD>(g, col0, 0, rb0);
     a_load<VECA>(g, row0, BK, ra1);
     b_load<WK, UD>(g, col0, BK, rb1);
     a_store(ra0, lds);
-    b_store<WK, BF16, AFFINE, UD>(g, col0, 0, rb0, lds + BM * LDS_STRIDE);
+    b_store<WK, BF16, AFFINE, UD, PD>(g, col0, 0, rb0, lds + BM * LDS_STRIDE);
+    a_load<VECA>(g, row0, 2 * BK, ra0);
+    b_load<WK, UD>(g, col0, 2 * BK, rb0);
+    a_store(ra1, lds + STAGE);
+    b_store<WK, BF16, AFFINE, UD, PD>(g, col0, BK, rb1, lds + STAGE + BM * LDS_STRIDE);
     __syncthreads();
 
+    uint4 fa0[4], fb0[4], fa1[4], fb1[4];  // kk = 0 / kk = 32 halves
+    read_half<BM>(lds, 0, wm, wn, lane, fa0, fb0);
+    uint32_t s_cur = 0;  // stage of step ks
     for (uint32_t ks = 0; ks < ksteps; ks += 2) {
-        // even step ks: LDS buffer 0; step ks+2 loads into register stage 0
-        a_load<VECA>(g, row0, (ks + 2) * BK, ra0);
-        b_load<WK, UD>(g, col0, (ks + 2) * BK, rb0);
-        compute_step<BF16, BM>(lds, wm, wn, lr, lk, acc);
-        a_store(ra1, lds + STAGE);
-        b_store<WK, BF16, AFFINE, UD>(g, col0, (ks + 1) * BK, rb1, lds + STAGE + BM * LDS_STRIDE);
-        __syncthreads();
-        // odd step ks+1: LDS buffer 1; step ks+3 loads into register stage 1
-        a_load<VECA>(g, row0, (ks + 3) * BK, ra1);
-        b_load<WK, UD>(g, col0, (ks + 3) * BK, rb1);
-        compute_step<BF16, BM>(lds + STAGE, wm, wn, lr, lk, acc);
-        a_store(ra0, lds);
-        b_store<WK, BF16, AFFINE, UD>(g, col0, (ks + 2) * BK, rb0, lds + BM * LDS_STRIDE);
-        __syncthreads();
+        // even step ks: its second half, the next step's first half, step
+        // ks+3's loads into register stage 1, step ks+2 (stage 0) into LDS
+        {
+            const uint32_t s1 = s_cur == 2 ? 0 : s_cur + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+            read_half<BM>(lds + s_cur * STAGE, 32, wm, wn, lane, fa1, fb1);
+            mma_half<BF16>(fa0, fb0, acc);
+            read_half<BM>(lds + s1 * STAGE, 0, wm, wn, lane, fa0, fb0);
+            a_load<VECA>(g, row0, (ks + 3) * BK, ra1);
+            b_load<WK, UD>(g, col0, (ks + 3) * BK, rb1);
+            a_store(ra0, lds + s2 * STAGE);
+            b_store<WK, BF16, AFFINE, UD, PD>(g, col0, (ks + 2) * BK, rb0, lds + s2 * STAGE + BM * LDS_STRIDE);
+            mma_half<BF16>(fa1, fb1, acc);
+            __syncthreads();
+            s_cur = s1;
+        }
+        // odd step ks+1: the same with the register stages swapped
+        {
+            const uint32_t s1 = s_cur == 2 ? 0 : s_cur + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+            read_half<BM>(lds + s_cur * STAGE, 32, wm, wn, lane, fa1, fb1);
+            mma_half<BF16>(fa0, fb0, acc);
+            read_half<BM>(lds + s1 * STAGE, 0, wm, wn, lane, fa0, fb0);
+            a_load<VECA>(g, row0, (ks + 4) * BK, ra0);
+            b_load<WK, UD>(g, col0, (ks + 4) * BK, rb0);
+            a_store(ra1, lds + s2 * STAGE);
+            b_store<WK, BF16, AFFINE, UD, PD>(g, col0, (ks + 3) * BK, rb1, lds + s2 * STAGE + BM * LDS_STRIDE);
+            mma_half<BF16>(fa1, fb1, acc);
+            __syncthreads();
+            s_cur = s1;
+        }
     }
 
     // Round beta*acc to 16 bits into LDS (the loop's last barrier freed it),
@@ -374,7 +405,7 @@ __global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
     // (src/exec/macros.rs:188-206). A lane holds D[4*(lane/16)+v][lane%16] of
     // each 16x16 MFMA tile.
     constexpr int CS = BN + 8;  // halfs per staged row
-    static_assert(BM * CS <= 2 * STAGE, "staged tile exceeds the LDS buffers");
+    static_assert(BM * CS <= 3 * STAGE, "staged tile exceeds the LDS buffers");
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -389,7 +420,7 @@ __global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
     // the cell loop below touches global memory only for TENSOR operands.
     float *colv = (float *)(lds + BM * CS);   // [node][BN]
     float *rowv = colv + SMG_MAX_EP_NODES * BN;  // [node][BM]
-    static_assert(BM * CS * 2 + SMG_MAX_EP_NODES * (BN + BM) * 4 <= 2 * STAGE * 2,
+    static_assert(BM * CS * 2 + SMG_MAX_EP_NODES * (BN + BM) * 4 <= 3 * STAGE * 2,
                   "epilogue operands exceed the LDS buffers");
     for (uint32_t q = 0; q < ep.n_nodes; q++) {
         const uint32_t cls = ep.cls[q];
@@ -418,7 +449,7 @@ __global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
                     F8 y;
 #pragma unroll
                     for (int e = 0; e < 8; e++) y.v[e] = x[e];
-                    y = act8(nd.aux, y, nd.scalar);
+                    y = act8_fast(nd.aux, y, nd.scalar);
 #pragma unroll
                     for (int e = 0; e < 8; e++) x[e] = y.v[e];
                     continue;
@@ -463,27 +494,40 @@ __global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
     }
 }
 
-template <int WK, bool BF16, bool AFFINE, int BM, bool VECA>
+template <int WK, bool BF16, bool AFFINE, int BM, bool VECA, bool PD>
 hipError_t launch_t(const GemmArgs &g, const EpArgs &ep, hipStream_t s) {
-    const size_t lds = 2 * (size_t)Tile<BM>::STAGE * 2;
+    const size_t lds = (size_t)Tile<BM>::NSTAGE * Tile<BM>::STAGE * 2;
     static bool attr_set = false;  // benign race: every setter writes the same value
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute((const void *)gemm_kernel<WK, BF16, AFFINE, BM, VECA>,
+        const hipError_t e = hipFuncSetAttribute((const void *)gemm_kernel<WK, BF16, AFFINE, BM, VECA, PD>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
     const uint32_t tiles = ((g.m + BM - 1) / BM) * ((g.n + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_kernel<WK, BF16, AFFINE, BM, VECA>), dim3(tiles), dim3(BM * 2), lds, s,
+    hipLaunchKernelGGL((gemm_kernel<WK, BF16, AFFINE, BM, VECA, PD>), dim3(tiles), dim3(BM * 2), lds, s,
                        g, ep);
     return hipGetLastError();
 }
 
 template <int WK, bool BF16, bool AFFINE>
 hipError_t launch_shape(const GemmArgs &g, const EpArgs &ep, bool vec_a, hipStream_t s) {
-    if (!vec_a) return launch_t<WK, BF16, AFFINE, 128, false>(g, ep, s);
-    if (g.m > 128) return launch_t<WK, BF16, AFFINE, 256, true>(g, ep, s);
-    return launch_t<WK, BF16, AFFINE, 128, true>(g, ep, s);
+    const uint32_t block = 1u << g.block_shift;
+    if constexpr (WK == W_Q4 || WK == W_Q2 || WK == W_Q1) {
+        if (!vec_a)
+            return block < 32 ? launch_t<WK, BF16, AFFINE, 128, false, true>(g, ep, s)
+                              : launch_t<WK, BF16, AFFINE, 128, false, false>(g, ep, s);
+        if (g.m > 128)
+            return block < 16 ? launch_t<WK, BF16, AFFINE, 256, true, true>(g, ep, s)
+                              : launch_t<WK, BF16, AFFINE, 256, true, false>(g, ep, s);
+        return block < 32 ? launch_t<WK, BF16, AFFINE, 128, true, true>(g, ep, s)
+                          : launch_t<WK, BF16, AFFINE, 128, true, false>(g, ep, s);
+    } else {
+        (void)block;
+        if (!vec_a) return launch_t<WK, BF16, AFFINE, 128, false, false>(g, ep, s);
+        if (g.m > 128) return launch_t<WK, BF16, AFFINE, 256, true, false>(g, ep, s);
+        return launch_t<WK, BF16, AFFINE, 128, true, false>(g, ep, s);
+    }
 }
 
 }  // namespace

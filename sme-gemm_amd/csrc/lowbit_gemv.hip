@@ -731,8 +731,11 @@ TileGeo tile_geometry(const WDev &w, size_t m) {
     TileGeo none = {false, 0, 0, 0, 0};
     if (m < 1 || m > 8 || w.block > QPASS || w.block < 16) return none;
     const size_t tiles16 = w.n_pad / 16;
-    uint32_t want = 0;  // smallest CG with at most ~1.5 workgroups per CU (256 CUs)
-    while (want < 2 && (tiles16 >> want) > 384) want++;
+    // one row: up to ~3 workgroups per CU (their quantization of A is one
+    // row's worth); more rows: about one per CU (measured on MI355X)
+    const size_t most = m == 1 ? 768 : 256;
+    uint32_t want = 0;
+    while (want < 2 && (tiles16 >> want) > most) want++;
     for (int cs = (int)want; cs >= 0; cs--) {
         const TileGeo g = tile_geometry_cg(w, m, (uint32_t)cs);
         if (g.ok) return g;

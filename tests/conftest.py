@@ -64,3 +64,12 @@ def bf16_tol(k):
 
 def rng_f16(rng, size, scale=1.0):
     return (rng.standard_normal(size) * scale).astype(np.float16).view(np.uint16)
+
+
+def ulp_dist(a, b):
+    """Largest distance in 16-bit ulps between two arrays of f16/bf16 bit
+    patterns (sign-magnitude mapped to a monotonic integer line)."""
+    def line(x):
+        x = np.asarray(x, np.uint16).astype(np.int32)
+        return np.where(x & 0x8000, -(x & 0x7FFF), x)
+    return int(np.max(np.abs(line(a) - line(b)))) if np.size(a) else 0
