@@ -310,12 +310,117 @@ __device__ __forceinline__ void mma_half(const uint4 (&fa)[4], const uint4 (&fb)
         for (int jt = 0; jt < 4; jt++) acc[i][jt] = mfma<BF16>(fa[i], fb[jt], acc[i][jt]);
 }
 
+// The tile store shared by the GEMM kernels. acc holds the wave's 64 x 64
+// sub-tile (wave (wm, wn) of the BM x 128 tile); the loop's last barrier has
+// freed the LDS.
+template <bool BF16, int BM>
+__device__ __forceinline__ void store_tile(const GemmArgs &g, const EpArgs &ep, const float4_t (&acc)[4][4],
+                                           uint16_t *lds, uint32_t row0, uint32_t col0, int wm, int wn,
+                                           int lane, int lds_halfs) {
+    const int t = threadIdx.x, lr = lane % 16;
+    (void)lds_halfs;
+    // Round beta*acc to 16 bits into LDS (the loop's last barrier freed it),
+    // then store rows of 8 consecutive columns: 16-byte stores when the
+    // destination is row-major, and the op-graph on the rounded value
+    // (src/exec/macros.rs:188-206). A lane holds D[4*(lane/16)+v][lane%16] of
+    // each 16x16 MFMA tile.
+    constexpr int CS = BN + 8;  // halfs per staged row
+    // (the caller's LDS holds lds_halfs >= BM * CS + the operand vectors)
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int jt = 0; jt < 4; jt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                lds[(wm * 64 + i * 16 + (lane / 16) * 4 + v) * CS + wn * 64 + jt * 16 + lr] =
+                    from_f32<BF16>(0.0f + g.beta * acc[i][jt][v]);
+    __syncthreads();
+    const bool plain = ep.n_nodes == 0;
+    // ROW / COL operand vectors are read once per tile into LDS (as f32), so
+    // the cell loop below touches global memory only for TENSOR operands.
+    float *colv = (float *)(lds + BM * CS);   // [node][BN]
+    float *rowv = colv + SMG_MAX_EP_NODES * BN;  // [node][BM]
+    for (uint32_t q = 0; q < ep.n_nodes; q++) {
+        const uint32_t cls = ep.cls[q];
+        const uint16_t *p = (const uint16_t *)ep.nodes[q].ptr;
+        if (cls == EPC_COL && t < BN)
+            colv[q * BN + t] = col0 + t < g.n ? to_f32<BF16>(p[col0 + t]) : 0.0f;
+        if (cls == EPC_ROW && t < BM)
+            rowv[q * BM + t] = row0 + t < g.m ? to_f32<BF16>(p[row0 + t]) : 0.0f;
+    }
+    __syncthreads();
+    for (int u = t; u < BM * (BN / 8); u += BM * 2) {
+        const int rl = u / (BN / 8), cl = (u % (BN / 8)) * 8;
+        const uint32_t row = row0 + rl, col = col0 + cl;
+        if (row >= g.m || col >= g.n) continue;
+        const uint32_t ne = g.n - col < 8 ? g.n - col : 8;  // cells of this row group
+        uint4 c8 = *(const uint4 *)(lds + rl * CS + cl);
+        if (!plain) {
+            uint32_t w4[4] = {c8.x, c8.y, c8.z, c8.w};
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = to_f32<BF16>((uint16_t)(w4[e / 2] >> (16 * (e % 2))));
+            for (uint32_t q = 0; q < ep.n_nodes; q++) {
+                const EpNode &nd = ep.nodes[q];
+                const uint32_t cls = ep.cls[q], fam = ep.fam[q];
+                if (fam == EPF_ACT) {
+                    F8 y;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) y.v[e] = x[e];
+                    y = act8_fast(nd.aux, y, nd.scalar);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) x[e] = y.v[e];
+                    continue;
+                }
+                float v[8];
+                if (cls == EPC_TENSOR) {
+                    // the 8 loads are issued together, then consumed
+                    const uint16_t *p = (const uint16_t *)nd.ptr + (size_t)row * (nd.ld == 0 ? g.n : nd.ld) + col;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = (uint32_t)e < ne ? to_f32<BF16>(p[e]) : 0.0f;
+                } else if (cls == EPC_COL) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = colv[q * BN + cl + e];
+                } else {
+                    const float vs = cls == EPC_ROW ? rowv[q * BM + rl] : nd.scalar;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = vs;
+                }
+                switch (fam) {  // uniform: one branch per node, then 8 lanes of arithmetic
+#define SMG_EP_FAM(F)                                                           \
+    case F:                                                                     \
+        _Pragma("unroll") for (int e = 0; e < 8; e++) x[e] = ep_arith(F, x[e], v[e]); \
+        break;
+                    SMG_EP_FAM(EPF_ADD) SMG_EP_FAM(EPF_MUL) SMG_EP_FAM(EPF_SUB)
+                    SMG_EP_FAM(EPF_DIV) SMG_EP_FAM(EPF_MAX) SMG_EP_FAM(EPF_MIN)
+#undef SMG_EP_FAM
+                default: break;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                w4[e] = (uint32_t)from_f32<BF16>(x[2 * e]) | ((uint32_t)from_f32<BF16>(x[2 * e + 1]) << 16);
+            c8 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+        uint16_t *dp = g.dst + (size_t)row * g.dst_rs + (size_t)col * g.dst_cs;
+        if (g.dst_cs == 1 && ne == 8 && ((uintptr_t)dp & 15) == 0) {
+            *(uint4 *)dp = c8;
+            continue;
+        }
+        const uint32_t w4[4] = {c8.x, c8.y, c8.z, c8.w};
+        for (uint32_t e = 0; e < ne; e++) dp[(size_t)e * g.dst_cs] = (uint16_t)(w4[e / 2] >> (16 * (e % 2)));
+    }
+}
+
+constexpr int EPI_LDS_HALFS(int bm) { return bm * (BN + 8) + SMG_MAX_EP_NODES * (BN + bm) * 2; }
+
 template <int BM>
 struct Tile {
     static constexpr int THREADS = BM * 2;          // BM/64 x 2 waves
     static constexpr int UD = 64 * 128 / THREADS;   // B depths per thread
     static constexpr int STAGE = (BM + BN) * LDS_STRIDE;  // halfs per LDS stage
     static constexpr int NSTAGE = 3;                // LDS ring
+    static_assert(EPI_LDS_HALFS(BM) <= NSTAGE * STAGE, "the tile store exceeds the LDS ring");
 };
 
 template <int WK, bool BF16, bool AFFINE, int BM, bool VECA, bool PD>
@@ -399,99 +504,7 @@ __global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
         }
     }
 
-    // Round beta*acc to 16 bits into LDS (the loop's last barrier freed it),
-    // then store rows of 8 consecutive columns: 16-byte stores when the
-    // destination is row-major, and the op-graph on the rounded value
-    // (src/exec/macros.rs:188-206). A lane holds D[4*(lane/16)+v][lane%16] of
-    // each 16x16 MFMA tile.
-    constexpr int CS = BN + 8;  // halfs per staged row
-    static_assert(BM * CS <= 3 * STAGE, "staged tile exceeds the LDS buffers");
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int jt = 0; jt < 4; jt++)
-#pragma unroll
-            for (int v = 0; v < 4; v++)
-                lds[(wm * 64 + i * 16 + (lane / 16) * 4 + v) * CS + wn * 64 + jt * 16 + lr] =
-                    from_f32<BF16>(0.0f + g.beta * acc[i][jt][v]);
-    __syncthreads();
-    const bool plain = ep.n_nodes == 0;
-    // ROW / COL operand vectors are read once per tile into LDS (as f32), so
-    // the cell loop below touches global memory only for TENSOR operands.
-    float *colv = (float *)(lds + BM * CS);   // [node][BN]
-    float *rowv = colv + SMG_MAX_EP_NODES * BN;  // [node][BM]
-    static_assert(BM * CS * 2 + SMG_MAX_EP_NODES * (BN + BM) * 4 <= 3 * STAGE * 2,
-                  "epilogue operands exceed the LDS buffers");
-    for (uint32_t q = 0; q < ep.n_nodes; q++) {
-        const uint32_t cls = ep.cls[q];
-        const uint16_t *p = (const uint16_t *)ep.nodes[q].ptr;
-        if (cls == EPC_COL && t < BN)
-            colv[q * BN + t] = col0 + t < g.n ? to_f32<BF16>(p[col0 + t]) : 0.0f;
-        if (cls == EPC_ROW && t < BM)
-            rowv[q * BM + t] = row0 + t < g.m ? to_f32<BF16>(p[row0 + t]) : 0.0f;
-    }
-    __syncthreads();
-    for (int u = t; u < BM * (BN / 8); u += BM * 2) {
-        const int rl = u / (BN / 8), cl = (u % (BN / 8)) * 8;
-        const uint32_t row = row0 + rl, col = col0 + cl;
-        if (row >= g.m || col >= g.n) continue;
-        const uint32_t ne = g.n - col < 8 ? g.n - col : 8;  // cells of this row group
-        uint4 c8 = *(const uint4 *)(lds + rl * CS + cl);
-        if (!plain) {
-            uint32_t w4[4] = {c8.x, c8.y, c8.z, c8.w};
-            float x[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) x[e] = to_f32<BF16>((uint16_t)(w4[e / 2] >> (16 * (e % 2))));
-            for (uint32_t q = 0; q < ep.n_nodes; q++) {
-                const EpNode &nd = ep.nodes[q];
-                const uint32_t cls = ep.cls[q], fam = ep.fam[q];
-                if (fam == EPF_ACT) {
-                    F8 y;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) y.v[e] = x[e];
-                    y = act8_fast(nd.aux, y, nd.scalar);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) x[e] = y.v[e];
-                    continue;
-                }
-                float v[8];
-                if (cls == EPC_TENSOR) {
-                    // the 8 loads are issued together, then consumed
-                    const uint16_t *p = (const uint16_t *)nd.ptr + (size_t)row * (nd.ld == 0 ? g.n : nd.ld) + col;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) v[e] = (uint32_t)e < ne ? to_f32<BF16>(p[e]) : 0.0f;
-                } else if (cls == EPC_COL) {
-#pragma unroll
-                    for (int e = 0; e < 8; e++) v[e] = colv[q * BN + cl + e];
-                } else {
-                    const float vs = cls == EPC_ROW ? rowv[q * BM + rl] : nd.scalar;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) v[e] = vs;
-                }
-                switch (fam) {  // uniform: one branch per node, then 8 lanes of arithmetic
-#define SMG_EP_FAM(F)                                                           \
-    case F:                                                                     \
-        _Pragma("unroll") for (int e = 0; e < 8; e++) x[e] = ep_arith(F, x[e], v[e]); \
-        break;
-                    SMG_EP_FAM(EPF_ADD) SMG_EP_FAM(EPF_MUL) SMG_EP_FAM(EPF_SUB)
-                    SMG_EP_FAM(EPF_DIV) SMG_EP_FAM(EPF_MAX) SMG_EP_FAM(EPF_MIN)
-#undef SMG_EP_FAM
-                default: break;
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                w4[e] = (uint32_t)from_f32<BF16>(x[2 * e]) | ((uint32_t)from_f32<BF16>(x[2 * e + 1]) << 16);
-            c8 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-        }
-        uint16_t *dp = g.dst + (size_t)row * g.dst_rs + (size_t)col * g.dst_cs;
-        if (g.dst_cs == 1 && ne == 8 && ((uintptr_t)dp & 15) == 0) {
-            *(uint4 *)dp = c8;
-            continue;
-        }
-        const uint32_t w4[4] = {c8.x, c8.y, c8.z, c8.w};
-        for (uint32_t e = 0; e < ne; e++) dp[(size_t)e * g.dst_cs] = (uint16_t)(w4[e / 2] >> (16 * (e % 2)));
-    }
+    store_tile<BF16, BM>(g, ep, acc, lds, row0, col0, wm, wn, lane, Tile<BM>::NSTAGE * STAGE);
 }
 
 template <int WK, bool BF16, bool AFFINE, int BM, bool VECA, bool PD>
