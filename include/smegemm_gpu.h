@@ -117,6 +117,22 @@ int smg_q1_create(const uint8_t *signs, const uint16_t *scales, int layout, size
 int smg_q1_create_band(const uint8_t *signs, const uint16_t *scales, size_t n, size_t k,
                        size_t block, smg_weights **out);
 
+/* Load-time quantizers (host code): f32 weights w (n outputs x k inputs;
+ * layout 0 = WeightLayout::OutIn, w[j*k + d]; 1 = InOut, w[d*n + j]) to the
+ * row-major input arrays the create functions above take. The caller owns the
+ * outputs: quants ceil(k*n/2) bytes, codes ceil(k*n/4), signs ceil(k*n/8)
+ * (OutIn, as Q1Weights::quantize packs them), scales / mins n*ceil(k/block)
+ * f16. Replace Q4Weights::quantize (src/kernels/q4/quantize.rs:29-81; affine
+ * 1 = Q4Form::Affine, else mins may be NULL), Q2Weights::quantize
+ * (src/kernels/lowbit/q2.rs:110-143; SMG_EINVAL for an all-zero codebook) and
+ * Q1Weights::quantize (src/kernels/lowbit/q1.rs:116-147). */
+int smg_q4_quantize(const float *w, int layout, size_t n, size_t k, size_t block, int affine,
+                    uint8_t *quants, uint16_t *scales, uint16_t *mins);
+int smg_q2_quantize(const float *w, int layout, size_t n, size_t k, size_t block,
+                    const int8_t *codebook, uint8_t *codes, uint16_t *scales);
+int smg_q1_quantize(const float *w, int layout, size_t n, size_t k, size_t block, uint8_t *signs,
+                    uint16_t *scales);
+
 /* Dense Packed<f16> / Packed<bf16>: replaces prepack_f16 / prepack_bf16
  * (src/kernels/f16.rs:212; bf16.rs:240) and gemm_sme_f16f16_packb
  * (csrc/sme_gemm_api.h:94). B[l][j] = rhs[l*rhs_rs + j*rhs_cs] (k x n). */
@@ -129,6 +145,15 @@ int smg_bf16_prepack(const uint16_t *rhs, size_t n, size_t k, long rhs_rs, long 
  * dequant_q4 / dequant_q4_with (f16: one RNE rounding of scale*code+min) and
  * dequant_q4_bf16 / _with (bf16 through f32), src/kernels/q4/mod.rs:145-257. */
 int smg_q4_dequant(const smg_weights *q4, int to_bf16, smg_weights **out);
+
+/* Column repacks on the device (exact: codes, scales and mins move unchanged).
+ * smg_q4_permute_columns: output column j is column perm[j] of q4 (perm holds
+ * n entries < n); replaces Q4Weights::permute_columns
+ * (src/kernels/q4/weights.rs:125-163). smg_q1_interleave: gate and up (same n,
+ * k, block) to 2n columns, each 32-column chunk of gate followed by the same
+ * chunk of up; replaces Q1Weights::interleave (src/kernels/lowbit/q1.rs:146-185). */
+int smg_q4_permute_columns(const smg_weights *q4, const size_t *perm, smg_weights **out);
+int smg_q1_interleave(const smg_weights *gate, const smg_weights *up, smg_weights **out);
 
 /* A second device copy of a handle's weights (device-to-device; no host
  * repack). Used to rotate benchmark weights past the 256 MB MALL. */

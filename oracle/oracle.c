@@ -616,3 +616,105 @@ void or_f32_to_bf16_array(const float *x, uint16_t *y, size_t len) {
 void or_act_f32_array(uint32_t kind, const float *x, float *y, size_t len, float alpha) {
     for (size_t i = 0; i < len; i++) y[i] = or_act_f32(kind, x[i], alpha);
 }
+
+/* ------------------------------------------------------------------------- */
+/* Load-time quantizers, restated from the reference's f32 code: outputs are the
+ * public input formats (row-major codes, idx = d*n + j; Q1 signs OutIn,
+ * idx = j*k + d), scales [j][blk]. layout 0 = OutIn w[j*k+d], 1 = InOut. */
+static inline float q_at(const float *w, int layout, size_t n, size_t k, size_t j, size_t d) {
+    return layout == 0 ? w[j * k + d] : w[d * n + j];
+}
+
+/* Q4Weights::quantize (src/kernels/q4/quantize.rs:29-81). */
+void or_q4_quantize(const float *w, int layout, size_t n, size_t k, size_t block, int affine,
+                    uint8_t *quants, uint16_t *scales, uint16_t *mins) {
+    size_t nbk = (k + block - 1) / block;
+    memset(quants, 0, (k * n + 1) / 2);
+    for (size_t j = 0; j < n; j++)
+        for (size_t b = 0; b < nbk; b++) {
+            size_t d0 = b * block, d1 = (b + 1) * block < k ? (b + 1) * block : k;
+            uint16_t sc, mn = 0;
+            if (affine) {
+                float lo = INFINITY, hi = -INFINITY;
+                for (size_t d = d0; d < d1; d++) {
+                    float x = q_at(w, layout, n, k, j, d);
+                    lo = fminf(lo, x); /* Rust f32::min / max ignore a NaN operand */
+                    hi = fmaxf(hi, x);
+                }
+                sc = or_f32_to_f16((hi - lo) / 15.0f);
+                mn = or_f32_to_f16(lo + 8.0f * or_f16_to_f32(sc));
+            } else {
+                float m = 0.0f;
+                for (size_t d = d0; d < d1; d++) {
+                    float x = q_at(w, layout, n, k, j, d);
+                    if (fabsf(x) > fabsf(m)) m = x;
+                }
+                sc = or_f32_to_f16(m / -8.0f);
+            }
+            scales[j * nbk + b] = sc;
+            if (affine) mins[j * nbk + b] = mn;
+            float s = or_f16_to_f32(sc), mm = or_f16_to_f32(mn);
+            float inv = s == 0.0f ? 0.0f : 1.0f / s;
+            for (size_t d = d0; d < d1; d++) {
+                float r = roundf((q_at(w, layout, n, k, j, d) - mm) * inv);
+                int code = isnan(r) ? 0 : (r < -8.0f ? -8 : (r > 7.0f ? 7 : (int)r)); /* clamp, `as i8` */
+                size_t idx = d * n + j;
+                quants[idx / 2] |= (uint8_t)((code & 0x0f) << (4 * (idx % 2)));
+            }
+        }
+}
+
+/* Q2Weights::quantize (src/kernels/lowbit/q2.rs:110-143); returns 0, or -1 for
+ * an all-zero codebook (the reference's assert). */
+int or_q2_quantize(const float *w, int layout, size_t n, size_t k, size_t block,
+                   const int8_t *codebook, uint8_t *codes, uint16_t *scales) {
+    float cb[4], cmax = 0.0f;
+    for (int i = 0; i < 4; i++) {
+        cb[i] = (float)codebook[i];
+        cmax = fmaxf(cmax, fabsf(cb[i]));
+    }
+    if (!(cmax > 0.0f)) return -1;
+    size_t nbk = (k + block - 1) / block;
+    memset(codes, 0, (k * n + 3) / 4);
+    for (size_t j = 0; j < n; j++)
+        for (size_t b = 0; b < nbk; b++) {
+            size_t d0 = b * block, d1 = (b + 1) * block < k ? (b + 1) * block : k;
+            float amax = 0.0f;
+            for (size_t d = d0; d < d1; d++) amax = fmaxf(amax, fabsf(q_at(w, layout, n, k, j, d)));
+            scales[j * nbk + b] = or_f32_to_f16(amax / cmax);
+            float s = or_f16_to_f32(scales[j * nbk + b]);
+            for (size_t d = d0; d < d1; d++) {
+                float x = q_at(w, layout, n, k, j, d);
+                /* min_by over total_cmp: the first minimum wins; the distances
+                 * are >= 0 or (positive) NaN, ordered by their bits */
+                int best = 0;
+                uint32_t bk = f32_bits(fabsf(x - s * cb[0]));
+                for (int a = 1; a < 4; a++) {
+                    uint32_t key = f32_bits(fabsf(x - s * cb[a]));
+                    if (key < bk) { bk = key; best = a; }
+                }
+                size_t idx = d * n + j;
+                codes[idx / 4] |= (uint8_t)(best << (2 * (idx % 4)));
+            }
+        }
+    return 0;
+}
+
+/* Q1Weights::quantize (src/kernels/lowbit/q1.rs:116-147). */
+void or_q1_quantize(const float *w, int layout, size_t n, size_t k, size_t block, uint8_t *signs,
+                    uint16_t *scales) {
+    size_t nbk = (k + block - 1) / block;
+    memset(signs, 0, (k * n + 7) / 8);
+    for (size_t j = 0; j < n; j++)
+        for (size_t b = 0; b < nbk; b++) {
+            size_t d0 = b * block, d1 = (b + 1) * block < k ? (b + 1) * block : k;
+            float sum = 0.0f;
+            for (size_t d = d0; d < d1; d++) sum += fabsf(q_at(w, layout, n, k, j, d));
+            scales[j * nbk + b] = or_f32_to_f16(sum / (float)(d1 - d0));
+            for (size_t d = d0; d < d1; d++)
+                if (q_at(w, layout, n, k, j, d) >= 0.0f) {
+                    size_t idx = j * k + d;
+                    signs[idx / 8] |= (uint8_t)(1u << (idx % 8));
+                }
+        }
+}

@@ -54,6 +54,12 @@ def lib() -> C.CDLL:
             getattr(L, name).argtypes = [P, P, SZ]
             getattr(L, name).restype = None
         L.or_act_f32_array.argtypes = [C.c_uint32, P, P, SZ, C.c_float]
+        L.or_q4_quantize.argtypes = [P, C.c_int, SZ, SZ, SZ, C.c_int, P, P, P]
+        L.or_q4_quantize.restype = None
+        L.or_q2_quantize.argtypes = [P, C.c_int, SZ, SZ, SZ, P, P, P]
+        L.or_q2_quantize.restype = C.c_int
+        L.or_q1_quantize.argtypes = [P, C.c_int, SZ, SZ, SZ, P, P]
+        L.or_q1_quantize.restype = None
         L.or_q4_dequant_f16.argtypes = [P, P, P, SZ, SZ, SZ, P]
         L.or_q4_dequant_bf16.argtypes = [P, P, P, SZ, SZ, SZ, P]
         L.or_gemm_f16.argtypes = [SZ, SZ, SZ, P, P, P, C.c_uint16, C.c_int, P]
@@ -120,6 +126,42 @@ def act_f32(kind: int, x, alpha: float = 0.0) -> np.ndarray:
     y = np.empty_like(x)
     lib().or_act_f32_array(kind, _p(x), _p(y), x.size, alpha)
     return y
+
+
+# ---- load-time quantizers ----------------------------------------------------
+
+def q4_quantize(w, layout, n, k, block, affine=False):
+    """Q4Weights::quantize (src/kernels/q4/quantize.rs:29-81): (quants, scales, mins)."""
+    w = _c(w, np.float32)
+    nbk = -(-k // block)
+    quants = np.zeros(-(-(k * n) // 2), np.uint8)
+    scales = np.zeros(n * nbk, np.uint16)
+    mins = np.zeros(n * nbk, np.uint16) if affine else None
+    lib().or_q4_quantize(_p(w), layout, n, k, block, int(affine), _p(quants), _p(scales),
+                         _p(mins) if affine else None)
+    return quants, scales, mins
+
+
+def q2_quantize(w, layout, n, k, block, codebook=(-1, 0, 1, 0)):
+    """Q2Weights::quantize (src/kernels/lowbit/q2.rs:110-143): (codes, scales)."""
+    w = _c(w, np.float32)
+    nbk = -(-k // block)
+    codes = np.zeros(-(-(k * n) // 4), np.uint8)
+    scales = np.zeros(n * nbk, np.uint16)
+    cb = np.asarray(codebook, np.int8)
+    if lib().or_q2_quantize(_p(w), layout, n, k, block, _p(cb), _p(codes), _p(scales)) != 0:
+        raise ValueError("q2 codebook is all zeros")
+    return codes, scales
+
+
+def q1_quantize(w, layout, n, k, block):
+    """Q1Weights::quantize (src/kernels/lowbit/q1.rs:116-147): (signs OutIn, scales)."""
+    w = _c(w, np.float32)
+    nbk = -(-k // block)
+    signs = np.zeros(-(-(k * n) // 8), np.uint8)
+    scales = np.zeros(n * nbk, np.uint16)
+    lib().or_q1_quantize(_p(w), layout, n, k, block, _p(signs), _p(scales))
+    return signs, scales
 
 
 # ---- Q4 --------------------------------------------------------------------

@@ -419,6 +419,51 @@ int check_kind(const smg_weights *w, int kind) {
     return SMG_OK;
 }
 
+// A handle of n_out columns whose column j is column cols[j] of a, or of b when
+// bit 30 of cols[j] is set. Every device array of a weight set is a
+// [rows][n_pad] grid of cells, so whole cells move unchanged.
+int gather_columns(const smg_weights *a, const smg_weights *b, const std::vector<int32_t> &cols,
+                   smg_weights **out) {
+    HIP_TRY(hipSetDevice(a->device), SMG_EHIP);
+    const WDev &s = a->d;
+    smg_weights *w = new_weights(s.kind, cols.size(), s.k, s.block);
+    WDev &d = w->d;
+    d.nchunks = s.nchunks;
+    d.sc_rows = s.sc_rows;
+    d.k_pad = s.k_pad;
+    d.codebook = s.codebook;
+    std::vector<int32_t> map(d.n_pad, -1);
+    std::copy(cols.begin(), cols.end(), map.begin());
+    int32_t *dmap = nullptr;
+    hipError_t e = hipMalloc((void **)&dmap, map.size() * sizeof(int32_t));
+    if (e != hipSuccess) { destroy(w); return fail(SMG_ENOMEM, "column map hipMalloc", e); }
+    e = hipMemcpy(dmap, map.data(), map.size() * sizeof(int32_t), hipMemcpyHostToDevice);
+    struct Field {
+        const void *s0, *s1;
+        const void **dst;
+        size_t rows, cell;
+    };
+    const Field f[3] = {
+        {s.codes, b ? b->d.codes : nullptr, (const void **)&d.codes, s.nchunks, s.kind == W_Q4 ? 16u : 64u},
+        {s.scales, b ? b->d.scales : nullptr, (const void **)&d.scales, s.sc_rows, 2},
+        {s.mins, b ? b->d.mins : nullptr, (const void **)&d.mins, s.sc_rows, 2}};
+    int rc = SMG_OK;
+    for (int i = 0; i < 3 && e == hipSuccess && rc == SMG_OK; i++) {
+        if (!f[i].s0) continue;
+        void *p;
+        if ((rc = alloc_dev(w, f[i].rows * d.n_pad * f[i].cell, &p))) break;
+        *f[i].dst = p;
+        e = launch_gather_columns(p, d.n_pad, f[i].s0, f[i].s1, s.n_pad, dmap, f[i].rows, f[i].cell,
+                                  nullptr);
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    (void)hipFree(dmap);
+    if (rc) { destroy(w); return rc; }
+    if (e != hipSuccess) { destroy(w); return fail(SMG_EHIP, "column gather", e); }
+    *out = w;
+    return SMG_OK;
+}
+
 // Q4 dispatch: GEMV up to Q4_GEMV_MAX_ROWS rows, MFMA GEMM above.
 hipError_t run_q4(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs, const EpArgs &ea,
                   bool bf16, hipStream_t s) {
@@ -449,6 +494,8 @@ float half_bits_to_float(uint16_t h, bool bf16) {
 }
 
 }  // namespace
+
+int smg::report(int code, const char *what) { return fail(code, what); }
 
 // ============================================================================
 extern "C" {
@@ -529,6 +576,40 @@ int smg_q4_dequant(const smg_weights *q4, int to_bf16, smg_weights **out) {
     if (e != hipSuccess) { destroy(w); return fail(SMG_EHIP, "q4 dequant", e); }
     *out = w;
     return SMG_OK;
+}
+
+int smg_q4_permute_columns(const smg_weights *q4, const size_t *perm, smg_weights **out) {
+    int rc = check_kind(q4, W_Q4);
+    if (rc) return rc;
+    const size_t n = q4->d.n;
+    if ((n && !perm) || !out) return fail(SMG_EINVAL, "null array");
+    if (n >= (size_t)1 << 30) return fail(SMG_EINVAL, "too many columns to permute");
+    std::vector<int32_t> cols(n);
+    for (size_t j = 0; j < n; j++) {
+        if (perm[j] >= n) return fail(SMG_EINVAL, "perm entry out of range");
+        cols[j] = (int32_t)perm[j];
+    }
+    return gather_columns(q4, nullptr, cols, out);
+}
+
+int smg_q1_interleave(const smg_weights *gate, const smg_weights *up, smg_weights **out) {
+    int rc = check_kind(gate, W_Q1);
+    if (!rc) rc = check_kind(up, W_Q1);
+    if (rc) return rc;
+    if (!out) return fail(SMG_EINVAL, "null output");
+    const WDev &g = gate->d, &u = up->d;
+    if (g.n != u.n || g.k != u.k || g.block != u.block)
+        return fail(SMG_EINVAL, "gate and up have the same shape and block size");
+    if (gate->device != up->device) return fail(SMG_EINVAL, "gate and up are on different devices");
+    if (g.n >= (size_t)1 << 29) return fail(SMG_EINVAL, "too many columns to interleave");
+    std::vector<int32_t> cols;
+    cols.reserve(2 * g.n);
+    for (size_t c0 = 0; c0 < g.n; c0 += 32) {  // q1.rs:160-182: 32 of gate, then 32 of up
+        const size_t c1 = std::min(c0 + 32, g.n);
+        for (size_t j = c0; j < c1; j++) cols.push_back((int32_t)j);
+        for (size_t j = c0; j < c1; j++) cols.push_back((int32_t)j | (1 << 30));
+    }
+    return gather_columns(gate, up, cols, out);
 }
 
 void smg_weights_destroy(smg_weights *w) { destroy(w); }

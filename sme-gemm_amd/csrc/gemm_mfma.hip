@@ -438,7 +438,6 @@ __global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
     const int t = threadIdx.x;
     const int lane = t % 64, wave = t / 64;
     const int wm = wave / 2, wn = wave % 2;
-    const int lr = lane % 16;
 
     float4_t acc[4][4];
 #pragma unroll

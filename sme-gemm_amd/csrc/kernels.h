@@ -47,4 +47,13 @@ hipError_t launch_gemm(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long
 hipError_t launch_q4_dequant_dense(const WDev &q4, uint16_t *dense, bool to_bf16,
                                    hipStream_t s);
 
+// dst[r][j] = (map[j] bit 30 ? src1 : src0)[r][map[j] & 0x3FFFFFFF], cells of
+// cell_bytes (2, 16 or 64) in [rows][pad] arrays; map[j] < 0 writes zeros.
+hipError_t launch_gather_columns(void *dst, size_t dst_pad, const void *src0, const void *src1,
+                                 size_t src_pad, const int32_t *map, size_t rows, size_t cell_bytes,
+                                 hipStream_t s);
+
+// Sets the calling thread's smg_last_error() text and returns code.
+int report(int code, const char *what);
+
 }  // namespace smg

@@ -68,10 +68,15 @@ def lib() -> C.CDLL:
     L.smg_q2_create_band.argtypes = [P, P, P, SZ, SZ, SZ, W]
     L.smg_q1_create.argtypes = [P, P, C.c_int, SZ, SZ, SZ, W]
     L.smg_q1_create_band.argtypes = [P, P, SZ, SZ, SZ, W]
+    L.smg_q4_quantize.argtypes = [P, C.c_int, SZ, SZ, SZ, C.c_int, P, P, P]
+    L.smg_q2_quantize.argtypes = [P, C.c_int, SZ, SZ, SZ, P, P, P]
+    L.smg_q1_quantize.argtypes = [P, C.c_int, SZ, SZ, SZ, P, P]
     L.smg_f16_prepack.argtypes = [P, SZ, SZ, C.c_long, C.c_long, W]
     L.smg_bf16_prepack.argtypes = [P, SZ, SZ, C.c_long, C.c_long, W]
     L.smg_q4_dequant.argtypes = [P, C.c_int, W]
     L.smg_weights_clone.argtypes = [P, W]
+    L.smg_q4_permute_columns.argtypes = [P, P, W]
+    L.smg_q1_interleave.argtypes = [P, P, W]
     L.smg_weights_destroy.argtypes = [P]
     L.smg_weights_destroy.restype = None
     L.smg_weights_info.argtypes = [P, C.POINTER(SZ), C.POINTER(SZ), C.POINTER(SZ), C.POINTER(SZ)]
@@ -370,6 +375,25 @@ class Q4Params:
         return self._affine
 
 
+def _f32(w, size: int) -> np.ndarray:
+    w = np.ascontiguousarray(np.asarray(w, dtype=np.float32).ravel())
+    if w.size != size:
+        raise ValueError("w holds n * k weights")
+    return w
+
+
+def _quantize_q4(w, layout: int, n: int, k: int, p: "Q4Params"):
+    """Q4Weights::quantize's arrays (src/kernels/q4/quantize.rs:29-81), on the host."""
+    w = _f32(w, n * k)
+    nbk = -(-k // p.block())
+    quants = np.zeros(-(-(k * n) // 2), np.uint8)
+    scales = np.zeros(n * nbk, np.uint16)
+    mins = np.zeros(n * nbk, np.uint16) if p.is_affine() else None
+    _check(lib().smg_q4_quantize(_ptr(w), layout, n, k, p.block(), int(p.is_affine()), _ptr(quants),
+                                 _ptr(scales), None if mins is None else _ptr(mins)), "smg_q4_quantize")
+    return quants, scales, mins
+
+
 def _u8(x) -> np.ndarray:
     return np.ascontiguousarray(x, dtype=np.uint8)
 
@@ -411,8 +435,29 @@ class Q4Weights(_Handle):
         """From the reference's band-major resident arrays (what src/ffi.rs passes)."""
         return cls(nibbles, scales, n, k, p, mins, _band=True)
 
+    @classmethod
+    def quantize(cls, w, layout: int, n: int, k: int, p: Q4Params | None = None):
+        """Q4Weights::quantize (src/kernels/q4/quantize.rs:29): f32 weights in
+        `layout` (WeightLayout.OutIn / InOut) to Q4_0 (p.affine() for Q4_1)."""
+        p = p or Q4Params()
+        quants, scales, mins = _quantize_q4(w, layout, n, k, p)
+        return cls(quants, scales, n, k, p, mins)
+
     def params(self) -> Q4Params:
         return self._params
+
+    def permute_columns(self, perm) -> "Q4Weights":
+        """Q4Weights::permute_columns (src/kernels/q4/weights.rs:128): output
+        column j is column perm[j]; codes, scales and mins move unchanged."""
+        import copy
+        perm = np.ascontiguousarray(perm, dtype=np.uintp)
+        if perm.size != self._n:
+            raise ValueError("perm reorders all n columns")
+        h = C.c_void_p()
+        _check(lib().smg_q4_permute_columns(self._h, _ptr(perm), C.byref(h)), "smg_q4_permute_columns")
+        c = copy.copy(self)
+        c._h = h
+        return c
 
 
 class Q2Params:
@@ -464,6 +509,14 @@ class Q2Weights(_Handle):
     def from_band(cls, codes, scales, n, k, p: Q2Params):
         return cls(codes, scales, n, k, p, _band=True)
 
+    @classmethod
+    def quantize(cls, w, layout: int, n: int, k: int, p: Q2Params | None = None):
+        """Q2Weights::quantize (src/kernels/lowbit/q2.rs:110): each weight to the
+        nearest scaled codebook value, scale = f16(amax / max|codebook|)."""
+        p = p or Q2Params()
+        codes, scales = quantize_q2_arrays(w, layout, n, k, p)
+        return cls(codes, scales, n, k, p)
+
     def params(self) -> Q2Params:
         return self._params
 
@@ -494,8 +547,56 @@ class Q1Weights(_Handle):
     def from_band(cls, signs, scales, n, k, block):
         return cls(signs, scales, 0, n, k, block, _band=True)
 
+    @classmethod
+    def quantize(cls, w, layout: int, n: int, k: int, block: int):
+        """Q1Weights::quantize (src/kernels/lowbit/q1.rs:116): scale = the block's
+        mean magnitude, sign = w >= 0."""
+        signs, scales = quantize_q1_arrays(w, layout, n, k, block)
+        return cls(signs, scales, WeightLayout.OutIn, n, k, block)
+
     def block(self) -> int:
         return self._block
+
+    @classmethod
+    def interleave(cls, gate: "Q1Weights", up: "Q1Weights") -> "Q1Weights":
+        """Q1Weights::interleave (src/kernels/lowbit/q1.rs:149): 2n columns,
+        each 32-column chunk of gate followed by the same chunk of up."""
+        import copy
+        h = C.c_void_p()
+        _check(lib().smg_q1_interleave(gate._h, up._h, C.byref(h)), "smg_q1_interleave")
+        c = copy.copy(gate)
+        c._h = h
+        c._n = 2 * gate.n()
+        return c
+
+
+def quantize_q4_arrays(w, layout: int, n: int, k: int, p: Q4Params | None = None):
+    """(quants, scales, mins) of Q4Weights::quantize, host arrays (no device)."""
+    return _quantize_q4(w, layout, n, k, p or Q4Params())
+
+
+def quantize_q2_arrays(w, layout: int, n: int, k: int, p: Q2Params | None = None):
+    """(codes, scales) of Q2Weights::quantize, host arrays (no device)."""
+    p = p or Q2Params()
+    w = _f32(w, n * k)
+    nbk = -(-k // p.block())
+    codes = np.zeros(-(-(k * n) // 4), np.uint8)
+    scales = np.zeros(n * nbk, np.uint16)
+    cb = np.asarray(p.codebook(), np.int8)
+    _check(lib().smg_q2_quantize(_ptr(w), layout, n, k, p.block(), _ptr(cb), _ptr(codes), _ptr(scales)),
+           "smg_q2_quantize")
+    return codes, scales
+
+
+def quantize_q1_arrays(w, layout: int, n: int, k: int, block: int):
+    """(signs in WeightLayout.OutIn, scales) of Q1Weights::quantize, host arrays."""
+    w = _f32(w, n * k)
+    nbk = -(-k // block)
+    signs = np.zeros(-(-(k * n) // 8), np.uint8)
+    scales = np.zeros(n * nbk, np.uint16)
+    _check(lib().smg_q1_quantize(_ptr(w), layout, n, k, block, _ptr(signs), _ptr(scales)),
+           "smg_q1_quantize")
+    return signs, scales
 
 
 class Packed(_Handle):

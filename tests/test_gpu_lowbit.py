@@ -244,3 +244,68 @@ def test_mopa_matches_eager_dequant(smg, orc, si, bi, block):
             want = orc.matmul_lowbit_mopa_ep(1, a, codes_, scales, m, n, k, block)
         assert max_rel(plain, want) <= f16_tol(k), f"q{kind} mopa plain"
         assert ulp_dist(fused, orc.apply_ep(plain, m, n, nodes, act)) <= 1, f"q{kind} mopa ep"
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("m,n,k,block", [(1, 96, 512, 64), (5, 70, 300, 64), (40, 33, 1000, 128)])
+def test_quantize_then_matmul(smg, orc, layout, m, n, k, block):
+    """Q2Weights::quantize / Q1Weights::quantize from f32 weights in either
+    layout, uploaded and multiplied on the device: bit-exact with the reference
+    path over the oracle's quantized arrays."""
+    rng = np.random.default_rng(m * 7 + n + k + layout)
+    w = rng.standard_normal(n * k).astype(np.float32)
+    x = w if layout == 0 else np.ascontiguousarray(w.reshape(n, k).T).ravel()
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    book = (-2, -1, 1, 2)
+    q2 = smg.Q2Weights.quantize(x, layout, n, k, smg.Q2Params(block).with_codebook(book))
+    codes, scales = orc.q2_quantize(x, layout, n, k, block, book)
+    got = np.zeros(m * n, np.uint16)
+    smg.matmul_q2(a, q2, got, m)
+    assert np.array_equal(got, orc.lowbit_reference(2, a, codes, scales, m, n, k, block, book))
+    q1 = smg.Q1Weights.quantize(x, layout, n, k, block)
+    signs, scales = orc.q1_quantize(x, layout, n, k, block)
+    got = np.zeros(m * n, np.uint16)
+    smg.matmul_q1(a, q1, got, m)
+    assert np.array_equal(got, orc.lowbit_reference(1, a, signs, scales, m, n, k, block))
+
+
+@pytest.mark.parametrize("n,k,block", [(70, 300, 64), (64, 512, 128), (33, 1000, 32), (5, 64, 16)])
+def test_q1_interleave(smg, orc, n, k, block):
+    """Q1Weights::interleave (q1.rs:149-185, test :279-320): 2n columns, each
+    32-column chunk of gate then the same chunk of up; every column is exactly
+    the source column, so outputs match the oracle over the interleaved arrays
+    and the separate gate / up products, bitwise."""
+    rng = np.random.default_rng(n + k)
+    wg = rng.standard_normal(n * k).astype(np.float32)
+    wu = -wg * np.float32(0.5) + rng.standard_normal(n * k).astype(np.float32) * np.float32(0.1)
+    gate = smg.Q1Weights.quantize(wg, 0, n, k, block)
+    up = smg.Q1Weights.quantize(wu, 0, n, k, block)
+    both = smg.Q1Weights.interleave(gate, up)
+    assert both.n() == 2 * n and both.k() == k
+    order = [(src, j) for c0 in range(0, n, 32) for src in (0, 1)
+             for j in range(c0, min(c0 + 32, n))]
+    arrays = [orc.q1_quantize(wg, 0, n, k, block), orc.q1_quantize(wu, 0, n, k, block)]
+    bits = [np.unpackbits(s, bitorder="little")[: n * k].reshape(n, k) for s, _ in arrays]
+    nbk = -(-k // block)
+    isig = np.packbits(np.stack([bits[s][j] for s, j in order]).ravel(), bitorder="little")
+    isc = np.concatenate([arrays[s][1][j * nbk:(j + 1) * nbk] for s, j in order])
+    for m in (1, 3, 9):
+        a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+        got = np.zeros(m * 2 * n, np.uint16)
+        smg.matmul_q1(a, both, got, m)
+        assert np.array_equal(got, orc.lowbit_reference(1, a, isig, isc, m, 2 * n, k, block)), m
+        g = np.zeros(m * n, np.uint16)
+        u = np.zeros(m * n, np.uint16)
+        smg.matmul_q1(a, gate, g, m)
+        smg.matmul_q1(a, up, u, m)
+        parts = [g.reshape(m, n), u.reshape(m, n)]
+        want = np.stack([parts[s][:, j] for s, j in order], 1).ravel()
+        assert np.array_equal(got, want), m
+
+
+def test_q1_interleave_rejects_mismatch(smg):
+    w = np.ones(64 * 32, np.float32)
+    a = smg.Q1Weights.quantize(w, 0, 32, 64, 32)
+    b = smg.Q1Weights.quantize(w, 0, 32, 64, 64)
+    with pytest.raises(smg.SmeGemmError, match="same shape"):
+        smg.Q1Weights.interleave(a, b)

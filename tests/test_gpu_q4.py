@@ -247,3 +247,59 @@ def test_q4_device_pointer_path_matches_host(smg, orc):
     smg.matmul_q4_ep(ad, w, cd, m, smg.Epilogue().add_col(bd).silu())
     torch.cuda.synchronize()
     assert np.array_equal(cd.cpu().numpy().view(np.uint16), host)
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("affine", [False, True])
+@pytest.mark.parametrize("m,n,k,block", [(1, 96, 512, 32), (3, 70, 300, 64), (40, 33, 1000, 32)])
+def test_quantize_then_matmul(smg, orc, layout, affine, m, n, k, block):
+    """Q4Weights::quantize from f32 weights in either layout, uploaded and
+    multiplied on the device, against the oracle over its own quantized arrays."""
+    rng = np.random.default_rng(m * 7 + n + k + layout + 2 * affine)
+    w = rng.standard_normal(n * k).astype(np.float32)
+    x = w if layout == 0 else np.ascontiguousarray(w.reshape(n, k).T).ravel()
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    p = smg.Q4Params(block).affine() if affine else smg.Q4Params(block)
+    q = smg.Q4Weights.quantize(x, layout, n, k, p)
+    quants, scales, mins = orc.q4_quantize(x, layout, n, k, block, affine)
+    c = np.zeros(m * n, np.uint16)
+    smg.matmul_q4(a, q, c, m)
+    want = orc.matmul_q4_ep(a, quants, scales, mins, m, n, k, block)
+    assert max_rel(c, want) <= f16_tol(k)
+
+
+@pytest.mark.parametrize("affine", [False, True])
+@pytest.mark.parametrize("m", [1, 5, 40])
+def test_q4_permute_columns(smg, orc, m, affine):
+    """Q4Weights::permute_columns (weights.rs:125-163): output column j is
+    column perm[j]; the permuted handle gives the permuted output of the
+    original, bitwise, and matches the oracle over permuted arrays."""
+    n, k, block = 300, 200, 32
+    rng = np.random.default_rng(m + 2 * affine)
+    w = rng.standard_normal(n * k).astype(np.float32)
+    p = smg.Q4Params(block).affine() if affine else smg.Q4Params(block)
+    q = smg.Q4Weights.quantize(w, 0, n, k, p)
+    perm = rng.permutation(n)
+    qp = q.permute_columns(perm)
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    c = np.zeros(m * n, np.uint16)
+    cp = np.zeros(m * n, np.uint16)
+    smg.matmul_q4(a, q, c, m)
+    smg.matmul_q4(a, qp, cp, m)
+    assert np.array_equal(cp.reshape(m, n), c.reshape(m, n)[:, perm])
+    quants, scales, mins = orc.q4_quantize(w, 0, n, k, block, affine)
+    nib = np.stack([quants & 15, quants >> 4], 1).ravel()[: n * k].reshape(k, n)[:, perm].ravel()
+    pq = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8)
+    nbk = -(-k // block)
+    ps = scales.reshape(n, nbk)[perm].ravel()
+    pm = mins.reshape(n, nbk)[perm].ravel() if affine else None
+    want = orc.matmul_q4_ep(a, pq, ps, pm, m, n, k, block)
+    assert max_rel(cp, want) <= f16_tol(k)
+
+
+def test_q4_permute_columns_rejects_bad_perm(smg):
+    q = smg.Q4Weights.quantize(np.ones(64 * 8, np.float32), 0, 8, 64)
+    with pytest.raises(smg.SmeGemmError, match="out of range"):
+        q.permute_columns([0, 1, 2, 3, 4, 5, 6, 8])
+    with pytest.raises(ValueError):
+        q.permute_columns([0, 1])
