@@ -234,7 +234,8 @@ __device__ __noinline__ F8 act8(uint32_t kind, F8 x, float alpha) {
     return x;
 }
 
-// The same activations evaluated in f32 (device libm), for the f16/bf16 GEMM
+// The same activations evaluated in f32 (device libm; the logistic kinds with
+// the hardware 2^x and reciprocal), for the f16/bf16 GEMM
 // stores, whose results are held to a tolerance rather than to the bits: the
 // value then rounds to 16 bits, so it differs from the f64 formula's only when
 // the two straddle a 16-bit rounding boundary (at most one 16-bit ulp).
@@ -244,13 +245,21 @@ __device__ __forceinline__ float clampf_(float x, float lo, float hi) {
     if (x > hi) x = hi;
     return x;
 }
+// x * 1/(1 + e^-y) with the hardware 2^x and reciprocal (about 1 ulp each in
+// f32): the logistic factor of silu, sigmoid and tanh-gelu. An infinite e^-y
+// gives a zero factor, as the exact quotient does.
+__device__ __forceinline__ float mul_logistic(float x, float y) {
+    const float e = __builtin_amdgcn_exp2f(-y * 1.4426950408889634f);
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
 __device__ __forceinline__ float act_f32_fast(uint32_t kind, float x, float a) {
     switch (kind) {
     case 1: return maxnumf(x, 0.0f);
-    case 2: return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x)));
-    case 3: return x / (1.0f + expf(-x));
+    // 0.5 x (1 + tanh(u)) = x / (1 + e^-2u)
+    case 2: return mul_logistic(x, 2.0f * 0.7978845608028654f * (x + 0.044715f * x * x * x));
+    case 3: return mul_logistic(x, x);
     case 4: return tanhf(x);
-    case 5: return 1.0f / (1.0f + expf(-x));
+    case 5: return mul_logistic(1.0f, x);
     case 6: return x >= 0.0f ? x : a * x;
     case 7: return clampf_(x, 0.0f, 6.0f);
     case 8: return clampf_(x / 6.0f + 0.5f, 0.0f, 1.0f);
@@ -490,6 +499,53 @@ __host__ __device__ __forceinline__ uint32_t lb_bit(size_t d) {
     if (KIND == 2) return 8 * b + 2 * i;
     const uint32_t h = (uint32_t)((d % Q1_GROUP) / LB_SLAB) % 2;
     return 8 * b + 4 * h + i;
+}
+
+// ---- Q4 dequant in registers -------------------------------------------------
+
+// v_bfi_b32 (mask in an SGPR, both data operands in VGPRs): the compiler
+// otherwise splits the insert into an and + an or with literal constants.
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t x, uint32_t y) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(x), "v"(y));
+    return r;
+}
+
+// dword of 8 biased nibbles (code+8; depth 2e at bits 4e, depth 2e+1 at bits
+// 16+4e) -> 8 f16 weights f16_RNE(scale*code) in depth order.
+__device__ __forceinline__ uint4 q4_deq8(uint32_t q, half2_t s2, uint32_t mag_lo, uint32_t mag_hi) {
+    const half2_t off_lo = {(_Float16)1032.0f, (_Float16)1032.0f};  // 0x6400|u = 1024+u
+    const half2_t off_hi = {(_Float16)72.0f, (_Float16)72.0f};      // 0x5400|u<<4 = 64+u
+    const uint32_t q8 = q >> 8;
+    // one v_bfi_b32 each: (mask & x) | (~mask & magic)
+    const uint32_t h0 = bfi(0x000F000Fu, q, mag_lo);
+    const uint32_t h1 = bfi(0x00F000F0u, q, mag_hi);
+    const uint32_t h2 = bfi(0x000F000Fu, q8, mag_lo);
+    const uint32_t h3 = bfi(0x00F000F0u, q8, mag_hi);
+    const half2_t w0 = (__builtin_bit_cast(half2_t, h0) - off_lo) * s2;
+    const half2_t w1 = (__builtin_bit_cast(half2_t, h1) - off_hi) * s2;
+    const half2_t w2 = (__builtin_bit_cast(half2_t, h2) - off_lo) * s2;
+    const half2_t w3 = (__builtin_bit_cast(half2_t, h3) - off_hi) * s2;
+    return make_uint4(__builtin_bit_cast(uint32_t, w0), __builtin_bit_cast(uint32_t, w1),
+                      __builtin_bit_cast(uint32_t, w2), __builtin_bit_cast(uint32_t, w3));
+}
+
+
+// Q4_1: 8 f16 weights f16_RNE(scale*code + min) -- one v_pk_fma_f16 per pair
+// rounds the exact value once, as the reference's f16::from_f64 of the f64 sum.
+__device__ __forceinline__ uint4 q4_deq8_affine(uint32_t q, half2_t s2, half2_t m2, uint32_t mag_lo,
+                                                uint32_t mag_hi) {
+    const half2_t off_lo = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const half2_t off_hi = {(_Float16)72.0f, (_Float16)72.0f};
+    const uint32_t q8 = q >> 8;
+    const half2_t c0 = __builtin_bit_cast(half2_t, bfi(0x000F000Fu, q, mag_lo)) - off_lo;
+    const half2_t c1 = __builtin_bit_cast(half2_t, bfi(0x00F000F0u, q, mag_hi)) - off_hi;
+    const half2_t c2 = __builtin_bit_cast(half2_t, bfi(0x000F000Fu, q8, mag_lo)) - off_lo;
+    const half2_t c3 = __builtin_bit_cast(half2_t, bfi(0x00F000F0u, q8, mag_hi)) - off_hi;
+    return make_uint4(__builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c0, s2, m2)),
+                      __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c1, s2, m2)),
+                      __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c2, s2, m2)),
+                      __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c3, s2, m2)));
 }
 
 }  // namespace smg

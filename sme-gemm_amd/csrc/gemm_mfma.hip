@@ -23,6 +23,7 @@
 // of step k, so each load has two steps of MFMA work to arrive behind. With
 // BM = 256 every Q4 weight is dequantized once per 256 output rows.
 #include "kernels.h"
+#include "tile_store.cuh"
 
 namespace smg {
 
@@ -60,12 +61,6 @@ __device__ __forceinline__ float4_t mfma(const uint4 &a, const uint4 &b, float4_
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                        __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
     }
-}
-
-__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t x, uint32_t y) {
-    uint32_t r;
-    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(x), "v"(y));
-    return r;
 }
 
 // ---- B tile: global -> registers (early) -> LDS (dequantized) ----------------
@@ -316,16 +311,12 @@ __device__ __forceinline__ void mma_half(const uint4 (&fa)[4], const uint4 (&fb)
 template <bool BF16, int BM>
 __device__ __forceinline__ void store_tile(const GemmArgs &g, const EpArgs &ep, const float4_t (&acc)[4][4],
                                            uint16_t *lds, uint32_t row0, uint32_t col0, int wm, int wn,
-                                           int lane, int lds_halfs) {
+                                           int lane) {
     const int t = threadIdx.x, lr = lane % 16;
-    (void)lds_halfs;
-    // Round beta*acc to 16 bits into LDS (the loop's last barrier freed it),
-    // then store rows of 8 consecutive columns: 16-byte stores when the
-    // destination is row-major, and the op-graph on the rounded value
-    // (src/exec/macros.rs:188-206). A lane holds D[4*(lane/16)+v][lane%16] of
-    // each 16x16 MFMA tile.
+    // Round beta*acc to 16 bits into LDS (the loop's last barrier freed it); a
+    // lane holds D[4*(lane/16)+v][lane%16] of each 16x16 MFMA tile. The LDS
+    // holds BM * CS halfs of tile plus the operand vectors (EPI_LDS_HALFS).
     constexpr int CS = BN + 8;  // halfs per staged row
-    // (the caller's LDS holds lds_halfs >= BM * CS + the operand vectors)
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -335,80 +326,14 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const EpArgs &ep, 
                 lds[(wm * 64 + i * 16 + (lane / 16) * 4 + v) * CS + wn * 64 + jt * 16 + lr] =
                     from_f32<BF16>(0.0f + g.beta * acc[i][jt][v]);
     __syncthreads();
-    const bool plain = ep.n_nodes == 0;
-    // ROW / COL operand vectors are read once per tile into LDS (as f32), so
-    // the cell loop below touches global memory only for TENSOR operands.
-    float *colv = (float *)(lds + BM * CS);   // [node][BN]
+    const StoreArgs sa = {g.dst, g.dst_rs, g.dst_cs, g.m, g.n};
+    float *colv = (float *)(lds + BM * CS);      // [node][BN]
     float *rowv = colv + SMG_MAX_EP_NODES * BN;  // [node][BM]
-    for (uint32_t q = 0; q < ep.n_nodes; q++) {
-        const uint32_t cls = ep.cls[q];
-        const uint16_t *p = (const uint16_t *)ep.nodes[q].ptr;
-        if (cls == EPC_COL && t < BN)
-            colv[q * BN + t] = col0 + t < g.n ? to_f32<BF16>(p[col0 + t]) : 0.0f;
-        if (cls == EPC_ROW && t < BM)
-            rowv[q * BM + t] = row0 + t < g.m ? to_f32<BF16>(p[row0 + t]) : 0.0f;
-    }
+    ep_load_vectors<BF16, BM, BN, BM * 2>(sa, ep, colv, rowv, row0, col0);
     __syncthreads();
     for (int u = t; u < BM * (BN / 8); u += BM * 2) {
         const int rl = u / (BN / 8), cl = (u % (BN / 8)) * 8;
-        const uint32_t row = row0 + rl, col = col0 + cl;
-        if (row >= g.m || col >= g.n) continue;
-        const uint32_t ne = g.n - col < 8 ? g.n - col : 8;  // cells of this row group
-        uint4 c8 = *(const uint4 *)(lds + rl * CS + cl);
-        if (!plain) {
-            uint32_t w4[4] = {c8.x, c8.y, c8.z, c8.w};
-            float x[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) x[e] = to_f32<BF16>((uint16_t)(w4[e / 2] >> (16 * (e % 2))));
-            for (uint32_t q = 0; q < ep.n_nodes; q++) {
-                const EpNode &nd = ep.nodes[q];
-                const uint32_t cls = ep.cls[q], fam = ep.fam[q];
-                if (fam == EPF_ACT) {
-                    F8 y;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) y.v[e] = x[e];
-                    y = act8_fast(nd.aux, y, nd.scalar);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) x[e] = y.v[e];
-                    continue;
-                }
-                float v[8];
-                if (cls == EPC_TENSOR) {
-                    // the 8 loads are issued together, then consumed
-                    const uint16_t *p = (const uint16_t *)nd.ptr + (size_t)row * (nd.ld == 0 ? g.n : nd.ld) + col;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) v[e] = (uint32_t)e < ne ? to_f32<BF16>(p[e]) : 0.0f;
-                } else if (cls == EPC_COL) {
-#pragma unroll
-                    for (int e = 0; e < 8; e++) v[e] = colv[q * BN + cl + e];
-                } else {
-                    const float vs = cls == EPC_ROW ? rowv[q * BM + rl] : nd.scalar;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) v[e] = vs;
-                }
-                switch (fam) {  // uniform: one branch per node, then 8 lanes of arithmetic
-#define SMG_EP_FAM(F)                                                           \
-    case F:                                                                     \
-        _Pragma("unroll") for (int e = 0; e < 8; e++) x[e] = ep_arith(F, x[e], v[e]); \
-        break;
-                    SMG_EP_FAM(EPF_ADD) SMG_EP_FAM(EPF_MUL) SMG_EP_FAM(EPF_SUB)
-                    SMG_EP_FAM(EPF_DIV) SMG_EP_FAM(EPF_MAX) SMG_EP_FAM(EPF_MIN)
-#undef SMG_EP_FAM
-                default: break;
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                w4[e] = (uint32_t)from_f32<BF16>(x[2 * e]) | ((uint32_t)from_f32<BF16>(x[2 * e + 1]) << 16);
-            c8 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-        }
-        uint16_t *dp = g.dst + (size_t)row * g.dst_rs + (size_t)col * g.dst_cs;
-        if (g.dst_cs == 1 && ne == 8 && ((uintptr_t)dp & 15) == 0) {
-            *(uint4 *)dp = c8;
-            continue;
-        }
-        const uint32_t w4[4] = {c8.x, c8.y, c8.z, c8.w};
-        for (uint32_t e = 0; e < ne; e++) dp[(size_t)e * g.dst_cs] = (uint16_t)(w4[e / 2] >> (16 * (e % 2)));
+        ep_store8<BF16, BM, BN>(sa, ep, colv, rowv, *(const uint4 *)(lds + rl * CS + cl), rl, cl, row0, col0);
     }
 }
 
@@ -503,7 +428,7 @@ __global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
         }
     }
 
-    store_tile<BF16, BM>(g, ep, acc, lds, row0, col0, wm, wn, lane, Tile<BM>::NSTAGE * STAGE);
+    store_tile<BF16, BM>(g, ep, acc, lds, row0, col0, wm, wn, lane);
 }
 
 template <int WK, bool BF16, bool AFFINE, int BM, bool VECA, bool PD>
@@ -547,6 +472,8 @@ hipError_t launch_shape(const GemmArgs &g, const EpArgs &ep, bool vec_a, hipStre
 hipError_t launch_gemm(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,
                        const uint16_t *lhs, long lhs_cs, long lhs_rs, float beta,
                        const EpArgs &ep, bool bf16, hipStream_t s) {
+    if (q4r_supported(w, m, lhs_cs, lhs_rs, lhs, bf16))
+        return launch_q4r(w, m, dst, dst_cs, dst_rs, lhs, lhs_rs, beta, ep, s);
     GemmArgs g = {};
     g.lhs = lhs;
     g.dst = dst;

@@ -1,0 +1,345 @@
+// Q4 x f16 prefill GEMM with the weights dequantized in registers:
+// C = ep(to16(beta * A @ dequant(B))) for matmul_q4 / matmul_q4_ep with m > 8
+// (src/kernels/q4/matmul.rs:37-103), replacing run_q4_panels + unpack_q4_f16
+// (csrc/gemm_f16f16_q4.h:57-118). Serves f16 activations, Q4_0 and Q4_1,
+// blocks of 32 depths or more, K a multiple of 64 and row-major A; every other
+// case goes to gemm_kernel (gemm_mfma.hip).
+//
+// Tile: 128 rows x 256 columns, eight waves, two per SIMD. Waves w and w+4 (on
+// one SIMD) own columns 64(w%4)..+63 for all 128 rows and split K: wave w
+// multiplies the first 32 depths of every 64-depth step, wave w+4 the second,
+// and their f32 partial tiles are added once at the end. Each wave holds 8 x 4
+// MFMA tiles of 16 x 16 on v_mfma_f32_16x16x32_f16. Every weight of the tile
+// is dequantized once, by the one wave that multiplies it, straight into MFMA
+// B registers: no f16 weight tile is written to or read from LDS, which is
+// what bounds a kernel that stages dequantized weights there. The weight is
+// rounded once, f16_RNE(scale*code) (+min: one fused rounding), as the
+// reference's dequant (src/kernels/q4/mod.rs:193-224).
+//
+// Everything a step needs goes global -> LDS by DMA (global_load_lds, no
+// registers): the 128 x 64 activation tile (16-byte chunks swizzled: chunk c of
+// row r at slot c ^ (r & 7), so fragment reads are conflict-free), the tile's
+// raw Q4 chunks and its scales (and mins). A ring of five stages: the DMA for
+// step k+4 is issued while step k multiplies, each step's barrier waits only
+// for step k+2's DMA, and a wave reads step k+1's fragments from LDS while its
+// step-k multiplies run.
+#include "kernels.h"
+#include "tile_store.cuh"
+
+namespace smg {
+
+namespace {
+
+constexpr int RBM = 128, RBN = 256, RNT = 512;  // tile rows, tile columns, threads
+constexpr int A_BYTES = RBM * 64 * 2;           // activations: [128 rows][64 depths] f16
+constexpr int B_BYTES = 2 * RBN * 16;           // raw Q4: [half][256 columns] 16-byte chunks
+constexpr int S_BYTES = 2 * RBN * 2;            // scales (mins): [half][256 columns] f16
+constexpr int STAGE_BYTES = A_BYTES + B_BYTES + 2 * S_BYTES;
+constexpr int CS = RBN + 8;                     // halfs per staged output row
+constexpr int NSTAGE = 5;                       // LDS ring depth
+constexpr int PS = 4;                           // DMA instructions per lane per step
+static_assert(RBM * CS * 2 <= NSTAGE * STAGE_BYTES, "store staging exceeds the ring");
+static_assert(4 * 4096 * 4 <= NSTAGE * STAGE_BYTES, "partial-tile exchange exceeds the ring");
+
+struct RArgs {
+    const uint16_t *lhs;
+    const uint8_t *codes;
+    const uint16_t *sc;
+    const uint16_t *mn;
+    StoreArgs st;
+    float beta;
+    long lhs_rs;
+    uint32_t m, n, k, n_pad, block_shift;
+};
+
+// LDS DMA: each lane's 16 (4) bytes from sbase + voff land at M0 + 16 (4) *
+// lane; sbase is wave-uniform (scalar registers), voff the lane's 32-bit byte
+// offset, so a step's addresses cost no vector instructions. The instructions
+// are issued from inline asm so that the compiler neither tracks them nor adds
+// waits of its own (it cannot tell which stage a DMA fills); the kernel's
+// explicit vmcnt waits and barriers order them. The "memory" clobber keeps LDS
+// reads from moving across an issue; s_nop covers the M0 write hazard. lds is a
+// wave-uniform LDS byte address. (M0 has no other user in this kernel, so
+// clobbering it is safe.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void *sbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+                 "s"(lds)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void *sbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase),
+                 "s"(lds)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
+}
+
+// s_waitcnt vmcnt(n) (gfx9 encoding; expcnt and lgkmcnt left unwaited).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier that orders LDS accesses without waiting on outstanding
+// DMA (a release fence would wait for all of it): the empty asm statements keep
+// the compiler from moving memory accesses across it; the caller first waits
+// for the DMA the next step reads.
+__device__ __forceinline__ void barrier_lds() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Per-lane DMA offsets that do not change from step to step. Thread t loads
+// activation chunks t and t+512, raw chunk t ([half t/256][column t%256]) and
+// one dword of scales (waves 0-3) or mins (waves 4-7; scales again, unused,
+// for Q4_0 so that every wave issues the same count). The halves are
+// wave-uniform, so each step's part of an address is a scalar base.
+struct DmaSrc {
+    uint32_t a[2];          // activation chunk byte offsets from A at depth 0
+    uint32_t b;             // raw chunk byte offset within a chunk row
+    uint32_t s;             // scale (min) pair byte offset within a scale row
+    uint32_t half_b, half_s;  // this wave's half of the step for raw chunks / scales
+    const uint16_t *src_s;  // scales or mins
+};
+
+__device__ __forceinline__ void dma_step(const RArgs &g, const DmaSrc &d, const uint8_t *S, uint32_t ks,
+                                         uint32_t wave) {
+    const uint32_t base = lds_addr(S);
+    // activations: chunk p = q*512 + t lands at byte 16p (row p/8, slot p%8)
+    const uint16_t *a = g.lhs + (size_t)ks * 64;
+#pragma unroll
+    for (int q = 0; q < 2; q++) dma16(a, d.a[q], base + (q * 512 + wave * 64) * 16);
+    // raw Q4: chunk (2ks + t/256, column t%256) at byte A_BYTES + 16t
+    dma16(g.codes + (size_t)(2 * ks + d.half_b) * g.n_pad * 16, d.b, base + A_BYTES + wave * 64 * 16);
+    // scales (mins): [half][column] f16, two per lane
+    const size_t row = (size_t)(((2 * ks + d.half_s) * 32) >> g.block_shift);
+    dma4(d.src_s + row * g.n_pad, d.s, base + A_BYTES + B_BYTES + wave * 256);
+}
+
+// One 32-depth half of a step as LDS reads: 8 activation fragments and, per
+// column tile, the raw dword and scale (min) of this lane's 8 depths.
+// (32-bit vector types, not arrays of 16-bit values: the fields stay in
+// registers, one element per register)
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+struct Half {
+    u32x4_t a[8];
+    u32x4_t q, s, mn;
+};
+
+// This lane's LDS byte offsets within a stage (constant over the loop).
+struct ReadOff {
+    uint32_t a, q, s;  // first activation fragment, first raw dword, first scale
+};
+
+__device__ __forceinline__ ReadOff read_offsets(int kk, int cw, int lane) {
+    const int lr = lane % 16, lg = lane / 16;
+    ReadOff o;
+    o.a = lr * 128 + (((kk * 4 + lg) ^ (lr & 7)) << 4);  // row & 7 == lr & 7 for rows 16i + lr
+    o.q = A_BYTES + (kk * 256 + cw * 64 + lr) * 16 + lg * 4;
+    o.s = A_BYTES + B_BYTES + kk * 512 + (cw * 64 + lr) * 2;
+    return o;
+}
+
+typedef const __attribute__((address_space(3))) uint8_t lds_u8_t;
+template <class T>
+__device__ __forceinline__ T lds_load(uint32_t addr) {
+    return *(const __attribute__((address_space(3))) T *)(lds_u8_t *)(uintptr_t)addr;
+}
+
+// Stage at LDS byte address sb: row tile i's fragment at o.a + 2048 i, column
+// tile jt's raw dword at o.q + 256 jt and scale at o.s + 32 jt (min S_BYTES
+// further on).
+template <bool AFFINE>
+__device__ __forceinline__ void read_half(uint32_t sb, const ReadOff &o, Half &h) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) h.a[i] = lds_load<u32x4_t>(sb + o.a + 2048 * i);
+#pragma unroll
+    for (int jt = 0; jt < 4; jt++) {
+        h.q[jt] = lds_load<uint32_t>(sb + o.q + 256 * jt);
+        h.s[jt] = lds_load<uint16_t>(sb + o.s + 32 * jt);
+        if (AFFINE) h.mn[jt] = lds_load<uint16_t>(sb + o.s + S_BYTES + 32 * jt);
+    }
+}
+
+template <bool AFFINE>
+__device__ __forceinline__ void mma_half(const Half &h, float4_t (&acc)[8][4], uint32_t mag_lo,
+                                         uint32_t mag_hi) {
+#pragma unroll
+    for (int jt = 0; jt < 4; jt++) {
+        const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)h.s[jt]);
+        const half2_t s2 = {s, s};
+        uint4 b;
+        if (AFFINE) {
+            const _Float16 mv = __builtin_bit_cast(_Float16, (uint16_t)h.mn[jt]);
+            b = q4_deq8_affine(h.q[jt], s2, (half2_t){mv, mv}, mag_lo, mag_hi);
+        } else {
+            b = q4_deq8(h.q[jt], s2, mag_lo, mag_hi);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            acc[i][jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, h.a[i]),
+                                                                __builtin_bit_cast(half8_t, b), acc[i][jt], 0, 0, 0);
+    }
+}
+
+template <bool AFFINE>
+__global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
+    __shared__ __align__(16) uint8_t ring[NSTAGE * STAGE_BYTES];
+    __shared__ __align__(16) float epv[SMG_MAX_EP_NODES * (RBN + RBM)];
+
+    // column-tile-major order: consecutive workgroups share a weight tile
+    const uint32_t mtiles = (g.m + RBM - 1) / RBM;
+    const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
+    const uint32_t tm = tile % mtiles, tn = tile / mtiles;
+    const uint32_t row0 = tm * RBM, col0 = tn * RBN;
+    const int t = threadIdx.x, lane = t % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(t / 64);  // uniform: DMA bases, branches
+    const int cw = wave % 4, kh = wave / 4;  // column block, half of each step
+
+    // Rows past m and columns past n_pad read clamped (valid) addresses; their
+    // results are never stored.
+    DmaSrc d;
+    {
+        const uint32_t c = (t % 8) ^ ((t / 8) % 8);  // source chunk of slot t%8 in row t/8 (+64q)
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const uint32_t row = min(row0 + q * 64 + t / 8, g.m - 1);
+            d.a[q] = (uint32_t)(((size_t)row * g.lhs_rs + c * 8) * 2);
+        }
+        d.b = min(col0 + t % 256, g.n_pad - 1) * 16;
+        d.s = min(col0 + 2 * (t % 128), g.n_pad - 2) * 2;
+        d.half_b = wave / 4;
+        d.half_s = (wave % 4) / 2;
+        d.src_s = (AFFINE && wave >= 4) ? g.mn : g.sc;
+    }
+    const uint32_t ksteps = g.k / 64;  // >= 1
+    const uint32_t last = ksteps - 1;
+
+    float4_t acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int jt = 0; jt < 4; jt++) acc[i][jt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    // the bfi magics live in VGPRs (a VOP3 takes one scalar operand)
+    uint32_t mag_lo = 0x64006400u, mag_hi = 0x54005400u;
+    asm volatile("" : "+v"(mag_lo), "+v"(mag_hi));
+
+#pragma unroll
+    for (int j = 0; j < NSTAGE - 1; j++) dma_step(g, d, ring + j * STAGE_BYTES, min((uint32_t)j, last), wave);
+    wait_vm<(NSTAGE - 3) * PS>();  // steps 0 and 1 landed
+    barrier_lds();
+
+    // Step ks: step ks+1's fragments are read (its stage was published by the
+    // barrier ending step ks-1) while step ks multiplies; then step ks+2's
+    // DMA is waited for and the barrier publishes it (and frees stage
+    // (ks+4)%5, last read during step ks-2), and step ks+4's DMA is issued into
+    // that stage. Steps past the end re-load the last step into the free stage
+    // and read a stage nobody multiplies.
+    const uint32_t ring0 = lds_addr(ring);
+    const ReadOff ro = read_offsets(kh, cw, lane);
+    auto step = [&](uint32_t ks, const Half &cur, Half &nxt) {
+        uint32_t sb = ring0 + ((ks + 1) % NSTAGE) * STAGE_BYTES;
+        asm volatile("" : "+s"(sb));  // opaque: one base add per operand kind, constant offsets after
+        read_half<AFFINE>(sb, ro, nxt);
+        mma_half<AFFINE>(cur, acc, mag_lo, mag_hi);
+        wait_vm<PS>();
+        barrier_lds();
+        dma_step(g, d, ring + ((ks + NSTAGE - 1) % NSTAGE) * STAGE_BYTES, min(ks + NSTAGE - 1, last), wave);
+    };
+    Half h0, h1;
+    read_half<AFFINE>(ring0, ro, h0);
+    uint32_t ks = 0;
+    for (; ks + 2 <= ksteps; ks += 2) {
+        step(ks, h0, h1);
+        step(ks + 1, h1, h0);
+    }
+    if (ks < ksteps) step(ks, h0, h1);
+    wait_vm<0>();
+    __syncthreads();
+
+    // The pair's partial tiles: wave w+4 hands its f32 tile to wave w through
+    // LDS (64 rows at a time; lane-contiguous, so conflict-free), wave w adds.
+    float *red = (float *)ring + cw * 4096;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        if (kh == 1) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int jt = 0; jt < 4; jt++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) red[((i * 4 + jt) * 4 + v) * 64 + lane] = acc[4 * r + i][jt][v];
+        }
+        __syncthreads();
+        if (kh == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int jt = 0; jt < 4; jt++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) acc[4 * r + i][jt][v] += red[((i * 4 + jt) * 4 + v) * 64 + lane];
+        }
+        __syncthreads();
+    }
+
+    // Store: beta*acc rounded to f16 into LDS ([128][CS]; a lane holds
+    // D[4*(lane/16)+v][lane%16] of each 16x16 tile), then groups of 8 columns
+    // through the op-graph by all eight waves.
+    uint16_t *stg = (uint16_t *)ring;
+    if (kh == 0) {
+        const int lr = lane % 16, lg = lane / 16;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int jt = 0; jt < 4; jt++)
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    stg[(i * 16 + lg * 4 + v) * CS + cw * 64 + jt * 16 + lr] = from_f32<false>(0.0f + g.beta * acc[i][jt][v]);
+    }
+    float *colv = epv, *rowv = epv + SMG_MAX_EP_NODES * RBN;
+    ep_load_vectors<false, RBM, RBN, RNT>(g.st, ep, colv, rowv, row0, col0);
+    __syncthreads();
+    // thread t: column group t % 32, rows t / 32 + 16 j
+    static_assert(RNT % (RBN / 8) == 0, "each thread keeps one column group");
+    ep_store_rows<false, RBM, RBN, RBM * (RBN / 8) / RNT>(g.st, ep, colv, rowv, stg, CS, t / (RBN / 8),
+                                                          RNT / (RBN / 8), (t % (RBN / 8)) * 8, row0, col0);
+}
+
+}  // namespace
+
+bool q4r_supported(const WDev &w, size_t m, long lhs_cs, long lhs_rs, const uint16_t *lhs, bool bf16) {
+    return w.kind == W_Q4 && !bf16 && m > 0 && w.k >= 64 && w.k % 64 == 0 && w.block >= 32 &&
+           lhs_cs == 1 && lhs_rs % 8 == 0 && lhs_rs >= (long)w.k && ((uintptr_t)lhs & 15) == 0 &&
+           m * (size_t)lhs_rs * 2 < ((size_t)1 << 31);  // 32-bit DMA offsets
+}
+
+hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,
+                      const uint16_t *lhs, long lhs_rs, float beta, const EpArgs &ep, hipStream_t s) {
+    RArgs g = {};
+    g.lhs = lhs;
+    g.codes = w.codes;
+    g.sc = w.scales;
+    g.mn = w.mins;
+    g.st = {dst, dst_rs, dst_cs, (uint32_t)m, (uint32_t)w.n};
+    g.beta = beta;
+    g.lhs_rs = lhs_rs;
+    g.m = (uint32_t)m;
+    g.n = (uint32_t)w.n;
+    g.k = (uint32_t)w.k;
+    g.n_pad = (uint32_t)w.n_pad;
+    g.block_shift = (uint32_t)__builtin_ctzll(w.block);
+    const uint32_t tiles = (uint32_t)(((m + RBM - 1) / RBM) * ((w.n + RBN - 1) / RBN));
+    if (w.mins)
+        hipLaunchKernelGGL(gemm_q4r<true>, dim3(tiles), dim3(RNT), 0, s, g, ep);
+    else
+        hipLaunchKernelGGL(gemm_q4r<false>, dim3(tiles), dim3(RNT), 0, s, g, ep);
+    return hipGetLastError();
+}
+
+}  // namespace smg

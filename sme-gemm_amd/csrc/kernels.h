@@ -43,6 +43,13 @@ hipError_t launch_gemm(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long
                        const uint16_t *lhs, long lhs_cs, long lhs_rs, float beta,
                        const EpArgs &ep, bool bf16, hipStream_t s);
 
+// Q4 x f16 GEMM with register-resident weights (gemm_q4r.hip): f16, block >=
+// 32, K a multiple of 64, row-major 16-byte-aligned A. launch_gemm uses it
+// whenever q4r_supported holds.
+bool q4r_supported(const WDev &w, size_t m, long lhs_cs, long lhs_rs, const uint16_t *lhs, bool bf16);
+hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,
+                      const uint16_t *lhs, long lhs_rs, float beta, const EpArgs &ep, hipStream_t s);
+
 // Device-side repacks / dequant.
 hipError_t launch_q4_dequant_dense(const WDev &q4, uint16_t *dense, bool to_bf16,
                                    hipStream_t s);

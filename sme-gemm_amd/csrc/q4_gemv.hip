@@ -52,33 +52,6 @@ constexpr int MF_U = 4;                      // steps (4 chunks each) in flight 
 constexpr int MF_SEG = 4096;                 // depths of A staged in LDS at a time
 constexpr int MF_SEG_CH = MF_SEG / Q4_CHUNK; // 128 chunks per segment
 
-// v_bfi_b32 (mask in an SGPR, both data operands in VGPRs): the compiler
-// otherwise splits the insert into an and + an or with literal constants.
-__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t x, uint32_t y) {
-    uint32_t r;
-    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(x), "v"(y));
-    return r;
-}
-
-// dword of 8 biased nibbles (code+8; depth 2e at bits 4e, depth 2e+1 at bits
-// 16+4e) -> 8 f16 weights f16_RNE(scale*code) in depth order.
-__device__ __forceinline__ uint4 deq8(uint32_t q, half2_t s2, uint32_t mag_lo, uint32_t mag_hi) {
-    const half2_t off_lo = {(_Float16)1032.0f, (_Float16)1032.0f};  // 0x6400|u = 1024+u
-    const half2_t off_hi = {(_Float16)72.0f, (_Float16)72.0f};      // 0x5400|u<<4 = 64+u
-    const uint32_t q8 = q >> 8;
-    // one v_bfi_b32 each: (mask & x) | (~mask & magic)
-    const uint32_t h0 = bfi(0x000F000Fu, q, mag_lo);
-    const uint32_t h1 = bfi(0x00F000F0u, q, mag_hi);
-    const uint32_t h2 = bfi(0x000F000Fu, q8, mag_lo);
-    const uint32_t h3 = bfi(0x00F000F0u, q8, mag_hi);
-    const half2_t w0 = (__builtin_bit_cast(half2_t, h0) - off_lo) * s2;
-    const half2_t w1 = (__builtin_bit_cast(half2_t, h1) - off_hi) * s2;
-    const half2_t w2 = (__builtin_bit_cast(half2_t, h2) - off_lo) * s2;
-    const half2_t w3 = (__builtin_bit_cast(half2_t, h3) - off_hi) * s2;
-    return make_uint4(__builtin_bit_cast(uint32_t, w0), __builtin_bit_cast(uint32_t, w1),
-                      __builtin_bit_cast(uint32_t, w2), __builtin_bit_cast(uint32_t, w3));
-}
-
 template <int MR>  // rows staged per segment (1, 2, 4, 8)
 __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpArgs ep) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -135,7 +108,7 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
             const uint32_t kcl = live ? kc - sc0 : 0;
 #pragma unroll
             for (int w = 0; w < 4; w++) {
-                uint4 wa = deq8(words[w], s2, mag_lo, mag_hi);
+                uint4 wa = q4_deq8(words[w], s2, mag_lo, mag_hi);
                 uint4 ab = make_uint4(0, 0, 0, 0);
                 if (row < MR) {
                     const uint4 v = *(const uint4 *)(a_lds + row * MF_SEG + kcl * Q4_CHUNK + w * 8);

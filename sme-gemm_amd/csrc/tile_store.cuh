@@ -1,0 +1,199 @@
+// The GEMM kernels' output store: C = ep(to16(beta * acc)), shared by every
+// prefill kernel. The caller rounds its accumulators to 16 bits into LDS, then
+// walks its tile in groups of 8 consecutive columns of one row; each group is
+// run through the op-graph on the rounded value (src/exec/macros.rs:188-206,
+// the portable path's apply_ep_scalar order, src/exec/scalar.rs:58-140) and
+// stored, 16 bytes at a time when the destination is row-major.
+#pragma once
+
+#include "common.cuh"
+
+namespace smg {
+
+struct StoreArgs {
+    uint16_t *dst;
+    long dst_rs, dst_cs;
+    uint32_t m, n;
+};
+
+// ROW / COL operand vectors of the graph, read once per tile into LDS as f32
+// (colv [node][TBN], rowv [node][TBM]), so the cell loop touches global memory
+// only for TENSOR operands. The caller puts a barrier between this and the
+// first ep_store8.
+template <bool BF16, int TBM, int TBN, int NT>
+__device__ __forceinline__ void ep_load_vectors(const StoreArgs &g, const EpArgs &ep, float *colv,
+                                                float *rowv, uint32_t row0, uint32_t col0) {
+    const int t = threadIdx.x;
+    for (uint32_t q = 0; q < ep.n_nodes; q++) {
+        const uint32_t cls = ep.cls[q];
+        const uint16_t *p = (const uint16_t *)ep.nodes[q].ptr;
+        if (cls == EPC_COL)
+            for (int c = t; c < TBN; c += NT) colv[q * TBN + c] = col0 + c < g.n ? to_f32<BF16>(p[col0 + c]) : 0.0f;
+        if (cls == EPC_ROW)
+            for (int r = t; r < TBM; r += NT) rowv[q * TBM + r] = row0 + r < g.m ? to_f32<BF16>(p[row0 + r]) : 0.0f;
+    }
+}
+
+// Cells (rl, cl .. cl+7) of the tile (local coordinates), c8 their rounded
+// 16-bit values.
+template <bool BF16, int TBM, int TBN>
+__device__ __forceinline__ void ep_store8(const StoreArgs &g, const EpArgs &ep, const float *colv,
+                                          const float *rowv, uint4 c8, int rl, int cl, uint32_t row0,
+                                          uint32_t col0) {
+    const uint32_t row = row0 + rl, col = col0 + cl;
+    if (row >= g.m || col >= g.n) return;
+    const uint32_t ne = g.n - col < 8 ? g.n - col : 8;  // cells of this row group
+    if (ep.n_nodes != 0) {
+        uint32_t w4[4] = {c8.x, c8.y, c8.z, c8.w};
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = to_f32<BF16>((uint16_t)(w4[e / 2] >> (16 * (e % 2))));
+        for (uint32_t q = 0; q < ep.n_nodes; q++) {
+            const EpNode &nd = ep.nodes[q];
+            const uint32_t cls = ep.cls[q], fam = ep.fam[q];
+            if (fam == EPF_ACT) {
+                F8 y;
+#pragma unroll
+                for (int e = 0; e < 8; e++) y.v[e] = x[e];
+                y = act8_fast(nd.aux, y, nd.scalar);
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[e] = y.v[e];
+                continue;
+            }
+            float v[8];
+            if (cls == EPC_TENSOR) {
+                // the 8 loads are issued together, then consumed
+                const uint16_t *p = (const uint16_t *)nd.ptr + (size_t)row * (nd.ld == 0 ? g.n : nd.ld) + col;
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = (uint32_t)e < ne ? to_f32<BF16>(p[e]) : 0.0f;
+            } else if (cls == EPC_COL) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = colv[q * TBN + cl + e];
+            } else {
+                const float vs = cls == EPC_ROW ? rowv[q * TBM + rl] : nd.scalar;
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = vs;
+            }
+            switch (fam) {  // uniform: one branch per node, then 8 lanes of arithmetic
+#define SMG_EP_FAM(F)                                                           \
+    case F:                                                                     \
+        _Pragma("unroll") for (int e = 0; e < 8; e++) x[e] = ep_arith(F, x[e], v[e]); \
+        break;
+                SMG_EP_FAM(EPF_ADD) SMG_EP_FAM(EPF_MUL) SMG_EP_FAM(EPF_SUB)
+                SMG_EP_FAM(EPF_DIV) SMG_EP_FAM(EPF_MAX) SMG_EP_FAM(EPF_MIN)
+#undef SMG_EP_FAM
+            default: break;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            w4[e] = (uint32_t)from_f32<BF16>(x[2 * e]) | ((uint32_t)from_f32<BF16>(x[2 * e + 1]) << 16);
+        c8 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    }
+    uint16_t *dp = g.dst + (size_t)row * g.dst_rs + (size_t)col * g.dst_cs;
+    if (g.dst_cs == 1 && ne == 8 && ((uintptr_t)dp & 15) == 0) {
+        *(uint4 *)dp = c8;
+        return;
+    }
+    const uint32_t w4[4] = {c8.x, c8.y, c8.z, c8.w};
+    for (uint32_t e = 0; e < ne; e++) dp[(size_t)e * g.dst_cs] = (uint16_t)(w4[e / 2] >> (16 * (e % 2)));
+}
+
+// R rows (rl0 + rstep * j) x the same 8 columns (cl .. cl+7) of the tile:
+// what one thread stores when the tile's column groups divide the thread count.
+// The staged 16-bit values are read from tile (row stride cs halfs); a COL
+// operand is read once for all R rows, and every node runs over the R x 8 cells
+// before the next, so the R rows' work overlaps.
+template <bool BF16, int TBM, int TBN, int R>
+__device__ __forceinline__ void ep_store_rows(const StoreArgs &g, const EpArgs &ep, const float *colv,
+                                              const float *rowv, const uint16_t *tile, int cs, int rl0,
+                                              int rstep, int cl, uint32_t row0, uint32_t col0) {
+    const uint32_t col = col0 + cl;
+    if (col >= g.n) return;
+    const uint32_t ne = g.n - col < 8 ? g.n - col : 8;
+    uint4 c8[R];
+#pragma unroll
+    for (int j = 0; j < R; j++) c8[j] = *(const uint4 *)(tile + (rl0 + rstep * j) * cs + cl);
+    if (ep.n_nodes != 0) {
+        F8 x[R];
+#pragma unroll
+        for (int j = 0; j < R; j++) {
+            const uint32_t w4[4] = {c8[j].x, c8[j].y, c8[j].z, c8[j].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[j].v[e] = to_f32<BF16>((uint16_t)(w4[e / 2] >> (16 * (e % 2))));
+        }
+        for (uint32_t q = 0; q < ep.n_nodes; q++) {
+            const EpNode &nd = ep.nodes[q];
+            const uint32_t cls = ep.cls[q], fam = ep.fam[q];
+            if (fam == EPF_ACT) {
+#pragma unroll
+                for (int j = 0; j < R; j++) x[j] = act8_fast(nd.aux, x[j], nd.scalar);
+                continue;
+            }
+            if (cls == EPC_TENSOR) {
+                const size_t ld = nd.ld == 0 ? g.n : nd.ld;
+#pragma unroll
+                for (int j = 0; j < R; j++) {
+                    const uint32_t row = row0 + rl0 + rstep * j;
+                    const uint16_t *p = (const uint16_t *)nd.ptr + (size_t)(row < g.m ? row : 0) * ld + col;
+                    float v[8];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = (uint32_t)e < ne ? to_f32<BF16>(p[e]) : 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) x[j].v[e] = ep_arith(fam, x[j].v[e], v[e]);
+                }
+                continue;
+            }
+            float v[R][8];
+            if (cls == EPC_COL) {
+                float cv[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) cv[e] = colv[q * TBN + cl + e];
+#pragma unroll
+                for (int j = 0; j < R; j++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[j][e] = cv[e];
+            } else {
+#pragma unroll
+                for (int j = 0; j < R; j++) {
+                    const float vs = cls == EPC_ROW ? rowv[q * TBM + rl0 + rstep * j] : nd.scalar;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[j][e] = vs;
+                }
+            }
+            switch (fam) {  // uniform: one branch per node, then R x 8 lanes of arithmetic
+#define SMG_EP_FAM(F)                                                                              \
+    case F:                                                                                        \
+        _Pragma("unroll") for (int j = 0; j < R; j++) _Pragma("unroll") for (int e = 0; e < 8; e++) \
+            x[j].v[e] = ep_arith(F, x[j].v[e], v[j][e]);                                            \
+        break;
+                SMG_EP_FAM(EPF_ADD) SMG_EP_FAM(EPF_MUL) SMG_EP_FAM(EPF_SUB)
+                SMG_EP_FAM(EPF_DIV) SMG_EP_FAM(EPF_MAX) SMG_EP_FAM(EPF_MIN)
+#undef SMG_EP_FAM
+            default: break;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < R; j++) {
+            uint32_t w4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                w4[e] = (uint32_t)from_f32<BF16>(x[j].v[2 * e]) | ((uint32_t)from_f32<BF16>(x[j].v[2 * e + 1]) << 16);
+            c8[j] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        const uint32_t row = row0 + rl0 + rstep * j;
+        if (row >= g.m) continue;
+        uint16_t *dp = g.dst + (size_t)row * g.dst_rs + (size_t)col * g.dst_cs;
+        if (g.dst_cs == 1 && ne == 8 && ((uintptr_t)dp & 15) == 0) {
+            *(uint4 *)dp = c8[j];
+            continue;
+        }
+        const uint32_t w4[4] = {c8[j].x, c8[j].y, c8[j].z, c8[j].w};
+        for (uint32_t e = 0; e < ne; e++) dp[(size_t)e * g.dst_cs] = (uint16_t)(w4[e / 2] >> (16 * (e % 2)));
+    }
+}
+
+}  // namespace smg

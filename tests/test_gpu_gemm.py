@@ -157,3 +157,30 @@ def test_q4_dequant_eager_matches_oracle_bits(smg, orc):
             smg.Gemm(eye, packed, k).run(c)
             want = orc.q4_dequant(quants, scales, mins, n, k, 32, bf16)
             assert np.array_equal(c, want), f"affine={affine} bf16={bf16}"
+
+
+@pytest.mark.parametrize("m,n,k,block,affine", [
+    (9, 256, 64, 32, False), (40, 300, 128, 64, True), (129, 520, 320, 32, False),
+    (200, 1000, 512, 128, True), (256, 768, 1024, 32, False), (17, 129, 192, 64, False),
+    (512, 512, 4096, 32, False), (130, 384, 256, 256, True)])
+def test_q4_register_weight_gemm(smg, orc, m, n, k, block, affine):
+    """The Q4 f16 prefill kernel that dequantizes weights in registers (K a
+    multiple of 64, block >= 32; two waves split each 64-depth step and add
+    their f32 partial tiles): within tolerance of the oracle and of the dense
+    GEMM over the eagerly dequantized weights."""
+    rng = np.random.default_rng(m + n + k + block)
+    nbk = -(-k // block)
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.002, 0.02, n * nbk).astype(np.float32))
+    mins = orc.f32_to_f16(rng.uniform(-0.05, 0.05, n * nbk).astype(np.float32)) if affine else None
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    p = smg.Q4Params(block).affine() if affine else smg.Q4Params(block)
+    w = smg.Q4Weights.with_params(quants, scales, mins, n, k, p)
+    c = np.zeros(m * n, np.uint16)
+    smg.matmul_q4(a, w, c, m)
+    want = orc.matmul_q4_ep(a, quants, scales, mins, m, n, k, block)
+    assert max_rel(c, want) <= f16_tol(k)
+    packed = smg.dequant_q4_with(quants, scales, mins, n, k, p)
+    d = np.zeros(m * n, np.uint16)
+    smg.Gemm(a, packed, m).run(d)
+    assert max_rel(c, d) <= f16_tol(k)
