@@ -82,6 +82,9 @@ __device__ __forceinline__ uint4 bload16(rsrc_t r, uint32_t off) {
 __device__ __forceinline__ uint16_t bload2(rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
 }
+__device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
 
 // 8 consecutive 16-bit elements A[row][d..d+8) of a row-major [rows][k] array
 // at `r` (zero outside rows x k). vec: k % 8 == 0, so rows are 16-byte aligned

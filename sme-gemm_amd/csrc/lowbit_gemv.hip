@@ -204,15 +204,19 @@ __global__ void __launch_bounds__(T) lowbit_gemv(LbArgs g, EpArgs ep) {
 
 // ---------------------------------------------------------------------------
 // Single-launch path (m <= 8, block <= 4096, K <= 8192, m*K <= 32 K): one
-// workgroup of 8 waves per 16-column tile, a straight-line program kept short
-// (each workgroup runs it once, so its instruction fetch is part of the
-// latency). Each workgroup quantizes the rows of A itself -- a few KB, read
-// from L2 -- so a call is one launch:
-//   1. loads: A, then the tile's code groups (a wave covers a contiguous K
-//      range in whole 16-byte groups: Q2 4 slabs, Q1 8), then its scale rows;
-//   2. quantize: thread t takes depths 8t..8t+7 (per 4096-depth pass) of every
-//      row; a block's amax and sum(q) are reduced over the block's lanes by
-//      shuffles, and through LDS over waves for blocks longer than 512;
+// workgroup of 8 waves per 16*CG-column tile, a straight-line program kept
+// short (each workgroup runs it once, so its instruction fetch is part of the
+// latency). With one row, each workgroup quantizes A itself -- 8 KB read from
+// L2 -- so a call is one launch; with more rows that work would repeat in every
+// workgroup, so lowbit_prequant quantizes them once before the launch and the
+// workgroups load the result:
+//   1. loads: A (or its quantized rows), then the scale rows, the epilogue
+//      operands and the tile's code groups (a wave covers a contiguous K range
+//      in whole 16-byte groups: Q2 4 slabs, Q1 8);
+//   2. quantize (quant_pass): thread t takes depths 8t..8t+7 (per 4096-depth
+//      pass) of every row; a block's amax and sum(q) are reduced over the
+//      block's lanes by shuffles, and through LDS over waves for blocks longer
+//      than 512;
 //   3. exact block sums on v_mfma_i32_16x16x64_i8, accumulated over a block's
 //      slabs inside one wave (a wave's K range holds whole blocks; shorter
 //      blocks take one masked product each), written to LDS per (row, column)
@@ -238,6 +242,10 @@ struct LtArgs {
     uint32_t nbq;          // blocks in kq (a multiple of 4)
     uint32_t codes_bytes;  // extent of the code array (buffer resource)
     uint32_t cg_shift;     // log2 of the 16-column groups per workgroup (CG)
+    // rows quantized beforehand by lowbit_prequant (multi-row calls):
+    const int8_t *q;       // [m][kq]
+    const float *qs;       // [m][nbq] activation block scales
+    const int32_t *qsum;   // [m][nbq] block sums of q
 };
 
 __device__ __forceinline__ float nanmax(float a, float b) {
@@ -284,6 +292,104 @@ size_t tile_lds_bytes(uint32_t kq, uint32_t nbq, int mr, uint32_t cg) {
            (size_t)16 * cg * (nbq + 4) * 2 + (size_t)mr * WV * 8;
 }
 
+// One 4096-depth pass of quantize_row (src/kernels/lowbit/matmul.rs:354-371)
+// over MR rows: thread t holds depths p*4096 + 8t .. +7 of each row in ar[r];
+// q goes to q + r*qstride + depth, the block's s and sum(q) to
+// s[r*nbq + block], sum[r*nbq + block] (sum(q) only for Q1, whose fold uses it).
+// A block's amax and sum(q) reduce over its lanes by DPP / shuffles, and
+// through the LDS words wmax / wsum ([MR][WV]) for blocks longer than 512.
+template <int KIND, int MR>
+__device__ __forceinline__ void quant_pass(const uint4 (&ar)[MR], uint32_t p, int8_t *q, uint32_t qstride,
+                                           float *s, int32_t *sum_out, uint32_t nbq, uint32_t kq,
+                                           uint32_t block_shift, float *wmax, int32_t *wsum) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t block = 1u << block_shift;
+    const uint32_t gl = block / 8 < 64u ? block / 8 : 64u;  // lanes of a block in a wave
+    const uint32_t wpb = block > 512u ? block / 512u : 1u;   // waves of a block
+    const uint32_t d0 = p * QPASS + 8 * t;
+    // |a| as f16 magnitude bits: their unsigned order is the numeric order,
+    // and every NaN pattern sorts above infinity, so an integer max is the
+    // reference's NaN-propagating amax
+    float am[MR];
+#pragma unroll
+    for (int r = 0; r < MR; r++) {
+        const uint32_t w0 = ar[r].x & 0x7FFF7FFFu, w1 = ar[r].y & 0x7FFF7FFFu;
+        const uint32_t w2 = ar[r].z & 0x7FFF7FFFu, w3 = ar[r].w & 0x7FFF7FFFu;
+        const uint32_t lo = max(max(w0 & 0xFFFFu, w1 & 0xFFFFu), max(w2 & 0xFFFFu, w3 & 0xFFFFu));
+        const uint32_t hi = max(max(w0 >> 16, w1 >> 16), max(w2 >> 16, w3 >> 16));
+        am[r] = f16_to_f32((uint16_t)group_max_u32(max(lo, hi), gl));
+    }
+    if (wpb > 1) {  // blocks longer than a wave: combine the waves' maxima
+        if (p > 0) __syncthreads();
+        if (lane == 0)
+#pragma unroll
+            for (int r = 0; r < MR; r++) wmax[r * WV + wave] = am[r];
+        __syncthreads();
+        const uint32_t w0 = (wave / wpb) * wpb;
+#pragma unroll
+        for (int r = 0; r < MR; r++) {
+            float a = 0.0f;
+            for (uint32_t w = 0; w < wpb; w++) a = nanmax(a, wmax[r * WV + w0 + w]);
+            am[r] = a;
+        }
+    }
+    int32_t qs[MR];
+#pragma unroll
+    for (int r = 0; r < MR; r++) {
+        const uint32_t wd[4] = {ar[r].x, ar[r].y, ar[r].z, ar[r].w};
+        const float inv = am[r] > 0.0f ? __fdiv_rn(127.0f, am[r]) : 0.0f;
+        uint32_t qw0 = 0, qw1 = 0;
+        int32_t sum = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float v = rintf(f16_to_f32((uint16_t)(wd[e / 2] >> (16 * (e % 2)))) * inv);
+            const int qi = (v != v) ? 0 : (int)fminf(fmaxf(v, -128.0f), 127.0f);
+            if (e < 4) qw0 |= ((uint32_t)qi & 0xFFu) << (8 * e);
+            else qw1 |= ((uint32_t)qi & 0xFFu) << (8 * (e - 4));
+            sum += qi;
+        }
+        if (d0 < kq) *(uint2 *)(q + r * qstride + d0) = make_uint2(qw0, qw1);
+        qs[r] = KIND == 1 ? group_sum_i32(sum, gl) : 0;
+    }
+    if (KIND == 1 && wpb > 1) {
+        if (lane == 0)
+#pragma unroll
+            for (int r = 0; r < MR; r++) wsum[r * WV + wave] = qs[r];
+        __syncthreads();
+        const uint32_t w0 = (wave / wpb) * wpb;
+#pragma unroll
+        for (int r = 0; r < MR; r++) {
+            int32_t sum = 0;
+            for (uint32_t w = 0; w < wpb; w++) sum += wsum[r * WV + w0 + w];
+            qs[r] = sum;
+        }
+    }
+    if ((uint32_t)lane % gl == 0 && (uint32_t)wave % wpb == 0 && d0 < kq) {
+        const uint32_t bb = d0 >> block_shift;
+#pragma unroll
+        for (int r = 0; r < MR; r++) {
+            s[r * nbq + bb] = __fdiv_rn(am[r], 127.0f);
+            sum_out[r * nbq + bb] = qs[r];
+        }
+    }
+}
+
+// The multi-row single-launch path quantizes A once per call, here, instead of
+// once per workgroup: one workgroup per (4096-depth pass, row) writes q
+// [m][kq] (zero past k) and the blocks' s and sum(q) [m][nbq].
+template <int KIND>
+__global__ void __launch_bounds__(T) lowbit_prequant(const uint16_t *lhs, uint32_t m, uint32_t k,
+                                                     uint32_t kq, uint32_t nbq, uint32_t block_shift,
+                                                     int8_t *q, float *s, int32_t *sum) {
+    __shared__ float wmax[WV];
+    __shared__ int32_t wsum[WV];
+    const uint32_t p = blockIdx.x, r = blockIdx.y;
+    const rsrc_t ar = make_rsrc(lhs, m * k * 2u);
+    const uint4 a[1] = {load_row8(ar, r, m, k, p * QPASS + 8 * threadIdx.x, (k & 7) == 0)};
+    quant_pass<KIND, 1>(a, p, q + (size_t)r * kq, 0, s + (size_t)r * nbq, sum + (size_t)r * nbq, nbq, kq,
+                        block_shift, wmax, wsum);
+}
+
 // SPB: slabs per block when fixed at compile time (2 = blocks of 128, the
 // usual decode format), 0 for any block (runtime block structure).
 template <int KIND, int MR, int NG, int SPB>
@@ -292,6 +398,7 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
     constexpr uint32_t SPG = KIND == 2 ? 4 : 8;  // slabs per code group
     constexpr int NSW = NG * (int)SPG;            // slabs per wave
     constexpr int QP = 2;                         // A passes held in registers (K <= 8192)
+    constexpr int PQ = 4;                         // pre-quantized block entries per thread
     const uint32_t block = 1u << g.block_shift;
     const uint32_t nbq = g.nbq, kq = g.kq;
     const uint32_t cg = 1u << g.cg_shift;         // 16-column groups in this workgroup
@@ -317,14 +424,31 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
     const rsrc_t ar = make_rsrc(g.lhs, g.m * g.k * 2u);
     const bool vec = (g.k & 7) == 0;
 
-    // -- 1. loads: A (waited on first), codes, scales
+    // -- 1. loads: A or its quantized rows (waited on first), codes, scales
     uint4 areg[QP][MR];
-#pragma unroll
-    for (int p = 0; p < QP; p++)
+    uint4 qreg[MR];
+    float pqs[PQ];      // quantized rows' block scales and sums, entries t + T*j
+    int32_t pqsum[PQ];  // (m * nbq <= PQ * T: the host checks)
+    if constexpr (MR > 1) {
+        const rsrc_t qr = make_rsrc(g.q, g.m * kq);
 #pragma unroll
         for (int r = 0; r < MR; r++)
-            areg[p][r] = (uint32_t)p * QPASS < kq ? load_row8(ar, r, g.m, g.k, p * QPASS + 8 * t, vec)
-                                                  : make_uint4(0, 0, 0, 0);
+            qreg[r] = bload16(qr, ((uint32_t)r < g.m && 16u * t < kq) ? r * kq + 16 * t : OOB);
+        const rsrc_t fr = make_rsrc(g.qs, g.m * nbq * 4u), ur = make_rsrc(g.qsum, g.m * nbq * 4u);
+#pragma unroll
+        for (int j = 0; j < PQ; j++) {
+            const uint32_t i = t + T * j;
+            pqs[j] = __uint_as_float(bload4(fr, i < g.m * nbq ? i * 4u : OOB));
+            pqsum[j] = (int32_t)bload4(ur, i < g.m * nbq ? i * 4u : OOB);
+        }
+    } else {
+#pragma unroll
+        for (int p = 0; p < QP; p++)
+#pragma unroll
+            for (int r = 0; r < MR; r++)
+                areg[p][r] = (uint32_t)p * QPASS < kq ? load_row8(ar, r, g.m, g.k, p * QPASS + 8 * t, vec)
+                                                      : make_uint4(0, 0, 0, 0);
+    }
     // scale rows next (waited on before the first barrier), then the
     // epilogue operands, then the codes: vmcnt retires in issue order, so
     // the codes can still be in flight when the waits before them end
@@ -348,77 +472,25 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
         }
     }
 
-    // -- 2. quantize A (quantize_row, src/kernels/lowbit/matmul.rs:354-371)
-    const uint32_t gl = block / 8 < 64u ? block / 8 : 64u;  // lanes of a block in a wave
-    const uint32_t wpb = block > 512u ? block / 512u : 1u;   // waves of a block
+    // -- 2. quantize A (quantize_row, src/kernels/lowbit/matmul.rs:354-371),
+    //       or store the rows quantized beforehand
+    if constexpr (MR > 1) {
 #pragma unroll
-    for (int p = 0; p < QP; p++) {
-        if ((uint32_t)p * QPASS >= kq) break;  // uniform
-        const uint32_t d0 = p * QPASS + 8 * t;
-        // |a| as f16 magnitude bits: their unsigned order is the numeric order,
-        // and every NaN pattern sorts above infinity, so an integer max is the
-        // reference's NaN-propagating amax
-        float am[MR];
+        for (int r = 0; r < MR; r++)
+            if (16u * t < kq) *(uint4 *)(ql + r * qs_ + 16 * t) = qreg[r];
 #pragma unroll
-        for (int r = 0; r < MR; r++) {
-            const uint32_t w0 = areg[p][r].x & 0x7FFF7FFFu, w1 = areg[p][r].y & 0x7FFF7FFFu;
-            const uint32_t w2 = areg[p][r].z & 0x7FFF7FFFu, w3 = areg[p][r].w & 0x7FFF7FFFu;
-            const uint32_t lo = max(max(w0 & 0xFFFFu, w1 & 0xFFFFu), max(w2 & 0xFFFFu, w3 & 0xFFFFu));
-            const uint32_t hi = max(max(w0 >> 16, w1 >> 16), max(w2 >> 16, w3 >> 16));
-            am[r] = f16_to_f32((uint16_t)group_max_u32(max(lo, hi), gl));
-        }
-        if (wpb > 1) {  // blocks longer than a wave: combine the waves' maxima
-            if (p > 0) __syncthreads();
-            if (lane == 0)
-#pragma unroll
-                for (int r = 0; r < MR; r++) wmax[r * WV + wave] = am[r];
-            __syncthreads();
-            const uint32_t w0 = (wave / wpb) * wpb;
-#pragma unroll
-            for (int r = 0; r < MR; r++) {
-                float a = 0.0f;
-                for (uint32_t w = 0; w < wpb; w++) a = nanmax(a, wmax[r * WV + w0 + w]);
-                am[r] = a;
+        for (int j = 0; j < PQ; j++) {
+            const uint32_t i = t + T * j;
+            if (i < MR * nbq) {  // rows m..MR-1 read zeros
+                sa[i] = pqs[j];
+                as[i] = pqsum[j];
             }
         }
-        int32_t qs[MR];
+    } else {
 #pragma unroll
-        for (int r = 0; r < MR; r++) {
-            const uint32_t wd[4] = {areg[p][r].x, areg[p][r].y, areg[p][r].z, areg[p][r].w};
-            const float inv = am[r] > 0.0f ? __fdiv_rn(127.0f, am[r]) : 0.0f;
-            uint32_t qw0 = 0, qw1 = 0;
-            int32_t sum = 0;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float v = rintf(f16_to_f32((uint16_t)(wd[e / 2] >> (16 * (e % 2)))) * inv);
-                const int qi = (v != v) ? 0 : (int)fminf(fmaxf(v, -128.0f), 127.0f);
-                if (e < 4) qw0 |= ((uint32_t)qi & 0xFFu) << (8 * e);
-                else qw1 |= ((uint32_t)qi & 0xFFu) << (8 * (e - 4));
-                sum += qi;
-            }
-            if (d0 < kq) *(uint2 *)(ql + r * qs_ + d0) = make_uint2(qw0, qw1);
-            qs[r] = KIND == 1 ? group_sum_i32(sum, gl) : 0;
-        }
-        if (KIND == 1 && wpb > 1) {
-            if (lane == 0)
-#pragma unroll
-                for (int r = 0; r < MR; r++) wsum[r * WV + wave] = qs[r];
-            __syncthreads();
-            const uint32_t w0 = (wave / wpb) * wpb;
-#pragma unroll
-            for (int r = 0; r < MR; r++) {
-                int32_t sum = 0;
-                for (uint32_t w = 0; w < wpb; w++) sum += wsum[r * WV + w0 + w];
-                qs[r] = sum;
-            }
-        }
-        if ((uint32_t)lane % gl == 0 && (uint32_t)wave % wpb == 0 && d0 < kq) {
-            const uint32_t bb = d0 >> g.block_shift;
-#pragma unroll
-            for (int r = 0; r < MR; r++) {
-                sa[r * nbq + bb] = __fdiv_rn(am[r], 127.0f);
-                as[r * nbq + bb] = qs[r];
-            }
+        for (int p = 0; p < QP; p++) {
+            if ((uint32_t)p * QPASS >= kq) break;  // uniform
+            quant_pass<KIND, MR>(areg[p], p, ql, qs_, sa, as, nbq, kq, g.block_shift, wmax, wsum);
         }
     }
     if ((uint32_t)t < 2 * cg * nbq) {  // transpose: scale of (block bb, column 8 piece + e)
@@ -699,9 +771,9 @@ struct TileGeo {
     int ng;
     uint32_t kq, nbq, cg_shift;
 };
-// Column groups per workgroup: enough that the grid is about one workgroup
-// per CU (the per-workgroup quantization of A and the fold are then paid once
-// per CU); a wave's K range grows with them.
+// Column groups per workgroup (CG): enough that the grid stays within a few
+// workgroups per CU (the per-workgroup staging of A and the fold are then paid
+// a few times per CU); a wave's K range grows with them.
 TileGeo tile_geometry_cg(const WDev &w, size_t m, uint32_t cg_shift) {
     TileGeo sg = {false, 0, 0, 0, cg_shift};
     const int mr = m <= 1 ? 1 : m <= 4 ? 4 : 8;  // the row counts the kernel is built for
@@ -721,6 +793,7 @@ TileGeo tile_geometry_cg(const WDev &w, size_t m, uint32_t cg_shift) {
     const size_t cg = (size_t)1 << cg_shift;
     if (2 * cg * nbq > (size_t)T || tile_lds_bytes((uint32_t)kq, (uint32_t)nbq, mr, (uint32_t)cg) > 96 * 1024)
         return sg;
+    if (mr > 1 && (size_t)mr * nbq > (size_t)4 * T) return sg;  // pre-quantized entries per thread (PQ)
     sg.ok = true;
     sg.ng = ng;
     sg.kq = (uint32_t)kq;
@@ -731,9 +804,9 @@ TileGeo tile_geometry(const WDev &w, size_t m) {
     TileGeo none = {false, 0, 0, 0, 0};
     if (m < 1 || m > 8 || w.block > QPASS || w.block < 16) return none;
     const size_t tiles16 = w.n_pad / 16;
-    // one row: up to ~3 workgroups per CU (their quantization of A is one
-    // row's worth); more rows: about one per CU (measured on MI355X)
-    const size_t most = m == 1 ? 768 : 256;
+    // up to ~3 workgroups per CU (measured on MI355X; the rows of a multi-row
+    // call are quantized once, before the launch)
+    const size_t most = 768;
     uint32_t want = 0;
     while (want < 2 && (tiles16 >> want) > most) want++;
     for (int cs = (int)want; cs >= 0; cs--) {
@@ -743,10 +816,14 @@ TileGeo tile_geometry(const WDev &w, size_t m) {
     return none;
 }
 
+// Bytes of the pre-quantized rows (q [m][kq], then s and sum(q) [m][nbq]).
+size_t prequant_bytes(size_t m, size_t kq, size_t nbq) { return (m * kq + 255) / 256 * 256 + m * nbq * 8; }
+
 }  // namespace
 
 size_t lowbit_scratch_bytes(const WDev &w, size_t m) {
-    if (tile_geometry(w, m).ok) return 0;
+    const TileGeo sg = tile_geometry(w, m);
+    if (sg.ok) return m > 1 ? prequant_bytes(m, sg.kq, sg.nbq) : 0;
     const Geo ge = geometry(w, m);
     return (m * ge.kq + 255) / 256 * 256 + m * ge.nbq * 8;
 }
@@ -777,6 +854,20 @@ hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint
         f.codes_bytes = (uint32_t)cb;
         f.cg_shift = sg.cg_shift;
         const int mr = m <= 1 ? 1 : m <= 4 ? 4 : 8;
+        if (m > 1) {
+            f.q = (const int8_t *)scratch;
+            f.qs = (const float *)((uint8_t *)scratch + (m * sg.kq + 255) / 256 * 256);
+            f.qsum = (const int32_t *)(f.qs + m * sg.nbq);
+            const dim3 grid((sg.kq + QPASS - 1) / QPASS, (uint32_t)m);
+            if (w.kind == W_Q2)
+                hipLaunchKernelGGL(lowbit_prequant<2>, grid, dim3(T), 0, s, lhs, f.m, f.k, f.kq, f.nbq,
+                                   f.block_shift, (int8_t *)f.q, (float *)f.qs, (int32_t *)f.qsum);
+            else
+                hipLaunchKernelGGL(lowbit_prequant<1>, grid, dim3(T), 0, s, lhs, f.m, f.k, f.kq, f.nbq,
+                                   f.block_shift, (int8_t *)f.q, (float *)f.qs, (int32_t *)f.qsum);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
         if (w.kind == W_Q2) return launch_tile<2>(f, ep, mr, sg.ng, s);
         return launch_tile<1>(f, ep, mr, sg.ng, s);
     }
