@@ -19,10 +19,10 @@
 // Everything a step needs goes global -> LDS by DMA (global_load_lds, no
 // registers): the 128 x 64 activation tile (16-byte chunks swizzled: chunk c of
 // row r at slot c ^ (r & 7), so fragment reads are conflict-free), the tile's
-// raw Q4 chunks and its scales (and mins). A ring of five stages: the DMA for
-// step k+4 is issued while step k multiplies, each step's barrier waits only
-// for step k+2's DMA, and a wave reads step k+1's fragments from LDS while its
-// step-k multiplies run.
+// raw Q4 chunks and its scales (and mins). A ring of five stages: step k+5's
+// DMA is issued as soon as step k's stage is free (after step k's barrier),
+// each step's barrier waits only for step k+2's DMA, and a wave reads step
+// k+1's fragments from LDS while its step-k multiplies run.
 #include "kernels.h"
 #include "tile_store.cuh"
 
@@ -167,24 +167,118 @@ __device__ __forceinline__ void read_half(uint32_t sb, const ReadOff &o, Half &h
     }
 }
 
+// One column tile's 8 MFMAs (row tiles i = 0..7, B operand b) with the next
+// column tile's dequant interleaved, in a fixed order: two vector instructions
+// between MFMAs keep the matrix core fed (the compiler's own schedule clusters
+// them). The dequant is q4_deq8 / q4_deq8_affine: v_bfi_b32 puts each biased
+// nibble under an f16 exponent (magic 0x6400 | u = 1024 + u; 0x5400 | u << 4 =
+// 64 + u), a packed add of -1032 / -72 leaves the exact code, then one packed
+// multiply by the scale pair s2 (Q4_0) or one packed fma with the min pair m2
+// (Q4_1) rounds the weight once. nb must not be read by an MFMA for two wait
+// states after its last write: each group ends with s_nop 1. nb was last read
+// by the MFMAs three groups earlier (four rotating buffers).
 template <bool AFFINE>
-__device__ __forceinline__ void mma_half(const Half &h, float4_t (&acc)[8][4], uint32_t mag_lo,
-                                         uint32_t mag_hi) {
+__device__ __forceinline__ void mma8_deq(float4_t &c0, float4_t &c1, float4_t &c2, float4_t &c3, float4_t &c4,
+                                         float4_t &c5, float4_t &c6, float4_t &c7, const u32x4_t (&a)[8],
+                                         const u32x4_t &b, u32x4_t &nb, uint32_t q, uint32_t s2, uint32_t m2,
+                                         uint32_t mag_lo, uint32_t mag_hi) {
+    uint32_t t;
+    if (AFFINE) {
+        asm volatile(
+            "v_mfma_f32_16x16x32_f16 %[c0], %[a0], %[b], %[c0]\n\t"
+            "v_lshrrev_b32 %[t], 8, %[q]\n\t"
+            "v_bfi_b32 %[n0], %[m1], %[q], %[ml]\n\t"
+            "v_mfma_f32_16x16x32_f16 %[c1], %[a1], %[b], %[c1]\n\t"
+            "v_bfi_b32 %[n1], %[m2m], %[q], %[mh]\n\t"
+            "v_bfi_b32 %[n2], %[m1], %[t], %[ml]\n\t"
+            "v_mfma_f32_16x16x32_f16 %[c2], %[a2], %[b], %[c2]\n\t"
+            "v_bfi_b32 %[n3], %[m2m], %[t], %[mh]\n\t"
+            "v_pk_add_f16 %[n0], %[n0], %[ol]\n\t"
+            "v_mfma_f32_16x16x32_f16 %[c3], %[a3], %[b], %[c3]\n\t"
+            "v_pk_add_f16 %[n1], %[n1], %[oh]\n\t"
+            "v_pk_add_f16 %[n2], %[n2], %[ol]\n\t"
+            "v_mfma_f32_16x16x32_f16 %[c4], %[a4], %[b], %[c4]\n\t"
+            "v_pk_add_f16 %[n3], %[n3], %[oh]\n\t"
+            "v_pk_fma_f16 %[n0], %[n0], %[s2], %[mn]\n\t"
+            "v_mfma_f32_16x16x32_f16 %[c5], %[a5], %[b], %[c5]\n\t"
+            "v_pk_fma_f16 %[n1], %[n1], %[s2], %[mn]\n\t"
+            "v_mfma_f32_16x16x32_f16 %[c6], %[a6], %[b], %[c6]\n\t"
+            "v_pk_fma_f16 %[n2], %[n2], %[s2], %[mn]\n\t"
+            "v_mfma_f32_16x16x32_f16 %[c7], %[a7], %[b], %[c7]\n\t"
+            "v_pk_fma_f16 %[n3], %[n3], %[s2], %[mn]\n\t"
+            "s_nop 1"
+            : [c0] "+v"(c0), [c1] "+v"(c1), [c2] "+v"(c2), [c3] "+v"(c3), [c4] "+v"(c4), [c5] "+v"(c5),
+              [c6] "+v"(c6), [c7] "+v"(c7), [n0] "=&v"(nb.x), [n1] "=&v"(nb.y), [n2] "=&v"(nb.z),
+              [n3] "=&v"(nb.w), [t] "=&v"(t)
+            : [a0] "v"(a[0]), [a1] "v"(a[1]), [a2] "v"(a[2]), [a3] "v"(a[3]), [a4] "v"(a[4]), [a5] "v"(a[5]),
+              [a6] "v"(a[6]), [a7] "v"(a[7]), [b] "v"(b), [q] "v"(q), [s2] "v"(s2), [mn] "v"(m2),
+              [ml] "v"(mag_lo), [mh] "v"(mag_hi), [m1] "s"(0x000F000Fu), [m2m] "s"(0x00F000F0u),
+              [ol] "s"(0xE408E408u), [oh] "s"(0xD480D480u));
+    } else {
+        (void)m2;
+        asm volatile(
+            "v_mfma_f32_16x16x32_f16 %[c0], %[a0], %[b], %[c0]\n\t"
+            "v_lshrrev_b32 %[t], 8, %[q]\n\t"
+            "v_bfi_b32 %[n0], %[m1], %[q], %[ml]\n\t"
+            "v_mfma_f32_16x16x32_f16 %[c1], %[a1], %[b], %[c1]\n\t"
+            "v_bfi_b32 %[n1], %[m2m], %[q], %[mh]\n\t"
+            "v_bfi_b32 %[n2], %[m1], %[t], %[ml]\n\t"
+            "v_mfma_f32_16x16x32_f16 %[c2], %[a2], %[b], %[c2]\n\t"
+            "v_bfi_b32 %[n3], %[m2m], %[t], %[mh]\n\t"
+            "v_pk_add_f16 %[n0], %[n0], %[ol]\n\t"
+            "v_mfma_f32_16x16x32_f16 %[c3], %[a3], %[b], %[c3]\n\t"
+            "v_pk_add_f16 %[n1], %[n1], %[oh]\n\t"
+            "v_pk_add_f16 %[n2], %[n2], %[ol]\n\t"
+            "v_mfma_f32_16x16x32_f16 %[c4], %[a4], %[b], %[c4]\n\t"
+            "v_pk_add_f16 %[n3], %[n3], %[oh]\n\t"
+            "v_pk_mul_f16 %[n0], %[n0], %[s2]\n\t"
+            "v_mfma_f32_16x16x32_f16 %[c5], %[a5], %[b], %[c5]\n\t"
+            "v_pk_mul_f16 %[n1], %[n1], %[s2]\n\t"
+            "v_mfma_f32_16x16x32_f16 %[c6], %[a6], %[b], %[c6]\n\t"
+            "v_pk_mul_f16 %[n2], %[n2], %[s2]\n\t"
+            "v_mfma_f32_16x16x32_f16 %[c7], %[a7], %[b], %[c7]\n\t"
+            "v_pk_mul_f16 %[n3], %[n3], %[s2]\n\t"
+            "s_nop 1"
+            : [c0] "+v"(c0), [c1] "+v"(c1), [c2] "+v"(c2), [c3] "+v"(c3), [c4] "+v"(c4), [c5] "+v"(c5),
+              [c6] "+v"(c6), [c7] "+v"(c7), [n0] "=&v"(nb.x), [n1] "=&v"(nb.y), [n2] "=&v"(nb.z),
+              [n3] "=&v"(nb.w), [t] "=&v"(t)
+            : [a0] "v"(a[0]), [a1] "v"(a[1]), [a2] "v"(a[2]), [a3] "v"(a[3]), [a4] "v"(a[4]), [a5] "v"(a[5]),
+              [a6] "v"(a[6]), [a7] "v"(a[7]), [b] "v"(b), [q] "v"(q), [s2] "v"(s2), [ml] "v"(mag_lo),
+              [mh] "v"(mag_hi), [m1] "s"(0x000F000Fu), [m2m] "s"(0x00F000F0u), [ol] "s"(0xE408E408u),
+              [oh] "s"(0xD480D480u));
+    }
+}
+
+__device__ __forceinline__ uint32_t pair16(uint32_t h) { return (h & 0xFFFFu) | (h << 16); }
+
+// The first column tile's B operand of a step (plain code, before the groups).
+template <bool AFFINE>
+__device__ __forceinline__ u32x4_t deq_first(const Half &h, uint32_t mag_lo, uint32_t mag_hi) {
+    const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)h.s[0]);
+    const half2_t s2 = {s, s};
+    uint4 b;
+    if (AFFINE) {
+        const _Float16 mv = __builtin_bit_cast(_Float16, (uint16_t)h.mn[0]);
+        b = q4_deq8_affine(h.q[0], s2, (half2_t){mv, mv}, mag_lo, mag_hi);
+    } else {
+        b = q4_deq8(h.q[0], s2, mag_lo, mag_hi);
+    }
+    return (u32x4_t){b.x, b.y, b.z, b.w};
+}
+
+// A step's 32 MFMAs: column tile jt multiplies B operand bb[jt] (dequantized
+// during the previous group) and dequantizes bb[jt+1] -- for the last tile,
+// the next step's first (raw operands in nxt).
+template <bool AFFINE>
+__device__ __forceinline__ void mma_step(const Half &cur, const Half &nxt, float4_t (&acc)[8][4],
+                                         u32x4_t (&bb)[4], uint32_t mag_lo, uint32_t mag_hi) {
 #pragma unroll
     for (int jt = 0; jt < 4; jt++) {
-        const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)h.s[jt]);
-        const half2_t s2 = {s, s};
-        uint4 b;
-        if (AFFINE) {
-            const _Float16 mv = __builtin_bit_cast(_Float16, (uint16_t)h.mn[jt]);
-            b = q4_deq8_affine(h.q[jt], s2, (half2_t){mv, mv}, mag_lo, mag_hi);
-        } else {
-            b = q4_deq8(h.q[jt], s2, mag_lo, mag_hi);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            acc[i][jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, h.a[i]),
-                                                                __builtin_bit_cast(half8_t, b), acc[i][jt], 0, 0, 0);
+        const Half &src = jt < 3 ? cur : nxt;
+        const int nj = (jt + 1) % 4;
+        mma8_deq<AFFINE>(acc[0][jt], acc[1][jt], acc[2][jt], acc[3][jt], acc[4][jt], acc[5][jt], acc[6][jt],
+                         acc[7][jt], cur.a, bb[jt], bb[nj], src.q[nj], pair16(src.s[nj]),
+                         AFFINE ? pair16(src.mn[nj]) : 0u, mag_lo, mag_hi);
     }
 }
 
@@ -231,29 +325,31 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
     asm volatile("" : "+v"(mag_lo), "+v"(mag_hi));
 
 #pragma unroll
-    for (int j = 0; j < NSTAGE - 1; j++) dma_step(g, d, ring + j * STAGE_BYTES, min((uint32_t)j, last), wave);
-    wait_vm<(NSTAGE - 3) * PS>();  // steps 0 and 1 landed
+    for (int j = 0; j < NSTAGE; j++) dma_step(g, d, ring + j * STAGE_BYTES, min((uint32_t)j, last), wave);
+    wait_vm<(NSTAGE - 2) * PS>();  // steps 0 and 1 landed
     barrier_lds();
 
     // Step ks: step ks+1's fragments are read (its stage was published by the
     // barrier ending step ks-1) while step ks multiplies; then step ks+2's
-    // DMA is waited for and the barrier publishes it (and frees stage
-    // (ks+4)%5, last read during step ks-2), and step ks+4's DMA is issued into
-    // that stage. Steps past the end re-load the last step into the free stage
-    // and read a stage nobody multiplies.
+    // DMA is waited for and the barrier publishes it -- and frees stage ks%5,
+    // whose fragments every wave has multiplied -- and step ks+5's DMA is
+    // issued into that stage. Steps past the end re-load the last step into a
+    // free stage and read a stage nobody multiplies.
     const uint32_t ring0 = lds_addr(ring);
     const ReadOff ro = read_offsets(kh, cw, lane);
+    u32x4_t bb[4];  // B operands of the four column tiles, rotating
     auto step = [&](uint32_t ks, const Half &cur, Half &nxt) {
         uint32_t sb = ring0 + ((ks + 1) % NSTAGE) * STAGE_BYTES;
         asm volatile("" : "+s"(sb));  // opaque: one base add per operand kind, constant offsets after
         read_half<AFFINE>(sb, ro, nxt);
-        mma_half<AFFINE>(cur, acc, mag_lo, mag_hi);
-        wait_vm<PS>();
+        mma_step<AFFINE>(cur, nxt, acc, bb, mag_lo, mag_hi);
+        wait_vm<(NSTAGE - 3) * PS>();
         barrier_lds();
-        dma_step(g, d, ring + ((ks + NSTAGE - 1) % NSTAGE) * STAGE_BYTES, min(ks + NSTAGE - 1, last), wave);
+        dma_step(g, d, ring + (ks % NSTAGE) * STAGE_BYTES, min(ks + NSTAGE, last), wave);
     };
     Half h0, h1;
     read_half<AFFINE>(ring0, ro, h0);
+    bb[0] = deq_first<AFFINE>(h0, mag_lo, mag_hi);
     uint32_t ks = 0;
     for (; ks + 2 <= ksteps; ks += 2) {
         step(ks, h0, h1);
