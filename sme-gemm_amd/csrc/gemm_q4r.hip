@@ -39,7 +39,6 @@ constexpr int CS = RBN + 8;                     // halfs per staged output row
 constexpr int NSTAGE = 5;                       // LDS ring depth
 constexpr int PS = 4;                           // DMA instructions per lane per step
 static_assert(RBM * CS * 2 <= NSTAGE * STAGE_BYTES, "store staging exceeds the ring");
-static_assert(4 * 4096 * 4 <= NSTAGE * STAGE_BYTES, "partial-tile exchange exceeds the ring");
 
 struct RArgs {
     const uint16_t *lhs;
@@ -249,6 +248,11 @@ __device__ __forceinline__ void mma8_deq(float4_t &c0, float4_t &c1, float4_t &c
     }
 }
 
+template <int N>
+struct IntC {
+    static constexpr int value = N;
+};
+
 __device__ __forceinline__ uint32_t pair16(uint32_t h) { return (h & 0xFFFFu) | (h << 16); }
 
 // The first column tile's B operand of a step (plain code, before the groups).
@@ -359,48 +363,47 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
     wait_vm<0>();
     __syncthreads();
 
-    // The pair's partial tiles: wave w+4 hands its f32 tile to wave w through
-    // LDS (64 rows at a time; lane-contiguous, so conflict-free), wave w adds.
-    float *red = (float *)ring + cw * 4096;
-#pragma unroll
-    for (int r = 0; r < 2; r++) {
-        if (kh == 1) {
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int jt = 0; jt < 4; jt++)
-#pragma unroll
-                    for (int v = 0; v < 4; v++) red[((i * 4 + jt) * 4 + v) * 64 + lane] = acc[4 * r + i][jt][v];
-        }
-        __syncthreads();
-        if (kh == 0) {
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int jt = 0; jt < 4; jt++)
-#pragma unroll
-                    for (int v = 0; v < 4; v++) acc[4 * r + i][jt][v] += red[((i * 4 + jt) * 4 + v) * 64 + lane];
-        }
-        __syncthreads();
-    }
+    float *colv = epv, *rowv = epv + SMG_MAX_EP_NODES * RBN;
+    // the op-graph's vectors first: their global loads overlap the exchange
+    ep_load_vectors<false, RBM, RBN, RNT>(g.st, ep, colv, rowv, row0, col0);
 
-    // Store: beta*acc rounded to f16 into LDS ([128][CS]; a lane holds
-    // D[4*(lane/16)+v][lane%16] of each 16x16 tile), then groups of 8 columns
-    // through the op-graph by all eight waves.
+    // The pair's partial tiles: each wave hands the other the half of its f32
+    // tile that the other finishes (wave w keeps row tiles 0-3, wave w+4 row
+    // tiles 4-7) through LDS, 16 bytes per lane and lane-contiguous
+    // (conflict-free). f32 addition commutes, so either wave's sum is the same
+    // value. Then each wave rounds beta * sum to f16 into the staged tile
+    // ([128][CS]; a lane holds D[4*(lane/16)+v][lane%16] of each 16x16 tile).
     uint16_t *stg = (uint16_t *)ring;
-    if (kh == 0) {
+    auto finish_half = [&](auto keep_c) {
+        constexpr int KEEP = decltype(keep_c)::value, GIVE = 4 - KEEP;
+        float4_t *mine = (float4_t *)ring + wave * 1024;  // 16 KB per wave
+        const float4_t *other = (const float4_t *)ring + ((wave + 4) % 8) * 1024;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int jt = 0; jt < 4; jt++) mine[(i * 4 + jt) * 64 + lane] = acc[GIVE + i][jt];
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int jt = 0; jt < 4; jt++) acc[KEEP + i][jt] += other[(i * 4 + jt) * 64 + lane];
+        __syncthreads();  // the staged tile overwrites the exchange
         const int lr = lane % 16, lg = lane / 16;
 #pragma unroll
-        for (int i = 0; i < 8; i++)
+        for (int i = KEEP; i < KEEP + 4; i++)
 #pragma unroll
             for (int jt = 0; jt < 4; jt++)
 #pragma unroll
                 for (int v = 0; v < 4; v++)
                     stg[(i * 16 + lg * 4 + v) * CS + cw * 64 + jt * 16 + lr] = from_f32<false>(0.0f + g.beta * acc[i][jt][v]);
-    }
-    float *colv = epv, *rowv = epv + SMG_MAX_EP_NODES * RBN;
-    ep_load_vectors<false, RBM, RBN, RNT>(g.st, ep, colv, rowv, row0, col0);
+    };
+    static_assert(8 * 1024 * sizeof(float4_t) <= NSTAGE * STAGE_BYTES, "exchange exceeds the ring");
+    if (kh == 0)
+        finish_half(IntC<0>{});
+    else
+        finish_half(IntC<4>{});
     __syncthreads();
+    // Store: groups of 8 columns through the op-graph by all eight waves.
     // thread t: column group t % 32, rows t / 32 + 16 j
     static_assert(RNT % (RBN / 8) == 0, "each thread keeps one column group");
     ep_store_rows<false, RBM, RBN, RBM * (RBN / 8) / RNT>(g.st, ep, colv, rowv, stg, CS, t / (RBN / 8),
