@@ -126,18 +126,26 @@ __device__ __forceinline__ void ep_store_rows(const StoreArgs &g, const EpArgs &
             const EpNode &nd = ep.nodes[q];
             const uint32_t cls = ep.cls[q], fam = ep.fam[q];
             if (fam == EPF_ACT) {
-                // the logistic kinds inline over all R x 8 cells (no call);
-                // the rest one call per row
-                if (nd.aux == 3 || nd.aux == 5 || nd.aux == 2) {
-                    const uint32_t kind = nd.aux;
+                // the logistic kinds inline over all R x 8 cells (no call),
+                // one loop per kind (as act_f32_fast: silu x*L(x), sigmoid
+                // L(x), tanh-gelu x*L(2u)); the rest one call per row
+                if (nd.aux == 3) {
+#pragma unroll
+                    for (int j = 0; j < R; j++)
+#pragma unroll
+                        for (int e = 0; e < 8; e++) x[j].v[e] = mul_logistic(x[j].v[e], x[j].v[e]);
+                } else if (nd.aux == 5) {
+#pragma unroll
+                    for (int j = 0; j < R; j++)
+#pragma unroll
+                        for (int e = 0; e < 8; e++) x[j].v[e] = mul_logistic(1.0f, x[j].v[e]);
+                } else if (nd.aux == 2) {
 #pragma unroll
                     for (int j = 0; j < R; j++)
 #pragma unroll
                         for (int e = 0; e < 8; e++) {
                             const float v = x[j].v[e];
-                            // act_f32_fast: silu x*L(x), sigmoid L(x), tanh-gelu x*L(2u)
-                            const float y = kind == 2 ? 2.0f * 0.7978845608028654f * (v + 0.044715f * v * v * v) : v;
-                            x[j].v[e] = mul_logistic(kind == 5 ? 1.0f : v, y);
+                            x[j].v[e] = mul_logistic(v, 2.0f * 0.7978845608028654f * (v + 0.044715f * v * v * v));
                         }
                 } else {
 #pragma unroll
