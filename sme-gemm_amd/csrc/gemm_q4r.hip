@@ -291,123 +291,133 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
     __shared__ __align__(16) uint8_t ring[NSTAGE * STAGE_BYTES];
     __shared__ __align__(16) float epv[SMG_MAX_EP_NODES * (RBN + RBM)];
 
-    // column-tile-major order: consecutive workgroups share a weight tile
     const uint32_t mtiles = (g.m + RBM - 1) / RBM;
-    const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
-    const uint32_t tm = tile % mtiles, tn = tile / mtiles;
-    const uint32_t row0 = tm * RBM, col0 = tn * RBN;
     const int t = threadIdx.x, lane = t % 64;
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);  // uniform: DMA bases, branches
     const int cw = wave % 4, kh = wave / 4;  // column block, half of each step
+    const uint32_t ksteps = g.k / 64;       // >= 1
 
-    // Rows past m and columns past n_pad read clamped (valid) addresses; their
-    // results are never stored.
-    DmaSrc d;
-    {
-        const uint32_t c = (t % 8) ^ ((t / 8) % 8);  // source chunk of slot t%8 in row t/8 (+64q)
-#pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const uint32_t row = min(row0 + q * 64 + t / 8, g.m - 1);
-            d.a[q] = (uint32_t)(((size_t)row * g.lhs_rs + c * 8) * 2);
-        }
-        d.b = min(col0 + t % 256, g.n_pad - 1) * 16;
-        d.s = min(col0 + 2 * (t % 128), g.n_pad - 2) * 2;
-        d.half_b = wave / 4;
-        d.half_s = (wave % 4) / 2;
-        d.src_s = (AFFINE && wave >= 4) ? g.mn : g.sc;
-    }
-    const uint32_t ksteps = g.k / 64;  // >= 1
-    const uint32_t last = ksteps - 1;
-
-    float4_t acc[8][4];
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-#pragma unroll
-        for (int jt = 0; jt < 4; jt++) acc[i][jt] = (float4_t){0.f, 0.f, 0.f, 0.f};
     // the bfi magics live in VGPRs (a VOP3 takes one scalar operand)
     uint32_t mag_lo = 0x64006400u, mag_hi = 0x54005400u;
     asm volatile("" : "+v"(mag_lo), "+v"(mag_hi));
-
-#pragma unroll
-    for (int j = 0; j < NSTAGE; j++) dma_step(g, d, ring + j * STAGE_BYTES, min((uint32_t)j, last), wave);
-    wait_vm<(NSTAGE - 2) * PS>();  // steps 0 and 1 landed
-    barrier_lds();
-
-    // Step ks: step ks+1's fragments are read (its stage was published by the
-    // barrier ending step ks-1) while step ks multiplies; then step ks+2's
-    // DMA is waited for and the barrier publishes it -- and frees stage ks%5,
-    // whose fragments every wave has multiplied -- and step ks+5's DMA is
-    // issued into that stage. Steps past the end re-load the last step into a
-    // free stage and read a stage nobody multiplies.
     const uint32_t ring0 = lds_addr(ring);
     const ReadOff ro = read_offsets(kh, cw, lane);
-    u32x4_t bb[4];  // B operands of the four column tiles, rotating
-    auto step = [&](uint32_t ks, const Half &cur, Half &nxt) {
-        uint32_t sb = ring0 + ((ks + 1) % NSTAGE) * STAGE_BYTES;
-        asm volatile("" : "+s"(sb));  // opaque: one base add per operand kind, constant offsets after
-        read_half<AFFINE>(sb, ro, nxt);
-        mma_step<AFFINE>(cur, nxt, acc, bb, mag_lo, mag_hi);
-        wait_vm<(NSTAGE - 3) * PS>();
+
+    // The tile's K loop, the pair's sum and the store. (Written as a lambda
+    // that the kernel calls once: in this form the compiler keeps the
+    // per-lane read offsets as immediates of paired ds_read2st64 reads instead
+    // of adding a base register per read.)
+    auto run_tile = [&](uint32_t tile) __attribute__((always_inline)) {
+        // column-tile-major order
+        const uint32_t tm = tile % mtiles, tn = tile / mtiles;
+        const uint32_t row0 = tm * RBM, col0 = tn * RBN;
+
+        // Rows past m and columns past n_pad read clamped (valid) addresses;
+        // their results are never stored.
+        DmaSrc d;
+        {
+            const uint32_t c = (t % 8) ^ ((t / 8) % 8);  // source chunk of slot t%8 in row t/8 (+64q)
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const uint32_t row = min(row0 + q * 64 + t / 8, g.m - 1);
+                d.a[q] = (uint32_t)(((size_t)row * g.lhs_rs + c * 8) * 2);
+            }
+            d.b = min(col0 + t % 256, g.n_pad - 1) * 16;
+            d.s = min(col0 + 2 * (t % 128), g.n_pad - 2) * 2;
+            d.half_b = wave / 4;
+            d.half_s = (wave % 4) / 2;
+            d.src_s = (AFFINE && wave >= 4) ? g.mn : g.sc;
+        }
+        const uint32_t last = ksteps - 1;
+
+        float4_t acc[8][4];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int jt = 0; jt < 4; jt++) acc[i][jt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+        for (int j = 0; j < NSTAGE; j++) dma_step(g, d, ring + j * STAGE_BYTES, min((uint32_t)j, last), wave);
+        wait_vm<(NSTAGE - 2) * PS>();  // steps 0 and 1 landed
         barrier_lds();
-        dma_step(g, d, ring + (ks % NSTAGE) * STAGE_BYTES, min(ks + NSTAGE, last), wave);
-    };
-    Half h0, h1;
-    read_half<AFFINE>(ring0, ro, h0);
-    bb[0] = deq_first<AFFINE>(h0, mag_lo, mag_hi);
-    uint32_t ks = 0;
-    for (; ks + 2 <= ksteps; ks += 2) {
-        step(ks, h0, h1);
-        step(ks + 1, h1, h0);
-    }
-    if (ks < ksteps) step(ks, h0, h1);
-    wait_vm<0>();
-    __syncthreads();
 
-    float *colv = epv, *rowv = epv + SMG_MAX_EP_NODES * RBN;
-    // the op-graph's vectors first: their global loads overlap the exchange
-    ep_load_vectors<false, RBM, RBN, RNT>(g.st, ep, colv, rowv, row0, col0);
-
-    // The pair's partial tiles: each wave hands the other the half of its f32
-    // tile that the other finishes (wave w keeps row tiles 0-3, wave w+4 row
-    // tiles 4-7) through LDS, 16 bytes per lane and lane-contiguous
-    // (conflict-free). f32 addition commutes, so either wave's sum is the same
-    // value. Then each wave rounds beta * sum to f16 into the staged tile
-    // ([128][CS]; a lane holds D[4*(lane/16)+v][lane%16] of each 16x16 tile).
-    uint16_t *stg = (uint16_t *)ring;
-    auto finish_half = [&](auto keep_c) {
-        constexpr int KEEP = decltype(keep_c)::value, GIVE = 4 - KEEP;
-        float4_t *mine = (float4_t *)ring + wave * 1024;  // 16 KB per wave
-        const float4_t *other = (const float4_t *)ring + ((wave + 4) % 8) * 1024;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int jt = 0; jt < 4; jt++) mine[(i * 4 + jt) * 64 + lane] = acc[GIVE + i][jt];
+        // Step ks: step ks+1's fragments are read (its stage was published by
+        // the barrier ending step ks-1) while step ks multiplies; then step
+        // ks+2's DMA is waited for and the barrier publishes it -- and frees
+        // stage ks%5, whose fragments every wave has multiplied -- and step
+        // ks+5's DMA is issued into that stage. Steps past the end re-load the
+        // last step into a free stage and read a stage nobody multiplies.
+        u32x4_t bb[4];  // B operands of the four column tiles, rotating
+        auto step = [&](uint32_t ks, const Half &cur, Half &nxt) {
+            uint32_t sb = ring0 + ((ks + 1) % NSTAGE) * STAGE_BYTES;
+            asm volatile("" : "+s"(sb));  // opaque: one base add per operand kind, constant offsets after
+            read_half<AFFINE>(sb, ro, nxt);
+            mma_step<AFFINE>(cur, nxt, acc, bb, mag_lo, mag_hi);
+            wait_vm<(NSTAGE - 3) * PS>();
+            barrier_lds();
+            dma_step(g, d, ring + (ks % NSTAGE) * STAGE_BYTES, min(ks + NSTAGE, last), wave);
+        };
+        Half h0, h1;
+        read_half<AFFINE>(ring0, ro, h0);
+        bb[0] = deq_first<AFFINE>(h0, mag_lo, mag_hi);
+        uint32_t ks = 0;
+        for (; ks + 2 <= ksteps; ks += 2) {
+            step(ks, h0, h1);
+            step(ks + 1, h1, h0);
+        }
+        if (ks < ksteps) step(ks, h0, h1);
+        wait_vm<0>();
         __syncthreads();
+
+        float *colv = epv, *rowv = epv + SMG_MAX_EP_NODES * RBN;
+        // the op-graph's vectors first: their global loads overlap the exchange
+        ep_load_vectors<false, RBM, RBN, RNT>(g.st, ep, colv, rowv, row0, col0);
+
+        // The pair's partial tiles: each wave hands the other the half of its
+        // f32 tile that the other finishes (wave w keeps row tiles 0-3, wave
+        // w+4 row tiles 4-7) through LDS, 16 bytes per lane and
+        // lane-contiguous (conflict-free). f32 addition commutes, so either
+        // wave's sum is the same value. Then each wave rounds beta * sum to f16
+        // into the staged tile ([128][CS]; a lane holds
+        // D[4*(lane/16)+v][lane%16] of each 16x16 tile).
+        uint16_t *stg = (uint16_t *)ring;
+        auto finish_half = [&](auto keep_c) {
+            constexpr int KEEP = decltype(keep_c)::value, GIVE = 4 - KEEP;
+            float4_t *mine = (float4_t *)ring + wave * 1024;  // 16 KB per wave
+            const float4_t *other = (const float4_t *)ring + ((wave + 4) % 8) * 1024;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+            for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int jt = 0; jt < 4; jt++) acc[KEEP + i][jt] += other[(i * 4 + jt) * 64 + lane];
-        __syncthreads();  // the staged tile overwrites the exchange
-        const int lr = lane % 16, lg = lane / 16;
+                for (int jt = 0; jt < 4; jt++) mine[(i * 4 + jt) * 64 + lane] = acc[GIVE + i][jt];
+            __syncthreads();
 #pragma unroll
-        for (int i = KEEP; i < KEEP + 4; i++)
+            for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int jt = 0; jt < 4; jt++)
+                for (int jt = 0; jt < 4; jt++) acc[KEEP + i][jt] += other[(i * 4 + jt) * 64 + lane];
+            __syncthreads();  // the staged tile overwrites the exchange
+            const int lr = lane % 16, lg = lane / 16;
 #pragma unroll
-                for (int v = 0; v < 4; v++)
-                    stg[(i * 16 + lg * 4 + v) * CS + cw * 64 + jt * 16 + lr] = from_f32<false>(0.0f + g.beta * acc[i][jt][v]);
+            for (int i = KEEP; i < KEEP + 4; i++)
+#pragma unroll
+                for (int jt = 0; jt < 4; jt++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        stg[(i * 16 + lg * 4 + v) * CS + cw * 64 + jt * 16 + lr] =
+                            from_f32<false>(0.0f + g.beta * acc[i][jt][v]);
+        };
+        static_assert(8 * 1024 * sizeof(float4_t) <= NSTAGE * STAGE_BYTES, "exchange exceeds the ring");
+        if (kh == 0)
+            finish_half(IntC<0>{});
+        else
+            finish_half(IntC<4>{});
+        __syncthreads();
+        // Store: groups of 8 columns through the op-graph by all eight waves.
+        // thread t: column group t % 32, rows t / 32 + 16 j
+        static_assert(RNT % (RBN / 8) == 0, "each thread keeps one column group");
+        ep_store_rows<false, RBM, RBN, RBM * (RBN / 8) / RNT>(g.st, ep, colv, rowv, stg, CS, t / (RBN / 8),
+                                                              RNT / (RBN / 8), (t % (RBN / 8)) * 8, row0, col0);
     };
-    static_assert(8 * 1024 * sizeof(float4_t) <= NSTAGE * STAGE_BYTES, "exchange exceeds the ring");
-    if (kh == 0)
-        finish_half(IntC<0>{});
-    else
-        finish_half(IntC<4>{});
-    __syncthreads();
-    // Store: groups of 8 columns through the op-graph by all eight waves.
-    // thread t: column group t % 32, rows t / 32 + 16 j
-    static_assert(RNT % (RBN / 8) == 0, "each thread keeps one column group");
-    ep_store_rows<false, RBM, RBN, RBM * (RBN / 8) / RNT>(g.st, ep, colv, rowv, stg, CS, t / (RBN / 8),
-                                                          RNT / (RBN / 8), (t % (RBN / 8)) * 8, row0, col0);
+    run_tile(xcd_tile(blockIdx.x, gridDim.x));  // consecutive workgroups share a weight tile
 }
 
 }  // namespace

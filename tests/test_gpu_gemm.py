@@ -162,7 +162,9 @@ def test_q4_dequant_eager_matches_oracle_bits(smg, orc):
 @pytest.mark.parametrize("m,n,k,block,affine", [
     (9, 256, 64, 32, False), (40, 300, 128, 64, True), (129, 520, 320, 32, False),
     (200, 1000, 512, 128, True), (256, 768, 1024, 32, False), (17, 129, 192, 64, False),
-    (512, 512, 4096, 32, False), (130, 384, 256, 256, True)])
+    (512, 512, 4096, 32, False), (130, 384, 256, 256, True),
+    # 128-240 tiles (about one per CU) with short K
+    (512, 8192, 256, 32, False), (640, 8192, 512, 64, True), (136, 30720, 128, 32, False)])
 def test_q4_register_weight_gemm(smg, orc, m, n, k, block, affine):
     """The Q4 f16 prefill kernel that dequantizes weights in registers (K a
     multiple of 64, block >= 32; two waves split each 64-depth step and add
@@ -184,3 +186,23 @@ def test_q4_register_weight_gemm(smg, orc, m, n, k, block, affine):
     d = np.zeros(m * n, np.uint16)
     smg.Gemm(a, packed, m).run(d)
     assert max_rel(c, d) <= f16_tol(k)
+
+
+def test_q4_register_weight_gemm_epilogue_repeat(smg, orc):
+    """The prefill configuration's op-graph (mul_col, add_col, silu) on a grid
+    of about one tile per CU, twice in a row into fresh outputs, within
+    tolerance of the oracle both times."""
+    m, n, k = 512, 8192, 256
+    rng = np.random.default_rng(7)
+    quants = rng.integers(0, 256, k * n // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.002, 0.02, n * (k // 32)).astype(np.float32))
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    sc = orc.f32_to_f16(rng.uniform(0.5, 1.5, n).astype(np.float32))
+    bias = orc.f32_to_f16((0.1 * rng.standard_normal(n)).astype(np.float32))
+    w = smg.Q4Weights.with_params(quants, scales, None, n, k, smg.Q4Params(32))
+    want = orc.matmul_q4_ep(a, quants, scales, None, m, n, k, 32,
+                            [(5, 0, 0.0, sc, 0), (4, 0, 0.0, bias, 0)], 3)
+    for _ in range(2):
+        c = np.zeros(m * n, np.uint16)
+        smg.matmul_q4_ep(a, w, c, m, smg.Epilogue().mul_col(sc).add_col(bias).silu())
+        assert max_rel(c, want) <= f16_tol(k)
