@@ -211,6 +211,33 @@ __device__ __forceinline__ float act_f32(uint32_t kind, float x, float alpha) {
     return (float)act_f64(kind, (double)x, (double)alpha);
 }
 
+// A trailing activation's 16-bit result, to16(f32(f64 formula)), as
+// from_f32<BF16>(act_f32(...)) gives it, with a fast path for the logistic
+// kinds (silu 3, sigmoid 5): y = x or 1 times 1 / (1 + 2^t), t = -x*log2(e)
+// carried as t_hi + t_lo (an fma recovers the product's rounding, a second term
+// the constant's), on v_exp_f32 / v_rcp_f32 (1 ulp each): y is within about 4
+// f32 ulps of the f64 formula, so if y scaled by 1 -+ 2^-19 (16 ulps) rounds
+// to the same 16-bit value, the f64 formula's f32 value -- inside that
+// interval -- rounds to it too (rounding is monotone). Otherwise, and for
+// non-finite values, the f64 path decides.
+template <bool BF16>
+__device__ __forceinline__ uint16_t act_round16(uint32_t kind, float x, float alpha) {
+    if (kind == 3 || kind == 5) {
+        constexpr float L_HI = 1.44269502162933349609375f;       // log2(e) rounded to f32
+        constexpr float L_LO = 1.925962991e-08f;                 // log2(e) - L_HI
+        const float t_hi = -x * L_HI;
+        const float t_lo = __builtin_fmaf(-x, L_HI, -t_hi) + -x * L_LO;
+        const float e = __builtin_amdgcn_exp2f(t_hi) * (1.0f + t_lo * 0.693147180559945309f);
+        const float y = (kind == 3 ? x : 1.0f) * __builtin_amdgcn_rcpf(1.0f + e);
+        if (__builtin_isfinite(x) && __builtin_isfinite(y)) {
+            const float d = __builtin_fabsf(y) * 0x1p-19f;
+            const uint16_t lo = from_f32<BF16>(y - d), hi = from_f32<BF16>(y + d);
+            if (lo == hi) return lo;
+        }
+    }
+    return from_f32<BF16>(act_f32(kind, x, alpha));
+}
+
 // Eight cells at once (GEMM stores): one call per 8 cells, the kind switch
 // taken once and each case's f64 formula inlined for a constant kind.
 struct F8 {
@@ -372,7 +399,7 @@ __device__ __forceinline__ float ep_arith(uint32_t fam, float x, float v) {
 // node's ld is 0. Nodes apply in order (the trailing activation is the last
 // node, as resolve_nodes appends it: src/exec/scalar.rs:28-53).
 template <bool BF16>
-__device__ float ep_cell(const EpArgs &ep, float x, size_t i, size_t j, size_t n) {
+__device__ uint16_t ep_cell(const EpArgs &ep, float x, size_t i, size_t j, size_t n) {
     for (uint32_t t = 0; t < ep.n_nodes; t++) {
         const EpNode &nd = ep.nodes[t];
         const uint16_t *p = (const uint16_t *)nd.ptr;
@@ -383,9 +410,10 @@ __device__ float ep_cell(const EpArgs &ep, float x, size_t i, size_t j, size_t n
         case EPC_TENSOR: v = to_f32<BF16>(p[i * (nd.ld == 0 ? n : nd.ld) + j]); break;
         default: break;
         }
+        if (ep.fam[t] == EPF_ACT && t + 1 == ep.n_nodes) return act_round16<BF16>(nd.aux, x, nd.scalar);
         x = ep.fam[t] == EPF_ACT ? act_f32(nd.aux, x, nd.scalar) : ep_arith(ep.fam[t], x, v);
     }
-    return x;
+    return from_f32<BF16>(x);
 }
 
 // Operands of the first EP_PRE nodes of one cell, loaded ahead of time (raw
@@ -426,6 +454,7 @@ __device__ __forceinline__ uint16_t finish_pre(const EpArgs &ep, const EpPre &pr
         if ((uint32_t)q < ep.n_nodes) {
             const EpNode &nd = ep.nodes[q];
             const float v = ep.cls[q] == EPC_SCALAR ? nd.scalar : to_f32<BF16>((uint16_t)pre.raw[q]);
+            if (ep.fam[q] == EPF_ACT && (uint32_t)q + 1 == ep.n_nodes) return act_round16<BF16>(nd.aux, x, nd.scalar);
             x = ep.fam[q] == EPF_ACT ? act_f32(nd.aux, x, nd.scalar) : ep_arith(ep.fam[q], x, v);
         }
     }
@@ -439,6 +468,7 @@ __device__ __forceinline__ uint16_t finish_pre(const EpArgs &ep, const EpPre &pr
         case EPC_TENSOR: v = to_f32<BF16>(p[i * (nd.ld == 0 ? n : nd.ld) + j]); break;
         default: break;
         }
+        if (ep.fam[q] == EPF_ACT && q + 1 == ep.n_nodes) return act_round16<BF16>(nd.aux, x, nd.scalar);
         x = ep.fam[q] == EPF_ACT ? act_f32(nd.aux, x, nd.scalar) : ep_arith(ep.fam[q], x, v);
     }
     return from_f32<BF16>(x);
@@ -452,7 +482,7 @@ __device__ __forceinline__ uint16_t finish(const EpArgs &ep, float acc, size_t i
                                            size_t n) {
     uint16_t c = from_f32<BF16>(acc);
     if (ep.n_nodes == 0) return c;
-    return from_f32<BF16>(ep_cell<BF16>(ep, to_f32<BF16>(c), i, j, n));
+    return ep_cell<BF16>(ep, to_f32<BF16>(c), i, j, n);
 }
 
 // ---------------------------------------------------------------------------

@@ -101,6 +101,28 @@ def test_config3_q1_add_col_silu(smg, orc):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("act", ["silu", "sigmoid"])
+def test_logistic_epilogue_bitwise_wide_range(smg, orc, act):
+    """A trailing silu / sigmoid over 32768 outputs whose pre-activation values
+    span -30..30 (bias added first): bit-identical to the reference's f64
+    formula rounded to f32 then f16, including where the stores take their
+    fast f32 path."""
+    m, n, k = 8, 4096, 256
+    rng = np.random.default_rng(99 + len(act))
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    codes = rng.integers(0, 256, (k * n + 3) // 4, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.01, 0.05, n * (k // 128)).astype(np.float32))
+    bias = orc.f32_to_f16(rng.uniform(-30.0, 30.0, n).astype(np.float32))
+    w = smg.Q2Weights(codes, scales, n, k, smg.Q2Params(128))
+    got = np.zeros(m * n, np.uint16)
+    ep = smg.Epilogue().add_col(bias)
+    ep = ep.silu() if act == "silu" else ep.sigmoid()
+    smg.matmul_q2_ep(a, w, got, m, ep)
+    want = orc.matmul_lowbit_ep(2, a, codes, scales, m, n, k, 128, [(4, 0, 0.0, bias, 0)],
+                                3 if act == "silu" else 5)
+    assert np.array_equal(got, want)
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 200, 300), (4, 1536, 512), (13, 70, 64)])
 def test_fused_epilogue_is_plain_then_applied(smg, orc, m, n, k):
     """q2.rs:83-108: bias, row scale and trailing gelu == plain product then the
