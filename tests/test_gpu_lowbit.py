@@ -331,3 +331,50 @@ def test_q1_interleave_rejects_mismatch(smg):
     b = smg.Q1Weights.quantize(w, 0, 32, 64, 64)
     with pytest.raises(smg.SmeGemmError, match="same shape"):
         smg.Q1Weights.interleave(a, b)
+
+
+def test_multi_row_calls_in_a_replayed_graph(smg, orc):
+    """Multi-row calls (A quantized once per call into the thread's staging
+    buffer, then the tile launch): three calls captured in a HIP graph after
+    eager warm-up, the graph replayed three times with eager calls between
+    replays, every replay bit-identical to the eager results and to the
+    reference."""
+    import torch
+    n, k, block = 2048, 1024, 128
+    rng = np.random.default_rng(5)
+    codes = rng.integers(0, 256, (k * n + 3) // 4, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.01, 0.05, n * (k // block)).astype(np.float32))
+    w = smg.Q2Weights(codes, scales, n, k, smg.Q2Params(block))
+    to_dev = lambda x: torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).cuda()
+    cases = []
+    for m in (8, 4, 2):
+        a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+        want = orc.matmul_lowbit_ep(2, a, codes, scales, m, n, k, block)
+        cases.append((m, to_dev(a), torch.zeros(m * n, dtype=torch.int16, device="cuda"), want))
+    for m, ad, cd, want in cases:  # eager (also sizes the staging buffer before capture)
+        smg.matmul_q2(ad, w, cd, m)
+    torch.cuda.synchronize()
+    for m, ad, cd, want in cases:
+        assert np.array_equal(cd.cpu().numpy().view(np.uint16), want), f"eager m={m}"
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for m, ad, cd, want in cases:  # warm the capture stream too
+            smg.matmul_q2(ad, w, cd, m)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=side):
+            for m, ad, cd, want in cases:
+                smg.matmul_q2(ad, w, cd, m)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for m, ad, cd, want in cases:
+            cd.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for m, ad, cd, want in cases:
+            assert np.array_equal(cd.cpu().numpy().view(np.uint16), want), f"replay {rep} m={m}"
+        for m, ad, cd, want in cases:  # eager work between replays
+            smg.matmul_q2(ad, w, cd, m)
+        torch.cuda.synchronize()
