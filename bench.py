@@ -113,7 +113,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(N-sharding is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "(the calls are independent per weight matrix; sharding N across GPUs "
+              "is left to the caller); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

@@ -23,7 +23,8 @@
  *
  * Weights live on the device behind an opaque handle (the "prepack"): the
  * reference keeps them in Q4Weights / Q2Weights / Q1Weights / Packed<f16>,
- * and a Rust binding keeps the handle there.
+ * and a Rust binding keeps the handle in those types (it owns one and calls
+ * smg_weights_destroy when they drop).
  */
 #ifndef SMEGEMM_GPU_H
 #define SMEGEMM_GPU_H
