@@ -97,25 +97,34 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
         for (int r = 0; r < MR; r++) *(uint4 *)(a_lds + r * MF_SEG + 8 * t) = areg[r];
         __syncthreads();
         // dequant + MFMA: A operand = 16 columns x 32 depths of weights, B
-        // operand = 32 depths x 16 rows of activations (rows >= m are zero)
+        // operand = 32 depths x 16 rows of activations (rows >= m are zero).
+        // All of this wave's activation fragments are read first, from a valid
+        // row (branch-free, then selected), so the LDS round trips overlap
+        // instead of each one preceding its MFMA.
         const int row = c;  // B-operand lane: activation row lane%16
+        const bool row_live = row < MR;
+        const uint16_t *arow = a_lds + (row_live ? row : 0) * MF_SEG;
+        uint4 abv[MF_U][4];
 #pragma unroll
         for (int u = 0; u < MF_U; u++) {
             const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
-            const bool live = kc < g.nchunks;
+            const bool live = row_live && kc < g.nchunks;
+            const uint32_t kcl = kc < g.nchunks ? kc - sc0 : 0;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const uint4 v = *(const uint4 *)(arow + kcl * Q4_CHUNK + w * 8);
+                abv[u][w] = live ? v : make_uint4(0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < MF_U; u++) {
             const half2_t s2 = {__builtin_bit_cast(_Float16, sv[u]), __builtin_bit_cast(_Float16, sv[u])};
             const uint32_t words[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
-            const uint32_t kcl = live ? kc - sc0 : 0;
 #pragma unroll
             for (int w = 0; w < 4; w++) {
                 uint4 wa = q4_deq8(words[w], s2, mag_lo, mag_hi);
-                uint4 ab = make_uint4(0, 0, 0, 0);
-                if (row < MR) {
-                    const uint4 v = *(const uint4 *)(a_lds + row * MF_SEG + kcl * Q4_CHUNK + w * 8);
-                    ab = live ? v : make_uint4(0, 0, 0, 0);
-                }
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wa),
-                                                             __builtin_bit_cast(half8_t, ab), acc,
+                                                             __builtin_bit_cast(half8_t, abv[u][w]), acc,
                                                              0, 0, 0);
             }
         }
