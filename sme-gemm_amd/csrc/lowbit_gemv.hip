@@ -522,23 +522,31 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
         }
         return wa;
     };
+    // q fragments: read from a valid row for every lane, then selected
+    // (branch-free, so a group's reads are issued together and overlap
+    // instead of each one preceding its MFMA)
     auto qload = [&](int i) {
         const uint32_t slab = kw * NSW + i;
-        const uint4 qb = c < MR ? *(const uint4 *)(ql + c * qs_ + slab * LB_SLAB + 16 * gq4)
-                                : make_uint4(0, 0, 0, 0);
-        return __builtin_bit_cast(int4_t, qb);
+        const uint4 qb = *(const uint4 *)(ql + (c < MR ? c : 0) * qs_ + slab * LB_SLAB + 16 * gq4);
+        return __builtin_bit_cast(int4_t, c < MR ? qb : make_uint4(0, 0, 0, 0));
     };
+    constexpr int PF = NSW < 8 ? NSW : 8;  // slabs whose q is read ahead at once
     if constexpr (SPB > 0) {
         // blocks of SPB slabs, whole inside this wave's range; independent
         // accumulators, written after the last product
         constexpr int NBW = NSW / SPB;
         int4_t acc[NBW];
 #pragma unroll
-        for (int b = 0; b < NBW; b++) {
-            acc[b] = (int4_t){0, 0, 0, 0};
+        for (int b = 0; b < NBW; b++) acc[b] = (int4_t){0, 0, 0, 0};
 #pragma unroll
-            for (int u = 0; u < SPB; u++)
-                acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(b * SPB + u), qload(b * SPB + u), acc[b], 0, 0, 0);
+        for (int i0 = 0; i0 < NSW; i0 += PF) {
+            int4_t qv[PF];
+#pragma unroll
+            for (int j = 0; j < PF; j++) qv[j] = qload(i0 + j);
+#pragma unroll
+            for (int j = 0; j < PF; j++)
+                acc[(i0 + j) / SPB] =
+                    __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(i0 + j), qv[j], acc[(i0 + j) / SPB], 0, 0, 0);
         }
         if (c < MR) {
 #pragma unroll
@@ -554,10 +562,15 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
         const uint32_t parts = block < (uint32_t)LB_SLAB ? LB_SLAB / block : 1;
         const uint32_t spb = block > (uint32_t)LB_SLAB ? block / LB_SLAB : 1;  // slabs per block
         int4_t acc = {0, 0, 0, 0};
+        int4_t qv[PF];
 #pragma unroll
         for (int i = 0; i < NSW; i++) {
+            if (i % PF == 0) {
+#pragma unroll
+                for (int j = 0; j < PF; j++) qv[j] = qload(i + j);
+            }
             const uint32_t slab = kw * NSW + i;
-            const int4_t wa = expand(i), ab = qload(i);
+            const int4_t wa = expand(i), ab = qv[i % PF];
             if (parts == 1) {
                 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa, ab, acc, 0, 0, 0);
                 if ((slab + 1) % spb == 0) {  // uniform: the block ends in this wave
