@@ -204,10 +204,34 @@ int gemm_gpu_b16b16_run_packed(size_t m, size_t n, size_t k, uint16_t *dst, long
 /* Whether an m-row Q4 call runs the GEMV kernel (replaces
  * gemm_sme_f16f16_q4_single, csrc/sme_gemm_api.h:107). */
 int gemm_gpu_f16f16_q4_single(size_t m, size_t n, size_t k);
+/* One link of a chain (q4_chained, src/kernels/q4/matmul.rs:116-164); replaces
+ * gemm_sme_f16f16_q4_chained (csrc/sme_gemm_api.h:102-105). done / ready are
+ * the reference's std::atomic<size_t> words (either NULL), written and read by
+ * other host threads: the call reads A only once *ready (acquire) covers all
+ * k depths, computes as gemm_gpu_f16f16_q4 (the whole op-graph in the kernel,
+ * the same bits), and raises *done (release) to n once C is stored. */
+int gemm_gpu_f16f16_q4_chained(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                               const ep_desc16 *ep, size_t *done, const size_t *ready);
 
 /* ---- device-pointer entry points (asynchronous on `stream`) --------------- */
 int smg_q4_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
                       const ep_desc16 *ep, int bf16, void *stream);
+/* The chained link between kernels on the device (the GPU form of
+ * gemm_sme_f16f16_q4_chained, csrc/sme_gemm_api.h:102-105, for the decode
+ * GEMV: f16, scale-only Q4, block >= 32, k > 0, 1 <= m <= 8; SMG_EINVAL
+ * otherwise). ready / done are device words (either NULL) counting depths of A
+ * and columns of C: each workgroup first issues its weight loads, then waits
+ * until *ready covers the 4096-depth segment of A it reads next, and once
+ * every workgroup has stored its columns the last one raises *done to n
+ * (release; all columns form one pass). A producer kernel on another stream
+ * raises *ready with a release store. sync: two device words, zero before
+ * the first call; sync[0] is zero again after each call, sync[1] becomes 1 if
+ * a wait lasted wait_us (0: 100 ms) without *ready covering its segment, and
+ * then *done is not raised and the columns of the workgroups that timed out
+ * are not stored. Chains that run at once each need their own sync words. */
+int smg_q4_chained_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                       const ep_desc16 *ep, unsigned long long *done, const unsigned long long *ready,
+                       unsigned int *sync, unsigned int wait_us, void *stream);
 int smg_lowbit_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
                           const ep_desc16 *ep, void *stream);
 int smg_lowbit_mopa_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,

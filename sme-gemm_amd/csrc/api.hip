@@ -12,6 +12,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "kernels.h"
@@ -752,6 +753,21 @@ int gemm_gpu_b16b16_run_packed(size_t m, size_t n, size_t k, uint16_t *dst, long
                        beta_bits, ep);
 }
 
+// The reference's chained link (csrc/gemm_f16f16_q4.h:541-549) with host
+// progress words: all of A's depths are awaited first, as its MOPA route does
+// (:531-533), then the call runs as gemm_gpu_f16f16_q4 (the same bits, the
+// whole op-graph in the kernel) and *done is raised to n once C is stored.
+int gemm_gpu_f16f16_q4_chained(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                               const ep_desc16 *ep, size_t *done, const size_t *ready) {
+    int rc = check_kind(w, W_Q4);
+    if (rc) return rc;
+    if (ready && m != 0 && w->d.n != 0)
+        while (__atomic_load_n(ready, __ATOMIC_ACQUIRE) < w->d.k) std::this_thread::yield();
+    rc = q4_host(m, w, dst, lhs, ep, false);
+    if (rc == SMG_OK && done) __atomic_store_n(done, w->d.n, __ATOMIC_RELEASE);
+    return rc;
+}
+
 int gemm_gpu_f16f16_q4_single(size_t m, size_t n, size_t k) {
     (void)n;
     (void)k;
@@ -769,6 +785,30 @@ int smg_q4_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint1
     if ((rc = ep_args(ep, &ea))) return rc;
     hipError_t e = run_q4(w->d, m, dst, lhs, ea, bf16 != 0, (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_q4_matmul_dev", e);
+}
+
+int smg_q4_chained_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
+                       const ep_desc16 *ep, unsigned long long *done, const unsigned long long *ready,
+                       unsigned int *sync, unsigned int wait_us, void *stream) {
+    int rc = check_kind(w, W_Q4);
+    if (rc) return rc;
+    if (m == 0 || w->d.n == 0) return fail(SMG_EINVAL, "smg_q4_chained_dev: empty call");
+    if (done && !sync) return fail(SMG_EINVAL, "smg_q4_chained_dev: done needs the sync words");
+    EpArgs ea;
+    if ((rc = ep_args(ep, &ea))) return rc;
+    // the device wall clock's rate (kHz), read once per device
+    static std::atomic<int> clock_khz[64];
+    int khz = w->device < 64 ? clock_khz[w->device].load(std::memory_order_relaxed) : 0;
+    if (khz <= 0) {
+        HIP_TRY(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, w->device), SMG_EHIP);
+        if (w->device < 64) clock_khz[w->device].store(khz, std::memory_order_relaxed);
+    }
+    const unsigned long long us = wait_us ? wait_us : 100000u;
+    ChainArgs ch = {ready, done, sync, us * (unsigned long long)(khz > 0 ? khz : 100000) / 1000u, w->d.n};
+    hipError_t e = launch_q4_gemv_chained(w->d, m, dst, lhs, ea, ch, (hipStream_t)stream);
+    if (e == hipErrorNotSupported)
+        return fail(SMG_EINVAL, "smg_q4_chained_dev: needs f16 scale-only Q4, block >= 32, k > 0, m <= 8");
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_q4_chained_dev", e);
 }
 
 int smg_lowbit_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,

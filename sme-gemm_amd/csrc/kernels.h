@@ -31,6 +31,26 @@ constexpr size_t Q4_GEMV_MAX_ROWS = 8;
 hipError_t launch_q4_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
                           const EpArgs &ep, bool bf16, hipStream_t s);
 
+// Progress words of a chained GEMV (device memory). Before each 4096-depth
+// segment of A a workgroup waits, at most wait_ticks of the device wall clock,
+// until *ready covers the segment; once every workgroup has stored its
+// columns, the last one raises *done to done_value. sync[0] counts finished
+// workgroups (zero before the call, zero again after it); sync[1] is set to 1
+// when a wait timed out, and then *done is not raised.
+struct ChainArgs {
+    const unsigned long long *ready;  // or null: A complete at launch
+    unsigned long long *done;         // or null
+    unsigned int *sync;               // [2], needed when done is set
+    unsigned long long wait_ticks;
+    unsigned long long done_value;
+};
+
+// The chained form of launch_q4_gemv for the MFMA GEMV's domain (f16,
+// scale-only, block >= 32, k > 0, m <= Q4_GEMV_MAX_ROWS); hipErrorNotSupported
+// outside it.
+hipError_t launch_q4_gemv_chained(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
+                                  const EpArgs &ep, const ChainArgs &ch, hipStream_t s);
+
 // Low-bit int8 path. scratch: device buffer of lowbit_scratch_bytes() bytes
 // (only used when the block is too large to quantize in-kernel).
 size_t lowbit_scratch_bytes(const WDev &w, size_t m);

@@ -52,8 +52,26 @@ constexpr int MF_U = 4;                      // steps (4 chunks each) in flight 
 constexpr int MF_SEG = 4096;                 // depths of A staged in LDS at a time
 constexpr int MF_SEG_CH = MF_SEG / Q4_CHUNK; // 128 chunks per segment
 
-template <int MR>  // rows staged per segment (1, 2, 4, 8)
-__global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpArgs ep) {
+// One wait of a chained call (thread 0 of the workgroup): polls *ready until it
+// reaches need or the device wall clock has advanced `ticks` (and at most 2^24
+// polls), then an agent-scope acquire, so the producer's stores of A below
+// need are visible to the loads that follow the workgroup barrier.
+__device__ __forceinline__ bool chain_wait(const unsigned long long *ready, unsigned long long need,
+                                           unsigned long long ticks) {
+    const unsigned long long t0 = wall_clock64();
+    for (uint32_t it = 0; it < (1u << 24); it++) {
+        if (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= need) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            return true;
+        }
+        if (wall_clock64() - t0 > ticks) break;
+        __builtin_amdgcn_s_sleep(4);
+    }
+    return false;
+}
+
+template <int MR, bool CHAIN>  // rows staged per segment (1, 2, 4, 8); chained call
+__global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpArgs ep, ChainArgs ch) {
     extern __shared__ __align__(16) uint8_t smem[];
     uint16_t *a_lds = (uint16_t *)smem;          // [MR][MF_SEG]
     float *red = (float *)smem;                   // reused: [MF_WAVES][16 cols][MR]
@@ -68,6 +86,7 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
     const uint32_t mag_hi = __builtin_amdgcn_readfirstlane(0x54005400u) | (uint32_t)(t >> 30);
 
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    bool timed_out = false;  // chained: a wait for A expired (uniform)
     const uint32_t last = g.nchunks - 1;  // nchunks >= 1 here
     const uint32_t nseg = (g.nchunks + MF_SEG_CH - 1) / MF_SEG_CH;
     for (uint32_t seg = 0; seg < nseg; seg++) {
@@ -78,8 +97,10 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
         const rsrc_t ar = make_rsrc(g.lhs, g.m * g.k * 2u);
         const bool vec = (g.k & 7) == 0;
         uint4 areg[MR];  // row r, depths d0 + 8t .. +8 (MF_SEG / 8 == 512 threads)
+        if constexpr (!CHAIN) {
 #pragma unroll
-        for (int r = 0; r < MR; r++) areg[r] = load_row8(ar, r, g.m, g.k, d0 + 8 * t, vec);
+            for (int r = 0; r < MR; r++) areg[r] = load_row8(ar, r, g.m, g.k, d0 + 8 * t, vec);
+        }
         // steps of this wave within the segment: chunks sc0 + 4*(wave + 8*u) + grp
         uint4 wq[MF_U];
         uint16_t sv[MF_U];
@@ -90,6 +111,24 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
             wq[u] = *(const uint4 *)(g.nib + ((size_t)kcc * g.n_pad + col) * 16);
             const uint16_t sl = g.sc[(size_t)((kcc * Q4_CHUNK) >> g.block_shift) * g.n_pad + col];
             sv[u] = kc < g.nchunks ? sl : (uint16_t)0;  // a dead step's weights become 0
+        }
+        if constexpr (CHAIN) {
+            // the weights stream in while the producer of A finishes; A's
+            // segment is read only once *ready covers it
+            if (ch.ready) {
+                __shared__ uint32_t seg_ok;
+                if (t == 0) {
+                    const uint32_t need = g.k < d0 + MF_SEG ? g.k : d0 + MF_SEG;
+                    seg_ok = chain_wait(ch.ready, need, ch.wait_ticks) ? 1u : 0u;
+                }
+                __syncthreads();
+                if (!seg_ok) {
+                    timed_out = true;
+                    break;
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < MR; r++) areg[r] = load_row8(ar, r, g.m, g.k, d0 + 8 * t, vec);
         }
         // stage A[:, segment] (rows < m, zero past k)
         __syncthreads();
@@ -142,7 +181,28 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
 #pragma unroll
         for (int w = 0; w < MF_WAVES; w++) total = total + red[(w * 16 + cc) * MR + r];
         const uint32_t j = tile * 16 + cc;
-        if (r < (int)g.m && j < g.n) g.dst[(size_t)r * g.n + j] = finish<false>(ep, total, r, j, g.n);
+        if (!timed_out && r < (int)g.m && j < g.n) g.dst[(size_t)r * g.n + j] = finish<false>(ep, total, r, j, g.n);
+    }
+    if constexpr (CHAIN) {
+        if (ch.done) {
+            // one count per workgroup, a release that writes wave 0's stores
+            // back (a wave's release waits for all of its own stores); a
+            // second storing wave (8 rows) writes its own back first. The
+            // last workgroup to count publishes.
+            if (t >= 64 && t < 16 * MR) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            __syncthreads();
+            if (t == 0) {
+                if (timed_out) __hip_atomic_store(ch.sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint32_t prev =
+                    __hip_atomic_fetch_add(ch.sync, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                if (prev == gridDim.x - 1) {
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+                    const bool bad = __hip_atomic_load(ch.sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+                    __hip_atomic_store(ch.sync, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (!bad) __hip_atomic_store(ch.done, ch.done_value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
     }
 }
 
@@ -314,19 +374,16 @@ hipError_t launch_variant(const Q4GemvArgs &g, const EpArgs &ep, bool bf16, bool
     return launch_generic<M, true, true>(g, ep, s);
 }
 
-template <int MR>
-hipError_t launch_mfma(const Q4GemvArgs &g, const EpArgs &ep, hipStream_t s) {
+template <int MR, bool CHAIN = false>
+hipError_t launch_mfma(const Q4GemvArgs &g, const EpArgs &ep, hipStream_t s, const ChainArgs &ch = {}) {
     size_t lds = (size_t)MR * MF_SEG * 2;
     const size_t red = (size_t)MF_WAVES * 16 * MR * 4;
     if (red > lds) lds = red;
-    hipLaunchKernelGGL((q4_gemv_mfma<MR>), dim3(g.n_pad / 16), dim3(MF_WAVES * 64), lds, s, g, ep);
+    hipLaunchKernelGGL((q4_gemv_mfma<MR, CHAIN>), dim3(g.n_pad / 16), dim3(MF_WAVES * 64), lds, s, g, ep, ch);
     return hipGetLastError();
 }
 
-}  // namespace
-
-hipError_t launch_q4_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
-                          const EpArgs &ep, bool bf16, hipStream_t s) {
+Q4GemvArgs gemv_args(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs) {
     Q4GemvArgs g;
     g.nib = w.codes;
     g.sc = w.scales;
@@ -339,6 +396,14 @@ hipError_t launch_q4_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t
     g.nchunks = (uint32_t)w.nchunks;
     g.m = (uint32_t)m;
     g.block_shift = (uint32_t)__builtin_ctzll(w.block);
+    return g;
+}
+
+}  // namespace
+
+hipError_t launch_q4_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
+                          const EpArgs &ep, bool bf16, hipStream_t s) {
+    const Q4GemvArgs g = gemv_args(w, m, dst, lhs);
     const bool affine = w.mins != nullptr;
     if ((size_t)m * w.k * 2 >= ((size_t)1 << 31)) return hipErrorInvalidValue;  // buffer range
     if (w.nchunks == 0) {
@@ -357,6 +422,18 @@ hipError_t launch_q4_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t
     if (m <= 2) return launch_variant<2>(g, ep, bf16, affine, s);
     if (m <= 4) return launch_variant<4>(g, ep, bf16, affine, s);
     return launch_variant<8>(g, ep, bf16, affine, s);
+}
+
+hipError_t launch_q4_gemv_chained(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
+                                  const EpArgs &ep, const ChainArgs &ch, hipStream_t s) {
+    if (m < 1 || m > Q4_GEMV_MAX_ROWS || w.mins != nullptr || w.block < (size_t)Q4_CHUNK || w.nchunks == 0)
+        return hipErrorNotSupported;
+    if ((size_t)m * w.k * 2 >= ((size_t)1 << 31)) return hipErrorInvalidValue;  // buffer range
+    const Q4GemvArgs g = gemv_args(w, m, dst, lhs);
+    if (m <= 1) return launch_mfma<1, true>(g, ep, s, ch);
+    if (m <= 2) return launch_mfma<2, true>(g, ep, s, ch);
+    if (m <= 4) return launch_mfma<4, true>(g, ep, s, ch);
+    return launch_mfma<8, true>(g, ep, s, ch);
 }
 
 }  // namespace smg

@@ -88,6 +88,8 @@ def lib() -> C.CDLL:
                                      C.c_long, P, C.c_uint16, C.c_uint16, P]
     L.gemm_gpu_f16f16_q4_single.argtypes = [SZ, SZ, SZ]
     L.smg_q4_matmul_dev.argtypes = [SZ, P, P, P, P, C.c_int, P]
+    L.gemm_gpu_f16f16_q4_chained.argtypes = [SZ, P, P, P, P, P, P]
+    L.smg_q4_chained_dev.argtypes = [SZ, P, P, P, P, P, P, P, C.c_uint, P]
     L.smg_lowbit_matmul_dev.argtypes = [SZ, P, P, P, P, P]
     L.smg_lowbit_mopa_dev.argtypes = [SZ, P, P, P, P, P]
     L.smg_packed_matmul_dev.argtypes = [SZ, P, P, C.c_long, C.c_long, P, C.c_long, C.c_long,
@@ -678,6 +680,45 @@ def matmul_q4_ep(a, w: Q4Weights, c, m: int, ep: Epilogue):
     """src/kernels/q4/matmul.rs:21."""
     return _run_host_or_dev("gemm_gpu_f16f16_q4", lambda *x: lib().smg_q4_matmul_dev(*x[:5], 0, x[5]),
                             a, w, c, m, ep)
+
+
+def q4_chained(a, w: Q4Weights, c, ep: Epilogue | None = None, done=None, ready=None, *, m: int = 1,
+               sync=None, wait_us: int = 0) -> bool:
+    """One row of matmul_q4_ep as a link of a chain (src/kernels/q4/matmul.rs:116-164).
+
+    Host arrays: ``done`` / ``ready`` are ``ctypes.c_size_t`` words shared with
+    other threads (either None); A is read once ``ready`` covers all k depths,
+    and ``done`` is raised to n once C is stored. Device tensors: ``done`` /
+    ``ready`` are one-element int64 device tensors, raised and awaited by
+    kernels (a producer on another stream stores ``ready``), and ``sync`` is a
+    two-element int32 device tensor, zero before the first call (element 1
+    becomes 1 when a wait of ``wait_us`` microseconds, 0 for 100 ms, expired).
+    Returns False, with ``done`` not raised, when the kernel failed, as the
+    reference does; the reason is in ``last_error()``.
+    """
+    ep = ep or Epilogue()
+    n, k = w.n(), w.k()
+    if _is_dev(a):
+        if not _is_dev(c) or a.numel() != m * k or c.numel() != m * n:
+            raise ValueError("a is m*k and c is m*n, both device tensors")
+        ep.validate(m, n)
+        eptr, keep = _ep_ptr(ep, n)
+        ptr = lambda x: None if x is None else x.data_ptr()  # noqa: E731
+        return lib().smg_q4_chained_dev(m, w._h, c.data_ptr(), a.data_ptr(), eptr, ptr(done), ptr(ready),
+                                        ptr(sync), wait_us, _stream()) == 0
+    a = _host16(a, m * k, "a")
+    if not isinstance(c, np.ndarray) or c.dtype not in (np.uint16, np.float16) or c.size != m * n:
+        raise ValueError("c is m*n (uint16/float16 numpy array)")
+    ep.validate(m, n)
+    eptr, keep = _ep_ptr(ep, n)
+    ref = lambda x: None if x is None else C.addressof(x)  # noqa: E731
+    return lib().gemm_gpu_f16f16_q4_chained(m, w._h, c.ctypes.data, a.ctypes.data, eptr, ref(done),
+                                            ref(ready)) == 0
+
+
+def last_error() -> str:
+    """Text of the calling thread's last error in the library."""
+    return lib().smg_last_error().decode()
 
 
 def matmul_q4(a, w: Q4Weights, c, m: int):

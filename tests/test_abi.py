@@ -32,7 +32,8 @@ def test_header_declares_the_drop_ins():
     names = _declared_functions()
     for must in ("gemm_gpu_f16f16_q4", "gemm_gpu_b16b16_q4", "gemm_gpu_f16_q2", "gemm_gpu_f16_q1",
                  "gemm_gpu_f16f16_q2", "gemm_gpu_f16f16_q1", "gemm_gpu_f16f16_run_packed",
-                 "gemm_gpu_b16b16_run_packed", "gemm_gpu_f16f16_q4_single", "smg_q4_create",
+                 "gemm_gpu_b16b16_run_packed", "gemm_gpu_f16f16_q4_single", "gemm_gpu_f16f16_q4_chained",
+                 "smg_q4_create",
                  "smg_q4_create_band", "smg_q2_create", "smg_q1_create", "smg_f16_prepack"):
         assert must in names
 
