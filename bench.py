@@ -1,6 +1,6 @@
 """Benchmark of the quantized-weight matmul path on one MI355X.
 
-Headline (the JSON line's `value`): BASELINE config 1 -- Q4 GEMV, m=1,
+Headline (the JSON line's `value`): config 1 -- Q4 GEMV, m=1,
 K=N=4096, block 32 -- as whole-job HBM throughput in GB/s. A "step" is one
 GEMV call on its own copy of the weights: 64 device copies (605 MB) rotate so
 every call streams its weights from HBM, not from the 256 MB MALL. The K timed
@@ -243,7 +243,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": "synthetic (seeded; BASELINE config 1 distributions)",
+        "data": "synthetic (seeded; config 1 distributions)",
         "config": {"workload": "q4_gemv m=1 K=4096 N=4096 block=32, 64 rotating weight copies",
                    "m": 1, "k": 4096, "n": 4096, "block": 32},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -1,5 +1,5 @@
 """Prefill-shaped MFMA GEMM on the GPU: the dense Gemm builder path and the Q4
-GEMM of BASELINE config 4.
+GEMM of headline config 4.
 
 Mirrors tests/correctness/epilogue_half.rs:383 (opgraph_f16_mulcol_addcol_silu),
 gemv.rs (matmul_f16_packed over ragged shapes) and the strided builder options

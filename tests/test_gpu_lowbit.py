@@ -3,7 +3,7 @@
 Mirrors src/kernels/lowbit/matmul.rs:457 (kernels_match_reference_bits: 12
 shapes x 4 blocks x 3 codebooks, both Q1 layouts, the reference's own LCG
 data), tests/correctness/q2.rs:83 (fused epilogue == plain then applied) and
-the BASELINE config-2 / config-3 shapes. Integer quantization and i32 block
+the headline configs 2 and 3 (the benchmark shapes). Integer quantization and i32 block
 sums are exact, so outputs must be identical bits.
 """
 import numpy as np
@@ -78,7 +78,7 @@ def test_single_launch_blocks_and_segments(smg, orc, block, m, n, k):
 
 @pytest.mark.parametrize("m", [1, 8])
 def test_config2_q2_ternary(smg, orc, m):
-    """K=4096, N=11008, block 128, ternary; bitwise."""
+    """Headline config 2: K=4096, N=11008, block 128, ternary; bitwise."""
     import workloads
     n, k = 11008, 4096
     a, codes, scales = workloads.q2_inputs(m, n, k, seed=0)
@@ -90,7 +90,7 @@ def test_config2_q2_ternary(smg, orc, m):
 
 
 def test_config3_q1_add_col_silu(smg, orc):
-    """Q1 + add_col(bias) + silu, K=4096, N=14336; bitwise."""
+    """Headline config 3: Q1 + add_col(bias) + silu, K=4096, N=14336; bitwise."""
     import workloads
     m, n, k = 1, 14336, 4096
     a, signs, scales, bias = workloads.q1_inputs(m, n, k, seed=0)

@@ -2,7 +2,7 @@
 
 Mirrors tests/correctness/q4.rs (q4_resident :66, q4_blocks_and_affine :127,
 q4_fused_epilogue_matches_oracle :417), gemv.rs:229 (gemv_q4) and the
-BASELINE config-1 / config-4 shapes. Float outputs: max |g-w|/(1+|w|) against
+headline configs 1 and 4 (the benchmark shapes). Float outputs: max |g-w|/(1+|w|) against
 the oracle's rounded output within 2e-3*sqrt(K)/64 (f16) or 8x that (bf16);
 the empty epilogue is pinned bitwise to the plain call (q4.rs:508-513).
 """
@@ -85,7 +85,7 @@ def test_q4_block_sizes_gemv_and_gemm(smg, orc, block, m):
 
 
 def test_config1_q4_gemv(smg, orc):
-    """m=1, K=N=4096, block 32, seed 0."""
+    """Headline config 1: m=1, K=N=4096, block 32, seed 0."""
     import workloads
     m, n, k = 1, 4096, 4096
     a, quants, scales, _ = workloads.q4_inputs(m, n, k, seed=0)
