@@ -224,8 +224,9 @@ int smg_q4_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint1
  * until *ready covers the 4096-depth segment of A it reads next, and once
  * every workgroup has stored its columns the last one raises *done to n
  * (release; all columns form one pass). A producer kernel on another stream
- * raises *ready with a release store. sync: two device words, zero before
- * the first call; sync[0] is zero again after each call, sync[1] becomes 1 if
+ * raises *ready with a release store. sync (needed when done or ready is
+ * set): two device words, zero before the first call; sync[0] is zero again
+ * after each call, sync[1] becomes 1 if
  * a wait lasted wait_us (0: 100 ms) without *ready covering its segment, and
  * then *done is not raised and the columns of the workgroups that timed out
  * are not stored. Chains that run at once each need their own sync words. */

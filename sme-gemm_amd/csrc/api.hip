@@ -793,7 +793,7 @@ int smg_q4_chained_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint
     int rc = check_kind(w, W_Q4);
     if (rc) return rc;
     if (m == 0 || w->d.n == 0) return fail(SMG_EINVAL, "smg_q4_chained_dev: empty call");
-    if (done && !sync) return fail(SMG_EINVAL, "smg_q4_chained_dev: done needs the sync words");
+    if ((done || ready) && !sync) return fail(SMG_EINVAL, "smg_q4_chained_dev: done / ready need the sync words");
     EpArgs ea;
     if ((rc = ep_args(ep, &ea))) return rc;
     // the device wall clock's rate (kHz), read once per device

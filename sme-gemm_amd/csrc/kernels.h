@@ -40,7 +40,7 @@ hipError_t launch_q4_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t
 struct ChainArgs {
     const unsigned long long *ready;  // or null: A complete at launch
     unsigned long long *done;         // or null
-    unsigned int *sync;               // [2], needed when done is set
+    unsigned int *sync;               // [2], set whenever ready or done is
     unsigned long long wait_ticks;
     unsigned long long done_value;
 };

@@ -184,6 +184,7 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
         if (!timed_out && r < (int)g.m && j < g.n) g.dst[(size_t)r * g.n + j] = finish<false>(ep, total, r, j, g.n);
     }
     if constexpr (CHAIN) {
+        if (timed_out && t == 0) __hip_atomic_store(ch.sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (ch.done) {
             // one count per workgroup, a release that writes wave 0's stores
             // back (a wave's release waits for all of its own stores); a
@@ -192,7 +193,6 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
             if (t >= 64 && t < 16 * MR) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
             __syncthreads();
             if (t == 0) {
-                if (timed_out) __hip_atomic_store(ch.sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 const uint32_t prev =
                     __hip_atomic_fetch_add(ch.sync, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
                 if (prev == gridDim.x - 1) {

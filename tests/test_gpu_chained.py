@@ -201,3 +201,21 @@ def test_device_link_outside_its_domain_returns_false(smg, orc):
     assert "scale-only" in smg.last_error()
     torch.cuda.synchronize()
     assert done.item() == 0
+
+
+def test_device_link_wait_expiry_is_reported_without_done(smg, orc):
+    """With `ready` and no `done`, an expired wait still shows in sync[1], and
+    nothing is stored; without sync words the call is refused."""
+    import torch
+    m, n, k = 2, 256, 512
+    w, _, _ = _weights(smg, orc, n, k, 51)
+    ad = _dev(orc.f32_to_f16(np.random.default_rng(52).standard_normal(m * k).astype(np.float32)))
+    ready = torch.zeros(1, dtype=torch.int64, device="cuda")
+    sync = torch.zeros(2, dtype=torch.int32, device="cuda")
+    c = torch.full((m * n,), 0x1234, dtype=torch.int16, device="cuda")
+    assert not smg.q4_chained(ad, w, c, None, ready=ready, m=m)
+    assert "sync" in smg.last_error()
+    assert smg.q4_chained(ad, w, c, None, ready=ready, m=m, sync=sync, wait_us=200)
+    torch.cuda.synchronize()
+    assert sync.tolist() == [0, 1]
+    assert bool((c == 0x1234).all())
