@@ -87,6 +87,13 @@ class Gguf:
         with open(path, "rb") as f:
             self._map = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
         self._data = np.frombuffer(self._map, dtype=np.uint8)
+        try:
+            self._parse()
+        except Exception:
+            self.close()
+            raise
+
+    def _parse(self) -> None:
         r = _Reader(self._map)
         if r.take(4) != b"GGUF":
             raise GgufError("not a GGUF file")
