@@ -669,6 +669,7 @@ hipError_t launch_tile_ng(const LtArgs &g, const EpArgs &ep, int ng, hipStream_t
 template <int KIND>
 hipError_t launch_tile(const LtArgs &g, const EpArgs &ep, int mr, int ng, hipStream_t s) {
     if (mr <= 1) return launch_tile_ng<KIND, 1>(g, ep, ng, s);
+    if (mr <= 2) return launch_tile_ng<KIND, 2>(g, ep, ng, s);
     if (mr <= 4) return launch_tile_ng<KIND, 4>(g, ep, ng, s);
     return launch_tile_ng<KIND, 8>(g, ep, ng, s);
 }
@@ -789,7 +790,7 @@ struct TileGeo {
 // a few times per CU); a wave's K range grows with them.
 TileGeo tile_geometry_cg(const WDev &w, size_t m, uint32_t cg_shift) {
     TileGeo sg = {false, 0, 0, 0, cg_shift};
-    const int mr = m <= 1 ? 1 : m <= 4 ? 4 : 8;  // the row counts the kernel is built for
+    const int mr = m <= 2 ? (int)m : m <= 4 ? 4 : 8;  // the row counts the kernel is built for
     const size_t spg = w.kind == W_Q2 ? 4 : 8;
     const size_t wpg = (size_t)WV >> cg_shift;   // waves along K per column group
     const size_t nslab = (w.k + LB_SLAB - 1) / LB_SLAB;
@@ -866,7 +867,7 @@ hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint
         f.nbq = sg.nbq;
         f.codes_bytes = (uint32_t)cb;
         f.cg_shift = sg.cg_shift;
-        const int mr = m <= 1 ? 1 : m <= 4 ? 4 : 8;
+        const int mr = m <= 2 ? (int)m : m <= 4 ? 4 : 8;
         if (m > 1) {
             f.q = (const int8_t *)scratch;
             f.qs = (const float *)((uint8_t *)scratch + (m * sg.kq + 255) / 256 * 256);

@@ -76,7 +76,7 @@ def test_single_launch_blocks_and_segments(smg, orc, block, m, n, k):
     assert np.array_equal(got, orc.lowbit_reference(1, a, signs, scales, m, n, k, block, inout=True))
 
 
-@pytest.mark.parametrize("m", [1, 8])
+@pytest.mark.parametrize("m", [1, 2, 8])
 def test_config2_q2_ternary(smg, orc, m):
     """Headline config 2: K=4096, N=11008, block 128, ternary; bitwise."""
     import workloads
