@@ -97,7 +97,9 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
         const rsrc_t ar = make_rsrc(g.lhs, g.m * g.k * 2u);
         const bool vec = (g.k & 7) == 0;
         uint4 areg[MR];  // row r, depths d0 + 8t .. +8 (MF_SEG / 8 == 512 threads)
-        if constexpr (!CHAIN) {
+        bool a_first = true;  // a chained call that awaits A reads it after its weights
+        if constexpr (CHAIN) a_first = ch.ready == nullptr;
+        if (a_first) {
 #pragma unroll
             for (int r = 0; r < MR; r++) areg[r] = load_row8(ar, r, g.m, g.k, d0 + 8 * t, vec);
         }
@@ -126,9 +128,9 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
                     timed_out = true;
                     break;
                 }
-            }
 #pragma unroll
-            for (int r = 0; r < MR; r++) areg[r] = load_row8(ar, r, g.m, g.k, d0 + 8 * t, vec);
+                for (int r = 0; r < MR; r++) areg[r] = load_row8(ar, r, g.m, g.k, d0 + 8 * t, vec);
+            }
         }
         // stage A[:, segment] (rows < m, zero past k)
         __syncthreads();
