@@ -71,6 +71,22 @@ def test_q4_gemv_single_cut(lib):
     assert lib.gemm_gpu_f16f16_q4_single(9, 4096, 4096) == 0
 
 
+def test_chained_link_refuses_a_null_handle_without_raising_done(lib):
+    """A failed chained call returns non-zero and leaves `done` where it was
+    (src/kernels/q4/matmul.rs:105-115: `false` with nothing done); checked
+    before any device work, so it runs without a GPU."""
+    P = C.c_void_p
+    lib.gemm_gpu_f16f16_q4_chained.argtypes = [C.c_size_t, P, P, P, P, P, P]
+    lib.smg_q4_chained_dev.argtypes = [C.c_size_t, P, P, P, P, P, P, P, C.c_uint, P]
+    done, ready = C.c_size_t(7), C.c_size_t(0)
+    c = np.zeros(4, np.uint16)
+    a = np.zeros(4, np.uint16)
+    rc = lib.gemm_gpu_f16f16_q4_chained(1, None, c.ctypes.data, a.ctypes.data, None,
+                                        C.addressof(done), C.addressof(ready))
+    assert rc != 0 and done.value == 7
+    assert lib.smg_q4_chained_dev(1, None, None, None, None, None, None, None, 0, None) != 0
+
+
 def test_params_validation_mirrors_reference_panics():
     import smegemm as smg
     with pytest.raises(ValueError):
