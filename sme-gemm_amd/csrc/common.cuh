@@ -219,7 +219,7 @@ __device__ __forceinline__ float act_f32(uint32_t kind, float x, float alpha) {
 // f32 ulps of the f64 formula, so if y scaled by 1 -+ 2^-19 (16 ulps) rounds
 // to the same 16-bit value, the f64 formula's f32 value -- inside that
 // interval -- rounds to it too (rounding is monotone). Otherwise, and for
-// non-finite values, the f64 path decides.
+// non-finite values, the f64 formula (inline for these two kinds) decides.
 template <bool BF16>
 __device__ __forceinline__ uint16_t act_round16(uint32_t kind, float x, float alpha) {
     if (kind == 3 || kind == 5) {
@@ -234,6 +234,9 @@ __device__ __forceinline__ uint16_t act_round16(uint32_t kind, float x, float al
             const uint16_t lo = from_f32<BF16>(y - d), hi = from_f32<BF16>(y + d);
             if (lo == hi) return lo;
         }
+        // the f64 formula inline (a call would spill registers to scratch)
+        const double yd = kind == 3 ? act_f64_body(3, (double)x, 0.0) : act_f64_body(5, (double)x, 0.0);
+        return from_f32<BF16>((float)yd);
     }
     return from_f32<BF16>(act_f32(kind, x, alpha));
 }

@@ -449,19 +449,15 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
                 areg[p][r] = (uint32_t)p * QPASS < kq ? load_row8(ar, r, g.m, g.k, p * QPASS + 8 * t, vec)
                                                       : make_uint4(0, 0, 0, 0);
     }
-    // scale rows next (waited on before the first barrier), then the
-    // epilogue operands, then the codes: vmcnt retires in issue order, so
-    // the codes can still be in flight when the waits before them end
+    // scale rows next (waited on before the first barrier), then the codes,
+    // then the epilogue operands: vmcnt retires in issue order, so the codes
+    // can still be in flight when the waits before them end
     uint4 sreg;
     {
         const rsrc_t sr = make_rsrc(g.sc, g.sc_rows * g.n_pad * 2u);
         const uint32_t bb = t >> (g.cg_shift + 1), piece = t & (2 * cg - 1);  // 8 columns a piece
         sreg = bload16(sr, (bb < nbq && bb < g.sc_rows) ? (bb * g.n_pad + wg_col0 + piece * 8) * 2u : OOB);
     }
-    const bool folder = (uint32_t)t < ncol * g.m;
-    const int fc = t & (ncol - 1), frow = t >> (4 + g.cg_shift);
-    EpPre pre = {};
-    if (folder && wg_col0 + fc < g.n) pre = ep_prefetch(ep, frow, wg_col0 + fc, g.n);
     uint4 wreg[NG];
     {
         const rsrc_t cr = make_rsrc(g.codes, g.codes_bytes);
@@ -471,6 +467,12 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
             wreg[i] = bload16(cr, grp < g.ngroups ? ((grp * g.n_pad + col0 + c) * 4 + gq4) * 16 : OOB);
         }
     }
+    // the epilogue operands last: their addresses wait on the op-graph's
+    // kernel arguments, which must not hold up the codes
+    const bool folder = (uint32_t)t < ncol * g.m;
+    const int fc = t & (ncol - 1), frow = t >> (4 + g.cg_shift);
+    EpPre pre = {};
+    if (folder && wg_col0 + fc < g.n) pre = ep_prefetch(ep, frow, wg_col0 + fc, g.n);
 
     // -- 2. quantize A (quantize_row, src/kernels/lowbit/matmul.rs:354-371),
     //       or store the rows quantized beforehand
