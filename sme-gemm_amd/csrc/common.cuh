@@ -208,7 +208,17 @@ __device__ __noinline__ double act_f64(uint32_t kind, double x, double alpha) {
 }
 
 __device__ __forceinline__ float act_f32(uint32_t kind, float x, float alpha) {
-    return (float)act_f64(kind, (double)x, (double)alpha);
+    // kinds whose f64 formula on an f32 input is exact, or one product that
+    // the f32 operation rounds the same way, inline; the rest call the f64 body
+    switch (kind) {
+    case 1: return maxnumf(x, 0.0f);
+    case 6: return x >= 0.0f ? x : alpha * x;
+    case 10: return __builtin_fabsf(x);
+    case 11: return -x;
+    case 12: return x * x;
+    case 13: return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
+    default: return (float)act_f64(kind, (double)x, (double)alpha);
+    }
 }
 
 // A trailing activation's 16-bit result, to16(f32(f64 formula)), as
