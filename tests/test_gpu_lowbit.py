@@ -101,6 +101,50 @@ def test_config3_q1_add_col_silu(smg, orc):
     assert np.array_equal(got, want)
 
 
+ACT_METHODS = {1: ("relu", ()), 2: ("gelu", ()), 3: ("silu", ()), 4: ("tanh", ()), 5: ("sigmoid", ()),
+               6: ("leaky_relu", (0.2,)), 7: ("relu6", ()), 8: ("hardsigmoid", ()),
+               9: ("hardswish", ()), 10: ("abs", ()), 11: ("neg", ()), 12: ("square", ()),
+               13: ("sign", ()), 14: ("sqrt", ()), 15: ("softsign", ()), 16: ("recip", ()),
+               17: ("rsqrt", ()), 18: ("exp", ()), 19: ("log", ()), 20: ("elu", (0.7,)),
+               21: ("selu", ()), 22: ("softplus", ()), 23: ("mish", ()), 24: ("gelu_exact", ())}
+
+
+@pytest.mark.parametrize("kind", range(1, 25))
+def test_every_activation_bitwise(smg, orc, kind):
+    """Each of the 24 activation kinds on the int8 path, bit for bit with the
+    oracle: the named five as the trailing act (alone after add_col, then
+    after a mul_scalar node), the rest as in-order nodes, last in the graph and
+    then followed by mul_scalar 2. Pre-activation
+    values span -8..8 so every branch of the piecewise kinds is taken."""
+    m, n, k = 2, 512, 256
+    rng = np.random.default_rng(500 + kind)
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    codes = rng.integers(0, 256, (k * n + 3) // 4, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.01, 0.05, n * (k // 128)).astype(np.float32))
+    bias = orc.f32_to_f16(rng.uniform(-8.0, 8.0, n).astype(np.float32))
+    w = smg.Q2Weights(codes, scales, n, k, smg.Q2Params(128))
+    name, args = ACT_METHODS[kind]
+    alpha = float(np.float32(args[0])) if args else 0.0
+    for inner in (False, True):
+        ep, nodes, act = smg.Epilogue().add_col(bias), [(4, 0, 0.0, bias, 0)], None
+        if kind <= 5:  # a trailing act stays last (graph.rs:193-223); a node precedes it
+            if inner:
+                ep, nodes = ep.mul_scalar(2.0), nodes + [(1, 0, 2.0, None, 0)]
+            ep, act = getattr(ep, name)(*args), kind
+        else:
+            ep, nodes = getattr(ep, name)(*args), nodes + [(8, kind, alpha, None, 0)]
+            if inner:
+                ep, nodes = ep.mul_scalar(2.0), nodes + [(1, 0, 2.0, None, 0)]
+        got = np.zeros(m * n, np.uint16)
+        smg.matmul_q2_ep(a, w, got, m, ep)
+        want = orc.matmul_lowbit_ep(2, a, codes, scales, m, n, k, 128, nodes, act)
+        # a NaN's sign and payload are the platform's (log of a negative: glibc
+        # gives -NaN, the device +NaN): NaN must meet NaN, every other value its bits
+        nan_g, nan_w = (got & 0x7C00 == 0x7C00) & (got & 0x3FF != 0), (want & 0x7C00 == 0x7C00) & (want & 0x3FF != 0)
+        assert np.array_equal(nan_g, nan_w), f"{name} inner={inner}: NaN positions"
+        assert np.array_equal(got[~nan_g], want[~nan_w]), f"{name} inner={inner}"
+
+
 @pytest.mark.parametrize("act", ["silu", "sigmoid"])
 def test_logistic_epilogue_bitwise_wide_range(smg, orc, act):
     """A trailing silu / sigmoid over 32768 outputs whose pre-activation values
