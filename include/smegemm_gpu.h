@@ -83,6 +83,14 @@ typedef struct {
  * Longer graphs return SMG_EINVAL. */
 #define SMG_MAX_EP_NODES 16
 
+/* The checks every entry point makes of an epilogue before any device work,
+ * for an output n columns wide: at most SMG_MAX_EP_NODES nodes, known ops and
+ * activations, a non-NULL operand pointer on every ROW / COL / TENSOR node, a
+ * TENSOR row stride of 0 or >= n. 0 or SMG_EINVAL (reason in smg_last_error).
+ * Operand lengths are the caller's to check, as validate_ep does on the Rust
+ * side (src/exec/guard.rs:112-147). */
+int smg_ep_check(const ep_desc16 *ep, size_t n);
+
 /* ---- weight handles ------------------------------------------------------- */
 typedef struct smg_weights smg_weights;
 
@@ -163,6 +171,8 @@ int smg_weights_clone(const smg_weights *w, smg_weights **out);
 void smg_weights_destroy(smg_weights *w);
 /* n, k, block (0 for dense) and device bytes of a handle. */
 int smg_weights_info(const smg_weights *w, size_t *n, size_t *k, size_t *block, size_t *bytes);
+/* The HIP device ordinal a handle's weights live on (where its calls run). */
+int smg_weights_device(const smg_weights *w, int *device);
 
 /* ---- host-pointer drop-ins (synchronous) ---------------------------------- */
 

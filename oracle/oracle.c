@@ -229,21 +229,6 @@ void or_gemm_bf16(size_t m, size_t n, size_t k, uint16_t *c, const uint16_t *a, 
     gemm16(1, m, n, k, c, a, b, beta_bits, col_major, acc);
 }
 
-/* Column range [j0, j1) of the same GEMM, for the threaded CPU baseline
- * (identical per-output arithmetic: each output only depends on its column). */
-void or_gemm_f16_cols(size_t m, size_t n, size_t k, uint16_t *c, const uint16_t *a,
-                      const uint16_t *b, size_t j0, size_t j1, float *acc) {
-    for (size_t i = 0; i < m; i++) {
-        for (size_t j = j0; j < j1; j++) acc[j - j0] = 0.0f;
-        for (size_t l = 0; l < k; l++) {
-            float av = or_f16_to_f32(a[i * k + l]);
-            const uint16_t *brow = b + l * n;
-            for (size_t j = j0; j < j1; j++) acc[j - j0] = acc[j - j0] + av * or_f16_to_f32(brow[j]);
-        }
-        for (size_t j = j0; j < j1; j++) c[i * n + j] = or_f32_to_f16(0.0f + 1.0f * acc[j - j0]);
-    }
-}
-
 /* ------------------------------------------------------------------------ */
 /* Epilogue: src/exec/scalar.rs:58-140 (ep_apply_cell / apply_ep_scalar) and */
 /* src/epilogue/mod.rs:40-110 (act_apply_f64_a, erf_approx).                 */

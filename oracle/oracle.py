@@ -64,7 +64,6 @@ def lib() -> C.CDLL:
         L.or_q4_dequant_bf16.argtypes = [P, P, P, SZ, SZ, SZ, P]
         L.or_gemm_f16.argtypes = [SZ, SZ, SZ, P, P, P, C.c_uint16, C.c_int, P]
         L.or_gemm_bf16.argtypes = [SZ, SZ, SZ, P, P, P, C.c_uint16, C.c_int, P]
-        L.or_gemm_f16_cols.argtypes = [SZ, SZ, SZ, P, P, P, SZ, SZ, P]
         L.or_apply_ep.argtypes = [P, SZ, SZ, SZ, SZ, P, SZ, C.c_int, C.c_int]
         L.or_quantize_row.argtypes = [P, SZ, SZ, P, P]
         L.or_lowbit_reference.argtypes = [C.c_int, P, P, P, P, C.c_int, SZ, SZ, SZ, SZ, P, P, P]
@@ -300,6 +299,20 @@ def matmul_lowbit_mopa_ep(kind, a, codes, scales, m, n, k, block, nodes=(), act=
 
 
 # ---- the reference's band-major resident packs ------------------------------
+
+def q4_band_sizes(n, k, block):
+    """(nibble bytes, scale entries) of the band-major Q4 arrays."""
+    nl, sl = SZ(), SZ()
+    lib().or_q4_band_sizes(n, k, block, C.byref(nl), C.byref(sl))
+    return nl.value, sl.value
+
+
+def lowbit_band_sizes(kind, n, k, block):
+    """(code bytes, scale entries) of the band-major Q2 (kind 2) / Q1 arrays."""
+    cl, sl = SZ(), SZ()
+    lib().or_lowbit_band_sizes(kind, n, k, block, C.byref(cl), C.byref(sl))
+    return cl.value, sl.value
+
 
 def q4_pack_band(quants, scales, mins, n, k, block):
     nl, sl = SZ(), SZ()

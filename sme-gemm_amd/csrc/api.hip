@@ -11,11 +11,13 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
 
 #include "kernels.h"
+#include "scratch_pool.h"
 
 using namespace smg;
 
@@ -103,6 +105,28 @@ int ctx_for(int device, size_t bytes, Ctx **out) {
     return SMG_OK;
 }
 
+// ---- device-pointer scratch ---------------------------------------------------
+// The *_dev entry points return before their kernels run, and a HIP graph may
+// replay those kernels later still, so their scratch is never the thread's
+// host-call staging buffer (freed when it grows): it comes from a grow-only
+// pool keyed by (device, stream) whose outgrown buffers are retired, not freed.
+struct HipDevAlloc {
+    void *acquire(int device, size_t bytes) {
+        int cur = -1;
+        if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+        if (cur != device && hipSetDevice(device) != hipSuccess) return nullptr;
+        void *p = nullptr;
+        const bool ok = hipMalloc(&p, bytes) == hipSuccess;
+        if (cur != device) (void)hipSetDevice(cur);
+        return ok ? p : nullptr;
+    }
+    void release(int, void *) {}  // the pool lives until the process ends
+};
+ScratchPool<HipDevAlloc> &dev_pool() {
+    static ScratchPool<HipDevAlloc> *p = new ScratchPool<HipDevAlloc>();  // never destroyed
+    return *p;
+}
+
 bool trace_on() {
     static int on = -1;
     if (on < 0) {
@@ -136,16 +160,26 @@ size_t operand_elems(const EpNode &nd, size_t m, size_t n) {
     return 0;
 }
 
-int ep_args(const ep_desc16 *ep, EpArgs *out) {
+// The graph's nodes for the kernels. The Rust side validates operand lengths
+// (validate_ep, src/exec/guard.rs:112-147); what this C boundary can check
+// without lengths it checks here: known ops and activations, an operand
+// pointer on every ROW / COL / TENSOR node (a kernel would read address 0
+// otherwise), and a TENSOR row stride of at least n.
+int ep_args(const ep_desc16 *ep, EpArgs *out, size_t n) {
     std::memset(out, 0, sizeof(*out));
     if (!ep || ep->n_nodes == 0) return SMG_OK;
     if (ep->n_nodes > SMG_MAX_EP_NODES) return fail(SMG_EINVAL, "epilogue has too many nodes");
+    if (!ep->nodes) return fail(SMG_EINVAL, "epilogue has n_nodes > 0 and no node array");
     out->n_nodes = ep->n_nodes;
     for (uint32_t i = 0; i < ep->n_nodes; i++) {
         const EpNode &nd = ep->nodes[i];
         if (ep_family(nd.op) == EPF_NONE) return fail(SMG_EINVAL, "epilogue node has an unknown op");
         if (nd.op == EP_OP_ACT && nd.aux > EP_ACT_GELU_EXACT)
             return fail(SMG_EINVAL, "epilogue node has an unknown activation");
+        if ((op_is_row(nd.op) || op_is_col(nd.op) || op_is_tensor(nd.op)) && !nd.ptr)
+            return fail(SMG_EINVAL, "epilogue row / col / tensor node has a null operand pointer");
+        if (op_is_tensor(nd.op) && nd.ld != 0 && nd.ld < n)
+            return fail(SMG_EINVAL, "epilogue tensor row stride is below n");
         out->nodes[i] = nd;
         out->fam[i] = (uint8_t)ep_family(nd.op);
         out->cls[i] = (uint8_t)ep_class(nd.op);
@@ -360,7 +394,7 @@ int host_call(const char *name, int device, size_t m, size_t n, size_t k, uint16
               size_t dst_elems, bool preload_dst, const uint16_t *lhs, size_t lhs_elems,
               const ep_desc16 *ep, size_t extra_scratch, Launch launch) {
     EpArgs ea;
-    int rc = ep_args(ep, &ea);
+    int rc = ep_args(ep, &ea, n);
     if (rc) return rc;
     size_t op_elems[SMG_MAX_EP_NODES] = {0};
     size_t total = round_up(lhs_elems * 2, 256) + round_up(dst_elems * 2, 256) +
@@ -508,6 +542,11 @@ int smg_available(void) {
 
 const char *smg_last_error(void) { return g_err.c_str(); }
 
+int smg_ep_check(const ep_desc16 *ep, size_t n) {
+    EpArgs ea;
+    return ep_args(ep, &ea, n);
+}
+
 size_t smg_q4_gemv_max_rows(void) { return Q4_GEMV_MAX_ROWS; }
 
 int smg_q4_create(const uint8_t *quants, const uint16_t *scales, const uint16_t *mins, size_t n,
@@ -653,6 +692,12 @@ int smg_weights_info(const smg_weights *w, size_t *n, size_t *k, size_t *block, 
     return SMG_OK;
 }
 
+int smg_weights_device(const smg_weights *w, int *device) {
+    if (!w || !device) return fail(SMG_EINVAL, "null argument");
+    *device = w->device;
+    return SMG_OK;
+}
+
 // ---- host-pointer drop-ins -------------------------------------------------
 
 static int q4_host(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
@@ -782,7 +827,7 @@ int smg_q4_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint1
     if (rc) return rc;
     if (m == 0 || w->d.n == 0) return SMG_OK;
     EpArgs ea;
-    if ((rc = ep_args(ep, &ea))) return rc;
+    if ((rc = ep_args(ep, &ea, w->d.n))) return rc;
     hipError_t e = run_q4(w->d, m, dst, lhs, ea, bf16 != 0, (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_q4_matmul_dev", e);
 }
@@ -795,7 +840,7 @@ int smg_q4_chained_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint
     if (m == 0 || w->d.n == 0) return fail(SMG_EINVAL, "smg_q4_chained_dev: empty call");
     if ((done || ready) && !sync) return fail(SMG_EINVAL, "smg_q4_chained_dev: done / ready need the sync words");
     EpArgs ea;
-    if ((rc = ep_args(ep, &ea))) return rc;
+    if ((rc = ep_args(ep, &ea, w->d.n))) return rc;
     // the device wall clock's rate (kHz), read once per device
     static std::atomic<int> clock_khz[64];
     int khz = w->device < 64 ? clock_khz[w->device].load(std::memory_order_relaxed) : 0;
@@ -817,16 +862,15 @@ int smg_lowbit_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const u
     if (w->d.kind != W_Q2 && w->d.kind != W_Q1) return fail(SMG_EKIND, "not low-bit weights");
     if (m == 0 || w->d.n == 0) return SMG_OK;
     EpArgs ea;
-    int rc = ep_args(ep, &ea);
+    int rc = ep_args(ep, &ea, w->d.n);
     if (rc) return rc;
     const size_t sb = lowbit_scratch_bytes(w->d, m);
     void *scratch = nullptr;
     if (sb) {
-        // huge blocks (> in-kernel pass) need a staging buffer for the
-        // pre-quantized activations: the calling thread's own
-        Ctx *c;
-        if ((rc = ctx_for(w->device, sb, &c))) return rc;
-        scratch = c->buf;
+        // several rows (or blocks past one in-kernel pass): the activations
+        // are quantized once into a buffer of this stream's own
+        scratch = dev_pool().get(w->device, stream, sb);
+        if (!scratch) return fail(SMG_ENOMEM, "smg_lowbit_matmul_dev: scratch hipMalloc");
     }
     hipError_t e = launch_lowbit_gemv(w->d, m, dst, lhs, ea, scratch, (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_lowbit_matmul_dev", e);
@@ -838,7 +882,7 @@ int smg_lowbit_mopa_dev(size_t m, const smg_weights *w, uint16_t *dst, const uin
     if (w->d.kind != W_Q2 && w->d.kind != W_Q1) return fail(SMG_EKIND, "not low-bit weights");
     if (m == 0 || w->d.n == 0) return SMG_OK;
     EpArgs ea;
-    int rc = ep_args(ep, &ea);
+    int rc = ep_args(ep, &ea, w->d.n);
     if (rc) return rc;
     hipError_t e = launch_gemm(w->d, m, dst, 1, (long)w->d.n, lhs, 1, (long)w->d.k, 1.0f, ea,
                                false, (hipStream_t)stream);
@@ -852,7 +896,7 @@ int smg_packed_matmul_dev(size_t m, const smg_weights *b, uint16_t *dst, long ds
     if (rc) return rc;
     if (m == 0 || b->d.n == 0) return SMG_OK;
     EpArgs ea;
-    if ((rc = ep_args(ep, &ea))) return rc;
+    if ((rc = ep_args(ep, &ea, b->d.n))) return rc;
     hipError_t e = launch_gemm(b->d, m, dst, dst_cs, dst_rs, lhs, lhs_cs, lhs_rs,
                                half_bits_to_float(beta_bits, bf16 != 0), ea, bf16 != 0,
                                (hipStream_t)stream);

@@ -228,8 +228,11 @@ __device__ __forceinline__ float act_f32(uint32_t kind, float x, float alpha) {
 // the constant's), on v_exp_f32 / v_rcp_f32 (1 ulp each): y is within about 4
 // f32 ulps of the f64 formula, so if y scaled by 1 -+ 2^-19 (16 ulps) rounds
 // to the same 16-bit value, the f64 formula's f32 value -- inside that
-// interval -- rounds to it too (rounding is monotone). Otherwise, and for
-// non-finite values, the f64 formula (inline for these two kinds) decides.
+// interval -- rounds to it too (rounding is monotone). Otherwise, for
+// non-finite values, and once e^-x passes 2^100 (x below about -69, where the
+// quotient nears f32's subnormal range: at x = -90 silu is -7.4e-38, a normal
+// bf16 value, that 1 / (1 + e^-x) in f32 would flush to zero), the f64 formula
+// (inline for these two kinds) decides.
 template <bool BF16>
 __device__ __forceinline__ uint16_t act_round16(uint32_t kind, float x, float alpha) {
     if (kind == 3 || kind == 5) {
@@ -239,7 +242,7 @@ __device__ __forceinline__ uint16_t act_round16(uint32_t kind, float x, float al
         const float t_lo = __builtin_fmaf(-x, L_HI, -t_hi) + -x * L_LO;
         const float e = __builtin_amdgcn_exp2f(t_hi) * (1.0f + t_lo * 0.693147180559945309f);
         const float y = (kind == 3 ? x : 1.0f) * __builtin_amdgcn_rcpf(1.0f + e);
-        if (__builtin_isfinite(x) && __builtin_isfinite(y)) {
+        if (__builtin_isfinite(x) && e < 0x1p100f && __builtin_isfinite(y)) {
             const float d = __builtin_fabsf(y) * 0x1p-19f;
             const uint16_t lo = from_f32<BF16>(y - d), hi = from_f32<BF16>(y + d);
             if (lo == hi) return lo;
@@ -289,11 +292,15 @@ __device__ __forceinline__ float clampf_(float x, float lo, float hi) {
     return x;
 }
 // x * 1/(1 + e^-y) with the hardware 2^x and reciprocal (about 1 ulp each in
-// f32): the logistic factor of silu, sigmoid and tanh-gelu. An infinite e^-y
-// gives a zero factor, as the exact quotient does.
+// f32): the logistic factor of silu, sigmoid and tanh-gelu. Once e^-y passes
+// 2^100 the quotient is x * e^y to within 2^-100 relative, evaluated in f64:
+// the f32 reciprocal of 1 + e^-y would reach the subnormal range (or zero, for
+// an infinite e^-y) where the bf16 result, e.g. silu(-90) = -7.4e-38, is still
+// a normal value.
 __device__ __forceinline__ float mul_logistic(float x, float y) {
     const float e = __builtin_amdgcn_exp2f(-y * 1.4426950408889634f);
-    return x * __builtin_amdgcn_rcpf(1.0f + e);
+    if (e < 0x1p100f) return x * __builtin_amdgcn_rcpf(1.0f + e);
+    return (float)((double)x * exp((double)y));
 }
 __device__ __forceinline__ float act_f32_fast(uint32_t kind, float x, float a) {
     switch (kind) {

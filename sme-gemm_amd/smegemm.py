@@ -80,6 +80,7 @@ def lib() -> C.CDLL:
     L.smg_weights_destroy.argtypes = [P]
     L.smg_weights_destroy.restype = None
     L.smg_weights_info.argtypes = [P, C.POINTER(SZ), C.POINTER(SZ), C.POINTER(SZ), C.POINTER(SZ)]
+    L.smg_weights_device.argtypes = [P, C.POINTER(C.c_int)]
     for name in ("gemm_gpu_f16f16_q4", "gemm_gpu_b16b16_q4", "gemm_gpu_f16_q2", "gemm_gpu_f16_q1",
                  "gemm_gpu_f16f16_q2", "gemm_gpu_f16f16_q1"):
         getattr(L, name).argtypes = [SZ, P, P, P, P]
@@ -139,6 +140,25 @@ def _ptr(a) -> int:
     return a.ctypes.data
 
 
+def _dev16(x, n: int | None, what: str, device: int | None, bf16: bool | None = None):
+    """A device tensor the kernels read or write as `n` contiguous 16-bit
+    elements on `device`: anything else (a 1- or 4-byte dtype, a strided view,
+    another GPU) would make them read or store the wrong bytes."""
+    if x.element_size() != 2:
+        raise TypeError(f"{what}: expected a 16-bit tensor (float16/bfloat16/int16), got {x.dtype}")
+    if bf16 is not None:
+        import torch
+        if (bf16 and x.dtype == torch.float16) or (not bf16 and x.dtype == torch.bfloat16):
+            raise TypeError(f"{what}: {x.dtype} where {'bf16' if bf16 else 'f16'} values are expected")
+    if not x.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    if device is not None and x.device.index != device:
+        raise ValueError(f"{what} is on cuda:{x.device.index}, the weights on cuda:{device}")
+    if n is not None and x.numel() != n:
+        raise ValueError(f"{what} has {x.numel()} elements, expected {n}")
+    return x
+
+
 def _stream() -> int:
     import torch
     return torch.cuda.current_stream().cuda_stream
@@ -167,6 +187,19 @@ class EpNode(C.Structure):
 
 class EpDesc16(C.Structure):
     _fields_ = [("n_nodes", C.c_uint32), ("nodes", C.POINTER(EpNode))]
+
+
+def _host_operand(v, bf16: bool) -> np.ndarray:
+    """A host epilogue operand as contiguous 16-bit patterns: uint16 bits, or
+    float16 values for an f16 graph. Any other dtype is refused rather than
+    cast by value (a float32 bias cast to uint16 would be the wrong bits)."""
+    a = np.ascontiguousarray(v)
+    if a.dtype == np.uint16:
+        return a
+    if a.dtype == np.float16 and not bf16:
+        return a.view(np.uint16)
+    raise TypeError(f"epilogue operand: expected {'uint16 bf16 bits' if bf16 else 'float16 or uint16 bits'}, "
+                    f"got {a.dtype}")
 
 
 def _bf16_round(x: float) -> float:
@@ -271,9 +304,15 @@ class Epilogue:
     def is_empty(self) -> bool:
         return not self.nodes and self.act is None
 
-    def validate(self, m: int, n: int) -> None:
-        """validate_ep (src/exec/guard.rs:112-147)."""
+    def validate(self, m: int, n: int, device: int | None = None) -> None:
+        """validate_ep (src/exec/guard.rs:112-147), plus what the kernels need
+        of a device operand: 16-bit elements, contiguous, on the weights'
+        device (`device`); host operands are f16 / bf16 bit patterns."""
         for op, _aux, _s, v, ld in self.nodes:
+            if v is not None and _is_dev(v):
+                _dev16(v, None, "epilogue operand", device, self.bf16)
+            elif v is not None:
+                _host_operand(v, self.bf16)
             length = None if v is None else (v.numel() if _is_dev(v) else np.asarray(v).size)
             if op in _ROW and length != m:
                 raise ValueError("row operand is per-M (length m)")
@@ -296,8 +335,7 @@ class Epilogue:
             ptr = None
             if v is not None:
                 if not _is_dev(v):
-                    v = np.ascontiguousarray(v).view(np.uint16) if np.asarray(v).dtype in (
-                        np.float16, np.uint16) else np.ascontiguousarray(v, dtype=np.uint16)
+                    v = _host_operand(v, self.bf16)
                 keep.append(v)
                 ptr = _ptr(v)
             if op in _TENSOR and ld == 0:
@@ -355,6 +393,13 @@ class _Handle:
         _check(lib().smg_weights_info(self._h, None, None, None, C.byref(b)), "smg_weights_info")
         return b.value
 
+    def device(self) -> int:
+        """The GPU ordinal the weights live on (device tensors passed with
+        them must be there too)."""
+        d = C.c_int()
+        _check(lib().smg_weights_device(self._h, C.byref(d)), "smg_weights_device")
+        return d.value
+
 
 class Q4Params:
     """src/kernels/q4/mod.rs:56-103."""
@@ -400,6 +445,23 @@ def _u8(x) -> np.ndarray:
     return np.ascontiguousarray(x, dtype=np.uint8)
 
 
+def q4_band_sizes(n: int, k: int, block: int):
+    """(nibble bytes, scale entries) of Q4Weights' band-major arrays
+    (src/kernels/q4/weights.rs:89-113): 128-column bands, 64 bytes a depth,
+    scales [band][block][128]."""
+    bands, nbk = -(-n // 128), -(-k // block)
+    return bands * k * 64, bands * nbk * 128
+
+
+def lowbit_band_sizes(kind: int, n: int, k: int, block: int):
+    """(code bytes, scale entries) of Q2Weights / Q1Weights' band-major arrays
+    (src/kernels/lowbit/q2.rs:12-20,148-161, q1.rs:186-201): 64-column bands,
+    K padded to a multiple of 16, 16 (Q2) or 8 (Q1) bytes a band per depth,
+    scales [band][block][64]."""
+    bands, kp, nbk = -(-n // 64), -(-k // 16) * 16, -(-k // block)
+    return bands * kp * (16 if kind == 2 else 8), bands * nbk * 64
+
+
 class Q4Weights(_Handle):
     """Q4 weights kept 4-bit resident on the device (src/kernels/q4/weights.rs:26)."""
 
@@ -408,14 +470,16 @@ class Q4Weights(_Handle):
         p = params or Q4Params()
         nbk = -(-k // p.block())
         quants = _u8(quants)
-        scales = _host16(scales, (n * nbk) if not _band else scales.size, "scales")
+        # the library reads exactly these lengths from the host arrays
+        q_len, sc_len = q4_band_sizes(n, k, p.block()) if _band else (-(-(k * n) // 2), n * nbk)
+        scales = _host16(scales, sc_len, "scales")
         if p.is_affine() != (mins is not None):
             raise ValueError("Q4Form::Affine requires a mins array" if p.is_affine()
                              else "Q4Form::Scale takes no mins array")
         if mins is not None:
-            mins = _host16(mins, scales.size, "mins")
-        if not _band and quants.size != -(-(k * n) // 2):
-            raise ValueError("quants is ceil(k*n/2) bytes")
+            mins = _host16(mins, sc_len, "mins")
+        if quants.size != q_len:
+            raise ValueError(f"quants is {q_len} bytes" + (" (band-major)" if _band else " (ceil(k*n/2))"))
         _require_device()
         h = C.c_void_p()
         fn = lib().smg_q4_create_band if _band else lib().smg_q4_create
@@ -472,8 +536,13 @@ class Q2Params:
         self._codebook = tuple(Q2_TERNARY)
 
     def with_codebook(self, values) -> "Q2Params":
+        """Q2Params::with_codebook (src/kernels/lowbit/mod.rs:74-81): the four
+        int8 values codes 0..3 stand for (an `[i8; 4]` in the reference)."""
+        vals = tuple(int(v) for v in values)
+        if len(vals) != 4 or any(not -128 <= v <= 127 for v in vals):
+            raise ValueError(f"a Q2 codebook is exactly 4 int8 values, got {values!r}")
         p = Q2Params(self._block)
-        p._codebook = tuple(int(v) for v in values)
+        p._codebook = vals
         return p
 
     def block(self) -> int:
@@ -495,9 +564,10 @@ class Q2Weights(_Handle):
         p = p or Q2Params()
         nbk = -(-k // p.block())
         codes = _u8(codes)
-        if not _band and codes.size != -(-(k * n) // 4):
-            raise ValueError("codes is ceil(k*n/4) bytes")
-        scales = _host16(scales, (n * nbk) if not _band else scales.size, "scales")
+        c_len, sc_len = lowbit_band_sizes(2, n, k, p.block()) if _band else (-(-(k * n) // 4), n * nbk)
+        if codes.size != c_len:
+            raise ValueError(f"codes is {c_len} bytes" + (" (band-major)" if _band else " (ceil(k*n/4))"))
+        scales = _host16(scales, sc_len, "scales")
         cb = np.asarray(p.codebook(), np.int8)
         _require_device()
         h = C.c_void_p()
@@ -531,9 +601,10 @@ class Q1Weights(_Handle):
             raise ValueError(f"q1 block size must be a power of two from 16 to 65536, got {block}")
         nbk = -(-k // block)
         signs = _u8(signs)
-        if not _band and signs.size != -(-(k * n) // 8):
-            raise ValueError("signs is ceil(k*n/8) bytes")
-        scales = _host16(scales, (n * nbk) if not _band else scales.size, "scales")
+        s_len, sc_len = lowbit_band_sizes(1, n, k, block) if _band else (-(-(k * n) // 8), n * nbk)
+        if signs.size != s_len:
+            raise ValueError(f"signs is {s_len} bytes" + (" (band-major)" if _band else " (ceil(k*n/8))"))
+        scales = _host16(scales, sc_len, "scales")
         _require_device()
         h = C.c_void_p()
         if _band:
@@ -657,11 +728,10 @@ def _run_host_or_dev(name_host, dev_fn, a, w, c, m, ep, extra_dev=()):
     if (_is_dev(a)) != (_is_dev(c)):
         raise ValueError("a and c must both be host arrays or both device tensors")
     if _is_dev(a):
-        if a.numel() != m * k:
-            raise ValueError("a is m*k")
-        if c.numel() != m * n:
-            raise ValueError("c is m*n")
-        ep.validate(m, n)
+        dev = w.device()
+        _dev16(a, m * k, "a (m*k)", dev)
+        _dev16(c, m * n, "c (m*n)", dev)
+        ep.validate(m, n, dev)
         eptr, keep = _ep_ptr(ep, n)
         _check(dev_fn(m, w._h, c.data_ptr(), a.data_ptr(), eptr, *extra_dev, _stream()), name_host)
         return c
@@ -699,9 +769,12 @@ def q4_chained(a, w: Q4Weights, c, ep: Epilogue | None = None, done=None, ready=
     ep = ep or Epilogue()
     n, k = w.n(), w.k()
     if _is_dev(a):
-        if not _is_dev(c) or a.numel() != m * k or c.numel() != m * n:
+        if not _is_dev(c):
             raise ValueError("a is m*k and c is m*n, both device tensors")
-        ep.validate(m, n)
+        dev = w.device()
+        _dev16(a, m * k, "a (m*k)", dev)
+        _dev16(c, m * n, "c (m*n)", dev)
+        ep.validate(m, n, dev)
         eptr, keep = _ep_ptr(ep, n)
         ptr = lambda x: None if x is None else x.data_ptr()  # noqa: E731
         return lib().smg_q4_chained_dev(m, w._h, c.data_ptr(), a.data_ptr(), eptr, ptr(done), ptr(ready),
@@ -810,9 +883,10 @@ class Gemm:
         m, n, k = self.m, self.packed.n(), self.packed.k()
         dst_cs, dst_rs = (m, 1) if self._col_major else (1, n)
         if _is_dev(self.a):
-            if self.a.numel() != m * k or c.numel() != m * n:
-                raise ValueError("a is m*k, c is m*n")
-            self.ep.validate(m, n)
+            dev = self.packed.device()
+            _dev16(self.a, m * k, "a (m*k)", dev, self.packed.bf16)
+            _dev16(c, m * n, "c (m*n)", dev, self.packed.bf16)
+            self.ep.validate(m, n, dev)
             eptr, keep = _ep_ptr(self.ep, n)
             _check(lib().smg_packed_matmul_dev(m, self.packed._h, c.data_ptr(), dst_cs, dst_rs,
                                                self.a.data_ptr(), 1, k, self._beta, eptr,

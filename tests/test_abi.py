@@ -131,6 +131,96 @@ def test_epilogue_validate_lengths():
         smg.Epilogue().add_tensor(np.zeros(40, np.uint16), 5).validate(3, 6)
 
 
+def test_c_boundary_refuses_operand_nodes_without_a_pointer(lib):
+    """A ROW / COL / TENSOR node with a NULL operand (which a kernel would read
+    at address 0) or a tensor stride below n is refused with SMG_EINVAL at the
+    C boundary, before any device work; scalar and activation nodes need no
+    pointer."""
+    import smegemm as smg
+    lib.smg_ep_check.argtypes = [C.c_void_p, C.c_size_t]
+    lib.smg_last_error.restype = C.c_char_p
+    buf = np.zeros(64, np.uint16)
+
+    def check(nodes, n=8):
+        arr = (smg.EpNode * len(nodes))(*nodes)
+        d = smg.EpDesc16(len(nodes), C.cast(arr, C.POINTER(smg.EpNode)))
+        return lib.smg_ep_check(C.addressof(d), n)
+
+    for op in (2, 4, 6, 12, 13, 14, 16, 17, 18, 19, 20, 21, 22, 23, 24, 3, 5, 7):
+        assert check([smg.EpNode(op, 0, 0.0, None, 0)]) == -1, op
+        assert b"null operand" in lib.smg_last_error()
+        assert check([smg.EpNode(op, 0, 0.0, buf.ctypes.data, 0)]) == 0, op
+    assert check([smg.EpNode(6, 0, 0.0, buf.ctypes.data, 7)]) == -1  # ld 7 < n 8
+    assert check([smg.EpNode(6, 0, 0.0, buf.ctypes.data, 9)]) == 0
+    assert check([smg.EpNode(0, 0, 1.0, None, 0), smg.EpNode(8, 3, 0.0, None, 0)]) == 0
+    assert check([smg.EpNode(25, 0, 0.0, None, 0)]) == -1       # unknown op
+    assert check([smg.EpNode(8, 25, 0.0, None, 0)]) == -1       # unknown activation
+    assert check([smg.EpNode(0, 0, 1.0, None, 0)] * 17) == -1   # too many nodes
+    assert lib.smg_ep_check(None, 8) == 0                       # no epilogue
+    d = smg.EpDesc16(1, None)
+    assert lib.smg_ep_check(C.addressof(d), 8) == -1            # n_nodes without nodes
+
+
+def test_host_operands_must_be_16_bit_patterns():
+    """A host operand of another dtype is refused, not cast by value (a float32
+    bias cast to uint16 would hold the wrong bits)."""
+    import smegemm as smg
+    with pytest.raises(TypeError):
+        smg.Epilogue().add_col(np.linspace(-1, 1, 6, dtype=np.float32)).desc(6)
+    with pytest.raises(TypeError):
+        smg.Epilogue().add_col(np.zeros(6, np.int32)).validate(1, 6)
+    with pytest.raises(TypeError):  # f16 values into a bf16 graph
+        smg.Epilogue(bf16=True).add_col(np.zeros(6, np.float16)).desc(6)
+    d, keep = smg.Epilogue().add_col(np.full(6, 0.5, np.float16)).desc(6)
+    assert np.frombuffer((C.c_uint16 * 6).from_address(d.nodes[0].ptr), np.uint16)[0] == 0x3800
+
+
+def test_band_constructors_check_lengths_before_reading():
+    """from_band reads exactly the band-size formulas' lengths from the host
+    arrays (q4/weights.rs:89-113, q2.rs:148-161, q1.rs:186-201); shorter (or
+    longer) arrays are refused before the library is asked to read them."""
+    import smegemm as smg
+    n, k = 200, 96
+    nib, sc = smg.q4_band_sizes(n, k, 32)
+    assert (nib, sc) == (2 * 96 * 64, 2 * 3 * 128)
+    with pytest.raises(ValueError):
+        smg.Q4Weights.from_band(np.zeros(nib - 1, np.uint8), np.zeros(sc, np.uint16), None, n, k,
+                                smg.Q4Params())
+    with pytest.raises(ValueError):
+        smg.Q4Weights.from_band(np.zeros(nib, np.uint8), np.zeros(sc - 1, np.uint16), None, n, k,
+                                smg.Q4Params())
+    with pytest.raises(ValueError):
+        smg.Q4Weights.from_band(np.zeros(nib, np.uint8), np.zeros(sc, np.uint16),
+                                np.zeros(sc - 2, np.uint16), n, k, smg.Q4Params().affine())
+    c2, s2 = smg.lowbit_band_sizes(2, n, k, 32)
+    assert (c2, s2) == (4 * 96 * 16, 4 * 3 * 64)
+    with pytest.raises(ValueError):
+        smg.Q2Weights.from_band(np.zeros(c2 - 16, np.uint8), np.zeros(s2, np.uint16), n, k,
+                                smg.Q2Params(32))
+    c1, s1 = smg.lowbit_band_sizes(1, n, 100, 32)
+    assert (c1, s1) == (4 * 112 * 8, 4 * 4 * 64)
+    with pytest.raises(ValueError):
+        smg.Q1Weights.from_band(np.zeros(c1, np.uint8), np.zeros(s1 - 64, np.uint16), n, 100, 32)
+
+
+def test_band_sizes_match_the_oracle():
+    import oracle
+    import smegemm as smg
+    for n, k, block in ((1, 1, 16), (200, 96, 32), (129, 4097, 64), (64, 16, 16)):
+        assert smg.q4_band_sizes(n, k, block) == oracle.q4_band_sizes(n, k, block)
+        for kind in (1, 2):
+            assert smg.lowbit_band_sizes(kind, n, k, block) == oracle.lowbit_band_sizes(kind, n, k, block)
+
+
+def test_q2_codebook_is_four_int8_values():
+    """Q2Params::with_codebook takes an [i8; 4] (src/kernels/lowbit/mod.rs:74-81)."""
+    import smegemm as smg
+    assert smg.Q2Params().with_codebook([-2, -1, 1, 2]).codebook() == (-2, -1, 1, 2)
+    for bad in ([-1, 0, 1], [-1, 0, 1, 0, 2], [0, 0, 0, 128], [-129, 0, 0, 0]):
+        with pytest.raises(ValueError):
+            smg.Q2Params().with_codebook(bad)
+
+
 def test_scalar_operands_round_through_the_element_type():
     """Scalars are stored as T::ep_to_f32 (graph.rs:86-96)."""
     import smegemm as smg

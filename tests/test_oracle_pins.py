@@ -385,6 +385,82 @@ def _values(kind, codes, n, k, codebook=(-1, 0, 1, 0), inout=False):
     return v
 
 
+def _scale_sweep():
+    """f16 scales across the range: subnormals, the smallest normals, the
+    config ranges, and values whose product with an int8 overflows f16."""
+    fixed = [0x0001, 0x0003, 0x03FF, 0x0400, 0x0401, 0x1400, 0x2000, 0x211F, 0x2A8F, 0x3C00,
+             0x3C01, 0x4B00, 0x5800, 0x5BFF, 0x7000, 0x7BFF]
+    rng = np.random.default_rng(77)
+    rand = rng.integers(1, 0x7C00, 48, dtype=np.int64).tolist()
+    s = np.array(fixed + rand, np.uint16)
+    return np.concatenate([s, s | 0x8000])  # and every one negated
+
+
+@pytest.mark.parametrize("kind,inout,cb", [(2, False, (-1, 0, 1, 0)), (2, False, (-128, -3, 5, 127)),
+                                           (1, False, None), (1, True, None)])
+def test_lowbit_dequant_closed_form(kind, inout, cb):
+    """Codes::dequant (matmul.rs:178-197), the MOPA route's f16 weights, against
+    its closed form: f16_RNE(scale * codebook[code]) for Q2 (an f16 scale times
+    an int8 is exact in f64, so numpy's one f64 -> f16 rounding is the
+    reference's one rounding of the exact product) and +scale / -scale for Q1
+    (set bit = +). Every code (all 4 Q2 codes, both signs) meets every scale of
+    a sweep, in both Q1 layouts; the codes are read by this file's own reader."""
+    sweep = _scale_sweep()
+    n = sweep.size                  # one column per scale value
+    block = 16
+    k = 64                          # 4 blocks: each column's blocks share its scale
+    nbk = k // block
+    scales = np.repeat(sweep, nbk)  # scales[j*nbk + b] = sweep[j]
+    rng = np.random.default_rng(kind * 10 + inout)
+    if kind == 2:
+        # depth d of column j holds code (d + j) % 4: every code in every column
+        codes = np.zeros((k * n + 3) // 4, np.uint8)
+        for d in range(k):
+            for j in range(n):
+                idx = d * n + j
+                codes[idx // 4] |= ((d + j) % 4) << (2 * (idx % 4))
+    else:
+        codes = rng.integers(0, 256, (k * n + 7) // 8, dtype=np.uint8)
+    cbk = cb if cb is not None else (-1, 0, 1, 0)
+    got = O.lowbit_dequant(kind, codes, scales, n, k, block, cbk, inout).reshape(k, n)
+    vals = _values(kind, codes, n, k, cbk, inout)
+    s64 = sweep.view(np.float16).astype(np.float64)
+    if kind == 2:
+        with np.errstate(over="ignore"):  # large scales times 127 round to +-inf, as in f16
+            want = (s64[None, :] * vals.astype(np.float64)).astype(np.float16).view(np.uint16)
+    else:
+        want = np.where(vals > 0, sweep[None, :], sweep[None, :] ^ np.uint16(0x8000)).astype(np.uint16)
+    assert np.array_equal(got, want)
+    if kind == 2:
+        assert set(np.unique((np.arange(k)[:, None] + np.arange(n)[None, :]) % 4)) == {0, 1, 2, 3}
+    else:
+        assert (vals > 0).any() and (vals < 0).any()
+
+
+def test_lowbit_dequant_planted_mistakes_are_caught():
+    """The closed form above would catch the plausible mistakes: a sign-bit
+    flip (Q1 set bit = -scale), a transposed codebook, or rounding through
+    bf16; each is planted on the CPU copy and must differ somewhere."""
+    sweep = _scale_sweep()[:32]
+    n, k, block = sweep.size, 16, 16
+    codes = np.zeros((k * n + 3) // 4, np.uint8)
+    for d in range(k):
+        for j in range(n):
+            idx = d * n + j
+            codes[idx // 4] |= ((d + j) % 4) << (2 * (idx % 4))
+    good = O.lowbit_dequant(2, codes, sweep, n, k, block, (-2, -1, 1, 2)).reshape(k, n)
+    swapped = O.lowbit_dequant(2, codes, sweep, n, k, block, (2, 1, -1, -2)).reshape(k, n)
+    assert not np.array_equal(good, swapped)
+    s32 = sweep.view(np.float16).astype(np.float32)
+    vals = _values(2, codes, n, k, (-2, -1, 1, 2)).astype(np.float32)
+    via_bf16 = O.f32_to_f16(O.bf16_to_f32(O.f32_to_bf16((s32[None, :] * vals).ravel())))
+    assert not np.array_equal(good.ravel(), via_bf16)
+    signs = np.random.default_rng(3).integers(0, 256, (k * n + 7) // 8, dtype=np.uint8)
+    q1 = O.lowbit_dequant(1, signs, sweep, n, k, block).reshape(k, n)
+    flipped = O.lowbit_dequant(1, signs ^ np.uint8(0xFF), sweep, n, k, block).reshape(k, n)
+    assert np.array_equal(q1 ^ np.uint16(0x8000), flipped)
+
+
 @pytest.mark.parametrize("kind", [2, 1])
 @pytest.mark.parametrize("m,n,k,block", [(1, 7, 37, 16), (2, 5, 200, 64), (3, 4, 130, 128)])
 def test_lowbit_reference_exact_rational(kind, m, n, k, block):
