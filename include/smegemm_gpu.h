@@ -245,6 +245,20 @@ int smg_q4_chained_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint
                        unsigned int *sync, unsigned int wait_us, void *stream);
 int smg_lowbit_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
                           const ep_desc16 *ep, void *stream);
+/* smg_lowbit_matmul_dev that allocates nothing. It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, bits and stream semantics; the quantized activations of a
+ * multi-row call (q, block scales and sums: m*K bytes and a little more) are
+ * staged in a static device array of this library, SMG_NOALLOC_SCRATCH_BYTES
+ * per device and held by each device until the process ends, instead of an
+ * allocated buffer. A call needing more returns SMG_EINVAL with nothing
+ * enqueued. Every call on one device shares that array and each call rewrites
+ * what it reads: calls that overlap on one GPU (on different streams, or on
+ * one stream from several threads) race on it. */
+#define SMG_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
+int smg_lowbit_matmul_dev_noalloc(size_t m, const smg_weights *w, uint16_t *dst,
+                                  const uint16_t *lhs, const ep_desc16 *ep, void *stream);
 int smg_lowbit_mopa_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
                         const ep_desc16 *ep, void *stream);
 int smg_packed_matmul_dev(size_t m, const smg_weights *b_pack, uint16_t *dst, long dst_cs,

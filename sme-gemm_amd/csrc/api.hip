@@ -127,6 +127,45 @@ ScratchPool<HipDevAlloc> &dev_pool() {
     return *p;
 }
 
+// ---- allocation-free scratch (smg_lowbit_matmul_dev_noalloc) --------------------
+// One static array per device: the device keeps its copy until the process
+// ends. In host code `scratch` is only a stand-in for the symbol, not a device
+// address: kernels are given the address hipGetSymbolAddress returns for the
+// current device, looked up once per device at that device's first call.
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::atomic<void *> g_noalloc_ptr[NOALLOC_MAX_DEVICES];
+std::mutex g_noalloc_mu;
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[SMG_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+// The device address of `device`'s copy of `scratch` into *out (looked up with
+// that device current, the caller's device restored).
+int noalloc_scratch(int device, void **out) {
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES)
+        return fail(SMG_EINVAL, "smg_lowbit_matmul_dev_noalloc: device ordinal beyond the per-device table");
+    void *p = g_noalloc_ptr[device].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lk(g_noalloc_mu);
+        p = g_noalloc_ptr[device].load(std::memory_order_relaxed);
+        if (!p) {
+            int cur = -1;
+            hipError_t e = hipGetDevice(&cur);
+            if (e == hipSuccess && cur != device) e = hipSetDevice(device);
+            if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (cur >= 0 && cur != device) (void)hipSetDevice(cur);
+            if (e != hipSuccess || !p)
+                return fail(SMG_EHIP, "smg_lowbit_matmul_dev_noalloc: hipGetSymbolAddress(scratch)", e);
+            g_noalloc_ptr[device].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return SMG_OK;
+}
+
 bool trace_on() {
     static int on = -1;
     if (on < 0) {
@@ -874,6 +913,28 @@ int smg_lowbit_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const u
     }
     hipError_t e = launch_lowbit_gemv(w->d, m, dst, lhs, ea, scratch, (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_lowbit_matmul_dev", e);
+}
+
+// As smg_lowbit_matmul_dev, with the quantized activations in the device's
+// static `scratch` array (its looked-up address, never the host-side name):
+// no device memory is allocated or freed. Nothing there must start at zero:
+// the quantization kernel rewrites every entry the product kernel reads.
+int smg_lowbit_matmul_dev_noalloc(size_t m, const smg_weights *w, uint16_t *dst,
+                                  const uint16_t *lhs, const ep_desc16 *ep, void *stream) {
+    if (!w) return fail(SMG_EINVAL, "null weights");
+    if (w->d.kind != W_Q2 && w->d.kind != W_Q1) return fail(SMG_EKIND, "not low-bit weights");
+    if (m == 0 || w->d.n == 0) return SMG_OK;
+    EpArgs ea;
+    int rc = ep_args(ep, &ea, w->d.n);
+    if (rc) return rc;
+    const size_t sb = lowbit_scratch_bytes(w->d, m);
+    if (sb > SMG_NOALLOC_SCRATCH_BYTES)
+        return fail(SMG_EINVAL, "smg_lowbit_matmul_dev_noalloc: the call needs more scratch than "
+                                "SMG_NOALLOC_SCRATCH_BYTES (fewer rows or a shorter K)");
+    void *p = nullptr;
+    if (sb && (rc = noalloc_scratch(w->device, &p))) return rc;
+    hipError_t e = launch_lowbit_gemv(w->d, m, dst, lhs, ea, p, (hipStream_t)stream);
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_lowbit_matmul_dev_noalloc", e);
 }
 
 int smg_lowbit_mopa_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
