@@ -703,3 +703,125 @@ void or_q1_quantize(const float *w, int layout, size_t n, size_t k, size_t block
                 }
         }
 }
+
+/* ------------------------------------------------------------------------ */
+/* The decode block's row-wise passes (config 5): the portable bodies of     */
+/* nn::rms_norm (src/nn.rs:21-32,98-144,159), attention_kv_f16's one_row      */
+/* (src/kernels/kv_attention.rs:286-325), GatedLinear's glu                   */
+/* (src/linear.rs:803-826) and the NeoX RoPE of examples/bonsai/model.rs:31-107 */
+/* (no YaRN scaling: mscale 1). Rust never contracts a*b+c (this file is built */
+/* with -ffp-contract=off) and its f32 exp / tanh / sin / cos / f64 powf are  */
+/* the platform libm's (glibc here), as these calls are.                     */
+/* ------------------------------------------------------------------------ */
+
+/* norm_row with rms = true (nn.rs:128-143): lane_sum (nn.rs:21-32) keeps 8
+ * lane accumulators over whole chunks of 8, sums the tail in order, then adds
+ * the 8 lanes in order and the tail; r = 1 / sqrt(mean + eps) in f32; each
+ * output is (v - 0) * r * w + 0 (mean 0, no bias), left to right. */
+void or_rms_norm_row(const float *x, const float *w, size_t dim, float eps, float *out) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const size_t chunks = dim / 8;
+    for (size_t c = 0; c < chunks; c++)
+        for (size_t i = 0; i < 8; i++) {
+            const float v = x[8 * c + i] - 0.0f;
+            acc[i] = acc[i] + v * v;
+        }
+    float tail = -0.0f; /* an f32 iterator sum starts from -0.0 */
+    for (size_t t = chunks * 8; t < dim; t++) {
+        const float v = x[t] - 0.0f;
+        tail = tail + v * v;
+    }
+    float s = -0.0f;
+    for (size_t i = 0; i < 8; i++) s = s + acc[i];
+    s = s + tail;
+    const float r = 1.0f / sqrtf(s / (float)dim + eps);
+    for (size_t i = 0; i < dim; i++) out[i] = (x[i] - 0.0f) * r * w[i] + 0.0f;
+}
+
+/* nn::rms_norm into f16 (rows of `dim`; each row's f32 result rounded by
+ * to_f16, RNE). */
+void or_rms_norm_f16(const float *x, const float *w, size_t rows, size_t dim, float eps,
+                     uint16_t *y, float *row_scratch) {
+    for (size_t r = 0; r < rows; r++) {
+        or_rms_norm_row(x + r * dim, w, dim, eps, row_scratch);
+        for (size_t i = 0; i < dim; i++) y[r * dim + i] = or_f32_to_f16(row_scratch[i]);
+    }
+}
+
+/* Rope::new without YaRN (model.rs:44-57): inv_freq[i] = (1 / base^(2i/dim))
+ * in f64, then to f32. */
+void or_rope_inv_freq(size_t dim, double base, float *inv_freq) {
+    for (size_t i = 0; i < dim / 2; i++)
+        inv_freq[i] = (float)(1.0 / pow(base, (double)(2 * i) / (double)dim));
+}
+
+/* Rope::angles (model.rs:86-93): (pos as f32 * f).sin_cos(), times mscale 1. */
+void or_rope_angles(const float *inv_freq, size_t half, size_t pos, float *cos_out,
+                    float *sin_out) {
+    for (size_t i = 0; i < half; i++) {
+        const float a = (float)pos * inv_freq[i];
+        sin_out[i] = sinf(a) * 1.0f;
+        cos_out[i] = cosf(a) * 1.0f;
+    }
+}
+
+/* Rope::apply (model.rs:95-107): each 2*half-wide head's halves rotated
+ * against each other: x1' = u c - v s, x2' = v c + u s. */
+void or_rope_apply(float *x, size_t len, const float *cos_v, const float *sin_v, size_t half) {
+    for (size_t h0 = 0; h0 + 2 * half <= len; h0 += 2 * half)
+        for (size_t i = 0; i < half; i++) {
+            const float u = x[h0 + i], v = x[h0 + half + i];
+            x[h0 + i] = u * cos_v[i] - v * sin_v[i];
+            x[h0 + half + i] = v * cos_v[i] + u * sin_v[i];
+        }
+}
+
+/* one_row, the portable attention_kv_f16 (kv_attention.rs:286-325): per query
+ * head h (KV head h / (heads / kv_heads)): q rounded to f16 after the scale,
+ * scores as f32 sums in depth order, the running max by maxNum, exp(s - max)
+ * summed in key order, values accumulated in key order, then divided by the
+ * sum. scores: `len` floats of scratch. */
+void or_attention_kv_f16(const float *q, const uint16_t *k, const uint16_t *v, size_t len,
+                         size_t heads, size_t kv_heads, size_t hd, float scale, float *out,
+                         float *scores, float *qh) {
+    const size_t group = heads / kv_heads, ld = kv_heads * hd;
+    for (size_t h = 0; h < heads; h++) {
+        const size_t off = (h / group) * hd;
+        for (size_t d = 0; d < hd; d++) qh[d] = or_f16_to_f32(or_f32_to_f16(q[h * hd + d] * scale));
+        float mx = -INFINITY;
+        for (size_t t = 0; t < len; t++) {
+            float s = -0.0f;
+            for (size_t d = 0; d < hd; d++) s = s + qh[d] * or_f16_to_f32(k[t * ld + off + d]);
+            scores[t] = s;
+            mx = fmaxf(mx, s);
+        }
+        float sum = 0.0f;
+        for (size_t t = 0; t < len; t++) {
+            scores[t] = expf(scores[t] - mx);
+            sum = sum + scores[t];
+        }
+        float *oh = out + h * hd;
+        for (size_t d = 0; d < hd; d++) oh[d] = 0.0f;
+        for (size_t t = 0; t < len; t++)
+            for (size_t d = 0; d < hd; d++) oh[d] = oh[d] + scores[t] * or_f16_to_f32(v[t * ld + off + d]);
+        for (size_t d = 0; d < hd; d++) oh[d] = oh[d] / sum;
+    }
+}
+
+/* glu (linear.rs:803-826): m rows of 2n interleaved outputs -- each 32-column
+ * chunk (the last w < 32 wide) is w gate columns then w up columns -- to
+ * y = f16(act(gate) * up), act in f32: silu g / (1 + exp(-g)), or (gelu != 0)
+ * the tanh form 0.5 g (1 + tanh(0.7978846 (g + 0.044715 g g g))). */
+void or_glu_f16(uint16_t *y, const uint16_t *both, size_t m, size_t n, int gelu) {
+    for (size_t r = 0; r < m; r++)
+        for (size_t c0 = 0; c0 < n; c0 += 32) {
+            const size_t w = n - c0 < 32 ? n - c0 : 32;
+            for (size_t j = 0; j < w; j++) {
+                const float g = or_f16_to_f32(both[r * 2 * n + 2 * c0 + j]);
+                const float u = or_f16_to_f32(both[r * 2 * n + 2 * c0 + w + j]);
+                const float a = gelu ? 0.5f * g * (1.0f + tanhf(0.7978846f * (g + 0.044715f * g * g * g)))
+                                     : g / (1.0f + expf(-g));
+                y[r * n + c0 + j] = or_f32_to_f16(a * u);
+            }
+        }
+}

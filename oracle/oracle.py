@@ -75,6 +75,13 @@ def lib() -> C.CDLL:
         L.or_q4_pack_band.argtypes = [P, P, P, SZ, SZ, SZ, P, P, P]
         L.or_lowbit_band_sizes.argtypes = [C.c_int, SZ, SZ, SZ, C.POINTER(SZ), C.POINTER(SZ)]
         L.or_lowbit_pack_band.argtypes = [C.c_int, P, P, C.c_int, SZ, SZ, SZ, P, P]
+        L.or_rms_norm_row.argtypes = [P, P, SZ, C.c_float, P]
+        L.or_rms_norm_f16.argtypes = [P, P, SZ, SZ, C.c_float, P, P]
+        L.or_rope_inv_freq.argtypes = [SZ, C.c_double, P]
+        L.or_rope_angles.argtypes = [P, SZ, SZ, P, P]
+        L.or_rope_apply.argtypes = [P, SZ, P, P, SZ]
+        L.or_attention_kv_f16.argtypes = [P, P, P, SZ, SZ, SZ, SZ, C.c_float, P, P, P]
+        L.or_glu_f16.argtypes = [P, P, SZ, SZ, C.c_int]
     return _lib
 
 
@@ -357,3 +364,141 @@ def lcg_fill(seed: int, length: int):
         s = (s * 6364136223846793005 + 1442695040888963407) & 0xFFFFFFFFFFFFFFFF
         vals[i] = np.float32(s >> 40) / np.float32(1 << 24) - np.float32(0.5)
     return f32_to_f16(vals), s
+
+
+def lcg_fill_f32(seed: int, length: int):
+    """`fill_f32` of tests/correctness/main.rs:152-161: returns (f32 values,
+    new seed)."""
+    vals = np.empty(length, np.float32)
+    s = seed & 0xFFFFFFFFFFFFFFFF
+    for i in range(length):
+        s = (s * 6364136223846793005 + 1442695040888963407) & 0xFFFFFFFFFFFFFFFF
+        vals[i] = np.float32(s >> 40) / np.float32(1 << 24) - np.float32(0.5)
+    return vals, s
+
+
+# ---- the decode block's row-wise passes (config 5) ---------------------------
+
+def rms_norm_row(x, w, eps):
+    """norm_row with rms (src/nn.rs:128-143), f32 out."""
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    out = np.empty(x.size, np.float32)
+    lib().or_rms_norm_row(_p(x), _p(w), x.size, eps, _p(out))
+    return out
+
+
+def rms_norm_f16(x, w, eps, rows=1):
+    """nn::rms_norm into f16 (src/nn.rs:159): rows of len(w)."""
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    y = np.empty(x.size, np.uint16)
+    scratch = np.empty(w.size, np.float32)
+    lib().or_rms_norm_f16(_p(x), _p(w), rows, w.size, eps, _p(y), _p(scratch))
+    return y
+
+
+def rope_inv_freq(dim, base=10000.0):
+    """Rope::new without YaRN (examples/bonsai/model.rs:44-57)."""
+    out = np.empty(dim // 2, np.float32)
+    lib().or_rope_inv_freq(dim, base, _p(out))
+    return out
+
+
+def rope_angles(inv_freq, pos):
+    """Rope::angles (model.rs:86-93): (cos, sin) per frequency."""
+    inv_freq = _c(inv_freq, np.float32)
+    c = np.empty(inv_freq.size, np.float32)
+    s = np.empty(inv_freq.size, np.float32)
+    lib().or_rope_angles(_p(inv_freq), inv_freq.size, pos, _p(c), _p(s))
+    return c, s
+
+
+def rope_apply(x, cos_v, sin_v):
+    """Rope::apply (model.rs:95-107) on a copy of x (heads of 2*len(cos_v))."""
+    x = np.array(x, np.float32, copy=True)
+    cos_v = _c(cos_v, np.float32)
+    sin_v = _c(sin_v, np.float32)
+    lib().or_rope_apply(_p(x), x.size, _p(cos_v), _p(sin_v), cos_v.size)
+    return x
+
+
+def attention_kv_f16(q, k, v, length, heads, kv_heads, hd, scale):
+    """attention_kv_f16's portable one_row (src/kernels/kv_attention.rs:286-325):
+    q f32 [heads*hd], k/v f16 bits [length][kv_heads*hd]; returns f32."""
+    q = _c(q, np.float32)
+    k = _c(k, np.uint16)
+    v = _c(v, np.uint16)
+    out = np.empty(heads * hd, np.float32)
+    scores = np.empty(max(length, 1), np.float32)
+    qh = np.empty(hd, np.float32)
+    lib().or_attention_kv_f16(_p(q), _p(k), _p(v), length, heads, kv_heads, hd, scale, _p(out),
+                              _p(scores), _p(qh))
+    return out
+
+
+def glu_f16(both, m, n, gelu=False):
+    """glu (src/linear.rs:803-826) over m rows of 2n interleaved gate/up f16."""
+    both = _c(both, np.uint16)
+    y = np.empty(m * n, np.uint16)
+    lib().or_glu_f16(_p(y), _p(both), m, n, int(gelu))
+    return y
+
+
+def interleave32(g, u, n, k):
+    """GatedLinear's interleave (src/linear.rs:584-599) of two InOut k x n
+    arrays (any dtype): k x 2n, each 32-column chunk of g then of u."""
+    g = np.asarray(g).reshape(k, n)
+    u = np.asarray(u).reshape(k, n)
+    parts = []
+    for c0 in range(0, n, 32):
+        c1 = min(c0 + 32, n)
+        parts += [g[:, c0:c1], u[:, c0:c1]]
+    return np.concatenate(parts, axis=1)
+
+
+class Q4Lin:
+    """A 4-bit Linear as the reference's portable path runs it at one row
+    (Linear::forward -> matmul_q4_ep, src/linear.rs:533-552): the public
+    row-major arrays of Q4Weights (block 32, Scale form)."""
+
+    def __init__(self, quants, scales, n, k, block=32):
+        self.quants, self.scales, self.n, self.k, self.block = quants, scales, n, k, block
+
+    def forward(self, x16, m=1, nodes=(), act=None):
+        return matmul_q4_ep(x16, self.quants, self.scales, None, m, self.n, self.k, self.block,
+                            nodes, act)
+
+
+def block_decode(x, cache_k, cache_v, pos, p):
+    """One row of Block::accumulate (src/block.rs:90-106) with RoPE inserted as
+    examples/bonsai/model.rs:319-333 applies it (q and k rotated in f32 after
+    the qkv projection, k stored rotated; no q/k norm):
+      h = rms_norm(x, norm1) -> f16;  qkv = Q4 qkv(h) -> f16
+      q, k = rope(f32(q16), pos), rope(f32(k16), pos); cache[pos] = f16(k), v16
+      att = attention_kv_f16(q, K[0..=pos], V[0..=pos]) -> f16;  x += f32(out(att))
+      h = rms_norm(x, norm2) -> f16;  hid = glu(gate_up(h)) -> f16;  x += f32(down(hid))
+    x: f32 [d] (updated copy returned); cache_k / cache_v: f16 [cap][kv*hd]
+    (row pos written). p: dict of the block's parts (see tests)."""
+    d, H, KV, hd, eps = p["d"], p["heads"], p["kv_heads"], p["head_dim"], p["eps"]
+    x = np.array(x, np.float32, copy=True)
+    h = rms_norm_f16(x, p["norm1"], eps)
+    qkv = p["qkv"].forward(h)
+    ql, kl = H * hd, KV * hd
+    q32 = f16_to_f32(qkv[:ql])
+    k32 = f16_to_f32(qkv[ql:ql + kl])
+    if p.get("theta"):
+        cs, sn = rope_angles(rope_inv_freq(hd, p["theta"]), pos)
+        q32 = rope_apply(q32, cs, sn)
+        k32 = rope_apply(k32, cs, sn)
+    cache_k[pos] = f32_to_f16(k32)
+    cache_v[pos] = qkv[ql + kl:]
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    att = attention_kv_f16(q32, cache_k[:pos + 1], cache_v[:pos + 1], pos + 1, H, KV, hd, scale)
+    o = p["out"].forward(f32_to_f16(att))
+    x = (x + f16_to_f32(o)).astype(np.float32)
+    h = rms_norm_f16(x, p["norm2"], eps)
+    both = p["gate_up"].forward(h)
+    hid = glu_f16(both, 1, p["ffn"], p.get("gelu", False))
+    o = p["down"].forward(hid)
+    return (x + f16_to_f32(o)).astype(np.float32)
