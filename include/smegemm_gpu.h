@@ -162,6 +162,11 @@ int smg_q4_dequant(const smg_weights *q4, int to_bf16, smg_weights **out);
  * k, block) to 2n columns, each 32-column chunk of gate followed by the same
  * chunk of up; replaces Q1Weights::interleave (src/kernels/lowbit/q1.rs:146-185). */
 int smg_q4_permute_columns(const smg_weights *q4, const size_t *perm, smg_weights **out);
+/* smg_q1_interleave for Q4 (same n, k, block and form): the weights
+ * GatedLinear::quantize builds (src/linear.rs:601-619, 656-671), exactly, from
+ * the gate and up weights quantized on their own (Q4 blocks run along K, so a
+ * column's codes and scales do not depend on its neighbours). */
+int smg_q4_interleave(const smg_weights *gate, const smg_weights *up, smg_weights **out);
 int smg_q1_interleave(const smg_weights *gate, const smg_weights *up, smg_weights **out);
 
 /* A second device copy of a handle's weights (device-to-device; no host
@@ -264,6 +269,105 @@ int smg_lowbit_mopa_dev(size_t m, const smg_weights *w, uint16_t *dst, const uin
 int smg_packed_matmul_dev(size_t m, const smg_weights *b_pack, uint16_t *dst, long dst_cs,
                           long dst_rs, const uint16_t *lhs, long lhs_cs, long lhs_rs,
                           uint16_t beta_bits, const ep_desc16 *ep, int bf16, void *stream);
+
+/* ---- the decode block (src/block.rs path) ----------------------------------
+ * The model-level parts a Llama-style layer is built from, with the reference's
+ * names and argument meaning; device pointers, asynchronous on `stream`.
+ * Residual streams are f32, activations handed between parts f16, as in the
+ * reference (src/linear.rs:14-29). A part's calls on one stream are ordered by
+ * that stream; its scratch is the stream's own (the first call on a stream
+ * allocates it, so make one before capturing a HIP graph). */
+typedef struct smg_kv_cache smg_kv_cache;
+typedef struct smg_attn smg_attn;
+typedef struct smg_mlp smg_mlp;
+typedef struct smg_block smg_block;
+
+/* KvCache::new (src/kernels/kv_attention.rs:372-394): f16 keys and values for
+ * `capacity` positions of kv_heads*head_dim values each, zeroed, score scale
+ * 1/sqrt(head_dim). head_dim a multiple of 8 in 8..256, heads a positive
+ * multiple of kv_heads; SMG_EINVAL otherwise. On the current device. */
+int smg_kv_cache_create(size_t heads, size_t kv_heads, size_t head_dim, size_t capacity,
+                        smg_kv_cache **out);
+void smg_kv_cache_destroy(smg_kv_cache *c);
+/* len() / capacity() / scale() (kv_attention.rs:403-453). */
+int smg_kv_cache_info(const smg_kv_cache *c, size_t *len, size_t *capacity, float *scale);
+/* truncate (no-op past len) / clear (len 0) (kv_attention.rs:476-484). */
+int smg_kv_cache_truncate(smg_kv_cache *c, size_t len);
+/* with_scale (kv_attention.rs:396-400). */
+int smg_kv_cache_set_scale(smg_kv_cache *c, float scale);
+/* The device storage: keys and values, capacity rows of kv_heads*head_dim f16;
+ * keys() / values() (kv_attention.rs:522-531) are the first len rows. */
+int smg_kv_cache_storage(const smg_kv_cache *c, uint16_t **keys, uint16_t **values);
+/* The first len rows of the keys and / or values (either NULL) copied to
+ * device buffers of len*kv_heads*head_dim f16 (keys() / values()). */
+int smg_kv_cache_read_dev(const smg_kv_cache *c, uint16_t *keys, uint16_t *values, void *stream);
+/* extend / push (kv_attention.rs:489-519) with rows rows of f16 keys and values
+ * (device); SMG_EINVAL ("KvCache full") when they do not fit. */
+int smg_kv_cache_extend_dev(smg_kv_cache *c, const uint16_t *k, const uint16_t *v, size_t rows,
+                            void *stream);
+/* attend (kv_attention.rs:537-552): one query row (heads*head_dim f32) against
+ * every cached position into out (heads*head_dim f32); SMG_EINVAL when empty. */
+int smg_kv_cache_attend_dev(const smg_kv_cache *c, const float *q, float *out, void *stream);
+/* attention_kv_f16 (kv_attention.rs:29-78) on device arrays: q f32
+ * [heads*head_dim], k / v f16 [len][kv_heads*head_dim], out f32. Replaces the
+ * reference's attn_kv_f16 kernel (src/ffi.rs). */
+int smg_attention_kv_f16_dev(const float *q, const uint16_t *k, const uint16_t *v, size_t len,
+                             size_t heads, size_t kv_heads, size_t head_dim, float scale, float *out,
+                             void *stream);
+
+/* nn::rms_norm (src/nn.rs:147-161): rows of dim f32 x to f16 y, weight f32
+ * [dim]: x / sqrt(mean(x^2) + eps) * weight. */
+int smg_rms_norm_f16_dev(const float *x, const float *weight, size_t rows, size_t dim, float eps,
+                         uint16_t *y, void *stream);
+/* GatedLinear's glu (src/linear.rs:804-826): m rows of 2n f16 values, gate and
+ * up interleaved 32 columns at a time, to y = f16(act(gate) * up) [m][n];
+ * act EP_ACT_SILU or EP_ACT_GELU (Gate::Silu / Gate::Gelu). */
+int smg_glu_f16_dev(const uint16_t *both, size_t m, size_t n, uint32_t act, uint16_t *y,
+                    void *stream);
+/* Linear::accumulate for 4-bit weights (src/linear.rs:425-432): y (f32, m x n)
+ * += f32(f16(x @ W)), x f16 m x k. */
+int smg_q4_accumulate_dev(size_t m, const smg_weights *w, float *y, const uint16_t *x, void *stream);
+
+/* SelfAttention::new (src/self_attention.rs:86-130): qkv Q4 with
+ * (heads + 2 kv_heads)*head_dim outputs [q | k | v], out Q4 with heads*head_dim
+ * inputs; rope_theta > 0 adds the NeoX rotary embedding that
+ * examples/bonsai/model.rs:30-99 applies to q and k (base rope_theta, no
+ * scaling), 0 none, as the library's SelfAttention. The attention takes over
+ * both handles (as the Rust constructor moves its Linears): on success the
+ * caller no longer destroys them. head_dim a multiple of 16 with RoPE. */
+int smg_attn_create(smg_weights *qkv, smg_weights *out, size_t heads, size_t kv_heads,
+                    size_t head_dim, double rope_theta, smg_attn **attn);
+void smg_attn_destroy(smg_attn *a);
+/* SelfAttention::accumulate (self_attention.rs:148-183): y (f32 m x width) +=
+ * out(attention(qkv(x))) for x f16 (m x width) at the cache's next position,
+ * which it appends. m = 1 (decode); SMG_EINVAL when the cache is full or its
+ * heads differ. */
+int smg_attn_accumulate_dev(smg_attn *a, const uint16_t *x, smg_kv_cache *cache, float *y, size_t m,
+                            void *stream);
+
+/* Mlp::gated(GatedLinear, down) (gated != 0: up holds 2*hidden outputs, gate
+ * and up interleaved 32 columns at a time as GatedLinear stores them,
+ * src/linear.rs:601-619) or Mlp::new(up, act, down) (src/mlp.rs:62-86); act
+ * EP_ACT_SILU or EP_ACT_GELU. Takes over up and down on success. */
+int smg_mlp_create(smg_weights *up, smg_weights *down, uint32_t act, int gated, smg_mlp **mlp);
+void smg_mlp_destroy(smg_mlp *m);
+/* Mlp::accumulate (src/mlp.rs:113-149): y (f32 m x n) += down(act(up(x))) for
+ * x f16 m x k: the up GEMV with the activation (gated: glu) at its store, then
+ * the down GEMV adding into y -- two kernels for up to 8 rows. */
+int smg_mlp_accumulate_dev(smg_mlp *m, const uint16_t *x, float *y, size_t rows, void *stream);
+
+/* Block::new(Norm::rms(norm1, eps1), attn, Norm::rms(norm2, eps2), mlp)
+ * (src/block.rs:49-66; norms f32 [d], copied): takes over attn and mlp on
+ * success (destroying the block destroys them). */
+int smg_block_create(const float *norm1, float eps1, const float *norm2, float eps2, size_t d,
+                     smg_attn *attn, smg_mlp *mlp, smg_block **block);
+void smg_block_destroy(smg_block *b);
+/* Block::accumulate (block.rs:90-106): x (f32, rows x d, device) += the
+ * attention half, then += the MLP half, at the cache's next position, which it
+ * appends. rows = 1 (decode): six launches -- RMSNorm + qkv + RoPE + cache
+ * append, attention splits, their merge, out + residual, RMSNorm + gate/up +
+ * glu, down + residual. */
+int smg_block_accumulate_dev(smg_block *b, float *x, smg_kv_cache *cache, size_t rows, void *stream);
 
 /* ---- runtime --------------------------------------------------------------- */
 /* 1 when a gfx950 device is present and this library's kernels load on it. */

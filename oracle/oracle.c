@@ -706,15 +706,15 @@ void or_q1_quantize(const float *w, int layout, size_t n, size_t k, size_t block
 
 /* ------------------------------------------------------------------------ */
 /* The decode block's row-wise passes (config 5): the portable bodies of     */
-/* nn::rms_norm (src/nn.rs:21-32,98-144,159), attention_kv_f16's one_row      */
-/* (src/kernels/kv_attention.rs:286-325), GatedLinear's glu                   */
-/* (src/linear.rs:803-826) and the NeoX RoPE of examples/bonsai/model.rs:31-107 */
+/* nn::rms_norm (src/nn.rs:22-32,127-144,159), attention_kv_f16's one_row      */
+/* (src/kernels/kv_attention.rs:282-325), GatedLinear's glu                   */
+/* (src/linear.rs:804-826) and the NeoX RoPE of examples/bonsai/model.rs:30-99 */
 /* (no YaRN scaling: mscale 1). Rust never contracts a*b+c (this file is built */
 /* with -ffp-contract=off) and its f32 exp / tanh / sin / cos / f64 powf are  */
 /* the platform libm's (glibc here), as these calls are.                     */
 /* ------------------------------------------------------------------------ */
 
-/* norm_row with rms = true (nn.rs:128-143): lane_sum (nn.rs:21-32) keeps 8
+/* norm_row with rms = true (nn.rs:127-144): lane_sum (nn.rs:22-32) keeps 8
  * lane accumulators over whole chunks of 8, sums the tail in order, then adds
  * the 8 lanes in order and the tail; r = 1 / sqrt(mean + eps) in f32; each
  * output is (v - 0) * r * w + 0 (mean 0, no bias), left to right. */
@@ -748,14 +748,14 @@ void or_rms_norm_f16(const float *x, const float *w, size_t rows, size_t dim, fl
     }
 }
 
-/* Rope::new without YaRN (model.rs:44-57): inv_freq[i] = (1 / base^(2i/dim))
+/* Rope::new without YaRN (model.rs:38-51): inv_freq[i] = (1 / base^(2i/dim))
  * in f64, then to f32. */
 void or_rope_inv_freq(size_t dim, double base, float *inv_freq) {
     for (size_t i = 0; i < dim / 2; i++)
         inv_freq[i] = (float)(1.0 / pow(base, (double)(2 * i) / (double)dim));
 }
 
-/* Rope::angles (model.rs:86-93): (pos as f32 * f).sin_cos(), times mscale 1. */
+/* Rope::angles (model.rs:77-85): (pos as f32 * f).sin_cos(), times mscale 1. */
 void or_rope_angles(const float *inv_freq, size_t half, size_t pos, float *cos_out,
                     float *sin_out) {
     for (size_t i = 0; i < half; i++) {
@@ -765,7 +765,7 @@ void or_rope_angles(const float *inv_freq, size_t half, size_t pos, float *cos_o
     }
 }
 
-/* Rope::apply (model.rs:95-107): each 2*half-wide head's halves rotated
+/* Rope::apply (model.rs:87-99): each 2*half-wide head's halves rotated
  * against each other: x1' = u c - v s, x2' = v c + u s. */
 void or_rope_apply(float *x, size_t len, const float *cos_v, const float *sin_v, size_t half) {
     for (size_t h0 = 0; h0 + 2 * half <= len; h0 += 2 * half)
@@ -776,7 +776,7 @@ void or_rope_apply(float *x, size_t len, const float *cos_v, const float *sin_v,
         }
 }
 
-/* one_row, the portable attention_kv_f16 (kv_attention.rs:286-325): per query
+/* one_row, the portable attention_kv_f16 (kv_attention.rs:282-325): per query
  * head h (KV head h / (heads / kv_heads)): q rounded to f16 after the scale,
  * scores as f32 sums in depth order, the running max by maxNum, exp(s - max)
  * summed in key order, values accumulated in key order, then divided by the
@@ -808,7 +808,7 @@ void or_attention_kv_f16(const float *q, const uint16_t *k, const uint16_t *v, s
     }
 }
 
-/* glu (linear.rs:803-826): m rows of 2n interleaved outputs -- each 32-column
+/* glu (linear.rs:804-826): m rows of 2n interleaved outputs -- each 32-column
  * chunk (the last w < 32 wide) is w gate columns then w up columns -- to
  * y = f16(act(gate) * up), act in f32: silu g / (1 + exp(-g)), or (gelu != 0)
  * the tanh form 0.5 g (1 + tanh(0.7978846 (g + 0.044715 g g g))). */

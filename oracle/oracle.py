@@ -380,7 +380,7 @@ def lcg_fill_f32(seed: int, length: int):
 # ---- the decode block's row-wise passes (config 5) ---------------------------
 
 def rms_norm_row(x, w, eps):
-    """norm_row with rms (src/nn.rs:128-143), f32 out."""
+    """norm_row with rms (src/nn.rs:127-144), f32 out."""
     x = _c(x, np.float32)
     w = _c(w, np.float32)
     out = np.empty(x.size, np.float32)
@@ -399,14 +399,14 @@ def rms_norm_f16(x, w, eps, rows=1):
 
 
 def rope_inv_freq(dim, base=10000.0):
-    """Rope::new without YaRN (examples/bonsai/model.rs:44-57)."""
+    """Rope::new without YaRN (examples/bonsai/model.rs:38-51)."""
     out = np.empty(dim // 2, np.float32)
     lib().or_rope_inv_freq(dim, base, _p(out))
     return out
 
 
 def rope_angles(inv_freq, pos):
-    """Rope::angles (model.rs:86-93): (cos, sin) per frequency."""
+    """Rope::angles (model.rs:77-85): (cos, sin) per frequency."""
     inv_freq = _c(inv_freq, np.float32)
     c = np.empty(inv_freq.size, np.float32)
     s = np.empty(inv_freq.size, np.float32)
@@ -415,7 +415,7 @@ def rope_angles(inv_freq, pos):
 
 
 def rope_apply(x, cos_v, sin_v):
-    """Rope::apply (model.rs:95-107) on a copy of x (heads of 2*len(cos_v))."""
+    """Rope::apply (model.rs:87-99) on a copy of x (heads of 2*len(cos_v))."""
     x = np.array(x, np.float32, copy=True)
     cos_v = _c(cos_v, np.float32)
     sin_v = _c(sin_v, np.float32)
@@ -424,7 +424,7 @@ def rope_apply(x, cos_v, sin_v):
 
 
 def attention_kv_f16(q, k, v, length, heads, kv_heads, hd, scale):
-    """attention_kv_f16's portable one_row (src/kernels/kv_attention.rs:286-325):
+    """attention_kv_f16's portable one_row (src/kernels/kv_attention.rs:282-325):
     q f32 [heads*hd], k/v f16 bits [length][kv_heads*hd]; returns f32."""
     q = _c(q, np.float32)
     k = _c(k, np.uint16)
@@ -438,7 +438,7 @@ def attention_kv_f16(q, k, v, length, heads, kv_heads, hd, scale):
 
 
 def glu_f16(both, m, n, gelu=False):
-    """glu (src/linear.rs:803-826) over m rows of 2n interleaved gate/up f16."""
+    """glu (src/linear.rs:804-826) over m rows of 2n interleaved gate/up f16."""
     both = _c(both, np.uint16)
     y = np.empty(m * n, np.uint16)
     lib().or_glu_f16(_p(y), _p(both), m, n, int(gelu))
@@ -446,7 +446,7 @@ def glu_f16(both, m, n, gelu=False):
 
 
 def interleave32(g, u, n, k):
-    """GatedLinear's interleave (src/linear.rs:584-599) of two InOut k x n
+    """GatedLinear's interleave (src/linear.rs:601-619) of two InOut k x n
     arrays (any dtype): k x 2n, each 32-column chunk of g then of u."""
     g = np.asarray(g).reshape(k, n)
     u = np.asarray(u).reshape(k, n)
@@ -470,16 +470,18 @@ class Q4Lin:
                             nodes, act)
 
 
-def block_decode(x, cache_k, cache_v, pos, p):
+def block_decode(x, cache_k, cache_v, pos, p, parts=None):
     """One row of Block::accumulate (src/block.rs:90-106) with RoPE inserted as
-    examples/bonsai/model.rs:319-333 applies it (q and k rotated in f32 after
+    examples/bonsai/model.rs:329-349 applies it (q and k rotated in f32 after
     the qkv projection, k stored rotated; no q/k norm):
       h = rms_norm(x, norm1) -> f16;  qkv = Q4 qkv(h) -> f16
       q, k = rope(f32(q16), pos), rope(f32(k16), pos); cache[pos] = f16(k), v16
       att = attention_kv_f16(q, K[0..=pos], V[0..=pos]) -> f16;  x += f32(out(att))
       h = rms_norm(x, norm2) -> f16;  hid = glu(gate_up(h)) -> f16;  x += f32(down(hid))
     x: f32 [d] (updated copy returned); cache_k / cache_v: f16 [cap][kv*hd]
-    (row pos written). p: dict of the block's parts (see tests)."""
+    (row pos written). p: dict of the block's parts (see tests). parts: a
+    dict that receives the two f16 terms added to the residual, as f32
+    ("attn", "mlp")."""
     d, H, KV, hd, eps = p["d"], p["heads"], p["kv_heads"], p["head_dim"], p["eps"]
     x = np.array(x, np.float32, copy=True)
     h = rms_norm_f16(x, p["norm1"], eps)
@@ -496,9 +498,36 @@ def block_decode(x, cache_k, cache_v, pos, p):
     scale = np.float32(1.0) / np.sqrt(np.float32(hd))
     att = attention_kv_f16(q32, cache_k[:pos + 1], cache_v[:pos + 1], pos + 1, H, KV, hd, scale)
     o = p["out"].forward(f32_to_f16(att))
+    if parts is not None:
+        parts["attn"] = f16_to_f32(o)
     x = (x + f16_to_f32(o)).astype(np.float32)
     h = rms_norm_f16(x, p["norm2"], eps)
     both = p["gate_up"].forward(h)
     hid = glu_f16(both, 1, p["ffn"], p.get("gelu", False))
     o = p["down"].forward(hid)
+    if parts is not None:
+        parts["mlp"] = f16_to_f32(o)
     return (x + f16_to_f32(o)).astype(np.float32)
+
+
+def q4_interleave32(gq, gs, uq, us, n, k, block=32):
+    """The Q4 row-major arrays (quants, scales) of gate | up interleaved 32
+    columns at a time, as GatedLinear::quantize lays out its 2n outputs
+    (src/linear.rs:601-619): every column keeps its codes and scales (Q4 blocks
+    run along K), so this is the quantization of the interleaved weights."""
+    nbk = -(-k // block)
+    if n % 32 == 0:
+        # 32 columns of a depth are 16 whole bytes: move bytes, not nibbles
+        g = np.asarray(gq, np.uint8).reshape(k, n // 32, 1, 16)
+        u = np.asarray(uq, np.uint8).reshape(k, n // 32, 1, 16)
+        quants = np.ascontiguousarray(np.concatenate([g, u], axis=2)).ravel()
+    else:
+        idx = np.arange(k * n)
+
+        def nibs(q):
+            return np.where(idx % 2 == 0, q[idx // 2] & 15, q[idx // 2] >> 4).astype(np.uint8).reshape(k, n)
+        both = interleave32(nibs(gq), nibs(uq), n, k).ravel()
+        lo, hi = both[0::2], np.append(both[1::2], np.uint8(0))[:both[0::2].size]
+        quants = (lo | (hi << 4)).astype(np.uint8)
+    sc = interleave32(np.asarray(gs).reshape(n, nbk).T, np.asarray(us).reshape(n, nbk).T, n, nbk).T.ravel()
+    return quants, np.ascontiguousarray(sc)

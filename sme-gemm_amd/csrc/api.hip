@@ -8,6 +8,7 @@
 
 #include <atomic>
 #include <chrono>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -569,6 +570,272 @@ float half_bits_to_float(uint16_t h, bool bf16) {
 
 }  // namespace
 
+// ---- decode block handles ------------------------------------------------------
+struct smg_kv_cache {
+    int device;
+    size_t heads, kv_heads, hd, cap, len;
+    float scale;
+    uint16_t *k, *v;  // [cap][kv_heads * hd]
+};
+
+struct smg_attn {
+    int device;
+    smg_weights *qkv;  // columns in the fused store's order: tiles of RoPE pairs
+    smg_weights *out;
+    size_t heads, kv_heads, hd;
+    double theta;      // 0: no RoPE
+    std::vector<float> inv_freq;
+    float *rope = nullptr;  // device: cos [rope_cap][hd/2], then sin [rope_cap][hd/2]
+    size_t rope_cap = 0;
+    std::vector<float *> retired;  // outgrown tables, kept: queued work may read them
+    std::mutex mu;
+};
+
+struct smg_mlp {
+    int device;
+    smg_weights *up;  // gated: tiles of 8 gate + the same 8 up columns (zero-padded)
+    smg_weights *down;
+    uint32_t act;
+    bool gated;
+    size_t hidden;
+};
+
+struct smg_block {
+    int device;
+    float *norm1, *norm2;  // device f32 [d]
+    size_t d;
+    float eps1, eps2;
+    smg_attn *attn;
+    smg_mlp *mlp;
+};
+
+namespace {
+
+// Device column p of an attention's qkv: tile p/16 of head p/hd holds columns
+// 8q..8q+7 and hd/2+8q..hd/2+8q+7 (q = tile within the head), so each RoPE
+// pair (i, i + hd/2) sits in one workgroup's tile (lanes c and c ^ 8).
+std::vector<int32_t> qkv_store_order(size_t nq, size_t hd) {
+    std::vector<int32_t> cols(nq);
+    const size_t half = hd / 2;
+    for (size_t p = 0; p < nq; p++) {
+        const size_t head = p / hd, qt = (p % hd) / 16, cc = p % 16;
+        cols[p] = (int32_t)(head * hd + (cc < 8 ? 8 * qt + cc : half + 8 * qt + cc - 8));
+    }
+    return cols;
+}
+
+// Device column order of a gated MLP's up: tiles of 8 gate columns then the
+// same 8 up columns, from GatedLinear's interleave (32 gate, 32 up, ...; the
+// last chunk w < 32 wide; src/linear.rs:601-619); past `hidden`, zero columns.
+std::vector<int32_t> glu_store_order(size_t hidden) {
+    const size_t tiles = (hidden + 7) / 8;
+    std::vector<int32_t> cols(16 * tiles, -1);
+    for (size_t j = 0; j < hidden; j++) {
+        const size_t c0 = j / 32 * 32, w = std::min<size_t>(32, hidden - c0);
+        cols[16 * (j / 8) + j % 8] = (int32_t)(2 * c0 + (j - c0));          // gate j
+        cols[16 * (j / 8) + 8 + j % 8] = (int32_t)(2 * c0 + w + (j - c0));  // up j
+    }
+    return cols;
+}
+
+// The attention's RoPE table covering positions [0, cap): cos and sin of
+// (pos as f32 * inv_freq[i]) in f32 (examples/bonsai/model.rs:77-85), computed
+// here on the host as the reference computes its angles. A table that is
+// outgrown is retired, not freed.
+int ensure_rope(smg_attn *a, size_t cap) {
+    if (a->theta <= 0.0) return SMG_OK;
+    std::lock_guard<std::mutex> lk(a->mu);
+    if (a->rope_cap >= cap) return SMG_OK;
+    const size_t half = a->hd / 2, ncap = std::max(cap, 2 * a->rope_cap);
+    std::vector<float> tab(2 * ncap * half);
+    for (size_t pos = 0; pos < ncap; pos++)
+        for (size_t i = 0; i < half; i++) {
+            const float ang = (float)pos * a->inv_freq[i];
+            tab[pos * half + i] = std::cos(ang);
+            tab[ncap * half + pos * half + i] = std::sin(ang);
+        }
+    float *d = nullptr;
+    HIP_TRY(hipSetDevice(a->device), SMG_EHIP);
+    if (hipMalloc(&d, tab.size() * 4) != hipSuccess) return fail(SMG_ENOMEM, "rope table hipMalloc");
+    hipError_t e = hipMemcpy(d, tab.data(), tab.size() * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(d);
+        return fail(SMG_EHIP, "rope table upload", e);
+    }
+    if (a->rope) a->retired.push_back(a->rope);
+    a->rope = d;
+    a->rope_cap = ncap;
+    return SMG_OK;
+}
+
+// One call's device scratch, carved from the stream's pool buffer.
+struct DecodeScratch {
+    uint16_t *q16, *att16, *h16, *hid;
+    float *po;
+    float2 *pml;
+};
+int decode_scratch(int device, void *stream, size_t qlen, size_t nsplit, size_t heads, size_t h16_elems,
+                   size_t hid_elems, DecodeScratch *sc, size_t base = 0) {
+    const size_t a = 256;
+    const size_t sizes[6] = {round_up(qlen * 2, a), round_up(qlen * 2, a), round_up(h16_elems * 2, a),
+                             round_up(hid_elems * 2, a), round_up(nsplit * qlen * 4, a),
+                             round_up(nsplit * heads * 8, a)};
+    size_t total = 0;
+    for (size_t z : sizes) total += z;
+    uint8_t *p = (uint8_t *)dev_pool().get(device, stream, base + total);
+    if (!p) return fail(SMG_ENOMEM, "decode scratch hipMalloc");
+    p += base;  // what a caller keeps below `base` stays untouched
+    sc->q16 = (uint16_t *)p;
+    p += sizes[0];
+    sc->att16 = (uint16_t *)p;
+    p += sizes[1];
+    sc->h16 = (uint16_t *)p;
+    p += sizes[2];
+    sc->hid = (uint16_t *)p;
+    p += sizes[3];
+    sc->po = (float *)p;
+    p += sizes[4];
+    sc->pml = (float2 *)p;
+    return SMG_OK;
+}
+
+int check_cache(const smg_attn *a, const smg_kv_cache *c, size_t rows) {
+    if (!c) return fail(SMG_EINVAL, "null cache");
+    if (c->heads != a->heads || c->kv_heads != a->kv_heads || c->hd != a->hd)
+        return fail(SMG_EINVAL, "the cache's heads match the block's");
+    if (c->device != a->device) return fail(SMG_EINVAL, "the cache is on another device");
+    if (c->len + rows > c->cap) return fail(SMG_EINVAL, "KvCache full: the rows do not fit in the cache");
+    return SMG_OK;
+}
+
+// The attention half at one row: qkv (from x16, or the RMS norm of the f32 row
+// nx with weights nw), RoPE and the cache append at the store, attention, out
+// projection added into y. Appends the cache row.
+int attn_step(smg_attn *a, smg_kv_cache *c, const uint16_t *x16, const float *nx, const float *nw, float eps,
+              float *y, void *stream, size_t base = 0) {
+    int rc = check_cache(a, c, 1);
+    if (rc) return rc;
+    if ((rc = ensure_rope(a, c->cap))) return rc;
+    const size_t pos = c->len, ld = a->kv_heads * a->hd, qlen = a->heads * a->hd, half = a->hd / 2;
+    const size_t nsplit = attn_splits(pos + 1);
+    DecodeScratch sc;
+    if ((rc = decode_scratch(a->device, stream, qlen, nsplit, a->heads, 0, 0, &sc, base))) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    BlkArgs b = {};
+    b.nx = nx;
+    b.nw = nw;
+    b.eps = eps;
+    b.q_out = sc.q16;
+    b.k_row = c->k + pos * ld;
+    b.v_row = c->v + pos * ld;
+    if (a->theta > 0.0) {
+        b.cs = a->rope + pos * half;
+        b.sn = a->rope + a->rope_cap * half + pos * half;
+    }
+    b.scale = c->scale;
+    b.heads = (uint32_t)a->heads;
+    b.kv_heads = (uint32_t)a->kv_heads;
+    b.hd = (uint32_t)a->hd;
+    hipError_t e = launch_blk_gemv(a->qkv->d, 1, x16, b, BS_QKV, nx != nullptr, s);
+    if (e != hipSuccess) return fail(SMG_EHIP, "qkv projection", e);
+    AttnArgs at = {};
+    at.q = sc.q16;
+    at.k = c->k;
+    at.v = c->v;
+    at.po = sc.po;
+    at.pml = sc.pml;
+    at.len = (uint32_t)(pos + 1);
+    at.ld = (uint32_t)ld;
+    at.hd = (uint32_t)a->hd;
+    at.heads = (uint32_t)a->heads;
+    at.group = (uint32_t)(a->heads / a->kv_heads);
+    if ((e = launch_attention(at, sc.att16, true, s)) != hipSuccess) return fail(SMG_EHIP, "attention", e);
+    BlkArgs r = {};
+    r.x = y;
+    if ((e = launch_blk_gemv(a->out->d, 1, sc.att16, r, BS_RESID, false, s)) != hipSuccess)
+        return fail(SMG_EHIP, "out projection", e);
+    c->len = pos + 1;
+    return SMG_OK;
+}
+
+// The MLP half: y += down(act(up(x))) for `rows` rows of x16, or (nx) of the
+// RMS norm of the f32 rows nx with weights nw.
+int mlp_step(smg_mlp *m, const uint16_t *x16, const float *nx, const float *nw, float eps, float *y,
+             size_t rows, void *stream) {
+    const size_t k = m->up->d.k, d_out = m->down->d.n;
+    const bool fused_norm = nx && rows == 1 && m->gated && k <= 4096 && k % 8 == 0;
+    DecodeScratch sc;
+    const size_t both = m->gated ? m->up->d.n : 0;
+    int rc = decode_scratch(m->device, stream, 0, 0, 0, (nx && !fused_norm ? rows * k : 0) + rows * both +
+                                                             rows * d_out,
+                            rows * m->hidden, &sc);
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = hipSuccess;
+    if (nx && !fused_norm) {  // the norm as its own pass (nn::rms_norm)
+        if ((e = launch_rms_norm(nx, nw, rows, k, eps, sc.h16, s)) != hipSuccess) return fail(SMG_EHIP, "rms_norm", e);
+        x16 = sc.h16;
+    }
+    uint16_t *spare = sc.h16 + (nx && !fused_norm ? rows * k : 0);  // [rows][both], then [rows][d_out]
+    if (rows <= 8 && m->gated) {
+        BlkArgs b = {};
+        b.nx = fused_norm ? nx : nullptr;
+        b.nw = nw;
+        b.eps = eps;
+        b.y = sc.hid;
+        b.act = m->act;
+        b.nh = (uint32_t)m->hidden;
+        if ((e = launch_blk_gemv(m->up->d, rows, x16, b, BS_GLU, fused_norm, s)) != hipSuccess)
+            return fail(SMG_EHIP, "gate/up projection", e);
+    } else {
+        // Mlp::new's up with its activation at the store, or many rows: the
+        // GEMM, then (gated) glu over its tiles
+        EpArgs ea;
+        std::memset(&ea, 0, sizeof(ea));
+        if (!m->gated) {
+            ea.n_nodes = 1;
+            ea.nodes[0].op = EP_OP_ACT;
+            ea.nodes[0].aux = m->act;
+            ea.fam[0] = (uint8_t)ep_family(EP_OP_ACT);
+            ea.cls[0] = (uint8_t)ep_class(EP_OP_ACT);
+        }
+        uint16_t *dst = m->gated ? spare : sc.hid;
+        if ((e = run_q4(m->up->d, rows, dst, x16, ea, false, s)) != hipSuccess) return fail(SMG_EHIP, "up projection", e);
+        if (m->gated && (e = launch_glu(dst, rows, m->hidden, m->act, 1, sc.hid, s)) != hipSuccess)
+            return fail(SMG_EHIP, "glu", e);
+    }
+    if (rows <= 8) {
+        BlkArgs r = {};
+        r.x = y;
+        if ((e = launch_blk_gemv(m->down->d, rows, sc.hid, r, BS_RESID, false, s)) != hipSuccess)
+            return fail(SMG_EHIP, "down projection", e);
+    } else {
+        uint16_t *out16 = spare + rows * both;
+        if ((e = run_q4(m->down->d, rows, out16, sc.hid, EpArgs{}, false, s)) != hipSuccess)
+            return fail(SMG_EHIP, "down projection", e);
+        if ((e = launch_add_f16(out16, rows * d_out, y, s)) != hipSuccess) return fail(SMG_EHIP, "residual add", e);
+    }
+    return SMG_OK;
+}
+
+void destroy_attn(smg_attn *a) {
+    if (!a) return;
+    (void)hipSetDevice(a->device);
+    destroy(a->qkv);
+    destroy(a->out);
+    if (a->rope) (void)hipFree(a->rope);
+    for (float *p : a->retired) (void)hipFree(p);
+    delete a;
+}
+void destroy_mlp(smg_mlp *m) {
+    if (!m) return;
+    destroy(m->up);
+    destroy(m->down);
+    delete m;
+}
+
+}  // namespace
+
 int smg::report(int code, const char *what) { return fail(code, what); }
 
 // ============================================================================
@@ -671,24 +938,34 @@ int smg_q4_permute_columns(const smg_weights *q4, const size_t *perm, smg_weight
     return gather_columns(q4, nullptr, cols, out);
 }
 
-int smg_q1_interleave(const smg_weights *gate, const smg_weights *up, smg_weights **out) {
-    int rc = check_kind(gate, W_Q1);
-    if (!rc) rc = check_kind(up, W_Q1);
+// GatedLinear's 32-column interleave of two weight sets of one kind
+// (src/linear.rs:601-619, lowbit/q1.rs:160-182): 32 of gate, then 32 of up.
+static int interleave_kind(int kind, const smg_weights *gate, const smg_weights *up, smg_weights **out) {
+    int rc = check_kind(gate, kind);
+    if (!rc) rc = check_kind(up, kind);
     if (rc) return rc;
     if (!out) return fail(SMG_EINVAL, "null output");
     const WDev &g = gate->d, &u = up->d;
-    if (g.n != u.n || g.k != u.k || g.block != u.block)
+    if (g.n != u.n || g.k != u.k || g.block != u.block || (g.mins == nullptr) != (u.mins == nullptr))
         return fail(SMG_EINVAL, "gate and up have the same shape and block size");
     if (gate->device != up->device) return fail(SMG_EINVAL, "gate and up are on different devices");
     if (g.n >= (size_t)1 << 29) return fail(SMG_EINVAL, "too many columns to interleave");
     std::vector<int32_t> cols;
     cols.reserve(2 * g.n);
-    for (size_t c0 = 0; c0 < g.n; c0 += 32) {  // q1.rs:160-182: 32 of gate, then 32 of up
+    for (size_t c0 = 0; c0 < g.n; c0 += 32) {
         const size_t c1 = std::min(c0 + 32, g.n);
         for (size_t j = c0; j < c1; j++) cols.push_back((int32_t)j);
         for (size_t j = c0; j < c1; j++) cols.push_back((int32_t)j | (1 << 30));
     }
     return gather_columns(gate, up, cols, out);
+}
+
+int smg_q1_interleave(const smg_weights *gate, const smg_weights *up, smg_weights **out) {
+    return interleave_kind(W_Q1, gate, up, out);
+}
+
+int smg_q4_interleave(const smg_weights *gate, const smg_weights *up, smg_weights **out) {
+    return interleave_kind(W_Q4, gate, up, out);
 }
 
 void smg_weights_destroy(smg_weights *w) { destroy(w); }
@@ -962,6 +1239,312 @@ int smg_packed_matmul_dev(size_t m, const smg_weights *b, uint16_t *dst, long ds
                                half_bits_to_float(beta_bits, bf16 != 0), ea, bf16 != 0,
                                (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_packed_matmul_dev", e);
+}
+
+// ---- decode block ---------------------------------------------------------------
+
+static bool head_shape_ok(size_t heads, size_t kv_heads, size_t hd) {
+    return hd % 8 == 0 && hd >= 8 && hd <= 256 && kv_heads > 0 && heads > 0 && heads % kv_heads == 0;
+}
+
+int smg_kv_cache_create(size_t heads, size_t kv_heads, size_t head_dim, size_t capacity,
+                        smg_kv_cache **out) {
+    if (!out) return fail(SMG_EINVAL, "null output");
+    if (!head_shape_ok(heads, kv_heads, head_dim))
+        return fail(SMG_EINVAL, "head_dim must be a multiple of 8 in 8..=256 and heads a positive multiple of kv_heads");
+    if (!smg_available()) return fail(SMG_ENODEV, "no gfx950 device");
+    smg_kv_cache *c = new smg_kv_cache();
+    (void)hipGetDevice(&c->device);
+    c->heads = heads;
+    c->kv_heads = kv_heads;
+    c->hd = head_dim;
+    c->cap = capacity;
+    c->len = 0;
+    c->scale = 1.0f / std::sqrt((float)head_dim);  // kv_attention.rs:392
+    c->k = c->v = nullptr;
+    const size_t bytes = std::max<size_t>(capacity * kv_heads * head_dim * 2, 16);
+    if (hipMalloc((void **)&c->k, bytes) != hipSuccess || hipMalloc((void **)&c->v, bytes) != hipSuccess ||
+        hipMemset(c->k, 0, bytes) != hipSuccess || hipMemset(c->v, 0, bytes) != hipSuccess) {
+        smg_kv_cache_destroy(c);
+        return fail(SMG_ENOMEM, "KvCache hipMalloc");
+    }
+    *out = c;
+    return SMG_OK;
+}
+
+void smg_kv_cache_destroy(smg_kv_cache *c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->k) (void)hipFree(c->k);
+    if (c->v) (void)hipFree(c->v);
+    delete c;
+}
+
+int smg_kv_cache_info(const smg_kv_cache *c, size_t *len, size_t *capacity, float *scale) {
+    if (!c) return fail(SMG_EINVAL, "null cache");
+    if (len) *len = c->len;
+    if (capacity) *capacity = c->cap;
+    if (scale) *scale = c->scale;
+    return SMG_OK;
+}
+
+int smg_kv_cache_truncate(smg_kv_cache *c, size_t len) {
+    if (!c) return fail(SMG_EINVAL, "null cache");
+    c->len = std::min(c->len, len);
+    return SMG_OK;
+}
+
+int smg_kv_cache_set_scale(smg_kv_cache *c, float scale) {
+    if (!c) return fail(SMG_EINVAL, "null cache");
+    c->scale = scale;
+    return SMG_OK;
+}
+
+int smg_kv_cache_storage(const smg_kv_cache *c, uint16_t **keys, uint16_t **values) {
+    if (!c) return fail(SMG_EINVAL, "null cache");
+    if (keys) *keys = c->k;
+    if (values) *values = c->v;
+    return SMG_OK;
+}
+
+int smg_kv_cache_read_dev(const smg_kv_cache *c, uint16_t *keys, uint16_t *values, void *stream) {
+    if (!c) return fail(SMG_EINVAL, "null cache");
+    const size_t bytes = c->len * c->kv_heads * c->hd * 2;
+    if (bytes && keys)
+        HIP_TRY(hipMemcpyAsync(keys, c->k, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), SMG_EHIP);
+    if (bytes && values)
+        HIP_TRY(hipMemcpyAsync(values, c->v, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), SMG_EHIP);
+    return SMG_OK;
+}
+
+int smg_kv_cache_extend_dev(smg_kv_cache *c, const uint16_t *k, const uint16_t *v, size_t rows,
+                            void *stream) {
+    if (!c) return fail(SMG_EINVAL, "null cache");
+    if (rows == 0 || !k || !v)
+        return fail(SMG_EINVAL, "k and v hold the same whole number of kv_heads * head_dim rows");
+    if (c->len + rows > c->cap) return fail(SMG_EINVAL, "KvCache full: the rows do not fit in the cache");
+    const size_t ld = c->kv_heads * c->hd;
+    HIP_TRY(hipMemcpyAsync(c->k + c->len * ld, k, rows * ld * 2, hipMemcpyDeviceToDevice, (hipStream_t)stream),
+            SMG_EHIP);
+    HIP_TRY(hipMemcpyAsync(c->v + c->len * ld, v, rows * ld * 2, hipMemcpyDeviceToDevice, (hipStream_t)stream),
+            SMG_EHIP);
+    c->len += rows;
+    return SMG_OK;
+}
+
+static int attention_dev(int device, const float *q, const uint16_t *k, const uint16_t *v, size_t len,
+                         size_t heads, size_t kv_heads, size_t hd, float scale, float *out, void *stream) {
+    if (!head_shape_ok(heads, kv_heads, hd))
+        return fail(SMG_EINVAL, "head_dim must be a multiple of 8 in 8..=256 and heads a positive multiple of kv_heads");
+    if (len == 0) return fail(SMG_EINVAL, "attention_kv_f16 needs at least one cached key");
+    if (!q || !k || !v || !out) return fail(SMG_EINVAL, "null array");
+    const size_t qlen = heads * hd, nsplit = attn_splits(len);
+    DecodeScratch sc;
+    int rc = decode_scratch(device, stream, qlen, nsplit, heads, 0, 0, &sc);
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = launch_round_q(q, scale, qlen, sc.q16, s);
+    AttnArgs at = {};
+    at.q = sc.q16;
+    at.k = k;
+    at.v = v;
+    at.po = sc.po;
+    at.pml = sc.pml;
+    at.len = (uint32_t)len;
+    at.ld = (uint32_t)(kv_heads * hd);
+    at.hd = (uint32_t)hd;
+    at.heads = (uint32_t)heads;
+    at.group = (uint32_t)(heads / kv_heads);
+    if (e == hipSuccess) e = launch_attention(at, out, false, s);
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "attention", e);
+}
+
+int smg_kv_cache_attend_dev(const smg_kv_cache *c, const float *q, float *out, void *stream) {
+    if (!c) return fail(SMG_EINVAL, "null cache");
+    return attention_dev(c->device, q, c->k, c->v, c->len, c->heads, c->kv_heads, c->hd, c->scale, out, stream);
+}
+
+int smg_attention_kv_f16_dev(const float *q, const uint16_t *k, const uint16_t *v, size_t len,
+                             size_t heads, size_t kv_heads, size_t head_dim, float scale, float *out,
+                             void *stream) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev), SMG_EHIP);
+    return attention_dev(dev, q, k, v, len, heads, kv_heads, head_dim, scale, out, stream);
+}
+
+int smg_rms_norm_f16_dev(const float *x, const float *weight, size_t rows, size_t dim, float eps,
+                         uint16_t *y, void *stream) {
+    if (dim == 0) return fail(SMG_EINVAL, "a norm needs at least one feature");
+    if (rows == 0) return SMG_OK;
+    if (!x || !weight || !y) return fail(SMG_EINVAL, "null array");
+    hipError_t e = launch_rms_norm(x, weight, rows, dim, eps, y, (hipStream_t)stream);
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "rms_norm", e);
+}
+
+int smg_glu_f16_dev(const uint16_t *both, size_t m, size_t n, uint32_t act, uint16_t *y, void *stream) {
+    if (act != EP_ACT_SILU && act != EP_ACT_GELU) return fail(SMG_EINVAL, "a gate is silu or gelu");
+    if (m == 0 || n == 0) return SMG_OK;
+    if (!both || !y) return fail(SMG_EINVAL, "null array");
+    hipError_t e = launch_glu(both, m, n, act, 0, y, (hipStream_t)stream);
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "glu", e);
+}
+
+int smg_q4_accumulate_dev(size_t m, const smg_weights *w, float *y, const uint16_t *x, void *stream) {
+    int rc = check_kind(w, W_Q4);
+    if (rc) return rc;
+    if (m == 0 || w->d.n == 0) return SMG_OK;
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e;
+    if (m <= 8 && !w->d.mins && w->d.block >= (size_t)Q4_CHUNK && w->d.nchunks > 0) {
+        BlkArgs r = {};
+        r.x = y;
+        e = launch_blk_gemv(w->d, m, x, r, BS_RESID, false, s);
+    } else {
+        DecodeScratch sc;
+        if ((rc = decode_scratch(w->device, stream, 0, 0, 0, m * w->d.n, 0, &sc))) return rc;
+        e = run_q4(w->d, m, sc.h16, x, EpArgs{}, false, s);
+        if (e == hipSuccess) e = launch_add_f16(sc.h16, m * w->d.n, y, s);
+    }
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_q4_accumulate_dev", e);
+}
+
+int smg_attn_create(smg_weights *qkv, smg_weights *out, size_t heads, size_t kv_heads, size_t head_dim,
+                    double rope_theta, smg_attn **attn) {
+    int rc = check_kind(qkv, W_Q4);
+    if (!rc) rc = check_kind(out, W_Q4);
+    if (rc) return rc;
+    if (!attn) return fail(SMG_EINVAL, "null output");
+    if (!head_shape_ok(heads, kv_heads, head_dim) || head_dim % 16 != 0)
+        return fail(SMG_EINVAL, "heads must be a positive multiple of kv_heads and head_dim a multiple of 16 up to 256");
+    if (qkv->d.n != (heads + 2 * kv_heads) * head_dim)
+        return fail(SMG_EINVAL, "qkv has (heads + 2 kv_heads) * head_dim outputs");
+    if (out->d.k != heads * head_dim) return fail(SMG_EINVAL, "out takes heads * head_dim inputs");
+    if (qkv->d.mins || qkv->d.block < (size_t)Q4_CHUNK || out->d.mins || out->d.block < (size_t)Q4_CHUNK)
+        return fail(SMG_EINVAL, "the decode path takes Q4_0 (scale-only) weights with blocks of 32 or more");
+    if (qkv->device != out->device) return fail(SMG_EINVAL, "qkv and out are on different devices");
+    smg_weights *grouped = nullptr;
+    if ((rc = gather_columns(qkv, nullptr, qkv_store_order(qkv->d.n, head_dim), &grouped))) return rc;
+    smg_attn *a = new smg_attn();
+    a->device = qkv->device;
+    a->qkv = grouped;
+    a->out = out;
+    a->heads = heads;
+    a->kv_heads = kv_heads;
+    a->hd = head_dim;
+    a->theta = rope_theta > 0.0 ? rope_theta : 0.0;
+    for (size_t i = 0; i < head_dim / 2; i++)  // model.rs:41-51: (1 / base^(2i/dim)) as f32
+        a->inv_freq.push_back((float)(1.0 / std::pow(a->theta, (double)(2 * i) / (double)head_dim)));
+    destroy(qkv);  // taken over: its columns now live in `grouped`
+    *attn = a;
+    return SMG_OK;
+}
+
+void smg_attn_destroy(smg_attn *a) { destroy_attn(a); }
+
+int smg_attn_accumulate_dev(smg_attn *a, const uint16_t *x, smg_kv_cache *cache, float *y, size_t m,
+                            void *stream) {
+    if (!a) return fail(SMG_EINVAL, "null attention");
+    if (m == 0) return SMG_OK;
+    if (m != 1) return fail(SMG_EINVAL, "SelfAttention on the GPU takes one row (decode)");
+    if (!x || !y) return fail(SMG_EINVAL, "null array");
+    return attn_step(a, cache, x, nullptr, nullptr, 0.0f, y, stream);
+}
+
+int smg_mlp_create(smg_weights *up, smg_weights *down, uint32_t act, int gated, smg_mlp **mlp) {
+    int rc = check_kind(up, W_Q4);
+    if (!rc) rc = check_kind(down, W_Q4);
+    if (rc) return rc;
+    if (!mlp) return fail(SMG_EINVAL, "null output");
+    if (act != EP_ACT_SILU && act != EP_ACT_GELU) return fail(SMG_EINVAL, "a gate is silu or gelu");
+    const size_t hidden = gated ? up->d.n / 2 : up->d.n;
+    if (gated && up->d.n % 2 != 0) return fail(SMG_EINVAL, "a gated up has 2 * hidden outputs");
+    if (down->d.k != hidden) return fail(SMG_EINVAL, "down takes up's outputs");
+    if (up->device != down->device) return fail(SMG_EINVAL, "up and down are on different devices");
+    smg_weights *u = up;
+    if (gated) {
+        if (up->d.mins || up->d.block < (size_t)Q4_CHUNK)
+            return fail(SMG_EINVAL, "a gated MLP takes Q4_0 (scale-only) weights with blocks of 32 or more");
+        if ((rc = gather_columns(up, nullptr, glu_store_order(hidden), &u))) return rc;
+    }
+    smg_mlp *m = new smg_mlp();
+    m->device = up->device;
+    m->up = u;
+    m->down = down;
+    m->act = act;
+    m->gated = gated != 0;
+    m->hidden = hidden;
+    if (gated) destroy(up);  // taken over: its columns now live in `u`
+    *mlp = m;
+    return SMG_OK;
+}
+
+void smg_mlp_destroy(smg_mlp *m) { destroy_mlp(m); }
+
+int smg_mlp_accumulate_dev(smg_mlp *m, const uint16_t *x, float *y, size_t rows, void *stream) {
+    if (!m) return fail(SMG_EINVAL, "null mlp");
+    if (rows == 0) return SMG_OK;
+    if (!x || !y) return fail(SMG_EINVAL, "null array");
+    return mlp_step(m, x, nullptr, nullptr, 0.0f, y, rows, stream);
+}
+
+int smg_block_create(const float *norm1, float eps1, const float *norm2, float eps2, size_t d,
+                     smg_attn *attn, smg_mlp *mlp, smg_block **block) {
+    if (!attn || !mlp || !block || !norm1 || !norm2) return fail(SMG_EINVAL, "null argument");
+    if (d == 0 || attn->qkv->d.k != d || attn->out->d.n != d || mlp->up->d.k != d || mlp->down->d.n != d)
+        return fail(SMG_EINVAL, "the norms, attention and MLP share the residual's width");
+    if (attn->device != mlp->device) return fail(SMG_EINVAL, "attention and MLP are on different devices");
+    HIP_TRY(hipSetDevice(attn->device), SMG_EHIP);
+    smg_block *b = new smg_block();
+    b->device = attn->device;
+    b->d = d;
+    b->eps1 = eps1;
+    b->eps2 = eps2;
+    b->norm1 = b->norm2 = nullptr;
+    if (hipMalloc((void **)&b->norm1, d * 4) != hipSuccess || hipMalloc((void **)&b->norm2, d * 4) != hipSuccess ||
+        hipMemcpy(b->norm1, norm1, d * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(b->norm2, norm2, d * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        if (b->norm1) (void)hipFree(b->norm1);
+        if (b->norm2) (void)hipFree(b->norm2);
+        delete b;
+        return fail(SMG_ENOMEM, "block norm weights");
+    }
+    b->attn = attn;
+    b->mlp = mlp;
+    *block = b;
+    return SMG_OK;
+}
+
+void smg_block_destroy(smg_block *b) {
+    if (!b) return;
+    (void)hipSetDevice(b->device);
+    (void)hipFree(b->norm1);
+    (void)hipFree(b->norm2);
+    destroy_attn(b->attn);
+    destroy_mlp(b->mlp);
+    delete b;
+}
+
+int smg_block_accumulate_dev(smg_block *b, float *x, smg_kv_cache *cache, size_t rows, void *stream) {
+    if (!b) return fail(SMG_EINVAL, "null block");
+    if (rows == 0) return SMG_OK;
+    if (rows != 1) return fail(SMG_EINVAL, "Block on the GPU takes one row (decode)");
+    if (!x) return fail(SMG_EINVAL, "null array");
+    // x += attn(norm1(x)); x += mlp(norm2(x)) (block.rs:98-105), each norm
+    // fused into the projection that reads it
+    const bool fuse = b->d <= 4096 && b->d % 8 == 0;
+    int rc;
+    if (fuse) {
+        rc = attn_step(b->attn, cache, nullptr, x, b->norm1, b->eps1, x, stream);
+    } else {
+        DecodeScratch sc;
+        if ((rc = decode_scratch(b->device, stream, 0, 0, 0, b->d, 0, &sc))) return rc;
+        hipError_t e = launch_rms_norm(x, b->norm1, 1, b->d, b->eps1, sc.h16, (hipStream_t)stream);
+        if (e != hipSuccess) return fail(SMG_EHIP, "rms_norm", e);
+        // the attention's scratch above the normalized row
+        rc = attn_step(b->attn, cache, sc.h16, nullptr, nullptr, 0.0f, x, stream, round_up(b->d * 2, 256));
+    }
+    if (rc) return rc;
+    return mlp_step(b->mlp, nullptr, x, b->norm2, b->eps2, x, 1, stream);
 }
 
 }  // extern "C"

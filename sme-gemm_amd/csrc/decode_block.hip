@@ -1,0 +1,454 @@
+// The decode block (one row through src/block.rs's Block::accumulate) on
+// gfx950, with the reference's row-wise passes fused into the kernels that
+// need them:
+//
+//   blk_gemv<NORM, QKV>   RMSNorm of the f32 residual row (src/nn.rs:127-144)
+//                         staged as the GEMV's f16 activations, the qkv Q4 GEMV,
+//                         and at the store the NeoX RoPE (examples/bonsai/
+//                         model.rs:87-99) of q and k, the new key / value row
+//                         written into the cache, q rounded after the score
+//                         scale as attention_kv_f16 rounds it
+//                         (src/kernels/kv_attention.rs:298-302);
+//   attn_split            flash-decode partials: per (KV head, chunk of its
+//                         query heads, 64-key split) the scores, a local softmax
+//                         and its value sums;
+//   attn_combine          the splits merged (max-rescaled), / sum, rounded to
+//                         f16 for the out projection (or f32 for the API);
+//   blk_gemv<.., RESID>   the out / down Q4 GEMV adding its f16-rounded result
+//                         into the f32 residual (convert::add_f16, src/convert.rs);
+//   blk_gemv<NORM, GLU>   RMSNorm again, the gate/up Q4 GEMV, and GatedLinear's
+//                         glu (src/linear.rs:804-826) at the store.
+//
+// Numerics: every rounding point of the reference is kept (the f16 GEMV
+// outputs, q, the cache rows, the attention output, the hidden layer, the
+// residual adds); sums run in other orders (split-K GEMV, a tree for the sum
+// of squares, split softmax) and exp / tanh are the device's, so results are
+// held to a tolerance against the portable path, not to its bits.
+#include "q4_gemv_core.cuh"
+
+namespace smg {
+
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    return v;  // every lane holds the same bits (each pair adds the same two values)
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+__device__ __forceinline__ float4 bload16f(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// 1 / sqrt(mean(x^2) + eps) over a workgroup of MF_WAVES waves, from each
+// thread's partial sum of squares (fixed combination order: every thread gets
+// the same bits). Correctly rounded division and square root (HIP's default).
+__device__ __forceinline__ float rms_scale(float ss, uint32_t k, float eps) {
+    __shared__ float part[MF_WAVES];
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < MF_WAVES; w++) tot = tot + part[w];
+    return 1.0f / sqrtf(tot / (float)k + eps);
+}
+
+// Activation source of a fused norm: one f32 residual row x[k] (k <= MF_SEG, a
+// multiple of 8) and the norm's f32 weights; stage() writes
+// h = f16((x - 0) * r * w + 0), norm_row's expression (nn.rs:142), with r from
+// the whole row.
+struct SrcNormRow {
+    struct Regs {
+        float4 x0, x1, w0, w1;
+    };
+    rsrc_t xr, wr;
+    uint32_t k;
+    float eps;
+    __device__ SrcNormRow(const float *x, const float *w, uint32_t k_, float eps_)
+        : xr(make_rsrc(x, k_ * 4u)), wr(make_rsrc(w, k_ * 4u)), k(k_), eps(eps_) {}
+    __device__ void load(Regs &a, uint32_t d0, int t) const {
+        const uint32_t off = (d0 + 8u * (uint32_t)t) * 4u;  // past k: zeros
+        a.x0 = bload16f(xr, off);
+        a.x1 = bload16f(xr, off + 16);
+        a.w0 = bload16f(wr, off);
+        a.w1 = bload16f(wr, off + 16);
+    }
+    __device__ void stage(uint16_t *a_lds, const Regs &a, int t) const {
+        const float xs[8] = {a.x0.x, a.x0.y, a.x0.z, a.x0.w, a.x1.x, a.x1.y, a.x1.z, a.x1.w};
+        const float ws[8] = {a.w0.x, a.w0.y, a.w0.z, a.w0.w, a.w1.x, a.w1.y, a.w1.z, a.w1.w};
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) ss = ss + xs[i] * xs[i];
+        const float r = rms_scale(ss, k, eps);
+        uint16_t h[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = f32_to_f16((xs[i] - 0.0f) * r * ws[i] + 0.0f);
+        *(uint4 *)(a_lds + 8 * t) = make_uint4(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+                                               h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16));
+    }
+};
+
+// GatedLinear's activation on the gate (linear.rs:815-822), in f32.
+__device__ __forceinline__ float glu_act(uint32_t act, float g) {
+    if (act == EP_ACT_GELU) return 0.5f * g * (1.0f + tanhf(0.7978846f * (g + 0.044715f * g * g * g)));
+    return g / (1.0f + expf(-g));
+}
+
+template <int MR, bool NORM, int STORE>
+__global__ void __launch_bounds__(MF_WAVES * 64) blk_gemv(Q4GemvArgs g, BlkArgs a) {
+    static_assert(!NORM || MR == 1, "the fused norm serves one row");
+    static_assert(STORE != BS_QKV || MR == 1, "the rope / cache store serves one row");
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint16_t *a_lds = (uint16_t *)smem;
+    float *red = (float *)smem;
+    const int t = threadIdx.x;
+    const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
+    const uint32_t col = tile * 16 + (t & 15);
+    bool timed_out = false;
+    float4_t acc;
+    if constexpr (NORM) {
+        const SrcNormRow src(a.nx, a.nw, g.k, a.eps);
+        acc = q4_mfma_mainloop<1, false>(g, src, ChainArgs{}, a_lds, col, timed_out);
+    } else {
+        const SrcRows<MR> src(g.lhs, g.m, g.k);
+        acc = q4_mfma_mainloop<MR, false>(g, src, ChainArgs{}, a_lds, col, timed_out);
+    }
+    q4_mfma_reduce<MR>(acc, red);
+    if constexpr (STORE == BS_RESID) {
+        // y += f32(f16(x @ W)): Linear::accumulate's add_f16 (src/convert.rs:37-49)
+        if (t < 16 * MR) {
+            const int cc = t / MR, r = t % MR;
+            const uint32_t j = tile * 16 + cc;
+            if (r < (int)g.m && j < g.n) {
+                float *yp = a.x + (size_t)r * g.n + j;
+                *yp = *yp + f16_to_f32(f32_to_f16(tile_total<MR>(red, cc, r)));
+            }
+        }
+    } else if constexpr (STORE == BS_GLU) {
+        // device tile = 8 gate columns then the same 8 up columns
+        if (t < 8 * MR) {
+            const int cc = t / MR, r = t % MR;
+            const uint32_t jh = tile * 8 + cc;
+            if (r < (int)g.m && jh < a.nh) {
+                const float gv = f16_to_f32(f32_to_f16(tile_total<MR>(red, cc, r)));
+                const float uv = f16_to_f32(f32_to_f16(tile_total<MR>(red, cc + 8, r)));
+                a.y[(size_t)r * a.nh + jh] = f32_to_f16(glu_act(a.act, gv) * uv);
+            }
+        }
+    } else {
+        // device tile = columns 8q..8q+7 and half+8q..half+8q+7 of one head
+        // (q heads, then k heads, then v heads): each lane's RoPE partner is
+        // lane ^ 8 of the same tile.
+        const uint32_t p = tile * 16 + t;
+        const uint32_t nq = (a.heads + 2 * a.kv_heads) * a.hd;
+        if (t < 16 && p < nq) {
+            const uint32_t hd = a.hd, half = hd / 2;
+            const uint32_t H = p / hd, qt = (p % hd) / 16, cc = (uint32_t)t;
+            const uint32_t i = cc < 8 ? 8 * qt + cc : half + 8 * qt + cc - 8;
+            const uint16_t own16 = f32_to_f16(tile_total<1>(red, t, 0));
+            const uint16_t par16 = f32_to_f16(tile_total<1>(red, t ^ 8, 0));
+            if (H < a.heads + a.kv_heads) {
+                float val = f16_to_f32(own16);
+                if (a.cs) {
+                    const uint32_t pi = 8 * qt + (cc & 7);
+                    const float c = a.cs[pi], s = a.sn[pi];
+                    const float x1 = f16_to_f32(cc < 8 ? own16 : par16);
+                    const float x2 = f16_to_f32(cc < 8 ? par16 : own16);
+                    val = cc < 8 ? x1 * c - x2 * s : x2 * c + x1 * s;
+                }
+                if (H < a.heads) a.q_out[H * hd + i] = f32_to_f16(val * a.scale);
+                else a.k_row[(H - a.heads) * hd + i] = f32_to_f16(val);
+            } else {
+                a.v_row[(H - a.heads - a.kv_heads) * hd + i] = own16;
+            }
+        }
+    }
+}
+
+template <int MR, bool NORM, int STORE>
+hipError_t launch_blk(const Q4GemvArgs &g, const BlkArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL((blk_gemv<MR, NORM, STORE>), dim3(g.n_pad / 16), dim3(MF_WAVES * 64),
+                       q4_mfma_lds_bytes<MR>(), s, g, a);
+    return hipGetLastError();
+}
+
+template <bool NORM, int STORE>
+hipError_t launch_blk_rows(const Q4GemvArgs &g, const BlkArgs &a, size_t m, hipStream_t s) {
+    if constexpr (NORM || STORE == BS_QKV) {
+        if (m != 1) return hipErrorNotSupported;
+        return launch_blk<1, NORM, STORE>(g, a, s);
+    } else {
+        if (m <= 1) return launch_blk<1, NORM, STORE>(g, a, s);
+        if (m <= 2) return launch_blk<2, NORM, STORE>(g, a, s);
+        if (m <= 4) return launch_blk<4, NORM, STORE>(g, a, s);
+        return launch_blk<8, NORM, STORE>(g, a, s);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Attention over the f16 cache (one query row)
+// ---------------------------------------------------------------------------
+constexpr int AT_T = 256;    // threads
+constexpr int AT_KPS = 64;   // keys per split (one per lane of the softmax wave)
+constexpr int AT_HC = 4;     // query heads per workgroup (a chunk of one KV head's group)
+
+// Reduction over aligned groups of G lanes (a power of two up to 32).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// LPK lanes per key (8 depths each: head_dim <= 8 * LPK). Thread t takes key
+// slot t / LPK of each 256/LPK-key step and depths 8 (t % LPK) .. +8; all
+// its key, value and query loads are issued before the first is used.
+template <int LPK>
+__global__ void __launch_bounds__(AT_T) attn_split(AttnArgs a) {
+    constexpr int KPI = AT_T / LPK;   // keys per step
+    constexpr int IT = AT_KPS / KPI;  // steps per split
+    constexpr int HDM = 8 * LPK;      // largest head_dim served
+    __shared__ float sc[AT_HC][AT_KPS];
+    __shared__ float ored[KPI][AT_HC][HDM];
+    __shared__ float2 mls[AT_HC];
+    const int t = threadIdx.x;
+    const int ks = t / LPK, c = t % LPK;
+    const uint32_t split = blockIdx.x;
+    const uint32_t kvh = blockIdx.y / a.hchunks, hc0 = (blockIdx.y % a.hchunks) * AT_HC;
+    const bool dim_ok = 8u * c < a.hd;
+    const rsrc_t qr = make_rsrc(a.q, a.heads * a.hd * 2u);
+    const rsrc_t kr = make_rsrc(a.k, a.len * a.ld * 2u);
+    const rsrc_t vr = make_rsrc(a.v, a.len * a.ld * 2u);
+    uint4 qv[AT_HC];
+#pragma unroll
+    for (int hh = 0; hh < AT_HC; hh++) {
+        const uint32_t h = kvh * a.group + hc0 + hh;
+        const bool ok = dim_ok && hc0 + hh < a.group;
+        qv[hh] = bload16(qr, ok ? (h * a.hd + 8 * c) * 2u : OOB);
+    }
+    const uint32_t key0 = split * AT_KPS;
+    uint4 kv[IT], vv[IT];
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        const uint32_t key = key0 + ks + KPI * it;
+        const uint32_t off = (key < a.len && dim_ok) ? (key * a.ld + kvh * a.hd + 8 * c) * 2u : OOB;
+        kv[it] = bload16(kr, off);
+        vv[it] = bload16(vr, off);
+    }
+    // scores: q . k over this lane's 8 depths, summed over the key's lanes
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        const uint32_t key = key0 + ks + KPI * it;
+        const uint32_t kw[4] = {kv[it].x, kv[it].y, kv[it].z, kv[it].w};
+#pragma unroll
+        for (int hh = 0; hh < AT_HC; hh++) {
+            const uint32_t qw[4] = {qv[hh].x, qv[hh].y, qv[hh].z, qv[hh].w};
+            float s = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; w++)
+                s = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, qw[w]), __builtin_bit_cast(half2_t, kw[w]),
+                                           s, false);
+            s = group_sum<LPK>(s);
+            if (c == 0) sc[hh][ks + KPI * it] = key < a.len ? s : -INFINITY;
+        }
+    }
+    __syncthreads();
+    // softmax within the split: wave w takes query head w of the chunk
+    {
+        const int wave = t >> 6, lane = t & 63;
+        for (int hh = wave; hh < AT_HC; hh += AT_T / 64) {
+            const float v = sc[hh][lane];
+            const float m = wave_max(v);
+            const float p = v == -INFINITY ? 0.0f : expf(v - m);
+            const float l = wave_sum(p);
+            sc[hh][lane] = p;
+            if (lane == 0) mls[hh] = make_float2(m, l);
+        }
+    }
+    __syncthreads();
+    // value sums: this lane's 8 depths over its keys, then over the key slots
+    float acc[AT_HC][8];
+#pragma unroll
+    for (int hh = 0; hh < AT_HC; hh++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[hh][e] = 0.0f;
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        const uint32_t vw[4] = {vv[it].x, vv[it].y, vv[it].z, vv[it].w};
+        float vf[8];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            vf[2 * w] = f16_to_f32((uint16_t)vw[w]);
+            vf[2 * w + 1] = f16_to_f32((uint16_t)(vw[w] >> 16));
+        }
+#pragma unroll
+        for (int hh = 0; hh < AT_HC; hh++) {
+            const float p = sc[hh][ks + KPI * it];
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[hh][e] = __builtin_fmaf(p, vf[e], acc[hh][e]);
+        }
+    }
+#pragma unroll
+    for (int hh = 0; hh < AT_HC; hh++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) ored[ks][hh][8 * c + e] = acc[hh][e];
+    __syncthreads();
+    for (int o = t; o < AT_HC * HDM; o += AT_T) {
+        const uint32_t hh = (uint32_t)o / HDM, d = (uint32_t)o % HDM;
+        if (d < a.hd && hc0 + hh < a.group) {
+            float sum = 0.0f;
+            for (int q = 0; q < KPI; q++) sum = sum + ored[q][hh][d];
+            const uint32_t h = kvh * a.group + hc0 + hh;
+            a.po[((size_t)split * a.heads + h) * a.hd + d] = sum;
+        }
+    }
+    if (t < AT_HC && hc0 + t < a.group) a.pml[(size_t)split * a.heads + kvh * a.group + hc0 + t] = mls[t];
+}
+
+// The splits of head blockIdx.x merged: o = sum_s e^(m_s - M) o_s / sum_s
+// e^(m_s - M) l_s, in split order; f16 (the out projection's input) or f32.
+template <bool F16OUT>
+__global__ void attn_combine(const float *po, const float2 *pml, uint32_t nsplit, uint32_t heads,
+                             uint32_t hd, void *out) {
+    const uint32_t h = blockIdx.x, d = threadIdx.x;
+    if (d >= hd) return;
+    float m = -INFINITY;
+    for (uint32_t s = 0; s < nsplit; s++) m = fmaxf(m, pml[(size_t)s * heads + h].x);
+    float l = 0.0f, o = 0.0f;
+    for (uint32_t s = 0; s < nsplit; s++) {
+        const float2 ml = pml[(size_t)s * heads + h];
+        const float w = expf(ml.x - m);
+        l = __builtin_fmaf(w, ml.y, l);
+        o = __builtin_fmaf(w, po[((size_t)s * heads + h) * hd + d], o);
+    }
+    const float v = o / l;
+    if (F16OUT) ((uint16_t *)out)[h * hd + d] = f32_to_f16(v);
+    else ((float *)out)[h * hd + d] = v;
+}
+
+// q (f32) to the rounded query attention_kv_f16 scores with: f16(q * scale).
+__global__ void attn_round_q(const float *q, float scale, uint32_t count, uint16_t *qh) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) qh[i] = f32_to_f16(q[i] * scale);
+}
+
+// ---------------------------------------------------------------------------
+// Stand-alone row passes
+// ---------------------------------------------------------------------------
+// nn::rms_norm into f16, one workgroup of MF_WAVES waves per row.
+__global__ void __launch_bounds__(MF_WAVES * 64) rms_norm_rows(const float *x, const float *w, uint32_t dim,
+                                                               float eps, uint16_t *y) {
+    const float *xr = x + (size_t)blockIdx.x * dim;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) ss = ss + xr[i] * xr[i];
+    const float r = rms_scale(ss, dim, eps);
+    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x)
+        y[(size_t)blockIdx.x * dim + i] = f32_to_f16((xr[i] - 0.0f) * r * w[i] + 0.0f);
+}
+
+// glu over rows of 2n gate / up values: the reference's layout (each
+// 32-column chunk, the last w < 32 wide, gate then up: linear.rs:601-619,
+// 803-826) or the device tiles of 8 gate + 8 up columns (tile8).
+__global__ void glu_rows(const uint16_t *both, uint32_t m, uint32_t n, uint32_t act, int tile8, uint16_t *y) {
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (uint64_t)m * n) return;
+    const uint32_t r = (uint32_t)(idx / n), j = (uint32_t)(idx % n);
+    const uint32_t stride = tile8 ? 16 * ((n + 7) / 8) : 2 * n;  // tiles pad to whole 16-column tiles
+    const uint16_t *row = both + (size_t)r * stride;
+    uint32_t gi, ui;
+    if (tile8) {
+        gi = 16 * (j / 8) + j % 8;
+        ui = gi + 8;
+    } else {
+        const uint32_t c0 = j / 32 * 32, w = n - c0 < 32 ? n - c0 : 32;
+        gi = 2 * c0 + (j - c0);
+        ui = gi + w;
+    }
+    y[idx] = f32_to_f16(glu_act(act, f16_to_f32(row[gi])) * f16_to_f32(row[ui]));
+}
+
+__global__ void add_f16_values(const uint16_t *h, uint64_t count, float *y) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) y[i] = y[i] + f16_to_f32(h[i]);
+}
+
+}  // namespace
+
+hipError_t launch_blk_gemv(const WDev &w, size_t m, const uint16_t *lhs, const BlkArgs &a, int store,
+                           bool norm, hipStream_t s) {
+    if (w.kind != W_Q4 || w.mins || w.block < (size_t)Q4_CHUNK || w.nchunks == 0 || m == 0 || m > 8)
+        return hipErrorNotSupported;
+    if (norm && (w.k > (size_t)MF_SEG || w.k % 8 != 0)) return hipErrorNotSupported;
+    if ((size_t)m * w.k * 2 >= ((size_t)1 << 31)) return hipErrorInvalidValue;
+    const Q4GemvArgs g = q4_gemv_args(w, m, nullptr, lhs);
+    switch (store) {
+    case BS_RESID:
+        return norm ? launch_blk_rows<true, BS_RESID>(g, a, m, s) : launch_blk_rows<false, BS_RESID>(g, a, m, s);
+    case BS_GLU:
+        return norm ? launch_blk_rows<true, BS_GLU>(g, a, m, s) : launch_blk_rows<false, BS_GLU>(g, a, m, s);
+    case BS_QKV:
+        return norm ? launch_blk_rows<true, BS_QKV>(g, a, m, s) : launch_blk_rows<false, BS_QKV>(g, a, m, s);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+size_t attn_splits(size_t len) { return (len + AT_KPS - 1) / AT_KPS; }
+
+hipError_t launch_attention(const AttnArgs &a0, void *out, bool f16_out, hipStream_t s) {
+    AttnArgs a = a0;
+    if (a.len == 0 || a.hd == 0 || a.hd > 256 || a.hd % 8 != 0 || a.group == 0) return hipErrorInvalidValue;
+    if ((size_t)a.len * a.ld * 2 >= ((size_t)1 << 31)) return hipErrorInvalidValue;
+    a.nsplit = (uint32_t)attn_splits(a.len);
+    a.hchunks = (a.group + AT_HC - 1) / AT_HC;
+    const dim3 grid(a.nsplit, (a.heads / a.group) * a.hchunks);
+    if (a.hd <= 64) hipLaunchKernelGGL(attn_split<8>, grid, dim3(AT_T), 0, s, a);
+    else if (a.hd <= 128) hipLaunchKernelGGL(attn_split<16>, grid, dim3(AT_T), 0, s, a);
+    else hipLaunchKernelGGL(attn_split<32>, grid, dim3(AT_T), 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t threads = (a.hd + 63) / 64 * 64;
+    if (f16_out)
+        hipLaunchKernelGGL(attn_combine<true>, dim3(a.heads), dim3(threads), 0, s, a.po, a.pml, a.nsplit,
+                           a.heads, a.hd, out);
+    else
+        hipLaunchKernelGGL(attn_combine<false>, dim3(a.heads), dim3(threads), 0, s, a.po, a.pml, a.nsplit,
+                           a.heads, a.hd, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_round_q(const float *q, float scale, size_t count, uint16_t *qh, hipStream_t s) {
+    hipLaunchKernelGGL(attn_round_q, dim3((uint32_t)((count + 255) / 256)), dim3(256), 0, s, q, scale,
+                       (uint32_t)count, qh);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(const float *x, const float *w, size_t rows, size_t dim, float eps, uint16_t *y,
+                           hipStream_t s) {
+    hipLaunchKernelGGL(rms_norm_rows, dim3((uint32_t)rows), dim3(MF_WAVES * 64), 0, s, x, w, (uint32_t)dim,
+                       eps, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_glu(const uint16_t *both, size_t m, size_t n, uint32_t act, int tile8, uint16_t *y,
+                      hipStream_t s) {
+    const size_t total = m * n;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(glu_rows, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, s, both, (uint32_t)m,
+                       (uint32_t)n, act, tile8, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_f16(const uint16_t *h, size_t count, float *y, hipStream_t s) {
+    if (count == 0) return hipSuccess;
+    hipLaunchKernelGGL(add_f16_values, dim3((uint32_t)((count + 255) / 256)), dim3(256), 0, s, h,
+                       (uint64_t)count, y);
+    return hipGetLastError();
+}
+
+}  // namespace smg

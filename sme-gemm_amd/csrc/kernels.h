@@ -80,6 +80,53 @@ hipError_t launch_gather_columns(void *dst, size_t dst_pad, const void *src0, co
                                  size_t src_pad, const int32_t *map, size_t rows, size_t cell_bytes,
                                  hipStream_t s);
 
+// ---- decode block (decode_block.hip) ---------------------------------------
+// What the fused Q4 GEMVs of the decode block do at their source and store.
+enum BlkStore : int {
+    BS_RESID = 0,  // x[r][j] += f32(f16(result))        (Linear::accumulate)
+    BS_GLU = 1,    // y[r][j] = f16(act(g) * u), device tiles of 8 gate + 8 up columns
+    BS_QKV = 2     // RoPE'd q (scaled, f16) and the cache's new k / v row
+};
+struct BlkArgs {
+    const float *nx, *nw;  // fused RMSNorm source: the f32 row and the norm's weights
+    float eps;
+    float *x;              // BS_RESID: [m][n] f32
+    uint16_t *y;           // BS_GLU: [m][nh] f16
+    uint32_t act, nh;      // BS_GLU: EP_ACT_SILU / EP_ACT_GELU, hidden width
+    uint16_t *q_out;       // BS_QKV: [heads][hd] f16(q * scale)
+    uint16_t *k_row, *v_row;  // BS_QKV: the cache rows at the new position
+    const float *cs, *sn;  // BS_QKV: RoPE cos / sin at that position (null: no RoPE)
+    float scale;           // BS_QKV: the score scale
+    uint32_t heads, kv_heads, hd;
+};
+// A Q4 GEMV of m <= 8 rows (f16 `lhs`, or with norm the f32 row a.nx, m = 1,
+// k <= 4096) with one of the stores above. Device column order: BS_QKV tiles
+// are 8 columns of a head's first half and the same 8 of its second half;
+// BS_GLU tiles 8 gate then the same 8 up columns.
+hipError_t launch_blk_gemv(const WDev &w, size_t m, const uint16_t *lhs, const BlkArgs &a, int store,
+                           bool norm, hipStream_t s);
+
+// Attention of one query row over an f16 cache, split over keys.
+struct AttnArgs {
+    const uint16_t *q;       // [heads][hd] f16(q * scale)
+    const uint16_t *k, *v;   // [len][ld], KV head j at j*hd
+    float *po;               // partial sums [attn_splits(len)][heads][hd]
+    float2 *pml;             // partial (max, sum) [attn_splits(len)][heads]
+    uint32_t len, ld, hd, heads, group;  // group = heads / kv_heads
+    uint32_t nsplit, hchunks;            // set by launch_attention
+};
+size_t attn_splits(size_t len);
+hipError_t launch_attention(const AttnArgs &a, void *out, bool f16_out, hipStream_t s);
+hipError_t launch_round_q(const float *q, float scale, size_t count, uint16_t *qh, hipStream_t s);
+hipError_t launch_rms_norm(const float *x, const float *w, size_t rows, size_t dim, float eps, uint16_t *y,
+                           hipStream_t s);
+// glu over m rows of 2n gate / up values: tile8 = 0, the reference's
+// 32-column interleave; tile8 = 1, the device tiles of 8 gate + 8 up columns.
+hipError_t launch_glu(const uint16_t *both, size_t m, size_t n, uint32_t act, int tile8, uint16_t *y,
+                      hipStream_t s);
+// y[i] += f32(h[i]) over count values (convert::add_f16).
+hipError_t launch_add_f16(const uint16_t *h, size_t count, float *y, hipStream_t s);
+
 // Sets the calling thread's smg_last_error() text and returns code.
 int report(int code, const char *what);
 

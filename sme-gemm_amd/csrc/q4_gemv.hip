@@ -28,48 +28,17 @@
 //   16 lanes along K per workgroup, weights rounded per value, dot products on
 //   VALU. All loads are branch-free (clamped address, then a select) so they
 //   stay in flight together.
-#include "kernels.h"
+#include "q4_gemv_core.cuh"
 
 namespace smg {
 
 namespace {
 
-struct Q4GemvArgs {
-    const uint8_t *nib;
-    const uint16_t *sc;
-    const uint16_t *mn;
-    const uint16_t *lhs;
-    uint16_t *dst;
-    uint32_t n, k, n_pad, nchunks, m;
-    uint32_t block_shift;  // log2(block)
-};
-
 // ---------------------------------------------------------------------------
-// MFMA GEMV (fast path)
+// MFMA GEMV (fast path): the shared main loop (q4_gemv_core.cuh) over rows of
+// f16 activations, then the 8 waves' partial tiles summed through LDS in a
+// fixed order and the op-graph at the store.
 // ---------------------------------------------------------------------------
-constexpr int MF_WAVES = 8;                  // waves per workgroup (K slices)
-constexpr int MF_U = 4;                      // steps (4 chunks each) in flight per lane
-constexpr int MF_SEG = 4096;                 // depths of A staged in LDS at a time
-constexpr int MF_SEG_CH = MF_SEG / Q4_CHUNK; // 128 chunks per segment
-
-// One wait of a chained call (thread 0 of the workgroup): polls *ready until it
-// reaches need or the device wall clock has advanced `ticks` (and at most 2^24
-// polls), then an agent-scope acquire, so the producer's stores of A below
-// need are visible to the loads that follow the workgroup barrier.
-__device__ __forceinline__ bool chain_wait(const unsigned long long *ready, unsigned long long need,
-                                           unsigned long long ticks) {
-    const unsigned long long t0 = wall_clock64();
-    for (uint32_t it = 0; it < (1u << 24); it++) {
-        if (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= need) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            return true;
-        }
-        if (wall_clock64() - t0 > ticks) break;
-        __builtin_amdgcn_s_sleep(4);
-    }
-    return false;
-}
-
 template <int MR, bool CHAIN>  // rows staged per segment (1, 2, 4, 8); chained call
 __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpArgs ep, ChainArgs ch) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -77,111 +46,15 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
     float *red = (float *)smem;                   // reused: [MF_WAVES][16 cols][MR]
 
     const int t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6;
-    const int c = lane & 15, grp = lane >> 4;
     const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
-    const uint32_t col = tile * 16 + c;           // < n_pad
-    // the bfi magics live in VGPRs (a VOP3 takes one scalar operand)
-    const uint32_t mag_lo = __builtin_amdgcn_readfirstlane(0x64006400u) | (uint32_t)(t >> 30);
-    const uint32_t mag_hi = __builtin_amdgcn_readfirstlane(0x54005400u) | (uint32_t)(t >> 30);
-
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    const uint32_t col = tile * 16 + (t & 15);    // < n_pad
     bool timed_out = false;  // chained: a wait for A expired (uniform)
-    const uint32_t last = g.nchunks - 1;  // nchunks >= 1 here
-    const uint32_t nseg = (g.nchunks + MF_SEG_CH - 1) / MF_SEG_CH;
-    for (uint32_t seg = 0; seg < nseg; seg++) {
-        const uint32_t sc0 = seg * MF_SEG_CH;
-        // A[:, segment] first: vmcnt retires in issue order, so loads issued
-        // before the weights can be waited on while the weights stay in flight
-        const uint32_t d0 = sc0 * Q4_CHUNK;
-        const rsrc_t ar = make_rsrc(g.lhs, g.m * g.k * 2u);
-        const bool vec = (g.k & 7) == 0;
-        uint4 areg[MR];  // row r, depths d0 + 8t .. +8 (MF_SEG / 8 == 512 threads)
-        bool a_first = true;  // a chained call that awaits A reads it after its weights
-        if constexpr (CHAIN) a_first = ch.ready == nullptr;
-        if (a_first) {
-#pragma unroll
-            for (int r = 0; r < MR; r++) areg[r] = load_row8(ar, r, g.m, g.k, d0 + 8 * t, vec);
-        }
-        // steps of this wave within the segment: chunks sc0 + 4*(wave + 8*u) + grp
-        uint4 wq[MF_U];
-        uint16_t sv[MF_U];
-#pragma unroll
-        for (int u = 0; u < MF_U; u++) {
-            const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
-            const uint32_t kcc = kc < last ? kc : last;  // clamped: always a valid load
-            wq[u] = *(const uint4 *)(g.nib + ((size_t)kcc * g.n_pad + col) * 16);
-            const uint16_t sl = g.sc[(size_t)((kcc * Q4_CHUNK) >> g.block_shift) * g.n_pad + col];
-            sv[u] = kc < g.nchunks ? sl : (uint16_t)0;  // a dead step's weights become 0
-        }
-        if constexpr (CHAIN) {
-            // the weights stream in while the producer of A finishes; A's
-            // segment is read only once *ready covers it
-            if (ch.ready) {
-                __shared__ uint32_t seg_ok;
-                if (t == 0) {
-                    const uint32_t need = g.k < d0 + MF_SEG ? g.k : d0 + MF_SEG;
-                    seg_ok = chain_wait(ch.ready, need, ch.wait_ticks) ? 1u : 0u;
-                }
-                __syncthreads();
-                if (!seg_ok) {
-                    timed_out = true;
-                    break;
-                }
-#pragma unroll
-                for (int r = 0; r < MR; r++) areg[r] = load_row8(ar, r, g.m, g.k, d0 + 8 * t, vec);
-            }
-        }
-        // stage A[:, segment] (rows < m, zero past k)
-        __syncthreads();
-#pragma unroll
-        for (int r = 0; r < MR; r++) *(uint4 *)(a_lds + r * MF_SEG + 8 * t) = areg[r];
-        __syncthreads();
-        // dequant + MFMA: A operand = 16 columns x 32 depths of weights, B
-        // operand = 32 depths x 16 rows of activations (rows >= m are zero).
-        // All of this wave's activation fragments are read first, from a valid
-        // row (branch-free, then selected), so the LDS round trips overlap
-        // instead of each one preceding its MFMA.
-        const int row = c;  // B-operand lane: activation row lane%16
-        const bool row_live = row < MR;
-        const uint16_t *arow = a_lds + (row_live ? row : 0) * MF_SEG;
-        uint4 abv[MF_U][4];
-#pragma unroll
-        for (int u = 0; u < MF_U; u++) {
-            const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
-            const bool live = row_live && kc < g.nchunks;
-            const uint32_t kcl = kc < g.nchunks ? kc - sc0 : 0;
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                const uint4 v = *(const uint4 *)(arow + kcl * Q4_CHUNK + w * 8);
-                abv[u][w] = live ? v : make_uint4(0, 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < MF_U; u++) {
-            const half2_t s2 = {__builtin_bit_cast(_Float16, sv[u]), __builtin_bit_cast(_Float16, sv[u])};
-            const uint32_t words[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                uint4 wa = q4_deq8(words[w], s2, mag_lo, mag_hi);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wa),
-                                                             __builtin_bit_cast(half8_t, abv[u][w]), acc,
-                                                             0, 0, 0);
-            }
-        }
-    }
-    // lane holds D[col = 4*grp + v][row = c] for v = 0..3
-    __syncthreads();
-    if (c < MR) {
-#pragma unroll
-        for (int v = 0; v < 4; v++) red[(wave * 16 + 4 * grp + v) * MR + c] = acc[v];
-    }
-    __syncthreads();
+    const SrcRows<MR> src(g.lhs, g.m, g.k);
+    const float4_t acc = q4_mfma_mainloop<MR, CHAIN>(g, src, ch, a_lds, col, timed_out);
+    q4_mfma_reduce<MR>(acc, red);
     if (t < 16 * MR) {
         const int cc = t / MR, r = t % MR;
-        float total = 0.0f;
-#pragma unroll
-        for (int w = 0; w < MF_WAVES; w++) total = total + red[(w * 16 + cc) * MR + r];
+        const float total = tile_total<MR>(red, cc, r);
         const uint32_t j = tile * 16 + cc;
         if (!timed_out && r < (int)g.m && j < g.n) g.dst[(size_t)r * g.n + j] = finish<false>(ep, total, r, j, g.n);
     }
@@ -378,34 +251,17 @@ hipError_t launch_variant(const Q4GemvArgs &g, const EpArgs &ep, bool bf16, bool
 
 template <int MR, bool CHAIN = false>
 hipError_t launch_mfma(const Q4GemvArgs &g, const EpArgs &ep, hipStream_t s, const ChainArgs &ch = {}) {
-    size_t lds = (size_t)MR * MF_SEG * 2;
-    const size_t red = (size_t)MF_WAVES * 16 * MR * 4;
-    if (red > lds) lds = red;
-    hipLaunchKernelGGL((q4_gemv_mfma<MR, CHAIN>), dim3(g.n_pad / 16), dim3(MF_WAVES * 64), lds, s, g, ep, ch);
+    hipLaunchKernelGGL((q4_gemv_mfma<MR, CHAIN>), dim3(g.n_pad / 16), dim3(MF_WAVES * 64),
+                       q4_mfma_lds_bytes<MR>(), s, g, ep, ch);
     return hipGetLastError();
 }
 
-Q4GemvArgs gemv_args(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs) {
-    Q4GemvArgs g;
-    g.nib = w.codes;
-    g.sc = w.scales;
-    g.mn = w.mins;
-    g.lhs = lhs;
-    g.dst = dst;
-    g.n = (uint32_t)w.n;
-    g.k = (uint32_t)w.k;
-    g.n_pad = (uint32_t)w.n_pad;
-    g.nchunks = (uint32_t)w.nchunks;
-    g.m = (uint32_t)m;
-    g.block_shift = (uint32_t)__builtin_ctzll(w.block);
-    return g;
-}
 
 }  // namespace
 
 hipError_t launch_q4_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
                           const EpArgs &ep, bool bf16, hipStream_t s) {
-    const Q4GemvArgs g = gemv_args(w, m, dst, lhs);
+    const Q4GemvArgs g = q4_gemv_args(w, m, dst, lhs);
     const bool affine = w.mins != nullptr;
     if ((size_t)m * w.k * 2 >= ((size_t)1 << 31)) return hipErrorInvalidValue;  // buffer range
     if (w.nchunks == 0) {
@@ -431,7 +287,7 @@ hipError_t launch_q4_gemv_chained(const WDev &w, size_t m, uint16_t *dst, const 
     if (m < 1 || m > Q4_GEMV_MAX_ROWS || w.mins != nullptr || w.block < (size_t)Q4_CHUNK || w.nchunks == 0)
         return hipErrorNotSupported;
     if ((size_t)m * w.k * 2 >= ((size_t)1 << 31)) return hipErrorInvalidValue;  // buffer range
-    const Q4GemvArgs g = gemv_args(w, m, dst, lhs);
+    const Q4GemvArgs g = q4_gemv_args(w, m, dst, lhs);
     if (m <= 1) return launch_mfma<1, true>(g, ep, s, ch);
     if (m <= 2) return launch_mfma<2, true>(g, ep, s, ch);
     if (m <= 4) return launch_mfma<4, true>(g, ep, s, ch);

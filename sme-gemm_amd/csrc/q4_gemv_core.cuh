@@ -1,0 +1,222 @@
+// The main loop of the Q4 MFMA GEMV (decode-shaped m <= 8), shared by the plain
+// GEMV (q4_gemv.hip) and the decode block's fused kernels (decode_block.hip),
+// which differ only in where the activation rows come from (an f16 array, or
+// an RMS-normalized f32 residual row) and in what their stores do.
+//
+// A workgroup of 8 waves owns 16 output columns; wave w takes every 8th group
+// of 4 chunks (128 depths). Lane (g = lane/16, c = lane%16) loads the 16-byte
+// chunk g of column c, so a wave load reads four contiguous 256-byte runs, and
+// every lane issues all its weight loads before it waits. Each dword (8
+// depths) dequantizes to 8 f16 weights -- v_bfi_b32 puts the nibble under an
+// f16 exponent, a packed subtract leaves the exact code, a packed multiply by
+// the scale is the reference's single RNE rounding of scale*code -- and feeds
+// one v_mfma_f32_16x16x32_f16 as the A operand (16 columns x 32 depths), with
+// up to 16 activation rows as the B operand.
+#pragma once
+
+#include "kernels.h"
+
+namespace smg {
+
+struct Q4GemvArgs {
+    const uint8_t *nib;
+    const uint16_t *sc;
+    const uint16_t *mn;
+    const uint16_t *lhs;
+    uint16_t *dst;
+    uint32_t n, k, n_pad, nchunks, m;
+    uint32_t block_shift;  // log2(block)
+};
+
+constexpr int MF_WAVES = 8;                  // waves per workgroup (K slices)
+constexpr int MF_U = 4;                      // steps (4 chunks each) in flight per lane
+constexpr int MF_SEG = 4096;                 // depths of A staged in LDS at a time
+constexpr int MF_SEG_CH = MF_SEG / Q4_CHUNK; // 128 chunks per segment
+
+// One wait of a chained call (thread 0 of the workgroup): polls *ready until it
+// reaches need or the device wall clock has advanced `ticks` (and at most 2^24
+// polls), then an agent-scope acquire, so the producer's stores of A below
+// need are visible to the loads that follow the workgroup barrier.
+__device__ __forceinline__ bool chain_wait(const unsigned long long *ready, unsigned long long need,
+                                           unsigned long long ticks) {
+    const unsigned long long t0 = wall_clock64();
+    for (uint32_t it = 0; it < (1u << 24); it++) {
+        if (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= need) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            return true;
+        }
+        if (wall_clock64() - t0 > ticks) break;
+        __builtin_amdgcn_s_sleep(4);
+    }
+    return false;
+}
+
+// Activation source: MR rows of a row-major f16 [m][k] array (rows >= m and
+// depths >= k read as zero, through buffer loads with no branches).
+// A source loads thread t's share of a segment (`load`, issued before the
+// weight loads) into its Regs and writes the segment's f16 rows to LDS
+// (`stage`, all threads, between two barriers).
+template <int MR>
+struct SrcRows {
+    struct Regs {
+        uint4 r[MR];
+    };
+    rsrc_t ar;
+    uint32_t m, k;
+    bool vec;
+    __device__ SrcRows(const uint16_t *lhs, uint32_t m_, uint32_t k_)
+        : ar(make_rsrc(lhs, m_ * k_ * 2u)), m(m_), k(k_), vec((k_ & 7) == 0) {}
+    // thread t's 8 depths d0 + 8t .. +8 of every row
+    __device__ void load(Regs &a, uint32_t d0, int t) const {
+#pragma unroll
+        for (int r = 0; r < MR; r++) a.r[r] = load_row8(ar, r, m, k, d0 + 8 * t, vec);
+    }
+    __device__ void stage(uint16_t *a_lds, const Regs &a, int t) const {
+#pragma unroll
+        for (int r = 0; r < MR; r++) *(uint4 *)(a_lds + r * MF_SEG + 8 * t) = a.r[r];
+    }
+};
+
+// The workgroup's accumulator tile for 16 columns (col = tile*16 + lane%16):
+// lane holds D[col = 4*(lane/16) + v][row = lane%16] of its wave's K slice.
+// CHAIN: the chained GEMV's wait for its producer (ch.ready) between the weight
+// loads and the activation loads of each segment; timed_out reports a wait
+// that expired (uniform over the workgroup; the tile is then incomplete).
+template <int MR, bool CHAIN, class Src>
+__device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const Src &src,
+                                                     const ChainArgs &ch, uint16_t *a_lds, uint32_t col,
+                                                     bool &timed_out) {
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int c = lane & 15, grp = lane >> 4;
+    // the bfi magics live in VGPRs (a VOP3 takes one scalar operand)
+    const uint32_t mag_lo = __builtin_amdgcn_readfirstlane(0x64006400u) | (uint32_t)(t >> 30);
+    const uint32_t mag_hi = __builtin_amdgcn_readfirstlane(0x54005400u) | (uint32_t)(t >> 30);
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    timed_out = false;
+    const uint32_t last = g.nchunks - 1;  // nchunks >= 1 here
+    const uint32_t nseg = (g.nchunks + MF_SEG_CH - 1) / MF_SEG_CH;
+    for (uint32_t seg = 0; seg < nseg; seg++) {
+        const uint32_t sc0 = seg * MF_SEG_CH;
+        // A[:, segment] first: vmcnt retires in issue order, so loads issued
+        // before the weights can be waited on while the weights stay in flight
+        const uint32_t d0 = sc0 * Q4_CHUNK;
+        typename Src::Regs areg;
+        bool a_first = true;  // a chained call that awaits A reads it after its weights
+        if constexpr (CHAIN) a_first = ch.ready == nullptr;
+        if (a_first) src.load(areg, d0, t);
+        // steps of this wave within the segment: chunks sc0 + 4*(wave + 8*u) + grp
+        uint4 wq[MF_U];
+        uint16_t sv[MF_U];
+#pragma unroll
+        for (int u = 0; u < MF_U; u++) {
+            const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
+            const uint32_t kcc = kc < last ? kc : last;  // clamped: always a valid load
+            wq[u] = *(const uint4 *)(g.nib + ((size_t)kcc * g.n_pad + col) * 16);
+            const uint16_t sl = g.sc[(size_t)((kcc * Q4_CHUNK) >> g.block_shift) * g.n_pad + col];
+            sv[u] = kc < g.nchunks ? sl : (uint16_t)0;  // a dead step's weights become 0
+        }
+        if constexpr (CHAIN) {
+            // the weights stream in while the producer of A finishes; A's
+            // segment is read only once *ready covers it
+            if (ch.ready) {
+                __shared__ uint32_t seg_ok;
+                if (t == 0) {
+                    const uint32_t need = g.k < d0 + MF_SEG ? g.k : d0 + MF_SEG;
+                    seg_ok = chain_wait(ch.ready, need, ch.wait_ticks) ? 1u : 0u;
+                }
+                __syncthreads();
+                if (!seg_ok) {
+                    timed_out = true;
+                    break;
+                }
+                src.load(areg, d0, t);
+            }
+        }
+        // stage A[:, segment] (rows < m, zero past k)
+        __syncthreads();
+        src.stage(a_lds, areg, t);
+        __syncthreads();
+        // dequant + MFMA: A operand = 16 columns x 32 depths of weights, B
+        // operand = 32 depths x 16 rows of activations (rows >= m are zero).
+        // All of this wave's activation fragments are read first, from a valid
+        // row (branch-free, then selected), so the LDS round trips overlap
+        // instead of each one preceding its MFMA.
+        const int row = c;  // B-operand lane: activation row lane%16
+        const bool row_live = row < MR;
+        const uint16_t *arow = a_lds + (row_live ? row : 0) * MF_SEG;
+        uint4 abv[MF_U][4];
+#pragma unroll
+        for (int u = 0; u < MF_U; u++) {
+            const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
+            const bool live = row_live && kc < g.nchunks;
+            const uint32_t kcl = kc < g.nchunks ? kc - sc0 : 0;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const uint4 v = *(const uint4 *)(arow + kcl * Q4_CHUNK + w * 8);
+                abv[u][w] = live ? v : make_uint4(0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < MF_U; u++) {
+            const half2_t s2 = {__builtin_bit_cast(_Float16, sv[u]), __builtin_bit_cast(_Float16, sv[u])};
+            const uint32_t words[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                uint4 wa = q4_deq8(words[w], s2, mag_lo, mag_hi);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wa),
+                                                             __builtin_bit_cast(half8_t, abv[u][w]), acc,
+                                                             0, 0, 0);
+            }
+        }
+    }
+    return acc;
+}
+
+// The 8 waves' partial tiles into red[MF_WAVES][16 cols][MR] (LDS, after a
+// barrier; a_lds may alias red), then a barrier: afterwards tile_total(red,
+// cc, r) is column cc's (0..15) sum for row r, in a fixed wave order.
+template <int MR>
+__device__ __forceinline__ void q4_mfma_reduce(const float4_t &acc, float *red) {
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int c = lane & 15, grp = lane >> 4;
+    __syncthreads();
+    if (c < MR) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) red[(wave * 16 + 4 * grp + v) * MR + c] = acc[v];
+    }
+    __syncthreads();
+}
+template <int MR>
+__device__ __forceinline__ float tile_total(const float *red, int cc, int r) {
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < MF_WAVES; w++) total = total + red[(w * 16 + cc) * MR + r];
+    return total;
+}
+
+// LDS bytes of a q4_mfma_mainloop kernel staging MR rows (also covers red).
+template <int MR>
+constexpr size_t q4_mfma_lds_bytes() {
+    return (size_t)MR * MF_SEG * 2 > (size_t)MF_WAVES * 16 * MR * 4 ? (size_t)MR * MF_SEG * 2
+                                                                     : (size_t)MF_WAVES * 16 * MR * 4;
+}
+
+inline Q4GemvArgs q4_gemv_args(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs) {
+    Q4GemvArgs g;
+    g.nib = w.codes;
+    g.sc = w.scales;
+    g.mn = w.mins;
+    g.lhs = lhs;
+    g.dst = dst;
+    g.n = (uint32_t)w.n;
+    g.k = (uint32_t)w.k;
+    g.n_pad = (uint32_t)w.n_pad;
+    g.nchunks = (uint32_t)w.nchunks;
+    g.m = (uint32_t)m;
+    g.block_shift = (uint32_t)__builtin_ctzll(w.block);
+    return g;
+}
+
+}  // namespace smg

@@ -95,6 +95,35 @@ def lib() -> C.CDLL:
     L.smg_lowbit_mopa_dev.argtypes = [SZ, P, P, P, P, P]
     L.smg_packed_matmul_dev.argtypes = [SZ, P, P, C.c_long, C.c_long, P, C.c_long, C.c_long,
                                         C.c_uint16, P, C.c_int, P]
+    L.smg_ep_check.argtypes = [P, SZ]
+    L.smg_q4_interleave.argtypes = [P, P, W]
+    # the decode block
+    L.smg_kv_cache_create.argtypes = [SZ, SZ, SZ, SZ, W]
+    L.smg_kv_cache_destroy.argtypes = [P]
+    L.smg_kv_cache_destroy.restype = None
+    L.smg_kv_cache_info.argtypes = [P, C.POINTER(SZ), C.POINTER(SZ), C.POINTER(C.c_float)]
+    L.smg_kv_cache_truncate.argtypes = [P, SZ]
+    L.smg_kv_cache_set_scale.argtypes = [P, C.c_float]
+    L.smg_kv_cache_storage.argtypes = [P, W, W]
+    L.smg_kv_cache_read_dev.argtypes = [P, P, P, P]
+    L.smg_kv_cache_extend_dev.argtypes = [P, P, P, SZ, P]
+    L.smg_kv_cache_attend_dev.argtypes = [P, P, P, P]
+    L.smg_attention_kv_f16_dev.argtypes = [P, P, P, SZ, SZ, SZ, SZ, C.c_float, P, P]
+    L.smg_rms_norm_f16_dev.argtypes = [P, P, SZ, SZ, C.c_float, P, P]
+    L.smg_glu_f16_dev.argtypes = [P, SZ, SZ, C.c_uint32, P, P]
+    L.smg_q4_accumulate_dev.argtypes = [SZ, P, P, P, P]
+    L.smg_attn_create.argtypes = [P, P, SZ, SZ, SZ, C.c_double, W]
+    L.smg_attn_destroy.argtypes = [P]
+    L.smg_attn_destroy.restype = None
+    L.smg_attn_accumulate_dev.argtypes = [P, P, P, P, SZ, P]
+    L.smg_mlp_create.argtypes = [P, P, C.c_uint32, C.c_int, W]
+    L.smg_mlp_destroy.argtypes = [P]
+    L.smg_mlp_destroy.restype = None
+    L.smg_mlp_accumulate_dev.argtypes = [P, P, P, SZ, P]
+    L.smg_block_create.argtypes = [P, C.c_float, P, C.c_float, SZ, P, P, W]
+    L.smg_block_destroy.argtypes = [P]
+    L.smg_block_destroy.restype = None
+    L.smg_block_accumulate_dev.argtypes = [P, P, P, SZ, P]
     _lib = L
     return L
 
@@ -911,3 +940,449 @@ def matmul_f16_packed(a, packed: Packed, c, m: int):
 
 def matmul_bf16_packed(a, packed: Packed, c, m: int):
     return Gemm(a, packed, m).run(c)
+
+
+# ---- the model-level parts: Linear, GatedLinear, Mlp, KvCache, SelfAttention,
+# ---- Norm, Block and the nn passes (src/linear.rs, src/mlp.rs,
+# ---- src/self_attention.rs, src/kernels/kv_attention.rs, src/nn.rs, src/block.rs)
+#
+# They run on device tensors (torch, on torch's current stream): residual
+# streams float32, activations handed between parts float16, as the
+# reference's f32 residual / f16 kernel inputs (src/linear.rs:14-29).
+
+class Gate:
+    """src/linear.rs:563-575: the activation an MLP applies (silu / tanh gelu)."""
+    Silu = EP_ACT["silu"]
+    Gelu = EP_ACT["gelu"]
+
+
+def _take(w: _Handle) -> C.c_void_p:
+    """Hands a weight handle over to a part that takes it over (the reference's
+    constructors move their Linears): the Python object no longer owns it."""
+    h = w._h
+    if not h:
+        raise ValueError("these weights were already handed to another part")
+    w._h = None
+    return h
+
+
+def _f32dev(x, n, what, device):
+    if x.dtype.itemsize != 4 or not x.is_floating_point():
+        raise TypeError(f"{what}: expected a float32 tensor, got {x.dtype}")
+    if not x.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    if device is not None and x.device.index != device:
+        raise ValueError(f"{what} is on cuda:{x.device.index}, the weights on cuda:{device}")
+    if n is not None and x.numel() != n:
+        raise ValueError(f"{what} has {x.numel()} elements, expected {n}")
+    return x
+
+
+class Linear:
+    """A 4-bit linear layer y = x @ W, n outputs by k inputs (src/linear.rs:139):
+    Linear::from_q4 / quantize over resident Q4Weights."""
+
+    def __init__(self, q4: Q4Weights):
+        self.q4 = q4
+
+    @classmethod
+    def from_q4(cls, q4: Q4Weights) -> "Linear":
+        return cls(q4)
+
+    @classmethod
+    def quantize(cls, w, layout: int, n: int, k: int, p: Q4Params | None = None) -> "Linear":
+        """Linear::quantize / quantize_with (src/linear.rs:178-193)."""
+        return cls(Q4Weights.quantize(w, layout, n, k, p))
+
+    def n(self) -> int:
+        return self.q4.n()
+
+    def k(self) -> int:
+        return self.q4.k()
+
+    def forward(self, x, y, m: int):
+        """Linear::forward (src/linear.rs:373): y = x @ W, f16."""
+        return matmul_q4(x, self.q4, y, m)
+
+    def forward_ep(self, x, y, m: int, ep: Epilogue):
+        return matmul_q4_ep(x, self.q4, y, m, ep)
+
+    def accumulate(self, x, y, m: int):
+        """Linear::accumulate (src/linear.rs:425-432): y (f32) += f32(f16(x @ W))."""
+        dev = self.q4.device()
+        _dev16(x, m * self.k(), "x (m*k)", dev, False)
+        _f32dev(y, m * self.n(), "y (m*n)", dev)
+        _check(lib().smg_q4_accumulate_dev(m, self.q4._h, y.data_ptr(), x.data_ptr(), _stream()),
+               "smg_q4_accumulate_dev")
+        return y
+
+
+class GatedLinear:
+    """act(x @ W_gate) * (x @ W_up) as one 2n-output Q4 Linear, gate and up
+    interleaved 32 columns at a time (src/linear.rs:596-801)."""
+
+    def __init__(self, inner: Linear, gate: int):
+        if inner.n() % 2:
+            raise ValueError("a gated layer has 2n outputs")
+        self.inner = inner
+        self._gate = gate
+
+    @classmethod
+    def quantize(cls, w_gate, w_up, layout: int, n: int, k: int, gate: int,
+                 p: Q4Params | None = None) -> "GatedLinear":
+        """GatedLinear::quantize / quantize_with (src/linear.rs:625-671)."""
+        def inout(w):
+            w = np.asarray(w, np.float32).reshape(-1)
+            if w.size != n * k:
+                raise ValueError("w holds n * k weights")
+            return w.reshape(n, k).T if layout == WeightLayout.OutIn else w.reshape(k, n)
+        g, u = inout(w_gate), inout(w_up)
+        parts = []
+        for c0 in range(0, n, 32):
+            c1 = min(c0 + 32, n)
+            parts += [g[:, c0:c1], u[:, c0:c1]]
+        both = np.ascontiguousarray(np.concatenate(parts, axis=1))
+        return cls(Linear.quantize(both, WeightLayout.InOut, 2 * n, k, p), gate)
+
+    @classmethod
+    def from_q4(cls, gate_w: Q4Weights, up_w: Q4Weights, gate: int) -> "GatedLinear":
+        """The interleave of two Q4 weight sets, exactly (as
+        GatedLinear::from_q1 does for 1-bit weights, src/linear.rs:697-704)."""
+        import copy
+        h = C.c_void_p()
+        _check(lib().smg_q4_interleave(gate_w._h, up_w._h, C.byref(h)), "smg_q4_interleave")
+        c = copy.copy(gate_w)
+        c._h = h
+        c._n = 2 * gate_w.n()
+        return cls(Linear(c), gate)
+
+    def n(self) -> int:
+        return self.inner.n() // 2
+
+    def k(self) -> int:
+        return self.inner.k()
+
+    def gate(self) -> int:
+        return self._gate
+
+    def forward(self, x, y, m: int):
+        """GatedLinear::forward (src/linear.rs:779-791): the 2n-output GEMV, then glu."""
+        import torch
+        both = torch.empty(m * 2 * self.n(), dtype=torch.float16, device=x.device)
+        self.inner.forward(x, both, m)
+        return glu(both, m, self.n(), self._gate, y)
+
+
+class Mlp:
+    """y += down(act(up(x))) (Mlp::new) or y += down(act(x @ W_gate) * (x @ W_up))
+    (Mlp::gated), src/mlp.rs:56-149: the up GEMV with its activation (or glu)
+    at the store, then the down GEMV adding into y. Takes over its layers."""
+
+    def __init__(self, up, act: int, down: Linear, gated: bool):
+        if down.k() != (up.n()):
+            raise ValueError("down takes up's outputs")
+        self._k, self._n, self._hidden = up.k(), down.n(), up.n()
+        upw = up.inner.q4 if gated else up.q4
+        h = C.c_void_p()
+        _check(lib().smg_mlp_create(upw._h, down.q4._h, act, int(gated), C.byref(h)), "smg_mlp_create")
+        _take(upw)
+        _take(down.q4)
+        self._h = h
+        self._device = torch_device_index()
+
+    @classmethod
+    def new(cls, up: Linear, act: int, down: Linear) -> "Mlp":
+        return cls(up, act, down, False)
+
+    @classmethod
+    def gated(cls, up: GatedLinear, down: Linear) -> "Mlp":
+        return cls(up, up.gate(), down, True)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.smg_mlp_destroy(h)
+            self._h = None
+
+    def k(self) -> int:
+        return self._k
+
+    def n(self) -> int:
+        return self._n
+
+    def hidden(self) -> int:
+        return self._hidden
+
+    def accumulate(self, x, y, m: int):
+        """Mlp::accumulate (src/mlp.rs:113-149): y (f32 m x n) += ... for x f16."""
+        _dev16(x, m * self._k, "x (m*k)", self._device, False)
+        _f32dev(y, m * self._n, "y (m*n)", self._device)
+        _check(lib().smg_mlp_accumulate_dev(self._h, x.data_ptr(), y.data_ptr(), m, _stream()),
+               "smg_mlp_accumulate_dev")
+        return y
+
+
+def torch_device_index() -> int:
+    import torch
+    return torch.cuda.current_device()
+
+
+class KvCache:
+    """An f16 key/value cache for one attention layer on the device
+    (src/kernels/kv_attention.rs:342-578)."""
+
+    def __init__(self, heads: int, kv_heads: int, head_dim: int, capacity: int):
+        h = C.c_void_p()
+        _check(lib().smg_kv_cache_create(heads, kv_heads, head_dim, capacity, C.byref(h)),
+               "KvCache::new")
+        self._h = h
+        self._heads, self._kv_heads, self._hd = heads, kv_heads, head_dim
+        self._device = torch_device_index()
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.smg_kv_cache_destroy(h)
+            self._h = None
+
+    def _info(self):
+        ln, cap, sc = SZ(), SZ(), C.c_float()
+        _check(lib().smg_kv_cache_info(self._h, C.byref(ln), C.byref(cap), C.byref(sc)), "smg_kv_cache_info")
+        return ln.value, cap.value, sc.value
+
+    def with_scale(self, scale: float) -> "KvCache":
+        _check(lib().smg_kv_cache_set_scale(self._h, float(np.float32(scale))), "with_scale")
+        return self
+
+    def len(self) -> int:
+        return self._info()[0]
+
+    def is_empty(self) -> bool:
+        return self.len() == 0
+
+    def capacity(self) -> int:
+        return self._info()[1]
+
+    def scale(self) -> float:
+        return self._info()[2]
+
+    def heads(self) -> int:
+        return self._heads
+
+    def kv_heads(self) -> int:
+        return self._kv_heads
+
+    def head_dim(self) -> int:
+        return self._hd
+
+    def row_len(self) -> int:
+        return self._kv_heads * self._hd
+
+    def query_len(self) -> int:
+        return self._heads * self._hd
+
+    def clear(self):
+        _check(lib().smg_kv_cache_truncate(self._h, 0), "clear")
+
+    def truncate(self, length: int):
+        _check(lib().smg_kv_cache_truncate(self._h, length), "truncate")
+
+    def extend(self, k, v):
+        """KvCache::extend (kv_attention.rs:499-519): whole rows of f16 keys and values."""
+        row = self.row_len()
+        if k.numel() != v.numel() or k.numel() % row or k.numel() == 0:
+            raise ValueError("k and v hold the same whole number of kv_heads * head_dim rows")
+        _dev16(k, None, "k", self._device, False)
+        _dev16(v, None, "v", self._device, False)
+        _check(lib().smg_kv_cache_extend_dev(self._h, k.data_ptr(), v.data_ptr(), k.numel() // row,
+                                             _stream()), "KvCache::extend")
+
+    push = extend
+
+    def _rows(self, which: int):
+        """The first len() rows of the keys (0) or values (1), copied into a
+        new f16 device tensor (keys() / values(), kv_attention.rs:522-531)."""
+        import torch
+        n = self.len() * self.row_len()
+        out = torch.empty(n, dtype=torch.float16, device=f"cuda:{self._device}")
+        if n:
+            k = out.data_ptr() if which == 0 else None
+            v = out.data_ptr() if which == 1 else None
+            _check(lib().smg_kv_cache_read_dev(self._h, k, v, _stream()), "smg_kv_cache_read_dev")
+        return out
+
+    def keys(self):
+        return self._rows(0)
+
+    def values(self):
+        return self._rows(1)
+
+    def attend(self, q, out):
+        """KvCache::attend (kv_attention.rs:537-552): q and out f32 heads*head_dim."""
+        _f32dev(q, self.query_len(), "q", self._device)
+        _f32dev(out, self.query_len(), "out", self._device)
+        _check(lib().smg_kv_cache_attend_dev(self._h, q.data_ptr(), out.data_ptr(), _stream()), "attend")
+        return out
+
+
+class SelfAttention:
+    """y += out(attention(qkv(x))) over a KvCache (src/self_attention.rs:69-183),
+    at one row. rope_theta > 0 adds the NeoX rotary embedding to q and k as
+    examples/bonsai/model.rs:30-99 does (not part of the library's
+    SelfAttention). Takes over its two layers."""
+
+    def __init__(self, qkv: Linear, out: Linear, heads: int, kv_heads: int, head_dim: int,
+                 rope_theta: float = 0.0):
+        if kv_heads <= 0 or heads <= 0 or heads % kv_heads:
+            raise ValueError("heads must be a positive multiple of kv_heads")
+        if qkv.n() != (heads + 2 * kv_heads) * head_dim:
+            raise ValueError("qkv has (heads + 2 kv_heads) * head_dim outputs")
+        if out.k() != heads * head_dim:
+            raise ValueError("out takes heads * head_dim inputs")
+        self._width, self._out_width = qkv.k(), out.n()
+        self._heads, self._kv_heads, self._hd = heads, kv_heads, head_dim
+        h = C.c_void_p()
+        _check(lib().smg_attn_create(qkv.q4._h, out.q4._h, heads, kv_heads, head_dim, float(rope_theta),
+                                     C.byref(h)), "SelfAttention::new")
+        _take(qkv.q4)
+        _take(out.q4)
+        self._h = h
+        self._device = torch_device_index()
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.smg_attn_destroy(h)
+            self._h = None
+
+    def width(self) -> int:
+        return self._width
+
+    def out_width(self) -> int:
+        return self._out_width
+
+    def cache(self, capacity: int) -> KvCache:
+        return KvCache(self._heads, self._kv_heads, self._hd, capacity)
+
+    def accumulate(self, x, cache: KvCache, y, m: int):
+        """SelfAttention::accumulate (self_attention.rs:148-183) for m = 1."""
+        _dev16(x, m * self._width, "x (m*width)", self._device, False)
+        _f32dev(y, m * self._out_width, "y (m*out.n)", self._device)
+        _check(lib().smg_attn_accumulate_dev(self._h, x.data_ptr(), cache._h, y.data_ptr(), m, _stream()),
+               "SelfAttention::accumulate")
+        return y
+
+
+class Norm:
+    """nn::Norm (src/nn.rs:164-235): RMSNorm on the GPU path (Norm::rms)."""
+
+    def __init__(self, weight, eps: float):
+        w = np.ascontiguousarray(np.asarray(weight, np.float32).ravel())
+        if w.size == 0:
+            raise ValueError("a norm needs at least one feature")
+        self.weight = w
+        self.eps = float(np.float32(eps))
+        self._dev = None
+
+    @classmethod
+    def rms(cls, weight, eps: float) -> "Norm":
+        return cls(weight, eps)
+
+    @classmethod
+    def layer(cls, weight, bias, eps):
+        raise SmeGemmError("Norm::layer is not on the GPU path (the decode block uses RMSNorm)")
+
+    def width(self) -> int:
+        return self.weight.size
+
+    def forward(self, x, y):
+        """Norm::forward (src/nn.rs:227): f32 rows x to f16 y."""
+        import torch
+        if self._dev is None:
+            self._dev = torch.from_numpy(self.weight).cuda()
+        return rms_norm(x, self._dev, self.eps, y)
+
+
+class Block:
+    """A pre-norm transformer layer over an f32 residual stream
+    (src/block.rs:40-107): x += attn(norm1(x)), then x += mlp(norm2(x)).
+    Takes over its attention and MLP."""
+
+    def __init__(self, norm1: Norm, attn: SelfAttention, norm2: Norm, mlp: Mlp):
+        d = attn.width()
+        if not (norm1.width() == d and attn.out_width() == d and norm2.width() == d and mlp.k() == d
+                and mlp.n() == d):
+            raise ValueError("the norms, attention and MLP share the residual's width")
+        h = C.c_void_p()
+        _check(lib().smg_block_create(norm1.weight.ctypes.data, norm1.eps, norm2.weight.ctypes.data, norm2.eps,
+                                      d, attn._h, mlp._h, C.byref(h)), "Block::new")
+        attn._h = None
+        mlp._h = None
+        self._h = h
+        self._d = d
+        self._attn_shape = (attn._heads, attn._kv_heads, attn._hd)
+        self._device = torch_device_index()
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _lib is not None:
+            _lib.smg_block_destroy(h)
+            self._h = None
+
+    def width(self) -> int:
+        return self._d
+
+    def cache(self, capacity: int) -> KvCache:
+        return KvCache(*self._attn_shape, capacity)
+
+    def accumulate(self, x, cache: KvCache, rows: int):
+        """Block::accumulate (src/block.rs:90-106), rows = 1."""
+        _f32dev(x, rows * self._d, "x (rows*width)", self._device)
+        _check(lib().smg_block_accumulate_dev(self._h, x.data_ptr(), cache._h, rows, _stream()),
+               "Block::accumulate")
+        return x
+
+
+def rms_norm(x, weight, eps: float, y):
+    """nn::rms_norm (src/nn.rs:147-161): f32 rows of x to f16 y; weight f32 device."""
+    dim = weight.numel()
+    if dim == 0 or x.numel() % dim:
+        raise ValueError("x holds whole rows of weight.len()")
+    dev = x.device.index
+    _f32dev(x, None, "x", dev)
+    _f32dev(weight, dim, "weight", dev)
+    _dev16(y, x.numel(), "y", dev, False)
+    _check(lib().smg_rms_norm_f16_dev(x.data_ptr(), weight.data_ptr(), x.numel() // dim, dim,
+                                      float(np.float32(eps)), y.data_ptr(), _stream()), "rms_norm")
+    return y
+
+
+def glu(both, m: int, n: int, gate: int, y):
+    """GatedLinear's glu (src/linear.rs:804-826) over m rows of 2n interleaved f16."""
+    dev = both.device.index
+    _dev16(both, m * 2 * n, "both", dev, False)
+    _dev16(y, m * n, "y", dev, False)
+    _check(lib().smg_glu_f16_dev(both.data_ptr(), m, n, gate, y.data_ptr(), _stream()), "glu")
+    return y
+
+
+def attention_kv_f16(q, k, v, length: int, heads: int, kv_heads: int, head_dim: int, scale: float, out):
+    """attention_kv_f16 (src/kernels/kv_attention.rs:29-78) on device tensors."""
+    if length == 0:
+        raise ValueError("attention_kv_f16 needs at least one cached key")
+    if head_dim % 8 or not 8 <= head_dim <= 256:
+        raise ValueError("head_dim must be a multiple of 8 in 8..=256")
+    if kv_heads <= 0 or heads <= 0 or heads % kv_heads:
+        raise ValueError("heads must be a positive multiple of kv_heads")
+    ld = kv_heads * head_dim
+    dev = q.device.index
+    _f32dev(q, heads * head_dim, "q", dev)
+    _f32dev(out, heads * head_dim, "out", dev)
+    for t, name in ((k, "k"), (v, "v")):
+        _dev16(t, None, name, dev, False)
+        if t.numel() < length * ld:
+            raise ValueError(f"{name} holds len * kv_heads * head_dim")
+    _check(lib().smg_attention_kv_f16_dev(q.data_ptr(), k.data_ptr(), v.data_ptr(), length, heads, kv_heads,
+                                          head_dim, float(np.float32(scale)), out.data_ptr(), _stream()),
+           "attention_kv_f16")
+    return out

@@ -76,3 +76,44 @@ def q2_bytes(m, n, k, block=128):
 def q1_bytes(m, n, k, block=128, n_col_vectors=1):
     nbk = -(-k // block)
     return (k * n + 7) // 8 + 2 * n * nbk + 2 * m * k + 2 * m * n + 2 * n * n_col_vectors
+
+
+# Config 5: one Llama-style decoder block at one row (src/block.rs path).
+CONFIG5 = dict(d=4096, heads=32, kv_heads=8, head_dim=128, ffn=14336, past=4096, theta=10000.0,
+               eps=1e-5)
+
+
+def block_inputs(d: int, heads: int, kv_heads: int, head_dim: int, ffn: int, past: int,
+                 seed: int = 0, cap_extra: int = 8):
+    """The decode block's weights and state (config 5 at its default sizes):
+    Q4 linears as config 1 (nibbles uniform 0..15, scales ~ U[0.005, 0.02] per
+    32-block, row-major public input) -- qkv ((heads + 2 kv_heads) * head_dim
+    outputs, [q | k | v]), out, gate, up (ffn outputs each) and down --, RMSNorm
+    weights ~ U[0.9, 1.1] (f32), `past` cached positions of f16 keys and values
+    ~ N(0, 1) (capacity past + cap_extra), and a residual row x ~ N(0, 1) (f32)."""
+    rng = np.random.default_rng(seed)
+
+    def q4(n, k):
+        quants = rng.integers(0, 256, size=(k * n + 1) // 2, dtype=np.uint8)
+        scales = f16(rng.uniform(0.005, 0.02, size=n * -(-k // 32)))
+        return quants, scales, n, k
+
+    nq = (heads + 2 * kv_heads) * head_dim
+    ld = kv_heads * head_dim
+    cap = past + cap_extra
+    out = dict(
+        qkv=q4(nq, d), out=q4(d, heads * head_dim), gate=q4(ffn, d), up=q4(ffn, d), down=q4(d, ffn),
+        norm1=rng.uniform(0.9, 1.1, d).astype(np.float32),
+        norm2=rng.uniform(0.9, 1.1, d).astype(np.float32),
+        cache_k=np.zeros((cap, ld), np.uint16), cache_v=np.zeros((cap, ld), np.uint16),
+        x=rng.standard_normal(d).astype(np.float32))
+    out["cache_k"][:past] = f16(rng.standard_normal((past, ld)))
+    out["cache_v"][:past] = f16(rng.standard_normal((past, ld)))
+    return out
+
+
+def block_bytes(d, heads, kv_heads, head_dim, ffn, kv_len, block=32):
+    """Algorithmic HBM bytes of one decode step: every Q4 weight (0.5 B) and
+    its f16 scale (2 B per 32-block), and the f16 keys and values read."""
+    weights = d * (heads + 2 * kv_heads) * head_dim + heads * head_dim * d + 2 * ffn * d + ffn * d
+    return weights // 2 + weights // block * 2 + 2 * 2 * kv_len * kv_heads * head_dim

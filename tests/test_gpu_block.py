@@ -1,0 +1,399 @@
+"""The decode block (config 5) and its parts on the GPU against the oracle's
+restatement of the reference's portable path (oracle/: nn::rms_norm,
+attention_kv_f16's one_row, glu, the Q4 GEMV, Block::accumulate with
+examples/bonsai's RoPE).
+
+Bars (rel = |g - w| / (1 + |w|), the reference's max_rel,
+tests/correctness/main.rs:63-68):
+- f16 GEMV-derived values (projections, the hidden layer): rel <= f16_tol(K),
+  the north star's 2e-3 * sqrt(K)/64 at the GEMV's depth;
+- the block's f32 residual: it adds two f16 terms, the out projection's A
+  (K = heads*head_dim) and the down projection's M (K = ffn), each held to the
+  GEMV bar, so |g - w| <= f16_tol(K_A)(1 + |A|) + f16_tol(K_M)(1 + |M|) per
+  element with A, M the oracle's terms (an error relative to the result would
+  be wrong where A and M cancel); and the whole update within 1e-3 of the
+  oracle's in relative norm;
+- rms_norm: within one f16 ulp (the sum of squares runs in another order);
+- attention: within 2e-3 absolute of the f64 oracle on the reference's own
+  test data (tests/correctness/kv_attention.rs:43-82), and within
+  1e-4 * (1 + max |v|) of the portable one_row (same q rounding, sums in other
+  orders); one cached key gives its value row bit for bit.
+"""
+import numpy as np
+import pytest
+
+import workloads as WL
+from conftest import f16_tol, max_rel, ulp_dist
+
+pytestmark = pytest.mark.gpu
+
+
+def _h16(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x, np.uint16).view(np.float16)).cuda()
+
+
+def _f32(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+
+
+def _np16(t):
+    return t.cpu().numpy().view(np.uint16).ravel()
+
+
+def _rel32(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want) / (1.0 + np.abs(want))))
+
+
+# ---- row passes --------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,dim", [(1, 8), (3, 100), (2, 384), (1, 4096), (2, 4099), (1, 14336)])
+def test_rms_norm_within_one_ulp(smg, orc, rows, dim):
+    rng = np.random.default_rng(dim)
+    x = (rng.standard_normal(rows * dim) * 3 + 0.5).astype(np.float32)
+    w = rng.uniform(0.9, 1.1, dim).astype(np.float32)
+    import torch
+    y = torch.empty(rows * dim, dtype=torch.float16, device="cuda")
+    smg.rms_norm(_f32(x), _f32(w), 1e-5, y)
+    torch.cuda.synchronize()
+    want = orc.rms_norm_f16(x, w, 1e-5, rows)
+    got = _np16(y)
+    assert ulp_dist(got, want) <= 1
+    assert np.mean(got == want) > 0.99
+
+
+@pytest.mark.parametrize("n,gate", [(100, "Silu"), (64, "Gelu"), (14336, "Silu"), (5, "Silu")])
+def test_glu_matches_oracle(smg, orc, n, gate):
+    import torch
+    m = 3
+    rng = np.random.default_rng(n + len(gate))
+    both = orc.f32_to_f16((rng.standard_normal(m * 2 * n) * 4).astype(np.float32))
+    y = torch.empty(m * n, dtype=torch.float16, device="cuda")
+    smg.glu(_h16(both), m, n, getattr(smg.Gate, gate), y)
+    torch.cuda.synchronize()
+    want = orc.glu_f16(both, m, n, gate == "Gelu")
+    got = _np16(y)
+    # tests/correctness/model.rs:283: |got - want| <= 2e-3 (1 + |want|)
+    assert max_rel(got, want) <= 2e-3
+    if gate == "Silu":
+        # the same formula, the device's exp: nearly every value the same bits
+        # (gelu's 1 + tanh(x) cancels for negative gates, where the two libms'
+        # tanh near -1 decide the low bits and even the sign of a zero)
+        assert np.mean(got == want) > 0.98
+
+
+# ---- attention -----------------------------------------------------------------------
+
+def _attn64(q, k, v, length, heads, kv_heads, hd, scale):
+    ld = kv_heads * hd
+    g = heads // kv_heads
+    kf = np.asarray(k, np.uint16).view(np.float16).astype(np.float64).reshape(-1, ld)
+    vf = np.asarray(v, np.uint16).view(np.float16).astype(np.float64).reshape(-1, ld)
+    out = np.zeros(heads * hd)
+    for h in range(heads):
+        off = (h // g) * hd
+        s = kf[:length, off:off + hd] @ (q[h * hd:(h + 1) * hd].astype(np.float64) * float(scale))
+        e = np.exp(s - s.max())
+        out[h * hd:(h + 1) * hd] = (e / e.sum()) @ vf[:length, off:off + hd]
+    return out
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd", [(1, 1, 8), (6, 6, 64), (8, 2, 64), (4, 1, 128),
+                                               (2, 2, 256), (12, 4, 72), (64, 1, 32)])
+def test_attention_reference_cases(smg, orc, heads, kv_heads, hd):
+    """kv_f16_matches_oracle's shapes, lengths and LCG data, plus 4097 keys."""
+    import torch
+    for length in (1, 2, 3, 4, 5, 7, 31, 128, 257, 4097):
+        s = 0x5EED_0000 ^ (heads * 1000 + hd * 10 + length)
+        ld = kv_heads * hd
+        q, s = orc.lcg_fill_f32(s, heads * hd)
+        q = q * np.float32(8.0)
+        k, s = orc.lcg_fill(s, length * ld)
+        v, s = orc.lcg_fill(s, length * ld)
+        scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+        out = torch.empty(heads * hd, dtype=torch.float32, device="cuda")
+        smg.attention_kv_f16(_f32(q), _h16(k), _h16(v), length, heads, kv_heads, hd, float(scale), out)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        tag = (heads, kv_heads, hd, length)
+        assert np.max(np.abs(got - _attn64(q, k, v, length, heads, kv_heads, hd, scale))) < 2e-3, tag
+        one = orc.attention_kv_f16(q, k, v, length, heads, kv_heads, hd, scale)
+        assert np.max(np.abs(got - one)) <= 1e-4 * (1 + 0.5), tag
+        if length == 1:
+            g = heads // kv_heads
+            vrow = np.concatenate([orc.f16_to_f32(v[(h // g) * hd:(h // g + 1) * hd]) for h in range(heads)])
+            assert np.array_equal(got, vrow), tag
+
+
+def test_attention_config5_shape(smg, orc):
+    """32 query heads over 8 KV heads of 128, 4097 keys ~ N(0,1), q ~ N(0, 4)."""
+    import torch
+    heads, kv_heads, hd, length = 32, 8, 128, 4097
+    rng = np.random.default_rng(5)
+    q = (rng.standard_normal(heads * hd) * 4).astype(np.float32)
+    k = orc.f32_to_f16(rng.standard_normal(length * kv_heads * hd).astype(np.float32))
+    v = orc.f32_to_f16(rng.standard_normal(length * kv_heads * hd).astype(np.float32))
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    out = torch.empty(heads * hd, dtype=torch.float32, device="cuda")
+    smg.attention_kv_f16(_f32(q), _h16(k), _h16(v), length, heads, kv_heads, hd, float(scale), out)
+    torch.cuda.synchronize()
+    want = orc.attention_kv_f16(q, k, v, length, heads, kv_heads, hd, scale)
+    vmax = float(np.max(np.abs(orc.f16_to_f32(v))))
+    assert np.max(np.abs(out.cpu().numpy() - want)) <= 1e-4 * (1 + vmax)
+
+
+def test_kv_cache_api(smg, orc):
+    """KvCache on the device (kv_attention.rs:342-578; the reference's
+    kv_cache_matches_free_functions): rows pushed one at a time and in blocks
+    hold the same keys, attend is attention_kv_f16 over them, truncate and
+    clear, and a full cache refuses more rows."""
+    import torch
+    heads, kv_heads, hd = 8, 2, 64
+    ld = kv_heads * hd
+    rng = np.random.default_rng(9)
+    length = 37
+    k = orc.f32_to_f16((rng.standard_normal(length * ld) * 0.5).astype(np.float32))
+    v = orc.f32_to_f16((rng.standard_normal(length * ld) * 0.5).astype(np.float32))
+    one = smg.KvCache(heads, kv_heads, hd, 64)
+    for t in range(length):
+        one.push(_h16(k[t * ld:(t + 1) * ld]), _h16(v[t * ld:(t + 1) * ld]))
+    block = smg.KvCache(heads, kv_heads, hd, 64)
+    block.extend(_h16(k[:10 * ld]), _h16(v[:10 * ld]))
+    block.extend(_h16(k[10 * ld:]), _h16(v[10 * ld:]))
+    torch.cuda.synchronize()
+    assert one.len() == block.len() == length and one.capacity() == 64
+    assert np.array_equal(_np16(one.keys()), k) and np.array_equal(_np16(block.values()), v)
+    assert abs(one.scale() - 1.0 / np.sqrt(64.0)) < 1e-7
+    q = (rng.standard_normal(heads * hd) * 8).astype(np.float32)
+    got = torch.empty(heads * hd, dtype=torch.float32, device="cuda")
+    free = torch.empty(heads * hd, dtype=torch.float32, device="cuda")
+    one.attend(_f32(q), got)
+    smg.attention_kv_f16(_f32(q), _h16(k), _h16(v), length, heads, kv_heads, hd, one.scale(), free)
+    torch.cuda.synchronize()
+    assert torch.equal(got, free)
+    one.truncate(3)
+    assert one.len() == 3
+    one.clear()
+    assert one.is_empty()
+    full = smg.KvCache(1, 1, 8, 1)
+    row = _h16(np.zeros(8, np.uint16))
+    full.push(row, row)
+    with pytest.raises(smg.SmeGemmError, match="KvCache full"):
+        full.push(row, row)
+    with pytest.raises(smg.SmeGemmError):
+        smg.KvCache(3, 2, 64, 4)  # heads not a multiple of kv_heads
+    with pytest.raises(smg.SmeGemmError):
+        smg.KvCache(2, 2, 12, 4)  # head_dim not a multiple of 8
+
+
+# ---- projections ----------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (3, 200, 96), (8, 512, 1024), (12, 256, 512)])
+def test_linear_accumulate(smg, orc, m, n, k):
+    """Linear::accumulate (src/linear.rs:425-432): y += f32(f16(x @ W))."""
+    import torch
+    a, quants, scales, _ = WL.q4_inputs(m, n, k, seed=m + n)
+    lin = smg.Linear(smg.Q4Weights(quants, scales, n, k))
+    y0 = np.random.default_rng(1).standard_normal(m * n).astype(np.float32)
+    y = _f32(y0)
+    lin.accumulate(_h16(a), y, m)
+    torch.cuda.synchronize()
+    out16 = orc.matmul_q4_ep(a, quants, scales, None, m, n, k, 32)
+    want = y0 + orc.f16_to_f32(out16)
+    assert _rel32(y.cpu().numpy(), want) <= f16_tol(k)
+
+
+def _mlp_oracle(orc, x16, inp, m, d, ffn, gated, gelu=False):
+    gq, gs, _, _ = inp["gate"]
+    dq, ds, _, _ = inp["down"]
+    if gated:
+        uq, us, _, _ = inp["up"]
+        iq, isc = orc.q4_interleave32(gq, gs, uq, us, ffn, d)
+        both = orc.matmul_q4_ep(x16, iq, isc, None, m, 2 * ffn, d, 32)
+        hid = orc.glu_f16(both, m, ffn, gelu)
+    else:
+        hid = orc.matmul_q4_ep(x16, gq, gs, None, m, ffn, d, 32, (), 2 if gelu else 3)
+    return orc.f16_to_f32(orc.matmul_q4_ep(hid, dq, ds, None, m, d, ffn, 32))
+
+
+@pytest.mark.parametrize("gated,gelu,m,d,ffn", [(True, False, 1, 4096, 14336), (True, False, 3, 256, 320),
+                                                (True, True, 1, 256, 100), (False, True, 2, 256, 320),
+                                                (False, False, 1, 512, 1024), (True, False, 12, 256, 320)])
+def test_mlp_accumulate(smg, orc, gated, gelu, m, d, ffn):
+    """Mlp::gated / Mlp::new accumulate (src/mlp.rs:113-149): the up GEMV with
+    its activation (or glu) at the store, then down adding into y."""
+    import torch
+    inp = WL.block_inputs(d, 2, 1, 64, ffn, 1, seed=ffn + m)
+    gate = smg.Gate.Gelu if gelu else smg.Gate.Silu
+    W = lambda key: smg.Q4Weights(inp[key][0], inp[key][1], inp[key][2], inp[key][3])  # noqa: E731
+    if gated:
+        mlp = smg.Mlp.gated(smg.GatedLinear.from_q4(W("gate"), W("up"), gate), smg.Linear(W("down")))
+    else:
+        mlp = smg.Mlp.new(smg.Linear(W("gate")), gate, smg.Linear(W("down")))
+    assert (mlp.k(), mlp.n(), mlp.hidden()) == (d, d, ffn)
+    x16 = orc.f32_to_f16(np.random.default_rng(m).standard_normal(m * d).astype(np.float32))
+    y0 = np.full(m * d, 0.25, np.float32)
+    y = _f32(y0)
+    mlp.accumulate(_h16(x16), y, m)
+    torch.cuda.synchronize()
+    want = y0 + _mlp_oracle(orc, x16, inp, m, d, ffn, gated, gelu)
+    assert _rel32(y.cpu().numpy(), want) <= f16_tol(ffn)
+
+
+def test_gated_linear_forward(smg, orc):
+    """GatedLinear::forward (src/linear.rs:779-791) from two Q4 weight sets:
+    the interleaved GEMV then glu, against the oracle's interleave."""
+    import torch
+    n, k, m = 100, 256, 2
+    inp = WL.block_inputs(k, 2, 1, 64, n, 1, seed=3)
+    gl = smg.GatedLinear.from_q4(smg.Q4Weights(*inp["gate"][:2], n, k), smg.Q4Weights(*inp["up"][:2], n, k),
+                                 smg.Gate.Silu)
+    x16 = orc.f32_to_f16(np.random.default_rng(4).standard_normal(m * k).astype(np.float32))
+    y = torch.empty(m * n, dtype=torch.float16, device="cuda")
+    gl.forward(_h16(x16), y, m)
+    torch.cuda.synchronize()
+    iq, isc = orc.q4_interleave32(*inp["gate"][:2], *inp["up"][:2], n, k)
+    want = orc.glu_f16(orc.matmul_q4_ep(x16, iq, isc, None, m, 2 * n, k, 32), m, n)
+    assert max_rel(_np16(y), want) <= f16_tol(k)
+
+
+# ---- attention half and the block ----------------------------------------------------------------
+
+def _oracle_params(orc, inp, d, heads, kv_heads, hd, ffn, eps, theta):
+    p = dict(d=d, heads=heads, kv_heads=kv_heads, head_dim=hd, ffn=ffn, eps=eps, theta=theta,
+             norm1=inp["norm1"], norm2=inp["norm2"])
+    for key in ("qkv", "out", "down"):
+        q, s, n, k = inp[key]
+        p[key] = orc.Q4Lin(q, s, n, k)
+    iq, isc = orc.q4_interleave32(*inp["gate"][:2], *inp["up"][:2], ffn, d)
+    p["gate_up"] = orc.Q4Lin(iq, isc, 2 * ffn, d)
+    return p
+
+
+def _gpu_block(smg, inp, d, heads, kv_heads, hd, eps, theta):
+    W = lambda key: smg.Q4Weights(inp[key][0], inp[key][1], inp[key][2], inp[key][3])  # noqa: E731
+    attn = smg.SelfAttention(smg.Linear(W("qkv")), smg.Linear(W("out")), heads, kv_heads, hd, rope_theta=theta)
+    mlp = smg.Mlp.gated(smg.GatedLinear.from_q4(W("gate"), W("up"), smg.Gate.Silu), smg.Linear(W("down")))
+    return smg.Block(smg.Norm.rms(inp["norm1"], eps), attn, smg.Norm.rms(inp["norm2"], eps), mlp)
+
+
+def _check_step(got_x, want_x, x0, parts, k_attn, k_mlp):
+    err = np.abs(got_x.astype(np.float64) - want_x)
+    bound = f16_tol(k_attn) * (1 + np.abs(parts["attn"])) + f16_tol(k_mlp) * (1 + np.abs(parts["mlp"]))
+    assert np.all(err <= bound), float(np.max(err / bound))
+    upd_g, upd_w = got_x.astype(np.float64) - x0, want_x.astype(np.float64) - x0
+    assert np.linalg.norm(upd_g - upd_w) <= 1e-3 * np.linalg.norm(upd_w)
+
+
+def test_block_config5_decode_step(smg, orc):
+    """Config 5 at full size: d 4096, 32 / 8 heads of 128, SwiGLU 14336, 4096
+    cached positions, RoPE 10000, eps 1e-5: one Block::accumulate step against
+    the oracle's, and the cache row it appends."""
+    import torch
+    c = WL.CONFIG5
+    d, H, KV, hd, ffn, past = c["d"], c["heads"], c["kv_heads"], c["head_dim"], c["ffn"], c["past"]
+    inp = WL.block_inputs(d, H, KV, hd, ffn, past, seed=0)
+    blk = _gpu_block(smg, inp, d, H, KV, hd, c["eps"], c["theta"])
+    cache = blk.cache(past + 8)
+    cache.extend(_h16(inp["cache_k"][:past]), _h16(inp["cache_v"][:past]))
+    x = _f32(inp["x"])
+    blk.accumulate(x, cache, 1)
+    torch.cuda.synchronize()
+    p = _oracle_params(orc, inp, d, H, KV, hd, ffn, c["eps"], c["theta"])
+    ck, cv = inp["cache_k"].copy(), inp["cache_v"].copy()
+    parts = {}
+    want = orc.block_decode(inp["x"], ck, cv, past, p, parts)
+    _check_step(x.cpu().numpy(), want, inp["x"], parts, H * hd, ffn)
+    assert cache.len() == past + 1
+    keys = _np16(cache.keys()).reshape(past + 1, KV * hd)
+    vals = _np16(cache.values()).reshape(past + 1, KV * hd)
+    assert np.array_equal(keys[:past], inp["cache_k"][:past])
+    kg, kw = orc.f16_to_f32(keys[past]), orc.f16_to_f32(ck[past])
+    assert np.max(np.abs(kg - kw)) <= 4e-3 * (1 + np.max(np.abs(kw)))
+    assert max_rel(vals[past], cv[past]) <= f16_tol(d)
+
+
+@pytest.mark.parametrize("theta", [10000.0, 0.0])
+def test_block_decode_steps(smg, orc, theta):
+    """Eight decode steps of a small block (d 256, 4 / 2 heads of 64, SwiGLU
+    320) from 37 cached positions, with and without RoPE; each step's residual
+    against the oracle's fed the same input."""
+    import torch
+    d, H, KV, hd, ffn, past, eps = 256, 4, 2, 64, 320, 37, 1e-5
+    inp = WL.block_inputs(d, H, KV, hd, ffn, past, seed=11, cap_extra=16)
+    blk = _gpu_block(smg, inp, d, H, KV, hd, eps, theta)
+    cache = blk.cache(past + 16)
+    cache.extend(_h16(inp["cache_k"][:past]), _h16(inp["cache_v"][:past]))
+    p = _oracle_params(orc, inp, d, H, KV, hd, ffn, eps, theta)
+    ck, cv = inp["cache_k"].copy(), inp["cache_v"].copy()
+    rng = np.random.default_rng(12)
+    for step in range(8):
+        x0 = (rng.standard_normal(d) * 2).astype(np.float32)
+        x = _f32(x0)
+        blk.accumulate(x, cache, 1)
+        torch.cuda.synchronize()
+        parts = {}
+        want = orc.block_decode(x0, ck, cv, past + step, p, parts)
+        # the oracle's cache continues from the GPU's rows, so each step is
+        # checked on the same state
+        keys = _np16(cache.keys()).reshape(-1, KV * hd)
+        ck[past + step] = keys[past + step]
+        cv[past + step] = _np16(cache.values()).reshape(-1, KV * hd)[past + step]
+        _check_step(x.cpu().numpy(), want, x0, parts, H * hd, ffn)
+
+
+def test_self_attention_accumulate(smg, orc):
+    """SelfAttention::accumulate (self_attention.rs:148-183) on its own: y +=
+    out(attention(qkv(x))) for an f16 row, appending the cache."""
+    import torch
+    d, H, KV, hd, past = 512, 8, 2, 64, 100
+    inp = WL.block_inputs(d, H, KV, hd, 64, past, seed=21)
+    W = lambda key: smg.Q4Weights(inp[key][0], inp[key][1], inp[key][2], inp[key][3])  # noqa: E731
+    attn = smg.SelfAttention(smg.Linear(W("qkv")), smg.Linear(W("out")), H, KV, hd, rope_theta=10000.0)
+    cache = attn.cache(past + 4)
+    cache.extend(_h16(inp["cache_k"][:past]), _h16(inp["cache_v"][:past]))
+    x16 = orc.f32_to_f16(np.random.default_rng(22).standard_normal(d).astype(np.float32))
+    y0 = np.full(d, 0.25, np.float32)
+    y = _f32(y0)
+    attn.accumulate(_h16(x16), cache, y, 1)
+    torch.cuda.synchronize()
+    # the oracle's attention half: the block step without norms or MLP
+    qkv = orc.matmul_q4_ep(x16, *inp["qkv"][:2], None, 1, inp["qkv"][2], d, 32)
+    ql, kl = H * hd, KV * hd
+    cs, sn = orc.rope_angles(orc.rope_inv_freq(hd, 10000.0), past)
+    q = orc.rope_apply(orc.f16_to_f32(qkv[:ql]), cs, sn)
+    k = orc.rope_apply(orc.f16_to_f32(qkv[ql:ql + kl]), cs, sn)
+    ck, cv = inp["cache_k"].copy(), inp["cache_v"].copy()
+    ck[past], cv[past] = orc.f32_to_f16(k), qkv[ql + kl:]
+    att = orc.attention_kv_f16(q, ck[:past + 1], cv[:past + 1], past + 1, H, KV, hd,
+                               np.float32(1) / np.sqrt(np.float32(hd)))
+    want = y0 + orc.f16_to_f32(orc.matmul_q4_ep(orc.f32_to_f16(att), *inp["out"][:2], None, 1, d, H * hd, 32))
+    assert _rel32(y.cpu().numpy(), want) <= f16_tol(H * hd)
+    assert cache.len() == past + 1
+
+
+def test_decode_parts_refuse_bad_calls(smg, orc):
+    import torch
+    d, H, KV, hd, ffn = 256, 4, 2, 64, 320
+    inp = WL.block_inputs(d, H, KV, hd, ffn, 2, seed=31)
+    blk = _gpu_block(smg, inp, d, H, KV, hd, 1e-5, 10000.0)
+    cache = blk.cache(2)
+    x = _f32(inp["x"])
+    blk.accumulate(x, cache, 1)
+    blk.accumulate(x, cache, 1)
+    torch.cuda.synchronize()
+    with pytest.raises(smg.SmeGemmError, match="KvCache full"):
+        blk.accumulate(x, cache, 1)
+    with pytest.raises(smg.SmeGemmError, match="one row"):
+        blk.accumulate(_f32(np.zeros(2 * d, np.float32)), blk.cache(8), 2)
+    with pytest.raises(smg.SmeGemmError, match="heads match"):
+        blk.accumulate(x, smg.KvCache(8, 2, 64, 8), 1)
+    # a part takes its layers over (the Rust constructors move them): the
+    # weights cannot be handed to a second part
+    up = smg.Linear(smg.Q4Weights(*inp["gate"][:2], ffn, d))
+    smg.Mlp.new(up, smg.Gate.Silu, smg.Linear(smg.Q4Weights(*inp["down"][:2], d, ffn)))
+    assert up.q4._h is None
+    with pytest.raises(smg.SmeGemmError, match="null weights"):
+        smg.Mlp.new(up, smg.Gate.Silu, smg.Linear(smg.Q4Weights(*inp["down"][:2], d, ffn)))

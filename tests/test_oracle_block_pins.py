@@ -1,19 +1,19 @@
 """Pins for the oracle's decode-block passes (config 5), each checked against
 something other than itself:
 
-- rms_norm (src/nn.rs:128-159): an f64 computation (the reference's own
+- rms_norm (src/nn.rs:127-161): an f64 computation (the reference's own
   norms_match_f64 data and bound, tests/correctness/model.rs:100-141, tightened
   to a few f32 ulps), closed forms (constant and zero rows), and planted
   mistakes (a dropped eps, a dim - 1 divisor) that the bound catches.
-- RoPE (examples/bonsai/model.rs:31-107): inverse frequencies against numpy's
+- RoPE (examples/bonsai/model.rs:30-99): inverse frequencies against numpy's
   f64 power, the position-0 identity bit for bit, norm preservation, the
   relative-position property <R(m)q, R(n)k> = <R(m+t)q, R(n+t)k>, and an f64
   rotation.
-- attention_kv_f16 (src/kernels/kv_attention.rs:286-325): the reference's
+- attention_kv_f16 (src/kernels/kv_attention.rs:282-325): the reference's
   kv_f16_matches_oracle test restated (same shapes, lengths, LCG data and f64
   oracle, tests/correctness/kv_attention.rs:7-82), len = 1 giving V's row bit
   for bit, equal keys giving the mean of V.
-- glu (src/linear.rs:803-826): an f64 silu / gelu within one f16 ulp, with a
+- glu (src/linear.rs:804-826): an f64 silu / gelu within one f16 ulp, with a
   ragged last chunk, and a planted gate/up swap that must differ.
 - the block step (src/block.rs:90-106 with bonsai's RoPE): an independent
   numpy f64 block (its own Q4 decoding, f64 products and softmax) on a small
@@ -263,10 +263,10 @@ def small_block(seed, d=256, heads=4, kv_heads=2, hd=64, ffn=320, past=37, theta
     p["qkv"] = O.Q4Lin(*raw["qkv"][0], nq, d)
     p["out"] = O.Q4Lin(*raw["out"][0], d, heads * hd)
     p["down"] = O.Q4Lin(*raw["down"][0], d, ffn)
-    # GatedLinear: gate and up interleaved 32 columns at a time (linear.rs:584-599)
+    # GatedLinear: gate and up interleaved 32 columns at a time (linear.rs:601-619)
     gq, gs = raw["gate"][0]
     uq, us = raw["up"][0]
-    p["gate_up"] = O.Q4Lin(*interleave_q4(gq, gs, uq, us, ffn, d), 2 * ffn, d)
+    p["gate_up"] = O.Q4Lin(*O.q4_interleave32(gq, gs, uq, us, ffn, d), 2 * ffn, d)
     cap = past + 4
     ld = kv_heads * hd
     cache_k = np.zeros((cap, ld), np.uint16)
@@ -275,19 +275,6 @@ def small_block(seed, d=256, heads=4, kv_heads=2, hd=64, ffn=320, past=37, theta
     cache_v[:past] = O.f32_to_f16(rng.standard_normal(past * ld).astype(np.float32)).reshape(past, ld)
     x = rng.standard_normal(d).astype(np.float32)
     return p, x, cache_k, cache_v
-
-
-def interleave_q4(gq, gs, uq, us, n, k, block=32):
-    """The Q4 arrays of gate | up interleaved 32 columns at a time: the codes
-    and scales move with their columns (a column's weights are unchanged)."""
-    idx = np.arange(k * n)
-    def nibs(q):
-        return np.where(idx % 2 == 0, q[idx // 2] & 15, q[idx // 2] >> 4).astype(np.uint8).reshape(k, n)
-    both = O.interleave32(nibs(gq), nibs(uq), n, k).ravel()
-    quants = (both[0::2] | (np.append(both[1::2], 0)[:both[0::2].size] << 4)).astype(np.uint8)
-    nbk = k // block
-    sc = O.interleave32(gs.reshape(n, nbk).T, us.reshape(n, nbk).T, n, nbk).T.ravel()
-    return quants, np.ascontiguousarray(sc)
 
 
 def _block64(p, x, cache_k, cache_v, pos):
@@ -355,7 +342,7 @@ def test_interleaved_q4_is_gate_and_up_side_by_side():
     uq = rng.integers(0, 256, k * n // 2, dtype=np.uint8)
     gs = O.f32_to_f16(rng.uniform(0.1, 1, n * 2).astype(np.float32))
     us = O.f32_to_f16(rng.uniform(0.1, 1, n * 2).astype(np.float32))
-    q, s = interleave_q4(gq, gs, uq, us, n, k)
+    q, s = O.q4_interleave32(gq, gs, uq, us, n, k)
     both = _q4_decode64(q, s, 2 * n, k)
     G, U = _q4_decode64(gq, gs, n, k), _q4_decode64(uq, us, n, k)
     assert np.array_equal(both, O.interleave32(G, U, n, k))
