@@ -1,29 +1,38 @@
 """Benchmark of the quantized-weight matmul path on one MI355X.
 
-Headline (the JSON line's `value`): config 1 -- Q4 GEMV, m=1,
-K=N=4096, block 32 -- as whole-job HBM throughput in GB/s. A "step" is one
-GEMV call on its own copy of the weights: 64 device copies (605 MB) rotate so
-every call streams its weights from HBM, not from the 256 MB MALL. The K timed
-steps replay as one HIP graph on torch's current stream (launch-bound loop),
-bracketed by torch.cuda.synchronize().
+Headline (the JSON line's `value`): config 1 -- Q4 GEMV, m=1, K=N=4096,
+block 32 -- as whole-job HBM throughput in GB/s. A "step" is one GEMV call on
+its own copy of the weights: 64 device copies (605 MB) rotate, and the MALL
+(256 MB) is flushed with a 512 MB write before each timed replay, so every
+timed call streams its weights from HBM -- also when --steps is below the
+number of copies. The K timed steps are one HIP graph replayed on torch's
+current stream, bracketed by torch.cuda.synchronize(); the time per call is
+HIP events around the replay on that stream, so it includes the graph's
+inter-kernel gap (reported as `graph_gap_us`, from a graph of 1-element fills).
 
 `roofline` covers the dominant kernel (the Q4 GEMV): achieved = algorithmic
-bytes per call / average kernel duration, the duration measured with HIP
-events around the K graph-replayed calls on the stream they run on (so it
-includes the graph's inter-kernel gap, reported as `graph_gap_us` from a
-graph of near-empty kernels). `traffic` is the HBM bytes per launch read from
-the committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary in profiles/ (null if
-absent). `extra` reports configs 2-4 the same way (config 4 against the f16
-MFMA peak) plus a diagnostic per-launch event time (one event pair per eager
-launch, which adds the event overhead). `cpu_baseline` times the C restatement
-of the reference's portable path (oracle/) single-threaded on this host for a
-bounded sample of config-1 calls.
+bytes per call / time per call. `traffic` is the HBM bytes per launch from
+the committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary in profiles/.
+
+`extra` holds, timed the same way:
+  - configs 2-4 (config 4 against the f16 MFMA peak, with the shader clock
+    measured right after its GEMMs and torch's dense f16 GEMM of the same shape
+    as a same-box floor);
+  - config 5, the Llama-style decode block (src/block.rs path) in tokens/s
+    and its fraction of 139.5 MB/token at 8 TB/s, over 4 block copies (558 MB,
+    a 4-layer model's worth) so each step's weights come from HBM;
+  - `floors`: a plain streaming read of each config's bytes over the same
+    rotation (the time a single launch reading that much needs on this box).
+`cpu_baseline` is the C restatement of the reference's portable path (oracle/)
+on this host: config 1 single-threaded (faithful mode, a bounded sample) and
+over `cores` threads (threaded mode, bit-identical); `extra.cpu` the other
+configs' samples.
 
 --calib-copy first runs 16 device copies of 64 MiB (a kernel of known traffic)
 so that a rocprofv3 --pmc run of this script can scale its counters.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
-                       [--calib-copy]
+                       [--only CONFIGS] [--calib-copy]
 """
 from __future__ import annotations
 
@@ -39,12 +48,7 @@ sys.path.insert(0, os.path.join(ROOT, "sme-gemm_amd"))
 HBM_PEAK_GBS = 8000.0
 F16_MFMA_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 << 20
-
-
-def _events(torch, n):
-    return [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for _ in range(n)]
-
+FLUSH_BYTES = 512 << 20
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemv_mfma_config1_traffic.md")
 
@@ -61,44 +65,87 @@ def committed_traffic():
     return None
 
 
-def time_calls(torch, calls, reps: int, warmup: int):
-    """Graph-replayed time per call (us; events around the whole replay on the
-    stream it runs on) and a diagnostic per-launch time (an event pair around
-    each eager launch). `calls` is a list of zero-arg callables launching one
-    call each."""
-    s = torch.cuda.current_stream()
-    for i in range(warmup):
-        calls[i % len(calls)]()
-    torch.cuda.synchronize()
-    # per-launch durations
-    ev = _events(torch, reps)
-    for i in range(reps):
-        ev[i][0].record(s)
-        calls[i % len(calls)]()
-        ev[i][1].record(s)
-    torch.cuda.synchronize()
-    durs = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
-    per_launch = sum(durs) / len(durs)
-    # whole job: K calls captured once into a graph, replayed
-    g = torch.cuda.CUDAGraph()
-    side = torch.cuda.Stream()
-    side.wait_stream(s)
-    with torch.cuda.stream(side):
-        with torch.cuda.graph(g, stream=side):
-            for i in range(reps):
+class Timer:
+    """Graph-replayed timing: `steps` calls (cycling over `calls`) captured
+    once, warmed, then -- after a MALL flush -- replayed once between events on
+    the replaying stream. Returns microseconds per call."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.flush_buf = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
+
+    def flush(self):
+        self.flush_buf.zero_()
+
+    def __call__(self, calls, steps: int, warmup: int, flush: bool = True):
+        torch = self.torch
+        s = torch.cuda.current_stream()
+        side = torch.cuda.Stream()
+        side.wait_stream(s)
+        with torch.cuda.stream(side):
+            for i in range(max(warmup, len(calls))):  # every call once: scratch sized before capture
                 calls[i % len(calls)]()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                for i in range(steps):
+                    calls[i % len(calls)]()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        if flush:
+            self.flush()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(s)
+        g.replay()
+        t1.record(s)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) * 1e3 / steps
+
+
+def rotate(w, per_copy_bytes):
+    """Enough device copies of a weight set that one pass over them reads
+    more than twice the MALL."""
+    copies = max(1, -(-(2 * MALL_BYTES + 64 * 2**20) // per_copy_bytes))
+    return [w] + [w.clone() for _ in range(copies - 1)]
+
+
+def stream_floor(smg, torch, timer, nbytes, steps, warmup):
+    """A plain read of `nbytes` per call over a rotation past the MALL."""
+    per = (nbytes + 4095) // 4096 * 4096
+    copies = max(1, -(-(2 * MALL_BYTES + 64 * 2**20) // per))
+    buf = torch.zeros(per * copies // 4, dtype=torch.int32, device="cuda")
+    base = buf.data_ptr()
+    L = smg.lib()
+    calls = [(lambda i=i: L.smg_stream_read_dev(base + i * per, nbytes // 16 * 16,
+                                                torch.cuda.current_stream().cuda_stream))
+             for i in range(copies)]
+    us = timer(calls, steps, warmup)
+    del buf
+    return {"bytes": nbytes, "us": us, "GBps": nbytes / (us * 1e-6) / 1e9}
+
+
+def shader_clock_mhz(smg, torch):
+    """Shader clock from one wave's clock64 against the 100 MHz wall clock."""
+    import ctypes as C
+    out = torch.zeros(3, dtype=torch.int64, device="cuda")
+    smg.lib().smg_clock_probe_dev(C.c_void_p(out.data_ptr()), 1 << 18, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
-    g.replay()  # warm replay
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record(s)
-    g.replay()
-    t1.record(s)
-    torch.cuda.synchronize()
-    whole = t0.elapsed_time(t1) * 1e3 / reps
-    return {"us_kernel_avg": whole, "us_event_per_launch_avg": per_launch,
-            "us_event_per_launch_min": durs[0], "us_event_per_launch_median": durs[len(durs) // 2]}
+    ticks, wall = out[0].item(), out[1].item()
+    return ticks / wall * 100.0 if wall > 0 else None
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def main():
@@ -108,14 +155,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="config 1 only")
+    ap.add_argument("--only", default="12345", help="configs to run beside config 1 (digits)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="16 x 64 MiB device copies first (PMC counter scale)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the calls are independent per weight matrix; sharding N across GPUs "
-              "is left to the caller); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the calls are "
+              "independent per weight matrix; sharding N across GPUs is left to the caller); "
+              "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    only = "" if args.quick else args.only
 
     import numpy as np
     import torch
@@ -127,7 +176,9 @@ def main():
         raise SystemExit("libsmegemm_gpu.so not loadable or no gfx950 device")
     torch.cuda.init()
     dev = torch.device("cuda:0")
-    to_dev = lambda x: torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).to(dev)  # noqa
+    to_dev = lambda x: torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).to(dev)  # noqa: E731
+    timer = Timer(torch)
+    steps, warm = args.steps, args.warmup
 
     if args.calib_copy:
         src = torch.ones(32 << 20, dtype=torch.int16, device=dev)
@@ -137,13 +188,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    # inter-kernel gap of a replayed graph: near-empty kernels (1-element fill)
     tiny = torch.empty(1, dtype=torch.int16, device=dev)
-    gap = time_calls(torch, [lambda: tiny.fill_(1)], args.steps, 8)["us_kernel_avg"]
-
-    def rotate(w, per_copy_bytes):
-        copies = max(1, -(-(2 * MALL_BYTES + 64 * 2**20) // per_copy_bytes))
-        return [w] + [w.clone() for _ in range(copies - 1)]
+    gap = timer([lambda: tiny.fill_(1)], steps, 8, flush=False)
 
     # ---- config 1: Q4 GEMV m=1, K=N=4096 ----
     m, n, k = 1, 4096, 4096
@@ -154,18 +200,18 @@ def main():
     ad = to_dev(a)
     cs = [torch.empty(m * n, dtype=torch.int16, device=dev) for _ in range(4)]
     calls = [(lambda w=w, c=cs[i % 4]: smg.matmul_q4(ad, w, c, m)) for i, w in enumerate(ws)]
-    cold = time_calls(torch, calls, args.steps, args.warmup)
-    hot = time_calls(torch, calls[:1], args.steps, args.warmup)
-    t_kernel = cold["us_kernel_avg"]
-    achieved = bytes1 / (t_kernel * 1e-6) / 1e9
-    value = bytes1 / (cold["us_kernel_avg"] * 1e-6) / 1e9
-
+    us1 = timer(calls, steps, warm)
+    us1_hot = timer(calls[:1], steps, warm, flush=False)
+    achieved = bytes1 / (us1 * 1e-6) / 1e9
+    floors = {"config1": stream_floor(smg, torch, timer, bytes1, steps, warm)}
     extra = {"config1_q4_gemv": {
-        "bytes": bytes1, "weight_copies": len(ws), "cold": cold, "hot_mall": hot,
-        "GBps_cold_kernel": achieved, "GBps_hot_kernel": bytes1 / (hot["us_kernel_avg"] * 1e-6) / 1e9,
-        "frac_hbm_cold_kernel": achieved / HBM_PEAK_GBS}}
+        "bytes": bytes1, "weight_copies": len(ws), "us_cold": us1, "us_hot_mall": us1_hot,
+        "GBps_cold": achieved, "GBps_hot": bytes1 / (us1_hot * 1e-6) / 1e9,
+        "frac_hbm_cold": achieved / HBM_PEAK_GBS,
+        "vs_stream_floor": us1 / floors["config1"]["us"]}}
+    del ws, calls
 
-    if not args.quick:
+    if "2" in only:
         # ---- config 2: Q2 ternary, m=1 and m=8, K=4096, N=11008, block 128 ----
         for m2 in (1, 8):
             n2, k2 = 11008, 4096
@@ -176,13 +222,14 @@ def main():
             a2d = to_dev(a2)
             c2 = torch.empty(m2 * n2, dtype=torch.int16, device=dev)
             calls2 = [(lambda w=w: smg.matmul_q2(a2d, w, c2, m2)) for w in ws2]
-            r = time_calls(torch, calls2, 256, 32)
-            rh = time_calls(torch, calls2[:1], 256, 32)
+            us = timer(calls2, steps, warm)
+            ush = timer(calls2[:1], steps, warm, flush=False)
             extra[f"config2_q2_m{m2}"] = {
-                "bytes": b2, "cold": r, "hot_mall": rh,
-                "GBps_cold_kernel": b2 / (r["us_kernel_avg"] * 1e-6) / 1e9,
-                "frac_hbm_cold_kernel": b2 / (r["us_kernel_avg"] * 1e-6) / 1e9 / HBM_PEAK_GBS}
-            del ws2
+                "bytes": b2, "us_cold": us, "us_hot_mall": ush, "GBps_cold": b2 / (us * 1e-6) / 1e9,
+                "frac_hbm_cold": b2 / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+            del ws2, calls2
+        floors["config2_m1"] = stream_floor(smg, torch, timer, workloads.q2_bytes(1, 11008, 4096), steps, warm)
+    if "3" in only:
         # ---- config 3: Q1 + add_col + silu, m=1, K=4096, N=14336 ----
         n3, k3 = 14336, 4096
         a3, signs, sc3, bias = workloads.q1_inputs(1, n3, k3, seed=0)
@@ -193,13 +240,14 @@ def main():
         c3 = torch.empty(n3, dtype=torch.int16, device=dev)
         ep3 = smg.Epilogue().add_col(biasd).silu()
         calls3 = [(lambda w=w: smg.matmul_q1_ep(a3d, w, c3, 1, ep3)) for w in ws3]
-        r = time_calls(torch, calls3, 256, 32)
-        rh = time_calls(torch, calls3[:1], 256, 32)
+        us = timer(calls3, steps, warm)
+        ush = timer(calls3[:1], steps, warm, flush=False)
         extra["config3_q1_ep"] = {
-            "bytes": b3, "cold": r, "hot_mall": rh,
-            "GBps_cold_kernel": b3 / (r["us_kernel_avg"] * 1e-6) / 1e9,
-            "frac_hbm_cold_kernel": b3 / (r["us_kernel_avg"] * 1e-6) / 1e9 / HBM_PEAK_GBS}
-        del ws3
+            "bytes": b3, "us_cold": us, "us_hot_mall": ush, "GBps_cold": b3 / (us * 1e-6) / 1e9,
+            "frac_hbm_cold": b3 / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+        floors["config3"] = stream_floor(smg, torch, timer, b3, steps, warm)
+        del ws3, calls3
+    if "4" in only:
         # ---- config 4: Q4 GEMM m=512, K=4096, N=14336 + mul_col/add_col/silu ----
         m4, n4, k4 = 512, 14336, 4096
         a4, q4q, q4s, _ = workloads.q4_inputs(m4, n4, k4, seed=0)
@@ -209,43 +257,46 @@ def main():
         c4 = torch.empty(m4 * n4, dtype=torch.int16, device=dev)
         ep4 = smg.Epilogue().mul_col(s4d).add_col(b4d).silu()
         calls4 = [lambda: smg.matmul_q4_ep(a4d, w4, c4, m4, ep4)]
-        r = time_calls(torch, calls4, 20, 3)
+        st4 = max(8, min(steps, 40))
+        us = timer(calls4, st4, 3, flush=False)
+        mhz = shader_clock_mhz(smg, torch)  # right after the GEMMs
         flops = 2.0 * m4 * n4 * k4
-        tf = flops / (r["us_kernel_avg"] * 1e-6) / 1e12
-        extra["config4_q4_gemm"] = {"flops": flops, "timing": r, "TFLOPS_kernel": tf,
-                                    "frac_f16_mfma": tf / F16_MFMA_PEAK_TFLOPS}
+        tf = flops / (us * 1e-6) / 1e12
+        # torch's dense f16 GEMM (hipBLASLt) of the same shape: a same-box floor
+        ta = torch.randn(m4, k4, dtype=torch.float16, device=dev)
+        tb = torch.randn(k4, n4, dtype=torch.float16, device=dev)
+        tc = torch.empty(m4, n4, dtype=torch.float16, device=dev)
+        us_t = timer([lambda: torch.matmul(ta, tb, out=tc)], st4, 3, flush=False)
+        props = torch.cuda.get_device_properties(0)
+        extra["config4_q4_gemm"] = {
+            "flops": flops, "us": us, "TFLOPS": tf, "frac_f16_mfma": tf / F16_MFMA_PEAK_TFLOPS,
+            "shader_clock_mhz_after": mhz,
+            "shader_clock_mhz_max": getattr(props, "clock_rate", 0) / 1000.0 or None,
+            "torch_dense_f16_gemm": {"us": us_t, "TFLOPS": flops / (us_t * 1e-6) / 1e12}}
+        del ta, tb, tc
+    if "5" in only:
+        extra["config5_decode_block"] = bench_block(smg, torch, timer, workloads, steps, warm, to_dev)
 
+    extra["floors"] = floors
     cpu = None
     if not args.no_cpu:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import oracle
-        oracle.lib()
-        t0 = time.perf_counter()
-        calls_done = 0
-        while calls_done < 3 or time.perf_counter() - t0 < 10.0:
-            oracle.matmul_q4_ep(a, quants, scales, None, 1, 4096, 4096, 32)
-            calls_done += 1
-        dt = (time.perf_counter() - t0) / calls_done
-        cpu = {"value": bytes1 / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"{calls_done} config-1 calls (m=1, K=N=4096) of the portable path "
-                         f"restated in C (per-call Q4 dequant + f32 GEMM), "
-                         f"{dt * 1e3:.1f} ms/call, single thread"}
+        cpu, extra["cpu"] = cpu_baselines(np, workloads, a, quants, scales, bytes1, only)
 
     line = {
         "metric": "Q4 GEMV HBM GB/s at K=N=4096 (config 1, m=1)",
-        "value": value,
+        "value": achieved,
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": cold["us_kernel_avg"] / 1e3,
+        "steps": steps,
+        "warmup": warm,
+        "ms_per_step": us1 / 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (seeded; config 1 distributions)",
-        "config": {"workload": "q4_gemv m=1 K=4096 N=4096 block=32, 64 rotating weight copies",
-                   "m": 1, "k": 4096, "n": 4096, "block": 32},
+        "config": {"workload": "q4_gemv m=1 K=4096 N=4096 block=32, 64 rotating weight copies, MALL "
+                               "flushed before the timed replay", "m": 1, "k": 4096, "n": 4096, "block": 32},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": committed_traffic()},
         "cpu_baseline": cpu,
@@ -253,6 +304,115 @@ def main():
         "graph_gap_us": gap,
     }
     print(json.dumps(line))
+
+
+def bench_block(smg, torch, timer, workloads, steps, warm, to_dev):
+    """Config 5: one decode step of a Llama-style block (d 4096, 32 / 8 heads
+    of 128, SwiGLU 14336, 4096 cached positions, RoPE 10000) per call, cycling
+    over 4 block copies (each with its own cache) so each step streams its
+    139.5 MB from HBM; every captured step appends at position 4096 and the
+    replays repeat it."""
+    import numpy as np
+    c = workloads.CONFIG5
+    d, H, KV, hd, ffn, past = c["d"], c["heads"], c["kv_heads"], c["head_dim"], c["ffn"], c["past"]
+    copies = 4
+    blocks, caches, xs = [], [], []
+    for i in range(copies):
+        inp = workloads.block_inputs(d, H, KV, hd, ffn, past, seed=100 + i)
+        W = lambda key: smg.Q4Weights(inp[key][0], inp[key][1], inp[key][2], inp[key][3])  # noqa: E731
+        attn = smg.SelfAttention(smg.Linear(W("qkv")), smg.Linear(W("out")), H, KV, hd, rope_theta=c["theta"])
+        mlp = smg.Mlp.gated(smg.GatedLinear.from_q4(W("gate"), W("up"), smg.Gate.Silu), smg.Linear(W("down")))
+        blk = smg.Block(smg.Norm.rms(inp["norm1"], c["eps"]), attn, smg.Norm.rms(inp["norm2"], c["eps"]), mlp)
+        cache = blk.cache(past + 2 * max(warm, copies) + steps + 8)
+        cache.extend(to_dev(inp["cache_k"][:past]), to_dev(inp["cache_v"][:past]))
+        blocks.append(blk)
+        caches.append(cache)
+        xs.append(torch.from_numpy(inp["x"]).cuda())
+        del inp
+    torch.cuda.synchronize()
+
+    def step(i):
+        caches[i].truncate(past)  # every captured step appends at position `past`
+        blocks[i].accumulate(xs[i], caches[i], 1)
+    calls = [(lambda i=i: step(i)) for i in range(copies)]
+    st5 = max(copies, min(steps, 64)) // copies * copies
+    us = timer(calls, st5, max(warm, copies) // copies * copies)
+    us_hot = timer(calls[:1], st5, copies, flush=False)
+    nbytes = workloads.block_bytes(d, H, KV, hd, ffn, past + 1)
+    tok_s = 1e6 / us
+    return {"workload": "Block::accumulate, 1 row, d=4096, 32/8 heads x 128, SwiGLU 14336, "
+                        "4096 cached positions, RoPE theta 10000, Q4 block 32; 4 block copies",
+            "bytes_per_token": nbytes, "us_per_token": us, "tokens_per_s": tok_s,
+            "us_per_token_hot_mall": us_hot, "GBps": nbytes / (us * 1e-6) / 1e9,
+            "roofline_tokens_per_s": HBM_PEAK_GBS * 1e9 / nbytes,
+            "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "launches_per_token": 6}
+
+
+def cpu_baselines(np, workloads, a, quants, scales, bytes1, only):
+    """The oracle (the reference's portable path restated in C) on this host's
+    cores, on bounded samples of each config."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    oracle.lib()
+    threads = max(1, min(16, os.cpu_count() or 1))
+    model = cpu_model()
+
+    def timed(fn, budget_s, min_calls=1):
+        t0 = time.perf_counter()
+        calls = 0
+        while calls < min_calls or time.perf_counter() - t0 < budget_s:
+            fn()
+            calls += 1
+        return (time.perf_counter() - t0) / calls, calls
+
+    dt1, n1 = timed(lambda: oracle.matmul_q4_ep(a, quants, scales, None, 1, 4096, 4096, 32), 10.0, 3)
+    dtt, nt = timed(lambda: oracle.matmul_mt(4, a, quants, scales, 1, 4096, 4096, 32, threads), 3.0, 3)
+    cpu = {"value": bytes1 / dt1 / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+           "sample": f"{n1} config-1 calls (m=1, K=N=4096) of the portable path restated in C "
+                     f"(per-call Q4 dequant + f32 GEMM), {dt1 * 1e3:.1f} ms/call, single thread",
+           "threaded": {"value": bytes1 / dtt / 1e9, "unit": "GB/s", "cores": threads,
+                        "ms_per_call": dtt * 1e3, "calls": nt},
+           "cpu_model": model, "host_cpus": os.cpu_count()}
+    extra = {}
+    if "2" in only:
+        a2, codes, sc2 = workloads.q2_inputs(1, 11008, 4096, seed=0)
+        d1, c1 = timed(lambda: oracle.matmul_lowbit_ep(2, a2, codes, sc2, 1, 11008, 4096, 128), 3.0, 1)
+        dmt, cmt = timed(lambda: oracle.matmul_mt(2, a2, codes, sc2, 1, 11008, 4096, 128, threads), 2.0, 2)
+        b = workloads.q2_bytes(1, 11008, 4096)
+        extra["config2_q2_m1"] = {"single_GBps": b / d1 / 1e9, "single_ms": d1 * 1e3,
+                                  "threaded_GBps": b / dmt / 1e9, "threaded_ms": dmt * 1e3, "cores": threads}
+    if "3" in only:
+        a3, signs, sc3, bias = workloads.q1_inputs(1, 14336, 4096, seed=0)
+        d1, _ = timed(lambda: oracle.matmul_lowbit_ep(1, a3, signs, sc3, 1, 14336, 4096, 128,
+                                                      [(4, 0, 0.0, bias, 0)], 3), 3.0, 1)
+        b = workloads.q1_bytes(1, 14336, 4096)
+        extra["config3_q1_ep"] = {"single_GBps": b / d1 / 1e9, "single_ms": d1 * 1e3}
+    if "4" in only:
+        # a 16-row slice of config 4 (m=512), threaded; TFLOPS scale with the rows
+        mrows = 16
+        a4, q4q, q4s, _ = workloads.q4_inputs(mrows, 14336, 4096, seed=0)
+        dmt, _ = timed(lambda: oracle.matmul_mt(4, a4, q4q, q4s, mrows, 14336, 4096, 32, threads), 4.0, 1)
+        extra["config4_q4_gemm"] = {"sample": f"rows 0..{mrows} of config 4 (the per-call dequant of all "
+                                              f"14336 x 4096 weights included), threaded",
+                                    "TFLOPS": 2.0 * mrows * 14336 * 4096 / dmt / 1e12, "s_per_call": dmt,
+                                    "cores": threads}
+    if "5" in only:
+        c = workloads.CONFIG5
+        d, H, KV, hd, ffn, past = c["d"], c["heads"], c["kv_heads"], c["head_dim"], c["ffn"], c["past"]
+        inp = workloads.block_inputs(d, H, KV, hd, ffn, past, seed=100)
+        p = dict(d=d, heads=H, kv_heads=KV, head_dim=hd, ffn=ffn, eps=c["eps"], theta=c["theta"],
+                 norm1=inp["norm1"], norm2=inp["norm2"])
+        for key in ("qkv", "out", "down"):
+            p[key] = oracle.Q4Lin(*inp[key])
+        p["gate_up"] = oracle.Q4Lin(*oracle.q4_interleave32(*inp["gate"][:2], *inp["up"][:2], ffn, d),
+                                    2 * ffn, d)
+        t0 = time.perf_counter()
+        oracle.block_decode(inp["x"], inp["cache_k"], inp["cache_v"], past, p)
+        dt = time.perf_counter() - t0
+        extra["config5_decode_block"] = {"sample": "one Block::accumulate step of the portable path "
+                                                   "restated in C (single thread)",
+                                         "tokens_per_s": 1.0 / dt, "s_per_token": dt}
+    return cpu, extra
 
 
 if __name__ == "__main__":

@@ -369,6 +369,16 @@ void smg_block_destroy(smg_block *b);
  * glu, down + residual. */
 int smg_block_accumulate_dev(smg_block *b, float *x, smg_kv_cache *cache, size_t rows, void *stream);
 
+/* ---- measurement probes (not part of the matmul path) ----------------------- */
+/* One plain pass of 16-byte loads over `bytes` (a multiple of 16) of device
+ * memory, writing nothing: the time floor that a single launch reading that
+ * many bytes meets on this device. */
+int smg_stream_read_dev(const void *p, size_t bytes, void *stream);
+/* Spins one wave `iters` times and stores out[0] = shader-clock ticks
+ * (clock64) and out[1] = 100 MHz wall-clock ticks over the spin (device
+ * memory, 3 words): out[0] / out[1] * 100 MHz is the shader clock then. */
+int smg_clock_probe_dev(unsigned long long *out, unsigned iters, void *stream);
+
 /* ---- runtime --------------------------------------------------------------- */
 /* 1 when a gfx950 device is present and this library's kernels load on it. */
 int smg_available(void);

@@ -22,10 +22,14 @@
  *   - lowbit quantize_row/reference: numpy restatement on small shapes, the
  *     f64 activation-rounding bound of tests/correctness/q2.rs:39-77, grid
  *     recovery (q2.rs:228, q1.rs:279), and independence from m.
+ *   - the decode block's passes: see tests/test_oracle_block_pins.py.
+ *   - the threaded CPU baseline: bit for bit the single-threaded functions.
  */
 #include <math.h>
+#include <pthread.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* ------------------------------------------------------------------------ */
@@ -824,4 +828,86 @@ void or_glu_f16(uint16_t *y, const uint16_t *both, size_t m, size_t n, int gelu)
                 y[r * n + c0 + j] = or_f32_to_f16(a * u);
             }
         }
+}
+
+/* ------------------------------------------------------------------------ */
+/* The CPU baseline's threaded mode: the portable path's per-output          */
+/* arithmetic split over column ranges on host threads (each output depends  */
+/* on its own column only, so the bits are the single-threaded ones).       */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+    int kind; /* 4 = Q4 (dequant + f16 GEMM), 2 / 1 = low-bit int8 reference */
+    const uint16_t *a;
+    const uint8_t *codes;
+    const uint16_t *scales;
+    const int8_t *codebook;
+    size_t m, n, k, block, j0, j1;
+    uint16_t *c;
+    int ok;
+} OrColJob;
+
+static void *or_col_job(void *arg) {
+    OrColJob *jb = (OrColJob *)arg;
+    const size_t w = jb->j1 - jb->j0, k = jb->k, n = jb->n;
+    jb->ok = 0;
+    if (w == 0) { jb->ok = 1; return NULL; }
+    if (jb->kind == 4) {
+        /* q4_f16_impl (q4/matmul.rs:91-102): these columns dequantized to a
+         * k x w row-major panel (the same per-weight rounding), then the
+         * reference GEMM over them */
+        const size_t nbk = (k + jb->block - 1) / jb->block;
+        uint16_t *b = malloc(k * w * 2);
+        uint16_t *cc = malloc(jb->m * w * 2);
+        float *acc = malloc(w * 4);
+        if (!b || !cc || !acc) { free(b); free(cc); free(acc); return NULL; }
+        for (size_t d = 0; d < k; d++)
+            for (size_t j = jb->j0; j < jb->j1; j++) {
+                const double v = (double)or_f16_to_f32(jb->scales[j * nbk + d / jb->block]) *
+                                 (double)q4_code(jb->codes, d * n + j);
+                b[d * w + (j - jb->j0)] = or_f64_to_f16(v);
+            }
+        gemm16(0, jb->m, w, k, cc, jb->a, b, 0x3C00, 0, acc);
+        for (size_t i = 0; i < jb->m; i++) memcpy(jb->c + i * n + jb->j0, cc + i * w, w * 2);
+        free(b);
+        free(cc);
+        free(acc);
+    } else {
+        int8_t *q = malloc(k ? k : 1);
+        float *s = malloc(((k + jb->block - 1) / jb->block + 1) * 4);
+        if (!q || !s) { free(q); free(s); return NULL; }
+        or_lowbit_reference_cols(jb->kind, jb->a, jb->codes, jb->scales, jb->codebook, 0, jb->m, n, k,
+                                 jb->block, jb->c, jb->j0, jb->j1, q, s);
+        free(q);
+        free(s);
+    }
+    jb->ok = 1;
+    return NULL;
+}
+
+/* kind 4: matmul_q4 (scale form, row-major public arrays); kind 2 / 1:
+ * matmul_q2 / matmul_q1 (Q1 OutIn) without an epilogue. 0 on success. */
+int or_matmul_mt(int kind, const uint16_t *a, const uint8_t *codes, const uint16_t *scales,
+                 const int8_t *codebook, size_t m, size_t n, size_t k, size_t block, uint16_t *c,
+                 int threads) {
+    if (threads < 1) threads = 1;
+    if ((size_t)threads > n) threads = (int)(n ? n : 1);
+    OrColJob *jobs = calloc((size_t)threads, sizeof(OrColJob));
+    pthread_t *tid = calloc((size_t)threads, sizeof(pthread_t));
+    if (!jobs || !tid) { free(jobs); free(tid); return -1; }
+    for (int t = 0; t < threads; t++) {
+        OrColJob jb = {kind, a, codes, scales, codebook, m, n, k, block, n * (size_t)t / (size_t)threads,
+                       n * (size_t)(t + 1) / (size_t)threads, c, 0};
+        jobs[t] = jb;
+    }
+    int rc = 0;
+    for (int t = 1; t < threads; t++)
+        if (pthread_create(&tid[t], NULL, or_col_job, &jobs[t]) != 0) rc = -1;
+    or_col_job(&jobs[0]);
+    for (int t = 1; t < threads; t++)
+        if (rc == 0) pthread_join(tid[t], NULL);
+    for (int t = 0; t < threads; t++)
+        if (!jobs[t].ok) rc = -1;
+    free(jobs);
+    free(tid);
+    return rc;
 }

@@ -82,6 +82,8 @@ def lib() -> C.CDLL:
         L.or_rope_apply.argtypes = [P, SZ, P, P, SZ]
         L.or_attention_kv_f16.argtypes = [P, P, P, SZ, SZ, SZ, SZ, C.c_float, P, P, P]
         L.or_glu_f16.argtypes = [P, P, SZ, SZ, C.c_int]
+        L.or_matmul_mt.argtypes = [C.c_int, P, P, P, P, SZ, SZ, SZ, SZ, P, C.c_int]
+        L.or_matmul_mt.restype = C.c_int
     return _lib
 
 
@@ -531,3 +533,17 @@ def q4_interleave32(gq, gs, uq, us, n, k, block=32):
         quants = (lo | (hi << 4)).astype(np.uint8)
     sc = interleave32(np.asarray(gs).reshape(n, nbk).T, np.asarray(us).reshape(n, nbk).T, n, nbk).T.ravel()
     return quants, np.ascontiguousarray(sc)
+
+
+def matmul_mt(kind, a, codes, scales, m, n, k, block, threads, codebook=(-1, 0, 1, 0)):
+    """The CPU baseline's threaded mode: matmul_q4 (kind 4) or matmul_q2 / q1
+    (kind 2 / 1, Q1 OutIn), no epilogue, split over column ranges on `threads`
+    host threads; the bits of the single-threaded path."""
+    a = _c(a, np.uint16)
+    codes = _c(codes, np.uint8)
+    scales = _c(scales, np.uint16)
+    cb = np.asarray(codebook, np.int8)
+    c = np.empty(m * n, np.uint16)
+    if lib().or_matmul_mt(kind, _p(a), _p(codes), _p(scales), _p(cb), m, n, k, block, _p(c), threads) != 0:
+        raise MemoryError("or_matmul_mt: a thread's buffers could not be allocated")
+    return c

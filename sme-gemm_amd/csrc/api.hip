@@ -1547,4 +1547,18 @@ int smg_block_accumulate_dev(smg_block *b, float *x, smg_kv_cache *cache, size_t
     return mlp_step(b->mlp, nullptr, x, b->norm2, b->eps2, x, 1, stream);
 }
 
+// ---- measurement probes --------------------------------------------------------
+
+int smg_stream_read_dev(const void *p, size_t bytes, void *stream) {
+    if (!p || bytes % 16) return fail(SMG_EINVAL, "smg_stream_read_dev: a device pointer and a multiple of 16 bytes");
+    hipError_t e = launch_stream_read(p, bytes, nullptr, (hipStream_t)stream);
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_stream_read_dev", e);
+}
+
+int smg_clock_probe_dev(unsigned long long *out, unsigned iters, void *stream) {
+    if (!out) return fail(SMG_EINVAL, "null output");
+    hipError_t e = launch_clock_probe(out, iters, (hipStream_t)stream);
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_clock_probe_dev", e);
+}
+
 }  // extern "C"

@@ -127,6 +127,10 @@ hipError_t launch_glu(const uint16_t *both, size_t m, size_t n, uint32_t act, in
 // y[i] += f32(h[i]) over count values (convert::add_f16).
 hipError_t launch_add_f16(const uint16_t *h, size_t count, float *y, hipStream_t s);
 
+// Measurement probes (probes.hip).
+hipError_t launch_stream_read(const void *p, size_t bytes, unsigned *sink, hipStream_t s);
+hipError_t launch_clock_probe(unsigned long long *out, unsigned iters, hipStream_t s);
+
 // Sets the calling thread's smg_last_error() text and returns code.
 int report(int code, const char *what);
 

@@ -124,6 +124,8 @@ def lib() -> C.CDLL:
     L.smg_block_destroy.argtypes = [P]
     L.smg_block_destroy.restype = None
     L.smg_block_accumulate_dev.argtypes = [P, P, P, SZ, P]
+    L.smg_stream_read_dev.argtypes = [P, SZ, P]
+    L.smg_clock_probe_dev.argtypes = [P, C.c_uint, P]
     _lib = L
     return L
 

@@ -585,3 +585,27 @@ def test_lcg_generators_match_reference_formula():
     s = (1 * 6364136223846793005 + 1442695040888963407) % 2**64
     assert vals[0] == np.float16(np.float32(s >> 40) / np.float32(2**24) - np.float32(0.5)) \
         .view(np.uint16)
+
+
+@pytest.mark.parametrize("kind", [4, 2, 1])
+@pytest.mark.parametrize("threads", [1, 3, 8])
+def test_threaded_baseline_is_the_single_threaded_path(kind, threads):
+    """The CPU baseline's threaded mode splits columns over host threads; each
+    output keeps its own arithmetic, so the bits equal the single-threaded
+    oracle's."""
+    rng = np.random.default_rng(kind * 10 + threads)
+    m, n, k = 3, 131, 200
+    a = rng.standard_normal(m * k).astype(np.float16).view(np.uint16)
+    if kind == 4:
+        codes = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+        scales = rng.uniform(0.005, 0.02, n * -(-k // 32)).astype(np.float16).view(np.uint16)
+        want = O.matmul_q4_ep(a, codes, scales, None, m, n, k, 32)
+        block = 32
+    else:
+        block = 64
+        codes = rng.integers(0, 256, (k * n + (3 if kind == 2 else 7)) // (4 if kind == 2 else 8),
+                             dtype=np.uint8)
+        scales = rng.uniform(0.01, 0.05, n * -(-k // block)).astype(np.float16).view(np.uint16)
+        want = O.lowbit_reference(kind, a, codes, scales, m, n, k, block)
+    got = O.matmul_mt(kind, a, codes, scales, m, n, k, block, threads)
+    assert np.array_equal(got, want)
