@@ -483,7 +483,7 @@ def block_decode(x, cache_k, cache_v, pos, p, parts=None):
     x: f32 [d] (updated copy returned); cache_k / cache_v: f16 [cap][kv*hd]
     (row pos written). p: dict of the block's parts (see tests). parts: a
     dict that receives the two f16 terms added to the residual, as f32
-    ("attn", "mlp")."""
+    ("attn", "mlp"), and the residual between them ("x1")."""
     d, H, KV, hd, eps = p["d"], p["heads"], p["kv_heads"], p["head_dim"], p["eps"]
     x = np.array(x, np.float32, copy=True)
     h = rms_norm_f16(x, p["norm1"], eps)
@@ -503,13 +503,20 @@ def block_decode(x, cache_k, cache_v, pos, p, parts=None):
     if parts is not None:
         parts["attn"] = f16_to_f32(o)
     x = (x + f16_to_f32(o)).astype(np.float32)
-    h = rms_norm_f16(x, p["norm2"], eps)
+    o = block_mlp_term(x, p)
+    if parts is not None:
+        parts["x1"] = x.copy()
+        parts["mlp"] = o
+    return (x + o).astype(np.float32)
+
+
+def block_mlp_term(x, p):
+    """The MLP half's term of Block::accumulate (src/block.rs:90-106) for the
+    f32 residual row x: f32(down(glu(gate_up(rms_norm(x, norm2) -> f16))))."""
+    h = rms_norm_f16(np.asarray(x, np.float32), p["norm2"], p["eps"])
     both = p["gate_up"].forward(h)
     hid = glu_f16(both, 1, p["ffn"], p.get("gelu", False))
-    o = p["down"].forward(hid)
-    if parts is not None:
-        parts["mlp"] = f16_to_f32(o)
-    return (x + f16_to_f32(o)).astype(np.float32)
+    return f16_to_f32(p["down"].forward(hid))
 
 
 def q4_interleave32(gq, gs, uq, us, n, k, block=32):

@@ -299,7 +299,7 @@ int make_q4(Get get, const uint16_t *scales_rm, const uint16_t *mins_rm, const u
         const size_t byteoff = wd * 4 + bitpos / 8;
         const int shift = bitpos % 8;
         for (size_t j = 0; j < n; j++)
-            nib[(kc * d.n_pad + j) * 16 + byteoff] |= (uint8_t)((get(dd, j) ^ 8) << shift);
+            nib[cell_index(kc, j, d.nchunks) * 16 + byteoff] |= (uint8_t)((get(dd, j) ^ 8) << shift);
     }
     std::vector<uint16_t> sc(d.sc_rows * d.n_pad, 0), mn;
     const bool affine = mins_rm || mins_band;
@@ -309,12 +309,12 @@ int make_q4(Get get, const uint16_t *scales_rm, const uint16_t *mins_rm, const u
             size_t src;
             if (scales_rm) {
                 src = j * nbk + b;
-                sc[b * d.n_pad + j] = scales_rm[src];
-                if (affine) mn[b * d.n_pad + j] = mins_rm[src];
+                sc[cell_index(b, j, d.sc_rows)] = scales_rm[src];
+                if (affine) mn[cell_index(b, j, d.sc_rows)] = mins_rm[src];
             } else {
                 src = (j / 128) * (nbk * 128) + b * 128 + j % 128;
-                sc[b * d.n_pad + j] = scales_band[src];
-                if (affine) mn[b * d.n_pad + j] = mins_band[src];
+                sc[cell_index(b, j, d.sc_rows)] = scales_band[src];
+                if (affine) mn[cell_index(b, j, d.sc_rows)] = mins_band[src];
             }
         }
     void *p;
@@ -390,15 +390,15 @@ int make_lowbit(int kind, Get get, const uint16_t *scales, bool band_scales,
     for (size_t dd = 0; dd < k; dd++) {
         const uint32_t bit = kind == W_Q2 ? lb_bit<2>(dd) : lb_bit<1>(dd);
         for (size_t j = 0; j < n; j++) {
-            const size_t off = kind == W_Q2 ? lb_dword_offset<2>(dd, j, d.n_pad)
-                                            : lb_dword_offset<1>(dd, j, d.n_pad);
+            const size_t off = kind == W_Q2 ? lb_dword_offset<2>(dd, j, d.nchunks)
+                                            : lb_dword_offset<1>(dd, j, d.nchunks);
             codes[off + bit / 8] |= (uint8_t)(get(dd, j) << (bit % 8));
         }
     }
     std::vector<uint16_t> sc(d.sc_rows * d.n_pad, 0);
     for (size_t j = 0; j < n; j++)
         for (size_t b = 0; b < nbk; b++)
-            sc[b * d.n_pad + j] =
+            sc[cell_index(b, j, d.sc_rows)] =
                 band_scales ? scales[lb_scale_index(nbk * 64, b, j)] : scales[j * nbk + b];
     void *p;
     int rc;
@@ -496,7 +496,7 @@ int check_kind(const smg_weights *w, int kind) {
 
 // A handle of n_out columns whose column j is column cols[j] of a, or of b when
 // bit 30 of cols[j] is set. Every device array of a weight set is a
-// [rows][n_pad] grid of cells, so whole cells move unchanged.
+// tile-major [rows][n_pad] grid of cells, so whole cells move unchanged.
 int gather_columns(const smg_weights *a, const smg_weights *b, const std::vector<int32_t> &cols,
                    smg_weights **out) {
     HIP_TRY(hipSetDevice(a->device), SMG_EHIP);
@@ -528,8 +528,7 @@ int gather_columns(const smg_weights *a, const smg_weights *b, const std::vector
         void *p;
         if ((rc = alloc_dev(w, f[i].rows * d.n_pad * f[i].cell, &p))) break;
         *f[i].dst = p;
-        e = launch_gather_columns(p, d.n_pad, f[i].s0, f[i].s1, s.n_pad, dmap, f[i].rows, f[i].cell,
-                                  nullptr);
+        e = launch_gather_columns(p, d.n_pad, f[i].s0, f[i].s1, dmap, f[i].rows, f[i].cell, nullptr);
     }
     if (e == hipSuccess) e = hipDeviceSynchronize();
     (void)hipFree(dmap);

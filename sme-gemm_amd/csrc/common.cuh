@@ -509,28 +509,34 @@ __device__ __forceinline__ uint16_t finish(const EpArgs &ep, float acc, size_t i
 // Device weight layouts (this library's own; the reference's band-major
 // arrays are repacked into these at upload).
 //
-// Q4 ("chunk-major"): K is cut into chunks of 32 depths (16 bytes). Chunk kc of
-// column j sits at byte (kc*n_pad + j)*16, so a wave reading consecutive
-// columns of one chunk reads one contiguous run. Inside a chunk, dword w
+// Every array is a grid of fixed-size cells, [rows][n_pad] (a Q4 chunk, a
+// low-bit lane group, a scale or a min), stored tile-major: 16-column tiles,
+// one after another, each holding its rows in order and a row's 16 cells
+// adjacent -- cell (r, j) is cell number cell_index(r, j, rows). A decode GEMV
+// workgroup owns one 16-column tile, so everything it reads (codes, scales)
+// is one contiguous run instead of a 256-byte piece of every row.
+//
+// Q4: K is cut into chunks of 32 depths (16 bytes); chunk kc of column j is
+// cell (kc, j) of a grid of nchunks rows. Inside a chunk, dword w
 // (depths 8w..8w+7) holds depth 8w+2e at bits 4e..4e+3 and depth 8w+2e+1 at
 // bits 16+4e..16+4e+3 (e = 0..3), so ((dword >> 4e) & 0x000F000F) yields the
 // consecutive pair (8w+2e, 8w+2e+1) in two half-words. The stored nibble is
 // the reference's nibble (code two's complement, q4/mod.rs:213-214).
-// Scales (and mins): row kb = d/block of an [n_sc_rows][n_pad] f16 array.
+// Scales (and mins): cell (kb = d/block, j) of an f16 grid of sc_rows rows.
 //
 // Low-bit (Q2 / Q1) layouts are cut for v_mfma_i32_16x16x64_i8, whose A
 // operand gives each lane 16 depths of one column: K is split into 64-depth
 // slabs, a slab into four 16-depth quarters g. A "group" is the 16 bytes one
-// lane loads: quarter g of several consecutive slabs of one column. Group
-// (q, column j, quarter g) sits at byte ((q*n_pad + j)*4 + g)*16, so the four
-// quarters of a column are 64 contiguous bytes and 16 columns are 1 KB.
+// lane loads: quarter g of several consecutive slabs of one column. The four
+// quarters of group q of column j make the 64-byte cell (q, j) (quarter g at
+// byte 16g), so 16 columns of one group are 1 KB.
 // Q2: a group covers 4 slabs (256 depths); dword u is slab 4q+u, quarter g,
 //   depth 16g+4i+b of the slab at byte b, bits 2i..2i+1, so
 //   ((dword >> 2i) & 0x03030303) gives 4 consecutive depths' codes as bytes.
 // Q1: a group covers 8 slabs (512 depths); dword u holds slabs 8q+2u (bit i of
 //   byte b = depth 16g+4i+b, i < 4) and 8q+2u+1 (bit 4+i of byte b), so
 //   ((dword >> i) & 0x01010101) gives 4 consecutive sign bits as 0/1 bytes.
-// Low-bit scales: [sc_rows][n_pad] f16, row = block.
+// Low-bit scales: cell (block, j) of an f16 grid of sc_rows rows.
 // ---------------------------------------------------------------------------
 constexpr int Q4_CHUNK = 32;    // depths per 16-byte Q4 chunk
 constexpr int LB_SLAB = 64;     // depths per MFMA K step
@@ -539,12 +545,17 @@ constexpr int Q1_GROUP = 512;   // depths per 16-byte Q1 lane group
 
 // Byte offset of the dword holding (depth d, column j) in a low-bit layout,
 // and the bit of depth d inside that dword.
+// Cell number of cell (r, j) in a tile-major grid of `rows` rows.
+__host__ __device__ __forceinline__ size_t cell_index(size_t r, size_t j, size_t rows) {
+    return ((j >> 4) * rows + r) * 16 + (j & 15);
+}
+
 template <int KIND>
-__host__ __device__ __forceinline__ size_t lb_dword_offset(size_t d, size_t j, size_t n_pad) {
+__host__ __device__ __forceinline__ size_t lb_dword_offset(size_t d, size_t j, size_t ngroups) {
     const size_t grp = KIND == 2 ? Q2_GROUP : Q1_GROUP;
     const size_t q = d / grp, slab = (d % grp) / LB_SLAB, g = (d % LB_SLAB) / 16;
     const size_t u = KIND == 2 ? slab : slab / 2;
-    return ((q * n_pad + j) * 4 + g) * 16 + u * 4;
+    return (cell_index(q, j, ngroups) * 4 + g) * 16 + u * 4;
 }
 template <int KIND>
 __host__ __device__ __forceinline__ uint32_t lb_bit(size_t d) {

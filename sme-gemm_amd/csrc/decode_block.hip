@@ -24,6 +24,8 @@
 // residual adds); sums run in other orders (split-K GEMV, a tree for the sum
 // of squares, split softmax) and exp / tanh are the device's, so results are
 // held to a tolerance against the portable path, not to its bits.
+#include <atomic>
+
 #include "q4_gemv_core.cuh"
 
 namespace smg {
@@ -99,26 +101,36 @@ __device__ __forceinline__ float glu_act(uint32_t act, float g) {
     return g / (1.0f + expf(-g));
 }
 
-template <int MR, bool NORM, int STORE>
-__global__ void __launch_bounds__(MF_WAVES * 64) blk_gemv(Q4GemvArgs g, BlkArgs a) {
-    static_assert(!NORM || MR == 1, "the fused norm serves one row");
-    static_assert(STORE != BS_QKV || MR == 1, "the rope / cache store serves one row");
-    extern __shared__ __align__(16) uint8_t smem[];
-    uint16_t *a_lds = (uint16_t *)smem;
-    float *red = (float *)smem;
-    const int t = threadIdx.x;
-    const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
-    const uint32_t col = tile * 16 + (t & 15);
-    bool timed_out = false;
-    float4_t acc;
-    if constexpr (NORM) {
-        const SrcNormRow src(a.nx, a.nw, g.k, a.eps);
-        acc = q4_mfma_mainloop<1, false>(g, src, ChainArgs{}, a_lds, col, timed_out);
-    } else {
-        const SrcRows<MR> src(g.lhs, g.m, g.k);
-        acc = q4_mfma_mainloop<MR, false>(g, src, ChainArgs{}, a_lds, col, timed_out);
+// Loads a single-row tile store reads (the residual it adds to, the RoPE
+// angles), issued ahead of the next item's weight loads so the store does not
+// wait for those.
+struct BlkPre {
+    float y, c, s;
+};
+template <int STORE>
+__device__ __forceinline__ BlkPre blk_prefetch(const Q4GemvArgs &g, const BlkArgs &a, uint32_t tile) {
+    BlkPre p{0.0f, 1.0f, 0.0f};
+    const uint32_t t = threadIdx.x;
+    if constexpr (STORE == BS_RESID) {
+        const uint32_t j = tile * 16 + t;
+        if (t < 16 && j < g.n) p.y = a.x[j];
+    } else if constexpr (STORE == BS_QKV) {
+        const uint32_t pc = tile * 16 + t;
+        if (t < 16 && a.cs && pc < (a.heads + a.kv_heads) * a.hd) {
+            const uint32_t pi = 8 * ((pc % a.hd) / 16) + (t & 7);
+            p.c = a.cs[pi];
+            p.s = a.sn[pi];
+        }
     }
-    q4_mfma_reduce<MR>(acc, red);
+    return p;
+}
+
+// The tile's store from the reduced partials in red (after q4_mfma_reduce).
+// pre: blk_prefetch's loads for MR = 1 (MR > 1 reads the residual here).
+template <int MR, int STORE>
+__device__ __forceinline__ void blk_store(const Q4GemvArgs &g, const BlkArgs &a, uint32_t tile, const float *red,
+                                          const BlkPre &pre) {
+    const int t = threadIdx.x;
     if constexpr (STORE == BS_RESID) {
         // y += f32(f16(x @ W)): Linear::accumulate's add_f16 (src/convert.rs:37-49)
         if (t < 16 * MR) {
@@ -126,7 +138,8 @@ __global__ void __launch_bounds__(MF_WAVES * 64) blk_gemv(Q4GemvArgs g, BlkArgs 
             const uint32_t j = tile * 16 + cc;
             if (r < (int)g.m && j < g.n) {
                 float *yp = a.x + (size_t)r * g.n + j;
-                *yp = *yp + f16_to_f32(f32_to_f16(tile_total<MR>(red, cc, r)));
+                const float y0 = MR == 1 ? pre.y : *yp;
+                *yp = y0 + f16_to_f32(f32_to_f16(tile_total<MR>(red, cc, r)));
             }
         }
     } else if constexpr (STORE == BS_GLU) {
@@ -141,6 +154,7 @@ __global__ void __launch_bounds__(MF_WAVES * 64) blk_gemv(Q4GemvArgs g, BlkArgs 
             }
         }
     } else {
+        static_assert(MR == 1, "the rope / cache store serves one row");
         // device tile = columns 8q..8q+7 and half+8q..half+8q+7 of one head
         // (q heads, then k heads, then v heads): each lane's RoPE partner is
         // lane ^ 8 of the same tile.
@@ -155,11 +169,9 @@ __global__ void __launch_bounds__(MF_WAVES * 64) blk_gemv(Q4GemvArgs g, BlkArgs 
             if (H < a.heads + a.kv_heads) {
                 float val = f16_to_f32(own16);
                 if (a.cs) {
-                    const uint32_t pi = 8 * qt + (cc & 7);
-                    const float c = a.cs[pi], s = a.sn[pi];
                     const float x1 = f16_to_f32(cc < 8 ? own16 : par16);
                     const float x2 = f16_to_f32(cc < 8 ? par16 : own16);
-                    val = cc < 8 ? x1 * c - x2 * s : x2 * c + x1 * s;
+                    val = cc < 8 ? x1 * pre.c - x2 * pre.s : x2 * pre.c + x1 * pre.s;
                 }
                 if (H < a.heads) a.q_out[H * hd + i] = f32_to_f16(val * a.scale);
                 else a.k_row[(H - a.heads) * hd + i] = f32_to_f16(val);
@@ -171,18 +183,151 @@ __global__ void __launch_bounds__(MF_WAVES * 64) blk_gemv(Q4GemvArgs g, BlkArgs 
 }
 
 template <int MR, bool NORM, int STORE>
+__global__ void __launch_bounds__(MF_WAVES * 64) blk_gemv(Q4GemvArgs g, BlkArgs a) {
+    static_assert(!NORM || MR == 1, "the fused norm serves one row");
+    static_assert(STORE != BS_QKV || MR == 1, "the rope / cache store serves one row");
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint16_t *a_lds = (uint16_t *)smem;
+    float *red = (float *)smem;
+    const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
+    const uint32_t col = tile * 16 + (threadIdx.x & 15);
+    bool timed_out = false;
+    float4_t acc;
+    if constexpr (NORM) {
+        const SrcNormRow src(a.nx, a.nw, g.k, a.eps);
+        acc = q4_mfma_mainloop<1, false>(g, src, ChainArgs{}, a_lds, col, timed_out);
+    } else {
+        const SrcRows<MR> src(g.lhs, g.m, g.k);
+        acc = q4_mfma_mainloop<MR, false>(g, src, ChainArgs{}, a_lds, col, timed_out);
+    }
+    BlkPre pre{0.0f, 1.0f, 0.0f};
+    if constexpr (MR == 1) pre = blk_prefetch<STORE>(g, a, tile);
+    q4_mfma_reduce<MR>(acc, red);
+    blk_store<MR, STORE>(g, a, tile, red, pre);
+}
+
+// The single-row GEMV as a persistent grid (at most BP_WG_PER_CU workgroups a
+// CU): each workgroup stages the activation row once -- normalizing it once,
+// with the fused norm -- for the whole K (up to BP_MAX_SEG segments), then
+// walks its tiles (blockIdx.x, + gridDim.x, ...) segment by segment with
+// the next item's weights loading while the current one's MFMAs run.
+constexpr int BP_WG_PER_CU = 2;
+constexpr int BP_MAX_SEG = 4;  // K <= 16384
+constexpr size_t BP_RED_BYTES = MF_WAVES * 16 * 4;
+template <bool NORM, int STORE>
+__global__ void __launch_bounds__(MF_WAVES * 64) blk_gemv_p(Q4GemvArgs g, BlkArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int t = threadIdx.x, c = t & 15;
+    const uint32_t ntiles = g.n_pad / 16;
+    const uint32_t nseg = (g.nchunks + MF_SEG_CH - 1) / MF_SEG_CH;
+    // LDS: red, then the row (whole segments)
+    float *red = (float *)smem;
+    uint16_t *arow = (uint16_t *)(smem + BP_RED_BYTES);
+    const uint32_t mag_lo = __builtin_amdgcn_readfirstlane(0x64006400u) | (uint32_t)(t >> 30);
+    const uint32_t mag_hi = __builtin_amdgcn_readfirstlane(0x54005400u) | (uint32_t)(t >> 30);
+    const uint32_t mine = (ntiles - 1 - blockIdx.x) / gridDim.x + 1;  // the grid is at most ntiles
+    const uint32_t nitems = mine * nseg;
+    // item q: tile blockIdx.x + (q / nseg) gridDim.x, segment q % nseg
+    auto tile_of = [&](uint32_t q) { return blockIdx.x + (q / nseg) * gridDim.x; };
+    auto sc0_of = [&](uint32_t q) { return (q % nseg) * (uint32_t)MF_SEG_CH; };
+    Q4Item w0, w1;
+    // the activation row first (its loads retire before the weights'), then
+    // item 0's weights, then the row staged while those stream in
+    if constexpr (NORM) {
+        const SrcNormRow src(a.nx, a.nw, g.k, a.eps);
+        SrcNormRow::Regs ar;
+        src.load(ar, 0, t);
+        q4_item_load(g, sc0_of(0), tile_of(0) * 16 + c, w0);
+        src.stage(arow, ar, t);
+    } else {
+        const SrcRows<1> src(g.lhs, 1, g.k);
+        SrcRows<1>::Regs ar[BP_MAX_SEG];
+#pragma unroll
+        for (int sg = 0; sg < BP_MAX_SEG; sg++)
+            if ((uint32_t)sg < nseg) src.load(ar[sg], sg * MF_SEG, t);
+        q4_item_load(g, sc0_of(0), tile_of(0) * 16 + c, w0);
+#pragma unroll
+        for (int sg = 0; sg < BP_MAX_SEG; sg++)
+            if ((uint32_t)sg < nseg) src.stage(arow + sg * MF_SEG, ar[sg], t);
+    }
+    __syncthreads();
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t q = 0; q < nitems; q += 2) {
+        // clamped past the end: a repeat of the last item (a cache hit), unused
+        const uint32_t q1 = q + 1 < nitems ? q + 1 : nitems - 1;
+        const uint32_t tq = tile_of(q);
+        const bool end0 = q % nseg == nseg - 1;
+        BlkPre pre{0.0f, 1.0f, 0.0f};
+        if (end0) pre = blk_prefetch<STORE>(g, a, tq);
+        q4_item_load(g, sc0_of(q1), tile_of(q1) * 16 + c, w1);
+        q4_item_mma1(sc0_of(q), w0, arow, acc, mag_lo, mag_hi);
+        if (end0) {
+            q4_mfma_reduce<1>(acc, red);
+            blk_store<1, STORE>(g, a, tq, red, pre);
+            acc = float4_t{0.f, 0.f, 0.f, 0.f};
+        }
+        if (q + 1 >= nitems) break;
+        const uint32_t q2 = q + 2 < nitems ? q + 2 : nitems - 1;
+        const uint32_t t1 = tile_of(q1);
+        const bool end1 = q1 % nseg == nseg - 1;
+        BlkPre pre1{0.0f, 1.0f, 0.0f};
+        if (end1) pre1 = blk_prefetch<STORE>(g, a, t1);
+        q4_item_load(g, sc0_of(q2), tile_of(q2) * 16 + c, w0);
+        q4_item_mma1(sc0_of(q1), w1, arow, acc, mag_lo, mag_hi);
+        if (end1) {
+            q4_mfma_reduce<1>(acc, red);
+            blk_store<1, STORE>(g, a, t1, red, pre1);
+            acc = float4_t{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+}
+
+template <int MR, bool NORM, int STORE>
 hipError_t launch_blk(const Q4GemvArgs &g, const BlkArgs &a, hipStream_t s) {
     hipLaunchKernelGGL((blk_gemv<MR, NORM, STORE>), dim3(g.n_pad / 16), dim3(MF_WAVES * 64),
                        q4_mfma_lds_bytes<MR>(), s, g, a);
     return hipGetLastError();
 }
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+    static std::atomic<int> cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cus[dev].load(std::memory_order_relaxed);
+    if (v <= 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cus[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
+template <bool NORM, int STORE>
+hipError_t launch_blk_p(const Q4GemvArgs &g, const BlkArgs &a, hipStream_t s) {
+    const uint32_t ntiles = g.n_pad / 16;
+    const uint32_t nseg = (g.nchunks + MF_SEG_CH - 1) / MF_SEG_CH;
+    const uint32_t grid = std::min<uint32_t>(ntiles, (uint32_t)(BP_WG_PER_CU * device_cus()));
+    const size_t lds = BP_RED_BYTES + (size_t)nseg * MF_SEG * 2;
+    hipLaunchKernelGGL((blk_gemv_p<NORM, STORE>), dim3(grid), dim3(MF_WAVES * 64), lds, s, g, a);
+    return hipGetLastError();
+}
+
+// One row with at least two tiles for every workgroup of a full persistent
+// grid (K within its staging): the persistent grid, which then keeps the
+// next tile's weights in flight and normalizes the row once per workgroup
+// rather than once per tile. Fewer tiles (a workgroup would get about one)
+// run faster as one workgroup per tile (measured on the block's projections:
+// 28672 columns 15.7 vs 18.4 us, 4096-6144 columns 0.3-0.4 us slower).
 template <bool NORM, int STORE>
 hipError_t launch_blk_rows(const Q4GemvArgs &g, const BlkArgs &a, size_t m, hipStream_t s) {
+    const bool persistent = m == 1 && (g.nchunks + MF_SEG_CH - 1) / MF_SEG_CH <= (uint32_t)BP_MAX_SEG &&
+                            g.n_pad / 16 >= 2u * BP_WG_PER_CU * (uint32_t)device_cus();
     if constexpr (NORM || STORE == BS_QKV) {
         if (m != 1) return hipErrorNotSupported;
+        if (persistent) return launch_blk_p<NORM, STORE>(g, a, s);
         return launch_blk<1, NORM, STORE>(g, a, s);
     } else {
+        if (persistent) return launch_blk_p<NORM, STORE>(g, a, s);
         if (m <= 1) return launch_blk<1, NORM, STORE>(g, a, s);
         if (m <= 2) return launch_blk<2, NORM, STORE>(g, a, s);
         if (m <= 4) return launch_blk<4, NORM, STORE>(g, a, s);
@@ -310,25 +455,70 @@ __global__ void __launch_bounds__(AT_T) attn_split(AttnArgs a) {
     if (t < AT_HC && hc0 + t < a.group) a.pml[(size_t)split * a.heads + kvh * a.group + hc0 + t] = mls[t];
 }
 
-// The splits of head blockIdx.x merged: o = sum_s e^(m_s - M) o_s / sum_s
-// e^(m_s - M) l_s, in split order; f16 (the out projection's input) or f32.
+// The splits of head blockIdx.x merged, for depths 16 blockIdx.y .. +16:
+// o = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s, f16 (the out
+// projection's input) or f32. Thread (group g = t / 16, depth t % 16) takes
+// splits g, g + 16, ...: it issues the loads of CM_P of them at once, then
+// folds them into its running (m, l, o) -- rescaled by e^(m_old - m_new) --
+// so a context of up to 16 CM_P splits costs one memory round trip; the 16
+// groups' (m, l, o) are then merged through LDS in group order.
+constexpr int CM_T = 256;           // threads
+constexpr int CM_D = 16;            // depths per workgroup
+constexpr int CM_G = CM_T / CM_D;   // split groups
+constexpr int CM_P = 8;             // splits per thread per round trip
 template <bool F16OUT>
-__global__ void attn_combine(const float *po, const float2 *pml, uint32_t nsplit, uint32_t heads,
-                             uint32_t hd, void *out) {
-    const uint32_t h = blockIdx.x, d = threadIdx.x;
-    if (d >= hd) return;
-    float m = -INFINITY;
-    for (uint32_t s = 0; s < nsplit; s++) m = fmaxf(m, pml[(size_t)s * heads + h].x);
-    float l = 0.0f, o = 0.0f;
-    for (uint32_t s = 0; s < nsplit; s++) {
-        const float2 ml = pml[(size_t)s * heads + h];
-        const float w = expf(ml.x - m);
-        l = __builtin_fmaf(w, ml.y, l);
-        o = __builtin_fmaf(w, po[((size_t)s * heads + h) * hd + d], o);
+__global__ void __launch_bounds__(CM_T) attn_combine(const float *po, const float2 *pml, uint32_t nsplit,
+                                                     uint32_t heads, uint32_t hd, void *out) {
+    __shared__ float sm[CM_G][CM_D], sl[CM_G][CM_D], so[CM_G][CM_D];
+    const uint32_t h = blockIdx.x, t = threadIdx.x;
+    const uint32_t dl = t % CM_D, g = t / CM_D;
+    const uint32_t d = blockIdx.y * CM_D + dl;
+    const bool dok = d < hd;
+    float m = -INFINITY, l = 0.0f, o = 0.0f;
+    for (uint32_t s0 = g; s0 < nsplit; s0 += CM_G * CM_P) {
+        float2 ml[CM_P];
+        float ov[CM_P];
+#pragma unroll
+        for (int j = 0; j < CM_P; j++) {
+            const uint32_t s = s0 + CM_G * j;
+            const bool ok = s < nsplit;
+            ml[j] = ok ? pml[(size_t)s * heads + h] : make_float2(-INFINITY, 0.0f);
+            ov[j] = ok && dok ? po[((size_t)s * heads + h) * hd + d] : 0.0f;
+        }
+        // split s0 exists, and every split holds at least one key: mc is finite
+        float mc = m;
+#pragma unroll
+        for (int j = 0; j < CM_P; j++) mc = fmaxf(mc, ml[j].x);
+        const float r = expf(m - mc);
+        l = l * r;
+        o = o * r;
+#pragma unroll
+        for (int j = 0; j < CM_P; j++) {
+            const float w = expf(ml[j].x - mc);
+            l = __builtin_fmaf(w, ml[j].y, l);
+            o = __builtin_fmaf(w, ov[j], o);
+        }
+        m = mc;
     }
-    const float v = o / l;
-    if (F16OUT) ((uint16_t *)out)[h * hd + d] = f32_to_f16(v);
-    else ((float *)out)[h * hd + d] = v;
+    sm[g][dl] = m;
+    sl[g][dl] = l;
+    so[g][dl] = o;
+    __syncthreads();
+    if (t < CM_D && dok) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < CM_G; q++) mx = fmaxf(mx, sm[q][t]);
+        float lt = 0.0f, ot = 0.0f;
+#pragma unroll
+        for (int q = 0; q < CM_G; q++) {
+            const float w = expf(sm[q][t] - mx);  // a group with no split: e^-inf = 0
+            lt = __builtin_fmaf(w, sl[q][t], lt);
+            ot = __builtin_fmaf(w, so[q][t], ot);
+        }
+        const float v = ot / lt;
+        if (F16OUT) ((uint16_t *)out)[h * hd + d] = f32_to_f16(v);
+        else ((float *)out)[h * hd + d] = v;
+    }
 }
 
 // q (f32) to the rounded query attention_kv_f16 scores with: f16(q * scale).
@@ -412,13 +602,13 @@ hipError_t launch_attention(const AttnArgs &a0, void *out, bool f16_out, hipStre
     else hipLaunchKernelGGL(attn_split<32>, grid, dim3(AT_T), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const uint32_t threads = (a.hd + 63) / 64 * 64;
+    const dim3 cgrid(a.heads, (a.hd + CM_D - 1) / CM_D);
     if (f16_out)
-        hipLaunchKernelGGL(attn_combine<true>, dim3(a.heads), dim3(threads), 0, s, a.po, a.pml, a.nsplit,
-                           a.heads, a.hd, out);
+        hipLaunchKernelGGL(attn_combine<true>, cgrid, dim3(CM_T), 0, s, a.po, a.pml, a.nsplit, a.heads, a.hd,
+                           out);
     else
-        hipLaunchKernelGGL(attn_combine<false>, dim3(a.heads), dim3(threads), 0, s, a.po, a.pml, a.nsplit,
-                           a.heads, a.hd, out);
+        hipLaunchKernelGGL(attn_combine<false>, cgrid, dim3(CM_T), 0, s, a.po, a.pml, a.nsplit, a.heads, a.hd,
+                           out);
     return hipGetLastError();
 }
 

@@ -46,6 +46,7 @@ struct LbArgs {
     uint32_t codebook;
     uint32_t kq, nbq;     // row strides of q and of s / asum
     uint32_t sc_rows;
+    uint32_t ngroups;     // 16-byte code groups per column (rows of the code grid)
     uint32_t seg_depths;  // depths per segment (a multiple of max(block, 64))
 };
 
@@ -104,7 +105,7 @@ __global__ void __launch_bounds__(T) lowbit_gemv(LbArgs g, EpArgs ep) {
                                       ? (row0 + c) * g.kq + slab * LB_SLAB + 16 * gq4 : OOB);
             const uint32_t sl = live ? slab : sa0;  // dead slots reload a valid dword
             wreg[i] = *(const uint32_t *)(g.codes +
-                                          lb_dword_offset<KIND>((size_t)sl * LB_SLAB + 16 * gq4, col, g.n_pad));
+                                          lb_dword_offset<KIND>((size_t)sl * LB_SLAB + 16 * gq4, col, g.ngroups));
         }
         // scales of the 16 columns (32 bytes a block), activation scales, sums
         constexpr int RS = 4;  // up to 4 x 512 x 16 B = 32 KB of scale rows
@@ -112,7 +113,7 @@ __global__ void __launch_bounds__(T) lowbit_gemv(LbArgs g, EpArgs ep) {
 #pragma unroll
         for (int r = 0; r < RS; r++) {
             const uint32_t i = t + T * r, bb = i / 2, half = i % 2;
-            sreg[r] = bload16(sr, bb < nb ? ((b0 + bb) * g.n_pad + col0) * 2u + half * 16u : OOB);
+            sreg[r] = bload16(sr, bb < nb ? (uint32_t)cell_index(b0 + bb, col0, g.sc_rows) * 2u + half * 16u : OOB);
         }
         float fsa[2];
         int32_t fas[2];
@@ -456,7 +457,8 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
     {
         const rsrc_t sr = make_rsrc(g.sc, g.sc_rows * g.n_pad * 2u);
         const uint32_t bb = t >> (g.cg_shift + 1), piece = t & (2 * cg - 1);  // 8 columns a piece
-        sreg = bload16(sr, (bb < nbq && bb < g.sc_rows) ? (bb * g.n_pad + wg_col0 + piece * 8) * 2u : OOB);
+        sreg = bload16(sr, (bb < nbq && bb < g.sc_rows) ? (uint32_t)cell_index(bb, wg_col0 + piece * 8, g.sc_rows) * 2u
+                                                        : OOB);
     }
     uint4 wreg[NG];
     {
@@ -464,7 +466,7 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
 #pragma unroll
         for (int i = 0; i < NG; i++) {
             const uint32_t grp = kw * NG + i;
-            wreg[i] = bload16(cr, grp < g.ngroups ? ((grp * g.n_pad + col0 + c) * 4 + gq4) * 16 : OOB);
+            wreg[i] = bload16(cr, grp < g.ngroups ? ((uint32_t)cell_index(grp, col0 + c, g.ngroups) * 4 + gq4) * 16 : OOB);
         }
     }
     // the epilogue operands last: their addresses wait on the op-graph's
@@ -903,6 +905,7 @@ hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint
     g.kq = (uint32_t)ge.kq;
     g.nbq = (uint32_t)ge.nbq;
     g.sc_rows = (uint32_t)w.sc_rows;
+    g.ngroups = (uint32_t)w.nchunks;
     g.seg_depths = (uint32_t)ge.seg;
     int8_t *q = (int8_t *)scratch;
     float *sp = (float *)((uint8_t *)scratch + (m * ge.kq + 255) / 256 * 256);

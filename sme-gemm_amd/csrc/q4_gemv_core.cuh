@@ -5,8 +5,9 @@
 //
 // A workgroup of 8 waves owns 16 output columns; wave w takes every 8th group
 // of 4 chunks (128 depths). Lane (g = lane/16, c = lane%16) loads the 16-byte
-// chunk g of column c, so a wave load reads four contiguous 256-byte runs, and
-// every lane issues all its weight loads before it waits. Each dword (8
+// chunk g of column c, so a wave load reads one contiguous 1 KB run of the
+// tile-major layout, and every lane issues all its weight loads before it
+// waits. Each dword (8
 // depths) dequantizes to 8 f16 weights -- v_bfi_b32 puts the nibble under an
 // f16 exponent, a packed subtract leaves the exact code, a packed multiply by
 // the scale is the reference's single RNE rounding of scale*code -- and feeds
@@ -25,6 +26,7 @@ struct Q4GemvArgs {
     const uint16_t *lhs;
     uint16_t *dst;
     uint32_t n, k, n_pad, nchunks, m;
+    uint32_t sc_rows;      // rows of the scale (and min) grids
     uint32_t block_shift;  // log2(block)
 };
 
@@ -112,8 +114,8 @@ __device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const 
         for (int u = 0; u < MF_U; u++) {
             const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
             const uint32_t kcc = kc < last ? kc : last;  // clamped: always a valid load
-            wq[u] = *(const uint4 *)(g.nib + ((size_t)kcc * g.n_pad + col) * 16);
-            const uint16_t sl = g.sc[(size_t)((kcc * Q4_CHUNK) >> g.block_shift) * g.n_pad + col];
+            wq[u] = *(const uint4 *)(g.nib + cell_index(kcc, col, g.nchunks) * 16);
+            const uint16_t sl = g.sc[cell_index((kcc * Q4_CHUNK) >> g.block_shift, col, g.sc_rows)];
             sv[u] = kc < g.nchunks ? sl : (uint16_t)0;  // a dead step's weights become 0
         }
         if constexpr (CHAIN) {
@@ -138,24 +140,20 @@ __device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const 
         src.stage(a_lds, areg, t);
         __syncthreads();
         // dequant + MFMA: A operand = 16 columns x 32 depths of weights, B
-        // operand = 32 depths x 16 rows of activations (rows >= m are zero).
-        // All of this wave's activation fragments are read first, from a valid
-        // row (branch-free, then selected), so the LDS round trips overlap
-        // instead of each one preceding its MFMA.
-        const int row = c;  // B-operand lane: activation row lane%16
-        const bool row_live = row < MR;
-        const uint16_t *arow = a_lds + (row_live ? row : 0) * MF_SEG;
+        // operand = 32 depths x 16 rows of activations. B lanes of rows >= MR
+        // read row MR-1 again: MFMA output rows are independent and those are
+        // never read, so nothing needs zeroing (no per-lane select, no masked
+        // branch). Chunks past K read the staged zeros of the segment and have
+        // zero weights. All of this wave's activation fragments are read
+        // first, so the LDS round trips overlap instead of each one preceding
+        // its MFMA.
+        const uint16_t *arow = a_lds + (c < MR ? c : MR - 1) * MF_SEG;
         uint4 abv[MF_U][4];
 #pragma unroll
         for (int u = 0; u < MF_U; u++) {
-            const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
-            const bool live = row_live && kc < g.nchunks;
-            const uint32_t kcl = kc < g.nchunks ? kc - sc0 : 0;
+            const uint32_t kcl = 4 * (wave + MF_WAVES * u) + grp;  // chunk within the segment
 #pragma unroll
-            for (int w = 0; w < 4; w++) {
-                const uint4 v = *(const uint4 *)(arow + kcl * Q4_CHUNK + w * 8);
-                abv[u][w] = live ? v : make_uint4(0, 0, 0, 0);
-            }
+            for (int w = 0; w < 4; w++) abv[u][w] = *(const uint4 *)(arow + kcl * Q4_CHUNK + w * 8);
         }
 #pragma unroll
         for (int u = 0; u < MF_U; u++) {
@@ -171,6 +169,52 @@ __device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const 
         }
     }
     return acc;
+}
+
+// One item of a persistent single-row GEMV (a workgroup that walks several
+// tiles): this lane's MF_U weight chunks of segment sc0 for column col, with
+// their scales, loaded before the previous item is multiplied so one item's
+// loads are always in flight behind the MFMAs. Past the last chunk the load
+// is clamped to a valid address and the scale is zero, as in the main loop.
+struct Q4Item {
+    uint4 wq[MF_U];
+    uint32_t sv[MF_U];
+};
+__device__ __forceinline__ void q4_item_load(const Q4GemvArgs &g, uint32_t sc0, uint32_t col, Q4Item &it) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, grp = lane >> 4;
+    const uint32_t last = g.nchunks - 1;
+#pragma unroll
+    for (int u = 0; u < MF_U; u++) {
+        const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
+        const uint32_t kcc = kc < last ? kc : last;
+        it.wq[u] = *(const uint4 *)(g.nib + cell_index(kcc, col, g.nchunks) * 16);
+        const uint16_t sl = g.sc[cell_index((kcc * Q4_CHUNK) >> g.block_shift, col, g.sc_rows)];
+        it.sv[u] = kc < g.nchunks ? sl : 0u;
+    }
+}
+// The item's MFMAs for activation row 0, staged in LDS at arow[depth] (the
+// whole row, zero-filled to whole segments): every B-operand lane reads row 0,
+// and only output row 0 is used.
+__device__ __forceinline__ void q4_item_mma1(uint32_t sc0, const Q4Item &it, const uint16_t *arow,
+                                             float4_t &acc, uint32_t mag_lo, uint32_t mag_hi) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int grp = lane >> 4;
+#pragma unroll
+    for (int u = 0; u < MF_U; u++) {
+        const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
+        uint4 ab[4];
+#pragma unroll
+        for (int w = 0; w < 4; w++) ab[w] = *(const uint4 *)(arow + kc * Q4_CHUNK + w * 8);
+        const half2_t s2 = {__builtin_bit_cast(_Float16, (uint16_t)it.sv[u]),
+                            __builtin_bit_cast(_Float16, (uint16_t)it.sv[u])};
+        const uint32_t words[4] = {it.wq[u].x, it.wq[u].y, it.wq[u].z, it.wq[u].w};
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            uint4 wa = q4_deq8(words[w], s2, mag_lo, mag_hi);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wa),
+                                                         __builtin_bit_cast(half8_t, ab[w]), acc, 0, 0, 0);
+        }
+    }
 }
 
 // The 8 waves' partial tiles into red[MF_WAVES][16 cols][MR] (LDS, after a
@@ -214,6 +258,7 @@ inline Q4GemvArgs q4_gemv_args(const WDev &w, size_t m, uint16_t *dst, const uin
     g.k = (uint32_t)w.k;
     g.n_pad = (uint32_t)w.n_pad;
     g.nchunks = (uint32_t)w.nchunks;
+    g.sc_rows = (uint32_t)w.sc_rows;
     g.m = (uint32_t)m;
     g.block_shift = (uint32_t)__builtin_ctzll(w.block);
     return g;

@@ -9,10 +9,16 @@ tests/correctness/main.rs:63-68):
   the north star's 2e-3 * sqrt(K)/64 at the GEMV's depth;
 - the block's f32 residual: it adds two f16 terms, the out projection's A
   (K = heads*head_dim) and the down projection's M (K = ffn), each held to the
-  GEMV bar, so |g - w| <= f16_tol(K_A)(1 + |A|) + f16_tol(K_M)(1 + |M|) per
-  element with A, M the oracle's terms (an error relative to the result would
-  be wrong where A and M cancel); and the whole update within 1e-3 of the
-  oracle's in relative norm;
+  GEMV bar, so |g - w| <= f16_tol(K_A)(1 + |A|) + f16_tol(K_M)(1 + |M|) + P
+  per element with A, M the oracle's terms (an error relative to the result
+  would be wrong where A and M cancel) and P how far A's error moves M, which
+  is computed from the residual A lands in (the oracle's MLP half re-run on
+  that residual shifted by A's tolerance); and the whole update within 1e-3
+  of the oracle's in relative norm;
+- a term added into a residual (Linear / Mlp / SelfAttention accumulate):
+  held to its GEMV bar relative to the term, plus how far the term moves when
+  an f16 input that is itself a GEMV result (the hidden layer, qkv) moves by
+  its own tolerance -- measured on the oracle with seeded random signs;
 - rms_norm: within one f16 ulp (the sum of squares runs in another order);
 - attention: within 2e-3 absolute of the f64 oracle on the reference's own
   test data (tests/correctness/kv_attention.rs:43-82), and within
@@ -42,9 +48,13 @@ def _np16(t):
     return t.cpu().numpy().view(np.uint16).ravel()
 
 
-def _rel32(got, want):
-    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
-    return float(np.max(np.abs(got - want) / (1.0 + np.abs(want))))
+def _check_term(got, y0, term, tol, moved=0.0):
+    """y = y0 + term: the added term held to the bar relative to the term
+    (not to the sum, which can cancel), plus `moved`, the part of its error
+    inherited from an f16 input that is itself a tolerance-checked result."""
+    err = np.abs(np.asarray(got, np.float64) - (np.asarray(y0, np.float64) + term))
+    bound = tol * (1 + np.abs(term)) + moved
+    assert np.all(err <= bound), float(np.max(err / bound))
 
 
 # ---- row passes --------------------------------------------------------------------
@@ -200,12 +210,11 @@ def test_linear_accumulate(smg, orc, m, n, k):
     y = _f32(y0)
     lin.accumulate(_h16(a), y, m)
     torch.cuda.synchronize()
-    out16 = orc.matmul_q4_ep(a, quants, scales, None, m, n, k, 32)
-    want = y0 + orc.f16_to_f32(out16)
-    assert _rel32(y.cpu().numpy(), want) <= f16_tol(k)
+    out = orc.f16_to_f32(orc.matmul_q4_ep(a, quants, scales, None, m, n, k, 32))
+    _check_term(y.cpu().numpy(), y0, out, f16_tol(k))
 
 
-def _mlp_oracle(orc, x16, inp, m, d, ffn, gated, gelu=False):
+def _mlp_oracle(orc, x16, inp, m, d, ffn, gated, gelu=False, parts=None):
     gq, gs, _, _ = inp["gate"]
     dq, ds, _, _ = inp["down"]
     if gated:
@@ -215,7 +224,23 @@ def _mlp_oracle(orc, x16, inp, m, d, ffn, gated, gelu=False):
         hid = orc.glu_f16(both, m, ffn, gelu)
     else:
         hid = orc.matmul_q4_ep(x16, gq, gs, None, m, ffn, d, 32, (), 2 if gelu else 3)
+    if parts is not None:
+        parts["hid"] = hid
     return orc.f16_to_f32(orc.matmul_q4_ep(hid, dq, ds, None, m, d, ffn, 32))
+
+
+def _down_moved(orc, inp, hid, m, d, ffn):
+    """How far the down projection's output moves when its f16 input (the
+    hidden layer, itself a GEMV result held to f16_tol(d)) moves by that
+    tolerance, with seeded random signs: the part of the MLP term's error that
+    comes from the hidden layer rather than from the down GEMV itself."""
+    dq, ds, _, _ = inp["down"]
+    h = orc.f16_to_f32(hid).astype(np.float64)
+    sign = np.where(np.random.default_rng(3).random(h.size) < 0.5, -1.0, 1.0)
+    h2 = orc.f32_to_f16((h + sign * f16_tol(d) * (1 + np.abs(h))).astype(np.float32))
+    a = orc.f16_to_f32(orc.matmul_q4_ep(hid, dq, ds, None, m, d, ffn, 32)).astype(np.float64)
+    b = orc.f16_to_f32(orc.matmul_q4_ep(h2, dq, ds, None, m, d, ffn, 32)).astype(np.float64)
+    return np.abs(b - a)
 
 
 @pytest.mark.parametrize("gated,gelu,m,d,ffn", [(True, False, 1, 4096, 14336), (True, False, 3, 256, 320),
@@ -238,8 +263,9 @@ def test_mlp_accumulate(smg, orc, gated, gelu, m, d, ffn):
     y = _f32(y0)
     mlp.accumulate(_h16(x16), y, m)
     torch.cuda.synchronize()
-    want = y0 + _mlp_oracle(orc, x16, inp, m, d, ffn, gated, gelu)
-    assert _rel32(y.cpu().numpy(), want) <= f16_tol(ffn)
+    parts = {}
+    term = _mlp_oracle(orc, x16, inp, m, d, ffn, gated, gelu, parts)
+    _check_term(y.cpu().numpy(), y0, term, f16_tol(ffn), _down_moved(orc, inp, parts["hid"], m, d, ffn))
 
 
 def test_gated_linear_forward(smg, orc):
@@ -279,9 +305,20 @@ def _gpu_block(smg, inp, d, heads, kv_heads, hd, eps, theta):
     return smg.Block(smg.Norm.rms(inp["norm1"], eps), attn, smg.Norm.rms(inp["norm2"], eps), mlp)
 
 
-def _check_step(got_x, want_x, x0, parts, k_attn, k_mlp):
+def _check_step(orc, p, got_x, want_x, x0, parts, k_attn, k_mlp):
+    """Per element: the attention term's own tolerance, the MLP term's own
+    tolerance, and how far the attention half's error moves the MLP term --
+    measured by re-running the oracle's MLP half on the post-attention
+    residual shifted by the attention tolerance itself (seeded random signs),
+    since the MLP term is a function of that residual, not only a sum beside
+    it. Then the whole update within 1e-3 in relative norm."""
     err = np.abs(got_x.astype(np.float64) - want_x)
-    bound = f16_tol(k_attn) * (1 + np.abs(parts["attn"])) + f16_tol(k_mlp) * (1 + np.abs(parts["mlp"]))
+    tol_a = f16_tol(k_attn) * (1 + np.abs(parts["attn"]))
+    sign = np.where(np.random.default_rng(7).random(tol_a.size) < 0.5, -1.0, 1.0)
+    x1 = parts["x1"].astype(np.float64)
+    moved = orc.block_mlp_term((x1 + sign * tol_a).astype(np.float32), p)
+    prop = np.abs(moved.astype(np.float64) - parts["mlp"])
+    bound = tol_a + f16_tol(k_mlp) * (1 + np.abs(parts["mlp"])) + prop
     assert np.all(err <= bound), float(np.max(err / bound))
     upd_g, upd_w = got_x.astype(np.float64) - x0, want_x.astype(np.float64) - x0
     assert np.linalg.norm(upd_g - upd_w) <= 1e-3 * np.linalg.norm(upd_w)
@@ -305,7 +342,7 @@ def test_block_config5_decode_step(smg, orc):
     ck, cv = inp["cache_k"].copy(), inp["cache_v"].copy()
     parts = {}
     want = orc.block_decode(inp["x"], ck, cv, past, p, parts)
-    _check_step(x.cpu().numpy(), want, inp["x"], parts, H * hd, ffn)
+    _check_step(orc, p, x.cpu().numpy(), want, inp["x"], parts, H * hd, ffn)
     assert cache.len() == past + 1
     keys = _np16(cache.keys()).reshape(past + 1, KV * hd)
     vals = _np16(cache.values()).reshape(past + 1, KV * hd)
@@ -341,7 +378,7 @@ def test_block_decode_steps(smg, orc, theta):
         keys = _np16(cache.keys()).reshape(-1, KV * hd)
         ck[past + step] = keys[past + step]
         cv[past + step] = _np16(cache.values()).reshape(-1, KV * hd)[past + step]
-        _check_step(x.cpu().numpy(), want, x0, parts, H * hd, ffn)
+        _check_step(orc, p, x.cpu().numpy(), want, x0, parts, H * hd, ffn)
 
 
 def test_self_attention_accumulate(smg, orc):
@@ -363,14 +400,22 @@ def test_self_attention_accumulate(smg, orc):
     qkv = orc.matmul_q4_ep(x16, *inp["qkv"][:2], None, 1, inp["qkv"][2], d, 32)
     ql, kl = H * hd, KV * hd
     cs, sn = orc.rope_angles(orc.rope_inv_freq(hd, 10000.0), past)
-    q = orc.rope_apply(orc.f16_to_f32(qkv[:ql]), cs, sn)
-    k = orc.rope_apply(orc.f16_to_f32(qkv[ql:ql + kl]), cs, sn)
-    ck, cv = inp["cache_k"].copy(), inp["cache_v"].copy()
-    ck[past], cv[past] = orc.f32_to_f16(k), qkv[ql + kl:]
-    att = orc.attention_kv_f16(q, ck[:past + 1], cv[:past + 1], past + 1, H, KV, hd,
-                               np.float32(1) / np.sqrt(np.float32(hd)))
-    want = y0 + orc.f16_to_f32(orc.matmul_q4_ep(orc.f32_to_f16(att), *inp["out"][:2], None, 1, d, H * hd, 32))
-    assert _rel32(y.cpu().numpy(), want) <= f16_tol(H * hd)
+
+    def half(qkv16):
+        q = orc.rope_apply(orc.f16_to_f32(qkv16[:ql]), cs, sn)
+        k = orc.rope_apply(orc.f16_to_f32(qkv16[ql:ql + kl]), cs, sn)
+        ck, cv = inp["cache_k"].copy(), inp["cache_v"].copy()
+        ck[past], cv[past] = orc.f32_to_f16(k), qkv16[ql + kl:]
+        att = orc.attention_kv_f16(q, ck[:past + 1], cv[:past + 1], past + 1, H, KV, hd,
+                                   np.float32(1) / np.sqrt(np.float32(hd)))
+        return orc.f16_to_f32(orc.matmul_q4_ep(orc.f32_to_f16(att), *inp["out"][:2], None, 1, d, H * hd, 32))
+    term = half(qkv)
+    # the qkv projection is itself a GEMV held to f16_tol(d): how far the term
+    # moves when it moves by that tolerance (seeded random signs)
+    v = orc.f16_to_f32(qkv).astype(np.float64)
+    sign = np.where(np.random.default_rng(4).random(v.size) < 0.5, -1.0, 1.0)
+    moved = np.abs(half(orc.f32_to_f16((v + sign * f16_tol(d) * (1 + np.abs(v))).astype(np.float32))) - term)
+    _check_term(y.cpu().numpy(), y0, term, f16_tol(H * hd), moved)
     assert cache.len() == past + 1
 
 
