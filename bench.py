@@ -276,6 +276,16 @@ def main():
         del ta, tb, tc
     if "5" in only:
         extra["config5_decode_block"] = bench_block(smg, torch, timer, workloads, steps, warm, to_dev)
+        # each stage's bytes as one plain read (the floor a separate launch of
+        # that size meets), and the whole step's bytes as one read
+        c5 = workloads.CONFIG5
+        stages = workloads.block_stage_bytes(c5["d"], c5["heads"], c5["kv_heads"], c5["head_dim"], c5["ffn"],
+                                             c5["past"] + 1)
+        f5 = {k: stream_floor(smg, torch, timer, v, steps, warm) for k, v in stages.items()}
+        f5["whole_step"] = stream_floor(smg, torch, timer, extra["config5_decode_block"]["bytes_per_token"],
+                                        steps, warm)
+        f5["sum_of_stage_floors_us"] = sum(f5[k]["us"] for k in stages)
+        floors["config5"] = f5
 
     extra["floors"] = floors
     cpu = None

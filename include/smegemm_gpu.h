@@ -205,9 +205,12 @@ int gemm_gpu_f16f16_q1(size_t m, const smg_weights *w, uint16_t *dst, const uint
 /* The dense packed GEMM behind Gemm::new(&a, &packed, m)...run(&mut c) and
  * matmul_f16_packed: replaces gemm_sme_f16f16_run_packed
  * (csrc/sme_gemm_api.h:120-123). C[i,j] at dst[i*dst_rs + j*dst_cs];
- * A[i,l] at lhs[i*lhs_rs + l*lhs_cs]; dst = ep(beta * A@B) with read_dst == 0
- * (the only form the reference's callers use, src/exec/macros.rs:131-150);
- * alpha_bits is ignored under read_dst == 0. */
+ * A[i,l] at lhs[i*lhs_rs + l*lhs_cs]; dst = ep(beta * A@B) (read_dst == 0,
+ * the only form the reference's callers use, src/exec/macros.rs:131-150;
+ * alpha_bits is then ignored). read_dst != 0: with no op-graph,
+ * dst = T(alpha * dst + beta * A@B), one rounding (src/reference.rs:349-387);
+ * with a graph, dst = T(graph result + alpha * dst), the SME epilogue's order
+ * (csrc/epilogue.h:8-12). */
 int gemm_gpu_f16f16_run_packed(size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs,
                                long dst_rs, int read_dst, const uint16_t *lhs, long lhs_cs,
                                long lhs_rs, const smg_weights *b_pack, uint16_t alpha_bits,
@@ -216,6 +219,42 @@ int gemm_gpu_b16b16_run_packed(size_t m, size_t n, size_t k, uint16_t *dst, long
                                long dst_rs, int read_dst, const uint16_t *lhs, long lhs_cs,
                                long lhs_rs, const smg_weights *b_pack, uint16_t alpha_bits,
                                uint16_t beta_bits, const ep_desc16 *ep);
+/* Strided unpacked dense GEMM, C = alpha*C + beta*(A @ B) (gemm_f16 /
+ * matmul_f16, src/kernels/f16.rs:89-204; gemm_bf16 / matmul_bf16,
+ * src/kernels/bf16.rs:101-200): replace gemm_sme_f16f16_run
+ * (csrc/sme_gemm_api.h:116-119), gemm_sme_f16f32_run (:84-87),
+ * gemm_sme_b16b16_run (:70-73) and gemm_sme_bf16f32_run (:80-83). Host
+ * pointers; C[i,j] at dst[i*dst_rs + j*dst_cs], A[i,l] at
+ * lhs[i*lhs_rs + l*lhs_cs], B[l,j] at rhs[l*rhs_rs + j*rhs_cs]. Strides are
+ * non-negative; A and B may repeat cells (a zero stride), C's cells must be
+ * distinct with nested strides (dst_rs >= n*dst_cs or dst_cs >= m*dst_rs; a
+ * single row or column needs only a positive stride), else SMG_EINVAL -- its
+ * cells are written in parallel. C is read only when read_dst != 0; then
+ * dst = T(alpha * dst + beta * acc) with one rounding. All four accumulate in
+ * f32, as the portable path they fall back to (src/reference.rs:308-387).
+ * B is packed on the device for the call. */
+int gemm_gpu_f16f16_run(size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs, long dst_rs,
+                        int read_dst, const uint16_t *lhs, long lhs_cs, long lhs_rs,
+                        const uint16_t *rhs, long rhs_cs, long rhs_rs, uint16_t alpha_bits,
+                        uint16_t beta_bits);
+int gemm_gpu_f16f32_run(size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs, long dst_rs,
+                        int read_dst, const uint16_t *lhs, long lhs_cs, long lhs_rs,
+                        const uint16_t *rhs, long rhs_cs, long rhs_rs, uint16_t alpha_bits,
+                        uint16_t beta_bits);
+int gemm_gpu_b16b16_run(size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs, long dst_rs,
+                        int read_dst, const uint16_t *lhs, long lhs_cs, long lhs_rs,
+                        const uint16_t *rhs, long rhs_cs, long rhs_rs, uint16_t alpha_bits,
+                        uint16_t beta_bits);
+int gemm_gpu_bf16f32_run(size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs, long dst_rs,
+                         int read_dst, const uint16_t *lhs, long lhs_cs, long lhs_rs,
+                         const uint16_t *rhs, long rhs_cs, long rhs_rs, uint16_t alpha_bits,
+                         uint16_t beta_bits);
+/* The same on device pointers, enqueued on `stream` (bf16 != 0: bf16 operands);
+ * B is packed into a scratch buffer of the stream's own (grow-only, kept). */
+int smg_gemm_run_dev(int bf16, size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs, long dst_rs,
+                     int read_dst, const uint16_t *lhs, long lhs_cs, long lhs_rs, const uint16_t *rhs,
+                     long rhs_cs, long rhs_rs, uint16_t alpha_bits, uint16_t beta_bits, void *stream);
+
 /* Whether an m-row Q4 call runs the GEMV kernel (replaces
  * gemm_sme_f16f16_q4_single, csrc/sme_gemm_api.h:107). */
 int gemm_gpu_f16f16_q4_single(size_t m, size_t n, size_t k);

@@ -200,27 +200,38 @@ void or_q4_dequant_bf16(const uint8_t *quants, const uint16_t *scales, const uin
 /* col_major selects C[i,j] at c[i + j*m] (Gemm::col_major_output).          */
 /* ------------------------------------------------------------------------ */
 
-static void gemm16(int is_bf16, size_t m, size_t n, size_t k, uint16_t *c, const uint16_t *a,
-                   const uint16_t *b, uint16_t beta_bits, int col_major, float *acc) {
+/* gemm_f16 / gemm_bf16 (src/reference.rs:308-387): C = alpha*C + beta*(A@B),
+ * C[i,j] = c[i*c_rs + j*c_cs], A[i,l] = a[i*a_rs + l*a_cs], B[l,j] =
+ * b[l*b_rs + j*b_cs]; ikj order with one f32 accumulator per column, then
+ * prev = alpha == 0 ? 0 : alpha * C (C unread), C = T(prev + beta * acc).
+ * acc: scratch of n floats. */
+void or_gemm_strided(int is_bf16, size_t m, size_t n, size_t k, uint16_t *c, size_t c_rs, size_t c_cs,
+                     const uint16_t *a, size_t a_rs, size_t a_cs, const uint16_t *b, size_t b_rs,
+                     size_t b_cs, uint16_t alpha_bits, uint16_t beta_bits, float *acc) {
     float (*to32)(uint16_t) = is_bf16 ? or_bf16_to_f32 : or_f16_to_f32;
     uint16_t (*to16)(float) = is_bf16 ? or_f32_to_bf16 : or_f32_to_f16;
-    float beta = to32(beta_bits);
+    float alpha = to32(alpha_bits), beta = to32(beta_bits);
     for (size_t i = 0; i < m; i++) {
         for (size_t j = 0; j < n; j++) acc[j] = 0.0f;
         for (size_t l = 0; l < k; l++) {
-            float av = to32(a[i * k + l]);
-            const uint16_t *brow = b + l * n;
+            float av = to32(a[i * a_rs + l * a_cs]);
             for (size_t j = 0; j < n; j++) {
-                float p = av * to32(brow[j]);
+                float p = av * to32(b[l * b_rs + j * b_cs]);
                 acc[j] = acc[j] + p;
             }
         }
         for (size_t j = 0; j < n; j++) {
-            float v = 0.0f + beta * acc[j];
-            size_t idx = col_major ? (i + j * m) : (i * n + j);
-            c[idx] = to16(v);
+            uint16_t *cref = c + i * c_rs + j * c_cs;
+            float prev = alpha == 0.0f ? 0.0f : alpha * to32(*cref);
+            *cref = to16(prev + beta * acc[j]);
         }
     }
+}
+
+static void gemm16(int is_bf16, size_t m, size_t n, size_t k, uint16_t *c, const uint16_t *a,
+                   const uint16_t *b, uint16_t beta_bits, int col_major, float *acc) {
+    or_gemm_strided(is_bf16, m, n, k, c, col_major ? 1 : n, col_major ? m : 1, a, k, 1, b, n, 1, 0, beta_bits,
+                    acc);
 }
 
 /* acc: scratch of n floats */

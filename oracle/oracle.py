@@ -64,6 +64,9 @@ def lib() -> C.CDLL:
         L.or_q4_dequant_bf16.argtypes = [P, P, P, SZ, SZ, SZ, P]
         L.or_gemm_f16.argtypes = [SZ, SZ, SZ, P, P, P, C.c_uint16, C.c_int, P]
         L.or_gemm_bf16.argtypes = [SZ, SZ, SZ, P, P, P, C.c_uint16, C.c_int, P]
+        L.or_gemm_strided.argtypes = [C.c_int, SZ, SZ, SZ, P, SZ, SZ, P, SZ, SZ, P, SZ, SZ, C.c_uint16,
+                                      C.c_uint16, P]
+        L.or_gemm_strided.restype = None
         L.or_apply_ep.argtypes = [P, SZ, SZ, SZ, SZ, P, SZ, C.c_int, C.c_int]
         L.or_quantize_row.argtypes = [P, SZ, SZ, P, P]
         L.or_lowbit_reference.argtypes = [C.c_int, P, P, P, P, C.c_int, SZ, SZ, SZ, SZ, P, P, P]
@@ -197,6 +200,20 @@ def gemm16(a, b, m, n, k, beta_bits=None, col_major=False, bf16=False) -> np.nda
     acc = np.empty(max(n, 1), np.float32)
     fn = lib().or_gemm_bf16 if bf16 else lib().or_gemm_f16
     fn(m, n, k, _p(c), _p(a), _p(b), beta_bits, int(col_major), _p(acc))
+    return c
+
+
+def gemm_strided(c, c_rs, c_cs, a, a_rs, a_cs, b, b_rs, b_cs, m, n, k, alpha_bits, beta_bits,
+                 bf16=False) -> np.ndarray:
+    """reference::gemm_f16 / gemm_bf16 (src/reference.rs:308-387) in full:
+    C = alpha*C + beta*(A@B) over strided uint16 arrays (C is read only when
+    alpha != 0). Returns an updated copy of c."""
+    c = np.array(c, np.uint16, copy=True)
+    a = _c(a, np.uint16)
+    b = _c(b, np.uint16)
+    acc = np.empty(max(n, 1), np.float32)
+    lib().or_gemm_strided(int(bf16), m, n, k, _p(c), c_rs, c_cs, _p(a), a_rs, a_cs, _p(b), b_rs, b_cs,
+                          alpha_bits, beta_bits, _p(acc))
     return c
 
 

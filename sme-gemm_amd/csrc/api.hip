@@ -1075,23 +1075,24 @@ int gemm_gpu_f16f16_q1(size_t m, const smg_weights *w, uint16_t *dst, const uint
 
 static int packed_host(bool bf16, size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs,
                        long dst_rs, int read_dst, const uint16_t *lhs, long lhs_cs, long lhs_rs,
-                       const smg_weights *b, uint16_t beta_bits, const ep_desc16 *ep) {
+                       const smg_weights *b, uint16_t alpha_bits, uint16_t beta_bits,
+                       const ep_desc16 *ep) {
     int rc = check_kind(b, bf16 ? W_BF16 : W_F16);
     if (rc) return rc;
     if (b->d.n != n || b->d.k != k) return fail(SMG_EINVAL, "packed weights shape mismatch");
-    if (read_dst) return fail(SMG_EINVAL, "read_dst != 0 is not supported");
     if (m == 0 || n == 0) return SMG_OK;
     if (dst_cs <= 0 || dst_rs <= 0 || lhs_cs <= 0 || lhs_rs <= 0)
         return fail(SMG_EINVAL, "strides must be positive");
     const size_t dst_elems = (m - 1) * (size_t)dst_rs + (n - 1) * (size_t)dst_cs + 1;
     const size_t lhs_elems = k ? (m - 1) * (size_t)lhs_rs + (k - 1) * (size_t)lhs_cs + 1 : 0;
     const bool dense_out = (dst_cs == 1 && (size_t)dst_rs == n) || (dst_rs == 1 && (size_t)dst_cs == m);
-    const float beta = half_bits_to_float(beta_bits, bf16);
+    const float beta = half_bits_to_float(beta_bits, bf16), alpha = half_bits_to_float(alpha_bits, bf16);
     const WDev d = b->d;
     return host_call(bf16 ? "gemm_gpu_b16b16_run_packed" : "gemm_gpu_f16f16_run_packed", b->device,
-                     m, n, k, dst, dst_elems, !dense_out, lhs, lhs_elems, ep, 0,
+                     m, n, k, dst, dst_elems, !dense_out || read_dst, lhs, lhs_elems, ep, 0,
                      [&](uint16_t *dd, const uint16_t *dl, const EpArgs &ea, void *, hipStream_t s) {
-                         return launch_gemm(d, m, dd, dst_cs, dst_rs, dl, lhs_cs, lhs_rs, beta, ea, bf16, s);
+                         return launch_gemm(d, m, dd, dst_cs, dst_rs, dl, lhs_cs, lhs_rs, beta, ea, bf16, s,
+                                            read_dst != 0, alpha);
                      });
 }
 
@@ -1099,18 +1100,133 @@ int gemm_gpu_f16f16_run_packed(size_t m, size_t n, size_t k, uint16_t *dst, long
                                long dst_rs, int read_dst, const uint16_t *lhs, long lhs_cs,
                                long lhs_rs, const smg_weights *b_pack, uint16_t alpha_bits,
                                uint16_t beta_bits, const ep_desc16 *ep) {
-    (void)alpha_bits;
     return packed_host(false, m, n, k, dst, dst_cs, dst_rs, read_dst, lhs, lhs_cs, lhs_rs, b_pack,
-                       beta_bits, ep);
+                       alpha_bits, beta_bits, ep);
 }
 
 int gemm_gpu_b16b16_run_packed(size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs,
                                long dst_rs, int read_dst, const uint16_t *lhs, long lhs_cs,
                                long lhs_rs, const smg_weights *b_pack, uint16_t alpha_bits,
                                uint16_t beta_bits, const ep_desc16 *ep) {
-    (void)alpha_bits;
     return packed_host(true, m, n, k, dst, dst_cs, dst_rs, read_dst, lhs, lhs_cs, lhs_rs, b_pack,
-                       beta_bits, ep);
+                       alpha_bits, beta_bits, ep);
+}
+
+// ---- strided unpacked dense GEMM -------------------------------------------------
+// gemm_f16 / gemm_bf16 (src/kernels/f16.rs:126-204, bf16.rs:140-...): B packed
+// on the device into the dense layout (a strided gather through LDS), then the
+// dense GEMM with A's and C's strides and, under read_dst, alpha * C joined
+// before the one rounding. One implementation serves the four reference
+// entry points: the f16- and bf16-accumulating ones accumulate in f32 here,
+// as the portable path they fall back to does (src/reference.rs:308-387).
+
+// Operand views: A and B may repeat cells (a zero stride broadcasts), C's
+// cells must be distinct -- nested strides, one dimension's stride spanning
+// the other's whole extent -- since its cells are written in parallel.
+static bool read_strides_ok(long rs, long cs) { return rs >= 0 && cs >= 0; }
+static bool write_strides_ok(size_t rows, long rs, size_t cols, long cs) {
+    if (rs < 0 || cs < 0) return false;
+    if (rows > 1 && rs == 0) return false;
+    if (cols > 1 && cs == 0) return false;
+    return rows <= 1 || cols <= 1 || (size_t)rs >= (size_t)cs * cols || (size_t)cs >= (size_t)rs * rows;
+}
+static size_t footprint(size_t rows, long rs, size_t cols, long cs) {
+    return rows && cols ? (rows - 1) * (size_t)rs + (cols - 1) * (size_t)cs + 1 : 0;
+}
+
+static int run_host(bool bf16, const char *name, size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs,
+                    long dst_rs, int read_dst, const uint16_t *lhs, long lhs_cs, long lhs_rs,
+                    const uint16_t *rhs, long rhs_cs, long rhs_rs, uint16_t alpha_bits, uint16_t beta_bits) {
+    if (m == 0 || n == 0) return SMG_OK;
+    if (!dst || (k && (!lhs || !rhs))) return fail(SMG_EINVAL, "null operand");
+    if (!write_strides_ok(m, dst_rs, n, dst_cs) || !read_strides_ok(lhs_rs, lhs_cs) ||
+        !read_strides_ok(rhs_rs, rhs_cs))
+        return fail(SMG_EINVAL, "strides must be non-negative and C's cells distinct");
+    if (!smg_available()) return fail(SMG_ENODEV, "no gfx950 device");
+    int device = 0;
+    HIP_TRY(hipGetDevice(&device), SMG_EHIP);
+    WDev d = {};
+    d.kind = bf16 ? W_BF16 : W_F16;
+    d.n = n;
+    d.k = k;
+    d.n_pad = round_up(n, 128);
+    d.k_pad = round_up(k ? k : 1, 64);
+    const size_t rhs_elems = footprint(k, rhs_rs, n, rhs_cs);
+    const size_t dense_bytes = round_up(d.n_pad * d.k_pad * 2, 256);
+    const size_t dst_elems = footprint(m, dst_rs, n, dst_cs);
+    const bool dense_out = (dst_cs == 1 && (size_t)dst_rs == n) || (dst_rs == 1 && (size_t)dst_cs == m);
+    const float alpha = half_bits_to_float(alpha_bits, bf16), beta = half_bits_to_float(beta_bits, bf16);
+    return host_call(name, device, m, n, k, dst, dst_elems, !dense_out || read_dst, lhs, footprint(m, lhs_rs, k, lhs_cs),
+                     nullptr, dense_bytes + rhs_elems * 2,
+                     [&](uint16_t *dd, const uint16_t *dl, const EpArgs &ea, void *sc, hipStream_t s) {
+                         uint16_t *dense = (uint16_t *)sc, *raw = (uint16_t *)((uint8_t *)sc + dense_bytes);
+                         if (rhs_elems) {
+                             const hipError_t e = hipMemcpyAsync(raw, rhs, rhs_elems * 2, hipMemcpyHostToDevice, s);
+                             if (e != hipSuccess) return e;
+                         }
+                         hipError_t e = launch_pack_dense_strided(raw, rhs_rs, rhs_cs, n, k, d.n_pad, d.k_pad,
+                                                                  dense, s);
+                         if (e != hipSuccess) return e;
+                         WDev w = d;
+                         w.dense = dense;
+                         return launch_gemm(w, m, dd, dst_cs, dst_rs, dl, lhs_cs, lhs_rs, beta, ea, bf16, s,
+                                            read_dst != 0, alpha);
+                     });
+}
+
+int gemm_gpu_f16f16_run(size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs, long dst_rs, int read_dst,
+                        const uint16_t *lhs, long lhs_cs, long lhs_rs, const uint16_t *rhs, long rhs_cs,
+                        long rhs_rs, uint16_t alpha_bits, uint16_t beta_bits) {
+    return run_host(false, "gemm_gpu_f16f16_run", m, n, k, dst, dst_cs, dst_rs, read_dst, lhs, lhs_cs, lhs_rs,
+                    rhs, rhs_cs, rhs_rs, alpha_bits, beta_bits);
+}
+int gemm_gpu_f16f32_run(size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs, long dst_rs, int read_dst,
+                        const uint16_t *lhs, long lhs_cs, long lhs_rs, const uint16_t *rhs, long rhs_cs,
+                        long rhs_rs, uint16_t alpha_bits, uint16_t beta_bits) {
+    return run_host(false, "gemm_gpu_f16f32_run", m, n, k, dst, dst_cs, dst_rs, read_dst, lhs, lhs_cs, lhs_rs,
+                    rhs, rhs_cs, rhs_rs, alpha_bits, beta_bits);
+}
+int gemm_gpu_b16b16_run(size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs, long dst_rs, int read_dst,
+                        const uint16_t *lhs, long lhs_cs, long lhs_rs, const uint16_t *rhs, long rhs_cs,
+                        long rhs_rs, uint16_t alpha_bits, uint16_t beta_bits) {
+    return run_host(true, "gemm_gpu_b16b16_run", m, n, k, dst, dst_cs, dst_rs, read_dst, lhs, lhs_cs, lhs_rs,
+                    rhs, rhs_cs, rhs_rs, alpha_bits, beta_bits);
+}
+int gemm_gpu_bf16f32_run(size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs, long dst_rs, int read_dst,
+                         const uint16_t *lhs, long lhs_cs, long lhs_rs, const uint16_t *rhs, long rhs_cs,
+                         long rhs_rs, uint16_t alpha_bits, uint16_t beta_bits) {
+    return run_host(true, "gemm_gpu_bf16f32_run", m, n, k, dst, dst_cs, dst_rs, read_dst, lhs, lhs_cs, lhs_rs,
+                    rhs, rhs_cs, rhs_rs, alpha_bits, beta_bits);
+}
+
+int smg_gemm_run_dev(int bf16, size_t m, size_t n, size_t k, uint16_t *dst, long dst_cs, long dst_rs,
+                     int read_dst, const uint16_t *lhs, long lhs_cs, long lhs_rs, const uint16_t *rhs,
+                     long rhs_cs, long rhs_rs, uint16_t alpha_bits, uint16_t beta_bits, void *stream) {
+    if (m == 0 || n == 0) return SMG_OK;
+    if (!dst || (k && (!lhs || !rhs))) return fail(SMG_EINVAL, "null operand");
+    if (!write_strides_ok(m, dst_rs, n, dst_cs) || !read_strides_ok(lhs_rs, lhs_cs) ||
+        !read_strides_ok(rhs_rs, rhs_cs))
+        return fail(SMG_EINVAL, "strides must be non-negative and C's cells distinct");
+    int device = 0;
+    HIP_TRY(hipGetDevice(&device), SMG_EHIP);
+    WDev d = {};
+    d.kind = bf16 ? W_BF16 : W_F16;
+    d.n = n;
+    d.k = k;
+    d.n_pad = round_up(n, 128);
+    d.k_pad = round_up(k ? k : 1, 64);
+    uint16_t *dense = (uint16_t *)dev_pool().get(device, stream, d.n_pad * d.k_pad * 2);
+    if (!dense) return fail(SMG_ENOMEM, "smg_gemm_run_dev: scratch hipMalloc");
+    hipError_t e = launch_pack_dense_strided(rhs, rhs_rs, rhs_cs, n, k, d.n_pad, d.k_pad, dense,
+                                             (hipStream_t)stream);
+    if (e == hipSuccess) {
+        d.dense = dense;
+        EpArgs ea = {};
+        const bool b = bf16 != 0;
+        e = launch_gemm(d, m, dst, dst_cs, dst_rs, lhs, lhs_cs, lhs_rs, half_bits_to_float(beta_bits, b), ea, b,
+                        (hipStream_t)stream, read_dst != 0, half_bits_to_float(alpha_bits, b));
+    }
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_gemm_run_dev", e);
 }
 
 // The reference's chained link (csrc/gemm_f16f16_q4.h:541-549) with host

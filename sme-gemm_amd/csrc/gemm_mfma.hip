@@ -49,6 +49,8 @@ struct GemmArgs {
     uint32_t block_shift;
     uint32_t codebook;
     float beta;
+    float alpha;         // read_dst: C = alpha * C + beta * A@B
+    uint32_t read_dst;
     uint32_t lhs_bytes;  // byte footprint of A (the buffer resource's range)
 };
 
@@ -317,17 +319,25 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const EpArgs &ep, 
     // Round beta*acc to 16 bits into LDS (the loop's last barrier freed it); a
     // lane holds D[4*(lane/16)+v][lane%16] of each 16x16 MFMA tile. The LDS
     // holds BM * CS halfs of tile plus the operand vectors (EPI_LDS_HALFS).
+    // With read_dst and no op-graph the old C joins before the one rounding,
+    // alpha * C + beta * acc in f32 (src/reference.rs:349-387); with a graph
+    // it is added after the graph (ep_store8).
     constexpr int CS = BN + 8;  // halfs per staged row
+    const bool rd_here = g.read_dst && ep.n_nodes == 0;
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int jt = 0; jt < 4; jt++)
 #pragma unroll
-            for (int v = 0; v < 4; v++)
-                lds[(wm * 64 + i * 16 + (lane / 16) * 4 + v) * CS + wn * 64 + jt * 16 + lr] =
-                    from_f32<BF16>(0.0f + g.beta * acc[i][jt][v]);
+            for (int v = 0; v < 4; v++) {
+                const int rl = wm * 64 + i * 16 + (lane / 16) * 4 + v, cl = wn * 64 + jt * 16 + lr;
+                float prev = 0.0f;
+                if (rd_here && row0 + rl < g.m && col0 + cl < g.n)
+                    prev = g.alpha * to_f32<BF16>(g.dst[(size_t)(row0 + rl) * g.dst_rs + (size_t)(col0 + cl) * g.dst_cs]);
+                lds[rl * CS + cl] = from_f32<BF16>(prev + g.beta * acc[i][jt][v]);
+            }
     __syncthreads();
-    const StoreArgs sa = {g.dst, g.dst_rs, g.dst_cs, g.m, g.n};
+    const StoreArgs sa = {g.dst, g.dst_rs, g.dst_cs, g.m, g.n, g.alpha, g.read_dst && ep.n_nodes != 0};
     float *colv = (float *)(lds + BM * CS);      // [node][BN]
     float *rowv = colv + SMG_MAX_EP_NODES * BN;  // [node][BM]
     ep_load_vectors<BF16, BM, BN, BM * 2>(sa, ep, colv, rowv, row0, col0);
@@ -472,8 +482,9 @@ hipError_t launch_shape(const GemmArgs &g, const EpArgs &ep, bool vec_a, hipStre
 
 hipError_t launch_gemm(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,
                        const uint16_t *lhs, long lhs_cs, long lhs_rs, float beta,
-                       const EpArgs &ep, bool bf16, hipStream_t s) {
-    if (q4r_supported(w, m, lhs_cs, lhs_rs, lhs, bf16))
+                       const EpArgs &ep, bool bf16, hipStream_t s, bool read_dst, float alpha) {
+    if (read_dst && w.kind != W_F16 && w.kind != W_BF16) return hipErrorInvalidValue;
+    if (!read_dst && q4r_supported(w, m, lhs_cs, lhs_rs, lhs, bf16))
         return launch_q4r(w, m, dst, dst_cs, dst_rs, lhs, lhs_rs, beta, ep, s);
     GemmArgs g = {};
     g.lhs = lhs;
@@ -496,6 +507,8 @@ hipError_t launch_gemm(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long
     g.block_shift = w.block ? (uint32_t)__builtin_ctzll(w.block) : 0;
     g.codebook = w.codebook;
     g.beta = beta;
+    g.alpha = alpha;
+    g.read_dst = read_dst ? 1u : 0u;
     const size_t fp = (m && w.k) ? ((m - 1) * (size_t)lhs_rs + (w.k - 1) * (size_t)lhs_cs + 1) * 2 : 0;
     if (fp >= ((size_t)1 << 31)) return hipErrorInvalidValue;  // one buffer resource spans < 2 GiB
     g.lhs_bytes = (uint32_t)fp;
@@ -511,6 +524,39 @@ hipError_t launch_gemm(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long
     case W_BF16: return launch_shape<W_BF16, true, false>(g, ep, vec_a, s);
     default: return hipErrorInvalidValue;
     }
+}
+
+// A strided k x n B into the dense layout, 32 x 32 blocks through LDS: the
+// reads run along whichever of B's two strides is 1 when the block's threads
+// walk j (a row-major B) and the writes along the dense column's K.
+namespace {
+__global__ void __launch_bounds__(256) pack_dense_strided(const uint16_t *rhs, long rhs_rs, long rhs_cs,
+                                                          uint32_t n, uint32_t k, uint32_t k_pad,
+                                                          uint16_t *dense) {
+    __shared__ uint16_t tile[32][33];
+    const uint32_t l0 = blockIdx.x * 32, j0 = blockIdx.y * 32;
+    const uint32_t tx = threadIdx.x % 32, ty = threadIdx.x / 32;  // 32 x 8
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint32_t l = l0 + ty + 8 * r, j = j0 + tx;
+        tile[ty + 8 * r][tx] = (l < k && j < n) ? rhs[(long)l * rhs_rs + (long)j * rhs_cs] : (uint16_t)0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint32_t j = j0 + ty + 8 * r, l = l0 + tx;
+        if (l < k_pad) dense[(size_t)j * k_pad + l] = tile[tx][ty + 8 * r];
+    }
+}
+}  // namespace
+
+hipError_t launch_pack_dense_strided(const uint16_t *rhs, long rhs_rs, long rhs_cs, size_t n, size_t k,
+                                     size_t n_pad, size_t k_pad, uint16_t *dense, hipStream_t s) {
+    if (n_pad % 32 || k_pad % 32 || n > n_pad || k > k_pad) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(k_pad / 32), (unsigned)(n_pad / 32));
+    hipLaunchKernelGGL(pack_dense_strided, grid, dim3(256), 0, s, rhs, rhs_rs, rhs_cs, (uint32_t)n, (uint32_t)k,
+                       (uint32_t)k_pad, dense);
+    return hipGetLastError();
 }
 
 // Eager dequant of Q4 weights to the dense layout ([n_pad][k_pad], column's K

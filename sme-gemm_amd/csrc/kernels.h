@@ -61,7 +61,12 @@ hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint
 // or dense), C[i,j] at dst[i*rs + j*cs] = ep(to16(beta * acc)).
 hipError_t launch_gemm(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,
                        const uint16_t *lhs, long lhs_cs, long lhs_rs, float beta,
-                       const EpArgs &ep, bool bf16, hipStream_t s);
+                       const EpArgs &ep, bool bf16, hipStream_t s, bool read_dst = false,
+                       float alpha = 0.0f);
+// Dense F16/BF16 weights ([n_pad][k_pad], column j's K contiguous, zero
+// padded) from a k x n matrix B[l][j] = rhs[l*rhs_rs + j*rhs_cs].
+hipError_t launch_pack_dense_strided(const uint16_t *rhs, long rhs_rs, long rhs_cs, size_t n, size_t k,
+                                     size_t n_pad, size_t k_pad, uint16_t *dense, hipStream_t s);
 
 // Q4 x f16 GEMM with register-resident weights (gemm_q4r.hip): f16, block >=
 // 32, K a multiple of 64, row-major 16-byte-aligned A. launch_gemm uses it

@@ -14,6 +14,8 @@ struct StoreArgs {
     uint16_t *dst;
     long dst_rs, dst_cs;
     uint32_t m, n;
+    float alpha;        // add_dst: C = T(graph result + alpha * old C)
+    uint32_t add_dst;   // the SME epilogue's last step (csrc/epilogue.h:8-12)
 };
 
 // ROW / COL operand vectors of the graph, read once per tile into LDS as f32
@@ -91,6 +93,17 @@ __device__ __forceinline__ void ep_store8(const StoreArgs &g, const EpArgs &ep, 
         c8 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
     }
     uint16_t *dp = g.dst + (size_t)row * g.dst_rs + (size_t)col * g.dst_cs;
+    if (g.add_dst) {
+        uint32_t w4[4] = {c8.x, c8.y, c8.z, c8.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            if ((uint32_t)e >= ne) break;
+            const float x = to_f32<BF16>((uint16_t)(w4[e / 2] >> (16 * (e % 2))));
+            const uint16_t y = from_f32<BF16>(x + g.alpha * to_f32<BF16>(dp[(size_t)e * g.dst_cs]));
+            w4[e / 2] = (w4[e / 2] & (0xFFFF0000u >> (16 * (e % 2)))) | ((uint32_t)y << (16 * (e % 2)));
+        }
+        c8 = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    }
     if (g.dst_cs == 1 && ne == 8 && ((uintptr_t)dp & 15) == 0) {
         *(uint4 *)dp = c8;
         return;

@@ -95,6 +95,11 @@ def lib() -> C.CDLL:
     L.smg_lowbit_mopa_dev.argtypes = [SZ, P, P, P, P, P]
     L.smg_packed_matmul_dev.argtypes = [SZ, P, P, C.c_long, C.c_long, P, C.c_long, C.c_long,
                                         C.c_uint16, P, C.c_int, P]
+    for name in ("gemm_gpu_f16f16_run", "gemm_gpu_f16f32_run", "gemm_gpu_b16b16_run", "gemm_gpu_bf16f32_run"):
+        getattr(L, name).argtypes = [SZ, SZ, SZ, P, C.c_long, C.c_long, C.c_int, P, C.c_long, C.c_long,
+                                     P, C.c_long, C.c_long, C.c_uint16, C.c_uint16]
+    L.smg_gemm_run_dev.argtypes = [C.c_int, SZ, SZ, SZ, P, C.c_long, C.c_long, C.c_int, P, C.c_long,
+                                   C.c_long, P, C.c_long, C.c_long, C.c_uint16, C.c_uint16, P]
     L.smg_ep_check.argtypes = [P, SZ]
     L.smg_q4_interleave.argtypes = [P, P, W]
     # the decode block
@@ -301,8 +306,13 @@ class Epilogue:
     def div_tensor(self, t, ld=0): return self._vec(18, t, ld)
     def max_tensor(self, t, ld=0): return self._vec(21, t, ld)
     def min_tensor(self, t, ld=0): return self._vec(24, t, ld)
+    # *_tensor_strided (graph.rs / builder.rs:634-670): the ld argument above
     add_tensor_strided = add_tensor
     mul_tensor_strided = mul_tensor
+    sub_tensor_strided = sub_tensor
+    div_tensor_strided = div_tensor
+    max_tensor_strided = max_tensor
+    min_tensor_strided = min_tensor
 
     # trailing activations (graph.rs:193-223)
     def relu(self): self.act = 1; return self
@@ -942,6 +952,97 @@ def matmul_f16_packed(a, packed: Packed, c, m: int):
 
 def matmul_bf16_packed(a, packed: Packed, c, m: int):
     return Gemm(a, packed, m).run(c)
+
+
+class Accum:
+    """Accum (src/element.rs:19-27): the accumulation the reference's SME
+    kernels use. On this device every choice accumulates in f32, as the
+    portable path those kernels fall back to (src/reference.rs:308-387)."""
+    F32 = 0
+    F16 = 1
+    Bf16 = 2
+
+
+def _check_strided(what, length, d0, rs, d1, cs):
+    """check_strided (src/exec/guard.rs:49-60)."""
+    if d0 == 0 or d1 == 0:
+        return
+    if min(rs, cs) < 0 or (d0 - 1) * rs + (d1 - 1) * cs >= length:
+        raise ValueError(f"{what}: {d0}x{d1} view at strides {rs}/{cs} overflows the slice (len {length})")
+
+
+def _bits16(v, bf16):
+    if isinstance(v, (np.uint16,)) or (isinstance(v, int) and not isinstance(v, bool)):
+        return int(v)
+    if bf16:
+        return int(np.float32(_bf16_round(v)).view(np.uint32)) >> 16
+    return int(np.float16(v).view(np.uint16))
+
+
+def _gemm_strided(bf16, m, n, k, c, c_rs, c_cs, a, a_rs, a_cs, b, b_rs, b_cs, alpha, beta, accum):
+    if m == 0 or n == 0:
+        return c
+    ab, bb = _bits16(alpha, bf16), _bits16(beta, bf16)
+    read_dst = int((ab & 0x7FFF) != 0)  # alpha != 0 (+0 and -0 are zero; NaN is not)
+    if _is_dev(c):
+        dev = c.device.index
+        for t, name in ((c, "c"), (a, "a"), (b, "b")):
+            if not _is_dev(t):
+                raise TypeError(f"{name}: every operand on the device, or every one on the host")
+            _dev16(t, None, name, dev, bf16)
+        _check_strided("c", c.numel(), m, c_rs, n, c_cs)
+        _check_strided("a", a.numel(), m, a_rs, k, a_cs)
+        _check_strided("b", b.numel(), k, b_rs, n, b_cs)
+        _check(lib().smg_gemm_run_dev(int(bf16), m, n, k, c.data_ptr(), c_cs, c_rs, read_dst, a.data_ptr(), a_cs,
+                                      a_rs, b.data_ptr(), b_cs, b_rs, ab, bb, _stream()), "smg_gemm_run_dev")
+        return c
+    cc = np.asarray(c)
+    if cc.dtype not in (np.uint16, np.float16) or not cc.flags.c_contiguous:
+        raise TypeError("c: a contiguous uint16/float16 array (updated in place)")
+    av, bv = np.ascontiguousarray(a).view(np.uint16).ravel(), np.ascontiguousarray(b).view(np.uint16).ravel()
+    _check_strided("c", cc.size, m, c_rs, n, c_cs)
+    _check_strided("a", av.size, m, a_rs, k, a_cs)
+    _check_strided("b", bv.size, k, b_rs, n, b_cs)
+    _require_device()
+    if bf16:
+        fn = lib().gemm_gpu_b16b16_run if accum == Accum.Bf16 else lib().gemm_gpu_bf16f32_run
+    else:
+        fn = lib().gemm_gpu_f16f16_run if accum == Accum.F16 else lib().gemm_gpu_f16f32_run
+    _check(fn(m, n, k, cc.ctypes.data, c_cs, c_rs, read_dst, av.ctypes.data, a_cs, a_rs, bv.ctypes.data, b_cs,
+              b_rs, ab, bb), "gemm run")
+    return c
+
+
+def gemm_f16(m, n, k, c, c_row_stride, c_col_stride, a, a_row_stride, a_col_stride, b, b_row_stride,
+             b_col_stride, alpha, beta, accum=Accum.F32):
+    """gemm_f16 (src/kernels/f16.rs:126-204): C = alpha*C + beta*(A @ B) over
+    strided f16 views (host arrays, C updated in place; or device tensors);
+    C is read only when alpha != 0."""
+    return _gemm_strided(False, m, n, k, c, c_row_stride, c_col_stride, a, a_row_stride, a_col_stride, b,
+                         b_row_stride, b_col_stride, alpha, beta, accum)
+
+
+def gemm_bf16(m, n, k, c, c_row_stride, c_col_stride, a, a_row_stride, a_col_stride, b, b_row_stride,
+              b_col_stride, alpha, beta, accum=Accum.F32):
+    """gemm_bf16 (src/kernels/bf16.rs:140-200)."""
+    return _gemm_strided(True, m, n, k, c, c_row_stride, c_col_stride, a, a_row_stride, a_col_stride, b,
+                         b_row_stride, b_col_stride, alpha, beta, accum)
+
+
+def matmul_f16(a, b, c, m, n, k, accum=Accum.F32):
+    """matmul_f16 (src/kernels/f16.rs:89-111): row-major C = A @ B."""
+    for t, sz, name in ((a, m * k, "a is m*k"), (b, k * n, "b is k*n"), (c, m * n, "c is m*n")):
+        if (t.numel() if _is_dev(t) else np.asarray(t).size) != sz:
+            raise ValueError(name)
+    return gemm_f16(m, n, k, c, n, 1, a, k, 1, b, n, 1, 0, 0x3C00, accum)
+
+
+def matmul_bf16(a, b, c, m, n, k, accum=Accum.F32):
+    """matmul_bf16 (src/kernels/bf16.rs:101-137)."""
+    for t, sz, name in ((a, m * k, "a is m*k"), (b, k * n, "b is k*n"), (c, m * n, "c is m*n")):
+        if (t.numel() if _is_dev(t) else np.asarray(t).size) != sz:
+            raise ValueError(name)
+    return gemm_bf16(m, n, k, c, n, 1, a, k, 1, b, n, 1, 0, 0x3F80, accum)
 
 
 # ---- the model-level parts: Linear, GatedLinear, Mlp, KvCache, SelfAttention,

@@ -112,6 +112,14 @@ def block_inputs(d: int, heads: int, kv_heads: int, head_dim: int, ffn: int, pas
     return out
 
 
+def block_stage_bytes(d, heads, kv_heads, head_dim, ffn, kv_len, block=32):
+    """block_bytes split by the decode step's HBM-reading stages: each Q4
+    projection's codes and scales, and the cached keys and values."""
+    q4 = lambda n, k: n * k // 2 + n * (-(-k // block)) * 2  # noqa: E731
+    return {"qkv": q4((heads + 2 * kv_heads) * head_dim, d), "kv_cache": 2 * 2 * kv_len * kv_heads * head_dim,
+            "out": q4(d, heads * head_dim), "gate_up": q4(2 * ffn, d), "down": q4(d, ffn)}
+
+
 def block_bytes(d, heads, kv_heads, head_dim, ffn, kv_len, block=32):
     """Algorithmic HBM bytes of one decode step: every Q4 weight (0.5 B) and
     its f16 scale (2 B per 32-block), and the f16 keys and values read."""

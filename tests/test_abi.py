@@ -228,3 +228,26 @@ def test_scalar_operands_round_through_the_element_type():
     assert e.nodes[0][2] == float(np.float16(0.1))
     e = smg.Epilogue(bf16=True).add_scalar(0.1)
     assert e.nodes[0][2] == float(np.float32(0.10009765625))
+
+
+def test_strided_gemm_refuses_bad_views(lib):
+    """gemm_gpu_*_run check strides before touching a device: C's cells must
+    be distinct (a zero or overlapping stride would race), no stride is
+    negative (SMG_EINVAL, -1); an empty output returns at once. The mirror raises ValueError
+    for a view past its slice, as check_strided panics (guard.rs:49-60)."""
+    import smegemm as smg
+    SZ = C.c_size_t
+    for name in ("gemm_gpu_f16f16_run", "gemm_gpu_f16f32_run", "gemm_gpu_b16b16_run", "gemm_gpu_bf16f32_run"):
+        fn = getattr(lib, name)
+        fn.argtypes = [SZ, SZ, SZ, C.c_void_p, C.c_long, C.c_long, C.c_int, C.c_void_p, C.c_long, C.c_long,
+                       C.c_void_p, C.c_long, C.c_long, C.c_uint16, C.c_uint16]
+        buf = np.zeros(64, np.uint16)
+        p = buf.ctypes.data
+        assert fn(0, 4, 4, p, 1, 4, 0, p, 1, 4, p, 1, 4, 0, 0x3C00) == 0
+        # C rows overlapping (row stride 2 for 4 columns), a zero column stride, a negative stride
+        for dcs, drs in ((1, 2), (0, 4), (-1, 4)):
+            assert fn(3, 4, 2, p, dcs, drs, 0, p, 1, 2, p, 1, 4, 0, 0x3C00) == -1, (name, dcs, drs)
+        assert fn(3, 4, 2, p, 1, 4, 0, p, -1, 2, p, 1, 4, 0, 0x3C00) == -1  # SMG_EINVAL
+    with pytest.raises(ValueError, match="overflows"):
+        smg.gemm_f16(3, 4, 2, np.zeros(12, np.uint16), 4, 1, np.zeros(5, np.uint16), 2, 1,
+                     np.zeros(8, np.uint16), 4, 1, 0.0, 1.0)

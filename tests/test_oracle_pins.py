@@ -195,6 +195,77 @@ def test_gemm16_closed_forms():
     assert np.array_equal(rm, cm.T)
 
 
+def _strided_layout(x, rows, cols, layout, rng):
+    """x (rows x cols, row-major uint16) laid out row-major, column-major or
+    row-major with padded rows: (buffer, row stride, col stride). Padding
+    cells hold NaN bits so a read of one shows in the result."""
+    x = np.asarray(x, np.uint16).reshape(rows, cols)
+    if layout == "row":
+        return x.ravel().copy(), cols, 1
+    if layout == "col":
+        return x.T.ravel().copy(), 1, rows
+    ld = cols + 3
+    buf = np.full(rows * ld, 0x7E00, np.uint16)
+    buf.reshape(rows, ld)[:, :cols] = x
+    return buf, ld, 1
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("la,lb,lc", [("row", "row", "row"), ("col", "col", "col"), ("pad", "col", "pad"),
+                                      ("row", "pad", "col")])
+def test_gemm_strided_pins(bf16, la, lb, lc):
+    """or_gemm_strided against an independent numpy restatement on
+    materialized row-major operands (f32 K-order accumulator, then
+    alpha * C + beta * acc rounded once): layout-independent, alpha = 0 never
+    reads C (NaN there does not show), C's padding cells are left alone."""
+    m, n, k = 6, 9, 13
+    rng = np.random.default_rng(hash((bf16, la, lb, lc)) % 2**32)
+    cv = O.f32_to_bf16 if bf16 else O.f32_to_f16
+    to32 = O.bf16_to_f32 if bf16 else O.f16_to_f32
+    a = cv(rng.standard_normal(m * k).astype(np.float32))
+    b = cv(rng.standard_normal(k * n).astype(np.float32))
+    c0 = cv(rng.standard_normal(m * n).astype(np.float32))
+    A, B, C0 = (to32(v).reshape(r, q) for v, r, q in ((a, m, k), (b, k, n), (c0, m, n)))
+    for alpha, beta in ((0.0, 1.0), (0.5, -2.0), (1.0, 0.25)):
+        ab, bb = int(cv(np.float32(alpha))[0]), int(cv(np.float32(beta))[0])
+        acc = np.zeros((m, n), np.float32)
+        for l in range(k):
+            acc = acc + A[:, l:l + 1] * B[l]
+        prev = np.float32(alpha) * C0 if alpha != 0.0 else np.zeros((m, n), np.float32)
+        want = cv((prev + np.float32(beta) * acc).ravel())
+        abuf, ars, acs = _strided_layout(a, m, k, la, rng)
+        bbuf, brs, bcs = _strided_layout(b, k, n, lb, rng)
+        cin = c0 if alpha != 0.0 else np.full(m * n, 0x7E00, np.uint16)
+        cbuf, crs, ccs = _strided_layout(cin, m, n, lc, rng)
+        got = O.gemm_strided(cbuf, crs, ccs, abuf, ars, acs, bbuf, brs, bcs, m, n, k, ab, bb, bf16)
+        cells = np.array([[got[i * crs + j * ccs] for j in range(n)] for i in range(m)]).ravel()
+        assert np.array_equal(cells, want), (alpha, beta)
+        if lc == "pad":
+            assert np.all(got.reshape(m, crs)[:, n:] == 0x7E00)
+
+
+def test_gemm_strided_closed_forms():
+    """k = 0 leaves T(alpha * C) (an empty sum); alpha = 1, beta = 0 keeps C
+    exactly; all-ones A over small-integer B gives exact column sums."""
+    m, n = 4, 7
+    rng = np.random.default_rng(8)
+    c0 = O.f32_to_f16(rng.standard_normal(m * n).astype(np.float32))
+    half = int(O.f32_to_f16(np.float32(0.5))[0])
+    got = O.gemm_strided(c0, n, 1, np.zeros(0, np.uint16), 0, 1, np.zeros(0, np.uint16), n, 1, m, n, 0,
+                         half, 0x3C00)
+    assert np.array_equal(got, O.f32_to_f16(np.float32(0.5) * O.f16_to_f32(c0)))
+    k = 11
+    a = O.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    b = O.f32_to_f16(rng.standard_normal(k * n).astype(np.float32))
+    assert np.array_equal(O.gemm_strided(c0, n, 1, a, k, 1, b, n, 1, m, n, k, 0x3C00, 0), c0)
+    bi = rng.integers(-4, 5, k * n)
+    ones = np.full(m * k, 0x3C00, np.uint16)
+    got = O.gemm_strided(np.zeros(m * n, np.uint16), n, 1, ones, k, 1, bi.astype(np.float16).view(np.uint16),
+                         n, 1, m, n, k, 0, 0x3C00)
+    assert np.array_equal(got.view(np.float16).astype(np.int64).reshape(m, n),
+                          np.tile(bi.reshape(k, n).sum(0), (m, 1)))
+
+
 # ---- epilogue ----------------------------------------------------------------------
 
 def _maxnum(x, y):
