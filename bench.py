@@ -286,6 +286,7 @@ def main():
                                         steps, warm)
         f5["sum_of_stage_floors_us"] = sum(f5[k]["us"] for k in stages)
         floors["config5"] = f5
+        extra["config5_mlp"] = bench_mlp(smg, torch, timer, workloads, steps, warm)
 
     extra["floors"] = floors
     cpu = None
@@ -356,6 +357,49 @@ def bench_block(smg, torch, timer, workloads, steps, warm, to_dev):
             "us_per_token_hot_mall": us_hot, "GBps": nbytes / (us * 1e-6) / 1e9,
             "roofline_tokens_per_s": HBM_PEAK_GBS * 1e9 / nbytes,
             "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "launches_per_token": 6}
+
+
+def bench_mlp(smg, torch, timer, workloads, steps, warm):
+    """Config 5's MLP on one row (d 4096, SwiGLU 14336, Q4 block 32):
+    Mlp::accumulate as this library runs it -- the gate/up GEMV with glu at
+    its store, then the down GEMV adding into the f32 row, two launches in
+    stream order (the GPU form of Mlp::chained, src/mlp.rs:151-234) --
+    against the same work as plain calls: the 2n-column GEMV to f16, the glu
+    pass, the down GEMV to f16 and the add, four launches whose intermediates
+    round-trip through memory. Four weight copies cycle (99 MB each)."""
+    import numpy as np
+    c = workloads.CONFIG5
+    d, ffn = c["d"], c["ffn"]
+    inp = workloads.block_inputs(d, 2, 1, 64, ffn, 1, seed=7)
+    W = lambda key: smg.Q4Weights(inp[key][0], inp[key][1], inp[key][2], inp[key][3])  # noqa: E731
+    gate, up, down = W("gate"), W("up"), W("down")
+    copies = 4
+    fused, plain = [], []
+    for _ in range(copies):
+        fused.append(smg.Mlp.gated(smg.GatedLinear.from_q4(gate.clone(), up.clone(), smg.Gate.Silu),
+                                   smg.Linear(down.clone())))
+        plain.append((smg.GatedLinear.from_q4(gate.clone(), up.clone(), smg.Gate.Silu).inner,
+                      smg.Linear(down.clone())))
+    x16 = torch.from_numpy(np.random.default_rng(1).standard_normal(d).astype(np.float16)).cuda()
+    y = torch.zeros(d, dtype=torch.float32, device="cuda")
+    both = torch.empty(2 * ffn, dtype=torch.float16, device="cuda")
+    hid = torch.empty(ffn, dtype=torch.float16, device="cuda")
+    out = torch.empty(d, dtype=torch.float16, device="cuda")
+
+    def run_plain(i):
+        gu, dn = plain[i]
+        gu.forward(x16, both, 1)
+        smg.glu(both, 1, ffn, smg.Gate.Silu, hid)
+        dn.forward(hid, out, 1)
+        y.add_(out.float())
+    st = max(copies, min(steps, 64)) // copies * copies
+    us_fused = timer([(lambda i=i: fused[i].accumulate(x16, y, 1)) for i in range(copies)], st, copies)
+    us_plain = timer([(lambda i=i: run_plain(i)) for i in range(copies)], st, copies)
+    nbytes = workloads.block_stage_bytes(d, 2, 1, 64, ffn, 1)
+    mb = nbytes["gate_up"] + nbytes["down"]
+    return {"workload": "Mlp::accumulate, 1 row, d=4096, SwiGLU 14336, Q4 block 32; 4 weight copies",
+            "bytes": mb, "us_fused": us_fused, "us_plain_calls": us_plain, "speedup": us_plain / us_fused,
+            "GBps_fused": mb / (us_fused * 1e-6) / 1e9, "launches": {"fused": 2, "plain": 4}}
 
 
 def cpu_baselines(np, workloads, a, quants, scales, bytes1, only):
