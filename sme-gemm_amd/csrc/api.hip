@@ -292,29 +292,29 @@ int make_q4(Get get, const uint16_t *scales_rm, const uint16_t *mins_rm, const u
     // rows for every depth the kernels may touch: the GEMM steps K in 64s
     d.sc_rows = std::max(nbk, (round_up(d.nchunks * Q4_CHUNK, 64) + block - 1) / block);
     d.k_pad = round_up(k ? k : 1, 64);
-    std::vector<uint8_t> nib(d.nchunks * d.n_pad * 16, 0);
+    std::vector<uint8_t> nib(cell_grid_rows(d.nchunks) * d.n_pad * 16, 0);
     for (size_t dd = 0; dd < k; dd++) {
         const size_t kc = dd / 32, x = dd % 32, wd = x / 8, e = (x % 8) / 2, h = x % 2;
         const size_t bitpos = 16 * h + 4 * e;
         const size_t byteoff = wd * 4 + bitpos / 8;
         const int shift = bitpos % 8;
         for (size_t j = 0; j < n; j++)
-            nib[cell_index(kc, j, d.nchunks) * 16 + byteoff] |= (uint8_t)((get(dd, j) ^ 8) << shift);
+            nib[cell_index(kc, j, d.nchunks, d.n_pad) * 16 + byteoff] |= (uint8_t)((get(dd, j) ^ 8) << shift);
     }
-    std::vector<uint16_t> sc(d.sc_rows * d.n_pad, 0), mn;
+    std::vector<uint16_t> sc(cell_grid_rows(d.sc_rows) * d.n_pad, 0), mn;
     const bool affine = mins_rm || mins_band;
-    if (affine) mn.assign(d.sc_rows * d.n_pad, 0);
+    if (affine) mn.assign(cell_grid_rows(d.sc_rows) * d.n_pad, 0);
     for (size_t j = 0; j < n; j++)
         for (size_t b = 0; b < nbk; b++) {
             size_t src;
             if (scales_rm) {
                 src = j * nbk + b;
-                sc[cell_index(b, j, d.sc_rows)] = scales_rm[src];
-                if (affine) mn[cell_index(b, j, d.sc_rows)] = mins_rm[src];
+                sc[cell_index(b, j, d.sc_rows, d.n_pad)] = scales_rm[src];
+                if (affine) mn[cell_index(b, j, d.sc_rows, d.n_pad)] = mins_rm[src];
             } else {
                 src = (j / 128) * (nbk * 128) + b * 128 + j % 128;
-                sc[cell_index(b, j, d.sc_rows)] = scales_band[src];
-                if (affine) mn[cell_index(b, j, d.sc_rows)] = mins_band[src];
+                sc[cell_index(b, j, d.sc_rows, d.n_pad)] = scales_band[src];
+                if (affine) mn[cell_index(b, j, d.sc_rows, d.n_pad)] = mins_band[src];
             }
         }
     void *p;
@@ -386,19 +386,19 @@ int make_lowbit(int kind, Get get, const uint16_t *scales, bool band_scales,
     if (kind == W_Q2)
         d.codebook = (uint32_t)(uint8_t)codebook[0] | ((uint32_t)(uint8_t)codebook[1] << 8) |
                      ((uint32_t)(uint8_t)codebook[2] << 16) | ((uint32_t)(uint8_t)codebook[3] << 24);
-    std::vector<uint8_t> codes(d.nchunks * d.n_pad * 64, 0);
+    std::vector<uint8_t> codes(cell_grid_rows(d.nchunks) * d.n_pad * 64, 0);
     for (size_t dd = 0; dd < k; dd++) {
         const uint32_t bit = kind == W_Q2 ? lb_bit<2>(dd) : lb_bit<1>(dd);
         for (size_t j = 0; j < n; j++) {
-            const size_t off = kind == W_Q2 ? lb_dword_offset<2>(dd, j, d.nchunks)
-                                            : lb_dword_offset<1>(dd, j, d.nchunks);
+            const size_t off = kind == W_Q2 ? lb_dword_offset<2>(dd, j, d.nchunks, d.n_pad)
+                                            : lb_dword_offset<1>(dd, j, d.nchunks, d.n_pad);
             codes[off + bit / 8] |= (uint8_t)(get(dd, j) << (bit % 8));
         }
     }
-    std::vector<uint16_t> sc(d.sc_rows * d.n_pad, 0);
+    std::vector<uint16_t> sc(cell_grid_rows(d.sc_rows) * d.n_pad, 0);
     for (size_t j = 0; j < n; j++)
         for (size_t b = 0; b < nbk; b++)
-            sc[cell_index(b, j, d.sc_rows)] =
+            sc[cell_index(b, j, d.sc_rows, d.n_pad)] =
                 band_scales ? scales[lb_scale_index(nbk * 64, b, j)] : scales[j * nbk + b];
     void *p;
     int rc;
@@ -496,7 +496,7 @@ int check_kind(const smg_weights *w, int kind) {
 
 // A handle of n_out columns whose column j is column cols[j] of a, or of b when
 // bit 30 of cols[j] is set. Every device array of a weight set is a
-// tile-major [rows][n_pad] grid of cells, so whole cells move unchanged.
+// [rows][n_pad] grid of cells (common.cuh), so whole cells move unchanged.
 int gather_columns(const smg_weights *a, const smg_weights *b, const std::vector<int32_t> &cols,
                    smg_weights **out) {
     HIP_TRY(hipSetDevice(a->device), SMG_EHIP);
@@ -526,9 +526,9 @@ int gather_columns(const smg_weights *a, const smg_weights *b, const std::vector
     for (int i = 0; i < 3 && e == hipSuccess && rc == SMG_OK; i++) {
         if (!f[i].s0) continue;
         void *p;
-        if ((rc = alloc_dev(w, f[i].rows * d.n_pad * f[i].cell, &p))) break;
+        if ((rc = alloc_dev(w, cell_grid_rows(f[i].rows) * d.n_pad * f[i].cell, &p))) break;
         *f[i].dst = p;
-        e = launch_gather_columns(p, d.n_pad, f[i].s0, f[i].s1, dmap, f[i].rows, f[i].cell, nullptr);
+        e = launch_gather_columns(p, d.n_pad, f[i].s0, f[i].s1, s.n_pad, dmap, f[i].rows, f[i].cell, nullptr);
     }
     if (e == hipSuccess) e = hipDeviceSynchronize();
     (void)hipFree(dmap);
@@ -978,8 +978,8 @@ int smg_weights_clone(const smg_weights *w, smg_weights **out) {
         const void *src;
         size_t bytes;
     };
-    const size_t code_bytes = w->d.nchunks * w->d.n_pad * (w->d.kind == W_Q4 ? 16 : 64);
-    const size_t sc_bytes = w->d.sc_rows * w->d.n_pad * 2;
+    const size_t code_bytes = cell_grid_rows(w->d.nchunks) * w->d.n_pad * (w->d.kind == W_Q4 ? 16 : 64);
+    const size_t sc_bytes = cell_grid_rows(w->d.sc_rows) * w->d.n_pad * 2;
     const size_t dense_bytes = w->d.n_pad * w->d.k_pad * 2;
     const Field f[4] = {{w->d.codes, code_bytes}, {w->d.scales, sc_bytes},
                         {w->d.mins, sc_bytes}, {w->d.dense, dense_bytes}};

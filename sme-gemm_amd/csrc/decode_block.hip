@@ -195,10 +195,10 @@ __global__ void __launch_bounds__(MF_WAVES * 64) blk_gemv(Q4GemvArgs g, BlkArgs 
     float4_t acc;
     if constexpr (NORM) {
         const SrcNormRow src(a.nx, a.nw, g.k, a.eps);
-        acc = q4_mfma_mainloop<1, false>(g, src, ChainArgs{}, a_lds, col, timed_out);
+        acc = q4_mfma_mainloop<1, false, SrcNormRow, false>(g, src, ChainArgs{}, a_lds, col, timed_out);
     } else {
         const SrcRows<MR> src(g.lhs, g.m, g.k);
-        acc = q4_mfma_mainloop<MR, false>(g, src, ChainArgs{}, a_lds, col, timed_out);
+        acc = q4_mfma_mainloop<MR, false, SrcRows<MR>, false>(g, src, ChainArgs{}, a_lds, col, timed_out);
     }
     BlkPre pre{0.0f, 1.0f, 0.0f};
     if constexpr (MR == 1) pre = blk_prefetch<STORE>(g, a, tile);

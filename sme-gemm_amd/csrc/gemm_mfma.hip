@@ -106,7 +106,7 @@ __device__ __forceinline__ void b_load(const GemmArgs &g, uint32_t col0, uint32_
     const uint32_t kcc = live ? kc : g.nchunks - 1;
     const uint32_t dc = kcc * CH + d % CH;
     if constexpr (WK == W_Q4) {
-        const uint8_t *p = g.codes + cell_index(kcc, col, g.nchunks) * 16 + ((d % 32) / 8) * 4;
+        const uint8_t *p = g.codes + cell_index(kcc, col, g.nchunks, g.n_pad) * 16 + ((d % 32) / 8) * 4;
         if constexpr (UD == 32) {
             const uint4 x = *(const uint4 *)p;
             r.v[0] = x.x;
@@ -120,14 +120,14 @@ __device__ __forceinline__ void b_load(const GemmArgs &g, uint32_t col0, uint32_
         }
     } else {
         // quarter(s) of the unit's slab: dwords 16 bytes apart
-        const uint8_t *p = g.codes + lb_dword_offset<WK == W_Q2 ? 2 : 1>(dc, col, g.nchunks);
+        const uint8_t *p = g.codes + lb_dword_offset<WK == W_Q2 ? 2 : 1>(dc, col, g.nchunks, g.n_pad);
         r.v[0] = *(const uint32_t *)p;
         if constexpr (UD == 32) r.v[1] = *(const uint32_t *)(p + 16);
     }
     // Scale (and min) loads are unconditional so no wait is forced here: the
     // values are only consumed (and masked by `live`) in b_store. When the
     // block is shorter than the unit, b_store reads per-depth scales instead.
-    const size_t si = cell_index(dc >> g.block_shift, col, g.sc_rows);
+    const size_t si = cell_index(dc >> g.block_shift, col, g.sc_rows, g.n_pad);
     r.s = g.sc[si];
     if constexpr (WK == W_Q4) r.mn = (g.mn ? g.mn : g.sc)[si];
     r.live = live;
@@ -184,11 +184,11 @@ __device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, uint32
                     uint16_t s0 = us, s1 = us, m0 = um, m1 = um;
                     if (per_depth) {
                         const uint32_t b0 = dp >> g.block_shift, b1 = (dp + 1) >> g.block_shift;
-                        s0 = r.live ? g.sc[cell_index(b0, col, g.sc_rows)] : (uint16_t)0;
-                        s1 = r.live ? g.sc[cell_index(b1, col, g.sc_rows)] : (uint16_t)0;
+                        s0 = r.live ? g.sc[cell_index(b0, col, g.sc_rows, g.n_pad)] : (uint16_t)0;
+                        s1 = r.live ? g.sc[cell_index(b1, col, g.sc_rows, g.n_pad)] : (uint16_t)0;
                         if (AFFINE) {
-                            m0 = r.live ? g.mn[cell_index(b0, col, g.sc_rows)] : (uint16_t)0;
-                            m1 = r.live ? g.mn[cell_index(b1, col, g.sc_rows)] : (uint16_t)0;
+                            m0 = r.live ? g.mn[cell_index(b0, col, g.sc_rows, g.n_pad)] : (uint16_t)0;
+                            m1 = r.live ? g.mn[cell_index(b1, col, g.sc_rows, g.n_pad)] : (uint16_t)0;
                         }
                     }
                     uint16_t w0, w1;
@@ -218,7 +218,7 @@ __device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, uint32
 #pragma unroll
                 for (int b = 0; b < 4; b++) {
                     const uint32_t dp = d0 + w * 16 + 4 * i + b;
-                    const uint16_t sb = per_depth ? (r.live ? g.sc[cell_index(dp >> g.block_shift, col, g.sc_rows)] : (uint16_t)0) : us;
+                    const uint16_t sb = per_depth ? (r.live ? g.sc[cell_index(dp >> g.block_shift, col, g.sc_rows, g.n_pad)] : (uint16_t)0) : us;
                     h[b] = f32_to_f16(f16_to_f32(sb) * (float)(int8_t)(vals >> (8 * b)));
                 }
                 out[w * 8 + 2 * i] = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
@@ -239,7 +239,7 @@ __device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, uint32
 #pragma unroll
                 for (int b = 0; b < 4; b++) {
                     const uint32_t dp = d0 + w * 16 + 4 * i + b;
-                    const uint16_t sb = per_depth ? (r.live ? g.sc[cell_index(dp >> g.block_shift, col, g.sc_rows)] : (uint16_t)0) : us;
+                    const uint16_t sb = per_depth ? (r.live ? g.sc[cell_index(dp >> g.block_shift, col, g.sc_rows, g.n_pad)] : (uint16_t)0) : us;
                     h[b] = ((bits >> (8 * b)) & 1u) ? sb : (uint16_t)(sb ^ 0x8000u);
                 }
                 out[w * 8 + 2 * i] = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
@@ -573,7 +573,7 @@ __global__ void q4_dequant_kernel(WDev w, uint16_t *dense) {
         for (int q = 0; q < 32; q++) out[q] = 0;
         return;
     }
-    const uint4 raw = *(const uint4 *)(w.codes + cell_index(kc, col, w.nchunks) * 16);
+    const uint4 raw = *(const uint4 *)(w.codes + cell_index(kc, col, w.nchunks, w.n_pad) * 16);
     const uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
     const uint32_t shift = (uint32_t)__builtin_ctzll(w.block);
     for (int wd = 0; wd < 4; wd++) {
@@ -586,12 +586,12 @@ __global__ void q4_dequant_kernel(WDev w, uint16_t *dense) {
                 uint16_t v = 0;
                 if (d < w.k) {
                     const size_t kb = d >> shift;
-                    const float s = f16_to_f32(w.scales[cell_index(kb, col, w.sc_rows)]);
+                    const float s = f16_to_f32(w.scales[cell_index(kb, col, w.sc_rows, w.n_pad)]);
                     if (!AFFINE) {
                         v = from_f32<BF16>(s * (float)cs[h]);
                     } else {
                         const double x = (double)s * (double)cs[h] +
-                                         (double)f16_to_f32(w.mins[cell_index(kb, col, w.sc_rows)]);
+                                         (double)f16_to_f32(w.mins[cell_index(kb, col, w.sc_rows, w.n_pad)]);
                         v = BF16 ? f32_to_bf16((float)x) : f64_to_f16(x);
                     }
                 }

@@ -99,9 +99,9 @@ __device__ __forceinline__ void barrier_lds() {
 // activation chunks t and t+512, raw chunk t ([half t/256][column t%256]) and
 // one dword of scales (waves 0-3) or mins (waves 4-7; scales again, unused,
 // for Q4_0 so that every wave issues the same count). The halves are
-// wave-uniform, and in the tile-major grids a row's part of a cell's address
-// is row * 16 cells whatever the column, so each step's part of an address
-// is a scalar base and the column's part a per-lane offset.
+// wave-uniform, and a cell's index is a row part plus a column part
+// (cell_index), so each step's part of an address is a scalar base and the
+// column's part a per-lane offset.
 struct DmaSrc {
     uint32_t a[2];          // activation chunk byte offsets from A at depth 0
     uint32_t b;             // raw chunk byte offset of the column's cell in row 0
@@ -118,10 +118,10 @@ __device__ __forceinline__ void dma_step(const RArgs &g, const DmaSrc &d, const 
 #pragma unroll
     for (int q = 0; q < 2; q++) dma16(a, d.a[q], base + (q * 512 + wave * 64) * 16);
     // raw Q4: chunk (2ks + t/256, column t%256) at byte A_BYTES + 16t
-    dma16(g.codes + (size_t)(2 * ks + d.half_b) * 16 * 16, d.b, base + A_BYTES + wave * 64 * 16);
+    dma16(g.codes + cell_row_part(2 * ks + d.half_b, g.nchunks, g.n_pad) * 16, d.b, base + A_BYTES + wave * 64 * 16);
     // scales (mins): [half][column] f16, two per lane
     const size_t row = (size_t)(((2 * ks + d.half_s) * 32) >> g.block_shift);
-    dma4(d.src_s + row * 16, d.s, base + A_BYTES + B_BYTES + wave * 256);
+    dma4(d.src_s + cell_row_part(row, g.sc_rows, g.n_pad), d.s, base + A_BYTES + B_BYTES + wave * 256);
 }
 
 // One 32-depth half of a step as LDS reads: 8 activation fragments and, per
@@ -327,8 +327,8 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
             }
             const uint32_t cb = min(col0 + t % 256, g.n_pad - 1);
             const uint32_t cs = min(col0 + 2 * (t % 128), g.n_pad - 2);  // even: cs, cs+1 share a tile
-            d.b = (uint32_t)cell_index(0, cb, g.nchunks) * 16;
-            d.s = (uint32_t)cell_index(0, cs, g.sc_rows) * 2;
+            d.b = (uint32_t)cell_col_part(cb, g.nchunks, g.n_pad) * 16;
+            d.s = (uint32_t)cell_col_part(cs, g.sc_rows, g.n_pad) * 2;
             d.half_b = wave / 4;
             d.half_s = (wave % 4) / 2;
             d.src_s = (AFFINE && wave >= 4) ? g.mn : g.sc;
@@ -431,7 +431,7 @@ bool q4r_supported(const WDev &w, size_t m, long lhs_cs, long lhs_rs, const uint
     return w.kind == W_Q4 && !bf16 && m > 0 && w.k >= 64 && w.k % 64 == 0 && w.block >= 32 &&
            lhs_cs == 1 && lhs_rs % 8 == 0 && lhs_rs >= (long)w.k && ((uintptr_t)lhs & 15) == 0 &&
            m * (size_t)lhs_rs * 2 < ((size_t)1 << 31) &&  // 32-bit DMA offsets
-           w.nchunks * w.n_pad * 16 < ((size_t)1 << 32);
+           cell_grid_rows(w.nchunks) * w.n_pad * 16 < ((size_t)1 << 32);
 }
 
 hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,

@@ -80,10 +80,11 @@ hipError_t launch_q4_dequant_dense(const WDev &q4, uint16_t *dense, bool to_bf16
                                    hipStream_t s);
 
 // dst[r][j] = (map[j] bit 30 ? src1 : src0)[r][map[j] & 0x3FFFFFFF], cells of
-// cell_bytes (2, 16 or 64) in tile-major [rows][pad] grids (every source
-// column index below its grid's pad); map[j] < 0 writes zeros.
+// cell_bytes (2, 16 or 64) in [rows][pad] grids (common.cuh's cell order);
+// map[j] < 0 writes zeros.
 hipError_t launch_gather_columns(void *dst, size_t dst_pad, const void *src0, const void *src1,
-                                 const int32_t *map, size_t rows, size_t cell_bytes, hipStream_t s);
+                                 size_t src_pad, const int32_t *map, size_t rows, size_t cell_bytes,
+                                 hipStream_t s);
 
 // ---- decode block (decode_block.hip) ---------------------------------------
 // What the fused Q4 GEMVs of the decode block do at their source and store.

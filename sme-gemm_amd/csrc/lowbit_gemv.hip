@@ -70,7 +70,7 @@ __global__ void __launch_bounds__(T) lowbit_gemv(LbArgs g, EpArgs ep) {
     const uint32_t mr = min((uint32_t)MR, g.m - row0);
 
     const rsrc_t qr = make_rsrc(g.q, g.m * g.kq);
-    const rsrc_t sr = make_rsrc(g.sc, g.sc_rows * g.n_pad * 2u);
+    const rsrc_t sr = make_rsrc(g.sc, (uint32_t)cell_grid_rows(g.sc_rows) * g.n_pad * 2u);
     const rsrc_t fr = make_rsrc(g.s, g.m * g.nbq * 4u);
     const rsrc_t ur = make_rsrc(g.asum, g.m * g.nbq * 4u);
 
@@ -105,7 +105,7 @@ __global__ void __launch_bounds__(T) lowbit_gemv(LbArgs g, EpArgs ep) {
                                       ? (row0 + c) * g.kq + slab * LB_SLAB + 16 * gq4 : OOB);
             const uint32_t sl = live ? slab : sa0;  // dead slots reload a valid dword
             wreg[i] = *(const uint32_t *)(g.codes +
-                                          lb_dword_offset<KIND>((size_t)sl * LB_SLAB + 16 * gq4, col, g.ngroups));
+                                          lb_dword_offset<KIND>((size_t)sl * LB_SLAB + 16 * gq4, col, g.ngroups, g.n_pad));
         }
         // scales of the 16 columns (32 bytes a block), activation scales, sums
         constexpr int RS = 4;  // up to 4 x 512 x 16 B = 32 KB of scale rows
@@ -113,7 +113,7 @@ __global__ void __launch_bounds__(T) lowbit_gemv(LbArgs g, EpArgs ep) {
 #pragma unroll
         for (int r = 0; r < RS; r++) {
             const uint32_t i = t + T * r, bb = i / 2, half = i % 2;
-            sreg[r] = bload16(sr, bb < nb ? (uint32_t)cell_index(b0 + bb, col0, g.sc_rows) * 2u + half * 16u : OOB);
+            sreg[r] = bload16(sr, bb < nb ? (uint32_t)cell_index(b0 + bb, col0, g.sc_rows, g.n_pad) * 2u + half * 16u : OOB);
         }
         float fsa[2];
         int32_t fas[2];
@@ -455,9 +455,9 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
     // can still be in flight when the waits before them end
     uint4 sreg;
     {
-        const rsrc_t sr = make_rsrc(g.sc, g.sc_rows * g.n_pad * 2u);
+        const rsrc_t sr = make_rsrc(g.sc, (uint32_t)cell_grid_rows(g.sc_rows) * g.n_pad * 2u);
         const uint32_t bb = t >> (g.cg_shift + 1), piece = t & (2 * cg - 1);  // 8 columns a piece
-        sreg = bload16(sr, (bb < nbq && bb < g.sc_rows) ? (uint32_t)cell_index(bb, wg_col0 + piece * 8, g.sc_rows) * 2u
+        sreg = bload16(sr, (bb < nbq && bb < g.sc_rows) ? (uint32_t)cell_index(bb, wg_col0 + piece * 8, g.sc_rows, g.n_pad) * 2u
                                                         : OOB);
     }
     uint4 wreg[NG];
@@ -466,7 +466,7 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
 #pragma unroll
         for (int i = 0; i < NG; i++) {
             const uint32_t grp = kw * NG + i;
-            wreg[i] = bload16(cr, grp < g.ngroups ? ((uint32_t)cell_index(grp, col0 + c, g.ngroups) * 4 + gq4) * 16 : OOB);
+            wreg[i] = bload16(cr, grp < g.ngroups ? ((uint32_t)cell_index(grp, col0 + c, g.ngroups, g.n_pad) * 4 + gq4) * 16 : OOB);
         }
     }
     // the epilogue operands last: their addresses wait on the op-graph's
@@ -850,8 +850,8 @@ hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint
                               const EpArgs &ep, void *scratch, hipStream_t s) {
     const TileGeo sg = tile_geometry(w, m);
     if (sg.ok) {
-        const size_t cb = w.nchunks * w.n_pad * 64;
-        if (m * w.k * 2 >= ((size_t)1 << 31) || w.sc_rows * w.n_pad * 2 >= ((size_t)1 << 31) ||
+        const size_t cb = cell_grid_rows(w.nchunks) * w.n_pad * 64;
+        if (m * w.k * 2 >= ((size_t)1 << 31) || cell_grid_rows(w.sc_rows) * w.n_pad * 2 >= ((size_t)1 << 31) ||
             cb >= ((size_t)1 << 31))
             return hipErrorInvalidValue;  // one buffer resource spans < 2 GiB
         LtArgs f = {};
@@ -890,7 +890,7 @@ hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint
         return launch_tile<1>(f, ep, mr, sg.ng, s);
     }
     const Geo ge = geometry(w, m);
-    if (m * ge.kq >= ((size_t)1 << 31) || w.sc_rows * w.n_pad * 2 >= ((size_t)1 << 31))
+    if (m * ge.kq >= ((size_t)1 << 31) || cell_grid_rows(w.sc_rows) * w.n_pad * 2 >= ((size_t)1 << 31))
         return hipErrorInvalidValue;  // one buffer resource spans < 2 GiB
     LbArgs g = {};
     g.codes = w.codes;

@@ -15,7 +15,7 @@
 //   a workgroup of 8 waves owns 16 output columns; wave w takes every 8th
 //   group of 4 chunks (128 depths). Lane (g = lane/16, c = lane%16) loads the
 //   16-byte chunk g of column c, so a wave load reads one contiguous 1 KB run
-//   of the tile-major layout, and every lane issues all its weight loads
+//   of the blocked layout (common.cuh), and every lane issues all its weight loads
 //   before it waits. Each
 //   dword (8 depths) dequantizes to 8 f16 weights -- v_bfi_b32 puts the
 //   nibble under an f16 exponent, a packed subtract leaves the exact code, a
@@ -162,10 +162,10 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4GemvArgs g, EpArgs ep) {
         for (int p = 0; p < P; p++) {
             const uint32_t kc = kc0 + kl * P + p;
             const uint32_t kcc = kc < last ? kc : last;
-            wq[p] = *(const uint4 *)(g.nib + cell_index(kcc, j, g.nchunks) * 16);
+            wq[p] = *(const uint4 *)(g.nib + cell_index(kcc, j, g.nchunks, g.n_pad) * 16);
             const uint32_t kb = block >= Q4_CHUNK ? ((kcc * Q4_CHUNK) >> g.block_shift) : 0;
-            sv[p] = g.sc[cell_index(kb, j, g.sc_rows)];
-            mv[p] = AFFINE ? g.mn[cell_index(kb, j, g.sc_rows)] : (uint16_t)0;
+            sv[p] = g.sc[cell_index(kb, j, g.sc_rows, g.n_pad)];
+            mv[p] = AFFINE ? g.mn[cell_index(kb, j, g.sc_rows, g.n_pad)] : (uint16_t)0;
         }
         // 2. stage A[:, pass] into LDS (zero beyond k)
         __syncthreads();
@@ -198,11 +198,11 @@ __global__ void __launch_bounds__(256) q4_gemv_kernel(Q4GemvArgs g, EpArgs ep) {
                     uint16_t s0 = sv[p], s1 = sv[p], m0 = mv[p], m1 = mv[p];
                     if (block < Q4_CHUNK) {
                         const uint32_t b0 = dp >> g.block_shift, b1 = (dp + 1) >> g.block_shift;
-                        s0 = g.sc[cell_index(b0, j, g.sc_rows)];
-                        s1 = g.sc[cell_index(b1, j, g.sc_rows)];
+                        s0 = g.sc[cell_index(b0, j, g.sc_rows, g.n_pad)];
+                        s1 = g.sc[cell_index(b1, j, g.sc_rows, g.n_pad)];
                         if (AFFINE) {
-                            m0 = g.mn[cell_index(b0, j, g.sc_rows)];
-                            m1 = g.mn[cell_index(b1, j, g.sc_rows)];
+                            m0 = g.mn[cell_index(b0, j, g.sc_rows, g.n_pad)];
+                            m1 = g.mn[cell_index(b1, j, g.sc_rows, g.n_pad)];
                         }
                     }
                     const uint32_t wpair = deq_pair_generic<BF16, AFFINE>(c0, c1, s0, s1, m0, m1);

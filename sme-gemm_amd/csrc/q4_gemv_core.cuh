@@ -6,7 +6,7 @@
 // A workgroup of 8 waves owns 16 output columns; wave w takes every 8th group
 // of 4 chunks (128 depths). Lane (g = lane/16, c = lane%16) loads the 16-byte
 // chunk g of column c, so a wave load reads one contiguous 1 KB run of the
-// tile-major layout, and every lane issues all its weight loads before it
+// blocked layout (common.cuh), and every lane issues all its weight loads before it
 // waits. Each dword (8
 // depths) dequantizes to 8 f16 weights -- v_bfi_b32 puts the nibble under an
 // f16 exponent, a packed subtract leaves the exact code, a packed multiply by
@@ -84,7 +84,13 @@ struct SrcRows {
 // CHAIN: the chained GEMV's wait for its producer (ch.ready) between the weight
 // loads and the activation loads of each segment; timed_out reports a wait
 // that expired (uniform over the workgroup; the tile is then incomplete).
-template <int MR, bool CHAIN, class Src>
+// MASK_B: only the B lanes of rows < MR read LDS, under an exec mask, the
+// others zeroed; otherwise every lane reads (rows >= MR read row MR-1 again:
+// MFMA output rows are independent and those are never read). Measured on
+// MI355X, masking is 0.18 us faster for the lone config-1 GEMV from HBM, and
+// reading everywhere 1.7 us faster over a decode step's five projections,
+// whose wide GEMVs are bound by the VALU the zeroing adds.
+template <int MR, bool CHAIN, class Src, bool MASK_B = true>
 __device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const Src &src,
                                                      const ChainArgs &ch, uint16_t *a_lds, uint32_t col,
                                                      bool &timed_out) {
@@ -114,8 +120,8 @@ __device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const 
         for (int u = 0; u < MF_U; u++) {
             const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
             const uint32_t kcc = kc < last ? kc : last;  // clamped: always a valid load
-            wq[u] = *(const uint4 *)(g.nib + cell_index(kcc, col, g.nchunks) * 16);
-            const uint16_t sl = g.sc[cell_index((kcc * Q4_CHUNK) >> g.block_shift, col, g.sc_rows)];
+            wq[u] = *(const uint4 *)(g.nib + cell_index(kcc, col, g.nchunks, g.n_pad) * 16);
+            const uint16_t sl = g.sc[cell_index((kcc * Q4_CHUNK) >> g.block_shift, col, g.sc_rows, g.n_pad)];
             sv[u] = kc < g.nchunks ? sl : (uint16_t)0;  // a dead step's weights become 0
         }
         if constexpr (CHAIN) {
@@ -140,20 +146,24 @@ __device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const 
         src.stage(a_lds, areg, t);
         __syncthreads();
         // dequant + MFMA: A operand = 16 columns x 32 depths of weights, B
-        // operand = 32 depths x 16 rows of activations. B lanes of rows >= MR
-        // read row MR-1 again: MFMA output rows are independent and those are
-        // never read, so nothing needs zeroing (no per-lane select, no masked
-        // branch). Chunks past K read the staged zeros of the segment and have
-        // zero weights. All of this wave's activation fragments are read
-        // first, so the LDS round trips overlap instead of each one preceding
-        // its MFMA.
+        // operand = 32 depths x 16 rows of activations (B lanes per MASK_B).
+        // Chunks past K read the staged zeros of the segment and have zero
+        // weights. All of this wave's activation fragments are read first, so
+        // the LDS round trips overlap instead of each one preceding its MFMA.
         const uint16_t *arow = a_lds + (c < MR ? c : MR - 1) * MF_SEG;
         uint4 abv[MF_U][4];
+        if (!MASK_B || c < MR) {
 #pragma unroll
-        for (int u = 0; u < MF_U; u++) {
-            const uint32_t kcl = 4 * (wave + MF_WAVES * u) + grp;  // chunk within the segment
+            for (int u = 0; u < MF_U; u++) {
+                const uint32_t kcl = 4 * (wave + MF_WAVES * u) + grp;  // chunk within the segment
 #pragma unroll
-            for (int w = 0; w < 4; w++) abv[u][w] = *(const uint4 *)(arow + kcl * Q4_CHUNK + w * 8);
+                for (int w = 0; w < 4; w++) abv[u][w] = *(const uint4 *)(arow + kcl * Q4_CHUNK + w * 8);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < MF_U; u++)
+#pragma unroll
+                for (int w = 0; w < 4; w++) abv[u][w] = make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int u = 0; u < MF_U; u++) {
@@ -187,14 +197,14 @@ __device__ __forceinline__ void q4_item_load(const Q4GemvArgs &g, uint32_t sc0, 
     for (int u = 0; u < MF_U; u++) {
         const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
         const uint32_t kcc = kc < last ? kc : last;
-        it.wq[u] = *(const uint4 *)(g.nib + cell_index(kcc, col, g.nchunks) * 16);
-        const uint16_t sl = g.sc[cell_index((kcc * Q4_CHUNK) >> g.block_shift, col, g.sc_rows)];
+        it.wq[u] = *(const uint4 *)(g.nib + cell_index(kcc, col, g.nchunks, g.n_pad) * 16);
+        const uint16_t sl = g.sc[cell_index((kcc * Q4_CHUNK) >> g.block_shift, col, g.sc_rows, g.n_pad)];
         it.sv[u] = kc < g.nchunks ? sl : 0u;
     }
 }
 // The item's MFMAs for activation row 0, staged in LDS at arow[depth] (the
-// whole row, zero-filled to whole segments): every B-operand lane reads row 0,
-// and only output row 0 is used.
+// whole row, zero-filled to whole segments): every B-operand lane reads row 0
+// (q4_mfma_mainloop's unmasked form), and only output row 0 is used.
 __device__ __forceinline__ void q4_item_mma1(uint32_t sc0, const Q4Item &it, const uint16_t *arow,
                                              float4_t &acc, uint32_t mag_lo, uint32_t mag_hi) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
