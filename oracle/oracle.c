@@ -911,11 +911,16 @@ int or_matmul_mt(int kind, const uint16_t *a, const uint8_t *codes, const uint16
         jobs[t] = jb;
     }
     int rc = 0;
-    for (int t = 1; t < threads; t++)
-        if (pthread_create(&tid[t], NULL, or_col_job, &jobs[t]) != 0) rc = -1;
+    char *started = calloc((size_t)threads, 1);
+    if (!started) { free(jobs); free(tid); return -1; }
+    for (int t = 1; t < threads; t++) {
+        if (pthread_create(&tid[t], NULL, or_col_job, &jobs[t]) == 0) started[t] = 1;
+        else rc = -1;
+    }
     or_col_job(&jobs[0]);
-    for (int t = 1; t < threads; t++)
-        if (rc == 0) pthread_join(tid[t], NULL);
+    for (int t = 1; t < threads; t++)  /* every thread that started, before jobs is freed */
+        if (started[t]) pthread_join(tid[t], NULL);
+    free(started);
     for (int t = 0; t < threads; t++)
         if (!jobs[t].ok) rc = -1;
     free(jobs);
