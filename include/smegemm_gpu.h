@@ -44,6 +44,14 @@ extern "C" {
 #define SMG_ENODEV -4  /* no usable gfx950 device */
 #define SMG_EKIND -5   /* weight handle of the wrong kind for this entry point */
 
+/* Test hook: while the environment holds SMG_TEST_FAIL_ALLOC=1 (read at each
+ * attempt) every device allocation the library makes fails, so the call
+ * returns SMG_ENOMEM before writing dst -- the contract the reference's
+ * callers rely on to take their portable path on a non-zero return
+ * (src/kernels/q4/matmul.rs:85-89). Buffers a call allocated earlier
+ * (the host-call staging area, the device-form scratch pool) are kept and
+ * reused, so only a first allocation or a growth fails. */
+
 /* ---- epilogue ABI: byte-identical to csrc/epilogue.h:136-236 -------------- */
 enum ep_act {
     EP_ACT_NONE = 0, EP_ACT_RELU = 1, EP_ACT_GELU = 2, EP_ACT_SILU = 3, EP_ACT_TANH = 4,

@@ -82,6 +82,20 @@ struct Ctx {
 };
 thread_local Ctx g_ctx;
 
+// hipMalloc, or a forced failure while the environment has
+// SMG_TEST_FAIL_ALLOC=1: a test hook for the reference's contract that a call
+// whose allocation fails returns non-zero and leaves its output untouched, so
+// the caller takes its portable path (src/kernels/q4/matmul.rs:85-89). The
+// variable is read at every allocation.
+hipError_t dev_malloc(void **p, size_t bytes) {
+    const char *f = std::getenv("SMG_TEST_FAIL_ALLOC");
+    if (f && f[0] == '1') {
+        *p = nullptr;
+        return hipErrorOutOfMemory;
+    }
+    return hipMalloc(p, bytes);
+}
+
 int ctx_for(int device, size_t bytes, Ctx **out) {
     Ctx &c = g_ctx;
     HIP_TRY(hipSetDevice(device), SMG_EHIP);
@@ -99,7 +113,7 @@ int ctx_for(int device, size_t bytes, Ctx **out) {
         c.buf = nullptr;
         c.cap = 0;
         size_t want = round_up(bytes, 1 << 20);
-        if (hipMalloc(&c.buf, want) != hipSuccess) return fail(SMG_ENOMEM, "staging hipMalloc");
+        if (dev_malloc(&c.buf, want) != hipSuccess) return fail(SMG_ENOMEM, "staging hipMalloc");
         c.cap = want;
     }
     *out = &c;
@@ -117,7 +131,7 @@ struct HipDevAlloc {
         if (hipGetDevice(&cur) != hipSuccess) return nullptr;
         if (cur != device && hipSetDevice(device) != hipSuccess) return nullptr;
         void *p = nullptr;
-        const bool ok = hipMalloc(&p, bytes) == hipSuccess;
+        const bool ok = dev_malloc(&p, bytes) == hipSuccess;
         if (cur != device) (void)hipSetDevice(cur);
         return ok ? p : nullptr;
     }
@@ -229,7 +243,7 @@ int ep_args(const ep_desc16 *ep, EpArgs *out, size_t n) {
 
 // ---- weight creation ---------------------------------------------------------
 int alloc_dev(smg_weights *w, size_t bytes, void **p) {
-    if (hipMalloc(p, bytes ? bytes : 16) != hipSuccess) return fail(SMG_ENOMEM, "weights hipMalloc");
+    if (dev_malloc(p, bytes ? bytes : 16) != hipSuccess) return fail(SMG_ENOMEM, "weights hipMalloc");
     w->allocs.push_back(*p);
     w->bytes += bytes;
     return SMG_OK;
@@ -510,7 +524,7 @@ int gather_columns(const smg_weights *a, const smg_weights *b, const std::vector
     std::vector<int32_t> map(d.n_pad, -1);
     std::copy(cols.begin(), cols.end(), map.begin());
     int32_t *dmap = nullptr;
-    hipError_t e = hipMalloc((void **)&dmap, map.size() * sizeof(int32_t));
+    hipError_t e = dev_malloc((void **)&dmap, map.size() * sizeof(int32_t));
     if (e != hipSuccess) { destroy(w); return fail(SMG_ENOMEM, "column map hipMalloc", e); }
     e = hipMemcpy(dmap, map.data(), map.size() * sizeof(int32_t), hipMemcpyHostToDevice);
     struct Field {
@@ -655,7 +669,7 @@ int ensure_rope(smg_attn *a, size_t cap) {
         }
     float *d = nullptr;
     HIP_TRY(hipSetDevice(a->device), SMG_EHIP);
-    if (hipMalloc(&d, tab.size() * 4) != hipSuccess) return fail(SMG_ENOMEM, "rope table hipMalloc");
+    if (dev_malloc((void **)&d, tab.size() * 4) != hipSuccess) return fail(SMG_ENOMEM, "rope table hipMalloc");
     hipError_t e = hipMemcpy(d, tab.data(), tab.size() * 4, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         (void)hipFree(d);
@@ -831,6 +845,43 @@ void destroy_mlp(smg_mlp *m) {
     destroy(m->up);
     destroy(m->down);
     delete m;
+}
+
+// A device-form call hands its pointers straight to the kernels, so each must
+// be memory the weights' device can read: that device's own memory, managed
+// memory or pinned host memory. Pageable host memory (a malloc'd buffer, a
+// numpy array) would make the kernel fault; it is refused with SMG_EINVAL
+// instead. The runtime's allocation table answers this on the host (a failed
+// lookup's error is cleared so it is not reported by a later call). While the
+// stream is being captured into a graph the lookup is skipped: a capture is
+// built from calls that have run eagerly, where it applies.
+bool device_readable(const void *p, int device) {
+    hipPointerAttribute_t at;
+    if (hipPointerGetAttributes(&at, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    if (at.type == hipMemoryTypeDevice) return at.device == device;
+    return at.type == hipMemoryTypeManaged || at.type == hipMemoryTypeHost;
+}
+
+int check_dev_ptrs(const char *who, int device, void *stream, const EpArgs &ea,
+                   std::initializer_list<const void *> ptrs) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(SMG_EHIP, who);
+    }
+    if (cs != hipStreamCaptureStatusNone) return SMG_OK;
+    for (const void *p : ptrs)
+        if (p && !device_readable(p, device))
+            return fail(SMG_EINVAL, "device call: an operand pointer is not memory this device can read "
+                                    "(host memory must be pinned; device memory must be on the weights' GPU)");
+    for (uint32_t i = 0; i < ea.n_nodes; i++)
+        if (ea.nodes[i].ptr && !device_readable(ea.nodes[i].ptr, device))
+            return fail(SMG_EINVAL, "device call: an epilogue operand is not memory this device can read "
+                                    "(host memory must be pinned; device memory must be on the weights' GPU)");
+    return SMG_OK;
 }
 
 }  // namespace
@@ -1209,6 +1260,9 @@ int smg_gemm_run_dev(int bf16, size_t m, size_t n, size_t k, uint16_t *dst, long
         return fail(SMG_EINVAL, "strides must be non-negative and C's cells distinct");
     int device = 0;
     HIP_TRY(hipGetDevice(&device), SMG_EHIP);
+    int rc = check_dev_ptrs("smg_gemm_run_dev", device, stream, EpArgs{},
+                            {dst, k ? lhs : nullptr, k ? rhs : nullptr});
+    if (rc) return rc;
     WDev d = {};
     d.kind = bf16 ? W_BF16 : W_F16;
     d.n = n;
@@ -1252,6 +1306,7 @@ int gemm_gpu_f16f16_q4_single(size_t m, size_t n, size_t k) {
 
 // ---- device-pointer entry points -------------------------------------------
 
+
 int smg_q4_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
                       const ep_desc16 *ep, int bf16, void *stream) {
     int rc = check_kind(w, W_Q4);
@@ -1259,6 +1314,7 @@ int smg_q4_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint1
     if (m == 0 || w->d.n == 0) return SMG_OK;
     EpArgs ea;
     if ((rc = ep_args(ep, &ea, w->d.n))) return rc;
+    if ((rc = check_dev_ptrs("smg_q4_matmul_dev", w->device, stream, ea, {dst, lhs}))) return rc;
     hipError_t e = run_q4(w->d, m, dst, lhs, ea, bf16 != 0, (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_q4_matmul_dev", e);
 }
@@ -1272,6 +1328,7 @@ int smg_q4_chained_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint
     if ((done || ready) && !sync) return fail(SMG_EINVAL, "smg_q4_chained_dev: done / ready need the sync words");
     EpArgs ea;
     if ((rc = ep_args(ep, &ea, w->d.n))) return rc;
+    if ((rc = check_dev_ptrs("smg_q4_chained_dev", w->device, stream, ea, {dst, lhs}))) return rc;
     // the device wall clock's rate (kHz), read once per device
     static std::atomic<int> clock_khz[64];
     int khz = w->device < 64 ? clock_khz[w->device].load(std::memory_order_relaxed) : 0;
@@ -1295,6 +1352,7 @@ int smg_lowbit_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const u
     EpArgs ea;
     int rc = ep_args(ep, &ea, w->d.n);
     if (rc) return rc;
+    if ((rc = check_dev_ptrs("smg_lowbit_matmul_dev", w->device, stream, ea, {dst, lhs}))) return rc;
     const size_t sb = lowbit_scratch_bytes(w->d, m);
     void *scratch = nullptr;
     if (sb) {
@@ -1319,6 +1377,7 @@ int smg_lowbit_matmul_dev_noalloc(size_t m, const smg_weights *w, uint16_t *dst,
     EpArgs ea;
     int rc = ep_args(ep, &ea, w->d.n);
     if (rc) return rc;
+    if ((rc = check_dev_ptrs("smg_lowbit_matmul_dev_noalloc", w->device, stream, ea, {dst, lhs}))) return rc;
     const size_t sb = lowbit_scratch_bytes(w->d, m);
     if (sb > SMG_NOALLOC_SCRATCH_BYTES)
         return fail(SMG_EINVAL, "smg_lowbit_matmul_dev_noalloc: the call needs more scratch than "
@@ -1337,6 +1396,7 @@ int smg_lowbit_mopa_dev(size_t m, const smg_weights *w, uint16_t *dst, const uin
     EpArgs ea;
     int rc = ep_args(ep, &ea, w->d.n);
     if (rc) return rc;
+    if ((rc = check_dev_ptrs("smg_lowbit_mopa_dev", w->device, stream, ea, {dst, lhs}))) return rc;
     hipError_t e = launch_gemm(w->d, m, dst, 1, (long)w->d.n, lhs, 1, (long)w->d.k, 1.0f, ea,
                                false, (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_lowbit_mopa_dev", e);
@@ -1350,6 +1410,7 @@ int smg_packed_matmul_dev(size_t m, const smg_weights *b, uint16_t *dst, long ds
     if (m == 0 || b->d.n == 0) return SMG_OK;
     EpArgs ea;
     if ((rc = ep_args(ep, &ea, b->d.n))) return rc;
+    if ((rc = check_dev_ptrs("smg_packed_matmul_dev", b->device, stream, ea, {dst, lhs}))) return rc;
     hipError_t e = launch_gemm(b->d, m, dst, dst_cs, dst_rs, lhs, lhs_cs, lhs_rs,
                                half_bits_to_float(beta_bits, bf16 != 0), ea, bf16 != 0,
                                (hipStream_t)stream);
@@ -1378,7 +1439,7 @@ int smg_kv_cache_create(size_t heads, size_t kv_heads, size_t head_dim, size_t c
     c->scale = 1.0f / std::sqrt((float)head_dim);  // kv_attention.rs:392
     c->k = c->v = nullptr;
     const size_t bytes = std::max<size_t>(capacity * kv_heads * head_dim * 2, 16);
-    if (hipMalloc((void **)&c->k, bytes) != hipSuccess || hipMalloc((void **)&c->v, bytes) != hipSuccess ||
+    if (dev_malloc((void **)&c->k, bytes) != hipSuccess || dev_malloc((void **)&c->v, bytes) != hipSuccess ||
         hipMemset(c->k, 0, bytes) != hipSuccess || hipMemset(c->v, 0, bytes) != hipSuccess) {
         smg_kv_cache_destroy(c);
         return fail(SMG_ENOMEM, "KvCache hipMalloc");
@@ -1615,7 +1676,7 @@ int smg_block_create(const float *norm1, float eps1, const float *norm2, float e
     b->eps1 = eps1;
     b->eps2 = eps2;
     b->norm1 = b->norm2 = nullptr;
-    if (hipMalloc((void **)&b->norm1, d * 4) != hipSuccess || hipMalloc((void **)&b->norm2, d * 4) != hipSuccess ||
+    if (dev_malloc((void **)&b->norm1, d * 4) != hipSuccess || dev_malloc((void **)&b->norm2, d * 4) != hipSuccess ||
         hipMemcpy(b->norm1, norm1, d * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(b->norm2, norm2, d * 4, hipMemcpyHostToDevice) != hipSuccess) {
         if (b->norm1) (void)hipFree(b->norm1);

@@ -346,14 +346,22 @@ class Epilogue:
         return not self.nodes and self.act is None
 
     def validate(self, m: int, n: int, device: int | None = None) -> None:
-        """validate_ep (src/exec/guard.rs:112-147), plus what the kernels need
-        of a device operand: 16-bit elements, contiguous, on the weights'
-        device (`device`); host operands are f16 / bf16 bit patterns."""
+        """validate_ep (src/exec/guard.rs:112-147), plus where the operands
+        live: a host-pointer call (`device` None) stages host arrays of f16 /
+        bf16 bit patterns; a device call on GPU `device` hands its operands to
+        the kernels, so they must be 16-bit, contiguous tensors on that GPU (a
+        host array there would be read through a host address by the kernel)."""
         for op, _aux, _s, v, ld in self.nodes:
-            if v is not None and _is_dev(v):
-                _dev16(v, None, "epilogue operand", device, self.bf16)
-            elif v is not None:
+            if v is not None and device is None:
+                if _is_dev(v):
+                    raise TypeError("host call: an epilogue operand is a device tensor (pass host arrays, "
+                                    "or call with device tensors for A and C)")
                 _host_operand(v, self.bf16)
+            elif v is not None:
+                if not _is_dev(v):
+                    raise TypeError(f"device call: an epilogue operand is a host array (pass tensors on "
+                                    f"cuda:{device})")
+                _dev16(v, None, "epilogue operand", device, self.bf16)
             length = None if v is None else (v.numel() if _is_dev(v) else np.asarray(v).size)
             if op in _ROW and length != m:
                 raise ValueError("row operand is per-M (length m)")

@@ -7,6 +7,10 @@
   that is not 16 bits wide, a strided view, too few elements.
 - A device-pointer call's scratch outlives later, larger calls on the same
   stream: a captured graph replays correctly after the pool has grown.
+- A device call refuses pageable host memory (epilogue operands, A, C) in
+  the mirror and at the C ABI; a host call refuses device operands.
+- With SMG_TEST_FAIL_ALLOC=1 every device allocation fails: the calls return
+  SMG_ENOMEM with dst untouched, and succeed once it is unset.
 - bf16 silu / sigmoid far below zero (where 1 / (1 + e^-x) leaves f32's normal
   range) match the reference's f64 formula bit for bit at the GEMV and GEMM
   stores.
@@ -136,3 +140,144 @@ def test_bf16_logistic_far_below_zero(smg, orc, act, m):
                             bf16=True)
     assert np.any(want[:n] & 0x7FFF), "some outputs are non-zero in bf16"
     assert np.array_equal(got, want)
+
+
+_ALLOC_FAIL_CHILD = r"""
+import ctypes as C, os, sys
+import numpy as np
+sys.path[:0] = sys.argv[1:4]
+import smegemm as smg, oracle as orc, torch
+from conftest import f16_tol, max_rel
+L = smg.lib()
+rng = np.random.default_rng(9)
+n, k, m = 256, 128, 3
+quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+scales = orc.f32_to_f16(rng.uniform(0.005, 0.02, n * (k // 32)).astype(np.float32))
+q4 = smg.Q4Weights(quants, scales, n, k)                       # created before the knob is set
+codes = rng.integers(0, 256, -(-(k * n) // 4), dtype=np.uint8)
+q2 = smg.Q2Weights(codes, scales, n, k, smg.Q2Params(32))
+a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+b = orc.f32_to_f16(rng.standard_normal(k * n).astype(np.float32))
+ad = torch.from_numpy(a.view(np.int16)).cuda()
+bd = torch.from_numpy(b.view(np.int16)).cuda()
+cd = torch.full((m * n,), 0x1234, dtype=torch.int16, device="cuda")
+stream = torch.cuda.current_stream().cuda_stream
+torch.cuda.synchronize()
+
+os.environ["SMG_TEST_FAIL_ALLOC"] = "1"
+c = np.full(m * n, 0x1234, np.uint16)
+rc = L.gemm_gpu_f16f16_q4(m, q4._h, c.ctypes.data, a.ctypes.data, None)
+print("host q4 (staging)", rc, flush=True)
+assert rc == -2 and np.all(c == 0x1234)
+rc = L.gemm_gpu_f16f16_run(m, n, k, c.ctypes.data, 1, n, 0, a.ctypes.data, 1, k, b.ctypes.data, 1, n, 0, 0x3C00)
+print("host strided gemm (staging)", rc, flush=True)
+assert rc == -2 and np.all(c == 0x1234)
+h = C.c_void_p()
+rc = L.smg_q4_create(quants.ctypes.data, scales.ctypes.data, None, n, k, 32, C.byref(h))
+print("q4 create (weights)", rc, h.value, flush=True)
+assert rc == -2 and not h.value
+rc = L.smg_lowbit_matmul_dev(m, q2._h, cd.data_ptr(), ad.data_ptr(), None, stream)
+print("device q2 (scratch pool)", rc, flush=True)
+rc2 = L.smg_gemm_run_dev(0, m, n, k, cd.data_ptr(), 1, n, 0, ad.data_ptr(), 1, k, bd.data_ptr(), 1, n,
+                         0, 0x3C00, stream)
+print("device strided gemm (scratch pool)", rc2, flush=True)
+torch.cuda.synchronize()
+assert rc == -2 and rc2 == -2 and bool((cd == 0x1234).all())
+assert b"hipMalloc" in L.smg_last_error()
+
+del os.environ["SMG_TEST_FAIL_ALLOC"]
+rc = L.gemm_gpu_f16f16_q4(m, q4._h, c.ctypes.data, a.ctypes.data, None)
+want = orc.matmul_q4_ep(a, quants, scales, None, m, n, k, 32)
+print("host q4 after", rc, max_rel(c, want), flush=True)
+assert rc == 0 and max_rel(c, want) <= f16_tol(k)
+rc = L.smg_gemm_run_dev(0, m, n, k, cd.data_ptr(), 1, n, 0, ad.data_ptr(), 1, k, bd.data_ptr(), 1, n,
+                        0, 0x3C00, stream)
+torch.cuda.synchronize()
+got = cd.cpu().numpy().view(np.uint16)
+print("device strided gemm after", rc, max_rel(got, orc.gemm16(a, b, m, n, k)), flush=True)
+assert rc == 0 and max_rel(got, orc.gemm16(a, b, m, n, k)) <= f16_tol(k)
+print("alloc-fail ok", flush=True)
+"""
+
+
+def test_forced_allocation_failure_returns_enomem_and_leaves_output_untouched():
+    """With SMG_TEST_FAIL_ALLOC=1 every device allocation fails: the host
+    entry points (staging), weight creation and the device forms (scratch
+    pool) return SMG_ENOMEM with dst untouched -- the reference's callers take
+    their portable path on that (src/kernels/q4/matmul.rs:85-89) -- and once
+    the variable is gone the same calls succeed. Run in a child process: the
+    staging area and the scratch pool are kept once allocated, so only a
+    process that has not allocated them yet sees the failure."""
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    env = dict(os.environ)
+    env.pop("SMG_TEST_FAIL_ALLOC", None)
+    r = subprocess.run([sys.executable, "-c", _ALLOC_FAIL_CHILD, here, os.path.join(root, "sme-gemm_amd"),
+                        os.path.join(root, "oracle")], env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and "alloc-fail ok" in r.stdout, r.stdout + r.stderr
+
+
+def _hip_runtime():
+    """The HIP runtime this process has loaded (torch's), through ctypes."""
+    with open("/proc/self/maps") as f:
+        paths = {ln.split()[-1] for ln in f if "libamdhip64.so" in ln}
+    assert paths, "no HIP runtime mapped"
+    return C.CDLL(sorted(paths)[0])
+
+
+def _query_says_unreadable(hip, ptr):
+    """True when hipPointerGetAttributes reports ptr as memory no device can
+    read (the query fails, or names it unregistered); the error a failed
+    query leaves is cleared so no later call reports it."""
+    class Attr(C.Structure):
+        _fields_ = [("type", C.c_int), ("device", C.c_int), ("devicePointer", C.c_void_p),
+                    ("hostPointer", C.c_void_p), ("isManaged", C.c_int), ("allocationFlags", C.c_uint)]
+    at = Attr()
+    rc = hip.hipPointerGetAttributes(C.byref(at), C.c_void_p(ptr))
+    if rc != 0:
+        hip.hipGetLastError()
+        return True
+    return at.type == 0
+
+
+def test_device_call_refuses_host_operands(smg, orc):
+    """A device call hands its pointers to the kernels, so a pageable host
+    array there (an epilogue operand, A or C) is refused: by the mirror with
+    TypeError / ValueError before any C call, and by the C ABI with SMG_EINVAL
+    and C untouched. The C-level calls are made only where the runtime's own
+    pointer query (the one the library asks) says the memory is not
+    device-readable, so a kernel can never be launched with it. A host call
+    given a device tensor as an epilogue operand is refused by the mirror."""
+    import torch
+    n, k, m = 256, 128, 2
+    _, _, w = _q4(smg, orc, n, k, 7)
+    ad = torch.zeros(m * k, dtype=torch.float16, device="cuda")
+    cd = torch.full((m * n,), 0x1234, dtype=torch.int16, device="cuda")
+    host_col = np.zeros(n, np.uint16)
+    with pytest.raises(TypeError):
+        smg.matmul_q4_ep(ad, w, cd.view(torch.float16), m, smg.Epilogue().add_col(host_col))
+    with pytest.raises(TypeError):
+        smg.matmul_q4_ep(np.zeros(m * k, np.uint16), w, np.zeros(m * n, np.uint16), m,
+                         smg.Epilogue().add_col(torch.zeros(n, dtype=torch.float16, device="cuda")))
+    hip = _hip_runtime()
+    host_a = np.zeros(m * k, np.uint16)
+    if not (_query_says_unreadable(hip, host_col.ctypes.data) and _query_says_unreadable(hip, host_a.ctypes.data)):
+        pytest.skip("the runtime reports pageable host memory as device-readable here")
+    L = smg.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    node = smg.EpNode(4, 0, 0.0, host_col.ctypes.data, 0)
+    arr = (smg.EpNode * 1)(node)
+    desc = smg.EpDesc16(1, C.cast(arr, C.POINTER(smg.EpNode)))
+    rc = L.smg_q4_matmul_dev(m, w._h, cd.data_ptr(), ad.data_ptr(), C.addressof(desc), 0, stream)
+    assert rc == -1 and b"epilogue operand" in L.smg_last_error()
+    rc = L.smg_q4_matmul_dev(m, w._h, cd.data_ptr(), host_a.ctypes.data, None, 0, stream)
+    assert rc == -1 and b"operand pointer" in L.smg_last_error()
+    torch.cuda.synchronize()
+    assert bool((cd == 0x1234).all())
+    # the refusals leave no error behind: a correct device call still runs
+    rc = L.smg_q4_matmul_dev(m, w._h, cd.data_ptr(), ad.data_ptr(), None, 0, stream)
+    torch.cuda.synchronize()
+    assert rc == 0 and bool((cd.view(torch.float16) == 0).all())
