@@ -527,7 +527,9 @@ __device__ __forceinline__ uint16_t finish(const EpArgs &ep, float acc, size_t i
 // (depths 8w..8w+7) holds depth 8w+2e at bits 4e..4e+3 and depth 8w+2e+1 at
 // bits 16+4e..16+4e+3 (e = 0..3), so ((dword >> 4e) & 0x000F000F) yields the
 // consecutive pair (8w+2e, 8w+2e+1) in two half-words. The stored nibble is
-// the reference's nibble (code two's complement, q4/mod.rs:213-214).
+// code + 8 (0..15): the reference's two's-complement nibble
+// (q4/mod.rs:205-214) with its top bit flipped at upload, so the dequant
+// subtracts a constant instead of sign-extending.
 // Scales (and mins): cell (kb = d/block, j) of an f16 grid of sc_rows rows.
 //
 // Low-bit (Q2 / Q1) layouts are cut for v_mfma_i32_16x16x64_i8, whose A
