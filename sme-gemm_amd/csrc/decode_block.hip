@@ -32,15 +32,43 @@ namespace smg {
 
 namespace {
 
+// Cross-lane reductions on DPP (a VALU operand modifier, no LDS round trip):
+// within a 16-lane row, quad_perm [1,0,3,2] and [2,3,0,1] pair lanes i ^ 1
+// and i ^ 2 (each lane then holds its quad's total), row_half_mirror pairs
+// lane i with 7 - i (the other quad of its half row) and row_mirror pairs i
+// with 15 - i (the other half row). Each pair adds the same two values, so
+// every lane of a group ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int G>  // aligned groups of G lanes, G = 8, 16 or 32
+__device__ __forceinline__ float dpp_group_sum(float v) {
+    v = v + dppf<0xB1>(v);
+    v = v + dppf<0x4E>(v);
+    v = v + dppf<0x141>(v);
+    if constexpr (G > 8) v = v + dppf<0x140>(v);
+    if constexpr (G > 16) v = v + __shfl_xor(v, 16);
+    return v;
+}
+__device__ __forceinline__ float row_max16(float v) {
+    v = fmaxf(v, dppf<0xB1>(v));
+    v = fmaxf(v, dppf<0x4E>(v));
+    v = fmaxf(v, dppf<0x141>(v));
+    return fmaxf(v, dppf<0x140>(v));
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+// Over the wave: the four rows' totals read into scalars and combined in
+// row order (the result is uniform: every lane holds the same bits).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    return v;  // every lane holds the same bits (each pair adds the same two values)
+    v = dpp_group_sum<16>(v);
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
+    v = row_max16(v);
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 __device__ __forceinline__ float4 bload16f(rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
@@ -342,13 +370,6 @@ constexpr int AT_T = 256;    // threads
 constexpr int AT_KPS = 64;   // keys per split (one per lane of the softmax wave)
 constexpr int AT_HC = 4;     // query heads per workgroup (a chunk of one KV head's group)
 
-// Reduction over aligned groups of G lanes (a power of two up to 32).
-template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
 
 // LPK lanes per key (8 depths each: head_dim <= 8 * LPK). Thread t takes key
 // slot t / LPK of each 256/LPK-key step and depths 8 (t % LPK) .. +8; all
@@ -398,7 +419,7 @@ __global__ void __launch_bounds__(AT_T) attn_split(AttnArgs a) {
             for (int w = 0; w < 4; w++)
                 s = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, qw[w]), __builtin_bit_cast(half2_t, kw[w]),
                                            s, false);
-            s = group_sum<LPK>(s);
+            s = dpp_group_sum<LPK>(s);
             if (c == 0) sc[hh][ks + KPI * it] = key < a.len ? s : -INFINITY;
         }
     }
