@@ -629,10 +629,15 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
                                          (uint16_t)(c4[h].y >> 16)};
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
-                    if (b0 + 4 * h + u < nb_live) {
-                        const int32_t sum = KIND == 1 ? 2 * s4[h][u] - q4[h][u] : s4[h][u];
-                        total = fmaf((float)sum, f16_to_f32(sc4[u]) * a4[h][u], total);
-                    }
+                    // a block past K (or past the last group) adds
+                    // fmaf(0, 0, total) == total: total starts at +0 and
+                    // never becomes -0, so its bits are unchanged. Selects,
+                    // not branches, keep the chain one straight line.
+                    const bool live = b0 + 4 * h + u < nb_live;
+                    const int32_t sum = KIND == 1 ? 2 * s4[h][u] - q4[h][u] : s4[h][u];
+                    const float x = live ? (float)sum : 0.0f;
+                    const float y = live ? f16_to_f32(sc4[u]) * a4[h][u] : 0.0f;
+                    total = fmaf(x, y, total);
                 }
             }
         }
