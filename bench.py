@@ -155,7 +155,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="config 1 only")
-    ap.add_argument("--only", default="12345", help="configs to run beside config 1 (digits)")
+    ap.add_argument("--only", default="12345v",
+                    help="configs to run beside config 1 (digits; v: config 1's shape in the bf16 and affine forms)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="16 x 64 MiB device copies first (PMC counter scale)")
     args = ap.parse_args()
@@ -210,6 +211,31 @@ def main():
         "frac_hbm_cold": achieved / HBM_PEAK_GBS,
         "vs_stream_floor": us1 / floors["config1"]["us"]}}
     del ws, calls
+
+    if "v" in only:
+        # ---- the config-1 shape in the other Q4 forms (same kernel family): bf16
+        #      activations and weights, Q4_1 (affine) f16 and bf16 ----
+        forms = {}
+        for name, bf16, affine in (("bf16", True, False), ("affine_f16", False, True),
+                                   ("affine_bf16", True, True)):
+            av, qv, sv, mv = workloads.q4_inputs(m, n, k, seed=0, affine=affine)
+            p = smg.Q4Params(32).affine() if affine else smg.Q4Params(32)
+            wv = smg.Q4Weights.with_params(qv, sv, mv, n, k, p)
+            bv = workloads.q4_bytes(m, n, k, affine=affine)
+            wsv = rotate(wv, bv)
+            avd = to_dev(av)
+            if bf16:
+                avd = avd.view(torch.float16).float().to(torch.bfloat16).view(torch.int16)
+            cv = torch.empty(m * n, dtype=torch.bfloat16 if bf16 else torch.int16, device=dev)
+            if bf16:
+                avd = avd.view(torch.bfloat16)
+            fn = smg.matmul_q4_bf16 if bf16 else smg.matmul_q4
+            callsv = [(lambda w=w: fn(avd, w, cv, m)) for w in wsv]
+            us = timer(callsv, steps, warm)
+            forms[name] = {"bytes": bv, "us_cold": us, "GBps_cold": bv / (us * 1e-6) / 1e9,
+                           "frac_hbm_cold": bv / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+            del wsv, callsv
+        extra["config1_forms"] = forms
 
     if "2" in only:
         # ---- config 2: Q2 ternary, m=1 and m=8, K=4096, N=11008, block 128 ----

@@ -633,4 +633,42 @@ __device__ __forceinline__ uint4 q4_deq8_affine(uint32_t q, half2_t s2, half2_t 
                       __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c3, s2, m2)));
 }
 
+// bf16 weights bf16_RNE(f32(scale) * code [+ f32(min)]), as dequant_q4_bf16
+// rounds them (through f32, src/kernels/q4/weights.rs:198-201): the codes
+// come out of the same bfi step as f16 values (exact small integers), and
+// v_fma_mix_f32 multiplies each by the f16 scale in f32 -- the product has at
+// most 15 significant bits, so it is exact -- adding mf (f32(min), or -0 so
+// that a zero keeps the product's sign) with the one rounding of the f32 sum;
+// v_cvt_pk_bf16_f32 then rounds pairs to bf16 (RNE).
+__device__ __forceinline__ float fma_mix_lo(uint32_t c2, uint32_t s1, float add) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,1,0]" : "=v"(r) : "v"(c2), "v"(s1), "v"(add));
+    return r;
+}
+__device__ __forceinline__ float fma_mix_hi(uint32_t c2, uint32_t s1, float add) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,1,0]" : "=v"(r) : "v"(c2), "v"(s1), "v"(add));
+    return r;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    typedef float float2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const float2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+__device__ __forceinline__ uint4 q4_deq8_bf16(uint32_t q, uint32_t s1, float mf, uint32_t mag_lo, uint32_t mag_hi) {
+    const half2_t off_lo = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const half2_t off_hi = {(_Float16)72.0f, (_Float16)72.0f};
+    const uint32_t q8 = q >> 8;
+    const uint32_t c[4] = {
+        __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, bfi(0x000F000Fu, q, mag_lo)) - off_lo),
+        __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, bfi(0x00F000F0u, q, mag_hi)) - off_hi),
+        __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, bfi(0x000F000Fu, q8, mag_lo)) - off_lo),
+        __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, bfi(0x00F000F0u, q8, mag_hi)) - off_hi)};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] = pack_bf16x2(fma_mix_lo(c[i], s1, mf), fma_mix_hi(c[i], s1, mf));
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 }  // namespace smg

@@ -11,7 +11,8 @@
 //
 // The call is HBM-bound (0.5625 B of weights per MAC at block 32). Two kernels:
 //
-// q4_gemv_mfma (f16, scale-only, block >= 32 -- the decode configuration):
+// q4_gemv_mfma (block >= 32, so one scale and min per chunk; f16 or bf16,
+// scale-only or affine -- f16 scale-only is the decode configuration):
 //   a workgroup of 8 waves owns 16 output columns; wave w takes every 8th
 //   group of 4 chunks (128 depths). Lane (g = lane/16, c = lane%16) loads the
 //   16-byte chunk g of column c, so a wave load reads one contiguous 1 KB run
@@ -22,10 +23,13 @@
 //   packed multiply by the scale is the reference's single RNE rounding -- and
 //   feeds one v_mfma_f32_16x16x32_f16 as the A operand (16 columns x 32
 //   depths), with up to 16 activation rows as the B operand. The matrix core
-//   does the dot products, so VALU work is the dequant alone. The 8 waves'
-//   partial 16x16 tiles are summed through LDS in a fixed order.
+//   does the dot products, so VALU work is the dequant alone. Affine weights
+//   take one packed fma (scale*code + min, one rounding) in place of the
+//   multiply; bf16 weights are formed in f32 (exact product, plus the min)
+//   and rounded to bf16 in pairs, then feed v_mfma_f32_16x16x32_bf16. The 8
+//   waves' partial 16x16 tiles are summed through LDS in a fixed order.
 //
-// q4_gemv_kernel (every other variant: bf16, affine, block < 32): 16 columns x
+// q4_gemv_kernel (blocks shorter than a chunk, and K = 0): 16 columns x
 //   16 lanes along K per workgroup, weights rounded per value, dot products on
 //   VALU. All loads are branch-free (clamped address, then a select) so they
 //   stay in flight together.
@@ -40,7 +44,9 @@ namespace {
 // f16 activations, then the 8 waves' partial tiles summed through LDS in a
 // fixed order and the op-graph at the store.
 // ---------------------------------------------------------------------------
-template <int MR, bool CHAIN>  // rows staged per segment (1, 2, 4, 8); chained call
+// rows staged per segment (1, 2, 4, 8); chained call; bf16 activations and
+// weights; Q4_1 (affine) weights
+template <int MR, bool CHAIN, bool BF16 = false, bool AFFINE = false>
 __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpArgs ep, ChainArgs ch) {
     extern __shared__ __align__(16) uint8_t smem[];
     uint16_t *a_lds = (uint16_t *)smem;          // [MR][MF_SEG]
@@ -51,13 +57,14 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
     const uint32_t col = tile * 16 + (t & 15);    // < n_pad
     bool timed_out = false;  // chained: a wait for A expired (uniform)
     const SrcRows<MR> src(g.lhs, g.m, g.k);
-    const float4_t acc = q4_mfma_mainloop<MR, CHAIN>(g, src, ch, a_lds, col, timed_out);
+    const float4_t acc = q4_mfma_mainloop<MR, CHAIN, SrcRows<MR>, true, BF16, AFFINE>(g, src, ch, a_lds, col,
+                                                                                   timed_out);
     q4_mfma_reduce<MR>(acc, red);
     if (t < 16 * MR) {
         const int cc = t / MR, r = t % MR;
         const float total = tile_total<MR>(red, cc, r);
         const uint32_t j = tile * 16 + cc;
-        if (!timed_out && r < (int)g.m && j < g.n) g.dst[(size_t)r * g.n + j] = finish<false>(ep, total, r, j, g.n);
+        if (!timed_out && r < (int)g.m && j < g.n) g.dst[(size_t)r * g.n + j] = finish<BF16>(ep, total, r, j, g.n);
     }
     if constexpr (CHAIN) {
         if (timed_out && t == 0) __hip_atomic_store(ch.sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -83,7 +90,7 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
 }
 
 // ---------------------------------------------------------------------------
-// Generic GEMV (bf16, affine, block < 32)
+// Generic GEMV (blocks below 32: scales vary inside a chunk; K = 0)
 // ---------------------------------------------------------------------------
 constexpr int TN = 16;        // output columns per workgroup
 constexpr int KL = 16;        // lanes along K per column
@@ -250,11 +257,19 @@ hipError_t launch_variant(const Q4GemvArgs &g, const EpArgs &ep, bool bf16, bool
     return launch_generic<M, true, true>(g, ep, s);
 }
 
-template <int MR, bool CHAIN = false>
+template <int MR, bool CHAIN = false, bool BF16 = false, bool AFFINE = false>
 hipError_t launch_mfma(const Q4GemvArgs &g, const EpArgs &ep, hipStream_t s, const ChainArgs &ch = {}) {
-    hipLaunchKernelGGL((q4_gemv_mfma<MR, CHAIN>), dim3(g.n_pad / 16), dim3(MF_WAVES * 64),
+    hipLaunchKernelGGL((q4_gemv_mfma<MR, CHAIN, BF16, AFFINE>), dim3(g.n_pad / 16), dim3(MF_WAVES * 64),
                        q4_mfma_lds_bytes<MR>(), s, g, ep, ch);
     return hipGetLastError();
+}
+
+template <bool BF16, bool AFFINE>
+hipError_t launch_mfma_rows(const Q4GemvArgs &g, size_t m, const EpArgs &ep, hipStream_t s) {
+    if (m <= 1) return launch_mfma<1, false, BF16, AFFINE>(g, ep, s);
+    if (m <= 2) return launch_mfma<2, false, BF16, AFFINE>(g, ep, s);
+    if (m <= 4) return launch_mfma<4, false, BF16, AFFINE>(g, ep, s);
+    return launch_mfma<8, false, BF16, AFFINE>(g, ep, s);
 }
 
 
@@ -271,11 +286,11 @@ hipError_t launch_q4_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t
         if (m <= 1) return launch_generic<1, false, false>(g, ep, s);
         return launch_generic<8, false, false>(g, ep, s);
     }
-    if (!bf16 && !affine && w.block >= (size_t)Q4_CHUNK) {
-        if (m <= 1) return launch_mfma<1>(g, ep, s);
-        if (m <= 2) return launch_mfma<2>(g, ep, s);
-        if (m <= 4) return launch_mfma<4>(g, ep, s);
-        return launch_mfma<8>(g, ep, s);
+    if (w.block >= (size_t)Q4_CHUNK) {  // one scale (and min) per chunk: the matrix-core GEMV
+        if (!bf16 && !affine) return launch_mfma_rows<false, false>(g, m, ep, s);
+        if (!bf16) return launch_mfma_rows<false, true>(g, m, ep, s);
+        if (!affine) return launch_mfma_rows<true, false>(g, m, ep, s);
+        return launch_mfma_rows<true, true>(g, m, ep, s);
     }
     if (m <= 1) return launch_variant<1>(g, ep, bf16, affine, s);
     if (m <= 2) return launch_variant<2>(g, ep, bf16, affine, s);

@@ -90,7 +90,10 @@ struct SrcRows {
 // MI355X, masking is 0.18 us faster for the lone config-1 GEMV from HBM, and
 // reading everywhere 1.7 us faster over a decode step's five projections,
 // whose wide GEMVs are bound by the VALU the zeroing adds.
-template <int MR, bool CHAIN, class Src, bool MASK_B = true>
+// BF16: bf16 activations and weights (v_mfma_f32_16x16x32_bf16; each weight
+// bf16_RNE(f32(scale) * code [+ f32(min)]), q4_deq8_bf16); AFFINE: Q4_1
+// weights with their mins (f16: q4_deq8_affine).
+template <int MR, bool CHAIN, class Src, bool MASK_B = true, bool BF16 = false, bool AFFINE = false>
 __device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const Src &src,
                                                      const ChainArgs &ch, uint16_t *a_lds, uint32_t col,
                                                      bool &timed_out) {
@@ -115,14 +118,19 @@ __device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const 
         if (a_first) src.load(areg, d0, t);
         // steps of this wave within the segment: chunks sc0 + 4*(wave + 8*u) + grp
         uint4 wq[MF_U];
-        uint16_t sv[MF_U];
+        uint16_t sv[MF_U], mv[MF_U];
 #pragma unroll
         for (int u = 0; u < MF_U; u++) {
             const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
             const uint32_t kcc = kc < last ? kc : last;  // clamped: always a valid load
             wq[u] = *(const uint4 *)(g.nib + cell_index(kcc, col, g.nchunks, g.n_pad) * 16);
-            const uint16_t sl = g.sc[cell_index((kcc * Q4_CHUNK) >> g.block_shift, col, g.sc_rows, g.n_pad)];
+            const size_t si = cell_index((kcc * Q4_CHUNK) >> g.block_shift, col, g.sc_rows, g.n_pad);
+            const uint16_t sl = g.sc[si];
             sv[u] = kc < g.nchunks ? sl : (uint16_t)0;  // a dead step's weights become 0
+            if constexpr (AFFINE) {
+                const uint16_t ml = g.mn[si];
+                mv[u] = kc < g.nchunks ? ml : (uint16_t)0;
+            }
         }
         if constexpr (CHAIN) {
             // the weights stream in while the producer of A finishes; A's
@@ -171,10 +179,26 @@ __device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const 
             const uint32_t words[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
 #pragma unroll
             for (int w = 0; w < 4; w++) {
-                uint4 wa = q4_deq8(words[w], s2, mag_lo, mag_hi);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wa),
-                                                             __builtin_bit_cast(half8_t, abv[u][w]), acc,
-                                                             0, 0, 0);
+                if constexpr (BF16) {
+                    const uint32_t s1 = sv[u];
+                    const float mf = AFFINE ? f16_to_f32(mv[u]) : -0.0f;
+                    const uint4 wa = q4_deq8_bf16(words[w], s1, mf, mag_lo, mag_hi);
+                    typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wa),
+                                                                  __builtin_bit_cast(bf16x8_t, abv[u][w]), acc,
+                                                                  0, 0, 0);
+                } else {
+                    uint4 wa;
+                    if constexpr (AFFINE) {
+                        const half2_t m2 = {__builtin_bit_cast(_Float16, mv[u]), __builtin_bit_cast(_Float16, mv[u])};
+                        wa = q4_deq8_affine(words[w], s2, m2, mag_lo, mag_hi);
+                    } else {
+                        wa = q4_deq8(words[w], s2, mag_lo, mag_hi);
+                    }
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wa),
+                                                                 __builtin_bit_cast(half8_t, abv[u][w]), acc,
+                                                                 0, 0, 0);
+                }
             }
         }
     }

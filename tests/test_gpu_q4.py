@@ -156,6 +156,38 @@ def test_q4_bf16(smg, orc, m, n, k, affine):
     assert max_rel(got, want, bf16=True) <= bf16_tol(k)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("affine", [False, True])
+@pytest.mark.parametrize("block", [32, 64])
+def test_gemv_weights_bitwise(smg, orc, bf16, affine, block):
+    """Every weight the GEMV multiplies, read back exactly: row r of A is one
+    at depth d_r and zero elsewhere, so C[r][j] is the weight (d_r, j) times
+    one plus exact zeros -- it must equal the portable dequant's weight bit
+    for bit (f16: RNE(scale*code [+ min]) once; bf16: through f32,
+    src/kernels/q4/mod.rs:193-257), for the first and last depths of a block,
+    the last depth of K, and the ragged last column."""
+    m, n, k = 8, 200, 300
+    nbk = -(-k // block)
+    rng = np.random.default_rng(block + 2 * affine + bf16)
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(-0.05, 0.05, n * nbk).astype(np.float32))
+    mins = orc.f32_to_f16(rng.uniform(-0.1, 0.1, n * nbk).astype(np.float32)) if affine else None
+    depths = [0, 1, block - 1, block, 2 * block + 5, k - 33, k - 2, k - 1]
+    one = 0x3F80 if bf16 else 0x3C00
+    a = np.zeros((m, k), np.uint16)
+    for r, d in enumerate(depths):
+        a[r, d] = one
+    p = smg.Q4Params(block).affine() if affine else smg.Q4Params(block)
+    w = smg.Q4Weights.with_params(quants, scales, mins, n, k, p)
+    got = np.zeros(m * n, np.uint16)
+    (smg.matmul_q4_bf16 if bf16 else smg.matmul_q4)(a.ravel(), w, got, m)
+    deq = orc.q4_dequant(quants, scales, mins, n, k, block, bf16).reshape(k, n)
+    want = deq[depths]
+    # a weight of -0 times one plus +0 terms sums to +0
+    want = np.where(want == 0x8000, np.uint16(0), want)
+    assert np.array_equal(got.reshape(m, n), want)
+
+
 @pytest.mark.parametrize("m", [1, 4, 20])
 @pytest.mark.parametrize("affine", [False, True])
 def test_q4_band_major_upload_matches_row_major(smg, orc, m, affine):
