@@ -263,8 +263,10 @@ int smg_gemm_run_dev(int bf16, size_t m, size_t n, size_t k, uint16_t *dst, long
                      int read_dst, const uint16_t *lhs, long lhs_cs, long lhs_rs, const uint16_t *rhs,
                      long rhs_cs, long rhs_rs, uint16_t alpha_bits, uint16_t beta_bits, void *stream);
 
-/* Whether an m-row Q4 call runs the GEMV kernel (replaces
- * gemm_sme_f16f16_q4_single, csrc/sme_gemm_api.h:107). */
+/* Whether an m-row Q4 call runs the GEMV kernel whatever the weights' block
+ * (m <= 8; replaces gemm_sme_f16f16_q4_single, csrc/sme_gemm_api.h:107).
+ * Weights with a block of 32 or more also take the GEMV up to 32 rows (one
+ * launch per 16 rows), which this query, given no block, does not report. */
 int gemm_gpu_f16f16_q4_single(size_t m, size_t n, size_t k);
 /* One link of a chain (q4_chained, src/kernels/q4/matmul.rs:116-164); replaces
  * gemm_sme_f16f16_q4_chained (csrc/sme_gemm_api.h:102-105). done / ready are

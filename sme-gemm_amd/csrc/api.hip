@@ -552,10 +552,36 @@ int gather_columns(const smg_weights *a, const smg_weights *b, const std::vector
     return SMG_OK;
 }
 
-// Q4 dispatch: GEMV up to Q4_GEMV_MAX_ROWS rows, MFMA GEMM above.
+// The op-graph of rows r0.. of a call, for a launch whose row 0 is row r0:
+// ROW operands advance by r0 values, TENSOR operands by r0 rows.
+EpArgs ep_from_row(const EpArgs &ea, size_t r0, size_t n) {
+    EpArgs out = ea;
+    for (uint32_t i = 0; i < ea.n_nodes; i++) {
+        EpNode &nd = out.nodes[i];
+        if (op_is_row(nd.op)) nd.ptr = (const uint16_t *)nd.ptr + r0;
+        if (op_is_tensor(nd.op)) nd.ptr = (const uint16_t *)nd.ptr + r0 * (nd.ld ? nd.ld : n);
+    }
+    return out;
+}
+
+// Q4 dispatch: the GEMV where q4_gemv_serves() (up to 8 rows, or 16 with a
+// scale per chunk); up to Q4_GEMV_CHUNK_ROWS rows with a scale per chunk, the
+// 16-row GEMV once per 16 rows (measured at K = 4096: 24 rows take 14 us
+// there against 51 us in the GEMM, whose 128 x 256 tiles leave most compute
+// units idle at N = 4096 to 14336); the MFMA GEMM above.
+constexpr size_t Q4_GEMV_CHUNK_ROWS = 32;
 hipError_t run_q4(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs, const EpArgs &ea,
                   bool bf16, hipStream_t s) {
-    if (m <= Q4_GEMV_MAX_ROWS) return launch_q4_gemv(w, m, dst, lhs, ea, bf16, s);
+    if (q4_gemv_serves(w, m)) return launch_q4_gemv(w, m, dst, lhs, ea, bf16, s);
+    if (m <= Q4_GEMV_CHUNK_ROWS && q4_gemv_serves(w, Q4_GEMV_WIDE_ROWS)) {
+        for (size_t r0 = 0; r0 < m; r0 += Q4_GEMV_WIDE_ROWS) {
+            const size_t rows = std::min(Q4_GEMV_WIDE_ROWS, m - r0);
+            const hipError_t e = launch_q4_gemv(w, rows, dst + r0 * w.n, lhs + r0 * w.k, ep_from_row(ea, r0, w.n),
+                                                bf16, s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     return launch_gemm(w, m, dst, 1, (long)w.n, lhs, 1, (long)w.k, 1.0f, ea, bf16, s);
 }
 

@@ -93,6 +93,7 @@ __device__ __forceinline__ float rms_scale(float ss, uint32_t k, float eps) {
 // h = f16((x - 0) * r * w + 0), norm_row's expression (nn.rs:142), with r from
 // the whole row.
 struct SrcNormRow {
+    static constexpr int SEG_D = MF_SEG;
     struct Regs {
         float4 x0, x1, w0, w1;
     };

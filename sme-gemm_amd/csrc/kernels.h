@@ -25,9 +25,17 @@ struct WDev {
     size_t k_pad;           // dense: K padded to a multiple of 64
 };
 
-// Rows at or below which the Q4 path runs the GEMV kernel.
+// Rows at or below which the Q4 path runs the GEMV kernel; up to
+// Q4_GEMV_WIDE_ROWS when the weights have one scale per 32-depth chunk (block
+// >= 32) and k > 0, which the matrix-core GEMV serves with all 16 rows of its
+// B operand (a 128-row GEMM tile would multiply mostly zero rows).
 constexpr size_t Q4_GEMV_MAX_ROWS = 8;
+constexpr size_t Q4_GEMV_WIDE_ROWS = 16;
+inline bool q4_gemv_serves(const WDev &w, size_t m) {
+    return m <= Q4_GEMV_MAX_ROWS || (m <= Q4_GEMV_WIDE_ROWS && w.block >= 32 && w.nchunks > 0);
+}
 
+// The Q4 GEMV for calls q4_gemv_serves() accepts; hipErrorNotSupported otherwise.
 hipError_t launch_q4_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
                           const EpArgs &ep, bool bf16, hipStream_t s);
 

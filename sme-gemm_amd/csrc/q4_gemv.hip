@@ -56,9 +56,10 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
     const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
     const uint32_t col = tile * 16 + (t & 15);    // < n_pad
     bool timed_out = false;  // chained: a wait for A expired (uniform)
-    const SrcRows<MR> src(g.lhs, g.m, g.k);
-    const float4_t acc = q4_mfma_mainloop<MR, CHAIN, SrcRows<MR>, true, BF16, AFFINE>(g, src, ch, a_lds, col,
-                                                                                   timed_out);
+    constexpr int U = MR > 8 ? 2 : MF_U;  // 16 rows: half segments (64 KB staged)
+    const SrcRows<MR, U * 1024> src(g.lhs, g.m, g.k);
+    const float4_t acc = q4_mfma_mainloop<MR, CHAIN, SrcRows<MR, U * 1024>, true, BF16, AFFINE, U>(
+        g, src, ch, a_lds, col, timed_out);
     q4_mfma_reduce<MR>(acc, red);
     if (t < 16 * MR) {
         const int cc = t / MR, r = t % MR;
@@ -259,8 +260,9 @@ hipError_t launch_variant(const Q4GemvArgs &g, const EpArgs &ep, bool bf16, bool
 
 template <int MR, bool CHAIN = false, bool BF16 = false, bool AFFINE = false>
 hipError_t launch_mfma(const Q4GemvArgs &g, const EpArgs &ep, hipStream_t s, const ChainArgs &ch = {}) {
-    hipLaunchKernelGGL((q4_gemv_mfma<MR, CHAIN, BF16, AFFINE>), dim3(g.n_pad / 16), dim3(MF_WAVES * 64),
-                       q4_mfma_lds_bytes<MR>(), s, g, ep, ch);
+    constexpr size_t lds = q4_mfma_lds_bytes<MR, (MR > 8 ? 2 : MF_U)>();
+    hipLaunchKernelGGL((q4_gemv_mfma<MR, CHAIN, BF16, AFFINE>), dim3(g.n_pad / 16), dim3(MF_WAVES * 64), lds, s,
+                       g, ep, ch);
     return hipGetLastError();
 }
 
@@ -269,7 +271,8 @@ hipError_t launch_mfma_rows(const Q4GemvArgs &g, size_t m, const EpArgs &ep, hip
     if (m <= 1) return launch_mfma<1, false, BF16, AFFINE>(g, ep, s);
     if (m <= 2) return launch_mfma<2, false, BF16, AFFINE>(g, ep, s);
     if (m <= 4) return launch_mfma<4, false, BF16, AFFINE>(g, ep, s);
-    return launch_mfma<8, false, BF16, AFFINE>(g, ep, s);
+    if (m <= 8) return launch_mfma<8, false, BF16, AFFINE>(g, ep, s);
+    return launch_mfma<16, false, BF16, AFFINE>(g, ep, s);
 }
 
 
@@ -277,6 +280,7 @@ hipError_t launch_mfma_rows(const Q4GemvArgs &g, size_t m, const EpArgs &ep, hip
 
 hipError_t launch_q4_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
                           const EpArgs &ep, bool bf16, hipStream_t s) {
+    if (!q4_gemv_serves(w, m)) return hipErrorNotSupported;
     const Q4GemvArgs g = q4_gemv_args(w, m, dst, lhs);
     const bool affine = w.mins != nullptr;
     if ((size_t)m * w.k * 2 >= ((size_t)1 << 31)) return hipErrorInvalidValue;  // buffer range

@@ -58,8 +58,9 @@ __device__ __forceinline__ bool chain_wait(const unsigned long long *ready, unsi
 // A source loads thread t's share of a segment (`load`, issued before the
 // weight loads) into its Regs and writes the segment's f16 rows to LDS
 // (`stage`, all threads, between two barriers).
-template <int MR>
+template <int MR, int SEG = MF_SEG>
 struct SrcRows {
+    static constexpr int SEG_D = SEG;  // depths staged per segment (the LDS row stride)
     struct Regs {
         uint4 r[MR];
     };
@@ -68,14 +69,18 @@ struct SrcRows {
     bool vec;
     __device__ SrcRows(const uint16_t *lhs, uint32_t m_, uint32_t k_)
         : ar(make_rsrc(lhs, m_ * k_ * 2u)), m(m_), k(k_), vec((k_ & 7) == 0) {}
-    // thread t's 8 depths d0 + 8t .. +8 of every row
+    // thread t's 8 depths d0 + 8t .. +8 of every row (threads past the
+    // segment load and stage nothing)
+    static constexpr bool ALL = SEG >= 8 * MF_WAVES * 64;  // every thread has depths of the segment
     __device__ void load(Regs &a, uint32_t d0, int t) const {
 #pragma unroll
-        for (int r = 0; r < MR; r++) a.r[r] = load_row8(ar, r, m, k, d0 + 8 * t, vec);
+        for (int r = 0; r < MR; r++)
+            a.r[r] = ALL || 8 * t < SEG ? load_row8(ar, r, m, k, d0 + 8 * t, vec) : make_uint4(0, 0, 0, 0);
     }
     __device__ void stage(uint16_t *a_lds, const Regs &a, int t) const {
 #pragma unroll
-        for (int r = 0; r < MR; r++) *(uint4 *)(a_lds + r * MF_SEG + 8 * t) = a.r[r];
+        for (int r = 0; r < MR; r++)
+            if (ALL || 8 * t < SEG) *(uint4 *)(a_lds + r * SEG + 8 * t) = a.r[r];
     }
 };
 
@@ -93,10 +98,16 @@ struct SrcRows {
 // BF16: bf16 activations and weights (v_mfma_f32_16x16x32_bf16; each weight
 // bf16_RNE(f32(scale) * code [+ f32(min)]), q4_deq8_bf16); AFFINE: Q4_1
 // weights with their mins (f16: q4_deq8_affine).
-template <int MR, bool CHAIN, class Src, bool MASK_B = true, bool BF16 = false, bool AFFINE = false>
+// U: steps per lane per segment (a segment is U * 1024 depths; Src::SEG_D
+// must match): 4, or 2 for 16 rows, whose staged segment then fits 64 KB.
+template <int MR, bool CHAIN, class Src, bool MASK_B = true, bool BF16 = false, bool AFFINE = false,
+          int U = MF_U>
 __device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const Src &src,
                                                      const ChainArgs &ch, uint16_t *a_lds, uint32_t col,
                                                      bool &timed_out) {
+    constexpr int SEG_CH = 4 * MF_WAVES * U;  // chunks per segment
+    constexpr int SEG = SEG_CH * Q4_CHUNK;    // depths per segment
+    static_assert(SEG == Src::SEG_D, "the source stages the segment the loop multiplies");
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int c = lane & 15, grp = lane >> 4;
@@ -106,9 +117,9 @@ __device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const 
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
     timed_out = false;
     const uint32_t last = g.nchunks - 1;  // nchunks >= 1 here
-    const uint32_t nseg = (g.nchunks + MF_SEG_CH - 1) / MF_SEG_CH;
+    const uint32_t nseg = (g.nchunks + SEG_CH - 1) / SEG_CH;
     for (uint32_t seg = 0; seg < nseg; seg++) {
-        const uint32_t sc0 = seg * MF_SEG_CH;
+        const uint32_t sc0 = seg * SEG_CH;
         // A[:, segment] first: vmcnt retires in issue order, so loads issued
         // before the weights can be waited on while the weights stay in flight
         const uint32_t d0 = sc0 * Q4_CHUNK;
@@ -117,10 +128,10 @@ __device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const 
         if constexpr (CHAIN) a_first = ch.ready == nullptr;
         if (a_first) src.load(areg, d0, t);
         // steps of this wave within the segment: chunks sc0 + 4*(wave + 8*u) + grp
-        uint4 wq[MF_U];
-        uint16_t sv[MF_U], mv[MF_U];
+        uint4 wq[U];
+        uint16_t sv[U], mv[U];
 #pragma unroll
-        for (int u = 0; u < MF_U; u++) {
+        for (int u = 0; u < U; u++) {
             const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
             const uint32_t kcc = kc < last ? kc : last;  // clamped: always a valid load
             wq[u] = *(const uint4 *)(g.nib + cell_index(kcc, col, g.nchunks, g.n_pad) * 16);
@@ -138,7 +149,7 @@ __device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const 
             if (ch.ready) {
                 __shared__ uint32_t seg_ok;
                 if (t == 0) {
-                    const uint32_t need = g.k < d0 + MF_SEG ? g.k : d0 + MF_SEG;
+                    const uint32_t need = g.k < d0 + SEG ? g.k : d0 + SEG;
                     seg_ok = chain_wait(ch.ready, need, ch.wait_ticks) ? 1u : 0u;
                 }
                 __syncthreads();
@@ -158,23 +169,23 @@ __device__ __forceinline__ float4_t q4_mfma_mainloop(const Q4GemvArgs &g, const 
         // Chunks past K read the staged zeros of the segment and have zero
         // weights. All of this wave's activation fragments are read first, so
         // the LDS round trips overlap instead of each one preceding its MFMA.
-        const uint16_t *arow = a_lds + (c < MR ? c : MR - 1) * MF_SEG;
-        uint4 abv[MF_U][4];
+        const uint16_t *arow = a_lds + (c < MR ? c : MR - 1) * SEG;
+        uint4 abv[U][4];
         if (!MASK_B || c < MR) {
 #pragma unroll
-            for (int u = 0; u < MF_U; u++) {
+            for (int u = 0; u < U; u++) {
                 const uint32_t kcl = 4 * (wave + MF_WAVES * u) + grp;  // chunk within the segment
 #pragma unroll
                 for (int w = 0; w < 4; w++) abv[u][w] = *(const uint4 *)(arow + kcl * Q4_CHUNK + w * 8);
             }
         } else {
 #pragma unroll
-            for (int u = 0; u < MF_U; u++)
+            for (int u = 0; u < U; u++)
 #pragma unroll
                 for (int w = 0; w < 4; w++) abv[u][w] = make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
-        for (int u = 0; u < MF_U; u++) {
+        for (int u = 0; u < U; u++) {
             const half2_t s2 = {__builtin_bit_cast(_Float16, sv[u]), __builtin_bit_cast(_Float16, sv[u])};
             const uint32_t words[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
 #pragma unroll
@@ -274,11 +285,12 @@ __device__ __forceinline__ float tile_total(const float *red, int cc, int r) {
     return total;
 }
 
-// LDS bytes of a q4_mfma_mainloop kernel staging MR rows (also covers red).
-template <int MR>
+// LDS bytes of a q4_mfma_mainloop kernel staging MR rows of a U-step segment
+// (also covers red).
+template <int MR, int U = MF_U>
 constexpr size_t q4_mfma_lds_bytes() {
-    return (size_t)MR * MF_SEG * 2 > (size_t)MF_WAVES * 16 * MR * 4 ? (size_t)MR * MF_SEG * 2
-                                                                     : (size_t)MF_WAVES * 16 * MR * 4;
+    return (size_t)MR * U * 1024 * 2 > (size_t)MF_WAVES * 16 * MR * 4 ? (size_t)MR * U * 1024 * 2
+                                                                       : (size_t)MF_WAVES * 16 * MR * 4;
 }
 
 inline Q4GemvArgs q4_gemv_args(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs) {

@@ -156,23 +156,25 @@ def test_q4_bf16(smg, orc, m, n, k, affine):
     assert max_rel(got, want, bf16=True) <= bf16_tol(k)
 
 
+@pytest.mark.parametrize("m", [8, 16])
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("affine", [False, True])
 @pytest.mark.parametrize("block", [32, 64])
-def test_gemv_weights_bitwise(smg, orc, bf16, affine, block):
+def test_gemv_weights_bitwise(smg, orc, m, bf16, affine, block):
     """Every weight the GEMV multiplies, read back exactly: row r of A is one
     at depth d_r and zero elsewhere, so C[r][j] is the weight (d_r, j) times
     one plus exact zeros -- it must equal the portable dequant's weight bit
     for bit (f16: RNE(scale*code [+ min]) once; bf16: through f32,
     src/kernels/q4/mod.rs:193-257), for the first and last depths of a block,
     the last depth of K, and the ragged last column."""
-    m, n, k = 8, 200, 300
+    n, k = 200, 300
     nbk = -(-k // block)
-    rng = np.random.default_rng(block + 2 * affine + bf16)
+    rng = np.random.default_rng(block + 2 * affine + bf16 + m)
     quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
     scales = orc.f32_to_f16(rng.uniform(-0.05, 0.05, n * nbk).astype(np.float32))
     mins = orc.f32_to_f16(rng.uniform(-0.1, 0.1, n * nbk).astype(np.float32)) if affine else None
-    depths = [0, 1, block - 1, block, 2 * block + 5, k - 33, k - 2, k - 1]
+    depths = [0, 1, block - 1, block, 2 * block + 5, k - 33, k - 2, k - 1,
+              2, 31, 32, 63, 64, 100, 200, 255][:m]
     one = 0x3F80 if bf16 else 0x3C00
     a = np.zeros((m, k), np.uint16)
     for r, d in enumerate(depths):
@@ -186,6 +188,36 @@ def test_gemv_weights_bitwise(smg, orc, bf16, affine, block):
     # a weight of -0 times one plus +0 terms sums to +0
     want = np.where(want == 0x8000, np.uint16(0), want)
     assert np.array_equal(got.reshape(m, n), want)
+
+
+@pytest.mark.parametrize("m", [9, 12, 16, 24, 32])
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("affine", [False, True])
+@pytest.mark.parametrize("n,k", [(200, 300), (1030, 4099), (4096, 4096)])
+def test_q4_wide_gemv_rows(smg, orc, m, bf16, affine, n, k):
+    """9-16 rows with a scale per chunk run the matrix-core GEMV with all 16
+    B-operand rows (half segments of 2048 depths staged), 17-32 rows as one
+    such launch per 16 rows: against the portable path, with an op-graph
+    whose ROW and (padded) TENSOR operands must follow each launch's rows."""
+    block = 32
+    nbk = -(-k // block)
+    rng = np.random.default_rng(m * 7 + n + k + bf16 + 2 * affine)
+    cv = orc.f32_to_bf16 if bf16 else orc.f32_to_f16
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.002, 0.01, n * nbk).astype(np.float32))
+    mins = orc.f32_to_f16(rng.uniform(-0.02, 0.02, n * nbk).astype(np.float32)) if affine else None
+    a = cv(rng.uniform(-0.5, 0.5, m * k).astype(np.float32))
+    row = cv(rng.uniform(-0.5, 0.5, m).astype(np.float32))
+    ld = n + 3
+    ten = cv(rng.uniform(-0.5, 0.5, m * ld).astype(np.float32))
+    p = smg.Q4Params(block).affine() if affine else smg.Q4Params(block)
+    w = smg.Q4Weights.with_params(quants, scales, mins, n, k, p)
+    got = np.zeros(m * n, np.uint16)
+    fn = smg.matmul_q4_bf16_ep if bf16 else smg.matmul_q4_ep
+    fn(a, w, got, m, smg.Epilogue(bf16=bf16).add_row(row).add_tensor(ten, ld).relu())
+    want = orc.matmul_q4_ep(a, quants, scales, mins, m, n, k, block,
+                            [(2, 0, 0.0, row, 0), (6, 0, 0.0, ten, ld)], 1, bf16)
+    assert max_rel(got, want, bf16) <= (bf16_tol(k) if bf16 else f16_tol(k))
 
 
 @pytest.mark.parametrize("m", [1, 4, 20])
