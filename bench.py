@@ -155,8 +155,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="config 1 only")
-    ap.add_argument("--only", default="12345v",
-                    help="configs to run beside config 1 (digits; v: config 1's shape in the bf16 and affine forms)")
+    ap.add_argument("--only", default="12345vr",
+                    help="configs to run beside config 1 (digits; v: config 1's shape in the bf16 and affine "
+                         "forms; r: 8, 16 and 24 rows at config 1's K)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="16 x 64 MiB device copies first (PMC counter scale)")
     args = ap.parse_args()
@@ -236,6 +237,23 @@ def main():
                            "frac_hbm_cold": bv / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
             del wsv, callsv
         extra["config1_forms"] = forms
+
+    if "r" in only:
+        # ---- a few rows of prefill at config 1's K (the GEMV up to 32 rows) ----
+        rows = {}
+        for nr in (4096, 14336):
+            for mr in (8, 16, 24):
+                ar_, qr_, sr_, _ = workloads.q4_inputs(mr, nr, k, seed=0)
+                wr = smg.Q4Weights(qr_, sr_, nr, k)
+                br = workloads.q4_bytes(mr, nr, k)
+                wsr = rotate(wr, br)
+                ard = to_dev(ar_)
+                cr = torch.empty(mr * nr, dtype=torch.int16, device=dev)
+                callsr = [(lambda w=w: smg.matmul_q4(ard, w, cr, mr)) for w in wsr]
+                us = timer(callsr, steps, warm)
+                rows[f"m{mr}_n{nr}"] = {"bytes": br, "us_cold": us, "GBps_cold": br / (us * 1e-6) / 1e9}
+                del wsr, callsr
+        extra["q4_few_rows_k4096"] = rows
 
     if "2" in only:
         # ---- config 2: Q2 ternary, m=1 and m=8, K=4096, N=11008, block 128 ----

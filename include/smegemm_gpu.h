@@ -17,7 +17,9 @@
  *     are host pointers there.
  *   - Device-pointer entry points (smg_*_dev) are asynchronous on `stream`
  *     (a hipStream_t, NULL = the null stream); lhs, dst and every epilogue
- *     operand pointer are device pointers.
+ *     operand pointer are device pointers (memory the weights' GPU can read:
+ *     its device memory, managed or pinned host memory -- anything else is
+ *     refused with SMG_EINVAL, except while the stream is being captured).
  *   - Safe for concurrent callers on different host threads: each thread gets
  *     its own stream and staging buffers for the host-pointer entry points.
  *
