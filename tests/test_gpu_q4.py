@@ -190,6 +190,29 @@ def test_gemv_weights_bitwise(smg, orc, m, bf16, affine, block):
     assert np.array_equal(got.reshape(m, n), want)
 
 
+@pytest.mark.parametrize("m", [1, 5, 16, 40])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_affine_zero_mins_equals_scale_bitwise(smg, orc, m, bf16):
+    """Q4Form::Scale is exactly Affine with all-zero mins
+    (src/kernels/q4/weights.rs:356-380, positive scales as there): the same
+    call through the affine kernels gives the same bits."""
+    n, k, block = 200, 320, 32
+    nbk = -(-k // block)
+    rng = np.random.default_rng(m + 10 * bf16)
+    cv = orc.f32_to_bf16 if bf16 else orc.f32_to_f16
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.01, 0.03, n * nbk).astype(np.float32))
+    zeros = np.zeros(n * nbk, np.uint16)
+    a = cv(rng.standard_normal(m * k).astype(np.float32))
+    plain = smg.Q4Weights.with_params(quants, scales, None, n, k, smg.Q4Params(block))
+    aff = smg.Q4Weights.with_params(quants, scales, zeros, n, k, smg.Q4Params(block).affine())
+    fn = smg.matmul_q4_bf16 if bf16 else smg.matmul_q4
+    c0, c1 = np.zeros(m * n, np.uint16), np.zeros(m * n, np.uint16)
+    fn(a, plain, c0, m)
+    fn(a, aff, c1, m)
+    assert np.array_equal(c0, c1)
+
+
 @pytest.mark.parametrize("m", [9, 12, 16, 24, 32])
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("affine", [False, True])
