@@ -235,8 +235,8 @@ int ep_args(const ep_desc16 *ep, EpArgs *out, size_t n) {
         if (op_is_tensor(nd.op) && nd.ld != 0 && nd.ld < n)
             return fail(SMG_EINVAL, "epilogue tensor row stride is below n");
         out->nodes[i] = nd;
-        out->fam[i] = (uint8_t)ep_family(nd.op);
-        out->cls[i] = (uint8_t)ep_class(nd.op);
+        out->fam[i] = ep_family(nd.op);
+        out->cls[i] = ep_class(nd.op);
     }
     return SMG_OK;
 }
@@ -835,8 +835,8 @@ int mlp_step(smg_mlp *m, const uint16_t *x16, const float *nx, const float *nw, 
             ea.n_nodes = 1;
             ea.nodes[0].op = EP_OP_ACT;
             ea.nodes[0].aux = m->act;
-            ea.fam[0] = (uint8_t)ep_family(EP_OP_ACT);
-            ea.cls[0] = (uint8_t)ep_class(EP_OP_ACT);
+            ea.fam[0] = ep_family(EP_OP_ACT);
+            ea.cls[0] = ep_class(EP_OP_ACT);
         }
         uint16_t *dst = m->gated ? spare : sc.hid;
         if ((e = run_q4(m->up->d, rows, dst, x16, ea, false, s)) != hipSuccess) return fail(SMG_EHIP, "up projection", e);

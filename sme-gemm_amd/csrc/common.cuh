@@ -123,8 +123,12 @@ struct EpArgs {
     uint32_t n_nodes;
     uint32_t pad;
     EpNode nodes[SMG_MAX_EP_NODES];
-    uint8_t fam[SMG_MAX_EP_NODES];  // ep_family(nodes[i].op), filled on the host
-    uint8_t cls[SMG_MAX_EP_NODES];  // ep_class(nodes[i].op)
+    // ep_family(nodes[i].op) / ep_class(nodes[i].op), filled on the host; 32-bit
+    // words so that a node index held in a scalar register reads them with a
+    // scalar load (a byte at a run-time offset takes a vector load and a wait
+    // for every load in flight, per node)
+    uint32_t fam[SMG_MAX_EP_NODES];
+    uint32_t cls[SMG_MAX_EP_NODES];
 };
 
 // maxNum / minNum with IEEE 754-2019 maximumNumber / minimumNumber results: a
@@ -464,8 +468,13 @@ __device__ __forceinline__ EpPre ep_prefetch(const EpArgs &ep, size_t i, size_t 
 
 // finish() with the first EP_PRE operands taken from ep_prefetch.
 template <bool BF16>
-__device__ __forceinline__ uint16_t finish_pre(const EpArgs &ep, const EpPre &pre, float acc, size_t i,
+__device__ __forceinline__ uint16_t finish_pre(const EpArgs &ep, EpPre pre, float acc, size_t i,
                                                size_t j, size_t n) {
+    // the prefetched elements are first read here: without this the compiler
+    // may convert them right after their loads, waiting there for every load
+    // issued before them
+#pragma unroll
+    for (int q = 0; q < EP_PRE; q++) asm volatile("" : "+v"(pre.raw[q]));
     uint16_t c = from_f32<BF16>(acc);
     if (ep.n_nodes == 0) return c;
     float x = to_f32<BF16>(c);

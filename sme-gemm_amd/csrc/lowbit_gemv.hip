@@ -23,6 +23,8 @@
 //   using sum(q*(2b-1)) = 2*sum(q*b) - sum(q)), B operand = 64 depths x up to 16
 //   rows of q. Sums go to LDS; then one lane per output folds them in block
 //   order -- the only sequential step, and it is one fma per block.
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace smg {
@@ -246,7 +248,7 @@ struct LtArgs {
     // rows quantized beforehand by lowbit_prequant (multi-row calls):
     const int8_t *q;       // [m][kq]
     const float *qs;       // [m][nbq] activation block scales
-    const int32_t *qsum;   // [m][nbq] block sums of q
+    const int32_t *qsum;   // [m][nbq] negated block sums of q
 };
 
 __device__ __forceinline__ float nanmax(float a, float b) {
@@ -286,7 +288,7 @@ __device__ __forceinline__ int32_t group_sum(int32_t a, uint32_t gl) {
     return a;
 }
 
-// LDS: q [MR][kq + 16] i8 | s [MR][nbq] f32 | sum(q) [MR][nbq] i32 |
+// LDS: q [MR][kq + 16] i8 | s [MR][nbq] f32 | -sum(q) [MR][nbq] i32 |
 //      block sums [MR][16 CG][nbq + 4] i32 | scales [16 CG][nbq + 4] f16 | wave partials
 size_t tile_lds_bytes(uint32_t kq, uint32_t nbq, int mr, uint32_t cg) {
     return (size_t)mr * (kq + 16) + (size_t)mr * nbq * 8 + (size_t)mr * 16 * cg * (nbq + 4) * 4 +
@@ -295,8 +297,9 @@ size_t tile_lds_bytes(uint32_t kq, uint32_t nbq, int mr, uint32_t cg) {
 
 // One 4096-depth pass of quantize_row (src/kernels/lowbit/matmul.rs:354-371)
 // over MR rows: thread t holds depths p*4096 + 8t .. +7 of each row in ar[r];
-// q goes to q + r*qstride + depth, the block's s and sum(q) to
-// s[r*nbq + block], sum[r*nbq + block] (sum(q) only for Q1, whose fold uses it).
+// q goes to q + r*qstride + depth, the block's s and -sum(q) to
+// s[r*nbq + block], sum[r*nbq + block] (-sum(q) only for Q1, whose fold adds
+// it to 2*sum(q*b)).
 // A block's amax and sum(q) reduce over its lanes by DPP / shuffles, and
 // through the LDS words wmax / wsum ([MR][WV]) for blocks longer than 512.
 template <int KIND, int MR>
@@ -370,14 +373,14 @@ __device__ __forceinline__ void quant_pass(const uint4 (&ar)[MR], uint32_t p, in
 #pragma unroll
         for (int r = 0; r < MR; r++) {
             s[r * nbq + bb] = __fdiv_rn(am[r], 127.0f);
-            sum_out[r * nbq + bb] = qs[r];
+            sum_out[r * nbq + bb] = -qs[r];
         }
     }
 }
 
 // The multi-row single-launch path quantizes A once per call, here, instead of
 // once per workgroup: one workgroup per (4096-depth pass, row) writes q
-// [m][kq] (zero past k) and the blocks' s and sum(q) [m][nbq].
+// [m][kq] (zero past k) and the blocks' s and -sum(q) [m][nbq].
 template <int KIND>
 __global__ void __launch_bounds__(T) lowbit_prequant(const uint16_t *lhs, uint32_t m, uint32_t k,
                                                      uint32_t kq, uint32_t nbq, uint32_t block_shift,
@@ -469,10 +472,17 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
             wreg[i] = bload16(cr, grp < g.ngroups ? ((uint32_t)cell_index(grp, col0 + c, g.ngroups, g.n_pad) * 4 + gq4) * 16 : OOB);
         }
     }
-    // the epilogue operands last: their addresses wait on the op-graph's
-    // kernel arguments, which must not hold up the codes
+    // this lane's block-sum slot (step 3), computed before the epilogue loads
+    // and pinned to a register of its own: the compiler can otherwise build it
+    // late with a 64-bit multiply-add whose unused high half is a register
+    // one of those loads targets, and wait for that load
+    uint32_t dp_off = (c * ncol + gi * 16 + 4 * gq4) * bs;
+    asm volatile("" : "+v"(dp_off));
     const bool folder = (uint32_t)t < ncol * g.m;
     const int fc = t & (ncol - 1), frow = t >> (4 + g.cg_shift);
+
+    // the epilogue operands last: their addresses wait on the op-graph's
+    // kernel arguments, which must not hold up the codes
     EpPre pre = {};
     if (folder && wg_col0 + fc < g.n) pre = ep_prefetch(ep, frow, wg_col0 + fc, g.n);
 
@@ -509,7 +519,7 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
     //       of expanded codes, B = 64 depths x up to 16 rows of q
     // lane (gq4, c) holds the sums of columns 4*gq4 + v, row c; rows m..MR-1
     // of q are zero, so their sums are too
-    int32_t *dp = sb + (c * ncol + gi * 16 + 4 * gq4) * bs;
+    int32_t *dp = sb + dp_off;
     auto expand = [&](int i) {
         const uint4 wv = wreg[i / SPG];
         const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
@@ -602,7 +612,11 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
     __syncthreads();
 
     // -- 4. fold in block order (reference, matmul.rs:380-393): four blocks'
-    //       sums, scales and factors per LDS load
+    //       sums, scales and factors per LDS load; per block one shift-add
+    //       (Q1: 2*sum(q*b) + (-sum(q))), one conversion, the product
+    //       f32(scale)*s by v_fma_mix (the f16 operand widened exactly, one
+    //       rounding; the -0 addend leaves every product as it is) and
+    //       the fma
     if (folder) {
         const int32_t *sp = sb + (frow * ncol + fc) * bs;
         const uint16_t *cp = scl + fc * bs;
@@ -610,14 +624,17 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
         const int32_t *qp = as + frow * nbq;
         const uint32_t nb_live = (g.k + block - 1) >> g.block_shift;
         float total = 0.0f;
-        for (uint32_t b0 = 0; b0 < nb_live; b0 += 16) {
-            // 16 blocks' operands in flight before the fma chain
+        // 16 blocks from b0; TAIL: some are past K, and add
+        // fmaf(0, 0, total) == total (total starts at +0 and never
+        // becomes -0, so its bits are unchanged) by selects, not branches
+        auto group16 = [&](uint32_t b0, auto tail_tag) {
+            constexpr bool TAIL = decltype(tail_tag)::value;
             int4_t s4[4], q4[4];
             uint2 c4[4];
             float4_t a4[4];
 #pragma unroll
-            for (int h = 0; h < 4; h++) {
-                const uint32_t bh = b0 + 4 * h < nbq ? b0 + 4 * h : 0;
+            for (int h = 0; h < 4; h++) {  // 16 blocks' operands in flight before the fma chain
+                const uint32_t bh = !TAIL || b0 + 4 * h < nbq ? b0 + 4 * h : 0;
                 s4[h] = *(const int4_t *)(sp + bh);
                 c4[h] = *(const uint2 *)(cp + bh);
                 a4[h] = *(const float4_t *)(ap + bh);
@@ -625,22 +642,30 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
             }
 #pragma unroll
             for (int h = 0; h < 4; h++) {
-                const uint16_t sc4[4] = {(uint16_t)c4[h].x, (uint16_t)(c4[h].x >> 16), (uint16_t)c4[h].y,
-                                         (uint16_t)(c4[h].y >> 16)};
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
-                    // a block past K (or past the last group) adds
-                    // fmaf(0, 0, total) == total: total starts at +0 and
-                    // never becomes -0, so its bits are unchanged. Selects,
-                    // not branches, keep the chain one straight line.
-                    const bool live = b0 + 4 * h + u < nb_live;
-                    const int32_t sum = KIND == 1 ? 2 * s4[h][u] - q4[h][u] : s4[h][u];
-                    const float x = live ? (float)sum : 0.0f;
-                    const float y = live ? f16_to_f32(sc4[u]) * a4[h][u] : 0.0f;
+                    const int32_t sum = KIND == 1 ? 2 * s4[h][u] + q4[h][u] : s4[h][u];
+                    const uint32_t cw = u < 2 ? c4[h].x : c4[h].y;
+                    float y;
+                    if (u % 2 == 0)
+                        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]"
+                            : "=v"(y) : "v"(cw), "v"(a4[h][u]), "v"(-0.0f));
+                    else
+                        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                            : "=v"(y) : "v"(cw), "v"(a4[h][u]), "v"(-0.0f));
+                    float x = (float)sum;
+                    if constexpr (TAIL) {
+                        const bool live = b0 + 4 * h + u < nb_live;
+                        x = live ? x : 0.0f;
+                        y = live ? y : 0.0f;
+                    }
                     total = fmaf(x, y, total);
                 }
             }
-        }
+        };
+        const uint32_t nb_full = nb_live & ~15u;
+        for (uint32_t b0 = 0; b0 < nb_full; b0 += 16) group16(b0, std::false_type{});
+        if (nb_full < nb_live) group16(nb_full, std::true_type{});
         const uint32_t j = wg_col0 + fc;
         if (j < g.n) g.dst[(size_t)frow * g.n + j] = finish_pre<false>(ep, pre, total, frow, j, g.n);
     }
