@@ -137,8 +137,7 @@ __device__ __forceinline__ void b_load(const GemmArgs &g, uint32_t col0, uint32_
 // PD: blocks shorter than a thread's UD depths, so scales vary per depth
 // (a separate instantiation keeps that rare path out of the common kernel).
 template <int WK, bool BF16, bool AFFINE, int UD, bool PD>
-__device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, uint32_t k0,
-                                        const BRegs<UD> &r, uint16_t *blds) {
+__device__ __forceinline__ void b_store(const GemmArgs &g, uint32_t col0, const BRegs<UD> &r, uint16_t *blds) {
     const int t = threadIdx.x;
     const int cl = t % 128;
     const int dl = (t / 128) * UD;
@@ -397,11 +396,11 @@ __global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
     a_load<VECA>(g, row0, BK, ra1);
     b_load<WK, UD>(g, col0, BK, rb1);
     a_store(ra0, lds);
-    b_store<WK, BF16, AFFINE, UD, PD>(g, col0, 0, rb0, lds + BM * LDS_STRIDE);
+    b_store<WK, BF16, AFFINE, UD, PD>(g, col0, rb0, lds + BM * LDS_STRIDE);
     a_load<VECA>(g, row0, 2 * BK, ra0);
     b_load<WK, UD>(g, col0, 2 * BK, rb0);
     a_store(ra1, lds + STAGE);
-    b_store<WK, BF16, AFFINE, UD, PD>(g, col0, BK, rb1, lds + STAGE + BM * LDS_STRIDE);
+    b_store<WK, BF16, AFFINE, UD, PD>(g, col0, rb1, lds + STAGE + BM * LDS_STRIDE);
     __syncthreads();
 
     uint4 fa0[4], fb0[4], fa1[4], fb1[4];  // kk = 0 / kk = 32 halves
@@ -418,7 +417,7 @@ __global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
             a_load<VECA>(g, row0, (ks + 3) * BK, ra1);
             b_load<WK, UD>(g, col0, (ks + 3) * BK, rb1);
             a_store(ra0, lds + s2 * STAGE);
-            b_store<WK, BF16, AFFINE, UD, PD>(g, col0, (ks + 2) * BK, rb0, lds + s2 * STAGE + BM * LDS_STRIDE);
+            b_store<WK, BF16, AFFINE, UD, PD>(g, col0, rb0, lds + s2 * STAGE + BM * LDS_STRIDE);
             mma_half<BF16>(fa1, fb1, acc);
             __syncthreads();
             s_cur = s1;
@@ -432,7 +431,7 @@ __global__ void __launch_bounds__(BM * 2) gemm_kernel(GemmArgs g, EpArgs ep) {
             a_load<VECA>(g, row0, (ks + 4) * BK, ra0);
             b_load<WK, UD>(g, col0, (ks + 4) * BK, rb0);
             a_store(ra1, lds + s2 * STAGE);
-            b_store<WK, BF16, AFFINE, UD, PD>(g, col0, (ks + 3) * BK, rb1, lds + s2 * STAGE + BM * LDS_STRIDE);
+            b_store<WK, BF16, AFFINE, UD, PD>(g, col0, rb1, lds + s2 * STAGE + BM * LDS_STRIDE);
             mma_half<BF16>(fa1, fb1, acc);
             __syncthreads();
             s_cur = s1;

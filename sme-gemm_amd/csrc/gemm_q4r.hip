@@ -441,7 +441,7 @@ hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long 
     g.codes = w.codes;
     g.sc = w.scales;
     g.mn = w.mins;
-    g.st = {dst, dst_rs, dst_cs, (uint32_t)m, (uint32_t)w.n};
+    g.st = {dst, dst_rs, dst_cs, (uint32_t)m, (uint32_t)w.n, 0.0f, 0u};
     g.beta = beta;
     g.lhs_rs = lhs_rs;
     g.m = (uint32_t)m;

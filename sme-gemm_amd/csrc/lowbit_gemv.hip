@@ -279,14 +279,6 @@ __device__ __forceinline__ int32_t group_sum_i32(int32_t a, uint32_t gl) {
     if (gl > 32) a += __shfl_xor(a, 32);
     return a;
 }
-__device__ __forceinline__ float group_max(float a, uint32_t gl) {
-    for (uint32_t off = 1; off < gl; off <<= 1) a = nanmax(a, __shfl_xor(a, (int)off));
-    return a;
-}
-__device__ __forceinline__ int32_t group_sum(int32_t a, uint32_t gl) {
-    for (uint32_t off = 1; off < gl; off <<= 1) a += __shfl_xor(a, (int)off);
-    return a;
-}
 
 // LDS: q [MR][kq + 16] i8 | s [MR][nbq] f32 | -sum(q) [MR][nbq] i32 |
 //      block sums [MR][16 CG][nbq + 4] i32 | scales [16 CG][nbq + 4] f16 | wave partials
