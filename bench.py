@@ -157,7 +157,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="config 1 only")
     ap.add_argument("--only", default="12345vr",
                     help="configs to run beside config 1 (digits; v: config 1's shape in the bf16 and affine "
-                         "forms; r: 8, 16 and 24 rows at config 1's K)")
+                         "forms; r: 8 to 128 rows at config 1's K)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="16 x 64 MiB device copies first (PMC counter scale)")
     args = ap.parse_args()
@@ -239,10 +239,12 @@ def main():
         extra["config1_forms"] = forms
 
     if "r" in only:
-        # ---- a few rows of prefill at config 1's K (the GEMV up to 32 rows) ----
+        # ---- rows of prefill at config 1's K: the GEMV up to 32 rows, then the
+        # GEMM with K split over the compute units (its tiles are few), beside
+        # torch's dense f16 GEMM (hipBLASLt) of the same shape ----
         rows = {}
         for nr in (4096, 14336):
-            for mr in (8, 16, 24):
+            for mr in (8, 16, 24, 64, 128):
                 ar_, qr_, sr_, _ = workloads.q4_inputs(mr, nr, k, seed=0)
                 wr = smg.Q4Weights(qr_, sr_, nr, k)
                 br = workloads.q4_bytes(mr, nr, k)
@@ -252,6 +254,15 @@ def main():
                 callsr = [(lambda w=w: smg.matmul_q4(ard, w, cr, mr)) for w in wsr]
                 us = timer(callsr, steps, warm)
                 rows[f"m{mr}_n{nr}"] = {"bytes": br, "us_cold": us, "GBps_cold": br / (us * 1e-6) / 1e9}
+                if mr > 32:
+                    fl = 2.0 * mr * nr * k
+                    ah = ard.view(torch.float16).view(mr, k)
+                    tbs = [torch.randn(k, nr, dtype=torch.float16, device=dev) for _ in range(3)]
+                    tcr = torch.empty(mr, nr, dtype=torch.float16, device=dev)
+                    us_t = timer([(lambda b=b: torch.matmul(ah, b, out=tcr)) for b in tbs], steps, warm)
+                    rows[f"m{mr}_n{nr}"].update({"TFLOPS": fl / (us * 1e-6) / 1e12,
+                                                 "torch_dense_f16_gemm_us": us_t})
+                    del tbs, tcr
                 del wsr, callsr
         extra["q4_few_rows_k4096"] = rows
 

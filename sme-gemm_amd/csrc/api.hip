@@ -567,11 +567,19 @@ EpArgs ep_from_row(const EpArgs &ea, size_t r0, size_t n) {
 // Q4 dispatch: the GEMV where q4_gemv_serves() (up to 8 rows, or 16 with a
 // scale per chunk); up to Q4_GEMV_CHUNK_ROWS rows with a scale per chunk, the
 // 16-row GEMV once per 16 rows (measured at K = 4096: 24 rows take 14 us
-// there against 51 us in the GEMM, whose 128 x 256 tiles leave most compute
-// units idle at N = 4096 to 14336); the MFMA GEMM above.
+// there against 51 us in the unsplit GEMM, whose 128 x 256 tiles leave most
+// compute units idle at N = 4096 to 14336); the MFMA GEMM above, K split over
+// the compute units when its tiles are few and `split` (q4_split_bytes) is
+// given.
 constexpr size_t Q4_GEMV_CHUNK_ROWS = 32;
+bool q4_gemv_rows(const WDev &w, size_t m) {
+    return q4_gemv_serves(w, m) || (m <= Q4_GEMV_CHUNK_ROWS && q4_gemv_serves(w, Q4_GEMV_WIDE_ROWS));
+}
+size_t q4_split_bytes(const WDev &w, size_t m, bool bf16) {
+    return q4_gemv_rows(w, m) || bf16 ? 0 : q4r_split_bytes(w, m);
+}
 hipError_t run_q4(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs, const EpArgs &ea,
-                  bool bf16, hipStream_t s) {
+                  bool bf16, hipStream_t s, void *split, size_t split_bytes) {
     if (q4_gemv_serves(w, m)) return launch_q4_gemv(w, m, dst, lhs, ea, bf16, s);
     if (m <= Q4_GEMV_CHUNK_ROWS && q4_gemv_serves(w, Q4_GEMV_WIDE_ROWS)) {
         for (size_t r0 = 0; r0 < m; r0 += Q4_GEMV_WIDE_ROWS) {
@@ -582,7 +590,24 @@ hipError_t run_q4(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs, c
         }
         return hipSuccess;
     }
+    if (q4r_supported(w, m, 1, (long)w.k, lhs, bf16))
+        return launch_q4r(w, m, dst, 1, (long)w.n, lhs, (long)w.k, 1.0f, ea, (float *)split, split_bytes, s);
     return launch_gemm(w, m, dst, 1, (long)w.n, lhs, 1, (long)w.k, 1.0f, ea, bf16, s);
+}
+
+// Split-K partial sums for the device-pointer callers of run_q4: a pool of
+// its own, so a buffer never aliases the dev_pool() scratch that the caller
+// (the MLP, the decode entry points) may hold on the same stream.
+ScratchPool<HipDevAlloc> &split_pool() {
+    static ScratchPool<HipDevAlloc> *p = new ScratchPool<HipDevAlloc>();  // never destroyed
+    return *p;
+}
+hipError_t run_q4_dev(int device, const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
+                      const EpArgs &ea, bool bf16, hipStream_t s) {
+    const size_t sb = q4_split_bytes(w, m, bf16);
+    void *part = nullptr;
+    if (sb && !(part = split_pool().get(device, s, sb))) return hipErrorOutOfMemory;
+    return run_q4(w, m, dst, lhs, ea, bf16, s, part, sb);
 }
 
 // k == 0: every output is the epilogue applied to +0 (reference GEMM of an
@@ -839,7 +864,7 @@ int mlp_step(smg_mlp *m, const uint16_t *x16, const float *nx, const float *nw, 
             ea.cls[0] = ep_class(EP_OP_ACT);
         }
         uint16_t *dst = m->gated ? spare : sc.hid;
-        if ((e = run_q4(m->up->d, rows, dst, x16, ea, false, s)) != hipSuccess) return fail(SMG_EHIP, "up projection", e);
+        if ((e = run_q4_dev(m->up->device, m->up->d, rows, dst, x16, ea, false, s)) != hipSuccess) return fail(SMG_EHIP, "up projection", e);
         if (m->gated && (e = launch_glu(dst, rows, m->hidden, m->act, 1, sc.hid, s)) != hipSuccess)
             return fail(SMG_EHIP, "glu", e);
     }
@@ -850,7 +875,7 @@ int mlp_step(smg_mlp *m, const uint16_t *x16, const float *nx, const float *nw, 
             return fail(SMG_EHIP, "down projection", e);
     } else {
         uint16_t *out16 = spare + rows * both;
-        if ((e = run_q4(m->down->d, rows, out16, sc.hid, EpArgs{}, false, s)) != hipSuccess)
+        if ((e = run_q4_dev(m->down->device, m->down->d, rows, out16, sc.hid, EpArgs{}, false, s)) != hipSuccess)
             return fail(SMG_EHIP, "down projection", e);
         if ((e = launch_add_f16(out16, rows * d_out, y, s)) != hipSuccess) return fail(SMG_EHIP, "residual add", e);
     }
@@ -1099,10 +1124,11 @@ static int q4_host(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t
     const size_t n = w->d.n, k = w->d.k;
     if (m == 0 || n == 0) return SMG_OK;  // q4/matmul.rs:43-44
     const WDev d = w->d;
+    const size_t sb = q4_split_bytes(d, m, bf16);  // split-K partials in the call's staging
     return host_call(bf16 ? "gemm_gpu_b16b16_q4" : "gemm_gpu_f16f16_q4", w->device, m, n, k, dst,
-                     m * n, false, lhs, m * k, ep, 0,
-                     [&](uint16_t *dd, const uint16_t *dl, const EpArgs &ea, void *, hipStream_t s) {
-                         return run_q4(d, m, dd, dl, ea, bf16, s);
+                     m * n, false, lhs, m * k, ep, sb,
+                     [&](uint16_t *dd, const uint16_t *dl, const EpArgs &ea, void *sc, hipStream_t s) {
+                         return run_q4(d, m, dd, dl, ea, bf16, s, sb ? sc : nullptr, sb);
                      });
 }
 
@@ -1341,7 +1367,7 @@ int smg_q4_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint1
     EpArgs ea;
     if ((rc = ep_args(ep, &ea, w->d.n))) return rc;
     if ((rc = check_dev_ptrs("smg_q4_matmul_dev", w->device, stream, ea, {dst, lhs}))) return rc;
-    hipError_t e = run_q4(w->d, m, dst, lhs, ea, bf16 != 0, (hipStream_t)stream);
+    hipError_t e = run_q4_dev(w->device, w->d, m, dst, lhs, ea, bf16 != 0, (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_q4_matmul_dev", e);
 }
 
@@ -1604,7 +1630,7 @@ int smg_q4_accumulate_dev(size_t m, const smg_weights *w, float *y, const uint16
     } else {
         DecodeScratch sc;
         if ((rc = decode_scratch(w->device, stream, 0, 0, 0, m * w->d.n, 0, &sc))) return rc;
-        e = run_q4(w->d, m, sc.h16, x, EpArgs{}, false, s);
+        e = run_q4_dev(w->device, w->d, m, sc.h16, x, EpArgs{}, false, s);
         if (e == hipSuccess) e = launch_add_f16(sc.h16, m * w->d.n, y, s);
     }
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_q4_accumulate_dev", e);

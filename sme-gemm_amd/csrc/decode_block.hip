@@ -318,19 +318,6 @@ hipError_t launch_blk(const Q4GemvArgs &g, const BlkArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Compute units of the current device (cached per device).
-int device_cus() {
-    static std::atomic<int> cus[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    int v = cus[dev].load(std::memory_order_relaxed);
-    if (v <= 0) {
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-        cus[dev].store(v, std::memory_order_relaxed);
-    }
-    return v;
-}
-
 template <bool NORM, int STORE>
 hipError_t launch_blk_p(const Q4GemvArgs &g, const BlkArgs &a, hipStream_t s) {
     const uint32_t ntiles = g.n_pad / 16;

@@ -23,6 +23,9 @@
 // DMA is issued as soon as step k's stage is free (after step k's barrier),
 // each step's barrier waits only for step k+2's DMA, and a wave reads step
 // k+1's fragments from LDS while its step-k multiplies run.
+#include <algorithm>
+#include <atomic>
+
 #include "kernels.h"
 #include "tile_store.cuh"
 
@@ -36,9 +39,11 @@ constexpr int B_BYTES = 2 * RBN * 16;           // raw Q4: [half][256 columns] 1
 constexpr int S_BYTES = 2 * RBN * 2;            // scales (mins): [half][256 columns] f16
 constexpr int STAGE_BYTES = A_BYTES + B_BYTES + 2 * S_BYTES;
 constexpr int CS = RBN + 8;                     // halfs per staged output row
+constexpr int SP = RBN + 4;                     // floats per staged split-K partial row
 constexpr int NSTAGE = 5;                       // LDS ring depth
 constexpr int PS = 4;                           // DMA instructions per lane per step
 static_assert(RBM * CS * 2 <= NSTAGE * STAGE_BYTES, "store staging exceeds the ring");
+static_assert(RBM * SP * 4 <= NSTAGE * STAGE_BYTES, "partial staging exceeds the ring");
 
 struct RArgs {
     const uint16_t *lhs;
@@ -50,6 +55,10 @@ struct RArgs {
     long lhs_rs;
     uint32_t m, n, k, n_pad, block_shift;
     uint32_t nchunks, sc_rows;  // rows of the code and scale grids
+    // split K (nsplit > 1): slice s of a tile writes its f32 sums to
+    // part[s][row][col] (row stride part_ld floats); q4r_reduce finishes them
+    float *part;
+    uint32_t nsplit, part_ld;
 };
 
 // LDS DMA: each lane's 16 (4) bytes from sbase + voff land at M0 + 16 (4) *
@@ -289,7 +298,7 @@ __device__ __forceinline__ void mma_step(const Half &cur, const Half &nxt, float
     }
 }
 
-template <bool AFFINE>
+template <bool AFFINE, bool SPLIT>
 __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
     __shared__ __align__(16) uint8_t ring[NSTAGE * STAGE_BYTES];
     __shared__ __align__(16) float epv[SMG_MAX_EP_NODES * (RBN + RBM)];
@@ -298,7 +307,17 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
     const int t = threadIdx.x, lane = t % 64;
     const int wave = __builtin_amdgcn_readfirstlane(t / 64);  // uniform: DMA bases, branches
     const int cw = wave % 4, kh = wave / 4;  // column block, half of each step
-    const uint32_t ksteps = g.k / 64;       // >= 1
+    // this workgroup's tile and its steps: all of K, or (SPLIT) slice `slice`
+    // of nsplit, the tile index running fastest so that consecutive
+    // workgroups still share a weight slice
+    uint32_t tile = xcd_tile(blockIdx.x, gridDim.x), slice = 0, ks0 = 0, ksteps = g.k / 64;  // >= 1
+    if constexpr (SPLIT) {
+        const uint32_t tiles = gridDim.x / g.nsplit;
+        slice = tile / tiles;
+        tile %= tiles;
+        ks0 = slice * ksteps / g.nsplit;  // nsplit <= ksteps: every slice has a step
+        ksteps = (slice + 1) * ksteps / g.nsplit - ks0;
+    }
 
     // the bfi magics live in VGPRs (a VOP3 takes one scalar operand)
     uint32_t mag_lo = 0x64006400u, mag_hi = 0x54005400u;
@@ -342,7 +361,7 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
             for (int jt = 0; jt < 4; jt++) acc[i][jt] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
-        for (int j = 0; j < NSTAGE; j++) dma_step(g, d, ring + j * STAGE_BYTES, min((uint32_t)j, last), wave);
+        for (int j = 0; j < NSTAGE; j++) dma_step(g, d, ring + j * STAGE_BYTES, ks0 + min((uint32_t)j, last), wave);
         wait_vm<(NSTAGE - 2) * PS>();  // steps 0 and 1 landed
         barrier_lds();
 
@@ -360,7 +379,7 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
             mma_step<AFFINE>(cur, nxt, acc, bb, mag_lo, mag_hi);
             wait_vm<(NSTAGE - 3) * PS>();
             barrier_lds();
-            dma_step(g, d, ring + (ks % NSTAGE) * STAGE_BYTES, min(ks + NSTAGE, last), wave);
+            dma_step(g, d, ring + (ks % NSTAGE) * STAGE_BYTES, ks0 + min(ks + NSTAGE, last), wave);
         };
         Half h0, h1;
         read_half<AFFINE>(ring0, ro, h0);
@@ -376,7 +395,7 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
 
         float *colv = epv, *rowv = epv + SMG_MAX_EP_NODES * RBN;
         // the op-graph's vectors first: their global loads overlap the exchange
-        ep_load_vectors<false, RBM, RBN, RNT>(g.st, ep, colv, rowv, row0, col0);
+        if constexpr (!SPLIT) ep_load_vectors<false, RBM, RBN, RNT>(g.st, ep, colv, rowv, row0, col0);
 
         // The pair's partial tiles: each wave hands the other the half of its
         // f32 tile that the other finishes (wave w keeps row tiles 0-3, wave
@@ -384,7 +403,10 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
         // lane-contiguous (conflict-free). f32 addition commutes, so either
         // wave's sum is the same value. Then each wave rounds beta * sum to f16
         // into the staged tile ([128][CS]; a lane holds
-        // D[4*(lane/16)+v][lane%16] of each 16x16 tile).
+        // D[4*(lane/16)+v][lane%16] of each 16x16 tile) -- or (SPLIT) stages
+        // the f32 sums ([128][SP]) for all eight waves to write the rows below
+        // m and the columns below part_ld to the slice's part of the partial
+        // buffer, 16 bytes a lane.
         uint16_t *stg = (uint16_t *)ring;
         auto finish_half = [&](auto keep_c) {
             constexpr int KEEP = decltype(keep_c)::value, GIVE = 4 - KEEP;
@@ -399,8 +421,20 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
             for (int i = 0; i < 4; i++)
 #pragma unroll
                 for (int jt = 0; jt < 4; jt++) acc[KEEP + i][jt] += other[(i * 4 + jt) * 64 + lane];
-            __syncthreads();  // the staged tile overwrites the exchange
             const int lr = lane % 16, lg = lane / 16;
+            if constexpr (SPLIT) {
+                __syncthreads();  // the staged tile overwrites the exchange
+                float *sf = (float *)ring;
+#pragma unroll
+                for (int i = KEEP; i < KEEP + 4; i++)
+#pragma unroll
+                    for (int jt = 0; jt < 4; jt++)
+#pragma unroll
+                        for (int v = 0; v < 4; v++)
+                            sf[(i * 16 + lg * 4 + v) * SP + cw * 64 + jt * 16 + lr] = acc[i][jt][v];
+                return;
+            }
+            __syncthreads();  // the staged tile overwrites the exchange
 #pragma unroll
             for (int i = KEEP; i < KEEP + 4; i++)
 #pragma unroll
@@ -416,13 +450,79 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
         else
             finish_half(IntC<4>{});
         __syncthreads();
+        if constexpr (SPLIT) {
+            // thread t: float4 t % 64 of rows t / 64 + 8 j, below m and part_ld
+            const float *sf = (const float *)ring;
+            const uint32_t c4 = (t % 64) * 4;
+            if (col0 + c4 >= g.part_ld) return;
+            float *pp = g.part + ((size_t)slice * g.m + row0) * g.part_ld + col0 + c4;
+#pragma unroll
+            for (int j = 0; j < RBM / 8; j++) {
+                const int r = t / 64 + 8 * j;
+                if (row0 + r >= g.m) break;
+                *(float4_t *)(pp + (size_t)r * g.part_ld) = *(const float4_t *)(sf + r * SP + c4);
+            }
+            return;
+        }
         // Store: groups of 8 columns through the op-graph by all eight waves.
         // thread t: column group t % 32, rows t / 32 + 16 j
         static_assert(RNT % (RBN / 8) == 0, "each thread keeps one column group");
         ep_store_rows<false, RBM, RBN, RBM * (RBN / 8) / RNT>(g.st, ep, colv, rowv, stg, CS, t / (RBN / 8),
                                                               RNT / (RBN / 8), (t % (RBN / 8)) * 8, row0, col0);
     };
-    run_tile(xcd_tile(blockIdx.x, gridDim.x));  // consecutive workgroups share a weight tile
+    run_tile(tile);  // consecutive workgroups share a weight tile
+}
+
+// Split K's second pass: C = ep(to16(beta * sum over the slices of part)),
+// the slices added in order (the result does not depend on which workgroup
+// finished first). Tile: QR_BM rows x 256 columns, one thread per row and
+// column group of 8 (two 16-byte loads a slice, four slices' loads issued
+// together), stored through the op-graph as the GEMM's own store does. The
+// tile is short so that even a few rows make a grid of many workgroups: the
+// pass is bound by how many loads are in flight.
+constexpr int QR_BN = 256, QR_NT = 256, QR_BM = QR_NT / (QR_BN / 8);
+__global__ void __launch_bounds__(QR_NT) q4r_reduce(RArgs g, EpArgs ep) {
+    __shared__ __align__(16) float epv[SMG_MAX_EP_NODES * (QR_BN + QR_BM)];
+    const uint32_t mtiles = (g.m + QR_BM - 1) / QR_BM;
+    const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
+    const uint32_t row0 = (tile % mtiles) * QR_BM, col0 = (tile / mtiles) * QR_BN;
+    float *colv = epv, *rowv = epv + SMG_MAX_EP_NODES * QR_BN;
+    ep_load_vectors<false, QR_BM, QR_BN, QR_NT>(g.st, ep, colv, rowv, row0, col0);
+    __syncthreads();
+    const int t = threadIdx.x;
+    const uint32_t cl = (t % (QR_BN / 8)) * 8, rl = t / (QR_BN / 8);
+    if (col0 + cl >= g.n || row0 + rl >= g.m) return;  // no barrier follows
+    const size_t stride = (size_t)g.m * g.part_ld / 4;  // float4s per slice
+    const float4_t *p = (const float4_t *)(g.part + (size_t)(row0 + rl) * g.part_ld + col0 + cl);
+    float4_t s0 = p[0], s1 = p[1];
+    uint32_t sl = 1;
+    for (; sl + 4 <= g.nsplit; sl += 4) {
+        float4_t v[4][2];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            v[u][0] = p[(sl + u) * stride];
+            v[u][1] = p[(sl + u) * stride + 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            s0 += v[u][0];
+            s1 += v[u][1];
+        }
+    }
+    for (; sl < g.nsplit; sl++) {
+        s0 += p[sl * stride];
+        s1 += p[sl * stride + 1];
+    }
+    uint32_t w4[4];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        w4[e] = (uint32_t)from_f32<false>(0.0f + g.beta * s0[2 * e]) |
+                ((uint32_t)from_f32<false>(0.0f + g.beta * s0[2 * e + 1]) << 16);
+        w4[2 + e] = (uint32_t)from_f32<false>(0.0f + g.beta * s1[2 * e]) |
+                    ((uint32_t)from_f32<false>(0.0f + g.beta * s1[2 * e + 1]) << 16);
+    }
+    ep_store8<false, QR_BM, QR_BN>(g.st, ep, colv, rowv, make_uint4(w4[0], w4[1], w4[2], w4[3]), rl, cl, row0,
+                                   col0);
 }
 
 }  // namespace
@@ -434,8 +534,41 @@ bool q4r_supported(const WDev &w, size_t m, long lhs_cs, long lhs_rs, const uint
            cell_grid_rows(w.nchunks) * w.n_pad * 16 < ((size_t)1 << 32);
 }
 
+int device_cus() {
+    static std::atomic<int> cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cus[dev].load(std::memory_order_relaxed);
+    if (v <= 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cus[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
+// One 512-thread workgroup of gemm_q4r fills a compute unit's LDS. A grid of
+// fewer tiles than half the compute units leaves most of them idle for the
+// whole of K (at K = 4096, 33 to 256 rows take about 52 us at N = 4096 with 16
+// to 32 tiles): then K is cut into as many slices as fill the compute units
+// once, each at least Q4R_MIN_SLICE_STEPS steps of 64 depths.
+constexpr uint32_t Q4R_MIN_SLICE_STEPS = 2;
+uint32_t q4r_nsplit(const WDev &w, size_t m) {
+    if (w.kind != W_Q4 || w.k < 64 || w.k % 64 != 0 || w.block < 32) return 1;  // not gemm_q4r's
+    const size_t tiles = ((m + RBM - 1) / RBM) * ((w.n + RBN - 1) / RBN);
+    const size_t cus = (size_t)device_cus();
+    if (tiles == 0 || tiles * 2 > cus) return 1;
+    const size_t by_k = std::max<size_t>(1, (w.k / 64) / Q4R_MIN_SLICE_STEPS);
+    return (uint32_t)std::min(cus / tiles, by_k);
+}
+
+size_t q4r_split_bytes(const WDev &w, size_t m) {
+    const uint32_t ns = q4r_nsplit(w, m);
+    return ns > 1 ? (size_t)ns * m * ((w.n + 7) / 8 * 8) * sizeof(float) : 0;
+}
+
 hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,
-                      const uint16_t *lhs, long lhs_rs, float beta, const EpArgs &ep, hipStream_t s) {
+                      const uint16_t *lhs, long lhs_rs, float beta, const EpArgs &ep, float *part,
+                      size_t part_bytes, hipStream_t s) {
     RArgs g = {};
     g.lhs = lhs;
     g.codes = w.codes;
@@ -452,10 +585,26 @@ hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long 
     g.nchunks = (uint32_t)w.nchunks;
     g.sc_rows = (uint32_t)w.sc_rows;
     const uint32_t tiles = (uint32_t)(((m + RBM - 1) / RBM) * ((w.n + RBN - 1) / RBN));
+    const size_t slice_bytes = m * ((w.n + 7) / 8 * 8) * sizeof(float);
+    const uint32_t ns = part ? (uint32_t)std::min<size_t>(q4r_nsplit(w, m), part_bytes / slice_bytes) : 1;
+    if (ns <= 1) {
+        if (w.mins)
+            hipLaunchKernelGGL((gemm_q4r<true, false>), dim3(tiles), dim3(RNT), 0, s, g, ep);
+        else
+            hipLaunchKernelGGL((gemm_q4r<false, false>), dim3(tiles), dim3(RNT), 0, s, g, ep);
+        return hipGetLastError();
+    }
+    g.part = part;
+    g.nsplit = ns;
+    g.part_ld = (uint32_t)((w.n + 7) / 8 * 8);
     if (w.mins)
-        hipLaunchKernelGGL(gemm_q4r<true>, dim3(tiles), dim3(RNT), 0, s, g, ep);
+        hipLaunchKernelGGL((gemm_q4r<true, true>), dim3(tiles * ns), dim3(RNT), 0, s, g, ep);
     else
-        hipLaunchKernelGGL(gemm_q4r<false>, dim3(tiles), dim3(RNT), 0, s, g, ep);
+        hipLaunchKernelGGL((gemm_q4r<false, true>), dim3(tiles * ns), dim3(RNT), 0, s, g, ep);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t rtiles = (uint32_t)(((m + QR_BM - 1) / QR_BM) * ((w.n + QR_BN - 1) / QR_BN));
+    hipLaunchKernelGGL(q4r_reduce, dim3(rtiles), dim3(QR_NT), 0, s, g, ep);
     return hipGetLastError();
 }
 

@@ -316,6 +316,50 @@ def test_q4_concurrent_callers_bit_identical(smg, orc):
         assert np.array_equal(o, ref)
 
 
+# Prefill shapes whose 128 x 256 GEMM tiles fill fewer than half of the 256
+# compute units, so K is split into slices (16 slices of 4 steps at 48 x 4096 x
+# 4096; 8 at 130 x 1000 x 1024 with two row tiles and a ragged N; 14 uneven
+# slices of 2 or 3 steps at 256 x 2304 x 2048) and a second kernel adds them.
+SPLIT_CASES = [(48, 4096, 4096), (130, 1000, 1024), (256, 2304, 2048), (33, 520, 512)]
+
+
+@pytest.mark.parametrize("m,n,k", SPLIT_CASES)
+@pytest.mark.parametrize("affine", [False, True])
+def test_q4_split_k_prefill(smg, orc, m, n, k, affine):
+    """The split-K GEMM against the oracle with an op-graph of every operand
+    class (ROW, COL, TENSOR, activation), bit-identical over repeated calls
+    (the slices are added in a fixed order), and the device-pointer entry
+    (its partials in the stream's pool) bit-identical to the host entry
+    (its partials in the call's staging)."""
+    import torch
+    rng = np.random.default_rng(m * 7 + n + k + affine)
+    nbk = k // 32
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.005, 0.02, n * nbk).astype(np.float32))
+    mins = orc.f32_to_f16(rng.uniform(-0.1, 0.0, n * nbk).astype(np.float32)) if affine else None
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    row = orc.f32_to_f16(rng.normal(0, 0.1, m).astype(np.float32))
+    col = orc.f32_to_f16(rng.normal(0, 0.1, n).astype(np.float32))
+    ten = orc.f32_to_f16(rng.normal(1, 0.1, m * n).astype(np.float32))
+    p = smg.Q4Params(32).affine() if affine else smg.Q4Params(32)
+    w = smg.Q4Weights.with_params(quants, scales, mins, n, k, p)
+    ep = smg.Epilogue().add_row(row).mul_tensor(ten).add_col(col).silu()
+    got = np.zeros(m * n, np.uint16)
+    smg.matmul_q4_ep(a, w, got, m, ep)
+    nodes = [(2, 0, 0.0, row, 0), (7, 0, 0.0, ten, 0), (4, 0, 0.0, col, 0)]
+    want = orc.matmul_q4_ep(a, quants, scales, mins, m, n, k, 32, nodes, 3)
+    assert max_rel(got, want) <= f16_tol(k), f"{m}x{n}x{k}"
+    again = np.zeros(m * n, np.uint16)
+    smg.matmul_q4_ep(a, w, again, m, ep)
+    assert np.array_equal(again, got)
+    dev = lambda x: torch.from_numpy(x.view(np.int16)).cuda()  # noqa: E731
+    cd = torch.zeros(m * n, dtype=torch.int16, device="cuda")
+    smg.matmul_q4_ep(dev(a), w, cd, m, smg.Epilogue().add_row(dev(row)).mul_tensor(dev(ten))
+                     .add_col(dev(col)).silu())
+    torch.cuda.synchronize()
+    assert np.array_equal(cd.cpu().numpy().view(np.uint16), got)
+
+
 def test_q4_device_pointer_path_matches_host(smg, orc):
     """smg_q4_matmul_dev (torch tensors on the current stream) == host path."""
     import torch
