@@ -550,15 +550,18 @@ int device_cus() {
 // fewer tiles than half the compute units leaves most of them idle for the
 // whole of K (at K = 4096, 33 to 256 rows take about 52 us at N = 4096 with 16
 // to 32 tiles): then K is cut into as many slices as fill the compute units
-// once, each at least Q4R_MIN_SLICE_STEPS steps of 64 depths.
-constexpr uint32_t Q4R_MIN_SLICE_STEPS = 2;
+// once, each at least Q4R_MIN_SLICE_STEPS steps of 64 depths, and at most
+// Q4R_MAX_SPLIT slices: every slice adds m x N f32 partials that the end of
+// the kernel writes back from L2 and the reduction reads again (16 slices
+// measured 1-2 us slower than 8 at N = 4096, K = 4096).
+constexpr uint32_t Q4R_MIN_SLICE_STEPS = 2, Q4R_MAX_SPLIT = 8;
 uint32_t q4r_nsplit(const WDev &w, size_t m) {
     if (w.kind != W_Q4 || w.k < 64 || w.k % 64 != 0 || w.block < 32) return 1;  // not gemm_q4r's
     const size_t tiles = ((m + RBM - 1) / RBM) * ((w.n + RBN - 1) / RBN);
     const size_t cus = (size_t)device_cus();
     if (tiles == 0 || tiles * 2 > cus) return 1;
     const size_t by_k = std::max<size_t>(1, (w.k / 64) / Q4R_MIN_SLICE_STEPS);
-    return (uint32_t)std::min(cus / tiles, by_k);
+    return (uint32_t)std::min(std::min(cus / tiles, by_k), (size_t)Q4R_MAX_SPLIT);
 }
 
 size_t q4r_split_bytes(const WDev &w, size_t m) {

@@ -317,10 +317,11 @@ def test_q4_concurrent_callers_bit_identical(smg, orc):
 
 
 # Prefill shapes whose 128 x 256 GEMM tiles fill fewer than half of the 256
-# compute units, so K is split into slices (16 slices of 4 steps at 48 x 4096 x
-# 4096; 8 at 130 x 1000 x 1024 with two row tiles and a ragged N; 14 uneven
-# slices of 2 or 3 steps at 256 x 2304 x 2048) and a second kernel adds them.
-SPLIT_CASES = [(48, 4096, 4096), (130, 1000, 1024), (256, 2304, 2048), (33, 520, 512)]
+# compute units, so K is split into slices (8 slices of 8 steps at 48 x 4096 x
+# 4096; 8 at 130 x 1000 x 1024 with two row tiles; 8 uneven slices of 2 or 3
+# steps at 200 x 1500 x 1472, N not a multiple of 8; 4 of 2 steps at 33 x 520
+# x 512) and a second kernel adds them.
+SPLIT_CASES = [(48, 4096, 4096), (130, 1000, 1024), (200, 1500, 1472), (256, 2304, 2048), (33, 520, 512)]
 
 
 @pytest.mark.parametrize("m,n,k", SPLIT_CASES)
