@@ -94,6 +94,18 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// At most n (uniform) steps' DMA still in flight.
+__device__ __forceinline__ void wait_vm_steps(int n) {
+    if (n >= 3)
+        wait_vm<3 * PS>();
+    else if (n == 2)
+        wait_vm<2 * PS>();
+    else if (n == 1)
+        wait_vm<PS>();
+    else
+        wait_vm<0>();
+}
+
 // Workgroup barrier that orders LDS accesses without waiting on outstanding
 // DMA (a release fence would wait for all of it): the empty asm statements keep
 // the compiler from moving memory accesses across it; the caller first waits
@@ -360,9 +372,18 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
 #pragma unroll
             for (int jt = 0; jt < 4; jt++) acc[i][jt] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
+        if constexpr (SPLIT) {
+            // a slice of a few steps issues no loads past its last step, so
+            // nothing is left in flight to drain at its end
 #pragma unroll
-        for (int j = 0; j < NSTAGE; j++) dma_step(g, d, ring + j * STAGE_BYTES, ks0 + min((uint32_t)j, last), wave);
-        wait_vm<(NSTAGE - 2) * PS>();  // steps 0 and 1 landed
+            for (int j = 0; j < NSTAGE; j++)
+                if ((uint32_t)j <= last) dma_step(g, d, ring + j * STAGE_BYTES, ks0 + j, wave);
+            wait_vm_steps(min((int)last, NSTAGE - 1) - 1);  // steps 0 and 1 landed
+        } else {
+#pragma unroll
+            for (int j = 0; j < NSTAGE; j++) dma_step(g, d, ring + j * STAGE_BYTES, min((uint32_t)j, last), wave);
+            wait_vm<(NSTAGE - 2) * PS>();  // steps 0 and 1 landed
+        }
         barrier_lds();
 
         // Step ks: step ks+1's fragments are read (its stage was published by
@@ -370,16 +391,25 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
         // ks+2's DMA is waited for and the barrier publishes it -- and frees
         // stage ks%5, whose fragments every wave has multiplied -- and step
         // ks+5's DMA is issued into that stage. Steps past the end re-load the
-        // last step into a free stage and read a stage nobody multiplies.
+        // last step into a free stage (SPLIT: issue nothing) and read a stage
+        // nobody multiplies.
         u32x4_t bb[4];  // B operands of the four column tiles, rotating
         auto step = [&](uint32_t ks, const Half &cur, Half &nxt) {
             uint32_t sb = ring0 + ((ks + 1) % NSTAGE) * STAGE_BYTES;
             asm volatile("" : "+s"(sb));  // opaque: one base add per operand kind, constant offsets after
             read_half<AFFINE>(sb, ro, nxt);
             mma_step<AFFINE>(cur, nxt, acc, bb, mag_lo, mag_hi);
-            wait_vm<(NSTAGE - 3) * PS>();
-            barrier_lds();
-            dma_step(g, d, ring + (ks % NSTAGE) * STAGE_BYTES, ks0 + min(ks + NSTAGE, last), wave);
+            if constexpr (SPLIT) {
+                // issued: steps up to min(ks + 4, last); step ks+2 must land
+                const int after = (int)last - (int)ks - 2;
+                wait_vm_steps(after > 2 ? 2 : after);
+                barrier_lds();
+                if (ks + NSTAGE <= last) dma_step(g, d, ring + (ks % NSTAGE) * STAGE_BYTES, ks0 + ks + NSTAGE, wave);
+            } else {
+                wait_vm<(NSTAGE - 3) * PS>();
+                barrier_lds();
+                dma_step(g, d, ring + (ks % NSTAGE) * STAGE_BYTES, min(ks + NSTAGE, last), wave);
+            }
         };
         Half h0, h1;
         read_half<AFFINE>(ring0, ro, h0);
@@ -412,11 +442,20 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
             constexpr int KEEP = decltype(keep_c)::value, GIVE = 4 - KEEP;
             float4_t *mine = (float4_t *)ring + wave * 1024;  // 16 KB per wave
             const float4_t *other = (const float4_t *)ring + ((wave + 4) % 8) * 1024;
+            // SPLIT, the tile's rows all below 64: row tiles 4-7 are padding,
+            // neither handed over nor finished
+            const bool pad_hi = SPLIT && row0 + 64 >= g.m;
+            if (!(pad_hi && GIVE == 4)) {
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+                for (int i = 0; i < 4; i++)
 #pragma unroll
-                for (int jt = 0; jt < 4; jt++) mine[(i * 4 + jt) * 64 + lane] = acc[GIVE + i][jt];
+                    for (int jt = 0; jt < 4; jt++) mine[(i * 4 + jt) * 64 + lane] = acc[GIVE + i][jt];
+            }
             __syncthreads();
+            if (pad_hi && KEEP == 4) {
+                __syncthreads();  // the SPLIT branch's barrier
+                return;
+            }
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
