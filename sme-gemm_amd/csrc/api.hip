@@ -602,6 +602,11 @@ ScratchPool<HipDevAlloc> &split_pool() {
     static ScratchPool<HipDevAlloc> *p = new ScratchPool<HipDevAlloc>();  // never destroyed
     return *p;
 }
+// SMG_ENOMEM for a failed allocation (the split-K partials), else SMG_EHIP.
+int q4_fail(const char *what, hipError_t e) {
+    if (e == hipErrorOutOfMemory) return fail(SMG_ENOMEM, (std::string(what) + ": split-K partials hipMalloc").c_str());
+    return fail(SMG_EHIP, what, e);
+}
 hipError_t run_q4_dev(int device, const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
                       const EpArgs &ea, bool bf16, hipStream_t s) {
     const size_t sb = q4_split_bytes(w, m, bf16);
@@ -864,7 +869,7 @@ int mlp_step(smg_mlp *m, const uint16_t *x16, const float *nx, const float *nw, 
             ea.cls[0] = ep_class(EP_OP_ACT);
         }
         uint16_t *dst = m->gated ? spare : sc.hid;
-        if ((e = run_q4_dev(m->up->device, m->up->d, rows, dst, x16, ea, false, s)) != hipSuccess) return fail(SMG_EHIP, "up projection", e);
+        if ((e = run_q4_dev(m->up->device, m->up->d, rows, dst, x16, ea, false, s)) != hipSuccess) return q4_fail("up projection", e);
         if (m->gated && (e = launch_glu(dst, rows, m->hidden, m->act, 1, sc.hid, s)) != hipSuccess)
             return fail(SMG_EHIP, "glu", e);
     }
@@ -876,7 +881,7 @@ int mlp_step(smg_mlp *m, const uint16_t *x16, const float *nx, const float *nw, 
     } else {
         uint16_t *out16 = spare + rows * both;
         if ((e = run_q4_dev(m->down->device, m->down->d, rows, out16, sc.hid, EpArgs{}, false, s)) != hipSuccess)
-            return fail(SMG_EHIP, "down projection", e);
+            return q4_fail("down projection", e);
         if ((e = launch_add_f16(out16, rows * d_out, y, s)) != hipSuccess) return fail(SMG_EHIP, "residual add", e);
     }
     return SMG_OK;
@@ -1368,7 +1373,7 @@ int smg_q4_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint1
     if ((rc = ep_args(ep, &ea, w->d.n))) return rc;
     if ((rc = check_dev_ptrs("smg_q4_matmul_dev", w->device, stream, ea, {dst, lhs}))) return rc;
     hipError_t e = run_q4_dev(w->device, w->d, m, dst, lhs, ea, bf16 != 0, (hipStream_t)stream);
-    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_q4_matmul_dev", e);
+    return e == hipSuccess ? SMG_OK : q4_fail("smg_q4_matmul_dev", e);
 }
 
 int smg_q4_chained_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t *lhs,
@@ -1633,7 +1638,7 @@ int smg_q4_accumulate_dev(size_t m, const smg_weights *w, float *y, const uint16
         e = run_q4_dev(w->device, w->d, m, sc.h16, x, EpArgs{}, false, s);
         if (e == hipSuccess) e = launch_add_f16(sc.h16, m * w->d.n, y, s);
     }
-    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_q4_accumulate_dev", e);
+    return e == hipSuccess ? SMG_OK : q4_fail("smg_q4_accumulate_dev", e);
 }
 
 int smg_attn_create(smg_weights *qkv, smg_weights *out, size_t heads, size_t kv_heads, size_t head_dim,

@@ -161,6 +161,14 @@ b = orc.f32_to_f16(rng.standard_normal(k * n).astype(np.float32))
 ad = torch.from_numpy(a.view(np.int16)).cuda()
 bd = torch.from_numpy(b.view(np.int16)).cuda()
 cd = torch.full((m * n,), 0x1234, dtype=torch.int16, device="cuda")
+# a Q4 call whose GEMM splits K (40 rows, one 128 x 256 tile, K = 512: 4 slices)
+ms, ks = 40, 512
+qs = rng.integers(0, 256, (ks * n + 1) // 2, dtype=np.uint8)
+ss = orc.f32_to_f16(rng.uniform(0.005, 0.02, n * (ks // 32)).astype(np.float32))
+q4s = smg.Q4Weights(qs, ss, n, ks)
+a_s = orc.f32_to_f16(rng.standard_normal(ms * ks).astype(np.float32))
+asd = torch.from_numpy(a_s.view(np.int16)).cuda()
+csd = torch.full((ms * n,), 0x1234, dtype=torch.int16, device="cuda")
 stream = torch.cuda.current_stream().cuda_stream
 torch.cuda.synchronize()
 
@@ -181,9 +189,11 @@ print("device q2 (scratch pool)", rc, flush=True)
 rc2 = L.smg_gemm_run_dev(0, m, n, k, cd.data_ptr(), 1, n, 0, ad.data_ptr(), 1, k, bd.data_ptr(), 1, n,
                          0, 0x3C00, stream)
 print("device strided gemm (scratch pool)", rc2, flush=True)
+rc3 = L.smg_q4_matmul_dev(ms, q4s._h, csd.data_ptr(), asd.data_ptr(), None, 0, stream)
+print("device q4 split K (partials pool)", rc3, flush=True)
 torch.cuda.synchronize()
-assert rc == -2 and rc2 == -2 and bool((cd == 0x1234).all())
-assert b"hipMalloc" in L.smg_last_error()
+assert rc == -2 and rc2 == -2 and rc3 == -2 and bool((cd == 0x1234).all()) and bool((csd == 0x1234).all())
+assert b"split-K partials hipMalloc" in L.smg_last_error()
 
 del os.environ["SMG_TEST_FAIL_ALLOC"]
 rc = L.gemm_gpu_f16f16_q4(m, q4._h, c.ctypes.data, a.ctypes.data, None)
@@ -196,6 +206,12 @@ torch.cuda.synchronize()
 got = cd.cpu().numpy().view(np.uint16)
 print("device strided gemm after", rc, max_rel(got, orc.gemm16(a, b, m, n, k)), flush=True)
 assert rc == 0 and max_rel(got, orc.gemm16(a, b, m, n, k)) <= f16_tol(k)
+rc = L.smg_q4_matmul_dev(ms, q4s._h, csd.data_ptr(), asd.data_ptr(), None, 0, stream)
+torch.cuda.synchronize()
+got = csd.cpu().numpy().view(np.uint16)
+want = orc.matmul_q4_ep(a_s, qs, ss, None, ms, n, ks, 32)
+print("device q4 split K after", rc, max_rel(got, want), flush=True)
+assert rc == 0 and max_rel(got, want) <= f16_tol(ks)
 print("alloc-fail ok", flush=True)
 """
 
