@@ -5,8 +5,9 @@
   contract, src/kernels/q4/matmul.rs:85-90).
 - The Python mirror refuses device tensors the kernels would misread: a dtype
   that is not 16 bits wide, a strided view, too few elements.
-- A device-pointer call's scratch outlives later, larger calls on the same
-  stream: a captured graph replays correctly after the pool has grown.
+- A device-pointer call's scratch (the low-bit quantized rows, the split-K
+  GEMM's partial sums) outlives later, larger calls on the same stream: a
+  captured graph replays correctly after the pool has grown.
 - A device call refuses pageable host memory (epilogue operands, A, C) in
   the mirror and at the C ABI; a host call refuses device operands.
 - With SMG_TEST_FAIL_ALLOC=1 every device allocation fails: the calls return
@@ -19,6 +20,8 @@ import ctypes as C
 
 import numpy as np
 import pytest
+
+from conftest import f16_tol, max_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -117,6 +120,49 @@ def test_dev_scratch_survives_growth_under_a_replayed_graph(smg, orc):
         assert np.array_equal(cd.cpu().numpy().view(np.uint16), want), f"replay {rep}"
         assert np.array_equal(c2d.cpu().numpy().view(np.uint16), want2), f"large dev call {rep}"
         assert np.array_equal(host_c, want2), f"large host call {rep}"
+
+
+def test_split_k_partials_survive_growth_under_a_replayed_graph(smg, orc):
+    """A Q4 call whose GEMM splits K is captured (its f32 partials live in the
+    stream's partial buffer); then, on the same stream, a split call with far
+    more partials (the buffer grows: a new one, the old one retired); every
+    replay, with that eager work between, gives the eager call's bits."""
+    import torch
+    rng = np.random.default_rng(12)
+    to_dev = lambda x: torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).cuda()  # noqa: E731
+
+    def case(m, n, k):
+        q = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+        s = orc.f32_to_f16(rng.uniform(0.005, 0.02, n * (k // 32)).astype(np.float32))
+        a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+        return smg.Q4Weights(q, s, n, k), to_dev(a), orc.matmul_q4_ep(a, q, s, None, m, n, k, 32)
+
+    m, n, k = 48, 1024, 1024          # 4 tiles x 8 slices: 1.5 MB of partials
+    w, ad, want = case(m, n, k)
+    m2, n2, k2 = 256, 2304, 2048      # 18 tiles x 8 slices: 19 MB
+    w2, a2d, want2 = case(m2, n2, k2)
+    cd = torch.zeros(m * n, dtype=torch.int16, device="cuda")
+    c2d = torch.zeros(m2 * n2, dtype=torch.int16, device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        smg.matmul_q4(ad, w, cd, m)  # sizes this stream's partial buffer before capture
+        torch.cuda.synchronize()
+        eager = cd.cpu().numpy().view(np.uint16).copy()
+        with torch.cuda.graph(g, stream=side):
+            smg.matmul_q4(ad, w, cd, m)
+    torch.cuda.synchronize()
+    assert max_rel(eager, want) <= f16_tol(k)
+    for rep in range(3):
+        cd.zero_()
+        with torch.cuda.stream(side):
+            smg.matmul_q4(a2d, w2, c2d, m2)  # the grown buffer
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(cd.cpu().numpy().view(np.uint16), eager), f"replay {rep}"
+        assert max_rel(c2d.cpu().numpy().view(np.uint16), want2) <= f16_tol(k2), f"large call {rep}"
 
 
 @pytest.mark.parametrize("act", [3, 5])
