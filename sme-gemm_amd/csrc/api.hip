@@ -571,17 +571,28 @@ EpArgs ep_from_row(const EpArgs &ea, size_t r0, size_t n) {
 // compute units idle at N = 4096 to 14336); the MFMA GEMM above, K split over
 // the compute units when its tiles are few and `split` (q4_split_bytes) is
 // given.
-constexpr size_t Q4_GEMV_CHUNK_ROWS = 32;
-bool q4_gemv_rows(const WDev &w, size_t m) {
-    return q4_gemv_serves(w, m) || (m <= Q4_GEMV_CHUNK_ROWS && q4_gemv_serves(w, Q4_GEMV_WIDE_ROWS));
+// Without gemm_q4r (bf16 activations, or an A it cannot read) the calls above
+// Q4_GEMV_CHUNK_ROWS go to gemm_kernel, whose 128 x 128 tiles are as few: at
+// K = 4096 it took 115 us for any of 33-128 rows at N = 4096 or 14336, where
+// 16-row GEMV launches take about 7.7 us (N = 4096) or 17.6 us (N = 14336)
+// each. So those calls stay on the GEMV up to Q4_GEMV_CHUNK_MAX rows while
+// (launches x N) stays within Q4_GEMV_CHUNK_COLS (N = 14336: up to 96 rows).
+constexpr size_t Q4_GEMV_CHUNK_ROWS = 32, Q4_GEMV_CHUNK_MAX = 128, Q4_GEMV_CHUNK_COLS = 6 * 14336;
+bool q4_gemv_rows(const WDev &w, size_t m, bool gemm_q4r) {
+    if (q4_gemv_serves(w, m)) return true;
+    if (!q4_gemv_serves(w, Q4_GEMV_WIDE_ROWS)) return false;
+    if (m <= Q4_GEMV_CHUNK_ROWS) return true;
+    return !gemm_q4r && m <= Q4_GEMV_CHUNK_MAX &&
+           (m + Q4_GEMV_WIDE_ROWS - 1) / Q4_GEMV_WIDE_ROWS * w.n <= Q4_GEMV_CHUNK_COLS;
 }
 size_t q4_split_bytes(const WDev &w, size_t m, bool bf16) {
-    return q4_gemv_rows(w, m) || bf16 ? 0 : q4r_split_bytes(w, m);
+    return bf16 || q4_gemv_rows(w, m, true) ? 0 : q4r_split_bytes(w, m);
 }
 hipError_t run_q4(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs, const EpArgs &ea,
                   bool bf16, hipStream_t s, void *split, size_t split_bytes) {
     if (q4_gemv_serves(w, m)) return launch_q4_gemv(w, m, dst, lhs, ea, bf16, s);
-    if (m <= Q4_GEMV_CHUNK_ROWS && q4_gemv_serves(w, Q4_GEMV_WIDE_ROWS)) {
+    const bool q4r = q4r_supported(w, m, 1, (long)w.k, lhs, bf16);
+    if (q4_gemv_rows(w, m, q4r)) {
         for (size_t r0 = 0; r0 < m; r0 += Q4_GEMV_WIDE_ROWS) {
             const size_t rows = std::min(Q4_GEMV_WIDE_ROWS, m - r0);
             const hipError_t e = launch_q4_gemv(w, rows, dst + r0 * w.n, lhs + r0 * w.k, ep_from_row(ea, r0, w.n),
@@ -590,8 +601,7 @@ hipError_t run_q4(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs, c
         }
         return hipSuccess;
     }
-    if (q4r_supported(w, m, 1, (long)w.k, lhs, bf16))
-        return launch_q4r(w, m, dst, 1, (long)w.n, lhs, (long)w.k, 1.0f, ea, (float *)split, split_bytes, s);
+    if (q4r) return launch_q4r(w, m, dst, 1, (long)w.n, lhs, (long)w.k, 1.0f, ea, (float *)split, split_bytes, s);
     return launch_gemm(w, m, dst, 1, (long)w.n, lhs, 1, (long)w.k, 1.0f, ea, bf16, s);
 }
 

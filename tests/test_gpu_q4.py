@@ -156,6 +156,30 @@ def test_q4_bf16(smg, orc, m, n, k, affine):
     assert max_rel(got, want, bf16=True) <= bf16_tol(k)
 
 
+@pytest.mark.parametrize("m,n,k", [(48, 1536, 1024), (100, 4096, 512), (128, 700, 1088)])
+@pytest.mark.parametrize("affine", [False, True])
+def test_q4_bf16_rows_on_gemv_launches(smg, orc, m, n, k, affine):
+    """bf16 calls of 33 to 128 rows run as 16-row GEMV launches (the MFMA
+    GEMM for bf16 leaves most compute units idle at these shapes): ROW and
+    TENSOR operands are offset per launch; against the bf16 portable path."""
+    nbk = k // 32
+    rng = np.random.default_rng(3 * m + n + k + affine)
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.005, 0.02, n * nbk).astype(np.float32))
+    mins = orc.f32_to_f16(rng.uniform(-0.1, 0.1, n * nbk).astype(np.float32)) if affine else None
+    a = orc.f32_to_bf16(rng.standard_normal(m * k).astype(np.float32))
+    row = orc.f32_to_bf16(rng.normal(0, 0.1, m).astype(np.float32))
+    ten = orc.f32_to_bf16(rng.normal(1, 0.1, m * n).astype(np.float32))
+    col = orc.f32_to_bf16(rng.normal(0, 0.1, n).astype(np.float32))
+    p = smg.Q4Params(32).affine() if affine else smg.Q4Params(32)
+    w = smg.Q4Weights.with_params(quants, scales, mins, n, k, p)
+    got = np.zeros(m * n, np.uint16)
+    smg.matmul_q4_bf16_ep(a, w, got, m, smg.Epilogue().add_row(row).mul_tensor(ten).add_col(col).silu())
+    nodes = [(2, 0, 0.0, row, 0), (7, 0, 0.0, ten, 0), (4, 0, 0.0, col, 0)]
+    want = orc.matmul_q4_ep(a, quants, scales, mins, m, n, k, 32, nodes, 3, bf16=True)
+    assert max_rel(got, want, bf16=True) <= bf16_tol(k)
+
+
 @pytest.mark.parametrize("m", [8, 16])
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("affine", [False, True])
