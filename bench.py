@@ -262,6 +262,10 @@ def main():
                     us_t = timer([(lambda b=b: torch.matmul(ah, b, out=tcr)) for b in tbs], steps, warm)
                     rows[f"m{mr}_n{nr}"].update({"TFLOPS": fl / (us * 1e-6) / 1e12,
                                                  "torch_dense_f16_gemm_us": us_t})
+                    if mr == 64:  # bf16 activations: 16-row GEMV launches
+                        callsb = [(lambda w=w: smg.matmul_q4_bf16(ard, w, cr, mr)) for w in wsr]
+                        rows[f"m{mr}_n{nr}"]["us_cold_bf16"] = timer(callsb, steps, warm)
+                        del callsb
                     del tbs, tcr
                 del wsr, callsr
         extra["q4_few_rows_k4096"] = rows
