@@ -1,20 +1,26 @@
 """Benchmark of the quantized-weight matmul path on one MI355X.
 
 Headline (the JSON line's `value`): config 1 -- Q4 GEMV, m=1, K=N=4096,
-block 32 -- as whole-job HBM throughput in GB/s. A "step" is one GEMV call on
-its own copy of the weights: 64 device copies (605 MB) rotate, and the MALL
-(256 MB) is flushed with a 512 MB write before each timed replay, so every
-timed call streams its weights from HBM -- also when --steps is below the
-number of copies. The K timed steps are one HIP graph replayed on torch's
-current stream, bracketed by torch.cuda.synchronize(); the time per call is
-HIP events around the replay on that stream, so it includes the graph's
-inter-kernel gap (reported as `graph_gap_us`, from a graph of 1-element fills).
+block 32 -- as whole-job HBM throughput in GB/s. A step is one pass of GEMV
+calls over 64 device copies of the weights (605 MB, more than twice the
+256 MB MALL, so each call streams its weights from HBM: one call per copy,
+as a decode step over a 64-layer stack would). The K timed steps are one HIP
+graph replayed on torch's current stream, bracketed by
+torch.cuda.synchronize(); before the replay the MALL is flushed by READING
+1 GiB of other data (a write flush would leave 256 MB of dirty lines whose
+write-back the first kernels after it pay for: about 40 us measured, 2 us a
+call at 20 calls). HIP events around the replay on that stream give the time
+per call, which includes the dispatch of each kernel (`launch_us`: a graph of
+empty launches timed the same way).
 
 `roofline` covers the dominant kernel (the Q4 GEMV): achieved = algorithmic
 bytes per call / time per call. `traffic` is the HBM bytes per launch from
 the committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary in profiles/.
+`python bench.py --trace-summary DIR` prints, from a rocprofv3 kernel trace
+of this script, each timed replay's span per call (which the line's per-call
+times must match) and the average kernel duration inside it.
 
-`extra` holds, timed the same way:
+`extra` holds, timed the same way (every graph at least 256 calls):
   - configs 2-4 (config 4 against the f16 MFMA peak, with the shader clock
     measured right after its GEMMs and torch's dense f16 GEMM of the same shape
     as a same-box floor);
@@ -32,7 +38,7 @@ configs' samples.
 so that a rocprofv3 --pmc run of this script can scale its counters.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
-                       [--only CONFIGS] [--calib-copy]
+                       [--only CONFIGS] [--calib-copy] [--trace-summary DIR]
 """
 from __future__ import annotations
 
@@ -48,7 +54,8 @@ sys.path.insert(0, os.path.join(ROOT, "sme-gemm_amd"))
 HBM_PEAK_GBS = 8000.0
 F16_MFMA_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 << 20
-FLUSH_BYTES = 512 << 20
+FLUSH_BYTES = 1 << 30
+MIN_CALLS = 256  # calls per timed graph outside the headline (the graph's fixed start amortized)
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemv_mfma_config1_traffic.md")
 
@@ -66,43 +73,103 @@ def committed_traffic():
 
 
 class Timer:
-    """Graph-replayed timing: `steps` calls (cycling over `calls`) captured
-    once, warmed, then -- after a MALL flush -- replayed once between events on
-    the replaying stream. Returns microseconds per call."""
+    """Graph-replayed timing of `passes` passes over `calls` (one call per
+    weight copy): captured once, warmed by `warmup` eager passes and one
+    replay, then -- after a read flush of the MALL -- replayed once between
+    events on the replaying stream. Returns microseconds per call."""
 
-    def __init__(self, torch):
+    def __init__(self, torch, smg):
         self.torch = torch
-        self.flush_buf = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
+        self.smg = smg
+        self.flush_buf = torch.zeros(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
+        self.mark_buf = torch.zeros(4, dtype=torch.int64, device="cuda")
+
+    def mark(self):
+        """A one-wave marker launch (clock_probe of 0 iterations) outside the
+        timed region, so a kernel trace of this script shows where each timed
+        replay begins and ends."""
+        torch = self.torch
+        self.smg.lib().smg_clock_probe_dev(self.mark_buf.data_ptr(), 0, torch.cuda.current_stream().cuda_stream)
 
     def flush(self):
-        self.flush_buf.zero_()
-
-    def __call__(self, calls, steps: int, warmup: int, flush: bool = True):
+        """Read 1 GiB (4x the MALL) so the cache holds only clean lines of it."""
         torch = self.torch
+        rc = self.smg.lib().smg_stream_read_dev(self.flush_buf.data_ptr(), FLUSH_BYTES,
+                                                torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError("smg_stream_read_dev failed")
+
+    def __call__(self, calls, passes: int, warmup: int, flush: bool = True, min_calls: int = MIN_CALLS):
+        torch = self.torch
+        passes = max(passes, -(-min_calls // len(calls)))
         s = torch.cuda.current_stream()
         side = torch.cuda.Stream()
         side.wait_stream(s)
         with torch.cuda.stream(side):
-            for i in range(max(warmup, len(calls))):  # every call once: scratch sized before capture
-                calls[i % len(calls)]()
+            for _ in range(max(1, warmup)):  # every call at least once: scratch sized before capture
+                for c in calls:
+                    c()
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.stream(side):
             with torch.cuda.graph(g, stream=side):
-                for i in range(steps):
-                    calls[i % len(calls)]()
+                for _ in range(passes):
+                    for c in calls:
+                        c()
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
         if flush:
             self.flush()
+        self.mark()
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
         t0.record(s)
         g.replay()
         t1.record(s)
+        self.mark()
         torch.cuda.synchronize()
-        return t0.elapsed_time(t1) * 1e3 / steps
+        n = passes * len(calls)
+        del g
+        return t0.elapsed_time(t1) * 1e3 / n
+
+
+def trace_summary(d):
+    """Each timed replay in a rocprofv3 kernel trace of this script: the
+    dispatches between two marker launches (clock_probe kernels of under
+    50 us). Prints the replay's dispatch count, the calls of its first kernel,
+    its span (first start to last end) per call, and each kernel's average
+    duration inside it. Under the profiler, dispatches of a graph replay are
+    time-stamped back to back (the next start is the previous end), so a
+    kernel's traced duration includes its dispatch, plus the profiler's own
+    per-dispatch cost."""
+    import csv
+    import glob
+    path = sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True))
+    if not path:
+        raise SystemExit(f"no *kernel_trace.csv under {d}")
+    rows = []
+    with open(path[0]) as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    short = lambda nm: nm.replace("smg::(anonymous namespace)::", "").split("(")[0][:60]  # noqa: E731
+    marks = [i for i, r in enumerate(rows) if "clock_probe" in r[2] and r[1] - r[0] < 50_000]
+    print("replay  dispatches  calls  span_us  us/call  kernels (count, avg traced us)")
+    nrep = 0
+    for a, b in zip(marks, marks[1:]):
+        rep = rows[a + 1:b]
+        if len(rep) < 16:
+            continue
+        nrep += 1
+        first = rep[0][2]
+        calls = sum(1 for r in rep if r[2] == first)
+        span = (rep[-1][1] - rep[0][0]) / 1e3
+        per = {}
+        for r in rep:
+            per.setdefault(short(r[2]), []).append((r[1] - r[0]) / 1e3)
+        ks = "; ".join(f"{k} x{len(v)} {sum(v) / len(v):.2f}" for k, v in per.items())
+        print(f"{nrep:6d}  {len(rep):10d}  {calls:5d}  {span:7.1f}  {span / calls:7.3f}  {ks}")
 
 
 def rotate(w, per_copy_bytes):
@@ -151,8 +218,8 @@ def cpu_model():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=512)
-    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--steps", type=int, default=20, help="timed passes (config 1: 64 calls a pass)")
+    ap.add_argument("--warmup", type=int, default=5, help="untimed eager passes before capture")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="config 1 only")
     ap.add_argument("--only", default="12345vr",
@@ -160,7 +227,12 @@ def main():
                          "forms; r: 8 to 128 rows at config 1's K)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="16 x 64 MiB device copies first (PMC counter scale)")
+    ap.add_argument("--trace-summary", metavar="DIR",
+                    help="summarize a rocprofv3 --kernel-trace CSV output directory of this script and exit")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the calls are "
               "independent per weight matrix; sharding N across GPUs is left to the caller); "
@@ -179,7 +251,7 @@ def main():
     torch.cuda.init()
     dev = torch.device("cuda:0")
     to_dev = lambda x: torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).to(dev)  # noqa: E731
-    timer = Timer(torch)
+    timer = Timer(torch, smg)
     steps, warm = args.steps, args.warmup
 
     if args.calib_copy:
@@ -191,7 +263,7 @@ def main():
         del src, dst
 
     tiny = torch.empty(1, dtype=torch.int16, device=dev)
-    gap = timer([lambda: tiny.fill_(1)], steps, 8, flush=False)
+    launch_us = timer([lambda: tiny.fill_(1)], steps, 8, flush=False, min_calls=1024)
 
     # ---- config 1: Q4 GEMV m=1, K=N=4096 ----
     m, n, k = 1, 4096, 4096
@@ -202,7 +274,7 @@ def main():
     ad = to_dev(a)
     cs = [torch.empty(m * n, dtype=torch.int16, device=dev) for _ in range(4)]
     calls = [(lambda w=w, c=cs[i % 4]: smg.matmul_q4(ad, w, c, m)) for i, w in enumerate(ws)]
-    us1 = timer(calls, steps, warm)
+    us1 = timer(calls, steps, warm, min_calls=0)  # exactly `steps` passes over the 64 copies
     us1_hot = timer(calls[:1], steps, warm, flush=False)
     achieved = bytes1 / (us1 * 1e-6) / 1e9
     floors = {"config1": stream_floor(smg, torch, timer, bytes1, steps, warm)}
@@ -210,7 +282,9 @@ def main():
         "bytes": bytes1, "weight_copies": len(ws), "us_cold": us1, "us_hot_mall": us1_hot,
         "GBps_cold": achieved, "GBps_hot": bytes1 / (us1_hot * 1e-6) / 1e9,
         "frac_hbm_cold": achieved / HBM_PEAK_GBS,
-        "vs_stream_floor": us1 / floors["config1"]["us"]}}
+        "vs_stream_floor": us1 / floors["config1"]["us"],
+        "launch_us": launch_us, "kernel_us_est": us1 - launch_us}}
+    len_rot1 = len(ws)
     del ws, calls
 
     if "v" in only:
@@ -316,8 +390,7 @@ def main():
         c4 = torch.empty(m4 * n4, dtype=torch.int16, device=dev)
         ep4 = smg.Epilogue().mul_col(s4d).add_col(b4d).silu()
         calls4 = [lambda: smg.matmul_q4_ep(a4d, w4, c4, m4, ep4)]
-        st4 = max(8, min(steps, 40))
-        us = timer(calls4, st4, 3, flush=False)
+        us = timer(calls4, steps, 3, flush=False)
         mhz = shader_clock_mhz(smg, torch)  # right after the GEMMs
         flops = 2.0 * m4 * n4 * k4
         tf = flops / (us * 1e-6) / 1e12
@@ -325,7 +398,7 @@ def main():
         ta = torch.randn(m4, k4, dtype=torch.float16, device=dev)
         tb = torch.randn(k4, n4, dtype=torch.float16, device=dev)
         tc = torch.empty(m4, n4, dtype=torch.float16, device=dev)
-        us_t = timer([lambda: torch.matmul(ta, tb, out=tc)], st4, 3, flush=False)
+        us_t = timer([lambda: torch.matmul(ta, tb, out=tc)], steps, 3, flush=False)
         props = torch.cuda.get_device_properties(0)
         extra["config4_q4_gemm"] = {
             "flops": flops, "us": us, "TFLOPS": tf, "frac_f16_mfma": tf / F16_MFMA_PEAK_TFLOPS,
@@ -359,19 +432,21 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": warm,
-        "ms_per_step": us1 / 1e3,
+        "ms_per_step": us1 * len_rot1 / 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (seeded; config 1 distributions)",
-        "config": {"workload": "q4_gemv m=1 K=4096 N=4096 block=32, 64 rotating weight copies, MALL "
-                               "flushed before the timed replay", "m": 1, "k": 4096, "n": 4096, "block": 32},
+        "config": {"workload": "q4_gemv m=1 K=4096 N=4096 block=32; a step = one call on each of 64 weight "
+                               "copies (605 MB, > 2x the MALL), K steps in one graph replay after a 1 GiB read "
+                               "flush; value = algorithmic bytes per call / time per call (dispatch included)",
+                   "m": 1, "k": 4096, "n": 4096, "block": 32, "calls_per_step": len_rot1},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": committed_traffic()},
         "cpu_baseline": cpu,
         "extra": extra,
-        "graph_gap_us": gap,
+        "launch_us": launch_us,
     }
     print(json.dumps(line))
 
@@ -393,7 +468,7 @@ def bench_block(smg, torch, timer, workloads, steps, warm, to_dev):
         attn = smg.SelfAttention(smg.Linear(W("qkv")), smg.Linear(W("out")), H, KV, hd, rope_theta=c["theta"])
         mlp = smg.Mlp.gated(smg.GatedLinear.from_q4(W("gate"), W("up"), smg.Gate.Silu), smg.Linear(W("down")))
         blk = smg.Block(smg.Norm.rms(inp["norm1"], c["eps"]), attn, smg.Norm.rms(inp["norm2"], c["eps"]), mlp)
-        cache = blk.cache(past + 2 * max(warm, copies) + steps + 8)
+        cache = blk.cache(past + 8)  # every step appends at position `past`
         cache.extend(to_dev(inp["cache_k"][:past]), to_dev(inp["cache_v"][:past]))
         blocks.append(blk)
         caches.append(cache)
@@ -405,9 +480,8 @@ def bench_block(smg, torch, timer, workloads, steps, warm, to_dev):
         caches[i].truncate(past)  # every captured step appends at position `past`
         blocks[i].accumulate(xs[i], caches[i], 1)
     calls = [(lambda i=i: step(i)) for i in range(copies)]
-    st5 = max(copies, min(steps, 64)) // copies * copies
-    us = timer(calls, st5, max(warm, copies) // copies * copies)
-    us_hot = timer(calls[:1], st5, copies, flush=False)
+    us = timer(calls, steps, warm)
+    us_hot = timer(calls[:1], steps, warm, flush=False)
     nbytes = workloads.block_bytes(d, H, KV, hd, ffn, past + 1)
     tok_s = 1e6 / us
     return {"workload": "Block::accumulate, 1 row, d=4096, 32/8 heads x 128, SwiGLU 14336, "
@@ -451,9 +525,8 @@ def bench_mlp(smg, torch, timer, workloads, steps, warm):
         smg.glu(both, 1, ffn, smg.Gate.Silu, hid)
         dn.forward(hid, out, 1)
         y.add_(out.float())
-    st = max(copies, min(steps, 64)) // copies * copies
-    us_fused = timer([(lambda i=i: fused[i].accumulate(x16, y, 1)) for i in range(copies)], st, copies)
-    us_plain = timer([(lambda i=i: run_plain(i)) for i in range(copies)], st, copies)
+    us_fused = timer([(lambda i=i: fused[i].accumulate(x16, y, 1)) for i in range(copies)], steps, warm)
+    us_plain = timer([(lambda i=i: run_plain(i)) for i in range(copies)], steps, warm)
     nbytes = workloads.block_stage_bytes(d, 2, 1, 64, ffn, 1)
     mb = nbytes["gate_up"] + nbytes["down"]
     return {"workload": "Mlp::accumulate, 1 row, d=4096, SwiGLU 14336, Q4 block 32; 4 weight copies",

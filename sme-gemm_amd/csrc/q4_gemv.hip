@@ -91,6 +91,53 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
 }
 
 // ---------------------------------------------------------------------------
+// MFMA GEMV, wave-staged (the unchained calls): the first 14 argument dwords
+// -- everything the loads need -- are what the dispatcher preloads into SGPRs
+// (this file is compiled with kernarg preloading), so a wave's first loads do
+// not wait on a kernel-argument fetch; the op-graph arguments that follow are
+// read only at the store. Each wave stages its own activations (q4_wave_loop),
+// so the one workgroup barrier is the partial-tile reduction's.
+// misc = m | block_shift << 8.
+// ---------------------------------------------------------------------------
+template <int MR, bool BF16, bool AFFINE>
+__global__ void __launch_bounds__(MF_WAVES * 64)
+    q4_gemv_wave(const uint8_t *nib, const uint16_t *sc, const uint16_t *lhs, uint16_t *dst, uint32_t n_pad,
+                 uint32_t nchunks, uint32_t k, uint32_t n, uint32_t tiles, uint32_t misc, const uint16_t *mn,
+                 EpArgs ep) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint16_t *wlds = (uint16_t *)smem + (threadIdx.x >> 6) * (MR * 512);  // [MR][4 runs][128]
+    float *red = (float *)(smem + MF_WAVES * MR * 1024);                   // [MF_WAVES][16 cols][MR]
+    const int t = threadIdx.x;
+    const uint32_t tile = xcd_tile(blockIdx.x, tiles);
+    const uint32_t col = tile * 16 + (t & 15);  // < n_pad
+    const uint32_t m = misc & 0xFF, bshift = misc >> 8;
+    Q4WaveArgs g;
+    g.nib = nib;
+    g.sc = sc;
+    g.mn = mn;
+    g.ar = make_rsrc(lhs, m * k * 2u);
+    g.n_pad = n_pad;
+    g.nchunks = nchunks;
+    g.k = k;
+    g.m = m;
+    g.sc_rows = (k + (1u << bshift) - 1) >> bshift;
+    g.block_shift = bshift;
+    const float4_t acc = q4_wave_loop<MR, BF16, AFFINE>(g, wlds, col);
+    const int lane = t & 63, wave = t >> 6, c = lane & 15, grp = lane >> 4;
+    if (c < MR) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) red[(wave * 16 + 4 * grp + v) * MR + c] = acc[v];
+    }
+    __syncthreads();
+    if (t < 16 * MR) {
+        const int cc = t / MR, r = t % MR;
+        const float total = tile_total<MR>(red, cc, r);
+        const uint32_t j = tile * 16 + cc;
+        if (r < (int)m && j < n) dst[(size_t)r * n + j] = finish<BF16>(ep, total, r, j, n);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Generic GEMV (blocks below 32: scales vary inside a chunk; K = 0)
 // ---------------------------------------------------------------------------
 constexpr int TN = 16;        // output columns per workgroup
@@ -266,13 +313,31 @@ hipError_t launch_mfma(const Q4GemvArgs &g, const EpArgs &ep, hipStream_t s, con
     return hipGetLastError();
 }
 
+template <int MR, bool BF16, bool AFFINE>
+hipError_t launch_wave(const Q4GemvArgs &g, const EpArgs &ep, hipStream_t s) {
+    constexpr size_t lds = (size_t)MF_WAVES * MR * 1024 + (size_t)MF_WAVES * 16 * MR * 4;
+    if (lds > 65536) {
+        static bool attr_set = false;  // benign race: every setter writes the same value
+        if (!attr_set) {
+            const hipError_t e = hipFuncSetAttribute((const void *)q4_gemv_wave<MR, BF16, AFFINE>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+            attr_set = true;
+        }
+    }
+    const uint32_t tiles = g.n_pad / 16;
+    hipLaunchKernelGGL((q4_gemv_wave<MR, BF16, AFFINE>), dim3(tiles), dim3(MF_WAVES * 64), lds, s, g.nib, g.sc,
+                       g.lhs, g.dst, g.n_pad, g.nchunks, g.k, g.n, tiles, g.m | (g.block_shift << 8), g.mn, ep);
+    return hipGetLastError();
+}
+
 template <bool BF16, bool AFFINE>
 hipError_t launch_mfma_rows(const Q4GemvArgs &g, size_t m, const EpArgs &ep, hipStream_t s) {
-    if (m <= 1) return launch_mfma<1, false, BF16, AFFINE>(g, ep, s);
-    if (m <= 2) return launch_mfma<2, false, BF16, AFFINE>(g, ep, s);
-    if (m <= 4) return launch_mfma<4, false, BF16, AFFINE>(g, ep, s);
-    if (m <= 8) return launch_mfma<8, false, BF16, AFFINE>(g, ep, s);
-    return launch_mfma<16, false, BF16, AFFINE>(g, ep, s);
+    if (m <= 1) return launch_wave<1, BF16, AFFINE>(g, ep, s);
+    if (m <= 2) return launch_wave<2, BF16, AFFINE>(g, ep, s);
+    if (m <= 4) return launch_wave<4, BF16, AFFINE>(g, ep, s);
+    if (m <= 8) return launch_wave<8, BF16, AFFINE>(g, ep, s);
+    return launch_wave<16, BF16, AFFINE>(g, ep, s);
 }
 
 

@@ -285,6 +285,107 @@ __device__ __forceinline__ float tile_total(const float *red, int cc, int r) {
     return total;
 }
 
+// ---------------------------------------------------------------------------
+// Wave-staged main loop (the plain GEMV's): the same 8 waves x 16 columns and
+// the same per-lane chunks as q4_mfma_mainloop, but each wave stages only the
+// activations its own chunks multiply -- wave w's chunks of a 4096-depth
+// segment are the four 128-depth runs at (seg*128 + 4*(w + 8u)) * 32, u = 0..3,
+// 256 bytes a row each -- into a 1 KB-a-row region of LDS that no other wave
+// reads. So no workgroup barrier separates a wave's activation loads from its
+// MFMAs: a wave starts as soon as its own bytes arrive (LDS operations of one
+// wave execute in order, so its reads see its writes). One load per lane and
+// row covers the wave's 1 KB: lane L loads 8 depths of run L/16 at offset
+// (L%16)*8, and writes them to LDS at L*16 bytes.
+// ---------------------------------------------------------------------------
+struct Q4WaveArgs {
+    const uint8_t *nib;
+    const uint16_t *sc;
+    const uint16_t *mn;
+    rsrc_t ar;            // activation rows [m][k] (zero outside)
+    uint32_t n_pad, nchunks, k, m, sc_rows, block_shift;
+};
+
+template <int MR, bool BF16, bool AFFINE>
+__device__ __forceinline__ float4_t q4_wave_loop(const Q4WaveArgs &g, uint16_t *wlds, uint32_t col) {
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int c = lane & 15, grp = lane >> 4;
+    const uint32_t mag_lo = __builtin_amdgcn_readfirstlane(0x64006400u) | (uint32_t)(t >> 30);
+    const uint32_t mag_hi = __builtin_amdgcn_readfirstlane(0x54005400u) | (uint32_t)(t >> 30);
+    const bool vec = (g.k & 7) == 0;
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    const uint32_t last = g.nchunks - 1;  // nchunks >= 1 here
+    const uint32_t nseg = (g.nchunks + MF_SEG_CH - 1) / MF_SEG_CH;
+    for (uint32_t seg = 0; seg < nseg; seg++) {
+        const uint32_t sc0 = seg * MF_SEG_CH;
+        // this wave's activations first (vmcnt retires in issue order)
+        uint4 areg[MR];
+        const uint32_t da = (sc0 + 4 * (wave + MF_WAVES * grp)) * Q4_CHUNK + (lane & 15) * 8;
+#pragma unroll
+        for (int r = 0; r < MR; r++) areg[r] = load_row8(g.ar, r, g.m, g.k, da, vec);
+        uint4 wq[MF_U];
+        uint16_t sv[MF_U], mv[MF_U];
+#pragma unroll
+        for (int u = 0; u < MF_U; u++) {
+            const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
+            const uint32_t kcc = kc < last ? kc : last;  // clamped: always a valid load
+            wq[u] = *(const uint4 *)(g.nib + cell_index(kcc, col, g.nchunks, g.n_pad) * 16);
+            const size_t si = cell_index((kcc * Q4_CHUNK) >> g.block_shift, col, g.sc_rows, g.n_pad);
+            const uint16_t sl = g.sc[si];
+            sv[u] = kc < g.nchunks ? sl : (uint16_t)0;  // a dead step's weights become 0
+            if constexpr (AFFINE) {
+                const uint16_t ml = g.mn[si];
+                mv[u] = kc < g.nchunks ? ml : (uint16_t)0;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < MR; r++) *(uint4 *)(wlds + r * 512 + lane * 8) = areg[r];
+        // fragments: lane (c, grp) reads row c's 8 depths of dword w of chunk
+        // grp of run u, at [c][u][grp * 32 + w * 8]
+        uint4 abv[MF_U][4];
+        if (c < MR) {
+#pragma unroll
+            for (int u = 0; u < MF_U; u++)
+#pragma unroll
+                for (int w = 0; w < 4; w++)
+                    abv[u][w] = *(const uint4 *)(wlds + c * 512 + u * 128 + grp * 32 + w * 8);
+        } else {
+#pragma unroll
+            for (int u = 0; u < MF_U; u++)
+#pragma unroll
+                for (int w = 0; w < 4; w++) abv[u][w] = make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < MF_U; u++) {
+            const half2_t s2 = {__builtin_bit_cast(_Float16, sv[u]), __builtin_bit_cast(_Float16, sv[u])};
+            const uint32_t words[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                if constexpr (BF16) {
+                    const float mf = AFFINE ? f16_to_f32(mv[u]) : -0.0f;
+                    const uint4 wa = q4_deq8_bf16(words[w], sv[u], mf, mag_lo, mag_hi);
+                    typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wa),
+                                                                  __builtin_bit_cast(bf16x8_t, abv[u][w]), acc,
+                                                                  0, 0, 0);
+                } else {
+                    uint4 wa;
+                    if constexpr (AFFINE) {
+                        const half2_t m2 = {__builtin_bit_cast(_Float16, mv[u]), __builtin_bit_cast(_Float16, mv[u])};
+                        wa = q4_deq8_affine(words[w], s2, m2, mag_lo, mag_hi);
+                    } else {
+                        wa = q4_deq8(words[w], s2, mag_lo, mag_hi);
+                    }
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wa),
+                                                                 __builtin_bit_cast(half8_t, abv[u][w]), acc,
+                                                                 0, 0, 0);
+                }
+            }
+        }
+    }
+    return acc;
+}
+
 // LDS bytes of a q4_mfma_mainloop kernel staging MR rows of a U-step segment
 // (also covers red).
 template <int MR, int U = MF_U>
