@@ -96,8 +96,8 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
 // (this file is compiled with kernarg preloading), so a wave's first loads do
 // not wait on a kernel-argument fetch; the op-graph arguments that follow are
 // read only at the store. Each wave stages its own activations (q4_wave_loop),
-// so the one workgroup barrier is the partial-tile reduction's.
-// misc = m | block_shift << 8.
+// so the one workgroup barrier is the partial-tile reduction's. Block 32, k a
+// multiple of 8 (16-byte activation rows), grids under 2 GiB; misc = m.
 // ---------------------------------------------------------------------------
 template <int MR, bool BF16, bool AFFINE>
 __global__ void __launch_bounds__(MF_WAVES * 64)
@@ -110,18 +110,17 @@ __global__ void __launch_bounds__(MF_WAVES * 64)
     const int t = threadIdx.x;
     const uint32_t tile = xcd_tile(blockIdx.x, tiles);
     const uint32_t col = tile * 16 + (t & 15);  // < n_pad
-    const uint32_t m = misc & 0xFF, bshift = misc >> 8;
+    const uint32_t m = misc;
+    const uint32_t grid_rows = (nchunks + 3) & ~3u;  // the nibble and (block 32) scale grids' rows
     Q4WaveArgs g;
-    g.nib = nib;
-    g.sc = sc;
-    g.mn = mn;
+    g.nr = make_rsrc(nib, grid_rows * n_pad * 16u);
+    g.sr = make_rsrc(sc, grid_rows * n_pad * 2u);
+    g.mr = make_rsrc(mn, AFFINE ? grid_rows * n_pad * 2u : 0u);
     g.ar = make_rsrc(lhs, m * k * 2u);
     g.n_pad = n_pad;
     g.nchunks = nchunks;
     g.k = k;
     g.m = m;
-    g.sc_rows = (k + (1u << bshift) - 1) >> bshift;
-    g.block_shift = bshift;
     const float4_t acc = q4_wave_loop<MR, BF16, AFFINE>(g, wlds, col);
     const int lane = t & 63, wave = t >> 6, c = lane & 15, grp = lane >> 4;
     if (c < MR) {
@@ -327,12 +326,21 @@ hipError_t launch_wave(const Q4GemvArgs &g, const EpArgs &ep, hipStream_t s) {
     }
     const uint32_t tiles = g.n_pad / 16;
     hipLaunchKernelGGL((q4_gemv_wave<MR, BF16, AFFINE>), dim3(tiles), dim3(MF_WAVES * 64), lds, s, g.nib, g.sc,
-                       g.lhs, g.dst, g.n_pad, g.nchunks, g.k, g.n, tiles, g.m | (g.block_shift << 8), g.mn, ep);
+                       g.lhs, g.dst, g.n_pad, g.nchunks, g.k, g.n, tiles, g.m, g.mn, ep);
     return hipGetLastError();
 }
 
 template <bool BF16, bool AFFINE>
 hipError_t launch_mfma_rows(const Q4GemvArgs &g, size_t m, const EpArgs &ep, hipStream_t s) {
+    // the wave-staged kernel: block 32, 16-byte activation rows, grids it
+    // addresses with 32-bit buffer offsets
+    if (g.block_shift != 5 || (g.k & 7) != 0 || cell_grid_rows(g.nchunks) * (size_t)g.n_pad * 16 >= ((size_t)1 << 31)) {
+        if (m <= 1) return launch_mfma<1, false, BF16, AFFINE>(g, ep, s);
+        if (m <= 2) return launch_mfma<2, false, BF16, AFFINE>(g, ep, s);
+        if (m <= 4) return launch_mfma<4, false, BF16, AFFINE>(g, ep, s);
+        if (m <= 8) return launch_mfma<8, false, BF16, AFFINE>(g, ep, s);
+        return launch_mfma<16, false, BF16, AFFINE>(g, ep, s);
+    }
     if (m <= 1) return launch_wave<1, BF16, AFFINE>(g, ep, s);
     if (m <= 2) return launch_wave<2, BF16, AFFINE>(g, ep, s);
     if (m <= 4) return launch_wave<4, BF16, AFFINE>(g, ep, s);

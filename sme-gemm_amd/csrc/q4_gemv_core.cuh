@@ -298,91 +298,101 @@ __device__ __forceinline__ float tile_total(const float *red, int cc, int r) {
 // (L%16)*8, and writes them to LDS at L*16 bytes.
 // ---------------------------------------------------------------------------
 struct Q4WaveArgs {
-    const uint8_t *nib;
-    const uint16_t *sc;
-    const uint16_t *mn;
-    rsrc_t ar;            // activation rows [m][k] (zero outside)
-    uint32_t n_pad, nchunks, k, m, sc_rows, block_shift;
+    rsrc_t nr, sr, mr;    // nibble / scale / min grids (byte counts under 2^31; past them reads 0)
+    rsrc_t ar;            // activation rows [m][k], k a multiple of 8 (zero outside)
+    uint32_t n_pad, nchunks, k, m;
 };
 
+// One 4096-depth segment of the wave-staged loop (block 32: one scale cell
+// per chunk). Addresses are 32-bit buffer offsets: chunk kc = sc0 +
+// 4*(wave + 8u) + grp of column col is cell (kc, col) of the nibble and of the
+// scale grid, whose 4-row block index is sc0/4 + wave + 8u, so the four
+// steps' offsets differ by the constant 8 blocks (512 * n_pad bytes of
+// nibbles, 64 * n_pad of scales).
 template <int MR, bool BF16, bool AFFINE>
-__device__ __forceinline__ float4_t q4_wave_loop(const Q4WaveArgs &g, uint16_t *wlds, uint32_t col) {
-    const int t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6;
+__device__ __forceinline__ void q4_wave_segment(const Q4WaveArgs &g, uint16_t *wlds, uint32_t col, uint32_t sc0,
+                                                uint32_t mag_lo, uint32_t mag_hi, float4_t &acc) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, grp = lane >> 4;
-    const uint32_t mag_lo = __builtin_amdgcn_readfirstlane(0x64006400u) | (uint32_t)(t >> 30);
-    const uint32_t mag_hi = __builtin_amdgcn_readfirstlane(0x54005400u) | (uint32_t)(t >> 30);
-    const bool vec = (g.k & 7) == 0;
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
-    const uint32_t last = g.nchunks - 1;  // nchunks >= 1 here
-    const uint32_t nseg = (g.nchunks + MF_SEG_CH - 1) / MF_SEG_CH;
-    for (uint32_t seg = 0; seg < nseg; seg++) {
-        const uint32_t sc0 = seg * MF_SEG_CH;
-        // this wave's activations first (vmcnt retires in issue order)
-        uint4 areg[MR];
-        const uint32_t da = (sc0 + 4 * (wave + MF_WAVES * grp)) * Q4_CHUNK + (lane & 15) * 8;
+    // this wave's activations first (vmcnt retires in issue order)
+    uint4 areg[MR];
+    const uint32_t da = (sc0 + 4 * (wave + MF_WAVES * grp)) * Q4_CHUNK + (lane & 15) * 8;
 #pragma unroll
-        for (int r = 0; r < MR; r++) areg[r] = load_row8(g.ar, r, g.m, g.k, da, vec);
-        uint4 wq[MF_U];
-        uint16_t sv[MF_U], mv[MF_U];
+    for (int r = 0; r < MR; r++) areg[r] = bload16(g.ar, (r < (int)g.m && da < g.k) ? (r * g.k + da) * 2u : OOB);
+    const uint32_t cell0 = ((sc0 >> 2) + wave) * 4 * g.n_pad + grp * 16 + (col >> 4) * 64 + (col & 15);
+    uint4 wq[MF_U];
+    uint16_t sv[MF_U], mv[MF_U];
 #pragma unroll
-        for (int u = 0; u < MF_U; u++) {
-            const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
-            const uint32_t kcc = kc < last ? kc : last;  // clamped: always a valid load
-            wq[u] = *(const uint4 *)(g.nib + cell_index(kcc, col, g.nchunks, g.n_pad) * 16);
-            const size_t si = cell_index((kcc * Q4_CHUNK) >> g.block_shift, col, g.sc_rows, g.n_pad);
-            const uint16_t sl = g.sc[si];
-            sv[u] = kc < g.nchunks ? sl : (uint16_t)0;  // a dead step's weights become 0
-            if constexpr (AFFINE) {
-                const uint16_t ml = g.mn[si];
-                mv[u] = kc < g.nchunks ? ml : (uint16_t)0;
-            }
+    for (int u = 0; u < MF_U; u++) {
+        const uint32_t kc = sc0 + 4 * (wave + MF_WAVES * u) + grp;
+        wq[u] = bload16(g.nr, cell0 * 16 + u * 512 * g.n_pad);
+        const uint32_t so = cell0 * 2 + u * 64 * g.n_pad;
+        const uint16_t sl = bload2(g.sr, so);
+        // a step past K has zero weights (the padding rows of a gathered grid
+        // are not written, so its nibbles and scales may hold anything finite
+        // or not: only the scale is replaced)
+        sv[u] = kc < g.nchunks ? sl : (uint16_t)0;
+        if constexpr (AFFINE) {
+            const uint16_t ml = bload2(g.mr, so);
+            mv[u] = kc < g.nchunks ? ml : (uint16_t)0;
         }
+    }
 #pragma unroll
-        for (int r = 0; r < MR; r++) *(uint4 *)(wlds + r * 512 + lane * 8) = areg[r];
-        // fragments: lane (c, grp) reads row c's 8 depths of dword w of chunk
-        // grp of run u, at [c][u][grp * 32 + w * 8]
-        uint4 abv[MF_U][4];
-        if (c < MR) {
+    for (int r = 0; r < MR; r++) *(uint4 *)(wlds + r * 512 + lane * 8) = areg[r];
+    // fragments: lane (c, grp) reads row c's 8 depths of dword w of chunk
+    // grp of run u, at [c][u][grp * 32 + w * 8]
+    uint4 abv[MF_U][4];
+    if (c < MR) {
 #pragma unroll
-            for (int u = 0; u < MF_U; u++)
+        for (int u = 0; u < MF_U; u++)
 #pragma unroll
-                for (int w = 0; w < 4; w++)
-                    abv[u][w] = *(const uint4 *)(wlds + c * 512 + u * 128 + grp * 32 + w * 8);
-        } else {
+            for (int w = 0; w < 4; w++) abv[u][w] = *(const uint4 *)(wlds + c * 512 + u * 128 + grp * 32 + w * 8);
+    } else {
 #pragma unroll
-            for (int u = 0; u < MF_U; u++)
+        for (int u = 0; u < MF_U; u++)
 #pragma unroll
-                for (int w = 0; w < 4; w++) abv[u][w] = make_uint4(0, 0, 0, 0);
-        }
+            for (int w = 0; w < 4; w++) abv[u][w] = make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
-        for (int u = 0; u < MF_U; u++) {
-            const half2_t s2 = {__builtin_bit_cast(_Float16, sv[u]), __builtin_bit_cast(_Float16, sv[u])};
-            const uint32_t words[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
+    for (int u = 0; u < MF_U; u++) {
+        const half2_t s2 = {__builtin_bit_cast(_Float16, sv[u]), __builtin_bit_cast(_Float16, sv[u])};
+        const uint32_t words[4] = {wq[u].x, wq[u].y, wq[u].z, wq[u].w};
 #pragma unroll
-            for (int w = 0; w < 4; w++) {
-                if constexpr (BF16) {
-                    const float mf = AFFINE ? f16_to_f32(mv[u]) : -0.0f;
-                    const uint4 wa = q4_deq8_bf16(words[w], sv[u], mf, mag_lo, mag_hi);
-                    typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wa),
-                                                                  __builtin_bit_cast(bf16x8_t, abv[u][w]), acc,
-                                                                  0, 0, 0);
+        for (int w = 0; w < 4; w++) {
+            if constexpr (BF16) {
+                const float mf = AFFINE ? f16_to_f32(mv[u]) : -0.0f;
+                const uint4 wa = q4_deq8_bf16(words[w], sv[u], mf, mag_lo, mag_hi);
+                typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wa),
+                                                              __builtin_bit_cast(bf16x8_t, abv[u][w]), acc, 0, 0, 0);
+            } else {
+                uint4 wa;
+                if constexpr (AFFINE) {
+                    const half2_t m2 = {__builtin_bit_cast(_Float16, mv[u]), __builtin_bit_cast(_Float16, mv[u])};
+                    wa = q4_deq8_affine(words[w], s2, m2, mag_lo, mag_hi);
                 } else {
-                    uint4 wa;
-                    if constexpr (AFFINE) {
-                        const half2_t m2 = {__builtin_bit_cast(_Float16, mv[u]), __builtin_bit_cast(_Float16, mv[u])};
-                        wa = q4_deq8_affine(words[w], s2, m2, mag_lo, mag_hi);
-                    } else {
-                        wa = q4_deq8(words[w], s2, mag_lo, mag_hi);
-                    }
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wa),
-                                                                 __builtin_bit_cast(half8_t, abv[u][w]), acc,
-                                                                 0, 0, 0);
+                    wa = q4_deq8(words[w], s2, mag_lo, mag_hi);
                 }
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wa),
+                                                             __builtin_bit_cast(half8_t, abv[u][w]), acc, 0, 0, 0);
             }
         }
     }
+}
+
+// The whole of K, segment by segment; the first segment is peeled so that a
+// call of K <= 4096 runs straight-line code from the kernel's entry to its
+// last MFMA (instruction fetch after a launch reaches far memory).
+template <int MR, bool BF16, bool AFFINE>
+__device__ __forceinline__ float4_t q4_wave_loop(const Q4WaveArgs &g, uint16_t *wlds, uint32_t col) {
+    const int t = threadIdx.x;
+    const uint32_t mag_lo = __builtin_amdgcn_readfirstlane(0x64006400u) | (uint32_t)(t >> 30);
+    const uint32_t mag_hi = __builtin_amdgcn_readfirstlane(0x54005400u) | (uint32_t)(t >> 30);
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    q4_wave_segment<MR, BF16, AFFINE>(g, wlds, col, 0, mag_lo, mag_hi, acc);
+    const uint32_t nseg = (g.nchunks + MF_SEG_CH - 1) / MF_SEG_CH;
+    for (uint32_t seg = 1; seg < nseg; seg++)
+        q4_wave_segment<MR, BF16, AFFINE>(g, wlds, col, seg * MF_SEG_CH, mag_lo, mag_hi, acc);
     return acc;
 }
 
