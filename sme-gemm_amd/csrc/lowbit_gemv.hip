@@ -388,16 +388,34 @@ __global__ void __launch_bounds__(T) lowbit_prequant(const uint16_t *lhs, uint32
 
 // SPB: slabs per block when fixed at compile time (2 = blocks of 128, the
 // usual decode format), 0 for any block (runtime block structure).
-template <int KIND, int MR, int NG, int SPB>
-__global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
+// EPV: the store's op-graph, compiled for the common shapes (the host picks
+// it from the graph): 0 any graph (ep), 1 none, 2 add_col(col_b) then a
+// trailing activation act (0: none, alpha its scalar), 3 mul_col(col_a),
+// add_col(col_b), then act. Each runs the graph's f32 steps in its order on
+// the f16-rounded sum, as the generic store does.
+// The first 14 argument dwords -- all that the first loads need -- arrive in
+// SGPRs with the wave (this file is compiled with kernarg preloading); the
+// rest derive from them: misc = m | block_shift << 8 | cg_shift << 16, src is
+// A (f16 [m][k], one row) or its pre-quantized rows (int8 [m][kq], several).
+template <int KIND, int MR, int NG, int SPB, int EPV>
+__global__ void __launch_bounds__(T)
+    lowbit_tile(const uint8_t *codes, const uint16_t *sc, const void *src, uint16_t *dst, uint32_t n_pad, uint32_t k,
+                uint32_t tiles, uint32_t misc, uint32_t codebook, uint32_t ngroups, uint32_t n,
+                const uint16_t *col_a, const uint16_t *col_b, uint32_t act, float alpha, const float *qs,
+                const int32_t *qsum, EpArgs ep) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr uint32_t SPG = KIND == 2 ? 4 : 8;  // slabs per code group
     constexpr int NSW = NG * (int)SPG;            // slabs per wave
     constexpr int QP = 2;                         // A passes held in registers (K <= 8192)
     constexpr int PQ = 4;                         // pre-quantized block entries per thread
-    const uint32_t block = 1u << g.block_shift;
-    const uint32_t nbq = g.nbq, kq = g.kq;
-    const uint32_t cg = 1u << g.cg_shift;         // 16-column groups in this workgroup
+    const uint32_t m = misc & 0xFF, block_shift = (misc >> 8) & 0xFF, cg_shift = misc >> 16;
+    const uint32_t block = 1u << block_shift;
+    // the host's geometry (tile_geometry_cg): 8 / CG waves along K cover kq
+    const uint32_t kq = (8u >> cg_shift) * NSW * LB_SLAB;
+    const uint32_t nbq = ((kq >> block_shift) + 3) & ~3u;
+    const uint32_t grp_depths = KIND == 2 ? Q2_GROUP : Q1_GROUP;
+    const uint32_t sc_rows = (ngroups * grp_depths + block - 1) >> block_shift;
+    const uint32_t cg = 1u << cg_shift;           // 16-column groups in this workgroup
     const uint32_t ncol = 16 * cg;
     const uint32_t qs_ = kq + 16;   // q row stride (bytes)
     const uint32_t bs = nbq + 4;    // block-sum / scale row stride (elements)
@@ -413,12 +431,12 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
     const int lane = t & 63, wave = t >> 6;
     const int gq4 = lane >> 4, c = lane & 15;
     // wave -> (column group gi, K range kw): 8 / CG waves share a column group
-    const uint32_t wpg_shift = 3 - g.cg_shift;
+    const uint32_t wpg_shift = 3 - cg_shift;
     const uint32_t gi = (uint32_t)wave >> wpg_shift, kw = (uint32_t)wave & ((1u << wpg_shift) - 1);
-    const uint32_t wg_col0 = xcd_tile(blockIdx.x, gridDim.x) * ncol;
+    const uint32_t wg_col0 = xcd_tile(blockIdx.x, tiles) * ncol;
     const uint32_t col0 = wg_col0 + gi * 16;  // this wave's 16 columns
-    const rsrc_t ar = make_rsrc(g.lhs, g.m * g.k * 2u);
-    const bool vec = (g.k & 7) == 0;
+    const rsrc_t ar = make_rsrc(src, m * k * 2u);
+    const bool vec = (k & 7) == 0;
 
     // -- 1. loads: A or its quantized rows (waited on first), codes, scales
     uint4 areg[QP][MR];
@@ -426,23 +444,23 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
     float pqs[PQ];      // quantized rows' block scales and sums, entries t + T*j
     int32_t pqsum[PQ];  // (m * nbq <= PQ * T: the host checks)
     if constexpr (MR > 1) {
-        const rsrc_t qr = make_rsrc(g.q, g.m * kq);
+        const rsrc_t qr = make_rsrc(src, m * kq);
 #pragma unroll
         for (int r = 0; r < MR; r++)
-            qreg[r] = bload16(qr, ((uint32_t)r < g.m && 16u * t < kq) ? r * kq + 16 * t : OOB);
-        const rsrc_t fr = make_rsrc(g.qs, g.m * nbq * 4u), ur = make_rsrc(g.qsum, g.m * nbq * 4u);
+            qreg[r] = bload16(qr, ((uint32_t)r < m && 16u * t < kq) ? r * kq + 16 * t : OOB);
+        const rsrc_t fr = make_rsrc(qs, m * nbq * 4u), ur = make_rsrc(qsum, m * nbq * 4u);
 #pragma unroll
         for (int j = 0; j < PQ; j++) {
             const uint32_t i = t + T * j;
-            pqs[j] = __uint_as_float(bload4(fr, i < g.m * nbq ? i * 4u : OOB));
-            pqsum[j] = (int32_t)bload4(ur, i < g.m * nbq ? i * 4u : OOB);
+            pqs[j] = __uint_as_float(bload4(fr, i < m * nbq ? i * 4u : OOB));
+            pqsum[j] = (int32_t)bload4(ur, i < m * nbq ? i * 4u : OOB);
         }
     } else {
 #pragma unroll
         for (int p = 0; p < QP; p++)
 #pragma unroll
             for (int r = 0; r < MR; r++)
-                areg[p][r] = (uint32_t)p * QPASS < kq ? load_row8(ar, r, g.m, g.k, p * QPASS + 8 * t, vec)
+                areg[p][r] = (uint32_t)p * QPASS < kq ? load_row8(ar, r, m, k, p * QPASS + 8 * t, vec)
                                                       : make_uint4(0, 0, 0, 0);
     }
     // scale rows next (waited on before the first barrier), then the codes,
@@ -450,18 +468,18 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
     // can still be in flight when the waits before them end
     uint4 sreg;
     {
-        const rsrc_t sr = make_rsrc(g.sc, (uint32_t)cell_grid_rows(g.sc_rows) * g.n_pad * 2u);
-        const uint32_t bb = t >> (g.cg_shift + 1), piece = t & (2 * cg - 1);  // 8 columns a piece
-        sreg = bload16(sr, (bb < nbq && bb < g.sc_rows) ? (uint32_t)cell_index(bb, wg_col0 + piece * 8, g.sc_rows, g.n_pad) * 2u
-                                                        : OOB);
+        const rsrc_t sr = make_rsrc(sc, ((sc_rows + 3) & ~3u) * n_pad * 2u);
+        const uint32_t bb = t >> (cg_shift + 1), piece = t & (2 * cg - 1);  // 8 columns a piece
+        sreg = bload16(sr, (bb < nbq && bb < sc_rows) ? (uint32_t)cell_index(bb, wg_col0 + piece * 8, sc_rows, n_pad) * 2u
+                                                      : OOB);
     }
     uint4 wreg[NG];
     {
-        const rsrc_t cr = make_rsrc(g.codes, g.codes_bytes);
+        const rsrc_t cr = make_rsrc(codes, ((ngroups + 3) & ~3u) * n_pad * 64u);
 #pragma unroll
         for (int i = 0; i < NG; i++) {
             const uint32_t grp = kw * NG + i;
-            wreg[i] = bload16(cr, grp < g.ngroups ? ((uint32_t)cell_index(grp, col0 + c, g.ngroups, g.n_pad) * 4 + gq4) * 16 : OOB);
+            wreg[i] = bload16(cr, grp < ngroups ? ((uint32_t)cell_index(grp, col0 + c, ngroups, n_pad) * 4 + gq4) * 16 : OOB);
         }
     }
     // this lane's block-sum slot (step 3), computed before the epilogue loads
@@ -470,13 +488,20 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
     // one of those loads targets, and wait for that load
     uint32_t dp_off = (c * ncol + gi * 16 + 4 * gq4) * bs;
     asm volatile("" : "+v"(dp_off));
-    const bool folder = (uint32_t)t < ncol * g.m;
-    const int fc = t & (ncol - 1), frow = t >> (4 + g.cg_shift);
+    const bool folder = (uint32_t)t < ncol * m;
+    const int fc = t & (ncol - 1), frow = t >> (4 + cg_shift);
 
     // the epilogue operands last: their addresses wait on the op-graph's
     // kernel arguments, which must not hold up the codes
     EpPre pre = {};
-    if (folder && wg_col0 + fc < g.n) pre = ep_prefetch(ep, frow, wg_col0 + fc, g.n);
+    uint16_t opa = 0, opb = 0;
+    if constexpr (EPV == 0) {
+        if (folder && wg_col0 + fc < n) pre = ep_prefetch(ep, frow, wg_col0 + fc, n);
+    } else if constexpr (EPV >= 2) {
+        const uint32_t ob = folder && wg_col0 + fc < n ? (wg_col0 + fc) * 2u : OOB;
+        opb = bload2(make_rsrc(col_b, n * 2u), ob);
+        if constexpr (EPV == 3) opa = bload2(make_rsrc(col_a, n * 2u), ob);
+    }
 
     // -- 2. quantize A (quantize_row, src/kernels/lowbit/matmul.rs:354-371),
     //       or store the rows quantized beforehand
@@ -496,11 +521,11 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
 #pragma unroll
         for (int p = 0; p < QP; p++) {
             if ((uint32_t)p * QPASS >= kq) break;  // uniform
-            quant_pass<KIND, MR>(areg[p], p, ql, qs_, sa, as, nbq, kq, g.block_shift, wmax, wsum);
+            quant_pass<KIND, MR>(areg[p], p, ql, qs_, sa, as, nbq, kq, block_shift, wmax, wsum);
         }
     }
     if ((uint32_t)t < 2 * cg * nbq) {  // transpose: scale of (block bb, column 8 piece + e)
-        const uint32_t bb = t >> (g.cg_shift + 1), piece = t & (2 * cg - 1);
+        const uint32_t bb = t >> (cg_shift + 1), piece = t & (2 * cg - 1);
         const uint32_t sw[4] = {sreg.x, sreg.y, sreg.z, sreg.w};
 #pragma unroll
         for (int e = 0; e < 8; e++) scl[(8 * piece + e) * bs + bb] = (uint16_t)(sw[e / 2] >> (16 * (e % 2)));
@@ -520,7 +545,7 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
             const uint32_t w = words[i % 4];
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                wa[j] = (int)__builtin_amdgcn_perm(g.codebook, g.codebook, (w >> (2 * j)) & 0x03030303u);
+                wa[j] = (int)__builtin_amdgcn_perm(codebook, codebook, (w >> (2 * j)) & 0x03030303u);
         } else {
             const uint32_t w = words[(i % 8) / 2], hs = 4 * (i % 2);
 #pragma unroll
@@ -614,7 +639,7 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
         const uint16_t *cp = scl + fc * bs;
         const float *ap = sa + frow * nbq;
         const int32_t *qp = as + frow * nbq;
-        const uint32_t nb_live = (g.k + block - 1) >> g.block_shift;
+        const uint32_t nb_live = (k + block - 1) >> block_shift;
         float total = 0.0f;
         // 16 blocks from b0; TAIL: some are past K, and add
         // fmaf(0, 0, total) == total (total starts at +0 and never
@@ -659,26 +684,90 @@ __global__ void __launch_bounds__(T) lowbit_tile(LtArgs g, EpArgs ep) {
         for (uint32_t b0 = 0; b0 < nb_full; b0 += 16) group16(b0, std::false_type{});
         if (nb_full < nb_live) group16(nb_full, std::true_type{});
         const uint32_t j = wg_col0 + fc;
-        if (j < g.n) g.dst[(size_t)frow * g.n + j] = finish_pre<false>(ep, pre, total, frow, j, g.n);
+        if (j < n) {
+            uint16_t out;
+            if constexpr (EPV == 0) {
+                out = finish_pre<false>(ep, pre, total, frow, j, n);
+            } else {
+                out = f32_to_f16(total);
+                if constexpr (EPV >= 2) {
+                    float x = f16_to_f32(out);
+                    if constexpr (EPV == 3) x = x * f16_to_f32(opa);
+                    x = x + f16_to_f32(opb);
+                    out = act == EP_ACT_NONE ? f32_to_f16(x) : act_round16<false>(act, x, alpha);
+                }
+            }
+            dst[(size_t)frow * n + j] = out;
+        }
     }
 }
 
-template <int KIND, int MR, int NG, int SPB>
-hipError_t launch_tile_t(const LtArgs &g, const EpArgs &ep, hipStream_t s) {
+// The compiled store variant for an op-graph (lowbit_tile's EPV): 1 for no
+// graph, 2 for [add_col] and 3 for [mul_col, add_col], each optionally
+// followed by a trailing activation; 0 (the generic store) for anything else.
+struct EpPick {
+    int v;
+    const uint16_t *a, *b;
+    uint32_t act;
+    float alpha;
+};
+EpPick pick_ep(const EpArgs &ep) {
+    EpPick p = {0, nullptr, nullptr, EP_ACT_NONE, 0.0f};
+    uint32_t n = ep.n_nodes;
+    if (n == 0) {
+        p.v = 1;
+        return p;
+    }
+    const EpNode &last = ep.nodes[n - 1];
+    if (last.op == EP_OP_ACT) {
+        p.act = last.aux;
+        p.alpha = last.scalar;
+        n--;
+    }
+    if (n == 1 && ep.nodes[0].op == EP_OP_ADD_COL) {
+        p.v = 2;
+        p.b = (const uint16_t *)ep.nodes[0].ptr;
+    } else if (n == 2 && ep.nodes[0].op == EP_OP_MUL_COL && ep.nodes[1].op == EP_OP_ADD_COL) {
+        p.v = 3;
+        p.a = (const uint16_t *)ep.nodes[0].ptr;
+        p.b = (const uint16_t *)ep.nodes[1].ptr;
+    }
+    if (p.v == 0) p = {0, nullptr, nullptr, EP_ACT_NONE, 0.0f};
+    return p;
+}
+
+template <int KIND, int MR, int NG, int SPB, int EPV>
+hipError_t launch_tile_v(const LtArgs &g, const EpArgs &ep, const EpPick &pk, hipStream_t s) {
     const size_t lds = tile_lds_bytes(g.kq, g.nbq, MR, 1u << g.cg_shift);
     if (lds > 64 * 1024) {
         static bool attr = false;  // benign race: every setter writes the same value
         if (!attr) {
-            const hipError_t e = hipFuncSetAttribute((const void *)lowbit_tile<KIND, MR, NG, SPB>,
+            const hipError_t e = hipFuncSetAttribute((const void *)lowbit_tile<KIND, MR, NG, SPB, EPV>,
                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                                      160 * 1024);
             if (e != hipSuccess) return e;
             attr = true;
         }
     }
-    hipLaunchKernelGGL((lowbit_tile<KIND, MR, NG, SPB>), dim3(g.n_pad / (16u << g.cg_shift)), dim3(T), lds,
-                       s, g, ep);
+    const uint32_t tiles = g.n_pad / (16u << g.cg_shift);
+    const void *src = MR > 1 ? (const void *)g.q : (const void *)g.lhs;
+    hipLaunchKernelGGL((lowbit_tile<KIND, MR, NG, SPB, EPV>), dim3(tiles), dim3(T), lds, s, g.codes, g.sc, src,
+                       g.dst, g.n_pad, g.k, tiles, g.m | (g.block_shift << 8) | (g.cg_shift << 16), g.codebook,
+                       g.ngroups, g.n, pk.a, pk.b, pk.act, pk.alpha, g.qs, g.qsum, ep);
     return hipGetLastError();
+}
+
+// Compiled stores serve the usual decode format (block 128, SPB 2); other
+// blocks take the generic store.
+template <int KIND, int MR, int NG, int SPB>
+hipError_t launch_tile_t(const LtArgs &g, const EpArgs &ep, hipStream_t s) {
+    const EpPick pk = SPB == 2 ? pick_ep(ep) : EpPick{0, nullptr, nullptr, EP_ACT_NONE, 0.0f};
+    if constexpr (SPB == 2) {
+        if (pk.v == 1) return launch_tile_v<KIND, MR, NG, SPB, 1>(g, ep, pk, s);
+        if (pk.v == 2) return launch_tile_v<KIND, MR, NG, SPB, 2>(g, ep, pk, s);
+        if (pk.v == 3) return launch_tile_v<KIND, MR, NG, SPB, 3>(g, ep, pk, s);
+    }
+    return launch_tile_v<KIND, MR, NG, SPB, 0>(g, ep, pk, s);
 }
 
 template <int KIND, int MR>
