@@ -585,8 +585,13 @@ bool q4_gemv_rows(const WDev &w, size_t m, bool gemm_q4r) {
     return !gemm_q4r && m <= Q4_GEMV_CHUNK_MAX &&
            (m + Q4_GEMV_WIDE_ROWS - 1) / Q4_GEMV_WIDE_ROWS * w.n <= Q4_GEMV_CHUNK_COLS;
 }
-size_t q4_split_bytes(const WDev &w, size_t m, bool bf16) {
-    return bf16 || q4_gemv_rows(w, m, true) ? 0 : q4r_split_bytes(w, m);
+// Bytes of split-K partials a run_q4 call with this A will use: only calls that
+// gemm_q4r serves (it reads A itself, so an A it cannot read goes elsewhere and
+// needs none). lhs == nullptr stands for the host entry points' staging copy of
+// A, which is 256-byte aligned.
+size_t q4_split_bytes(const WDev &w, size_t m, const uint16_t *lhs, bool bf16) {
+    if (bf16 || !q4r_supported(w, m, 1, (long)w.k, lhs, bf16) || q4_gemv_rows(w, m, true)) return 0;
+    return q4r_split_bytes(w, m);
 }
 hipError_t run_q4(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs, const EpArgs &ea,
                   bool bf16, hipStream_t s, void *split, size_t split_bytes) {
@@ -619,7 +624,7 @@ int q4_fail(const char *what, hipError_t e) {
 }
 hipError_t run_q4_dev(int device, const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
                       const EpArgs &ea, bool bf16, hipStream_t s) {
-    const size_t sb = q4_split_bytes(w, m, bf16);
+    const size_t sb = q4_split_bytes(w, m, lhs, bf16);
     void *part = nullptr;
     if (sb && !(part = split_pool().get(device, s, sb))) return hipErrorOutOfMemory;
     return run_q4(w, m, dst, lhs, ea, bf16, s, part, sb);
@@ -720,11 +725,19 @@ std::vector<int32_t> glu_store_order(size_t hidden) {
 // The attention's RoPE table covering positions [0, cap): cos and sin of
 // (pos as f32 * inv_freq[i]) in f32 (examples/bonsai/model.rs:77-85), computed
 // here on the host as the reference computes its angles. A table that is
-// outgrown is retired, not freed.
-int ensure_rope(smg_attn *a, size_t cap) {
+// outgrown is retired, not freed. *tab and *tab_cap receive the table and its
+// capacity as read under the lock (another thread may grow the table after the
+// lock is released, so a caller uses this snapshot, never a->rope / a->rope_cap).
+int ensure_rope(smg_attn *a, size_t cap, const float **tab_out, size_t *tab_cap) {
+    *tab_out = nullptr;
+    *tab_cap = 0;
     if (a->theta <= 0.0) return SMG_OK;
     std::lock_guard<std::mutex> lk(a->mu);
-    if (a->rope_cap >= cap) return SMG_OK;
+    if (a->rope_cap >= cap) {
+        *tab_out = a->rope;
+        *tab_cap = a->rope_cap;
+        return SMG_OK;
+    }
     const size_t half = a->hd / 2, ncap = std::max(cap, 2 * a->rope_cap);
     std::vector<float> tab(2 * ncap * half);
     for (size_t pos = 0; pos < ncap; pos++)
@@ -744,6 +757,8 @@ int ensure_rope(smg_attn *a, size_t cap) {
     if (a->rope) a->retired.push_back(a->rope);
     a->rope = d;
     a->rope_cap = ncap;
+    *tab_out = d;
+    *tab_cap = ncap;
     return SMG_OK;
 }
 
@@ -794,7 +809,9 @@ int attn_step(smg_attn *a, smg_kv_cache *c, const uint16_t *x16, const float *nx
               float *y, void *stream, size_t base = 0) {
     int rc = check_cache(a, c, 1);
     if (rc) return rc;
-    if ((rc = ensure_rope(a, c->cap))) return rc;
+    const float *rope = nullptr;
+    size_t rope_cap = 0;
+    if ((rc = ensure_rope(a, c->cap, &rope, &rope_cap))) return rc;
     const size_t pos = c->len, ld = a->kv_heads * a->hd, qlen = a->heads * a->hd, half = a->hd / 2;
     const size_t nsplit = attn_splits(pos + 1);
     DecodeScratch sc;
@@ -808,8 +825,8 @@ int attn_step(smg_attn *a, smg_kv_cache *c, const uint16_t *x16, const float *nx
     b.k_row = c->k + pos * ld;
     b.v_row = c->v + pos * ld;
     if (a->theta > 0.0) {
-        b.cs = a->rope + pos * half;
-        b.sn = a->rope + a->rope_cap * half + pos * half;
+        b.cs = rope + pos * half;
+        b.sn = rope + rope_cap * half + pos * half;
     }
     b.scale = c->scale;
     b.heads = (uint32_t)a->heads;
@@ -918,9 +935,7 @@ void destroy_mlp(smg_mlp *m) {
 // memory or pinned host memory. Pageable host memory (a malloc'd buffer, a
 // numpy array) would make the kernel fault; it is refused with SMG_EINVAL
 // instead. The runtime's allocation table answers this on the host (a failed
-// lookup's error is cleared so it is not reported by a later call). While the
-// stream is being captured into a graph the lookup is skipped: a capture is
-// built from calls that have run eagerly, where it applies.
+// lookup's error is cleared so it is not reported by a later call).
 bool device_readable(const void *p, int device) {
     hipPointerAttribute_t at;
     if (hipPointerGetAttributes(&at, p) != hipSuccess) {
@@ -931,14 +946,13 @@ bool device_readable(const void *p, int device) {
     return at.type == hipMemoryTypeManaged || at.type == hipMemoryTypeHost;
 }
 
+// The pointer query is not a stream operation, so it runs (and refuses a host
+// pointer) also while the stream is being captured into a graph: a captured
+// call never records a kernel that would read a pageable host address on replay.
 int check_dev_ptrs(const char *who, int device, void *stream, const EpArgs &ea,
                    std::initializer_list<const void *> ptrs) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess) {
-        (void)hipGetLastError();
-        return fail(SMG_EHIP, who);
-    }
-    if (cs != hipStreamCaptureStatusNone) return SMG_OK;
+    (void)who;
+    (void)stream;
     for (const void *p : ptrs)
         if (p && !device_readable(p, device))
             return fail(SMG_EINVAL, "device call: an operand pointer is not memory this device can read "
@@ -1139,7 +1153,7 @@ static int q4_host(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t
     const size_t n = w->d.n, k = w->d.k;
     if (m == 0 || n == 0) return SMG_OK;  // q4/matmul.rs:43-44
     const WDev d = w->d;
-    const size_t sb = q4_split_bytes(d, m, bf16);  // split-K partials in the call's staging
+    const size_t sb = q4_split_bytes(d, m, nullptr, bf16);  // split-K partials in the call's staging
     return host_call(bf16 ? "gemm_gpu_b16b16_q4" : "gemm_gpu_f16f16_q4", w->device, m, n, k, dst,
                      m * n, false, lhs, m * k, ep, sb,
                      [&](uint16_t *dd, const uint16_t *dl, const EpArgs &ea, void *sc, hipStream_t s) {

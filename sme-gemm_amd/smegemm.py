@@ -249,12 +249,15 @@ def _bf16_round(x: float) -> float:
 
 def _scalar_to_f32(v, bf16: bool) -> float:
     """A scalar operand is stored as `v.ep_to_f32()` of a T (graph.rs:86-96):
-    pass either a float (rounded to T here) or T's bit pattern as an int."""
-    if isinstance(v, (np.uint16, int)) and not isinstance(v, bool):
+    pass a number (int or float, rounded to T here) or T's bit pattern given
+    explicitly as np.uint16."""
+    if isinstance(v, np.uint16):
         if bf16:
             return float(np.uint32(int(v) << 16).view(np.float32))
-        return float(np.uint16(v).view(np.float16))
-    return _bf16_round(v) if bf16 else float(np.float16(v))
+        return float(v.view(np.float16))
+    if isinstance(v, bool) or not isinstance(v, (int, float, np.floating, np.integer)):
+        raise TypeError(f"scalar operand: a number or np.uint16 bits, got {type(v).__name__}")
+    return _bf16_round(float(v)) if bf16 else float(np.float16(float(v)))
 
 
 class Epilogue:
@@ -911,12 +914,9 @@ class Gemm:
         return self
 
     def beta(self, v) -> "Gemm":
-        if isinstance(v, (np.uint16,)) or (isinstance(v, int) and not isinstance(v, bool)):
-            self._beta = int(v)
-        elif self.packed.bf16:
-            self._beta = int(np.float32(_bf16_round(v)).view(np.uint32)) >> 16
-        else:
-            self._beta = int(np.float16(v).view(np.uint16))
+        """Gemm::beta(v: T): a value (int or float, rounded to T), or T's bit
+        pattern given explicitly as np.uint16."""
+        self._beta = _bits16(v, self.packed.bf16)
         return self
 
     def __getattr__(self, name):
@@ -980,11 +980,27 @@ def _check_strided(what, length, d0, rs, d1, cs):
 
 
 def _bits16(v, bf16):
-    if isinstance(v, (np.uint16,)) or (isinstance(v, int) and not isinstance(v, bool)):
+    """A scalar of T (f16 or bf16) as its bit pattern. Python ints and floats
+    are values, rounded to T (alpha=0, beta=1 mean 0.0 and 1.0, as the
+    reference's `alpha: T`); only an np.uint16 is taken as raw bits."""
+    if isinstance(v, np.uint16):
         return int(v)
+    if isinstance(v, bool) or not isinstance(v, (int, float, np.floating, np.integer)):
+        raise TypeError(f"alpha/beta: a number or np.uint16 bits, got {type(v).__name__}")
     if bf16:
-        return int(np.float32(_bf16_round(v)).view(np.uint32)) >> 16
-    return int(np.float16(v).view(np.uint16))
+        return int(np.float32(_bf16_round(float(v))).view(np.uint32)) >> 16
+    return int(np.float16(float(v)).view(np.uint16))
+
+
+def _gemm_host16(v, bf16: bool, name: str) -> np.ndarray:
+    """A host GEMM operand as its 16-bit patterns: uint16 bits, or float16
+    values for an f16 GEMM. Any other dtype is refused rather than
+    reinterpreted (a float32 array viewed as uint16 is twice as many
+    meaningless halves)."""
+    arr = np.asarray(v)
+    if arr.dtype == np.uint16 or (arr.dtype == np.float16 and not bf16):
+        return arr
+    raise TypeError(f"{name}: expected {'uint16 bf16 bits' if bf16 else 'float16 or uint16 bits'}, got {arr.dtype}")
 
 
 def _gemm_strided(bf16, m, n, k, c, c_rs, c_cs, a, a_rs, a_cs, b, b_rs, b_cs, alpha, beta, accum):
@@ -1004,10 +1020,11 @@ def _gemm_strided(bf16, m, n, k, c, c_rs, c_cs, a, a_rs, a_cs, b, b_rs, b_cs, al
         _check(lib().smg_gemm_run_dev(int(bf16), m, n, k, c.data_ptr(), c_cs, c_rs, read_dst, a.data_ptr(), a_cs,
                                       a_rs, b.data_ptr(), b_cs, b_rs, ab, bb, _stream()), "smg_gemm_run_dev")
         return c
-    cc = np.asarray(c)
-    if cc.dtype not in (np.uint16, np.float16) or not cc.flags.c_contiguous:
-        raise TypeError("c: a contiguous uint16/float16 array (updated in place)")
-    av, bv = np.ascontiguousarray(a).view(np.uint16).ravel(), np.ascontiguousarray(b).view(np.uint16).ravel()
+    cc = _gemm_host16(c, bf16, "c")
+    if not cc.flags.c_contiguous:
+        raise TypeError("c: a contiguous array (updated in place)")
+    av = np.ascontiguousarray(_gemm_host16(a, bf16, "a")).view(np.uint16).ravel()
+    bv = np.ascontiguousarray(_gemm_host16(b, bf16, "b")).view(np.uint16).ravel()
     _check_strided("c", cc.size, m, c_rs, n, c_cs)
     _check_strided("a", av.size, m, a_rs, k, a_cs)
     _check_strided("b", bv.size, k, b_rs, n, b_cs)
@@ -1042,7 +1059,7 @@ def matmul_f16(a, b, c, m, n, k, accum=Accum.F32):
     for t, sz, name in ((a, m * k, "a is m*k"), (b, k * n, "b is k*n"), (c, m * n, "c is m*n")):
         if (t.numel() if _is_dev(t) else np.asarray(t).size) != sz:
             raise ValueError(name)
-    return gemm_f16(m, n, k, c, n, 1, a, k, 1, b, n, 1, 0, 0x3C00, accum)
+    return gemm_f16(m, n, k, c, n, 1, a, k, 1, b, n, 1, 0.0, 1.0, accum)
 
 
 def matmul_bf16(a, b, c, m, n, k, accum=Accum.F32):
@@ -1050,7 +1067,7 @@ def matmul_bf16(a, b, c, m, n, k, accum=Accum.F32):
     for t, sz, name in ((a, m * k, "a is m*k"), (b, k * n, "b is k*n"), (c, m * n, "c is m*n")):
         if (t.numel() if _is_dev(t) else np.asarray(t).size) != sz:
             raise ValueError(name)
-    return gemm_bf16(m, n, k, c, n, 1, a, k, 1, b, n, 1, 0, 0x3F80, accum)
+    return gemm_bf16(m, n, k, c, n, 1, a, k, 1, b, n, 1, 0.0, 1.0, accum)
 
 
 # ---- the model-level parts: Linear, GatedLinear, Mlp, KvCache, SelfAttention,

@@ -230,6 +230,48 @@ def test_scalar_operands_round_through_the_element_type():
     assert e.nodes[0][2] == float(np.float32(0.10009765625))
 
 
+def test_alpha_beta_and_scalars_are_values_not_bits():
+    """alpha, beta and scalar operands are values of T (`alpha: T` in
+    src/kernels/f16.rs:126, `Gemm::beta(v: T)`, `EpOp::*Scalar(T)`): the
+    Python ints 0 and 1 mean 0.0 and 1.0, as the floats do; only an np.uint16
+    is taken as raw bits."""
+    import smegemm as smg
+    for bf16, one in ((False, 0x3C00), (True, 0x3F80)):
+        assert smg._bits16(1, bf16) == smg._bits16(1.0, bf16) == one
+        assert smg._bits16(0, bf16) == smg._bits16(0.0, bf16) == 0
+        assert smg._bits16(2, bf16) == smg._bits16(2.0, bf16)
+        assert smg._bits16(np.uint16(one), bf16) == one
+        assert smg._scalar_to_f32(1, bf16) == smg._scalar_to_f32(1.0, bf16) == 1.0
+        assert smg._scalar_to_f32(np.uint16(one), bf16) == 1.0
+        with pytest.raises(TypeError):
+            smg._bits16("1", bf16)
+        with pytest.raises(TypeError):
+            smg._bits16(True, bf16)
+    assert smg.Epilogue().add_scalar(3).nodes[0][2] == 3.0
+    assert smg.Epilogue().mul_scalar(np.uint16(0x4000)).nodes[0][2] == 2.0
+
+
+def test_strided_gemm_host_operands_must_be_16_bit(monkeypatch):
+    """The host strided GEMM takes uint16 bits (or float16 values for f16);
+    a float32 A or B is refused, not viewed as twice as many halves, and an
+    f16 C is refused for a bf16 GEMM. The checks run before any library
+    call (the device check is stubbed so no call can reach a GPU)."""
+    import smegemm as smg
+    monkeypatch.setattr(smg, "_require_device", lambda: (_ for _ in ()).throw(AssertionError("reached")))
+    m = n = k = 2
+    c16, a16, b16 = np.zeros(4, np.float16), np.zeros(4, np.float16), np.zeros(4, np.float16)
+    for bad_a, bad_b in ((np.zeros(4, np.float32), b16), (a16, np.zeros(4, np.float32)),
+                         (np.zeros(4, np.float64), b16), (a16, np.zeros(4, np.int32))):
+        with pytest.raises(TypeError):
+            smg.gemm_f16(m, n, k, c16, n, 1, bad_a, k, 1, bad_b, n, 1, 0.0, 1.0)
+    with pytest.raises(TypeError):  # f16 C for a bf16 GEMM
+        smg.gemm_bf16(m, n, k, c16, n, 1, np.zeros(4, np.uint16), k, 1, np.zeros(4, np.uint16), n, 1, 0.0, 1.0)
+    with pytest.raises(TypeError):  # f16 A for a bf16 GEMM
+        smg.gemm_bf16(m, n, k, np.zeros(4, np.uint16), n, 1, a16, k, 1, np.zeros(4, np.uint16), n, 1, 0.0, 1.0)
+    with pytest.raises(AssertionError, match="reached"):  # well-typed operands pass every check
+        smg.gemm_f16(m, n, k, c16, n, 1, a16, k, 1, np.zeros(4, np.uint16), n, 1, 0, 1)
+
+
 def test_strided_gemm_refuses_bad_views(lib):
     """gemm_gpu_*_run check strides before touching a device: C's cells must
     be distinct (a zero or overlapping stride would race), no stride is

@@ -385,6 +385,36 @@ def test_q4_split_k_prefill(smg, orc, m, n, k, affine):
     assert np.array_equal(cd.cpu().numpy().view(np.uint16), got)
 
 
+@pytest.mark.parametrize("m", [40, 100])
+def test_q4_device_a_gemm_q4r_cannot_read(smg, orc, m):
+    """An f16 device A that is not 16-byte aligned (a view one element into
+    its buffer) cannot be read by the split-K GEMM's DMA, so the call runs on
+    the 16-row GEMV launches or gemm_kernel -- and allocates no split-K
+    partials for it -- with the same result as the aligned A, within the f16
+    bar of the oracle."""
+    import torch
+    n, k = 1024, 4096
+    rng = np.random.default_rng(m)
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.005, 0.02, n * (k // 32)).astype(np.float32))
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    w = smg.Q4Weights(quants, scales, n, k)
+    want = orc.matmul_q4_ep(a, quants, scales, None, m, n, k, 32)
+    buf = torch.zeros(m * k + 1, dtype=torch.int16, device="cuda")
+    buf[1:] = torch.from_numpy(a.view(np.int16)).cuda()
+    ad = buf[1:]
+    assert ad.data_ptr() % 16 == 2
+    cd = torch.zeros(m * n, dtype=torch.int16, device="cuda")
+    smg.matmul_q4(ad, w, cd, m)
+    torch.cuda.synchronize()
+    got = cd.cpu().numpy().view(np.uint16)
+    assert max_rel(got, want) <= f16_tol(k)
+    aligned = torch.zeros(m * n, dtype=torch.int16, device="cuda")
+    smg.matmul_q4(torch.from_numpy(a.view(np.int16)).cuda(), w, aligned, m)
+    torch.cuda.synchronize()
+    assert max_rel(aligned.cpu().numpy().view(np.uint16), want) <= f16_tol(k)
+
+
 def test_q4_device_pointer_path_matches_host(smg, orc):
     """smg_q4_matmul_dev (torch tensors on the current stream) == host path."""
     import torch

@@ -343,3 +343,54 @@ def test_device_call_refuses_host_operands(smg, orc):
     rc = L.smg_q4_matmul_dev(m, w._h, cd.data_ptr(), ad.data_ptr(), None, 0, stream)
     torch.cuda.synchronize()
     assert rc == 0 and bool((cd.view(torch.float16) == 0).all())
+
+
+def test_device_call_refuses_host_operands_while_capturing(smg, orc):
+    """The device entry points' pointer check also runs while the stream is
+    being captured into a graph (the query is not a stream operation): a
+    pageable host epilogue operand or A is refused with SMG_EINVAL and nothing
+    is recorded for it, while a well-formed device call in the same capture is
+    recorded and replays correctly. The graph is replayed only when every
+    refused call returned before recording, i.e. it holds device pointers only
+    (checked by its replay matching the eager result)."""
+    import torch
+    n, k, m = 256, 128, 2
+    _, _, w = _q4(smg, orc, n, k, 8)
+    hip = _hip_runtime()
+    host_col = np.zeros(n, np.uint16)
+    host_a = np.zeros(m * k, np.uint16)
+    if not (_query_says_unreadable(hip, host_col.ctypes.data) and _query_says_unreadable(hip, host_a.ctypes.data)):
+        pytest.skip("the runtime reports pageable host memory as device-readable here")
+    L = smg.lib()
+    ad = torch.randn(m * k, dtype=torch.float16, device="cuda")
+    cd = torch.full((m * n,), 0x1234, dtype=torch.int16, device="cuda")
+    want = torch.empty(m * n, dtype=torch.int16, device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # eager reference (and any scratch sized before capture)
+        assert L.smg_q4_matmul_dev(m, w._h, want.data_ptr(), ad.data_ptr(), None, 0, side.cuda_stream) == 0
+    torch.cuda.synchronize()
+    node = smg.EpNode(4, 0, 0.0, host_col.ctypes.data, 0)
+    arr = (smg.EpNode * 1)(node)
+    desc = smg.EpDesc16(1, C.cast(arr, C.POINTER(smg.EpNode)))
+    g = torch.cuda.CUDAGraph()
+    rcs = []
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            s = side.cuda_stream
+            rcs.append(L.smg_q4_matmul_dev(m, w._h, cd.data_ptr(), ad.data_ptr(), C.addressof(desc), 0, s))
+            e1 = L.smg_last_error()
+            rcs.append(L.smg_q4_matmul_dev(m, w._h, cd.data_ptr(), host_a.ctypes.data, None, 0, s))
+            e2 = L.smg_last_error()
+            rcs.append(L.smg_q4_matmul_dev(m, w._h, cd.data_ptr(), ad.data_ptr(), None, 0, s))
+    torch.cuda.synchronize()
+    assert rcs[0] == -1 and b"epilogue operand" in e1, (rcs, e1)
+    assert rcs[1] == -1 and b"operand pointer" in e2, (rcs, e2)
+    assert rcs[2] == 0, rcs
+    assert bool((cd == 0x1234).all())  # nothing ran at capture
+    for _ in range(2):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(cd, want)
+        cd.fill_(0x1234)
+        torch.cuda.synchronize()
