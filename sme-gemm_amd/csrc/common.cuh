@@ -79,6 +79,14 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
 __device__ __forceinline__ uint4 bload16(rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
+// Streaming forms (the nt cache policy): data read once per call, such as a
+// GEMV's weights, so that it does not displace what later calls reuse.
+__device__ __forceinline__ uint4 bload16_nt(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+}
+__device__ __forceinline__ uint16_t bload2_nt(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 2);
+}
 __device__ __forceinline__ uint16_t bload2(rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
 }
@@ -256,6 +264,41 @@ __device__ __forceinline__ uint16_t act_round16(uint32_t kind, float x, float al
         return from_f32<BF16>((float)yd);
     }
     return from_f32<BF16>(act_f32(kind, x, alpha));
+}
+
+// The compiled store variant for an op-graph (the kernels' EPV template
+// argument): 1 for no graph, 2 for [add_col] and 3 for [mul_col, add_col],
+// each optionally followed by a trailing activation; 0 (the generic,
+// interpreted store) for anything else. Host code.
+struct EpPick {
+    int v;
+    const uint16_t *a, *b;
+    uint32_t act;
+    float alpha;
+};
+inline EpPick pick_ep(const EpArgs &ep) {
+    EpPick p = {0, nullptr, nullptr, EP_ACT_NONE, 0.0f};
+    uint32_t n = ep.n_nodes;
+    if (n == 0) {
+        p.v = 1;
+        return p;
+    }
+    const EpNode &last = ep.nodes[n - 1];
+    if (last.op == EP_OP_ACT) {
+        p.act = last.aux;
+        p.alpha = last.scalar;
+        n--;
+    }
+    if (n == 1 && ep.nodes[0].op == EP_OP_ADD_COL) {
+        p.v = 2;
+        p.b = (const uint16_t *)ep.nodes[0].ptr;
+    } else if (n == 2 && ep.nodes[0].op == EP_OP_MUL_COL && ep.nodes[1].op == EP_OP_ADD_COL) {
+        p.v = 3;
+        p.a = (const uint16_t *)ep.nodes[0].ptr;
+        p.b = (const uint16_t *)ep.nodes[1].ptr;
+    }
+    if (p.v == 0) p = {0, nullptr, nullptr, EP_ACT_NONE, 0.0f};
+    return p;
 }
 
 // Eight cells at once (GEMM stores): one call per 8 cells, the kind switch

@@ -59,6 +59,10 @@ struct RArgs {
     // part[s][row][col] (row stride part_ld floats); q4r_reduce finishes them
     float *part;
     uint32_t nsplit, part_ld;
+    // the compiled store's operands (EPV 2, 3: EpPick's a, b, act, alpha)
+    const uint16_t *col_a, *col_b;
+    uint32_t act;
+    float act_alpha;
 };
 
 // LDS DMA: each lane's 16 (4) bytes from sbase + voff land at M0 + 16 (4) *
@@ -310,10 +314,14 @@ __device__ __forceinline__ void mma_step(const Half &cur, const Half &nxt, float
     }
 }
 
-template <bool AFFINE, bool SPLIT>
+// EPV: the store's op-graph, compiled for the common shapes (pick_ep): 0 any
+// graph (the interpreted store), 1 none, 2 [add_col] + act, 3 [mul_col,
+// add_col] + act. SPLIT kernels store partials only (EPV 0).
+template <bool AFFINE, bool SPLIT, int EPV = 0>
 __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
+    static_assert(!SPLIT || EPV == 0, "a split kernel's store is q4r_reduce's");
     __shared__ __align__(16) uint8_t ring[NSTAGE * STAGE_BYTES];
-    __shared__ __align__(16) float epv[SMG_MAX_EP_NODES * (RBN + RBM)];
+    __shared__ __align__(16) float epv[EPV == 0 ? SMG_MAX_EP_NODES * (RBN + RBM) : 4];
 
     const uint32_t mtiles = (g.m + RBM - 1) / RBM;
     const int t = threadIdx.x, lane = t % 64;
@@ -425,7 +433,9 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
 
         float *colv = epv, *rowv = epv + SMG_MAX_EP_NODES * RBN;
         // the op-graph's vectors first: their global loads overlap the exchange
-        if constexpr (!SPLIT) ep_load_vectors<false, RBM, RBN, RNT>(g.st, ep, colv, rowv, row0, col0);
+        if constexpr (!SPLIT && EPV == 0) ep_load_vectors<false, RBM, RBN, RNT>(g.st, ep, colv, rowv, row0, col0);
+        EpCols cv;
+        if constexpr (EPV >= 2) ep_cols_load<EPV>(g.col_a, g.col_b, col0 + (t % (RBN / 8)) * 8, g.n, cv);
 
         // The pair's partial tiles: each wave hands the other the half of its
         // f32 tile that the other finishes (wave w keeps row tiles 0-3, wave
@@ -506,8 +516,12 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
         // Store: groups of 8 columns through the op-graph by all eight waves.
         // thread t: column group t % 32, rows t / 32 + 16 j
         static_assert(RNT % (RBN / 8) == 0, "each thread keeps one column group");
-        ep_store_rows<false, RBM, RBN, RBM * (RBN / 8) / RNT>(g.st, ep, colv, rowv, stg, CS, t / (RBN / 8),
-                                                              RNT / (RBN / 8), (t % (RBN / 8)) * 8, row0, col0);
+        if constexpr (EPV == 0)
+            ep_store_rows<false, RBM, RBN, RBM * (RBN / 8) / RNT>(g.st, ep, colv, rowv, stg, CS, t / (RBN / 8),
+                                                                  RNT / (RBN / 8), (t % (RBN / 8)) * 8, row0, col0);
+        else
+            ep_store_rows_c<false, RBM * (RBN / 8) / RNT, EPV>(g.st, g.act, g.act_alpha, cv, stg, CS, t / (RBN / 8),
+                                                               RNT / (RBN / 8), (t % (RBN / 8)) * 8, row0, col0);
     };
     run_tile(tile);  // consecutive workgroups share a weight tile
 }
@@ -630,10 +644,24 @@ hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long 
     const size_t slice_bytes = m * ((w.n + 7) / 8 * 8) * sizeof(float);
     const uint32_t ns = part ? (uint32_t)std::min<size_t>(q4r_nsplit(w, m), part_bytes / slice_bytes) : 1;
     if (ns <= 1) {
-        if (w.mins)
-            hipLaunchKernelGGL((gemm_q4r<true, false>), dim3(tiles), dim3(RNT), 0, s, g, ep);
-        else
-            hipLaunchKernelGGL((gemm_q4r<false, false>), dim3(tiles), dim3(RNT), 0, s, g, ep);
+        const EpPick pk = pick_ep(ep);
+        g.col_a = pk.a;
+        g.col_b = pk.b;
+        g.act = pk.act;
+        g.act_alpha = pk.alpha;
+#define SMG_Q4R_LAUNCH(AF)                                                                              \
+    switch (pk.v) {                                                                                     \
+    case 1: hipLaunchKernelGGL((gemm_q4r<AF, false, 1>), dim3(tiles), dim3(RNT), 0, s, g, ep); break; \
+    case 2: hipLaunchKernelGGL((gemm_q4r<AF, false, 2>), dim3(tiles), dim3(RNT), 0, s, g, ep); break; \
+    case 3: hipLaunchKernelGGL((gemm_q4r<AF, false, 3>), dim3(tiles), dim3(RNT), 0, s, g, ep); break; \
+    default: hipLaunchKernelGGL((gemm_q4r<AF, false, 0>), dim3(tiles), dim3(RNT), 0, s, g, ep); break; \
+    }
+        if (w.mins) {
+            SMG_Q4R_LAUNCH(true)
+        } else {
+            SMG_Q4R_LAUNCH(false)
+        }
+#undef SMG_Q4R_LAUNCH
         return hipGetLastError();
     }
     g.part = part;

@@ -702,40 +702,6 @@ __global__ void __launch_bounds__(T)
     }
 }
 
-// The compiled store variant for an op-graph (lowbit_tile's EPV): 1 for no
-// graph, 2 for [add_col] and 3 for [mul_col, add_col], each optionally
-// followed by a trailing activation; 0 (the generic store) for anything else.
-struct EpPick {
-    int v;
-    const uint16_t *a, *b;
-    uint32_t act;
-    float alpha;
-};
-EpPick pick_ep(const EpArgs &ep) {
-    EpPick p = {0, nullptr, nullptr, EP_ACT_NONE, 0.0f};
-    uint32_t n = ep.n_nodes;
-    if (n == 0) {
-        p.v = 1;
-        return p;
-    }
-    const EpNode &last = ep.nodes[n - 1];
-    if (last.op == EP_OP_ACT) {
-        p.act = last.aux;
-        p.alpha = last.scalar;
-        n--;
-    }
-    if (n == 1 && ep.nodes[0].op == EP_OP_ADD_COL) {
-        p.v = 2;
-        p.b = (const uint16_t *)ep.nodes[0].ptr;
-    } else if (n == 2 && ep.nodes[0].op == EP_OP_MUL_COL && ep.nodes[1].op == EP_OP_ADD_COL) {
-        p.v = 3;
-        p.a = (const uint16_t *)ep.nodes[0].ptr;
-        p.b = (const uint16_t *)ep.nodes[1].ptr;
-    }
-    if (p.v == 0) p = {0, nullptr, nullptr, EP_ACT_NONE, 0.0f};
-    return p;
-}
-
 template <int KIND, int MR, int NG, int SPB, int EPV>
 hipError_t launch_tile_v(const LtArgs &g, const EpArgs &ep, const EpPick &pk, hipStream_t s) {
     const size_t lds = tile_lds_bytes(g.kq, g.nbq, MR, 1u << g.cg_shift);

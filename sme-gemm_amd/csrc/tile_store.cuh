@@ -112,6 +112,35 @@ __device__ __forceinline__ void ep_store8(const StoreArgs &g, const EpArgs &ep, 
     for (uint32_t e = 0; e < ne; e++) dp[(size_t)e * g.dst_cs] = (uint16_t)(w4[e / 2] >> (16 * (e % 2)));
 }
 
+// An activation over R x 8 cells: the logistic kinds inline (no call), one
+// loop per kind (as act_f32_fast: silu x*L(x), sigmoid L(x), tanh-gelu
+// x*L(2u)); the rest one act8_fast call per row.
+template <int R>
+__device__ __forceinline__ void act_rows(uint32_t aux, float alpha, F8 (&x)[R]) {
+    if (aux == 3) {
+#pragma unroll
+        for (int j = 0; j < R; j++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[j].v[e] = mul_logistic(x[j].v[e], x[j].v[e]);
+    } else if (aux == 5) {
+#pragma unroll
+        for (int j = 0; j < R; j++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[j].v[e] = mul_logistic(1.0f, x[j].v[e]);
+    } else if (aux == 2) {
+#pragma unroll
+        for (int j = 0; j < R; j++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float v = x[j].v[e];
+                x[j].v[e] = mul_logistic(v, 2.0f * 0.7978845608028654f * (v + 0.044715f * v * v * v));
+            }
+    } else if (aux != EP_ACT_NONE) {
+#pragma unroll
+        for (int j = 0; j < R; j++) x[j] = act8_fast(aux, x[j], alpha);
+    }
+}
+
 // R rows (rl0 + rstep * j) x the same 8 columns (cl .. cl+7) of the tile:
 // what one thread stores when the tile's column groups divide the thread count.
 // The staged 16-bit values are read from tile (row stride cs halfs); a COL
@@ -139,31 +168,7 @@ __device__ __forceinline__ void ep_store_rows(const StoreArgs &g, const EpArgs &
             const EpNode &nd = ep.nodes[q];
             const uint32_t cls = ep.cls[q], fam = ep.fam[q];
             if (fam == EPF_ACT) {
-                // the logistic kinds inline over all R x 8 cells (no call),
-                // one loop per kind (as act_f32_fast: silu x*L(x), sigmoid
-                // L(x), tanh-gelu x*L(2u)); the rest one call per row
-                if (nd.aux == 3) {
-#pragma unroll
-                    for (int j = 0; j < R; j++)
-#pragma unroll
-                        for (int e = 0; e < 8; e++) x[j].v[e] = mul_logistic(x[j].v[e], x[j].v[e]);
-                } else if (nd.aux == 5) {
-#pragma unroll
-                    for (int j = 0; j < R; j++)
-#pragma unroll
-                        for (int e = 0; e < 8; e++) x[j].v[e] = mul_logistic(1.0f, x[j].v[e]);
-                } else if (nd.aux == 2) {
-#pragma unroll
-                    for (int j = 0; j < R; j++)
-#pragma unroll
-                        for (int e = 0; e < 8; e++) {
-                            const float v = x[j].v[e];
-                            x[j].v[e] = mul_logistic(v, 2.0f * 0.7978845608028654f * (v + 0.044715f * v * v * v));
-                        }
-                } else {
-#pragma unroll
-                    for (int j = 0; j < R; j++) x[j] = act8_fast(nd.aux, x[j], nd.scalar);
-                }
+                act_rows<R>(nd.aux, nd.scalar, x);
                 continue;
             }
             if (cls == EPC_TENSOR) {
@@ -209,6 +214,85 @@ __device__ __forceinline__ void ep_store_rows(const StoreArgs &g, const EpArgs &
             default: break;
             }
         }
+#pragma unroll
+        for (int j = 0; j < R; j++) {
+            uint32_t w4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                w4[e] = (uint32_t)from_f32<BF16>(x[j].v[2 * e]) | ((uint32_t)from_f32<BF16>(x[j].v[2 * e + 1]) << 16);
+            c8[j] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        const uint32_t row = row0 + rl0 + rstep * j;
+        if (row >= g.m) continue;
+        uint16_t *dp = g.dst + (size_t)row * g.dst_rs + (size_t)col * g.dst_cs;
+        if (g.dst_cs == 1 && ne == 8 && ((uintptr_t)dp & 15) == 0) {
+            *(uint4 *)dp = c8[j];
+            continue;
+        }
+        const uint32_t w4[4] = {c8[j].x, c8[j].y, c8[j].z, c8[j].w};
+        for (uint32_t e = 0; e < ne; e++) dp[(size_t)e * g.dst_cs] = (uint16_t)(w4[e / 2] >> (16 * (e % 2)));
+    }
+}
+
+// The 8 column operand values (col .. col+7) of a compiled store, as 16-bit
+// patterns, read before the tile is staged so that their latency overlaps the
+// accumulator exchange; columns past n read zero (never stored).
+struct EpCols {
+    uint16_t a[8], b[8];
+};
+template <int EPV>
+__device__ __forceinline__ void ep_cols_load(const uint16_t *col_a, const uint16_t *col_b, uint32_t col,
+                                             uint32_t n, EpCols &cv) {
+    if constexpr (EPV >= 2) {
+        const rsrc_t rb = make_rsrc(col_b, n * 2u);
+#pragma unroll
+        for (int e = 0; e < 8; e++) cv.b[e] = bload2(rb, col + e < n ? (col + e) * 2u : OOB);
+    }
+    if constexpr (EPV == 3) {
+        const rsrc_t ra = make_rsrc(col_a, n * 2u);
+#pragma unroll
+        for (int e = 0; e < 8; e++) cv.a[e] = bload2(ra, col + e < n ? (col + e) * 2u : OOB);
+    }
+}
+
+// ep_store_rows compiled for the common graphs (EpPick's v = EPV: 1 none, 2
+// [add_col] + act, 3 [mul_col, add_col] + act; add_dst must be 0): the same
+// f32 steps in the same order on the rounded value -- x * a, then + b, then
+// the activation as act_rows -- without the per-node interpretation, whose
+// code (every family and class, unrolled over R x 8 cells) is what a tile's
+// store otherwise spends its time fetching and branching through.
+template <bool BF16, int R, int EPV>
+__device__ __forceinline__ void ep_store_rows_c(const StoreArgs &g, uint32_t act, float alpha, const EpCols &cv,
+                                                const uint16_t *tile, int cs, int rl0, int rstep, int cl,
+                                                uint32_t row0, uint32_t col0) {
+    const uint32_t col = col0 + cl;
+    if (col >= g.n) return;
+    const uint32_t ne = g.n - col < 8 ? g.n - col : 8;
+    uint4 c8[R];
+#pragma unroll
+    for (int j = 0; j < R; j++) c8[j] = *(const uint4 *)(tile + (rl0 + rstep * j) * cs + cl);
+    if constexpr (EPV >= 2) {
+        float va[8], vb[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            va[e] = to_f32<BF16>(cv.a[e]);
+            vb[e] = to_f32<BF16>(cv.b[e]);
+        }
+        F8 x[R];
+#pragma unroll
+        for (int j = 0; j < R; j++) {
+            const uint32_t w4[4] = {c8[j].x, c8[j].y, c8[j].z, c8[j].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                float v = to_f32<BF16>((uint16_t)(w4[e / 2] >> (16 * (e % 2))));
+                if constexpr (EPV == 3) v = v * va[e];
+                x[j].v[e] = v + vb[e];
+            }
+        }
+        act_rows<R>(act, alpha, x);
 #pragma unroll
         for (int j = 0; j < R; j++) {
             uint32_t w4[4];

@@ -206,3 +206,51 @@ def test_q4_register_weight_gemm_epilogue_repeat(smg, orc):
         c = np.zeros(m * n, np.uint16)
         smg.matmul_q4_ep(a, w, c, m, smg.Epilogue().mul_col(sc).add_col(bias).silu())
         assert max_rel(c, want) <= f16_tol(k)
+
+
+@pytest.mark.parametrize("graph", ["none", "add_col", "add_col_relu", "mul_add_silu", "mul_add_gelu",
+                                   "mul_add_sigmoid", "add_col_tanh"])
+@pytest.mark.parametrize("m,n,k,affine", [(200, 1000, 512, False), (512, 2056, 1024, True), (130, 300, 256, False)])
+def test_q4_gemm_compiled_store_equals_interpreted(smg, orc, graph, m, n, k, affine):
+    """The prefill GEMM compiles its store for the common op-graphs (none,
+    [add_col] + act, [mul_col, add_col] + act). The same graph with an extra
+    mul_scalar(1.0) node (x * 1 is exact in f32) takes the interpreted store:
+    the two give the same bits, and both are within tolerance of the oracle."""
+    rng = np.random.default_rng(m + n + k)
+    nbk = k // 32
+    quants = rng.integers(0, 256, k * n // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.002, 0.02, n * nbk).astype(np.float32))
+    mins = orc.f32_to_f16(rng.uniform(-0.05, 0.05, n * nbk).astype(np.float32)) if affine else None
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    sc = orc.f32_to_f16(rng.uniform(0.5, 1.5, n).astype(np.float32))
+    bias = orc.f32_to_f16((0.1 * rng.standard_normal(n)).astype(np.float32))
+    p = smg.Q4Params(32).affine() if affine else smg.Q4Params(32)
+    w = smg.Q4Weights.with_params(quants, scales, mins, n, k, p)
+
+    def build(extra):
+        e = smg.Epilogue()
+        nodes, act = [], None
+        if graph.startswith("mul_add"):
+            e = e.mul_col(sc).add_col(bias)
+            nodes = [(5, 0, 0.0, sc, 0), (4, 0, 0.0, bias, 0)]
+        elif graph.startswith("add_col"):
+            e = e.add_col(bias)
+            nodes = [(4, 0, 0.0, bias, 0)]
+        if extra:
+            e = e.mul_scalar(1.0)
+            nodes = nodes + [(1, 0, 1.0, None, 0)]
+        for name, kind in (("relu", 1), ("gelu", 2), ("silu", 3), ("tanh", 4), ("sigmoid", 5)):
+            if graph.endswith(name):
+                e = getattr(e, name)()
+                act = kind
+        return e, nodes, act
+
+    e0, nodes0, act0 = build(False)
+    e1, _, _ = build(True)
+    c0 = np.zeros(m * n, np.uint16)
+    smg.matmul_q4_ep(a, w, c0, m, e0)
+    c1 = np.zeros(m * n, np.uint16)
+    smg.matmul_q4_ep(a, w, c1, m, e1)
+    assert np.array_equal(c0, c1), graph
+    want = orc.matmul_q4_ep(a, quants, scales, mins, m, n, k, 32, nodes0, act0)
+    assert max_rel(c0, want) <= f16_tol(k)
