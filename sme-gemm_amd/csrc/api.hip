@@ -571,7 +571,7 @@ EpArgs ep_from_row(const EpArgs &ea, size_t r0, size_t n) {
 // compute units idle at N = 4096 to 14336); the MFMA GEMM above, K split over
 // the compute units when its tiles are few and `split` (q4_split_bytes) is
 // given.
-// Without gemm_q4r (bf16 activations, or an A it cannot read) the calls above
+// Without gemm_q4r (an A it cannot read: not 16-byte aligned) the calls above
 // Q4_GEMV_CHUNK_ROWS go to gemm_kernel, whose 128 x 128 tiles are as few: at
 // K = 4096 it took 115 us for any of 33-128 rows at N = 4096 or 14336, where
 // 16-row GEMV launches take about 7.7 us (N = 4096) or 17.6 us (N = 14336)
@@ -590,7 +590,7 @@ bool q4_gemv_rows(const WDev &w, size_t m, bool gemm_q4r) {
 // needs none). lhs == nullptr stands for the host entry points' staging copy of
 // A, which is 256-byte aligned.
 size_t q4_split_bytes(const WDev &w, size_t m, const uint16_t *lhs, bool bf16) {
-    if (bf16 || !q4r_supported(w, m, 1, (long)w.k, lhs, bf16) || q4_gemv_rows(w, m, true)) return 0;
+    if (!q4r_supported(w, m, 1, (long)w.k, lhs, bf16) || q4_gemv_rows(w, m, true)) return 0;
     return q4r_split_bytes(w, m);
 }
 hipError_t run_q4(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs, const EpArgs &ea,
@@ -606,7 +606,7 @@ hipError_t run_q4(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs, c
         }
         return hipSuccess;
     }
-    if (q4r) return launch_q4r(w, m, dst, 1, (long)w.n, lhs, (long)w.k, 1.0f, ea, (float *)split, split_bytes, s);
+    if (q4r) return launch_q4r(w, m, dst, 1, (long)w.n, lhs, (long)w.k, 1.0f, ea, (float *)split, split_bytes, bf16, s);
     return launch_gemm(w, m, dst, 1, (long)w.n, lhs, 1, (long)w.k, 1.0f, ea, bf16, s);
 }
 

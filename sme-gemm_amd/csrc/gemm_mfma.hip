@@ -484,7 +484,7 @@ hipError_t launch_gemm(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long
                        const EpArgs &ep, bool bf16, hipStream_t s, bool read_dst, float alpha) {
     if (read_dst && w.kind != W_F16 && w.kind != W_BF16) return hipErrorInvalidValue;
     if (!read_dst && q4r_supported(w, m, lhs_cs, lhs_rs, lhs, bf16))
-        return launch_q4r(w, m, dst, dst_cs, dst_rs, lhs, lhs_rs, beta, ep, nullptr, 0, s);
+        return launch_q4r(w, m, dst, dst_cs, dst_rs, lhs, lhs_rs, beta, ep, nullptr, 0, bf16, s);
     GemmArgs g = {};
     g.lhs = lhs;
     g.dst = dst;

@@ -1,9 +1,12 @@
-// Q4 x f16 prefill GEMM with the weights dequantized in registers:
-// C = ep(to16(beta * A @ dequant(B))) for matmul_q4 / matmul_q4_ep with m > 8
-// (src/kernels/q4/matmul.rs:37-103), replacing run_q4_panels + unpack_q4_f16
-// (csrc/gemm_f16f16_q4.h:57-118). Serves f16 activations, Q4_0 and Q4_1,
-// blocks of 32 depths or more, K a multiple of 64 and row-major A; every other
-// case goes to gemm_kernel (gemm_mfma.hip).
+// Q4 prefill GEMM with the weights dequantized in registers:
+// C = ep(to16(beta * A @ dequant(B))) for matmul_q4 / matmul_q4_ep and their
+// bf16 forms past the GEMV's rows (src/kernels/q4/matmul.rs:37-103,:187-271),
+// replacing run_q4_panels + unpack_q4_f16 (csrc/gemm_f16f16_q4.h:57-118) and
+// q4_bf16_core (csrc/gemm_b16b16_q4.h:293). Serves f16 or bf16 activations,
+// Q4_0 and Q4_1, blocks of 32 depths or more, K a multiple of 64 and
+// row-major 16-byte-aligned A; every other case goes to gemm_kernel
+// (gemm_mfma.hip). bf16 calls multiply on v_mfma_f32_16x16x32_bf16 with each
+// weight formed in f32 and rounded to bf16 once, as the portable bf16 path.
 //
 // Tile: 128 rows x 256 columns, eight waves, two per SIMD. Waves w and w+4 (on
 // one SIMD) own columns 64(w%4)..+63 for all 128 rows and split K: wave w
@@ -276,6 +279,59 @@ __device__ __forceinline__ void mma8_deq(float4_t &c0, float4_t &c1, float4_t &c
     }
 }
 
+// The bf16 form of mma8_deq (matmul_q4_bf16 prefill): v_mfma_f32_16x16x32_bf16
+// with the weights formed as q4_deq8_bf16 forms them -- the biased nibble
+// under an f16 exponent less its offset is the exact code as f16, then
+// v_fma_mix_f32 gives f32(code) * f32(scale) + f32(min) (min -0 for Q4_0: the
+// product unchanged) with the f32 rounding of the reference's f32 dequant, and
+// v_cvt_pk_bf16_f32 rounds each pair to bf16 once (src/kernels/q4/mod.rs
+// dequant to bf16). s1 holds the f16 scale in its low half, mf the min as f32.
+__device__ __forceinline__ void mma8_deq_bf16(float4_t &c0, float4_t &c1, float4_t &c2, float4_t &c3, float4_t &c4,
+                                              float4_t &c5, float4_t &c6, float4_t &c7, const u32x4_t (&a)[8],
+                                              const u32x4_t &b, u32x4_t &nb, uint32_t q, uint32_t s1, float mf,
+                                              uint32_t mag_lo, uint32_t mag_hi) {
+    uint32_t t;
+    float f0, f1;
+    asm volatile(
+        "v_mfma_f32_16x16x32_bf16 %[c0], %[a0], %[b], %[c0]\n\t"
+        "v_lshrrev_b32 %[t], 8, %[q]\n\t"
+        "v_bfi_b32 %[n0], %[m1], %[q], %[ml]\n\t"
+        "v_mfma_f32_16x16x32_bf16 %[c1], %[a1], %[b], %[c1]\n\t"
+        "v_bfi_b32 %[n1], %[m2m], %[q], %[mh]\n\t"
+        "v_bfi_b32 %[n2], %[m1], %[t], %[ml]\n\t"
+        "v_mfma_f32_16x16x32_bf16 %[c2], %[a2], %[b], %[c2]\n\t"
+        "v_bfi_b32 %[n3], %[m2m], %[t], %[mh]\n\t"
+        "v_pk_add_f16 %[n0], %[n0], %[ol]\n\t"
+        "v_pk_add_f16 %[n1], %[n1], %[oh]\n\t"
+        "v_mfma_f32_16x16x32_bf16 %[c3], %[a3], %[b], %[c3]\n\t"
+        "v_pk_add_f16 %[n2], %[n2], %[ol]\n\t"
+        "v_pk_add_f16 %[n3], %[n3], %[oh]\n\t"
+        "v_fma_mix_f32 %[f0], %[n0], %[s1], %[mf] op_sel_hi:[1,1,0]\n\t"
+        "v_mfma_f32_16x16x32_bf16 %[c4], %[a4], %[b], %[c4]\n\t"
+        "v_fma_mix_f32 %[f1], %[n0], %[s1], %[mf] op_sel:[1,0,0] op_sel_hi:[1,1,0]\n\t"
+        "v_cvt_pk_bf16_f32 %[n0], %[f0], %[f1]\n\t"
+        "v_fma_mix_f32 %[f0], %[n1], %[s1], %[mf] op_sel_hi:[1,1,0]\n\t"
+        "v_mfma_f32_16x16x32_bf16 %[c5], %[a5], %[b], %[c5]\n\t"
+        "v_fma_mix_f32 %[f1], %[n1], %[s1], %[mf] op_sel:[1,0,0] op_sel_hi:[1,1,0]\n\t"
+        "v_cvt_pk_bf16_f32 %[n1], %[f0], %[f1]\n\t"
+        "v_fma_mix_f32 %[f0], %[n2], %[s1], %[mf] op_sel_hi:[1,1,0]\n\t"
+        "v_mfma_f32_16x16x32_bf16 %[c6], %[a6], %[b], %[c6]\n\t"
+        "v_fma_mix_f32 %[f1], %[n2], %[s1], %[mf] op_sel:[1,0,0] op_sel_hi:[1,1,0]\n\t"
+        "v_cvt_pk_bf16_f32 %[n2], %[f0], %[f1]\n\t"
+        "v_fma_mix_f32 %[f0], %[n3], %[s1], %[mf] op_sel_hi:[1,1,0]\n\t"
+        "v_mfma_f32_16x16x32_bf16 %[c7], %[a7], %[b], %[c7]\n\t"
+        "v_fma_mix_f32 %[f1], %[n3], %[s1], %[mf] op_sel:[1,0,0] op_sel_hi:[1,1,0]\n\t"
+        "v_cvt_pk_bf16_f32 %[n3], %[f0], %[f1]\n\t"
+        "s_nop 1"
+        : [c0] "+v"(c0), [c1] "+v"(c1), [c2] "+v"(c2), [c3] "+v"(c3), [c4] "+v"(c4), [c5] "+v"(c5),
+          [c6] "+v"(c6), [c7] "+v"(c7), [n0] "=&v"(nb.x), [n1] "=&v"(nb.y), [n2] "=&v"(nb.z),
+          [n3] "=&v"(nb.w), [t] "=&v"(t), [f0] "=&v"(f0), [f1] "=&v"(f1)
+        : [a0] "v"(a[0]), [a1] "v"(a[1]), [a2] "v"(a[2]), [a3] "v"(a[3]), [a4] "v"(a[4]), [a5] "v"(a[5]),
+          [a6] "v"(a[6]), [a7] "v"(a[7]), [b] "v"(b), [q] "v"(q), [s1] "v"(s1), [mf] "v"(mf),
+          [ml] "v"(mag_lo), [mh] "v"(mag_hi), [m1] "s"(0x000F000Fu), [m2m] "s"(0x00F000F0u),
+          [ol] "s"(0xE408E408u), [oh] "s"(0xD480D480u));
+}
+
 template <int N>
 struct IntC {
     static constexpr int value = N;
@@ -284,12 +340,14 @@ struct IntC {
 __device__ __forceinline__ uint32_t pair16(uint32_t h) { return (h & 0xFFFFu) | (h << 16); }
 
 // The first column tile's B operand of a step (plain code, before the groups).
-template <bool AFFINE>
+template <bool AFFINE, bool BF16>
 __device__ __forceinline__ u32x4_t deq_first(const Half &h, uint32_t mag_lo, uint32_t mag_hi) {
     const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)h.s[0]);
     const half2_t s2 = {s, s};
     uint4 b;
-    if (AFFINE) {
+    if (BF16) {
+        b = q4_deq8_bf16(h.q[0], h.s[0], AFFINE ? f16_to_f32((uint16_t)h.mn[0]) : -0.0f, mag_lo, mag_hi);
+    } else if (AFFINE) {
         const _Float16 mv = __builtin_bit_cast(_Float16, (uint16_t)h.mn[0]);
         b = q4_deq8_affine(h.q[0], s2, (half2_t){mv, mv}, mag_lo, mag_hi);
     } else {
@@ -301,23 +359,28 @@ __device__ __forceinline__ u32x4_t deq_first(const Half &h, uint32_t mag_lo, uin
 // A step's 32 MFMAs: column tile jt multiplies B operand bb[jt] (dequantized
 // during the previous group) and dequantizes bb[jt+1] -- for the last tile,
 // the next step's first (raw operands in nxt).
-template <bool AFFINE>
+template <bool AFFINE, bool BF16>
 __device__ __forceinline__ void mma_step(const Half &cur, const Half &nxt, float4_t (&acc)[8][4],
                                          u32x4_t (&bb)[4], uint32_t mag_lo, uint32_t mag_hi) {
 #pragma unroll
     for (int jt = 0; jt < 4; jt++) {
         const Half &src = jt < 3 ? cur : nxt;
         const int nj = (jt + 1) % 4;
-        mma8_deq<AFFINE>(acc[0][jt], acc[1][jt], acc[2][jt], acc[3][jt], acc[4][jt], acc[5][jt], acc[6][jt],
-                         acc[7][jt], cur.a, bb[jt], bb[nj], src.q[nj], pair16(src.s[nj]),
-                         AFFINE ? pair16(src.mn[nj]) : 0u, mag_lo, mag_hi);
+        if constexpr (BF16)
+            mma8_deq_bf16(acc[0][jt], acc[1][jt], acc[2][jt], acc[3][jt], acc[4][jt], acc[5][jt], acc[6][jt],
+                          acc[7][jt], cur.a, bb[jt], bb[nj], src.q[nj], src.s[nj],
+                          AFFINE ? f16_to_f32((uint16_t)src.mn[nj]) : -0.0f, mag_lo, mag_hi);
+        else
+            mma8_deq<AFFINE>(acc[0][jt], acc[1][jt], acc[2][jt], acc[3][jt], acc[4][jt], acc[5][jt], acc[6][jt],
+                             acc[7][jt], cur.a, bb[jt], bb[nj], src.q[nj], pair16(src.s[nj]),
+                             AFFINE ? pair16(src.mn[nj]) : 0u, mag_lo, mag_hi);
     }
 }
 
 // EPV: the store's op-graph, compiled for the common shapes (pick_ep): 0 any
 // graph (the interpreted store), 1 none, 2 [add_col] + act, 3 [mul_col,
 // add_col] + act. SPLIT kernels store partials only (EPV 0).
-template <bool AFFINE, bool SPLIT, int EPV = 0>
+template <bool AFFINE, bool SPLIT, int EPV = 0, bool BF16 = false>
 __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
     static_assert(!SPLIT || EPV == 0, "a split kernel's store is q4r_reduce's");
     __shared__ __align__(16) uint8_t ring[NSTAGE * STAGE_BYTES];
@@ -406,7 +469,7 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
             uint32_t sb = ring0 + ((ks + 1) % NSTAGE) * STAGE_BYTES;
             asm volatile("" : "+s"(sb));  // opaque: one base add per operand kind, constant offsets after
             read_half<AFFINE>(sb, ro, nxt);
-            mma_step<AFFINE>(cur, nxt, acc, bb, mag_lo, mag_hi);
+            mma_step<AFFINE, BF16>(cur, nxt, acc, bb, mag_lo, mag_hi);
             if constexpr (SPLIT) {
                 // issued: steps up to min(ks + 4, last); step ks+2 must land
                 const int after = (int)last - (int)ks - 2;
@@ -421,7 +484,7 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
         };
         Half h0, h1;
         read_half<AFFINE>(ring0, ro, h0);
-        bb[0] = deq_first<AFFINE>(h0, mag_lo, mag_hi);
+        bb[0] = deq_first<AFFINE, BF16>(h0, mag_lo, mag_hi);
         uint32_t ks = 0;
         for (; ks + 2 <= ksteps; ks += 2) {
             step(ks, h0, h1);
@@ -433,7 +496,7 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
 
         float *colv = epv, *rowv = epv + SMG_MAX_EP_NODES * RBN;
         // the op-graph's vectors first: their global loads overlap the exchange
-        if constexpr (!SPLIT && EPV == 0) ep_load_vectors<false, RBM, RBN, RNT>(g.st, ep, colv, rowv, row0, col0);
+        if constexpr (!SPLIT && EPV == 0) ep_load_vectors<BF16, RBM, RBN, RNT>(g.st, ep, colv, rowv, row0, col0);
         EpCols cv;
         if constexpr (EPV >= 2) ep_cols_load<EPV>(g.col_a, g.col_b, col0 + (t % (RBN / 8)) * 8, g.n, cv);
 
@@ -491,7 +554,7 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
 #pragma unroll
                     for (int v = 0; v < 4; v++)
                         stg[(i * 16 + lg * 4 + v) * CS + cw * 64 + jt * 16 + lr] =
-                            from_f32<false>(0.0f + g.beta * acc[i][jt][v]);
+                            from_f32<BF16>(0.0f + g.beta * acc[i][jt][v]);
         };
         static_assert(8 * 1024 * sizeof(float4_t) <= NSTAGE * STAGE_BYTES, "exchange exceeds the ring");
         if (kh == 0)
@@ -517,11 +580,11 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
         // thread t: column group t % 32, rows t / 32 + 16 j
         static_assert(RNT % (RBN / 8) == 0, "each thread keeps one column group");
         if constexpr (EPV == 0)
-            ep_store_rows<false, RBM, RBN, RBM * (RBN / 8) / RNT>(g.st, ep, colv, rowv, stg, CS, t / (RBN / 8),
-                                                                  RNT / (RBN / 8), (t % (RBN / 8)) * 8, row0, col0);
+            ep_store_rows<BF16, RBM, RBN, RBM * (RBN / 8) / RNT>(g.st, ep, colv, rowv, stg, CS, t / (RBN / 8),
+                                                                 RNT / (RBN / 8), (t % (RBN / 8)) * 8, row0, col0);
         else
-            ep_store_rows_c<false, RBM * (RBN / 8) / RNT, EPV>(g.st, g.act, g.act_alpha, cv, stg, CS, t / (RBN / 8),
-                                                               RNT / (RBN / 8), (t % (RBN / 8)) * 8, row0, col0);
+            ep_store_rows_c<BF16, RBM * (RBN / 8) / RNT, EPV>(g.st, g.act, g.act_alpha, cv, stg, CS, t / (RBN / 8),
+                                                              RNT / (RBN / 8), (t % (RBN / 8)) * 8, row0, col0);
     };
     run_tile(tile);  // consecutive workgroups share a weight tile
 }
@@ -534,13 +597,14 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
 // tile is short so that even a few rows make a grid of many workgroups: the
 // pass is bound by how many loads are in flight.
 constexpr int QR_BN = 256, QR_NT = 256, QR_BM = QR_NT / (QR_BN / 8);
+template <bool BF16>
 __global__ void __launch_bounds__(QR_NT) q4r_reduce(RArgs g, EpArgs ep) {
     __shared__ __align__(16) float epv[SMG_MAX_EP_NODES * (QR_BN + QR_BM)];
     const uint32_t mtiles = (g.m + QR_BM - 1) / QR_BM;
     const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
     const uint32_t row0 = (tile % mtiles) * QR_BM, col0 = (tile / mtiles) * QR_BN;
     float *colv = epv, *rowv = epv + SMG_MAX_EP_NODES * QR_BN;
-    ep_load_vectors<false, QR_BM, QR_BN, QR_NT>(g.st, ep, colv, rowv, row0, col0);
+    ep_load_vectors<BF16, QR_BM, QR_BN, QR_NT>(g.st, ep, colv, rowv, row0, col0);
     __syncthreads();
     const int t = threadIdx.x;
     const uint32_t cl = (t % (QR_BN / 8)) * 8, rl = t / (QR_BN / 8);
@@ -569,19 +633,20 @@ __global__ void __launch_bounds__(QR_NT) q4r_reduce(RArgs g, EpArgs ep) {
     uint32_t w4[4];
 #pragma unroll
     for (int e = 0; e < 2; e++) {
-        w4[e] = (uint32_t)from_f32<false>(0.0f + g.beta * s0[2 * e]) |
-                ((uint32_t)from_f32<false>(0.0f + g.beta * s0[2 * e + 1]) << 16);
-        w4[2 + e] = (uint32_t)from_f32<false>(0.0f + g.beta * s1[2 * e]) |
-                    ((uint32_t)from_f32<false>(0.0f + g.beta * s1[2 * e + 1]) << 16);
+        w4[e] = (uint32_t)from_f32<BF16>(0.0f + g.beta * s0[2 * e]) |
+                ((uint32_t)from_f32<BF16>(0.0f + g.beta * s0[2 * e + 1]) << 16);
+        w4[2 + e] = (uint32_t)from_f32<BF16>(0.0f + g.beta * s1[2 * e]) |
+                    ((uint32_t)from_f32<BF16>(0.0f + g.beta * s1[2 * e + 1]) << 16);
     }
-    ep_store8<false, QR_BM, QR_BN>(g.st, ep, colv, rowv, make_uint4(w4[0], w4[1], w4[2], w4[3]), rl, cl, row0,
+    ep_store8<BF16, QR_BM, QR_BN>(g.st, ep, colv, rowv, make_uint4(w4[0], w4[1], w4[2], w4[3]), rl, cl, row0,
                                    col0);
 }
 
 }  // namespace
 
 bool q4r_supported(const WDev &w, size_t m, long lhs_cs, long lhs_rs, const uint16_t *lhs, bool bf16) {
-    return w.kind == W_Q4 && !bf16 && m > 0 && w.k >= 64 && w.k % 64 == 0 && w.block >= 32 &&
+    (void)bf16;  // f16 and bf16 activations alike
+    return w.kind == W_Q4 && m > 0 && w.k >= 64 && w.k % 64 == 0 && w.block >= 32 &&
            lhs_cs == 1 && lhs_rs % 8 == 0 && lhs_rs >= (long)w.k && ((uintptr_t)lhs & 15) == 0 &&
            m * (size_t)lhs_rs * 2 < ((size_t)1 << 31) &&  // 32-bit DMA offsets
            cell_grid_rows(w.nchunks) * w.n_pad * 16 < ((size_t)1 << 32);
@@ -624,7 +689,7 @@ size_t q4r_split_bytes(const WDev &w, size_t m) {
 
 hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,
                       const uint16_t *lhs, long lhs_rs, float beta, const EpArgs &ep, float *part,
-                      size_t part_bytes, hipStream_t s) {
+                      size_t part_bytes, bool bf16, hipStream_t s) {
     RArgs g = {};
     g.lhs = lhs;
     g.codes = w.codes;
@@ -649,17 +714,21 @@ hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long 
         g.col_b = pk.b;
         g.act = pk.act;
         g.act_alpha = pk.alpha;
-#define SMG_Q4R_LAUNCH(AF)                                                                              \
-    switch (pk.v) {                                                                                     \
-    case 1: hipLaunchKernelGGL((gemm_q4r<AF, false, 1>), dim3(tiles), dim3(RNT), 0, s, g, ep); break; \
-    case 2: hipLaunchKernelGGL((gemm_q4r<AF, false, 2>), dim3(tiles), dim3(RNT), 0, s, g, ep); break; \
-    case 3: hipLaunchKernelGGL((gemm_q4r<AF, false, 3>), dim3(tiles), dim3(RNT), 0, s, g, ep); break; \
-    default: hipLaunchKernelGGL((gemm_q4r<AF, false, 0>), dim3(tiles), dim3(RNT), 0, s, g, ep); break; \
+#define SMG_Q4R_LAUNCH(AF, BF)                                                                              \
+    switch (pk.v) {                                                                                         \
+    case 1: hipLaunchKernelGGL((gemm_q4r<AF, false, 1, BF>), dim3(tiles), dim3(RNT), 0, s, g, ep); break; \
+    case 2: hipLaunchKernelGGL((gemm_q4r<AF, false, 2, BF>), dim3(tiles), dim3(RNT), 0, s, g, ep); break; \
+    case 3: hipLaunchKernelGGL((gemm_q4r<AF, false, 3, BF>), dim3(tiles), dim3(RNT), 0, s, g, ep); break; \
+    default: hipLaunchKernelGGL((gemm_q4r<AF, false, 0, BF>), dim3(tiles), dim3(RNT), 0, s, g, ep); break; \
     }
-        if (w.mins) {
-            SMG_Q4R_LAUNCH(true)
+        if (w.mins && bf16) {
+            SMG_Q4R_LAUNCH(true, true)
+        } else if (w.mins) {
+            SMG_Q4R_LAUNCH(true, false)
+        } else if (bf16) {
+            SMG_Q4R_LAUNCH(false, true)
         } else {
-            SMG_Q4R_LAUNCH(false)
+            SMG_Q4R_LAUNCH(false, false)
         }
 #undef SMG_Q4R_LAUNCH
         return hipGetLastError();
@@ -667,14 +736,21 @@ hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long 
     g.part = part;
     g.nsplit = ns;
     g.part_ld = (uint32_t)((w.n + 7) / 8 * 8);
-    if (w.mins)
+    if (w.mins && bf16)
+        hipLaunchKernelGGL((gemm_q4r<true, true, 0, true>), dim3(tiles * ns), dim3(RNT), 0, s, g, ep);
+    else if (w.mins)
         hipLaunchKernelGGL((gemm_q4r<true, true>), dim3(tiles * ns), dim3(RNT), 0, s, g, ep);
+    else if (bf16)
+        hipLaunchKernelGGL((gemm_q4r<false, true, 0, true>), dim3(tiles * ns), dim3(RNT), 0, s, g, ep);
     else
         hipLaunchKernelGGL((gemm_q4r<false, true>), dim3(tiles * ns), dim3(RNT), 0, s, g, ep);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t rtiles = (uint32_t)(((m + QR_BM - 1) / QR_BM) * ((w.n + QR_BN - 1) / QR_BN));
-    hipLaunchKernelGGL(q4r_reduce, dim3(rtiles), dim3(QR_NT), 0, s, g, ep);
+    if (bf16)
+        hipLaunchKernelGGL(q4r_reduce<true>, dim3(rtiles), dim3(QR_NT), 0, s, g, ep);
+    else
+        hipLaunchKernelGGL(q4r_reduce<false>, dim3(rtiles), dim3(QR_NT), 0, s, g, ep);
     return hipGetLastError();
 }
 

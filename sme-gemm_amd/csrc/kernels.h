@@ -76,9 +76,9 @@ hipError_t launch_gemm(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long
 hipError_t launch_pack_dense_strided(const uint16_t *rhs, long rhs_rs, long rhs_cs, size_t n, size_t k,
                                      size_t n_pad, size_t k_pad, uint16_t *dense, hipStream_t s);
 
-// Q4 x f16 GEMM with register-resident weights (gemm_q4r.hip): f16, block >=
-// 32, K a multiple of 64, row-major 16-byte-aligned A. launch_gemm uses it
-// whenever q4r_supported holds.
+// Q4 GEMM with register-resident weights (gemm_q4r.hip): f16 or bf16
+// activations, block >= 32, K a multiple of 64, row-major 16-byte-aligned A.
+// launch_gemm uses it whenever q4r_supported holds.
 // With part (part_bytes of device memory, q4r_split_bytes(w, m) for the full
 // split, untouched between the call and its kernels' completion) a grid too
 // small to fill the device splits K into as many slices as part holds and
@@ -88,7 +88,7 @@ bool q4r_supported(const WDev &w, size_t m, long lhs_cs, long lhs_rs, const uint
 size_t q4r_split_bytes(const WDev &w, size_t m);
 hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,
                       const uint16_t *lhs, long lhs_rs, float beta, const EpArgs &ep, float *part,
-                      size_t part_bytes, hipStream_t s);
+                      size_t part_bytes, bool bf16, hipStream_t s);
 
 // Compute units of the current device (cached per device).
 int device_cus();

@@ -159,9 +159,11 @@ def test_q4_bf16(smg, orc, m, n, k, affine):
 @pytest.mark.parametrize("m,n,k", [(48, 1536, 1024), (100, 4096, 512), (128, 700, 1088)])
 @pytest.mark.parametrize("affine", [False, True])
 def test_q4_bf16_rows_on_gemv_launches(smg, orc, m, n, k, affine):
-    """bf16 calls of 33 to 128 rows run as 16-row GEMV launches (the MFMA
-    GEMM for bf16 leaves most compute units idle at these shapes): ROW and
-    TENSOR operands are offset per launch; against the bf16 portable path."""
+    """bf16 calls of 33 to 128 rows: the register-dequant GEMM with K split
+    over the compute units (ROW and TENSOR operands through the reduction's
+    store), and -- with A one element off 16-byte alignment, which the GEMM's
+    DMA cannot read -- 16-row GEMV launches with ROW and TENSOR operands
+    offset per launch; both against the bf16 portable path."""
     nbk = k // 32
     rng = np.random.default_rng(3 * m + n + k + affine)
     quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
@@ -178,6 +180,48 @@ def test_q4_bf16_rows_on_gemv_launches(smg, orc, m, n, k, affine):
     nodes = [(2, 0, 0.0, row, 0), (7, 0, 0.0, ten, 0), (4, 0, 0.0, col, 0)]
     want = orc.matmul_q4_ep(a, quants, scales, mins, m, n, k, 32, nodes, 3, bf16=True)
     assert max_rel(got, want, bf16=True) <= bf16_tol(k)
+    import torch
+    dev = lambda x: torch.from_numpy(x.view(np.int16)).cuda()  # noqa: E731
+    buf = torch.zeros(m * k + 1, dtype=torch.int16, device="cuda")
+    buf[1:] = dev(a)
+    cd = torch.zeros(m * n, dtype=torch.int16, device="cuda")
+    smg.matmul_q4_bf16_ep(buf[1:].view(torch.bfloat16), w, cd.view(torch.bfloat16), m,
+                          smg.Epilogue(bf16=True).add_row(dev(row)).mul_tensor(dev(ten)).add_col(dev(col)).silu())
+    torch.cuda.synchronize()
+    assert max_rel(cd.cpu().numpy().view(np.uint16), want, bf16=True) <= bf16_tol(k)
+
+
+@pytest.mark.parametrize("m,n,k,affine", [(512, 8192, 256, False), (512, 8192, 256, True), (256, 2048, 1024, False),
+                                          (200, 1000, 4096, True), (64, 4096, 4096, False)])
+def test_q4_bf16_prefill_gemm(smg, orc, m, n, k, affine):
+    """matmul_q4_bf16 prefill on the register-dequant MFMA GEMM (bf16
+    activations and weights, v_mfma_f32_16x16x32_bf16): unsplit grids (at least
+    half the compute units of tiles) with the compiled [mul_col, add_col] +
+    silu store and the interpreted store (the same graph with an exact
+    mul_scalar(1.0): the same bits), and K-split grids; against the bf16
+    portable path (q4/matmul.rs:258-270) at the bf16 bound."""
+    nbk = k // 32
+    rng = np.random.default_rng(m + n + k + affine)
+    quants = rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8)
+    scales = orc.f32_to_f16(rng.uniform(0.005, 0.02, n * nbk).astype(np.float32))
+    mins = orc.f32_to_f16(rng.uniform(-0.1, 0.1, n * nbk).astype(np.float32)) if affine else None
+    a = orc.f32_to_bf16(rng.standard_normal(m * k).astype(np.float32))
+    sc = orc.f32_to_bf16(rng.uniform(0.5, 1.5, n).astype(np.float32))
+    bias = orc.f32_to_bf16(rng.normal(0, 0.1, n).astype(np.float32))
+    p = smg.Q4Params(32).affine() if affine else smg.Q4Params(32)
+    w = smg.Q4Weights.with_params(quants, scales, mins, n, k, p)
+    got = np.zeros(m * n, np.uint16)
+    smg.matmul_q4_bf16_ep(a, w, got, m, smg.Epilogue(bf16=True).mul_col(sc).add_col(bias).silu())
+    want = orc.matmul_q4_ep(a, quants, scales, mins, m, n, k, 32,
+                            [(5, 0, 0.0, sc, 0), (4, 0, 0.0, bias, 0)], 3, bf16=True)
+    assert max_rel(got, want, bf16=True) <= bf16_tol(k)
+    interp = np.zeros(m * n, np.uint16)
+    smg.matmul_q4_bf16_ep(a, w, interp, m, smg.Epilogue(bf16=True).mul_col(sc).add_col(bias).mul_scalar(1.0).silu())
+    assert np.array_equal(interp, got)
+    plain = np.zeros(m * n, np.uint16)
+    smg.matmul_q4_bf16(a, w, plain, m)
+    assert max_rel(plain, orc.matmul_q4_ep(a, quants, scales, mins, m, n, k, 32, bf16=True), bf16=True) \
+        <= bf16_tol(k)
 
 
 @pytest.mark.parametrize("m", [8, 16])
