@@ -365,11 +365,28 @@ int smg_kv_cache_attend_dev(const smg_kv_cache *c, const float *q, float *out, v
 int smg_attention_kv_f16_dev(const float *q, const uint16_t *k, const uint16_t *v, size_t len,
                              size_t heads, size_t kv_heads, size_t head_dim, float scale, float *out,
                              void *stream);
+/* attention_kv_causal_f16 (kv_attention.rs:140-240) on device arrays: q f32
+ * [rows][heads*head_dim], k / v f16 [start + rows][kv_heads*head_dim]; query
+ * row i attends to keys 0 .. start + i, each row as attention_kv_f16 over its
+ * prefix (the portable path's one_row per row), into out f32
+ * [rows][heads*head_dim]. Replaces attn_kv_causal_f16 / _sme_f16 (src/ffi.rs). */
+int smg_attention_kv_causal_f16_dev(const float *q, const uint16_t *k, const uint16_t *v, size_t start,
+                                    size_t rows, size_t heads, size_t kv_heads, size_t head_dim, float scale,
+                                    float *out, void *stream);
+/* KvCache::attend_causal (kv_attention.rs:560-578): `rows` query rows that are
+ * the last `rows` cached positions, each attending causally; q and out f32
+ * [rows][heads*head_dim]. SMG_EINVAL when fewer than rows positions are cached. */
+int smg_kv_cache_attend_causal_dev(const smg_kv_cache *c, const float *q, size_t rows, float *out, void *stream);
 
 /* nn::rms_norm (src/nn.rs:147-161): rows of dim f32 x to f16 y, weight f32
  * [dim]: x / sqrt(mean(x^2) + eps) * weight. */
 int smg_rms_norm_f16_dev(const float *x, const float *weight, size_t rows, size_t dim, float eps,
                          uint16_t *y, void *stream);
+/* nn::layer_norm (src/nn.rs:73-86,133-143): rows of dim f32 x to f16 y,
+ * (x - mean) / sqrt(var + eps) * weight + bias (bias NULL: none); mean and
+ * variance two passes in f32. */
+int smg_layer_norm_f16_dev(const float *x, const float *weight, const float *bias, size_t rows, size_t dim,
+                           float eps, uint16_t *y, void *stream);
 /* GatedLinear's glu (src/linear.rs:804-826): m rows of 2n f16 values, gate and
  * up interleaved 32 columns at a time, to y = f16(act(gate) * up) [m][n];
  * act EP_ACT_SILU or EP_ACT_GELU (Gate::Silu / Gate::Gelu). */
@@ -390,9 +407,10 @@ int smg_attn_create(smg_weights *qkv, smg_weights *out, size_t heads, size_t kv_
                     size_t head_dim, double rope_theta, smg_attn **attn);
 void smg_attn_destroy(smg_attn *a);
 /* SelfAttention::accumulate (self_attention.rs:148-183): y (f32 m x width) +=
- * out(attention(qkv(x))) for x f16 (m x width) at the cache's next position,
- * which it appends. m = 1 (decode); SMG_EINVAL when the cache is full or its
- * heads differ. */
+ * out(attention(qkv(x))) for x f16 (m x width) at the cache's next m
+ * positions, which it appends; m > 1 attends causally (attend_rows,
+ * self_attention.rs:192-240). SMG_EINVAL when the rows do not fit in the cache
+ * or its heads differ. */
 int smg_attn_accumulate_dev(smg_attn *a, const uint16_t *x, smg_kv_cache *cache, float *y, size_t m,
                             void *stream);
 
@@ -412,12 +430,20 @@ int smg_mlp_accumulate_dev(smg_mlp *m, const uint16_t *x, float *y, size_t rows,
  * success (destroying the block destroys them). */
 int smg_block_create(const float *norm1, float eps1, const float *norm2, float eps2, size_t d,
                      smg_attn *attn, smg_mlp *mlp, smg_block **block);
+/* Block::new with either norm kind (src/nn.rs:164-214): layer != 0 is
+ * Norm::layer(weight, bias, eps) (bias may be NULL), else Norm::rms(weight,
+ * eps) (bias must be NULL). As smg_block_create otherwise. */
+int smg_block_create_norms(const float *norm1, const float *bias1, float eps1, int layer1, const float *norm2,
+                           const float *bias2, float eps2, int layer2, size_t d, smg_attn *attn, smg_mlp *mlp,
+                           smg_block **block);
 void smg_block_destroy(smg_block *b);
 /* Block::accumulate (block.rs:90-106): x (f32, rows x d, device) += the
- * attention half, then += the MLP half, at the cache's next position, which it
- * appends. rows = 1 (decode): six launches -- RMSNorm + qkv + RoPE + cache
- * append, attention splits, their merge, out + residual, RMSNorm + gate/up +
- * glu, down + residual. */
+ * attention half, then += the MLP half, at the cache's next `rows` positions,
+ * which it appends. rows = 1 with RMS norms (decode): six launches -- RMSNorm
+ * + qkv + RoPE + cache append, attention splits, their merge, out + residual,
+ * RMSNorm + gate/up + glu, down + residual. More rows (prefill): the norm pass,
+ * the qkv GEMM, RoPE and the cache append, causal attention, the out GEMM and
+ * its add, then the MLP half over all rows. */
 int smg_block_accumulate_dev(smg_block *b, float *x, smg_kv_cache *cache, size_t rows, void *stream);
 
 /* ---- measurement probes (not part of the matmul path) ----------------------- */

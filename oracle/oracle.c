@@ -763,6 +763,44 @@ void or_rms_norm_f16(const float *x, const float *w, size_t rows, size_t dim, fl
     }
 }
 
+/* norm_row with rms = false (nn.rs:133-143): mean = lane_sum(x) / dim, then
+ * r = 1 / sqrt(lane_sum((v - mean)^2) / dim + eps), both sums in lane_sum's
+ * order (8 lane accumulators over whole chunks of 8, the tail summed in order
+ * from -0.0, the lanes added in order, then the tail); each output is
+ * (v - mean) * r * w + b (b = 0 without a bias), left to right. */
+static float or_lane_sum(const float *x, size_t dim, float mean, int square) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const size_t chunks = dim / 8;
+    for (size_t c = 0; c < chunks; c++)
+        for (size_t i = 0; i < 8; i++) {
+            const float v = x[8 * c + i] - mean;
+            acc[i] = acc[i] + (square ? v * v : x[8 * c + i]);
+        }
+    float tail = -0.0f;
+    for (size_t t = chunks * 8; t < dim; t++) {
+        const float v = x[t] - mean;
+        tail = tail + (square ? v * v : x[t]);
+    }
+    float s = -0.0f;
+    for (size_t i = 0; i < 8; i++) s = s + acc[i];
+    return s + tail;
+}
+void or_layer_norm_row(const float *x, const float *w, const float *b, size_t dim, float eps, float *out) {
+    const float mean = or_lane_sum(x, dim, 0.0f, 0) / (float)dim;
+    const float r = 1.0f / sqrtf(or_lane_sum(x, dim, mean, 1) / (float)dim + eps);
+    for (size_t i = 0; i < dim; i++) out[i] = (x[i] - mean) * r * w[i] + (b ? b[i] : 0.0f);
+}
+
+/* nn::layer_norm into f16 (rows of `dim`; each row's f32 result rounded by
+ * to_f16, RNE). */
+void or_layer_norm_f16(const float *x, const float *w, const float *b, size_t rows, size_t dim, float eps,
+                       uint16_t *y, float *row_scratch) {
+    for (size_t r = 0; r < rows; r++) {
+        or_layer_norm_row(x + r * dim, w, b, dim, eps, row_scratch);
+        for (size_t i = 0; i < dim; i++) y[r * dim + i] = or_f32_to_f16(row_scratch[i]);
+    }
+}
+
 /* Rope::new without YaRN (model.rs:38-51): inv_freq[i] = (1 / base^(2i/dim))
  * in f64, then to f32. */
 void or_rope_inv_freq(size_t dim, double base, float *inv_freq) {

@@ -80,6 +80,8 @@ def lib() -> C.CDLL:
         L.or_lowbit_pack_band.argtypes = [C.c_int, P, P, C.c_int, SZ, SZ, SZ, P, P]
         L.or_rms_norm_row.argtypes = [P, P, SZ, C.c_float, P]
         L.or_rms_norm_f16.argtypes = [P, P, SZ, SZ, C.c_float, P, P]
+        L.or_layer_norm_row.argtypes = [P, P, P, SZ, C.c_float, P]
+        L.or_layer_norm_f16.argtypes = [P, P, P, SZ, SZ, C.c_float, P, P]
         L.or_rope_inv_freq.argtypes = [SZ, C.c_double, P]
         L.or_rope_angles.argtypes = [P, SZ, SZ, P, P]
         L.or_rope_apply.argtypes = [P, SZ, P, P, SZ]
@@ -417,6 +419,36 @@ def rms_norm_f16(x, w, eps, rows=1):
     return y
 
 
+def layer_norm_row(x, w, b, eps):
+    """norm_row with rms = false (src/nn.rs:133-143), f32 out; b may be None."""
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    bb = None if b is None else _c(b, np.float32)
+    out = np.empty(x.size, np.float32)
+    lib().or_layer_norm_row(_p(x), _p(w), None if bb is None else _p(bb), x.size, eps, _p(out))
+    return out
+
+
+def layer_norm_f16(x, w, b, eps, rows=1):
+    """nn::layer_norm into f16 (src/nn.rs:73-86): rows of len(w); b may be None."""
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    bb = None if b is None else _c(b, np.float32)
+    y = np.empty(x.size, np.uint16)
+    scratch = np.empty(w.size, np.float32)
+    lib().or_layer_norm_f16(_p(x), _p(w), None if bb is None else _p(bb), rows, w.size, eps, _p(y),
+                            _p(scratch))
+    return y
+
+
+def norm_f16(x, p, which):
+    """The block's norm `which` (1 or 2): Norm::layer when p["norm"] is "layer"
+    (weights p["norm<which>"], optional bias p["bias<which>"]), else Norm::rms."""
+    if p.get("norm") == "layer":
+        return layer_norm_f16(x, p[f"norm{which}"], p.get(f"bias{which}"), p["eps"])
+    return rms_norm_f16(x, p[f"norm{which}"], p["eps"])
+
+
 def rope_inv_freq(dim, base=10000.0):
     """Rope::new without YaRN (examples/bonsai/model.rs:38-51)."""
     out = np.empty(dim // 2, np.float32)
@@ -503,7 +535,7 @@ def block_decode(x, cache_k, cache_v, pos, p, parts=None):
     ("attn", "mlp"), and the residual between them ("x1")."""
     d, H, KV, hd, eps = p["d"], p["heads"], p["kv_heads"], p["head_dim"], p["eps"]
     x = np.array(x, np.float32, copy=True)
-    h = rms_norm_f16(x, p["norm1"], eps)
+    h = norm_f16(x, p, 1)
     qkv = p["qkv"].forward(h)
     ql, kl = H * hd, KV * hd
     q32 = f16_to_f32(qkv[:ql])
@@ -529,11 +561,46 @@ def block_decode(x, cache_k, cache_v, pos, p, parts=None):
 
 def block_mlp_term(x, p):
     """The MLP half's term of Block::accumulate (src/block.rs:90-106) for the
-    f32 residual row x: f32(down(glu(gate_up(rms_norm(x, norm2) -> f16))))."""
-    h = rms_norm_f16(np.asarray(x, np.float32), p["norm2"], p["eps"])
-    both = p["gate_up"].forward(h)
-    hid = glu_f16(both, 1, p["ffn"], p.get("gelu", False))
+    f32 residual row x: f32(down(glu(gate_up(norm2(x) -> f16)))) (Mlp::gated),
+    or with p["up"], f32(down(act(up(h)))) (Mlp::new, the activation at the up
+    projection's f16 store: src/mlp.rs:113-149, act p["act"])."""
+    h = norm_f16(np.asarray(x, np.float32), p, 2)
+    if "up" in p:
+        hid = p["up"].forward(h, 1, (), p["act"])
+    else:
+        both = p["gate_up"].forward(h)
+        hid = glu_f16(both, 1, p["ffn"], p.get("gelu", False))
     return f16_to_f32(p["down"].forward(hid))
+
+
+def block_rows(x, cache_k, cache_v, pos, rows, p):
+    """Block::accumulate for `rows` rows at positions pos .. pos + rows - 1
+    (src/block.rs:90-106): every output row depends on its own input row and
+    on the cache -- the qkv, out and MLP products and the norms act row by
+    row, and attend_causal gives row r the portable one_row over positions
+    0 .. pos + r (kv_attention.rs:214-238) -- so the block of rows is
+    block_decode applied to the rows in order. x: f32 [rows][d] (updated copy
+    returned); cache rows pos .. pos + rows - 1 written."""
+    d = p["d"]
+    x = np.array(x, np.float32, copy=True).reshape(rows, d)
+    for r in range(rows):
+        x[r] = block_decode(x[r], cache_k, cache_v, pos + r, p)
+    return x.ravel()
+
+
+def attention_kv_causal_f16(q, k, v, start, rows, heads, kv_heads, hd, scale):
+    """attention_kv_causal_f16's portable path (src/kernels/kv_attention.rs:214-238):
+    query row i is one_row over keys 0 .. start + i. q f32 [rows][heads*hd],
+    k/v f16 bits [start + rows][kv_heads*hd]; returns f32 [rows][heads*hd]."""
+    q = _c(q, np.float32).reshape(rows, heads * hd)
+    ld = kv_heads * hd
+    k = _c(k, np.uint16).reshape(-1, ld)
+    v = _c(v, np.uint16).reshape(-1, ld)
+    out = np.empty((rows, heads * hd), np.float32)
+    for i in range(rows):
+        out[i] = attention_kv_f16(q[i], k[:start + i + 1], v[:start + i + 1], start + i + 1, heads, kv_heads,
+                                  hd, scale)
+    return out.ravel()
 
 
 def q4_interleave32(gq, gs, uq, us, n, k, block=32):

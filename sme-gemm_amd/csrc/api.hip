@@ -687,6 +687,8 @@ struct smg_mlp {
 struct smg_block {
     int device;
     float *norm1, *norm2;  // device f32 [d]
+    float *bias1, *bias2;  // device f32 [d] or null (Norm::layer's bias)
+    bool layer1, layer2;   // Norm::layer (else Norm::rms)
     size_t d;
     float eps1, eps2;
     smg_attn *attn;
@@ -854,12 +856,130 @@ int attn_step(smg_attn *a, smg_kv_cache *c, const uint16_t *x16, const float *nx
     return SMG_OK;
 }
 
+// Device scratch carved from the stream's pool above `base`: each size is
+// rounded up to 256 bytes; the pointers come back in order.
+int carve_scratch(int device, void *stream, size_t base, std::initializer_list<size_t> sizes, uint8_t **out) {
+    size_t total = 0;
+    for (size_t z : sizes) total += round_up(z, 256);
+    uint8_t *p = (uint8_t *)dev_pool().get(device, stream, base + total);
+    if (!p) return fail(SMG_ENOMEM, "scratch hipMalloc");
+    p += base;
+    size_t i = 0;
+    for (size_t z : sizes) {
+        out[i++] = p;
+        p += round_up(z, 256);
+    }
+    return SMG_OK;
+}
+
+// The attention partial sums one launch may hold: a causal block of rows is
+// attended in chunks of rows whose partials fit (row r of a chunk needs
+// attn_splits(its prefix) x heads x (hd + 2) floats).
+constexpr size_t ATT_PART_BYTES = 64u << 20;
+size_t causal_chunk_rows(size_t rows, size_t last_len, size_t heads, size_t hd) {
+    const size_t per_row = attn_partial_floats(1, last_len, heads, hd) * 4;
+    return std::max<size_t>(1, std::min(rows, ATT_PART_BYTES / per_row));
+}
+
+// Causal attention of `rows` f16 query rows (q16 [rows][heads hd], already
+// f16(q * scale)) over k / v whose row r attends to keys 0 .. start + r: one
+// launch_attention per chunk of rows, partials in `part`
+// (causal_chunk_rows(...) rows' worth).
+hipError_t causal_attention(const uint16_t *q16, const uint16_t *k, const uint16_t *v, size_t start, size_t rows,
+                            size_t heads, size_t kv_heads, size_t hd, float *part, void *out, bool f16_out,
+                            hipStream_t s) {
+    const size_t qlen = heads * hd, last = start + rows;
+    const size_t rc = causal_chunk_rows(rows, last, heads, hd);
+    const size_t po_floats = rc * attn_splits(last) * heads * hd;
+    for (size_t r0 = 0; r0 < rows; r0 += rc) {
+        AttnArgs at = {};
+        at.q = q16 + r0 * qlen;
+        at.k = k;
+        at.v = v;
+        at.po = part;
+        at.pml = (float2 *)(part + po_floats);
+        at.len = (uint32_t)(start + r0 + 1);
+        at.rows = (uint32_t)std::min(rc, rows - r0);
+        at.ld = (uint32_t)(kv_heads * hd);
+        at.hd = (uint32_t)hd;
+        at.heads = (uint32_t)heads;
+        at.group = (uint32_t)(heads / kv_heads);
+        void *o = f16_out ? (void *)((uint16_t *)out + r0 * qlen) : (void *)((float *)out + r0 * qlen);
+        const hipError_t e = launch_attention(at, o, f16_out, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// The attention half for m > 1 rows of x16 (SelfAttention::accumulate,
+// self_attention.rs:148-240: qkv over all rows, every row's key and value
+// appended, then attend_causal, then out): the qkv projection as one Q4 call
+// over the rows (the GEMM past the GEMV's rows), qkv_rows for RoPE, the cache
+// append and q's rounding at positions pos .. pos + m - 1, causal attention
+// (row r over positions 0 .. pos + r, kv_attention.rs:155-240), and the out
+// projection added into y (8-row GEMV launches adding in their store, or a
+// GEMM and an add). Appends m cache rows.
+int attn_rows(smg_attn *a, smg_kv_cache *c, const uint16_t *x16, float *y, size_t m, void *stream,
+              size_t base = 0) {
+    int rc = check_cache(a, c, m);
+    if (rc) return rc;
+    const float *rope = nullptr;
+    size_t rope_cap = 0;
+    if ((rc = ensure_rope(a, c->cap, &rope, &rope_cap))) return rc;
+    const size_t pos = c->len, ld = a->kv_heads * a->hd, qlen = a->heads * a->hd, half = a->hd / 2;
+    const size_t nq = a->qkv->d.n, d_out = a->out->d.n;
+    const size_t crow = causal_chunk_rows(m, pos + m, a->heads, a->hd);
+    uint8_t *bufs[5];
+    if ((rc = carve_scratch(a->device, stream, base,
+                            {m * nq * 2, m * qlen * 2, m * qlen * 2, m > 8 ? m * d_out * 2 : 0,
+                             attn_partial_floats(crow, pos + m, a->heads, a->hd) * 4},
+                            bufs)))
+        return rc;
+    uint16_t *qkv16 = (uint16_t *)bufs[0], *q16 = (uint16_t *)bufs[1], *att16 = (uint16_t *)bufs[2];
+    uint16_t *out16 = (uint16_t *)bufs[3];
+    float *part = (float *)bufs[4];
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = run_q4_dev(a->qkv->device, a->qkv->d, m, qkv16, x16, EpArgs{}, false, s);
+    if (e != hipSuccess) return q4_fail("qkv projection", e);
+    QkvRowsArgs qa = {};
+    qa.qkv = qkv16;
+    qa.q_out = q16;
+    qa.k_cache = c->k + pos * ld;
+    qa.v_cache = c->v + pos * ld;
+    if (a->theta > 0.0) {
+        qa.cs = rope + pos * half;
+        qa.sn = rope + rope_cap * half + pos * half;
+    }
+    qa.scale = c->scale;
+    qa.m = (uint32_t)m;
+    qa.heads = (uint32_t)a->heads;
+    qa.kv_heads = (uint32_t)a->kv_heads;
+    qa.hd = (uint32_t)a->hd;
+    if ((e = launch_qkv_rows(qa, s)) != hipSuccess) return fail(SMG_EHIP, "qkv rows", e);
+    if ((e = causal_attention(q16, c->k, c->v, pos, m, a->heads, a->kv_heads, a->hd, part, att16, true, s)) !=
+        hipSuccess)
+        return fail(SMG_EHIP, "causal attention", e);
+    if (m <= 8) {
+        BlkArgs r = {};
+        r.x = y;
+        if ((e = launch_blk_gemv(a->out->d, m, att16, r, BS_RESID, false, s)) != hipSuccess)
+            return fail(SMG_EHIP, "out projection", e);
+    } else {
+        if ((e = run_q4_dev(a->out->device, a->out->d, m, out16, att16, EpArgs{}, false, s)) != hipSuccess)
+            return q4_fail("out projection", e);
+        if ((e = launch_add_f16(out16, m * d_out, y, s)) != hipSuccess) return fail(SMG_EHIP, "residual add", e);
+    }
+    c->len = pos + m;
+    return SMG_OK;
+}
+
 // The MLP half: y += down(act(up(x))) for `rows` rows of x16, or (nx) of the
-// RMS norm of the f32 rows nx with weights nw.
+// norm of the f32 rows nx with weights nw: RMS (fused into the gate/up GEMV for
+// one row), or with layer, nn::layer_norm with bias nb (may be null).
 int mlp_step(smg_mlp *m, const uint16_t *x16, const float *nx, const float *nw, float eps, float *y,
-             size_t rows, void *stream) {
+             size_t rows, void *stream, bool layer = false, const float *nb = nullptr) {
     const size_t k = m->up->d.k, d_out = m->down->d.n;
-    const bool fused_norm = nx && rows == 1 && m->gated && k <= 4096 && k % 8 == 0;
+    const bool fused_norm = nx && !layer && rows == 1 && m->gated && k <= 4096 && k % 8 == 0;
     DecodeScratch sc;
     const size_t both = m->gated ? m->up->d.n : 0;
     int rc = decode_scratch(m->device, stream, 0, 0, 0, (nx && !fused_norm ? rows * k : 0) + rows * both +
@@ -868,8 +988,9 @@ int mlp_step(smg_mlp *m, const uint16_t *x16, const float *nx, const float *nw, 
     if (rc) return rc;
     hipStream_t s = (hipStream_t)stream;
     hipError_t e = hipSuccess;
-    if (nx && !fused_norm) {  // the norm as its own pass (nn::rms_norm)
-        if ((e = launch_rms_norm(nx, nw, rows, k, eps, sc.h16, s)) != hipSuccess) return fail(SMG_EHIP, "rms_norm", e);
+    if (nx && !fused_norm) {  // the norm as its own pass (nn::rms_norm / nn::layer_norm)
+        if ((e = launch_norm_rows(nx, nw, nb, rows, k, eps, layer, sc.h16, s)) != hipSuccess)
+            return fail(SMG_EHIP, layer ? "layer_norm" : "rms_norm", e);
         x16 = sc.h16;
     }
     uint16_t *spare = sc.h16 + (nx && !fused_norm ? rows * k : 0);  // [rows][both], then [rows][d_out]
@@ -1589,6 +1710,24 @@ int smg_kv_cache_extend_dev(smg_kv_cache *c, const uint16_t *k, const uint16_t *
     return SMG_OK;
 }
 
+// rows query rows (f32 [rows][heads hd]), row r attending to keys 0 .. start + r
+// (rows = 1, start = len - 1: attention_kv_f16; more rows: the causal form).
+static int causal_dev(int device, const float *q, const uint16_t *k, const uint16_t *v, size_t start, size_t rows,
+                      size_t heads, size_t kv_heads, size_t hd, float scale, float *out, void *stream) {
+    if (!q || !k || !v || !out) return fail(SMG_EINVAL, "null array");
+    const size_t qlen = heads * hd, crow = causal_chunk_rows(rows, start + rows, heads, hd);
+    uint8_t *bufs[2];
+    int rc = carve_scratch(device, stream, 0, {rows * qlen * 2, attn_partial_floats(crow, start + rows, heads, hd) * 4},
+                           bufs);
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = launch_round_q(q, scale, rows * qlen, (uint16_t *)bufs[0], s);
+    if (e == hipSuccess)
+        e = causal_attention((uint16_t *)bufs[0], k, v, start, rows, heads, kv_heads, hd, (float *)bufs[1], out,
+                             false, s);
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "causal attention", e);
+}
+
 static int attention_dev(int device, const float *q, const uint16_t *k, const uint16_t *v, size_t len,
                          size_t heads, size_t kv_heads, size_t hd, float scale, float *out, void *stream) {
     if (!head_shape_ok(heads, kv_heads, hd))
@@ -1629,6 +1768,26 @@ int smg_attention_kv_f16_dev(const float *q, const uint16_t *k, const uint16_t *
     return attention_dev(dev, q, k, v, len, heads, kv_heads, head_dim, scale, out, stream);
 }
 
+int smg_attention_kv_causal_f16_dev(const float *q, const uint16_t *k, const uint16_t *v, size_t start,
+                                    size_t rows, size_t heads, size_t kv_heads, size_t head_dim, float scale,
+                                    float *out, void *stream) {
+    if (rows == 0) return fail(SMG_EINVAL, "attention_kv_causal_f16 needs at least one query row");
+    if (!head_shape_ok(heads, kv_heads, head_dim))
+        return fail(SMG_EINVAL, "head_dim must be a multiple of 8 in 8..=256 and heads a positive multiple of kv_heads");
+    if (start > ((size_t)1 << 31) || rows > ((size_t)1 << 31)) return fail(SMG_EINVAL, "start + rows overflows");
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev), SMG_EHIP);
+    return causal_dev(dev, q, k, v, start, rows, heads, kv_heads, head_dim, scale, out, stream);
+}
+
+int smg_kv_cache_attend_causal_dev(const smg_kv_cache *c, const float *q, size_t rows, float *out, void *stream) {
+    if (!c) return fail(SMG_EINVAL, "null cache");
+    if (rows == 0) return fail(SMG_EINVAL, "attention_kv_causal_f16 needs at least one query row");
+    if (rows > c->len) return fail(SMG_EINVAL, "attend_causal: more rows than cached positions");
+    return causal_dev(c->device, q, c->k, c->v, c->len - rows, rows, c->heads, c->kv_heads, c->hd, c->scale, out,
+                      stream);
+}
+
 int smg_rms_norm_f16_dev(const float *x, const float *weight, size_t rows, size_t dim, float eps,
                          uint16_t *y, void *stream) {
     if (dim == 0) return fail(SMG_EINVAL, "a norm needs at least one feature");
@@ -1636,6 +1795,15 @@ int smg_rms_norm_f16_dev(const float *x, const float *weight, size_t rows, size_
     if (!x || !weight || !y) return fail(SMG_EINVAL, "null array");
     hipError_t e = launch_rms_norm(x, weight, rows, dim, eps, y, (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "rms_norm", e);
+}
+
+int smg_layer_norm_f16_dev(const float *x, const float *weight, const float *bias, size_t rows, size_t dim,
+                           float eps, uint16_t *y, void *stream) {
+    if (dim == 0) return fail(SMG_EINVAL, "a norm needs at least one feature");
+    if (rows == 0) return SMG_OK;
+    if (!x || !weight || !y) return fail(SMG_EINVAL, "null array");
+    hipError_t e = launch_norm_rows(x, weight, bias, rows, dim, eps, true, y, (hipStream_t)stream);
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "layer_norm", e);
 }
 
 int smg_glu_f16_dev(const uint16_t *both, size_t m, size_t n, uint32_t act, uint16_t *y, void *stream) {
@@ -1702,8 +1870,9 @@ int smg_attn_accumulate_dev(smg_attn *a, const uint16_t *x, smg_kv_cache *cache,
                             void *stream) {
     if (!a) return fail(SMG_EINVAL, "null attention");
     if (m == 0) return SMG_OK;
-    if (m != 1) return fail(SMG_EINVAL, "SelfAttention on the GPU takes one row (decode)");
     if (!x || !y) return fail(SMG_EINVAL, "null array");
+    if (m > 65535) return fail(SMG_EINVAL, "at most 65535 rows a call");
+    if (m > 1) return attn_rows(a, cache, x, y, m, stream);
     return attn_step(a, cache, x, nullptr, nullptr, 0.0f, y, stream);
 }
 
@@ -1744,9 +1913,11 @@ int smg_mlp_accumulate_dev(smg_mlp *m, const uint16_t *x, float *y, size_t rows,
     return mlp_step(m, x, nullptr, nullptr, 0.0f, y, rows, stream);
 }
 
-int smg_block_create(const float *norm1, float eps1, const float *norm2, float eps2, size_t d,
-                     smg_attn *attn, smg_mlp *mlp, smg_block **block) {
+int smg_block_create_norms(const float *norm1, const float *bias1, float eps1, int layer1, const float *norm2,
+                           const float *bias2, float eps2, int layer2, size_t d, smg_attn *attn, smg_mlp *mlp,
+                           smg_block **block) {
     if (!attn || !mlp || !block || !norm1 || !norm2) return fail(SMG_EINVAL, "null argument");
+    if ((bias1 && !layer1) || (bias2 && !layer2)) return fail(SMG_EINVAL, "only Norm::layer takes a bias");
     if (d == 0 || attn->qkv->d.k != d || attn->out->d.n != d || mlp->up->d.k != d || mlp->down->d.n != d)
         return fail(SMG_EINVAL, "the norms, attention and MLP share the residual's width");
     if (attn->device != mlp->device) return fail(SMG_EINVAL, "attention and MLP are on different devices");
@@ -1756,12 +1927,17 @@ int smg_block_create(const float *norm1, float eps1, const float *norm2, float e
     b->d = d;
     b->eps1 = eps1;
     b->eps2 = eps2;
-    b->norm1 = b->norm2 = nullptr;
-    if (dev_malloc((void **)&b->norm1, d * 4) != hipSuccess || dev_malloc((void **)&b->norm2, d * 4) != hipSuccess ||
-        hipMemcpy(b->norm1, norm1, d * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(b->norm2, norm2, d * 4, hipMemcpyHostToDevice) != hipSuccess) {
-        if (b->norm1) (void)hipFree(b->norm1);
-        if (b->norm2) (void)hipFree(b->norm2);
+    b->layer1 = layer1 != 0;
+    b->layer2 = layer2 != 0;
+    b->norm1 = b->norm2 = b->bias1 = b->bias2 = nullptr;
+    auto upload = [&](float **dst, const float *src) {
+        return !src || (dev_malloc((void **)dst, d * 4) == hipSuccess &&
+                        hipMemcpy(*dst, src, d * 4, hipMemcpyHostToDevice) == hipSuccess);
+    };
+    if (!upload(&b->norm1, norm1) || !upload(&b->norm2, norm2) || !upload(&b->bias1, bias1) ||
+        !upload(&b->bias2, bias2)) {
+        for (float *p : {b->norm1, b->norm2, b->bias1, b->bias2})
+            if (p) (void)hipFree(p);
         delete b;
         return fail(SMG_ENOMEM, "block norm weights");
     }
@@ -1771,11 +1947,18 @@ int smg_block_create(const float *norm1, float eps1, const float *norm2, float e
     return SMG_OK;
 }
 
+int smg_block_create(const float *norm1, float eps1, const float *norm2, float eps2, size_t d,
+                     smg_attn *attn, smg_mlp *mlp, smg_block **block) {
+    return smg_block_create_norms(norm1, nullptr, eps1, 0, norm2, nullptr, eps2, 0, d, attn, mlp, block);
+}
+
 void smg_block_destroy(smg_block *b) {
     if (!b) return;
     (void)hipSetDevice(b->device);
     (void)hipFree(b->norm1);
     (void)hipFree(b->norm2);
+    if (b->bias1) (void)hipFree(b->bias1);
+    if (b->bias2) (void)hipFree(b->bias2);
     destroy_attn(b->attn);
     destroy_mlp(b->mlp);
     delete b;
@@ -1784,24 +1967,28 @@ void smg_block_destroy(smg_block *b) {
 int smg_block_accumulate_dev(smg_block *b, float *x, smg_kv_cache *cache, size_t rows, void *stream) {
     if (!b) return fail(SMG_EINVAL, "null block");
     if (rows == 0) return SMG_OK;
-    if (rows != 1) return fail(SMG_EINVAL, "Block on the GPU takes one row (decode)");
     if (!x) return fail(SMG_EINVAL, "null array");
-    // x += attn(norm1(x)); x += mlp(norm2(x)) (block.rs:98-105), each norm
-    // fused into the projection that reads it
-    const bool fuse = b->d <= 4096 && b->d % 8 == 0;
+    if (rows > 65535) return fail(SMG_EINVAL, "at most 65535 rows a call");
+    // x += attn(norm1(x)); x += mlp(norm2(x)) (block.rs:98-105); for one row
+    // an RMS norm is fused into the projection that reads it
+    const bool fuse = rows == 1 && !b->layer1 && b->d <= 4096 && b->d % 8 == 0;
     int rc;
     if (fuse) {
         rc = attn_step(b->attn, cache, nullptr, x, b->norm1, b->eps1, x, stream);
     } else {
-        DecodeScratch sc;
-        if ((rc = decode_scratch(b->device, stream, 0, 0, 0, b->d, 0, &sc))) return rc;
-        hipError_t e = launch_rms_norm(x, b->norm1, 1, b->d, b->eps1, sc.h16, (hipStream_t)stream);
-        if (e != hipSuccess) return fail(SMG_EHIP, "rms_norm", e);
-        // the attention's scratch above the normalized row
-        rc = attn_step(b->attn, cache, sc.h16, nullptr, nullptr, 0.0f, x, stream, round_up(b->d * 2, 256));
+        if ((rc = check_cache(b->attn, cache, rows))) return rc;
+        uint8_t *h16;
+        if ((rc = carve_scratch(b->device, stream, 0, {rows * b->d * 2}, &h16))) return rc;
+        hipError_t e = launch_norm_rows(x, b->norm1, b->bias1, rows, b->d, b->eps1, b->layer1, (uint16_t *)h16,
+                                        (hipStream_t)stream);
+        if (e != hipSuccess) return fail(SMG_EHIP, b->layer1 ? "layer_norm" : "rms_norm", e);
+        // the attention's scratch above the normalized rows
+        const size_t base = round_up(rows * b->d * 2, 256);
+        rc = rows == 1 ? attn_step(b->attn, cache, (uint16_t *)h16, nullptr, nullptr, 0.0f, x, stream, base)
+                       : attn_rows(b->attn, cache, (uint16_t *)h16, x, rows, stream, base);
     }
     if (rc) return rc;
-    return mlp_step(b->mlp, nullptr, x, b->norm2, b->eps2, x, 1, stream);
+    return mlp_step(b->mlp, nullptr, x, b->norm2, b->eps2, x, rows, stream, b->layer2, b->bias2);
 }
 
 // ---- measurement probes --------------------------------------------------------

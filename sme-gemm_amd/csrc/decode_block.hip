@@ -372,12 +372,16 @@ __global__ void __launch_bounds__(AT_T) attn_split(AttnArgs a) {
     __shared__ float2 mls[AT_HC];
     const int t = threadIdx.x;
     const int ks = t / LPK, c = t % LPK;
-    const uint32_t split = blockIdx.x;
+    const uint32_t split = blockIdx.x, row = blockIdx.z;
+    const uint32_t len = a.len + row;  // this row's causal prefix
+    if (split * AT_KPS >= len) return;  // past the row's last split (uniform: before any barrier)
     const uint32_t kvh = blockIdx.y / a.hchunks, hc0 = (blockIdx.y % a.hchunks) * AT_HC;
     const bool dim_ok = 8u * c < a.hd;
-    const rsrc_t qr = make_rsrc(a.q, a.heads * a.hd * 2u);
-    const rsrc_t kr = make_rsrc(a.k, a.len * a.ld * 2u);
-    const rsrc_t vr = make_rsrc(a.v, a.len * a.ld * 2u);
+    const rsrc_t qr = make_rsrc(a.q + (size_t)row * a.heads * a.hd, a.heads * a.hd * 2u);
+    const rsrc_t kr = make_rsrc(a.k, len * a.ld * 2u);
+    const rsrc_t vr = make_rsrc(a.v, len * a.ld * 2u);
+    float *po = a.po + (size_t)row * a.nsplit * a.heads * a.hd;
+    float2 *pml = a.pml + (size_t)row * a.nsplit * a.heads;
     uint4 qv[AT_HC];
 #pragma unroll
     for (int hh = 0; hh < AT_HC; hh++) {
@@ -390,7 +394,7 @@ __global__ void __launch_bounds__(AT_T) attn_split(AttnArgs a) {
 #pragma unroll
     for (int it = 0; it < IT; it++) {
         const uint32_t key = key0 + ks + KPI * it;
-        const uint32_t off = (key < a.len && dim_ok) ? (key * a.ld + kvh * a.hd + 8 * c) * 2u : OOB;
+        const uint32_t off = (key < len && dim_ok) ? (key * a.ld + kvh * a.hd + 8 * c) * 2u : OOB;
         kv[it] = bload16(kr, off);
         vv[it] = bload16(vr, off);
     }
@@ -408,7 +412,7 @@ __global__ void __launch_bounds__(AT_T) attn_split(AttnArgs a) {
                 s = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, qw[w]), __builtin_bit_cast(half2_t, kw[w]),
                                            s, false);
             s = dpp_group_sum<LPK>(s);
-            if (c == 0) sc[hh][ks + KPI * it] = key < a.len ? s : -INFINITY;
+            if (c == 0) sc[hh][ks + KPI * it] = key < len ? s : -INFINITY;
         }
     }
     __syncthreads();
@@ -458,10 +462,10 @@ __global__ void __launch_bounds__(AT_T) attn_split(AttnArgs a) {
             float sum = 0.0f;
             for (int q = 0; q < KPI; q++) sum = sum + ored[q][hh][d];
             const uint32_t h = kvh * a.group + hc0 + hh;
-            a.po[((size_t)split * a.heads + h) * a.hd + d] = sum;
+            po[((size_t)split * a.heads + h) * a.hd + d] = sum;
         }
     }
-    if (t < AT_HC && hc0 + t < a.group) a.pml[(size_t)split * a.heads + kvh * a.group + hc0 + t] = mls[t];
+    if (t < AT_HC && hc0 + t < a.group) pml[(size_t)split * a.heads + kvh * a.group + hc0 + t] = mls[t];
 }
 
 // The splits of head blockIdx.x merged, for depths 16 blockIdx.y .. +16:
@@ -475,11 +479,17 @@ constexpr int CM_T = 256;           // threads
 constexpr int CM_D = 16;            // depths per workgroup
 constexpr int CM_G = CM_T / CM_D;   // split groups
 constexpr int CM_P = 8;             // splits per thread per round trip
+// Row blockIdx.z merges its own splits: attn_splits(len0 + row) of the
+// nsplit_max allotted to each row.
 template <bool F16OUT>
-__global__ void __launch_bounds__(CM_T) attn_combine(const float *po, const float2 *pml, uint32_t nsplit,
-                                                     uint32_t heads, uint32_t hd, void *out) {
+__global__ void __launch_bounds__(CM_T) attn_combine(const float *po, const float2 *pml, uint32_t nsplit_max,
+                                                     uint32_t len0, uint32_t heads, uint32_t hd, void *out) {
     __shared__ float sm[CM_G][CM_D], sl[CM_G][CM_D], so[CM_G][CM_D];
-    const uint32_t h = blockIdx.x, t = threadIdx.x;
+    const uint32_t h = blockIdx.x, t = threadIdx.x, row = blockIdx.z;
+    const uint32_t nsplit = (len0 + row + AT_KPS - 1) / AT_KPS;
+    po += (size_t)row * nsplit_max * heads * hd;
+    pml += (size_t)row * nsplit_max * heads;
+    out = F16OUT ? (void *)((uint16_t *)out + (size_t)row * heads * hd) : (void *)((float *)out + (size_t)row * heads * hd);
     const uint32_t dl = t % CM_D, g = t / CM_D;
     const uint32_t d = blockIdx.y * CM_D + dl;
     const bool dok = d < hd;
@@ -528,6 +538,81 @@ __global__ void __launch_bounds__(CM_T) attn_combine(const float *po, const floa
         if (F16OUT) ((uint16_t *)out)[h * hd + d] = f32_to_f16(v);
         else ((float *)out)[h * hd + d] = v;
     }
+}
+
+// m rows of the qkv projection (an f16 GEMM output in the fused QKV store's
+// device column order: a 16-column tile holds depths 8q..8q+7 and
+// half+8q..half+8q+7 of one head, each RoPE pair in lanes c, c ^ 8) to the
+// attention's inputs at positions pos0 + r, with the fused store's arithmetic
+// (the rotation in f32 of the f16 outputs, x1 c - x2 s and x2 c + x1 s as
+// examples/bonsai/model.rs:87-99; q16 = f16(q * scale), kv_attention.rs:298-302;
+// k rounded to f16, v copied). One thread per (row, column).
+__global__ void __launch_bounds__(256) qkv_rows(QkvRowsArgs a) {
+    const uint32_t r = blockIdx.y;
+    const uint32_t n = (a.heads + 2 * a.kv_heads) * a.hd;
+    const uint32_t p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= n) return;
+    const uint32_t hd = a.hd, half = hd / 2;
+    const uint32_t H = p / hd, qt = (p % hd) / 16, cc = p % 16;
+    const uint32_t i = cc < 8 ? 8 * qt + cc : half + 8 * qt + cc - 8;
+    const uint16_t *row = a.qkv + (size_t)r * n;
+    const uint16_t own16 = row[p];
+    const size_t ld = (size_t)a.kv_heads * hd;
+    if (H < a.heads + a.kv_heads) {
+        float val = f16_to_f32(own16);
+        if (a.cs) {
+            const uint16_t par16 = row[p ^ 8];
+            const uint32_t pi = 8 * qt + (cc & 7);
+            const float c = a.cs[(size_t)r * half + pi], s = a.sn[(size_t)r * half + pi];
+            const float x1 = f16_to_f32(cc < 8 ? own16 : par16);
+            const float x2 = f16_to_f32(cc < 8 ? par16 : own16);
+            val = cc < 8 ? x1 * c - x2 * s : x2 * c + x1 * s;
+        }
+        if (H < a.heads) a.q_out[(size_t)r * a.heads * hd + H * hd + i] = f32_to_f16(val * a.scale);
+        else a.k_cache[(size_t)r * ld + (H - a.heads) * hd + i] = f32_to_f16(val);
+    } else {
+        a.v_cache[(size_t)r * ld + (H - a.heads - a.kv_heads) * hd + i] = own16;
+    }
+}
+
+// The sum of each thread's f32 partial over the workgroup (MF_WAVES waves):
+// a wave reduction, then the waves' sums in wave order (every thread gets the
+// same bits). part: MF_WAVES floats of LDS, free on entry and on return.
+__device__ __forceinline__ float wg_sum(float v, float *part) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < MF_WAVES; w++) tot = tot + part[w];
+    __syncthreads();
+    return tot;
+}
+
+// One row per workgroup of nn::layer_norm (LAYER: mean, then the variance
+// about it, two passes in f32; out = (v - mean) * r * w + b, nn.rs:133-143) or
+// nn::rms_norm (mean 0, no bias), r = 1 / sqrt(var + eps), into f16. The sums
+// run in another order than lane_sum's, so the f16 outputs agree with the
+// portable path's within an f16 rounding.
+template <bool LAYER>
+__global__ void __launch_bounds__(MF_WAVES * 64) norm_rows(const float *x, const float *w, const float *b,
+                                                           uint32_t dim, float eps, uint16_t *y) {
+    __shared__ float part[MF_WAVES];
+    const float *xr = x + (size_t)blockIdx.x * dim;
+    float mean = 0.0f;
+    if constexpr (LAYER) {
+        float s = 0.0f;
+        for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) s = s + xr[i];
+        mean = wg_sum(s, part) / (float)dim;
+    }
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) {
+        const float d = xr[i] - mean;
+        ss = ss + d * d;
+    }
+    const float r = 1.0f / sqrtf(wg_sum(ss, part) / (float)dim + eps);
+    for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x)
+        y[(size_t)blockIdx.x * dim + i] = f32_to_f16((xr[i] - mean) * r * w[i] + (b ? b[i] : 0.0f));
 }
 
 // q (f32) to the rounded query attention_kv_f16 scores with: f16(q * scale).
@@ -599,25 +684,53 @@ hipError_t launch_blk_gemv(const WDev &w, size_t m, const uint16_t *lhs, const B
 
 size_t attn_splits(size_t len) { return (len + AT_KPS - 1) / AT_KPS; }
 
+size_t attn_partial_floats(size_t rows, size_t last_len, size_t heads, size_t hd) {
+    return std::max<size_t>(rows, 1) * attn_splits(last_len) * heads * (hd + 2);
+}
+
 hipError_t launch_attention(const AttnArgs &a0, void *out, bool f16_out, hipStream_t s) {
     AttnArgs a = a0;
-    if (a.len == 0 || a.hd == 0 || a.hd > 256 || a.hd % 8 != 0 || a.group == 0) return hipErrorInvalidValue;
-    if ((size_t)a.len * a.ld * 2 >= ((size_t)1 << 31)) return hipErrorInvalidValue;
-    a.nsplit = (uint32_t)attn_splits(a.len);
+    if (a.rows == 0) a.rows = 1;
+    if (a.len == 0 || a.hd == 0 || a.hd > 256 || a.hd % 8 != 0 || a.group == 0 || a.rows > 65535)
+        return hipErrorInvalidValue;
+    const size_t last = (size_t)a.len + a.rows - 1;
+    if (last * a.ld * 2 >= ((size_t)1 << 31)) return hipErrorInvalidValue;
+    a.nsplit = (uint32_t)attn_splits(last);
     a.hchunks = (a.group + AT_HC - 1) / AT_HC;
-    const dim3 grid(a.nsplit, (a.heads / a.group) * a.hchunks);
+    const dim3 grid(a.nsplit, (a.heads / a.group) * a.hchunks, a.rows);
     if (a.hd <= 64) hipLaunchKernelGGL(attn_split<8>, grid, dim3(AT_T), 0, s, a);
     else if (a.hd <= 128) hipLaunchKernelGGL(attn_split<16>, grid, dim3(AT_T), 0, s, a);
     else hipLaunchKernelGGL(attn_split<32>, grid, dim3(AT_T), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const dim3 cgrid(a.heads, (a.hd + CM_D - 1) / CM_D);
+    const dim3 cgrid(a.heads, (a.hd + CM_D - 1) / CM_D, a.rows);
     if (f16_out)
-        hipLaunchKernelGGL(attn_combine<true>, cgrid, dim3(CM_T), 0, s, a.po, a.pml, a.nsplit, a.heads, a.hd,
-                           out);
+        hipLaunchKernelGGL(attn_combine<true>, cgrid, dim3(CM_T), 0, s, a.po, a.pml, a.nsplit, a.len, a.heads,
+                           a.hd, out);
     else
-        hipLaunchKernelGGL(attn_combine<false>, cgrid, dim3(CM_T), 0, s, a.po, a.pml, a.nsplit, a.heads, a.hd,
-                           out);
+        hipLaunchKernelGGL(attn_combine<false>, cgrid, dim3(CM_T), 0, s, a.po, a.pml, a.nsplit, a.len, a.heads,
+                           a.hd, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_qkv_rows(const QkvRowsArgs &a, hipStream_t s) {
+    const uint32_t n = (a.heads + 2 * a.kv_heads) * a.hd;
+    if (a.m == 0 || n == 0) return hipSuccess;
+    if (a.m > 65535 || a.hd % 16 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(qkv_rows, dim3((n + 255) / 256, a.m), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_norm_rows(const float *x, const float *w, const float *b, size_t rows, size_t dim, float eps,
+                            bool layer, uint16_t *y, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    if (rows > 0x7FFFFFFF || dim == 0) return hipErrorInvalidValue;
+    if (layer)
+        hipLaunchKernelGGL(norm_rows<true>, dim3((uint32_t)rows), dim3(MF_WAVES * 64), 0, s, x, w, b,
+                           (uint32_t)dim, eps, y);
+    else
+        hipLaunchKernelGGL(norm_rows<false>, dim3((uint32_t)rows), dim3(MF_WAVES * 64), 0, s, x, w, b,
+                           (uint32_t)dim, eps, y);
     return hipGetLastError();
 }
 

@@ -130,17 +130,41 @@ struct BlkArgs {
 hipError_t launch_blk_gemv(const WDev &w, size_t m, const uint16_t *lhs, const BlkArgs &a, int store,
                            bool norm, hipStream_t s);
 
-// Attention of one query row over an f16 cache, split over keys.
+// Attention of query rows over an f16 cache, split over keys. Row r (of
+// rows, 1 for a decode step) attends to keys 0 .. len + r - 1: the causal
+// prefix of a block of rows whose own keys are the cache's last rows.
 struct AttnArgs {
-    const uint16_t *q;       // [heads][hd] f16(q * scale)
-    const uint16_t *k, *v;   // [len][ld], KV head j at j*hd
-    float *po;               // partial sums [attn_splits(len)][heads][hd]
-    float2 *pml;             // partial (max, sum) [attn_splits(len)][heads]
-    uint32_t len, ld, hd, heads, group;  // group = heads / kv_heads
-    uint32_t nsplit, hchunks;            // set by launch_attention
+    const uint16_t *q;       // [rows][heads][hd] f16(q * scale)
+    const uint16_t *k, *v;   // [len + rows - 1][ld], KV head j at j*hd
+    float *po;               // partial sums [rows][nsplit][heads][hd]
+    float2 *pml;             // partial (max, sum) [rows][nsplit][heads]
+    uint32_t len, ld, hd, heads, group;  // len: row 0's keys; group = heads / kv_heads
+    uint32_t nsplit, hchunks;            // set by launch_attention (nsplit: the last row's)
+    uint32_t rows;                       // 0 is taken as 1
 };
 size_t attn_splits(size_t len);
+// Partial-sum bytes (po, then pml) launch_attention needs for `rows` rows whose
+// last attends to `last_len` keys.
+size_t attn_partial_floats(size_t rows, size_t last_len, size_t heads, size_t hd);
 hipError_t launch_attention(const AttnArgs &a, void *out, bool f16_out, hipStream_t s);
+// m rows of a qkv projection's f16 output (the device column order of the
+// fused QKV store) to attention inputs at positions pos0 .. pos0 + m - 1:
+// q and k rotated by NeoX RoPE (cs / sn: the table rows from position pos0,
+// half = hd / 2 a row; null: no RoPE), q16 = f16(q * scale), k into k_cache
+// and v into v_cache (the cache rows from pos0), as the fused store does.
+struct QkvRowsArgs {
+    const uint16_t *qkv;            // [m][(heads + 2 kv_heads) hd]
+    uint16_t *q_out;                // [m][heads][hd]
+    uint16_t *k_cache, *v_cache;    // [m][kv_heads hd]
+    const float *cs, *sn;
+    float scale;
+    uint32_t m, heads, kv_heads, hd;
+};
+hipError_t launch_qkv_rows(const QkvRowsArgs &a, hipStream_t s);
+// nn::layer_norm (bias may be null) or nn::rms_norm (layer = false) of f32 rows
+// into f16.
+hipError_t launch_norm_rows(const float *x, const float *w, const float *b, size_t rows, size_t dim, float eps,
+                            bool layer, uint16_t *y, hipStream_t s);
 hipError_t launch_round_q(const float *q, float scale, size_t count, uint16_t *qh, hipStream_t s);
 hipError_t launch_rms_norm(const float *x, const float *w, size_t rows, size_t dim, float eps, uint16_t *y,
                            hipStream_t s);

@@ -115,6 +115,9 @@ def lib() -> C.CDLL:
     L.smg_kv_cache_attend_dev.argtypes = [P, P, P, P]
     L.smg_attention_kv_f16_dev.argtypes = [P, P, P, SZ, SZ, SZ, SZ, C.c_float, P, P]
     L.smg_rms_norm_f16_dev.argtypes = [P, P, SZ, SZ, C.c_float, P, P]
+    L.smg_layer_norm_f16_dev.argtypes = [P, P, P, SZ, SZ, C.c_float, P, P]
+    L.smg_attention_kv_causal_f16_dev.argtypes = [P, P, P, SZ, SZ, SZ, SZ, SZ, C.c_float, P, P]
+    L.smg_kv_cache_attend_causal_dev.argtypes = [P, P, SZ, P, P]
     L.smg_glu_f16_dev.argtypes = [P, SZ, SZ, C.c_uint32, P, P]
     L.smg_q4_accumulate_dev.argtypes = [SZ, P, P, P, P]
     L.smg_attn_create.argtypes = [P, P, SZ, SZ, SZ, C.c_double, W]
@@ -126,6 +129,7 @@ def lib() -> C.CDLL:
     L.smg_mlp_destroy.restype = None
     L.smg_mlp_accumulate_dev.argtypes = [P, P, P, SZ, P]
     L.smg_block_create.argtypes = [P, C.c_float, P, C.c_float, SZ, P, P, W]
+    L.smg_block_create_norms.argtypes = [P, P, C.c_float, C.c_int, P, P, C.c_float, C.c_int, SZ, P, P, W]
     L.smg_block_destroy.argtypes = [P]
     L.smg_block_destroy.restype = None
     L.smg_block_accumulate_dev.argtypes = [P, P, P, SZ, P]
@@ -1352,10 +1356,23 @@ class KvCache:
         _check(lib().smg_kv_cache_attend_dev(self._h, q.data_ptr(), out.data_ptr(), _stream()), "attend")
         return out
 
+    def attend_causal(self, q, rows: int, out):
+        """KvCache::attend_causal (kv_attention.rs:560-578): `rows` query rows
+        that are the last `rows` cached positions, each attending to itself and
+        everything before it; q and out f32 rows * heads * head_dim."""
+        if rows > self.len():
+            raise ValueError(f"attend_causal: {rows} rows but {self.len()} cached")
+        _f32dev(q, rows * self.query_len(), "q", self._device)
+        _f32dev(out, rows * self.query_len(), "out", self._device)
+        _check(lib().smg_kv_cache_attend_causal_dev(self._h, q.data_ptr(), rows, out.data_ptr(), _stream()),
+               "attend_causal")
+        return out
+
 
 class SelfAttention:
-    """y += out(attention(qkv(x))) over a KvCache (src/self_attention.rs:69-183),
-    at one row. rope_theta > 0 adds the NeoX rotary embedding to q and k as
+    """y += out(attention(qkv(x))) over a KvCache (src/self_attention.rs:69-240),
+    for m rows (m > 1 attends causally). rope_theta > 0 adds the NeoX rotary
+    embedding to q and k as
     examples/bonsai/model.rs:30-99 does (not part of the library's
     SelfAttention). Takes over its two layers."""
 
@@ -1393,7 +1410,8 @@ class SelfAttention:
         return KvCache(self._heads, self._kv_heads, self._hd, capacity)
 
     def accumulate(self, x, cache: KvCache, y, m: int):
-        """SelfAttention::accumulate (self_attention.rs:148-183) for m = 1."""
+        """SelfAttention::accumulate (self_attention.rs:148-183): m rows at the
+        cache's next m positions (attend_rows, :192-240, for m > 1)."""
         _dev16(x, m * self._width, "x (m*width)", self._device, False)
         _f32dev(y, m * self._out_width, "y (m*out.n)", self._device)
         _check(lib().smg_attn_accumulate_dev(self._h, x.data_ptr(), cache._h, y.data_ptr(), m, _stream()),
@@ -1402,14 +1420,22 @@ class SelfAttention:
 
 
 class Norm:
-    """nn::Norm (src/nn.rs:164-235): RMSNorm on the GPU path (Norm::rms)."""
+    """nn::Norm (src/nn.rs:164-235): Norm::layer (GPT-2's LayerNorm, optional
+    bias) or Norm::rms (Llama's RMSNorm)."""
 
-    def __init__(self, weight, eps: float):
+    def __init__(self, weight, eps: float, bias=None, rms: bool = True):
         w = np.ascontiguousarray(np.asarray(weight, np.float32).ravel())
         if w.size == 0:
             raise ValueError("a norm needs at least one feature")
+        b = None
+        if bias is not None:
+            b = np.ascontiguousarray(np.asarray(bias, np.float32).ravel())
+            if b.size != w.size:
+                raise ValueError("bias holds weight.len() values")
         self.weight = w
+        self.bias = b
         self.eps = float(np.float32(eps))
+        self.rms_kind = rms
         self._dev = None
 
     @classmethod
@@ -1417,8 +1443,9 @@ class Norm:
         return cls(weight, eps)
 
     @classmethod
-    def layer(cls, weight, bias, eps):
-        raise SmeGemmError("Norm::layer is not on the GPU path (the decode block uses RMSNorm)")
+    def layer(cls, weight, bias, eps: float) -> "Norm":
+        """Norm::layer(weight, bias, eps) (src/nn.rs:187-198); bias may be None."""
+        return cls(weight, eps, bias, rms=False)
 
     def width(self) -> int:
         return self.weight.size
@@ -1427,8 +1454,11 @@ class Norm:
         """Norm::forward (src/nn.rs:227): f32 rows x to f16 y."""
         import torch
         if self._dev is None:
-            self._dev = torch.from_numpy(self.weight).cuda()
-        return rms_norm(x, self._dev, self.eps, y)
+            self._dev = (torch.from_numpy(self.weight).cuda(),
+                         None if self.bias is None else torch.from_numpy(self.bias).cuda())
+        if self.rms_kind:
+            return rms_norm(x, self._dev[0], self.eps, y)
+        return layer_norm(x, self._dev[0], self._dev[1], self.eps, y)
 
 
 class Block:
@@ -1442,8 +1472,10 @@ class Block:
                 and mlp.n() == d):
             raise ValueError("the norms, attention and MLP share the residual's width")
         h = C.c_void_p()
-        _check(lib().smg_block_create(norm1.weight.ctypes.data, norm1.eps, norm2.weight.ctypes.data, norm2.eps,
-                                      d, attn._h, mlp._h, C.byref(h)), "Block::new")
+        bp = lambda nm: None if nm.bias is None else nm.bias.ctypes.data  # noqa: E731
+        _check(lib().smg_block_create_norms(norm1.weight.ctypes.data, bp(norm1), norm1.eps, int(not norm1.rms_kind),
+                                            norm2.weight.ctypes.data, bp(norm2), norm2.eps, int(not norm2.rms_kind),
+                                            d, attn._h, mlp._h, C.byref(h)), "Block::new")
         attn._h = None
         mlp._h = None
         self._h = h
@@ -1464,7 +1496,9 @@ class Block:
         return KvCache(*self._attn_shape, capacity)
 
     def accumulate(self, x, cache: KvCache, rows: int):
-        """Block::accumulate (src/block.rs:90-106), rows = 1."""
+        """Block::accumulate (src/block.rs:90-106): rows rows of the f32
+        residual at the cache's next rows positions (causal attention among
+        them), which it appends."""
         _f32dev(x, rows * self._d, "x (rows*width)", self._device)
         _check(lib().smg_block_accumulate_dev(self._h, x.data_ptr(), cache._h, rows, _stream()),
                "Block::accumulate")
@@ -1483,6 +1517,48 @@ def rms_norm(x, weight, eps: float, y):
     _check(lib().smg_rms_norm_f16_dev(x.data_ptr(), weight.data_ptr(), x.numel() // dim, dim,
                                       float(np.float32(eps)), y.data_ptr(), _stream()), "rms_norm")
     return y
+
+
+def layer_norm(x, weight, bias, eps: float, y):
+    """nn::layer_norm (src/nn.rs:73-86): f32 rows of x to f16 y; weight (and
+    bias, or None) f32 device tensors."""
+    dim = weight.numel()
+    if dim == 0 or x.numel() % dim:
+        raise ValueError("x holds whole rows of weight.len()")
+    dev = x.device.index
+    _f32dev(x, None, "x", dev)
+    _f32dev(weight, dim, "weight", dev)
+    if bias is not None:
+        _f32dev(bias, dim, "bias", dev)
+    _dev16(y, x.numel(), "y", dev, False)
+    _check(lib().smg_layer_norm_f16_dev(x.data_ptr(), weight.data_ptr(), None if bias is None else bias.data_ptr(),
+                                        x.numel() // dim, dim, float(np.float32(eps)), y.data_ptr(), _stream()),
+           "layer_norm")
+    return y
+
+
+def attention_kv_causal_f16(q, k, v, start: int, rows: int, heads: int, kv_heads: int, head_dim: int,
+                            scale: float, out):
+    """attention_kv_causal_f16 (src/kernels/kv_attention.rs:140-240) on device
+    tensors: query row i attends to keys 0 .. start + i."""
+    if rows == 0:
+        raise ValueError("attention_kv_causal_f16 needs at least one query row")
+    if head_dim % 8 or not 8 <= head_dim <= 256:
+        raise ValueError("head_dim must be a multiple of 8 in 8..=256")
+    if kv_heads <= 0 or heads <= 0 or heads % kv_heads:
+        raise ValueError("heads must be a positive multiple of kv_heads")
+    ld = kv_heads * head_dim
+    dev = q.device.index
+    _f32dev(q, rows * heads * head_dim, "q", dev)
+    _f32dev(out, rows * heads * head_dim, "out", dev)
+    for t, name in ((k, "k"), (v, "v")):
+        _dev16(t, None, name, dev, False)
+        if t.numel() < (start + rows) * ld:
+            raise ValueError(f"{name} holds (start + rows) * kv_heads * head_dim")
+    _check(lib().smg_attention_kv_causal_f16_dev(q.data_ptr(), k.data_ptr(), v.data_ptr(), start, rows, heads,
+                                                 kv_heads, head_dim, float(np.float32(scale)), out.data_ptr(),
+                                                 _stream()), "attention_kv_causal_f16")
+    return out
 
 
 def glu(both, m: int, n: int, gate: int, y):

@@ -346,3 +346,197 @@ def test_interleaved_q4_is_gate_and_up_side_by_side():
     both = _q4_decode64(q, s, 2 * n, k)
     G, U = _q4_decode64(gq, gs, n, k), _q4_decode64(uq, us, n, k)
     assert np.array_equal(both, O.interleave32(G, U, n, k))
+
+
+# ---- LayerNorm, causal attention, blocks of rows ----------------------------------------
+
+def _ln64(x, w, b, eps):
+    x = np.asarray(x, np.float64)
+    mu = np.mean(x)
+    y = (x - mu) / np.sqrt(np.mean((x - mu) ** 2) + eps) * np.asarray(w, np.float64)
+    return y + (0.0 if b is None else np.asarray(b, np.float64))
+
+
+@pytest.mark.parametrize("dim,bias", [(4, False), (8, True), (100, True), (384, False), (4099, True)])
+def test_layer_norm_matches_f64(dim, bias):
+    """norm_row's LayerNorm form (src/nn.rs:133-143: two lane_sum passes in
+    f32) against an f64 two-pass LayerNorm: within 1e-4 and 16 f32 ulps (the
+    f32 mean's rounding enters every centred value)."""
+    rng = np.random.default_rng(dim)
+    x = (rng.standard_normal(dim) * 3 + 0.7).astype(np.float32)
+    w = rng.uniform(0.9, 1.1, dim).astype(np.float32)
+    b = rng.normal(0, 0.1, dim).astype(np.float32) if bias else None
+    got = O.layer_norm_row(x, w, b, 1e-5)
+    want = _ln64(x, w, b, 1e-5)
+    assert np.max(np.abs(got - want)) < 1e-4
+    assert np.all(np.abs(got - want) <= 16 * np.spacing(np.abs(want).astype(np.float32)) + 1e-6)
+
+
+def test_layer_norm_doc_example_and_closed_forms():
+    """nn::layer_norm's own doc example (src/nn.rs:64-68: x = 1, 2, 3, 4, unit
+    weights, eps 1e-5): mean 2.5, variance 1.25, so (x - 2.5) / sqrt(1.25001);
+    a constant row gives the bias (zero centred values); f16 output is the f32
+    row rounded once."""
+    x = np.array([1, 2, 3, 4], np.float32)
+    got = O.layer_norm_row(x, np.ones(4, np.float32), None, 1e-5)
+    want = (x.astype(np.float64) - 2.5) / np.sqrt(1.25 + 1e-5)
+    assert np.all(_ulps32(got, want.astype(np.float32)) <= 2)
+    b = np.linspace(-1, 1, 96).astype(np.float32)
+    const = O.layer_norm_row(np.full(96, 7.25, np.float32), np.ones(96, np.float32), b, 1e-5)
+    assert np.array_equal(const, b)
+    xs = np.random.default_rng(2).standard_normal(2 * 96).astype(np.float32)
+    w = np.linspace(0.5, 1.5, 96).astype(np.float32)
+    y = O.layer_norm_f16(xs, w, b, 1e-5, rows=2)
+    for r in range(2):
+        assert np.array_equal(y[r * 96:(r + 1) * 96], O.f32_to_f16(O.layer_norm_row(xs[r * 96:(r + 1) * 96], w, b,
+                                                                                    1e-5)))
+
+
+def test_layer_norm_planted_mistakes_exceed_the_bound():
+    """The f64 bound would catch a missing centring (RMS in place of the
+    variance), a dim - 1 divisor and a dropped bias."""
+    dim = 384
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(dim) * 0.5 + 1.0).astype(np.float32)
+    w = np.ones(dim, np.float32)
+    b = rng.normal(0, 0.1, dim).astype(np.float32)
+    good = O.layer_norm_row(x, w, b, 1e-5)
+    assert np.max(np.abs(good - _ln64(x, w, b, 1e-5))) < 1e-4
+    x64 = x.astype(np.float64)
+    mu = x64.mean()
+    uncentred = (x64 - mu) / np.sqrt(np.mean(x64 ** 2) + 1e-5) + b
+    wrong_div = (x64 - mu) / np.sqrt(np.sum((x64 - mu) ** 2) / (dim - 1) + 1e-5) + b
+    no_bias = _ln64(x, w, None, 1e-5)
+    for bad in (uncentred, wrong_div, no_bias):
+        assert np.max(np.abs(good - bad)) > 1e-3
+
+
+def _causal64(q, k, v, start, rows, heads, kv_heads, hd, scale):
+    ld = kv_heads * hd
+    K = O.f16_to_f32(k).astype(np.float64).reshape(-1, ld)
+    V = O.f16_to_f32(v).astype(np.float64).reshape(-1, ld)
+    g = heads // kv_heads
+    out = np.zeros((rows, heads * hd))
+    for i in range(rows):
+        n = start + i + 1
+        for h in range(heads):
+            off = (h // g) * hd
+            # q rounded as one_row rounds it (f16(q * scale), kv_attention.rs:298-302)
+            qh = O.f16_to_f32(O.f32_to_f16(q[i * heads * hd + h * hd:i * heads * hd + (h + 1) * hd] * scale))
+            s = K[:n, off:off + hd] @ qh.astype(np.float64)
+            e = np.exp(s - s.max())
+            out[i, h * hd:(h + 1) * hd] = (e / e.sum()) @ V[:n, off:off + hd]
+    return out.ravel()
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd,start,rows", [(4, 2, 64, 0, 5), (6, 6, 64, 10, 7), (8, 1, 32, 3, 12)])
+def test_causal_attention_matches_f64(heads, kv_heads, hd, start, rows):
+    """attention_kv_causal_f16's portable path (kv_attention.rs:214-238):
+    against an f64 masked softmax (row i sees keys 0 .. start + i; q rounded
+    to f16 after the scale, as one_row rounds it) within 2e-4, and with a
+    planted off-by-one in the mask (row i seeing start + i keys, or
+    start + i + 2) failing that bound by far."""
+    rng = np.random.default_rng(heads + start + rows)
+    ld = kv_heads * hd
+    q = (rng.standard_normal(rows * heads * hd) * 4).astype(np.float32)
+    k = O.f32_to_f16(rng.standard_normal((start + rows + 1) * ld).astype(np.float32))
+    v = O.f32_to_f16(rng.standard_normal((start + rows + 1) * ld).astype(np.float32))
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    got = O.attention_kv_causal_f16(q, k, v, start, rows, heads, kv_heads, hd, scale)
+    want = _causal64(q, k, v, start, rows, heads, kv_heads, hd, scale)
+    assert np.max(np.abs(got - want)) < 2e-4
+    short = _causal64(q, k, v, start - 1, rows, heads, kv_heads, hd, scale) if start > 0 else None
+    long = _causal64(q, k, v, start + 1, rows, heads, kv_heads, hd, scale)
+    for bad in (short, long):
+        if bad is not None:
+            assert np.max(np.abs(got - bad)) > 1e-2
+
+
+def test_block_rows_match_an_f64_block_row_by_row():
+    """block_rows (src/block.rs:90-106 for many rows): against the f64 block
+    applied row by row with each row's own key and value appended in f64 --
+    the whole block of rows agrees to the f16 roundings' size -- and a block
+    of rows whose attention skipped the rows' own keys (every row seeing only
+    the cached prefix) fails that bound."""
+    p, x, ck, cv = small_block(31)
+    rows, pos = 4, 37
+    rng = np.random.default_rng(32)
+    xs = rng.standard_normal((rows, p["d"])).astype(np.float32)
+    cap = pos + rows + 1
+    ck2 = np.zeros((cap, ck.shape[1]), np.uint16)
+    cv2 = np.zeros_like(ck2)
+    ck2[:pos], cv2[:pos] = ck[:pos], cv[:pos]
+    got = O.block_rows(xs.ravel(), ck2, cv2, pos, rows, p).reshape(rows, -1)
+    K64, V64 = ck2.copy(), cv2.copy()
+    for r in range(rows):
+        want = _block64(p, xs[r], K64, V64, pos + r)
+        upd_g, upd_w = got[r].astype(np.float64) - xs[r], want - xs[r]
+        assert np.linalg.norm(upd_g - upd_w) <= 1e-2 * np.linalg.norm(upd_w), r
+    # the cache rows written are exactly the one-row steps' (row order kept)
+    ck3, cv3 = ck2.copy(), cv2.copy()
+    ck3[pos:], cv3[pos:] = 0, 0
+    for r in range(rows):
+        O.block_decode(xs[r], ck3, cv3, pos + r, p)
+    assert np.array_equal(ck3, ck2) and np.array_equal(cv3, cv2)
+    # planted: row 3 attending as if rows 0-2 had not been appended
+    ck4, cv4 = ck2.copy(), cv2.copy()
+    ck4[pos:pos + 3] = ck4[pos + 3]
+    cv4[pos:pos + 3] = cv4[pos + 3]
+    bad = O.block_decode(xs[3], np.delete(ck4, [pos, pos + 1, pos + 2], 0), np.delete(cv4, [pos, pos + 1, pos + 2], 0),
+                         pos, p)
+    assert np.linalg.norm(bad - got[3]) > 1e-2 * np.linalg.norm(got[3].astype(np.float64) - xs[3])
+
+
+def _gpt2_64(p, raw, x, K, V, pos):
+    """A GPT-2-style step in f64 from its own Q4 decoding: LayerNorm (with
+    bias), multi-head attention without RoPE, up -> tanh-gelu -> down."""
+    d, H, hd, eps = p["d"], p["heads"], p["head_dim"], p["eps"]
+    W = {name: _q4_decode64(q[0], q[1], n, k) for name, (q, n, k) in raw.items()}
+    x = x.astype(np.float64)
+    h = _ln64(x, p["norm1"], p["bias1"], eps)
+    qkv = h @ W["qkv"]
+    ql = H * hd
+    q, k, v = qkv[:ql], qkv[ql:2 * ql], qkv[2 * ql:]
+    Kf = np.vstack([O.f16_to_f32(K[:pos]).astype(np.float64).reshape(pos, ql), k])
+    Vf = np.vstack([O.f16_to_f32(V[:pos]).astype(np.float64).reshape(pos, ql), v])
+    att = np.zeros(ql)
+    for hh in range(H):
+        s = Kf[:, hh * hd:(hh + 1) * hd] @ q[hh * hd:(hh + 1) * hd] / np.sqrt(hd)
+        e = np.exp(s - s.max())
+        att[hh * hd:(hh + 1) * hd] = (e / e.sum()) @ Vf[:, hh * hd:(hh + 1) * hd]
+    x = x + att @ W["out"]
+    h = _ln64(x, p["norm2"], p["bias2"], eps)
+    u = h @ W["up"]
+    g = 0.5 * u * (1 + np.tanh(0.7978845608028654 * (u + 0.044715 * u ** 3)))
+    return x + g @ W["down"]
+
+
+def test_gpt2_style_block_step_matches_f64():
+    """The oracle's one-row step with Norm::layer norms and Mlp::new(up, gelu,
+    down), no RoPE, heads = kv_heads (examples/shakespeare/model.rs:91-112)
+    against the f64 step: the update to the f16 roundings' size."""
+    rng = np.random.default_rng(51)
+    d, H, hd, ffn, pos = 128, 4, 32, 256, 9
+
+    def q4(n, k):
+        return (rng.integers(0, 256, (k * n + 1) // 2, dtype=np.uint8),
+                O.f32_to_f16(rng.uniform(0.005, 0.02, n * (k // 32)).astype(np.float32)))
+    raw = {"qkv": (q4(3 * H * hd, d), 3 * H * hd, d), "out": (q4(d, H * hd), d, H * hd),
+           "up": (q4(ffn, d), ffn, d), "down": (q4(d, ffn), d, ffn)}
+    p = dict(d=d, heads=H, kv_heads=H, head_dim=hd, ffn=ffn, eps=1e-5, theta=0.0, norm="layer", act=2,
+             norm1=rng.uniform(0.9, 1.1, d).astype(np.float32), norm2=rng.uniform(0.9, 1.1, d).astype(np.float32),
+             bias1=rng.normal(0, 0.1, d).astype(np.float32), bias2=rng.normal(0, 0.1, d).astype(np.float32))
+    for name, (q, n, k) in raw.items():
+        p[name] = O.Q4Lin(*q, n, k)
+    K = np.zeros((pos + 1, H * hd), np.uint16)
+    V = np.zeros_like(K)
+    K[:pos] = O.f32_to_f16(rng.standard_normal(pos * H * hd).astype(np.float32)).reshape(pos, -1)
+    V[:pos] = O.f32_to_f16(rng.standard_normal(pos * H * hd).astype(np.float32)).reshape(pos, -1)
+    x = rng.standard_normal(d).astype(np.float32)
+    got = O.block_decode(x, K.copy(), V.copy(), pos, p)
+    want = _gpt2_64(p, raw, x, K, V, pos)
+    assert np.linalg.norm(got - want) <= 1e-2 * np.linalg.norm(want - x)
+    # a silu in place of the gelu, or an RMS norm in place of the LayerNorm, fails it
+    for bad_p in (dict(p, act=3), dict(p, norm="rms")):
+        bad = O.block_decode(x, K.copy(), V.copy(), pos, bad_p)
+        assert np.linalg.norm(bad - want) > 1e-2 * np.linalg.norm(want - x)
