@@ -57,7 +57,7 @@ MALL_BYTES = 256 << 20
 FLUSH_BYTES = 1 << 30
 MIN_CALLS = 256  # calls per timed graph outside the headline (the graph's fixed start amortized)
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemv_mfma_config1_traffic.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemv_wave_config1_traffic.md")
 
 
 def committed_traffic():
@@ -399,13 +399,21 @@ def main():
         tb = torch.randn(k4, n4, dtype=torch.float16, device=dev)
         tc = torch.empty(m4, n4, dtype=torch.float16, device=dev)
         us_t = timer([lambda: torch.matmul(ta, tb, out=tc)], steps, 3, flush=False)
+        # the same call with bf16 activations, scales and output (matmul_q4_bf16_ep)
+        a4b = a4d.view(torch.float16).float().to(torch.bfloat16)
+        s4b, b4b = (t.view(torch.float16).float().to(torch.bfloat16) for t in (s4d, b4d))
+        c4b = torch.empty(m4 * n4, dtype=torch.bfloat16, device=dev)
+        ep4b = smg.Epilogue(bf16=True).mul_col(s4b).add_col(b4b).silu()
+        us_b = timer([lambda: smg.matmul_q4_bf16_ep(a4b, w4, c4b, m4, ep4b)], steps, 3, flush=False)
         props = torch.cuda.get_device_properties(0)
         extra["config4_q4_gemm"] = {
             "flops": flops, "us": us, "TFLOPS": tf, "frac_f16_mfma": tf / F16_MFMA_PEAK_TFLOPS,
             "shader_clock_mhz_after": mhz,
             "shader_clock_mhz_max": getattr(props, "clock_rate", 0) / 1000.0 or None,
-            "torch_dense_f16_gemm": {"us": us_t, "TFLOPS": flops / (us_t * 1e-6) / 1e12}}
-        del ta, tb, tc
+            "torch_dense_f16_gemm": {"us": us_t, "TFLOPS": flops / (us_t * 1e-6) / 1e12},
+            "bf16": {"us": us_b, "TFLOPS": flops / (us_b * 1e-6) / 1e12,
+                     "frac_bf16_mfma": flops / (us_b * 1e-6) / 1e12 / F16_MFMA_PEAK_TFLOPS}}
+        del ta, tb, tc, a4b, c4b
     if "5" in only:
         extra["config5_decode_block"] = bench_block(smg, torch, timer, workloads, steps, warm, to_dev)
         # each stage's bytes as one plain read (the floor a separate launch of
@@ -470,6 +478,8 @@ def bench_block(smg, torch, timer, workloads, steps, warm, to_dev):
         blk = smg.Block(smg.Norm.rms(inp["norm1"], c["eps"]), attn, smg.Norm.rms(inp["norm2"], c["eps"]), mlp)
         cache = blk.cache(past + 8)  # every step appends at position `past`
         cache.extend(to_dev(inp["cache_k"][:past]), to_dev(inp["cache_v"][:past]))
+        if i == 0:
+            kv0 = (to_dev(inp["cache_k"][:past]), to_dev(inp["cache_v"][:past]))
         blocks.append(blk)
         caches.append(cache)
         xs.append(torch.from_numpy(inp["x"]).cuda())
@@ -484,12 +494,31 @@ def bench_block(smg, torch, timer, workloads, steps, warm, to_dev):
     us_hot = timer(calls[:1], steps, warm, flush=False)
     nbytes = workloads.block_bytes(d, H, KV, hd, ffn, past + 1)
     tok_s = 1e6 / us
+    # prefill: 512 rows in one Block::accumulate (causal among them) after the
+    # 4096 cached positions, block copy 0 (its cache holds past + 520 rows)
+    rows = 512
+    pc = blocks[0].cache(past + rows + 8)
+    pc.extend(*kv0)
+    xp = torch.from_numpy(np.random.default_rng(5).standard_normal(rows * d).astype(np.float32)).cuda()
+
+    def prefill():
+        pc.truncate(past)
+        blocks[0].accumulate(xp, pc, rows)
+    us_pre = timer([prefill], max(1, steps // 4), 2, flush=False, min_calls=1)
+    # FLOPs of the prefill's projections (2 per weight per row) and causal attention
+    # (QK and PV: 4 * heads * head_dim per (row, key) pair)
+    proj = 2.0 * rows * (d * (H + 2 * KV) * hd + H * hd * d + 3 * ffn * d)
+    att = 4.0 * H * hd * sum(past + r + 1 for r in range(rows))
     return {"workload": "Block::accumulate, 1 row, d=4096, 32/8 heads x 128, SwiGLU 14336, "
                         "4096 cached positions, RoPE theta 10000, Q4 block 32; 4 block copies",
             "bytes_per_token": nbytes, "us_per_token": us, "tokens_per_s": tok_s,
             "us_per_token_hot_mall": us_hot, "GBps": nbytes / (us * 1e-6) / 1e9,
             "roofline_tokens_per_s": HBM_PEAK_GBS * 1e9 / nbytes,
-            "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "launches_per_token": 6}
+            "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "launches_per_token": 6,
+            "prefill_512_rows": {"us": us_pre, "tokens_per_s": rows / (us_pre * 1e-6),
+                                 "TFLOPS": (proj + att) / (us_pre * 1e-6) / 1e12,
+                                 "workload": "one Block::accumulate of 512 rows after 4096 cached positions "
+                                             "(weights and cache MALL-warm: the same call replayed)"}}
 
 
 def bench_mlp(smg, torch, timer, workloads, steps, warm):
