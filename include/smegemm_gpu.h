@@ -446,6 +446,41 @@ void smg_block_destroy(smg_block *b);
  * its add, then the MLP half over all rows. */
 int smg_block_accumulate_dev(smg_block *b, float *x, smg_kv_cache *cache, size_t rows, void *stream);
 
+/* ---- host-slice forms of the model parts ------------------------------------
+ * The reference's model parts take host slices (&[X] / &mut [f32]). Each entry
+ * below is the synchronous host-memory twin of the *_dev entry of the same
+ * name: the same arguments without the stream, every array in host memory,
+ * staged through the calling thread's device buffer and stream. It returns
+ * once its outputs are in host memory, and leaves them untouched when it
+ * fails (the caches and handles it names are updated as by the device form).
+ * Weight handles, caches and blocks stay on their device; the free functions
+ * run on the current device. An f32 caller rounds x to f16 first, as the
+ * reference's ModelFloat::as_f16 does (src/linear.rs:23-78). */
+/* Linear::accumulate (src/linear.rs:425-432). */
+int smg_q4_accumulate(size_t m, const smg_weights *w, float *y, const uint16_t *x);
+/* SelfAttention::accumulate (src/self_attention.rs:148-183). */
+int smg_attn_accumulate(smg_attn *a, const uint16_t *x, smg_kv_cache *cache, float *y, size_t m);
+/* Mlp::accumulate (src/mlp.rs:113-149). */
+int smg_mlp_accumulate(smg_mlp *m, const uint16_t *x, float *y, size_t rows);
+/* Block::accumulate (src/block.rs:90-106): x f32 rows x d, updated in place. */
+int smg_block_accumulate(smg_block *b, float *x, smg_kv_cache *cache, size_t rows);
+/* KvCache::extend (kv_attention.rs:499-519). */
+int smg_kv_cache_extend(smg_kv_cache *c, const uint16_t *k, const uint16_t *v, size_t rows);
+/* keys() / values() (kv_attention.rs:522-531): len rows each, either NULL. */
+int smg_kv_cache_read(const smg_kv_cache *c, uint16_t *keys, uint16_t *values);
+/* KvCache::attend / attend_causal (kv_attention.rs:537-578). */
+int smg_kv_cache_attend(const smg_kv_cache *c, const float *q, float *out);
+int smg_kv_cache_attend_causal(const smg_kv_cache *c, const float *q, size_t rows, float *out);
+/* attention_kv_f16 / attention_kv_causal_f16 (kv_attention.rs:29-78,140-240). */
+int smg_attention_kv_f16(const float *q, const uint16_t *k, const uint16_t *v, size_t len, size_t heads,
+                         size_t kv_heads, size_t head_dim, float scale, float *out);
+int smg_attention_kv_causal_f16(const float *q, const uint16_t *k, const uint16_t *v, size_t start, size_t rows,
+                                size_t heads, size_t kv_heads, size_t head_dim, float scale, float *out);
+/* nn::rms_norm / nn::layer_norm (src/nn.rs:73-86,133-161). */
+int smg_rms_norm_f16(const float *x, const float *weight, size_t rows, size_t dim, float eps, uint16_t *y);
+int smg_layer_norm_f16(const float *x, const float *weight, const float *bias, size_t rows, size_t dim, float eps,
+                       uint16_t *y);
+
 /* ---- measurement probes (not part of the matmul path) ----------------------- */
 /* One plain pass of 16-byte loads over `bytes` (a multiple of 16) of device
  * memory, writing nothing: the time floor that a single launch reading that

@@ -502,6 +502,51 @@ int host_call(const char *name, int device, size_t m, size_t n, size_t k, uint16
     return SMG_OK;
 }
 
+// ---- one host-slice call of a model part -----------------------------------------
+// A host array of a model part's call: `in` is copied to the device before
+// the part runs, `out` back after it finished without error.
+struct Slice {
+    void *host;
+    size_t bytes;
+    bool in, out;
+};
+
+// n * elems * width bytes, or false when the product overflows.
+bool slice_bytes(size_t n, size_t elems, size_t width, size_t *out) {
+    size_t t;
+    return !__builtin_mul_overflow(n, elems, &t) && !__builtin_mul_overflow(t, width, out);
+}
+
+// Stages the slices in the thread's staging buffer, runs `run(dev, stream)`
+// (the part's device form over the staged pointers, null where the host one
+// is null) on the thread's stream, waits, and copies the written slices back
+// only when it succeeded: on an error they are untouched.
+template <size_t N, class Run>
+int slice_call(int device, Slice (&s)[N], Run run) {
+    size_t total = 256;
+    for (const Slice &x : s) total += round_up(x.bytes, 256);
+    Ctx *c;
+    int rc = ctx_for(device, total, &c);
+    if (rc) return rc;
+    void *d[N];
+    uint8_t *p = (uint8_t *)c->buf;
+    for (size_t i = 0; i < N; i++) {
+        d[i] = s[i].host ? p : nullptr;
+        if (s[i].host && s[i].in && s[i].bytes)
+            HIP_TRY(hipMemcpyAsync(p, s[i].host, s[i].bytes, hipMemcpyHostToDevice, c->stream), SMG_EHIP);
+        p += round_up(s[i].bytes, 256);
+    }
+    rc = run(d, (void *)c->stream);
+    const hipError_t e = hipStreamSynchronize(c->stream);
+    if (rc) return rc;
+    if (e != hipSuccess) return fail(SMG_EHIP, "hipStreamSynchronize", e);
+    for (size_t i = 0; i < N; i++)
+        if (s[i].host && s[i].out && s[i].bytes)
+            HIP_TRY(hipMemcpyAsync(s[i].host, d[i], s[i].bytes, hipMemcpyDeviceToHost, c->stream), SMG_EHIP);
+    HIP_TRY(hipStreamSynchronize(c->stream), SMG_EHIP);
+    return SMG_OK;
+}
+
 int check_kind(const smg_weights *w, int kind) {
     if (!w) return fail(SMG_EINVAL, "null weights");
     if (w->d.kind != kind) return fail(SMG_EKIND, "weight handle of another kind");
@@ -1990,6 +2035,181 @@ int smg_block_accumulate_dev(smg_block *b, float *x, smg_kv_cache *cache, size_t
     if (rc) return rc;
     return mlp_step(b->mlp, nullptr, x, b->norm2, b->eps2, x, rows, stream, b->layer2, b->bias2);
 }
+
+// ---- host-slice forms ---------------------------------------------------------------
+// Synchronous twins of the device forms above over host arrays, as the
+// reference's model parts take them: each returns once its outputs are in
+// host memory, and leaves them untouched when it fails.
+
+#define SLICE_BYTES(var, n, elems, width)                                        \
+    size_t var;                                                                  \
+    if (!slice_bytes((n), (elems), (width), &var)) return fail(SMG_EINVAL, "array size overflows")
+
+int smg_q4_accumulate(size_t m, const smg_weights *w, float *y, const uint16_t *x) {
+    int rc = check_kind(w, W_Q4);
+    if (rc) return rc;
+    if (m == 0 || w->d.n == 0) return SMG_OK;
+    if (!x || !y) return fail(SMG_EINVAL, "null array");
+    SLICE_BYTES(xb, m, w->d.k, 2);
+    SLICE_BYTES(yb, m, w->d.n, 4);
+    Slice s[] = {{(void *)x, xb, true, false}, {y, yb, true, true}};
+    return slice_call(w->device, s, [&](void **d, void *st) {
+        return smg_q4_accumulate_dev(m, w, (float *)d[1], (const uint16_t *)d[0], st);
+    });
+}
+
+int smg_attn_accumulate(smg_attn *a, const uint16_t *x, smg_kv_cache *cache, float *y, size_t m) {
+    if (!a) return fail(SMG_EINVAL, "null attention");
+    if (m == 0) return SMG_OK;
+    if (!x || !y) return fail(SMG_EINVAL, "null array");
+    if (m > 65535) return fail(SMG_EINVAL, "at most 65535 rows a call");
+    int rc = check_cache(a, cache, m);
+    if (rc) return rc;
+    SLICE_BYTES(xb, m, a->qkv->d.k, 2);
+    SLICE_BYTES(yb, m, a->out->d.n, 4);
+    Slice s[] = {{(void *)x, xb, true, false}, {y, yb, true, true}};
+    return slice_call(a->device, s, [&](void **d, void *st) {
+        return smg_attn_accumulate_dev(a, (const uint16_t *)d[0], cache, (float *)d[1], m, st);
+    });
+}
+
+int smg_mlp_accumulate(smg_mlp *m, const uint16_t *x, float *y, size_t rows) {
+    if (!m) return fail(SMG_EINVAL, "null mlp");
+    if (rows == 0) return SMG_OK;
+    if (!x || !y) return fail(SMG_EINVAL, "null array");
+    SLICE_BYTES(xb, rows, m->up->d.k, 2);
+    SLICE_BYTES(yb, rows, m->down->d.n, 4);
+    Slice s[] = {{(void *)x, xb, true, false}, {y, yb, true, true}};
+    return slice_call(m->device, s, [&](void **d, void *st) {
+        return smg_mlp_accumulate_dev(m, (const uint16_t *)d[0], (float *)d[1], rows, st);
+    });
+}
+
+int smg_block_accumulate(smg_block *b, float *x, smg_kv_cache *cache, size_t rows) {
+    if (!b) return fail(SMG_EINVAL, "null block");
+    if (rows == 0) return SMG_OK;
+    if (!x) return fail(SMG_EINVAL, "null array");
+    if (rows > 65535) return fail(SMG_EINVAL, "at most 65535 rows a call");
+    int rc = check_cache(b->attn, cache, rows);
+    if (rc) return rc;
+    SLICE_BYTES(xb, rows, b->d, 4);
+    Slice s[] = {{x, xb, true, true}};
+    return slice_call(b->device, s, [&](void **d, void *st) {
+        return smg_block_accumulate_dev(b, (float *)d[0], cache, rows, st);
+    });
+}
+
+int smg_kv_cache_extend(smg_kv_cache *c, const uint16_t *k, const uint16_t *v, size_t rows) {
+    if (!c) return fail(SMG_EINVAL, "null cache");
+    if (rows == 0 || !k || !v)
+        return fail(SMG_EINVAL, "k and v hold the same whole number of kv_heads * head_dim rows");
+    if (rows > c->cap - c->len) return fail(SMG_EINVAL, "KvCache full: the rows do not fit in the cache");
+    SLICE_BYTES(kb, rows, c->kv_heads * c->hd, 2);
+    Slice s[] = {{(void *)k, kb, true, false}, {(void *)v, kb, true, false}};
+    return slice_call(c->device, s, [&](void **d, void *st) {
+        return smg_kv_cache_extend_dev(c, (const uint16_t *)d[0], (const uint16_t *)d[1], rows, st);
+    });
+}
+
+int smg_kv_cache_read(const smg_kv_cache *c, uint16_t *keys, uint16_t *values) {
+    if (!c) return fail(SMG_EINVAL, "null cache");
+    const size_t bytes = c->len * c->kv_heads * c->hd * 2;
+    if (bytes == 0) return SMG_OK;
+    Slice s[] = {{keys, bytes, false, true}, {values, bytes, false, true}};
+    return slice_call(c->device, s, [&](void **d, void *st) {
+        return smg_kv_cache_read_dev(c, (uint16_t *)d[0], (uint16_t *)d[1], st);
+    });
+}
+
+int smg_kv_cache_attend(const smg_kv_cache *c, const float *q, float *out) {
+    if (!c) return fail(SMG_EINVAL, "null cache");
+    if (!q || !out) return fail(SMG_EINVAL, "null array");
+    const size_t qb = c->heads * c->hd * 4;
+    Slice s[] = {{(void *)q, qb, true, false}, {out, qb, false, true}};
+    return slice_call(c->device, s, [&](void **d, void *st) {
+        return smg_kv_cache_attend_dev(c, (const float *)d[0], (float *)d[1], st);
+    });
+}
+
+int smg_kv_cache_attend_causal(const smg_kv_cache *c, const float *q, size_t rows, float *out) {
+    if (!c) return fail(SMG_EINVAL, "null cache");
+    if (rows == 0) return fail(SMG_EINVAL, "attention_kv_causal_f16 needs at least one query row");
+    if (rows > c->len) return fail(SMG_EINVAL, "attend_causal: more rows than cached positions");
+    if (!q || !out) return fail(SMG_EINVAL, "null array");
+    const size_t qb = rows * c->heads * c->hd * 4;
+    Slice s[] = {{(void *)q, qb, true, false}, {out, qb, false, true}};
+    return slice_call(c->device, s, [&](void **d, void *st) {
+        return smg_kv_cache_attend_causal_dev(c, (const float *)d[0], rows, (float *)d[1], st);
+    });
+}
+
+int smg_attention_kv_f16(const float *q, const uint16_t *k, const uint16_t *v, size_t len, size_t heads,
+                         size_t kv_heads, size_t head_dim, float scale, float *out) {
+    if (!head_shape_ok(heads, kv_heads, head_dim))
+        return fail(SMG_EINVAL, "head_dim must be a multiple of 8 in 8..=256 and heads a positive multiple of kv_heads");
+    if (len == 0) return fail(SMG_EINVAL, "attention_kv_f16 needs at least one cached key");
+    if (!q || !k || !v || !out) return fail(SMG_EINVAL, "null array");
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev), SMG_EHIP);
+    SLICE_BYTES(kb, len, kv_heads * head_dim, 2);
+    const size_t qb = heads * head_dim * 4;
+    Slice s[] = {{(void *)q, qb, true, false}, {(void *)k, kb, true, false}, {(void *)v, kb, true, false},
+                 {out, qb, false, true}};
+    return slice_call(dev, s, [&](void **d, void *st) {
+        return smg_attention_kv_f16_dev((const float *)d[0], (const uint16_t *)d[1], (const uint16_t *)d[2], len,
+                                        heads, kv_heads, head_dim, scale, (float *)d[3], st);
+    });
+}
+
+int smg_attention_kv_causal_f16(const float *q, const uint16_t *k, const uint16_t *v, size_t start, size_t rows,
+                                size_t heads, size_t kv_heads, size_t head_dim, float scale, float *out) {
+    if (rows == 0) return fail(SMG_EINVAL, "attention_kv_causal_f16 needs at least one query row");
+    if (!head_shape_ok(heads, kv_heads, head_dim))
+        return fail(SMG_EINVAL, "head_dim must be a multiple of 8 in 8..=256 and heads a positive multiple of kv_heads");
+    if (start > ((size_t)1 << 31) || rows > ((size_t)1 << 31)) return fail(SMG_EINVAL, "start + rows overflows");
+    if (!q || !k || !v || !out) return fail(SMG_EINVAL, "null array");
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev), SMG_EHIP);
+    SLICE_BYTES(kb, start + rows, kv_heads * head_dim, 2);
+    SLICE_BYTES(qb, rows, heads * head_dim, 4);
+    Slice s[] = {{(void *)q, qb, true, false}, {(void *)k, kb, true, false}, {(void *)v, kb, true, false},
+                 {out, qb, false, true}};
+    return slice_call(dev, s, [&](void **d, void *st) {
+        return smg_attention_kv_causal_f16_dev((const float *)d[0], (const uint16_t *)d[1], (const uint16_t *)d[2],
+                                               start, rows, heads, kv_heads, head_dim, scale, (float *)d[3], st);
+    });
+}
+
+int smg_rms_norm_f16(const float *x, const float *weight, size_t rows, size_t dim, float eps, uint16_t *y) {
+    if (dim == 0) return fail(SMG_EINVAL, "a norm needs at least one feature");
+    if (rows == 0) return SMG_OK;
+    if (!x || !weight || !y) return fail(SMG_EINVAL, "null array");
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev), SMG_EHIP);
+    SLICE_BYTES(xb, rows, dim, 4);
+    Slice s[] = {{(void *)x, xb, true, false}, {(void *)weight, dim * 4, true, false}, {y, xb / 2, false, true}};
+    return slice_call(dev, s, [&](void **d, void *st) {
+        return smg_rms_norm_f16_dev((const float *)d[0], (const float *)d[1], rows, dim, eps, (uint16_t *)d[2], st);
+    });
+}
+
+int smg_layer_norm_f16(const float *x, const float *weight, const float *bias, size_t rows, size_t dim, float eps,
+                       uint16_t *y) {
+    if (dim == 0) return fail(SMG_EINVAL, "a norm needs at least one feature");
+    if (rows == 0) return SMG_OK;
+    if (!x || !weight || !y) return fail(SMG_EINVAL, "null array");
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev), SMG_EHIP);
+    SLICE_BYTES(xb, rows, dim, 4);
+    Slice s[] = {{(void *)x, xb, true, false}, {(void *)weight, dim * 4, true, false},
+                 {(void *)bias, bias ? dim * 4 : 0, true, false}, {y, xb / 2, false, true}};
+    return slice_call(dev, s, [&](void **d, void *st) {
+        return smg_layer_norm_f16_dev((const float *)d[0], (const float *)d[1], (const float *)d[2], rows, dim, eps,
+                                      (uint16_t *)d[3], st);
+    });
+}
+
+#undef SLICE_BYTES
 
 // ---- measurement probes --------------------------------------------------------
 

@@ -133,6 +133,19 @@ def lib() -> C.CDLL:
     L.smg_block_destroy.argtypes = [P]
     L.smg_block_destroy.restype = None
     L.smg_block_accumulate_dev.argtypes = [P, P, P, SZ, P]
+    # host-slice forms of the model parts
+    L.smg_q4_accumulate.argtypes = [SZ, P, P, P]
+    L.smg_attn_accumulate.argtypes = [P, P, P, P, SZ]
+    L.smg_mlp_accumulate.argtypes = [P, P, P, SZ]
+    L.smg_block_accumulate.argtypes = [P, P, P, SZ]
+    L.smg_kv_cache_extend.argtypes = [P, P, P, SZ]
+    L.smg_kv_cache_read.argtypes = [P, P, P]
+    L.smg_kv_cache_attend.argtypes = [P, P, P]
+    L.smg_kv_cache_attend_causal.argtypes = [P, P, SZ, P]
+    L.smg_attention_kv_f16.argtypes = [P, P, P, SZ, SZ, SZ, SZ, C.c_float, P]
+    L.smg_attention_kv_causal_f16.argtypes = [P, P, P, SZ, SZ, SZ, SZ, SZ, C.c_float, P]
+    L.smg_rms_norm_f16.argtypes = [P, P, SZ, SZ, C.c_float, P]
+    L.smg_layer_norm_f16.argtypes = [P, P, P, SZ, SZ, C.c_float, P]
     L.smg_stream_read_dev.argtypes = [P, SZ, P]
     L.smg_clock_probe_dev.argtypes = [P, C.c_uint, P]
     _lib = L
@@ -197,6 +210,44 @@ def _dev16(x, n: int | None, what: str, device: int | None, bf16: bool | None = 
     if n is not None and x.numel() != n:
         raise ValueError(f"{what} has {x.numel()} elements, expected {n}")
     return x
+
+
+def _host_x16(x, n: int, what: str) -> np.ndarray:
+    """A host input of a model part as f16 bits: float16 / uint16 as they are,
+    float32 rounded to nearest even as the reference's ModelFloat::as_f16
+    does for f32 callers (src/linear.rs:61-66)."""
+    a = np.asarray(x)
+    if a.dtype == np.float32:
+        with np.errstate(over="ignore"):  # past the f16 range: infinity, as the conversion rounds
+            a = np.ascontiguousarray(a).astype(np.float16)
+    return _host16(a, n, what)
+
+
+def _host_out(x, n: int | None, dtypes, what: str) -> np.ndarray:
+    """A host array a host-slice call writes in place: a contiguous, writable
+    numpy array of one of `dtypes` with n elements."""
+    if not isinstance(x, np.ndarray) or x.dtype not in dtypes:
+        raise TypeError(f"{what}: expected a numpy array of {' or '.join(np.dtype(d).name for d in dtypes)}")
+    if not x.flags["C_CONTIGUOUS"] or not x.flags["WRITEABLE"]:
+        raise ValueError(f"{what} must be contiguous and writable")
+    if n is not None and x.size != n:
+        raise ValueError(f"{what} has {x.size} elements, expected {n}")
+    return x
+
+
+def _host_f32(x, n: int | None, what: str) -> np.ndarray:
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    if n is not None and a.size != n:
+        raise ValueError(f"{what} has {a.size} elements, expected {n}")
+    return a
+
+
+def _same_side(*xs):
+    """True for device tensors, False for host arrays; mixing them raises."""
+    dev = {_is_dev(x) for x in xs if x is not None}
+    if len(dev) > 1:
+        raise ValueError("the arrays must all be host arrays or all device tensors")
+    return dev == {True}
 
 
 def _stream() -> int:
@@ -1140,7 +1191,14 @@ class Linear:
         return matmul_q4_ep(x, self.q4, y, m, ep)
 
     def accumulate(self, x, y, m: int):
-        """Linear::accumulate (src/linear.rs:425-432): y (f32) += f32(f16(x @ W))."""
+        """Linear::accumulate (src/linear.rs:425-432): y (f32) += f32(f16(x @ W)).
+        Host arrays (x f16 or f32, y float32 numpy, updated in place) or
+        device tensors (x f16, y float32)."""
+        if not _same_side(x, y):
+            xh = _host_x16(x, m * self.k(), "x (m*k)")
+            _host_out(y, m * self.n(), (np.float32,), "y (m*n)")
+            _check(lib().smg_q4_accumulate(m, self.q4._h, y.ctypes.data, xh.ctypes.data), "smg_q4_accumulate")
+            return y
         dev = self.q4.device()
         _dev16(x, m * self.k(), "x (m*k)", dev, False)
         _f32dev(y, m * self.n(), "y (m*n)", dev)
@@ -1246,7 +1304,13 @@ class Mlp:
         return self._hidden
 
     def accumulate(self, x, y, m: int):
-        """Mlp::accumulate (src/mlp.rs:113-149): y (f32 m x n) += ... for x f16."""
+        """Mlp::accumulate (src/mlp.rs:113-149): y (f32 m x n) += ... for x f16
+        (host arrays, where x may also be f32, or device tensors)."""
+        if not _same_side(x, y):
+            xh = _host_x16(x, m * self._k, "x (m*k)")
+            _host_out(y, m * self._n, (np.float32,), "y (m*n)")
+            _check(lib().smg_mlp_accumulate(self._h, xh.ctypes.data, y.ctypes.data, m), "Mlp::accumulate")
+            return y
         _dev16(x, m * self._k, "x (m*k)", self._device, False)
         _f32dev(y, m * self._n, "y (m*n)", self._device)
         _check(lib().smg_mlp_accumulate_dev(self._h, x.data_ptr(), y.data_ptr(), m, _stream()),
@@ -1322,6 +1386,15 @@ class KvCache:
     def extend(self, k, v):
         """KvCache::extend (kv_attention.rs:499-519): whole rows of f16 keys and values."""
         row = self.row_len()
+        if not _same_side(k, v):
+            kh, vh = np.asarray(k), np.asarray(v)
+            if kh.size != vh.size or kh.size % row or kh.size == 0:
+                raise ValueError("k and v hold the same whole number of kv_heads * head_dim rows")
+            kh = _host_x16(kh, kh.size, "k")
+            vh = _host_x16(vh, vh.size, "v")
+            _check(lib().smg_kv_cache_extend(self._h, kh.ctypes.data, vh.ctypes.data, kh.size // row),
+                   "KvCache::extend")
+            return
         if k.numel() != v.numel() or k.numel() % row or k.numel() == 0:
             raise ValueError("k and v hold the same whole number of kv_heads * head_dim rows")
         _dev16(k, None, "k", self._device, False)
@@ -1349,8 +1422,30 @@ class KvCache:
     def values(self):
         return self._rows(1)
 
+    def keys_host(self) -> np.ndarray:
+        """keys() copied into a new float16 numpy array."""
+        return self._rows_host(0)
+
+    def values_host(self) -> np.ndarray:
+        """values() copied into a new float16 numpy array."""
+        return self._rows_host(1)
+
+    def _rows_host(self, which: int) -> np.ndarray:
+        out = np.empty(self.len() * self.row_len(), np.float16)
+        if out.size:
+            p = out.ctypes.data
+            _check(lib().smg_kv_cache_read(self._h, p if which == 0 else None, p if which == 1 else None),
+                   "smg_kv_cache_read")
+        return out
+
     def attend(self, q, out):
-        """KvCache::attend (kv_attention.rs:537-552): q and out f32 heads*head_dim."""
+        """KvCache::attend (kv_attention.rs:537-552): q and out f32 heads*head_dim
+        (host arrays or device tensors)."""
+        if not _same_side(q, out):
+            qh = _host_f32(q, self.query_len(), "q")
+            _host_out(out, self.query_len(), (np.float32,), "out")
+            _check(lib().smg_kv_cache_attend(self._h, qh.ctypes.data, out.ctypes.data), "attend")
+            return out
         _f32dev(q, self.query_len(), "q", self._device)
         _f32dev(out, self.query_len(), "out", self._device)
         _check(lib().smg_kv_cache_attend_dev(self._h, q.data_ptr(), out.data_ptr(), _stream()), "attend")
@@ -1362,6 +1457,12 @@ class KvCache:
         everything before it; q and out f32 rows * heads * head_dim."""
         if rows > self.len():
             raise ValueError(f"attend_causal: {rows} rows but {self.len()} cached")
+        if not _same_side(q, out):
+            qh = _host_f32(q, rows * self.query_len(), "q")
+            _host_out(out, rows * self.query_len(), (np.float32,), "out")
+            _check(lib().smg_kv_cache_attend_causal(self._h, qh.ctypes.data, rows, out.ctypes.data),
+                   "attend_causal")
+            return out
         _f32dev(q, rows * self.query_len(), "q", self._device)
         _f32dev(out, rows * self.query_len(), "out", self._device)
         _check(lib().smg_kv_cache_attend_causal_dev(self._h, q.data_ptr(), rows, out.data_ptr(), _stream()),
@@ -1411,7 +1512,14 @@ class SelfAttention:
 
     def accumulate(self, x, cache: KvCache, y, m: int):
         """SelfAttention::accumulate (self_attention.rs:148-183): m rows at the
-        cache's next m positions (attend_rows, :192-240, for m > 1)."""
+        cache's next m positions (attend_rows, :192-240, for m > 1). Host
+        arrays (x f16 or f32, y float32, updated in place) or device tensors."""
+        if not _same_side(x, y):
+            xh = _host_x16(x, m * self._width, "x (m*width)")
+            _host_out(y, m * self._out_width, (np.float32,), "y (m*out.n)")
+            _check(lib().smg_attn_accumulate(self._h, xh.ctypes.data, cache._h, y.ctypes.data, m),
+                   "SelfAttention::accumulate")
+            return y
         _dev16(x, m * self._width, "x (m*width)", self._device, False)
         _f32dev(y, m * self._out_width, "y (m*out.n)", self._device)
         _check(lib().smg_attn_accumulate_dev(self._h, x.data_ptr(), cache._h, y.data_ptr(), m, _stream()),
@@ -1451,7 +1559,12 @@ class Norm:
         return self.weight.size
 
     def forward(self, x, y):
-        """Norm::forward (src/nn.rs:227): f32 rows x to f16 y."""
+        """Norm::forward (src/nn.rs:227): f32 rows x to f16 y (host arrays or
+        device tensors)."""
+        if not _same_side(x, y):
+            if self.rms_kind:
+                return rms_norm(x, self.weight, self.eps, y)
+            return layer_norm(x, self.weight, self.bias, self.eps, y)
         import torch
         if self._dev is None:
             self._dev = (torch.from_numpy(self.weight).cuda(),
@@ -1498,7 +1611,12 @@ class Block:
     def accumulate(self, x, cache: KvCache, rows: int):
         """Block::accumulate (src/block.rs:90-106): rows rows of the f32
         residual at the cache's next rows positions (causal attention among
-        them), which it appends."""
+        them), which it appends. x a float32 numpy array (host) or device
+        tensor, updated in place."""
+        if not _is_dev(x):
+            _host_out(x, rows * self._d, (np.float32,), "x (rows*width)")
+            _check(lib().smg_block_accumulate(self._h, x.ctypes.data, cache._h, rows), "Block::accumulate")
+            return x
         _f32dev(x, rows * self._d, "x (rows*width)", self._device)
         _check(lib().smg_block_accumulate_dev(self._h, x.data_ptr(), cache._h, rows, _stream()),
                "Block::accumulate")
@@ -1506,7 +1624,17 @@ class Block:
 
 
 def rms_norm(x, weight, eps: float, y):
-    """nn::rms_norm (src/nn.rs:147-161): f32 rows of x to f16 y; weight f32 device."""
+    """nn::rms_norm (src/nn.rs:147-161): f32 rows of x to f16 y; weight f32.
+    Host arrays (y a float16 / uint16 numpy array) or device tensors."""
+    if not _same_side(x, weight, y):
+        w = _host_f32(weight, None, "weight")
+        xh = _host_f32(x, None, "x")
+        if w.size == 0 or xh.size % w.size:
+            raise ValueError("x holds whole rows of weight.len()")
+        _host_out(y, xh.size, (np.float16, np.uint16), "y")
+        _check(lib().smg_rms_norm_f16(xh.ctypes.data, w.ctypes.data, xh.size // w.size, w.size,
+                                      float(np.float32(eps)), y.ctypes.data), "rms_norm")
+        return y
     dim = weight.numel()
     if dim == 0 or x.numel() % dim:
         raise ValueError("x holds whole rows of weight.len()")
@@ -1521,7 +1649,19 @@ def rms_norm(x, weight, eps: float, y):
 
 def layer_norm(x, weight, bias, eps: float, y):
     """nn::layer_norm (src/nn.rs:73-86): f32 rows of x to f16 y; weight (and
-    bias, or None) f32 device tensors."""
+    bias, or None) f32. Host arrays (y a float16 / uint16 numpy array) or
+    device tensors."""
+    if not _same_side(x, weight, bias, y):
+        w = _host_f32(weight, None, "weight")
+        b = None if bias is None else _host_f32(bias, w.size, "bias")
+        xh = _host_f32(x, None, "x")
+        if w.size == 0 or xh.size % w.size:
+            raise ValueError("x holds whole rows of weight.len()")
+        _host_out(y, xh.size, (np.float16, np.uint16), "y")
+        _check(lib().smg_layer_norm_f16(xh.ctypes.data, w.ctypes.data, None if b is None else b.ctypes.data,
+                                        xh.size // w.size, w.size, float(np.float32(eps)), y.ctypes.data),
+               "layer_norm")
+        return y
     dim = weight.numel()
     if dim == 0 or x.numel() % dim:
         raise ValueError("x holds whole rows of weight.len()")
@@ -1540,7 +1680,7 @@ def layer_norm(x, weight, bias, eps: float, y):
 def attention_kv_causal_f16(q, k, v, start: int, rows: int, heads: int, kv_heads: int, head_dim: int,
                             scale: float, out):
     """attention_kv_causal_f16 (src/kernels/kv_attention.rs:140-240) on device
-    tensors: query row i attends to keys 0 .. start + i."""
+    tensors or host arrays: query row i attends to keys 0 .. start + i."""
     if rows == 0:
         raise ValueError("attention_kv_causal_f16 needs at least one query row")
     if head_dim % 8 or not 8 <= head_dim <= 256:
@@ -1548,6 +1688,16 @@ def attention_kv_causal_f16(q, k, v, start: int, rows: int, heads: int, kv_heads
     if kv_heads <= 0 or heads <= 0 or heads % kv_heads:
         raise ValueError("heads must be a positive multiple of kv_heads")
     ld = kv_heads * head_dim
+    if not _same_side(q, k, v, out):
+        n_kv = (start + rows) * ld
+        qh = _host_f32(q, rows * heads * head_dim, "q")
+        kh = _host_x16(np.asarray(k).ravel()[:n_kv], n_kv, "k")
+        vh = _host_x16(np.asarray(v).ravel()[:n_kv], n_kv, "v")
+        _host_out(out, rows * heads * head_dim, (np.float32,), "out")
+        _check(lib().smg_attention_kv_causal_f16(qh.ctypes.data, kh.ctypes.data, vh.ctypes.data, start, rows,
+                                                 heads, kv_heads, head_dim, float(np.float32(scale)),
+                                                 out.ctypes.data), "attention_kv_causal_f16")
+        return out
     dev = q.device.index
     _f32dev(q, rows * heads * head_dim, "q", dev)
     _f32dev(out, rows * heads * head_dim, "out", dev)
@@ -1571,7 +1721,8 @@ def glu(both, m: int, n: int, gate: int, y):
 
 
 def attention_kv_f16(q, k, v, length: int, heads: int, kv_heads: int, head_dim: int, scale: float, out):
-    """attention_kv_f16 (src/kernels/kv_attention.rs:29-78) on device tensors."""
+    """attention_kv_f16 (src/kernels/kv_attention.rs:29-78) on device tensors
+    or host arrays."""
     if length == 0:
         raise ValueError("attention_kv_f16 needs at least one cached key")
     if head_dim % 8 or not 8 <= head_dim <= 256:
@@ -1579,6 +1730,15 @@ def attention_kv_f16(q, k, v, length: int, heads: int, kv_heads: int, head_dim: 
     if kv_heads <= 0 or heads <= 0 or heads % kv_heads:
         raise ValueError("heads must be a positive multiple of kv_heads")
     ld = kv_heads * head_dim
+    if not _same_side(q, k, v, out):
+        n_kv = length * ld
+        qh = _host_f32(q, heads * head_dim, "q")
+        kh = _host_x16(np.asarray(k).ravel()[:n_kv], n_kv, "k")
+        vh = _host_x16(np.asarray(v).ravel()[:n_kv], n_kv, "v")
+        _host_out(out, heads * head_dim, (np.float32,), "out")
+        _check(lib().smg_attention_kv_f16(qh.ctypes.data, kh.ctypes.data, vh.ctypes.data, length, heads, kv_heads,
+                                          head_dim, float(np.float32(scale)), out.ctypes.data), "attention_kv_f16")
+        return out
     dev = q.device.index
     _f32dev(q, heads * head_dim, "q", dev)
     _f32dev(out, heads * head_dim, "out", dev)

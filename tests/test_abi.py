@@ -293,3 +293,69 @@ def test_strided_gemm_refuses_bad_views(lib):
     with pytest.raises(ValueError, match="overflows"):
         smg.gemm_f16(3, 4, 2, np.zeros(12, np.uint16), 4, 1, np.zeros(5, np.uint16), 2, 1,
                      np.zeros(8, np.uint16), 4, 1, 0.0, 1.0)
+
+
+def test_host_slice_forms_check_before_any_device_call(lib):
+    """The host-slice model entries refuse null handles and bad shapes, and
+    return at once for empty work, before touching a device (SMG_EINVAL, -1)."""
+    SZ, P = C.c_size_t, C.c_void_p
+    buf = np.zeros(64, np.float32)
+    p = buf.ctypes.data
+    lib.smg_q4_accumulate.argtypes = [SZ, P, P, P]
+    lib.smg_block_accumulate.argtypes = [P, P, P, SZ]
+    lib.smg_attn_accumulate.argtypes = [P, P, P, P, SZ]
+    lib.smg_mlp_accumulate.argtypes = [P, P, P, SZ]
+    lib.smg_kv_cache_read.argtypes = [P, P, P]
+    lib.smg_kv_cache_extend.argtypes = [P, P, P, SZ]
+    lib.smg_attention_kv_f16.argtypes = [P, P, P, SZ, SZ, SZ, SZ, C.c_float, P]
+    lib.smg_rms_norm_f16.argtypes = [P, P, SZ, SZ, C.c_float, P]
+    assert lib.smg_q4_accumulate(1, None, p, p) == -1
+    assert lib.smg_block_accumulate(None, p, None, 1) == -1
+    assert lib.smg_attn_accumulate(None, p, None, p, 1) == -1
+    assert lib.smg_mlp_accumulate(None, p, p, 1) == -1
+    assert lib.smg_kv_cache_read(None, p, p) == -1
+    assert lib.smg_kv_cache_extend(None, p, p, 1) == -1
+    assert lib.smg_attention_kv_f16(p, p, p, 4, 3, 2, 64, 1.0, p) == -1   # heads not a multiple of kv_heads
+    assert lib.smg_attention_kv_f16(p, p, p, 4, 2, 2, 12, 1.0, p) == -1   # head_dim not a multiple of 8
+    assert lib.smg_rms_norm_f16(p, p, 2, 0, 1e-5, p) == -1
+    assert lib.smg_rms_norm_f16(p, p, 0, 8, 1e-5, p) == 0                 # no rows: nothing to do
+
+
+def test_host_slice_arrays_in_the_mirror():
+    """The mirror's host-array rules: f32 inputs round to f16 to nearest even
+    (ModelFloat::as_f16, src/linear.rs:61-66), outputs written in place must
+    be contiguous, writable and of the output's type, and host arrays and
+    device tensors do not mix in one call."""
+    import smegemm as smg
+    x = np.array([1.0, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 65520.0, -0.0], np.float32)
+    got = smg._host_x16(x, 5, "x")
+    assert got.dtype == np.uint16
+    assert list(got) == [0x3C00, 0x3C00, 0x3C02, 0x7C00, 0x8000]
+    with np.errstate(over="ignore"):
+        x16 = x.astype(np.float16)
+    assert np.array_equal(smg._host_x16(x16, 5, "x"), got)
+    with pytest.raises(TypeError):
+        smg._host_x16(np.zeros(5, np.float64), 5, "x")
+    with pytest.raises(ValueError, match="elements"):
+        smg._host_x16(x, 4, "x")
+    y = np.zeros(8, np.float32)
+    assert smg._host_out(y, 8, (np.float32,), "y") is y
+    with pytest.raises(TypeError):
+        smg._host_out(np.zeros(8, np.float64), 8, (np.float32,), "y")
+    with pytest.raises(TypeError):
+        smg._host_out([0.0] * 8, 8, (np.float32,), "y")
+    with pytest.raises(ValueError, match="contiguous"):
+        smg._host_out(np.zeros(16, np.float32)[::2], 8, (np.float32,), "y")
+    ro = np.zeros(8, np.float32)
+    ro.flags.writeable = False
+    with pytest.raises(ValueError, match="writable"):
+        smg._host_out(ro, 8, (np.float32,), "y")
+    with pytest.raises(ValueError, match="elements"):
+        smg._host_out(y, 9, (np.float32,), "y")
+
+    class FakeDev:
+        is_cuda = True
+    assert smg._same_side(y, None, y) is False
+    assert smg._same_side(FakeDev(), FakeDev()) is True
+    with pytest.raises(ValueError, match="host arrays or all device tensors"):
+        smg._same_side(y, FakeDev())
