@@ -224,9 +224,11 @@ __global__ void __launch_bounds__(T) lowbit_gemv(LbArgs g, EpArgs ep) {
 //      slabs inside one wave (a wave's K range holds whole blocks; shorter
 //      blocks take one masked product each), written to LDS per (row, column)
 //      with blocks contiguous;
-//   4. one lane per output folds its blocks in order with fmaf, reading four
-//      blocks' sums, scales and activation factors per LDS load, then the
-//      op-graph and the f16 store.
+//   4. every thread turns a few (row, column, block) sums into the fold's two
+//      factors, f32(sum) and f32(scale)*s, so that
+//   5. one lane per output folds its blocks in order with fmaf -- four LDS
+//      loads and 16 fmas per 16 blocks, the one sequential step, after the
+//      bytes have arrived -- then the op-graph and the f16 store.
 // LDS rows are padded so these accesses do not collide on banks.
 // ---------------------------------------------------------------------------
 constexpr uint32_t QPASS = T * 8;  // depths quantized per pass (8 per thread)
@@ -280,11 +282,17 @@ __device__ __forceinline__ int32_t group_sum_i32(int32_t a, uint32_t gl) {
     return a;
 }
 
-// LDS: q [MR][kq + 16] i8 | s [MR][nbq] f32 | -sum(q) [MR][nbq] i32 |
-//      block sums [MR][16 CG][nbq + 4] i32 | scales [16 CG][nbq + 4] f16 | wave partials
+// LDS: q [MR][kq + 16] i8, for one row later the fold's y [16 CG][nbq + 4]
+//      f32 (the products have read q by then) | s [MR][nbq] f32 |
+//      -sum(q) [MR][nbq] i32 | block sums [MR][16 CG][nbq + 4] i32 (for one
+//      row then the fold's x, f32) | scales [16 CG][nbq + 4] f16 | wave partials
+__host__ __device__ inline uint32_t tile_q_region(uint32_t kq, uint32_t nbq, uint32_t mr, uint32_t cg) {
+    const uint32_t q = mr * (kq + 16), y = mr == 1 ? 16 * cg * (nbq + 4) * 4 : 0;
+    return q > y ? q : y;
+}
 size_t tile_lds_bytes(uint32_t kq, uint32_t nbq, int mr, uint32_t cg) {
-    return (size_t)mr * (kq + 16) + (size_t)mr * nbq * 8 + (size_t)mr * 16 * cg * (nbq + 4) * 4 +
-           (size_t)16 * cg * (nbq + 4) * 2 + (size_t)mr * WV * 8;
+    return (size_t)tile_q_region(kq, nbq, (uint32_t)mr, cg) + (size_t)mr * nbq * 8 +
+           (size_t)mr * 16 * cg * (nbq + 4) * 4 + (size_t)16 * cg * (nbq + 4) * 2 + (size_t)mr * WV * 8;
 }
 
 // One 4096-depth pass of quantize_row (src/kernels/lowbit/matmul.rs:354-371)
@@ -420,7 +428,8 @@ __global__ void __launch_bounds__(T)
     const uint32_t qs_ = kq + 16;   // q row stride (bytes)
     const uint32_t bs = nbq + 4;    // block-sum / scale row stride (elements)
     int8_t *ql = (int8_t *)smem;                        // [MR][qs_]
-    float *sa = (float *)(smem + MR * qs_);             // [MR][nbq]
+    float *yl = (float *)smem;                          // [ncol][bs] (one row), after the products
+    float *sa = (float *)(smem + tile_q_region(kq, nbq, MR, cg));  // [MR][nbq]
     int32_t *as = (int32_t *)(sa + MR * nbq);           // [MR][nbq]
     int32_t *sb = as + MR * nbq;                        // [MR][ncol][bs]
     uint16_t *scl = (uint16_t *)(sb + MR * ncol * bs);  // [ncol][bs]
@@ -501,6 +510,9 @@ __global__ void __launch_bounds__(T)
         const uint32_t ob = folder && wg_col0 + fc < n ? (wg_col0 + fc) * 2u : OOB;
         opb = bload2(make_rsrc(col_b, n * 2u), ob);
         if constexpr (EPV == 3) opa = bload2(make_rsrc(col_a, n * 2u), ob);
+        // the activation's kernel arguments are read here, not after the
+        // fold, where their scalar load would sit on the kernel's last steps
+        asm volatile("" : "+s"(act), "+s"(alpha));
     }
 
     // -- 2. quantize A (quantize_row, src/kernels/lowbit/matmul.rs:354-371),
@@ -537,6 +549,9 @@ __global__ void __launch_bounds__(T)
     // lane (gq4, c) holds the sums of columns 4*gq4 + v, row c; rows m..MR-1
     // of q are zero, so their sums are too
     int32_t *dp = sb + dp_off;
+    // (the q fragments below are not masked: lanes c >= MR read row 0 again,
+    // and an MFMA's output column c depends only on its B column c, so those
+    // lanes' sums are never stored)
     auto expand = [&](int i) {
         const uint4 wv = wreg[i / SPG];
         const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
@@ -553,13 +568,12 @@ __global__ void __launch_bounds__(T)
         }
         return wa;
     };
-    // q fragments: read from a valid row for every lane, then selected
-    // (branch-free, so a group's reads are issued together and overlap
-    // instead of each one preceding its MFMA)
+    // q fragments: every lane reads a valid row, unconditionally, so a
+    // group's reads are issued together and overlap instead of each one
+    // preceding its MFMA
     auto qload = [&](int i) {
         const uint32_t slab = kw * NSW + i;
-        const uint4 qb = *(const uint4 *)(ql + (c < MR ? c : 0) * qs_ + slab * LB_SLAB + 16 * gq4);
-        return __builtin_bit_cast(int4_t, c < MR ? qb : make_uint4(0, 0, 0, 0));
+        return __builtin_bit_cast(int4_t, *(const uint4 *)(ql + (c < MR ? c : 0) * qs_ + slab * LB_SLAB + 16 * gq4));
     };
     constexpr int PF = NSW < 8 ? NSW : 8;  // slabs whose q is read ahead at once
     if constexpr (SPB > 0) {
@@ -580,14 +594,19 @@ __global__ void __launch_bounds__(T)
                     __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(i0 + j), qv[j], acc[(i0 + j) / SPB], 0, 0, 0);
         }
         if (c < MR) {
+            // block kw * NBW + b < kq / block <= nbq (the waves hold whole
+            // blocks); one base offset per column, held in a register of its
+            // own, and the block as the stores' immediate offset
+            uint32_t o[4];
 #pragma unroll
-            for (int b = 0; b < NBW; b++) {
-                const uint32_t bb = kw * NBW + b;
-                if (bb < nbq) {
-#pragma unroll
-                    for (int v = 0; v < 4; v++) dp[v * bs + bb] = acc[b][v];
-                }
+            for (int v = 0; v < 4; v++) {
+                o[v] = dp_off + v * bs + kw * NBW;
+                asm volatile("" : "+v"(o[v]));
             }
+#pragma unroll
+            for (int b = 0; b < NBW; b++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) sb[o[v] + b] = acc[b][v];
         }
     } else {
         const uint32_t parts = block < (uint32_t)LB_SLAB ? LB_SLAB / block : 1;
@@ -628,22 +647,67 @@ __global__ void __launch_bounds__(T)
     }
     __syncthreads();
 
-    // -- 4. fold in block order (reference, matmul.rs:380-393): four blocks'
-    //       sums, scales and factors per LDS load; per block one shift-add
-    //       (Q1: 2*sum(q*b) + (-sum(q))), one conversion, the product
-    //       f32(scale)*s by v_fma_mix (the f16 operand widened exactly, one
-    //       rounding; the -0 addend leaves every product as it is) and
-    //       the fma
-    if (folder) {
+    // -- 4. fold in block order (reference, matmul.rs:380-393): per block
+    //       x = f32(sum) (Q1: 2*sum(q*b) + (-sum(q))) and y = f32(scale)*s by
+    //       v_fma_mix (the f16 operand widened exactly, one rounding; the -0
+    //       addend leaves every product as it is), then total = fmaf(x, y,
+    //       total). Blocks past K add fmaf(0, 0, total) == total (total starts
+    //       at +0 and never becomes -0, so its bits are unchanged).
+    const uint32_t nb_live = (k + block - 1) >> block_shift;
+    float total = 0.0f;
+    if constexpr (MR == 1) {
+        // one row: 16 * CG folding lanes, so every thread first computes a
+        // few blocks' x and y (x in place of the sum), and the folding lanes
+        // then only load them, 16 blocks per four LDS loads, and run the fmas
+        const uint32_t nbf = (nb_live + 3) & ~3u;  // <= nbq; x = y = 0 past nb_live
+        {
+            float *xl = (float *)sb;
+            const uint32_t j = t & (ncol - 1), bstep = (uint32_t)T >> (4 + cg_shift);
+            for (uint32_t b = (uint32_t)t >> (4 + cg_shift); b < nbf; b += bstep) {
+                const uint32_t e = j * bs + b;
+                float x = 0.0f, y = 0.0f;
+                if (b < nb_live) {
+                    const int32_t sum = sb[e];
+                    x = (float)(KIND == 1 ? 2 * sum + as[b] : sum);
+                    const uint32_t cw = scl[e];
+                    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(y) : "v"(cw), "v"(sa[b]), "v"(-0.0f));
+                }
+                xl[e] = x;
+                yl[e] = y;
+            }
+        }
+        __syncthreads();
+        if (folder) {
+            const float *xp = (const float *)sb + fc * bs;
+            const float *yp = yl + fc * bs;
+            auto group16 = [&](uint32_t b0, auto tail_tag) {
+                constexpr bool TAIL = decltype(tail_tag)::value;
+                float4_t x4[4], y4[4];
+#pragma unroll
+                for (int h = 0; h < 4; h++) {
+                    const bool live = !TAIL || b0 + 4 * h < nbf;
+                    const uint32_t bh = live ? b0 + 4 * h : 0;
+                    x4[h] = *(const float4_t *)(xp + bh);
+                    y4[h] = *(const float4_t *)(yp + bh);
+                    if (TAIL && !live) x4[h] = y4[h] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
+                }
+#pragma unroll
+                for (int h = 0; h < 4; h++)
+#pragma unroll
+                    for (int u = 0; u < 4; u++) total = fmaf(x4[h][u], y4[h][u], total);
+            };
+            const uint32_t nb16 = nbf & ~15u;
+            for (uint32_t b0 = 0; b0 < nb16; b0 += 16) group16(b0, std::false_type{});
+            if (nb16 < nbf) group16(nb16, std::true_type{});
+        }
+    } else if (folder) {
+        // several rows: 16 * CG lanes per row fold, each reading four blocks'
+        // sums, scales and factors per LDS load
         const int32_t *sp = sb + (frow * ncol + fc) * bs;
         const uint16_t *cp = scl + fc * bs;
         const float *ap = sa + frow * nbq;
         const int32_t *qp = as + frow * nbq;
-        const uint32_t nb_live = (k + block - 1) >> block_shift;
-        float total = 0.0f;
-        // 16 blocks from b0; TAIL: some are past K, and add
-        // fmaf(0, 0, total) == total (total starts at +0 and never
-        // becomes -0, so its bits are unchanged) by selects, not branches
+        // 16 blocks from b0; TAIL: some are past K, zeroed by selects
         auto group16 = [&](uint32_t b0, auto tail_tag) {
             constexpr bool TAIL = decltype(tail_tag)::value;
             int4_t s4[4], q4[4];
@@ -683,6 +747,8 @@ __global__ void __launch_bounds__(T)
         const uint32_t nb_full = nb_live & ~15u;
         for (uint32_t b0 = 0; b0 < nb_full; b0 += 16) group16(b0, std::false_type{});
         if (nb_full < nb_live) group16(nb_full, std::true_type{});
+    }
+    if (folder) {
         const uint32_t j = wg_col0 + fc;
         if (j < n) {
             uint16_t out;
