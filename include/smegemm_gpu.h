@@ -90,8 +90,15 @@ typedef struct {
 } ep_desc16;
 
 /* Nodes one call carries to the device (by value, in the kernel arguments).
- * Longer graphs return SMG_EINVAL. */
-#define SMG_MAX_EP_NODES 16
+ * Up to SMG_FUSED_EP_NODES run in the product kernel's store; a longer graph
+ * runs as a second pass over C that reads each stored cell (the product
+ * rounded to T) and applies the whole graph -- the reference's own order,
+ * GEMM to T then apply_ep_scalar (src/exec/macros.rs:188-206), so the
+ * results are the same. Longer than SMG_MAX_EP_NODES returns SMG_EINVAL, as
+ * does a graph longer than SMG_FUSED_EP_NODES on the chained GEMV (its done
+ * flag is raised by the product kernel itself). */
+#define SMG_FUSED_EP_NODES 16
+#define SMG_MAX_EP_NODES 64
 
 /* The checks every entry point makes of an epilogue before any device work,
  * for an output n columns wide: at most SMG_MAX_EP_NODES nodes, known ops and

@@ -214,17 +214,31 @@ size_t operand_elems(const EpNode &nd, size_t m, size_t n) {
     return 0;
 }
 
-// The graph's nodes for the kernels. The Rust side validates operand lengths
-// (validate_ep, src/exec/guard.rs:112-147); what this C boundary can check
-// without lengths it checks here: known ops and activations, an operand
-// pointer on every ROW / COL / TENSOR node (a kernel would read address 0
-// otherwise), and a TENSOR row stride of at least n.
-int ep_args(const ep_desc16 *ep, EpArgs *out, size_t n) {
-    std::memset(out, 0, sizeof(*out));
+// The graph's nodes for the kernels: up to EP_FUSED in `fused`, which the
+// product kernel's store applies, a longer graph in `tail`, which
+// launch_ep_tail applies as a pass over C after a store with no graph. The
+// Rust side validates operand lengths (validate_ep, src/exec/guard.rs:112-147);
+// what this C boundary can check without lengths it checks here: known ops and
+// activations, an operand pointer on every ROW / COL / TENSOR node (a kernel
+// would read address 0 otherwise), and a TENSOR row stride of at least n.
+struct EpPlan {
+    EpArgs fused;
+    EpLong tail;
+    uint32_t count() const { return fused.n_nodes + tail.n_nodes; }
+    const EpNode *nodes() const { return tail.n_nodes ? tail.nodes : fused.nodes; }
+    EpNode *nodes() { return tail.n_nodes ? tail.nodes : fused.nodes; }
+};
+
+int ep_plan(const ep_desc16 *ep, EpPlan *p, size_t n, bool allow_tail = true) {
+    std::memset(p, 0, sizeof(*p));
     if (!ep || ep->n_nodes == 0) return SMG_OK;
     if (ep->n_nodes > SMG_MAX_EP_NODES) return fail(SMG_EINVAL, "epilogue has too many nodes");
+    if (ep->n_nodes > (uint32_t)EP_FUSED && !allow_tail)
+        return fail(SMG_EINVAL, "this call applies at most SMG_FUSED_EP_NODES epilogue nodes");
     if (!ep->nodes) return fail(SMG_EINVAL, "epilogue has n_nodes > 0 and no node array");
-    out->n_nodes = ep->n_nodes;
+    const bool tail = ep->n_nodes > (uint32_t)EP_FUSED;
+    EpNode *nodes = tail ? p->tail.nodes : p->fused.nodes;
+    uint32_t *fam = tail ? p->tail.fam : p->fused.fam, *cls = tail ? p->tail.cls : p->fused.cls;
     for (uint32_t i = 0; i < ep->n_nodes; i++) {
         const EpNode &nd = ep->nodes[i];
         if (ep_family(nd.op) == EPF_NONE) return fail(SMG_EINVAL, "epilogue node has an unknown op");
@@ -234,11 +248,20 @@ int ep_args(const ep_desc16 *ep, EpArgs *out, size_t n) {
             return fail(SMG_EINVAL, "epilogue row / col / tensor node has a null operand pointer");
         if (op_is_tensor(nd.op) && nd.ld != 0 && nd.ld < n)
             return fail(SMG_EINVAL, "epilogue tensor row stride is below n");
-        out->nodes[i] = nd;
-        out->fam[i] = ep_family(nd.op);
-        out->cls[i] = ep_class(nd.op);
+        nodes[i] = nd;
+        fam[i] = ep_family(nd.op);
+        cls[i] = ep_class(nd.op);
     }
+    (tail ? p->tail.n_nodes : p->fused.n_nodes) = ep->n_nodes;
     return SMG_OK;
+}
+
+// After a product stored without a graph: the plan's tail, if it has one,
+// over the m x n C at dst (row stride rs, column stride cs).
+hipError_t plan_tail(const EpPlan &p, uint16_t *dst, long cs, long rs, size_t m, size_t n, bool bf16,
+                     hipStream_t s) {
+    return p.tail.n_nodes ? launch_ep_tail(dst, rs, cs, dst, rs, cs, m, n, 0.0f, false, p.tail, bf16, s)
+                          : hipSuccess;
 }
 
 // ---- weight creation ---------------------------------------------------------
@@ -447,14 +470,16 @@ template <class Launch>
 int host_call(const char *name, int device, size_t m, size_t n, size_t k, uint16_t *dst,
               size_t dst_elems, bool preload_dst, const uint16_t *lhs, size_t lhs_elems,
               const ep_desc16 *ep, size_t extra_scratch, Launch launch) {
-    EpArgs ea;
-    int rc = ep_args(ep, &ea, n);
+    EpPlan plan;
+    int rc = ep_plan(ep, &plan, n);
     if (rc) return rc;
+    EpNode *nodes = plan.nodes();
+    const uint32_t nn = plan.count();
     size_t op_elems[SMG_MAX_EP_NODES] = {0};
     size_t total = round_up(lhs_elems * 2, 256) + round_up(dst_elems * 2, 256) +
                    round_up(extra_scratch, 256);
-    for (uint32_t i = 0; i < ea.n_nodes; i++) {
-        op_elems[i] = ea.nodes[i].ptr ? operand_elems(ea.nodes[i], m, n) : 0;
+    for (uint32_t i = 0; i < nn; i++) {
+        op_elems[i] = nodes[i].ptr ? operand_elems(nodes[i], m, n) : 0;
         total += round_up(op_elems[i] * 2, 256);
     }
     Ctx *c;
@@ -466,11 +491,11 @@ int host_call(const char *name, int device, size_t m, size_t n, size_t k, uint16
     p += round_up(dst_elems * 2, 256);
     void *scratch = p;
     p += round_up(extra_scratch, 256);
-    for (uint32_t i = 0; i < ea.n_nodes; i++) {
+    for (uint32_t i = 0; i < nn; i++) {
         if (!op_elems[i]) continue;
-        HIP_TRY(hipMemcpyAsync(p, ea.nodes[i].ptr, op_elems[i] * 2, hipMemcpyHostToDevice,
+        HIP_TRY(hipMemcpyAsync(p, nodes[i].ptr, op_elems[i] * 2, hipMemcpyHostToDevice,
                                c->stream), SMG_EHIP);
-        ea.nodes[i].ptr = p;
+        nodes[i].ptr = p;
         p += round_up(op_elems[i] * 2, 256);
     }
     if (lhs_elems)
@@ -486,7 +511,7 @@ int host_call(const char *name, int device, size_t m, size_t n, size_t k, uint16
         (void)hipEventCreate(&e1);
         (void)hipEventRecord(e0, c->stream);
     }
-    hipError_t e = launch(d_dst, d_lhs, ea, scratch, c->stream);
+    hipError_t e = launch(d_dst, d_lhs, plan, scratch, c->stream);
     if (e != hipSuccess) return fail(SMG_EHIP, name, e);
     if (tr) (void)hipEventRecord(e1, c->stream);
     HIP_TRY(hipStreamSynchronize(c->stream), SMG_EHIP);
@@ -1115,7 +1140,7 @@ bool device_readable(const void *p, int device) {
 // The pointer query is not a stream operation, so it runs (and refuses a host
 // pointer) also while the stream is being captured into a graph: a captured
 // call never records a kernel that would read a pageable host address on replay.
-int check_dev_ptrs(const char *who, int device, void *stream, const EpArgs &ea,
+int check_dev_ptrs(const char *who, int device, void *stream, const EpPlan &ep,
                    std::initializer_list<const void *> ptrs) {
     (void)who;
     (void)stream;
@@ -1123,8 +1148,9 @@ int check_dev_ptrs(const char *who, int device, void *stream, const EpArgs &ea,
         if (p && !device_readable(p, device))
             return fail(SMG_EINVAL, "device call: an operand pointer is not memory this device can read "
                                     "(host memory must be pinned; device memory must be on the weights' GPU)");
-    for (uint32_t i = 0; i < ea.n_nodes; i++)
-        if (ea.nodes[i].ptr && !device_readable(ea.nodes[i].ptr, device))
+    const EpNode *nodes = ep.nodes();
+    for (uint32_t i = 0; i < ep.count(); i++)
+        if (nodes[i].ptr && !device_readable(nodes[i].ptr, device))
             return fail(SMG_EINVAL, "device call: an epilogue operand is not memory this device can read "
                                     "(host memory must be pinned; device memory must be on the weights' GPU)");
     return SMG_OK;
@@ -1145,8 +1171,8 @@ int smg_available(void) {
 const char *smg_last_error(void) { return g_err.c_str(); }
 
 int smg_ep_check(const ep_desc16 *ep, size_t n) {
-    EpArgs ea;
-    return ep_args(ep, &ea, n);
+    EpPlan p;
+    return ep_plan(ep, &p, n);
 }
 
 size_t smg_q4_gemv_max_rows(void) { return Q4_GEMV_MAX_ROWS; }
@@ -1322,8 +1348,9 @@ static int q4_host(size_t m, const smg_weights *w, uint16_t *dst, const uint16_t
     const size_t sb = q4_split_bytes(d, m, nullptr, bf16);  // split-K partials in the call's staging
     return host_call(bf16 ? "gemm_gpu_b16b16_q4" : "gemm_gpu_f16f16_q4", w->device, m, n, k, dst,
                      m * n, false, lhs, m * k, ep, sb,
-                     [&](uint16_t *dd, const uint16_t *dl, const EpArgs &ea, void *sc, hipStream_t s) {
-                         return run_q4(d, m, dd, dl, ea, bf16, s, sb ? sc : nullptr, sb);
+                     [&](uint16_t *dd, const uint16_t *dl, const EpPlan &p, void *sc, hipStream_t s) {
+                         const hipError_t e = run_q4(d, m, dd, dl, p.fused, bf16, s, sb ? sc : nullptr, sb);
+                         return e == hipSuccess ? plan_tail(p, dd, 1, (long)n, m, n, bf16, s) : e;
                      });
 }
 
@@ -1348,9 +1375,11 @@ static int lowbit_host(int kind, bool mopa, size_t m, const smg_weights *w, uint
     const char *name = mopa ? (kind == W_Q2 ? "gemm_gpu_f16f16_q2" : "gemm_gpu_f16f16_q1")
                             : (kind == W_Q2 ? "gemm_gpu_f16_q2" : "gemm_gpu_f16_q1");
     return host_call(name, w->device, m, n, k, dst, m * n, false, lhs, m * k, ep, scratch,
-                     [&](uint16_t *dd, const uint16_t *dl, const EpArgs &ea, void *sc, hipStream_t s) {
-                         if (mopa) return launch_gemm(d, m, dd, 1, (long)n, dl, 1, (long)k, 1.0f, ea, false, s);
-                         return launch_lowbit_gemv(d, m, dd, dl, ea, sc, s);
+                     [&](uint16_t *dd, const uint16_t *dl, const EpPlan &p, void *sc, hipStream_t s) {
+                         const hipError_t e = mopa ? launch_gemm(d, m, dd, 1, (long)n, dl, 1, (long)k, 1.0f, p.fused,
+                                                                 false, s)
+                                                   : launch_lowbit_gemv(d, m, dd, dl, p.fused, sc, s);
+                         return e == hipSuccess ? plan_tail(p, dd, 1, (long)n, m, n, false, s) : e;
                      });
 }
 
@@ -1386,11 +1415,24 @@ static int packed_host(bool bf16, size_t m, size_t n, size_t k, uint16_t *dst, l
     const bool dense_out = (dst_cs == 1 && (size_t)dst_rs == n) || (dst_rs == 1 && (size_t)dst_cs == m);
     const float beta = half_bits_to_float(beta_bits, bf16), alpha = half_bits_to_float(alpha_bits, bf16);
     const WDev d = b->d;
+    // a graph past the store's nodes with read_dst: the product goes to the
+    // call's scratch, and the graph's pass adds alpha * old C (the store's
+    // add_dst step)
+    const bool tail_add = read_dst && ep && ep->n_nodes > (uint32_t)EP_FUSED;
     return host_call(bf16 ? "gemm_gpu_b16b16_run_packed" : "gemm_gpu_f16f16_run_packed", b->device,
-                     m, n, k, dst, dst_elems, !dense_out || read_dst, lhs, lhs_elems, ep, 0,
-                     [&](uint16_t *dd, const uint16_t *dl, const EpArgs &ea, void *, hipStream_t s) {
-                         return launch_gemm(d, m, dd, dst_cs, dst_rs, dl, lhs_cs, lhs_rs, beta, ea, bf16, s,
-                                            read_dst != 0, alpha);
+                     m, n, k, dst, dst_elems, !dense_out || read_dst, lhs, lhs_elems, ep, tail_add ? m * n * 2 : 0,
+                     [&](uint16_t *dd, const uint16_t *dl, const EpPlan &p, void *sc, hipStream_t s) {
+                         if (tail_add) {
+                             uint16_t *prod = (uint16_t *)sc;
+                             const hipError_t e = launch_gemm(d, m, prod, 1, (long)n, dl, lhs_cs, lhs_rs, beta,
+                                                              p.fused, bf16, s, false, 0.0f);
+                             return e == hipSuccess ? launch_ep_tail(prod, (long)n, 1, dd, dst_rs, dst_cs, m, n, alpha,
+                                                                     true, p.tail, bf16, s)
+                                                    : e;
+                         }
+                         const hipError_t e = launch_gemm(d, m, dd, dst_cs, dst_rs, dl, lhs_cs, lhs_rs, beta, p.fused,
+                                                          bf16, s, read_dst != 0, alpha);
+                         return e == hipSuccess ? plan_tail(p, dd, dst_cs, dst_rs, m, n, bf16, s) : e;
                      });
 }
 
@@ -1456,7 +1498,8 @@ static int run_host(bool bf16, const char *name, size_t m, size_t n, size_t k, u
     const float alpha = half_bits_to_float(alpha_bits, bf16), beta = half_bits_to_float(beta_bits, bf16);
     return host_call(name, device, m, n, k, dst, dst_elems, !dense_out || read_dst, lhs, footprint(m, lhs_rs, k, lhs_cs),
                      nullptr, dense_bytes + rhs_elems * 2,
-                     [&](uint16_t *dd, const uint16_t *dl, const EpArgs &ea, void *sc, hipStream_t s) {
+                     [&](uint16_t *dd, const uint16_t *dl, const EpPlan &p, void *sc, hipStream_t s) {
+                         const EpArgs &ea = p.fused;  // no op-graph on these entry points
                          uint16_t *dense = (uint16_t *)sc, *raw = (uint16_t *)((uint8_t *)sc + dense_bytes);
                          if (rhs_elems) {
                              const hipError_t e = hipMemcpyAsync(raw, rhs, rhs_elems * 2, hipMemcpyHostToDevice, s);
@@ -1507,7 +1550,7 @@ int smg_gemm_run_dev(int bf16, size_t m, size_t n, size_t k, uint16_t *dst, long
         return fail(SMG_EINVAL, "strides must be non-negative and C's cells distinct");
     int device = 0;
     HIP_TRY(hipGetDevice(&device), SMG_EHIP);
-    int rc = check_dev_ptrs("smg_gemm_run_dev", device, stream, EpArgs{},
+    int rc = check_dev_ptrs("smg_gemm_run_dev", device, stream, EpPlan{},
                             {dst, k ? lhs : nullptr, k ? rhs : nullptr});
     if (rc) return rc;
     WDev d = {};
@@ -1559,10 +1602,11 @@ int smg_q4_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint1
     int rc = check_kind(w, W_Q4);
     if (rc) return rc;
     if (m == 0 || w->d.n == 0) return SMG_OK;
-    EpArgs ea;
-    if ((rc = ep_args(ep, &ea, w->d.n))) return rc;
-    if ((rc = check_dev_ptrs("smg_q4_matmul_dev", w->device, stream, ea, {dst, lhs}))) return rc;
-    hipError_t e = run_q4_dev(w->device, w->d, m, dst, lhs, ea, bf16 != 0, (hipStream_t)stream);
+    EpPlan ep_p;
+    if ((rc = ep_plan(ep, &ep_p, w->d.n))) return rc;
+    if ((rc = check_dev_ptrs("smg_q4_matmul_dev", w->device, stream, ep_p, {dst, lhs}))) return rc;
+    hipError_t e = run_q4_dev(w->device, w->d, m, dst, lhs, ep_p.fused, bf16 != 0, (hipStream_t)stream);
+    if (e == hipSuccess) e = plan_tail(ep_p, dst, 1, (long)w->d.n, m, w->d.n, bf16 != 0, (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : q4_fail("smg_q4_matmul_dev", e);
 }
 
@@ -1573,9 +1617,10 @@ int smg_q4_chained_dev(size_t m, const smg_weights *w, uint16_t *dst, const uint
     if (rc) return rc;
     if (m == 0 || w->d.n == 0) return fail(SMG_EINVAL, "smg_q4_chained_dev: empty call");
     if ((done || ready) && !sync) return fail(SMG_EINVAL, "smg_q4_chained_dev: done / ready need the sync words");
-    EpArgs ea;
-    if ((rc = ep_args(ep, &ea, w->d.n))) return rc;
-    if ((rc = check_dev_ptrs("smg_q4_chained_dev", w->device, stream, ea, {dst, lhs}))) return rc;
+    EpPlan ep_p;
+    if ((rc = ep_plan(ep, &ep_p, w->d.n, false))) return rc;
+    if ((rc = check_dev_ptrs("smg_q4_chained_dev", w->device, stream, ep_p, {dst, lhs}))) return rc;
+    const EpArgs &ea = ep_p.fused;
     // the device wall clock's rate (kHz), read once per device
     static std::atomic<int> clock_khz[64];
     int khz = w->device < 64 ? clock_khz[w->device].load(std::memory_order_relaxed) : 0;
@@ -1596,10 +1641,11 @@ int smg_lowbit_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const u
     if (!w) return fail(SMG_EINVAL, "null weights");
     if (w->d.kind != W_Q2 && w->d.kind != W_Q1) return fail(SMG_EKIND, "not low-bit weights");
     if (m == 0 || w->d.n == 0) return SMG_OK;
-    EpArgs ea;
-    int rc = ep_args(ep, &ea, w->d.n);
+    EpPlan ep_p;
+    int rc = ep_plan(ep, &ep_p, w->d.n);
     if (rc) return rc;
-    if ((rc = check_dev_ptrs("smg_lowbit_matmul_dev", w->device, stream, ea, {dst, lhs}))) return rc;
+    if ((rc = check_dev_ptrs("smg_lowbit_matmul_dev", w->device, stream, ep_p, {dst, lhs}))) return rc;
+    const EpArgs &ea = ep_p.fused;
     const size_t sb = lowbit_scratch_bytes(w->d, m);
     void *scratch = nullptr;
     if (sb) {
@@ -1609,6 +1655,7 @@ int smg_lowbit_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const u
         if (!scratch) return fail(SMG_ENOMEM, "smg_lowbit_matmul_dev: scratch hipMalloc");
     }
     hipError_t e = launch_lowbit_gemv(w->d, m, dst, lhs, ea, scratch, (hipStream_t)stream);
+    if (e == hipSuccess) e = plan_tail(ep_p, dst, 1, (long)w->d.n, m, w->d.n, false, (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_lowbit_matmul_dev", e);
 }
 
@@ -1621,10 +1668,11 @@ int smg_lowbit_matmul_dev_noalloc(size_t m, const smg_weights *w, uint16_t *dst,
     if (!w) return fail(SMG_EINVAL, "null weights");
     if (w->d.kind != W_Q2 && w->d.kind != W_Q1) return fail(SMG_EKIND, "not low-bit weights");
     if (m == 0 || w->d.n == 0) return SMG_OK;
-    EpArgs ea;
-    int rc = ep_args(ep, &ea, w->d.n);
+    EpPlan ep_p;
+    int rc = ep_plan(ep, &ep_p, w->d.n);
     if (rc) return rc;
-    if ((rc = check_dev_ptrs("smg_lowbit_matmul_dev_noalloc", w->device, stream, ea, {dst, lhs}))) return rc;
+    if ((rc = check_dev_ptrs("smg_lowbit_matmul_dev_noalloc", w->device, stream, ep_p, {dst, lhs}))) return rc;
+    const EpArgs &ea = ep_p.fused;
     const size_t sb = lowbit_scratch_bytes(w->d, m);
     if (sb > SMG_NOALLOC_SCRATCH_BYTES)
         return fail(SMG_EINVAL, "smg_lowbit_matmul_dev_noalloc: the call needs more scratch than "
@@ -1632,6 +1680,7 @@ int smg_lowbit_matmul_dev_noalloc(size_t m, const smg_weights *w, uint16_t *dst,
     void *p = nullptr;
     if (sb && (rc = noalloc_scratch(w->device, &p))) return rc;
     hipError_t e = launch_lowbit_gemv(w->d, m, dst, lhs, ea, p, (hipStream_t)stream);
+    if (e == hipSuccess) e = plan_tail(ep_p, dst, 1, (long)w->d.n, m, w->d.n, false, (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_lowbit_matmul_dev_noalloc", e);
 }
 
@@ -1640,12 +1689,14 @@ int smg_lowbit_mopa_dev(size_t m, const smg_weights *w, uint16_t *dst, const uin
     if (!w) return fail(SMG_EINVAL, "null weights");
     if (w->d.kind != W_Q2 && w->d.kind != W_Q1) return fail(SMG_EKIND, "not low-bit weights");
     if (m == 0 || w->d.n == 0) return SMG_OK;
-    EpArgs ea;
-    int rc = ep_args(ep, &ea, w->d.n);
+    EpPlan ep_p;
+    int rc = ep_plan(ep, &ep_p, w->d.n);
     if (rc) return rc;
-    if ((rc = check_dev_ptrs("smg_lowbit_mopa_dev", w->device, stream, ea, {dst, lhs}))) return rc;
+    if ((rc = check_dev_ptrs("smg_lowbit_mopa_dev", w->device, stream, ep_p, {dst, lhs}))) return rc;
+    const EpArgs &ea = ep_p.fused;
     hipError_t e = launch_gemm(w->d, m, dst, 1, (long)w->d.n, lhs, 1, (long)w->d.k, 1.0f, ea,
                                false, (hipStream_t)stream);
+    if (e == hipSuccess) e = plan_tail(ep_p, dst, 1, (long)w->d.n, m, w->d.n, false, (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_lowbit_mopa_dev", e);
 }
 
@@ -1655,12 +1706,13 @@ int smg_packed_matmul_dev(size_t m, const smg_weights *b, uint16_t *dst, long ds
     int rc = check_kind(b, bf16 ? W_BF16 : W_F16);
     if (rc) return rc;
     if (m == 0 || b->d.n == 0) return SMG_OK;
-    EpArgs ea;
-    if ((rc = ep_args(ep, &ea, b->d.n))) return rc;
-    if ((rc = check_dev_ptrs("smg_packed_matmul_dev", b->device, stream, ea, {dst, lhs}))) return rc;
+    EpPlan ep_p;
+    if ((rc = ep_plan(ep, &ep_p, b->d.n))) return rc;
+    if ((rc = check_dev_ptrs("smg_packed_matmul_dev", b->device, stream, ep_p, {dst, lhs}))) return rc;
     hipError_t e = launch_gemm(b->d, m, dst, dst_cs, dst_rs, lhs, lhs_cs, lhs_rs,
-                               half_bits_to_float(beta_bits, bf16 != 0), ea, bf16 != 0,
+                               half_bits_to_float(beta_bits, bf16 != 0), ep_p.fused, bf16 != 0,
                                (hipStream_t)stream);
+    if (e == hipSuccess) e = plan_tail(ep_p, dst, dst_cs, dst_rs, m, b->d.n, bf16 != 0, (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_packed_matmul_dev", e);
 }
 

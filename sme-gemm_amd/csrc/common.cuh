@@ -126,15 +126,31 @@ __device__ __forceinline__ uint16_t f64_to_f16(double x) {
 // ---------------------------------------------------------------------------
 // Epilogue (src/exec/scalar.rs:58-140). The node list travels by value in the
 // kernel arguments; operand pointers are device pointers to T (f16/bf16).
+// A kernel's store applies graphs of up to EP_FUSED nodes itself (its LDS
+// holds that many ROW / COL operand vectors); a longer graph, up to
+// SMG_MAX_EP_NODES, is applied by ep_tail, a pass over C after a store with
+// no graph -- the reference's own order, the GEMM rounded to T and then
+// apply_ep_scalar over C (src/exec/macros.rs:188-206), so the results are the
+// same.
 // ---------------------------------------------------------------------------
+constexpr int EP_FUSED = SMG_FUSED_EP_NODES;
 struct EpArgs {
     uint32_t n_nodes;
     uint32_t pad;
-    EpNode nodes[SMG_MAX_EP_NODES];
+    EpNode nodes[EP_FUSED];
     // ep_family(nodes[i].op) / ep_class(nodes[i].op), filled on the host; 32-bit
     // words so that a node index held in a scalar register reads them with a
     // scalar load (a byte at a run-time offset takes a vector load and a wait
     // for every load in flight, per node)
+    uint32_t fam[EP_FUSED];
+    uint32_t cls[EP_FUSED];
+};
+// A graph of EP_FUSED + 1 .. SMG_MAX_EP_NODES nodes, for ep_tail (2.6 KB of
+// kernel arguments).
+struct EpLong {
+    uint32_t n_nodes;
+    uint32_t pad;
+    EpNode nodes[SMG_MAX_EP_NODES];
     uint32_t fam[SMG_MAX_EP_NODES];
     uint32_t cls[SMG_MAX_EP_NODES];
 };
@@ -465,8 +481,8 @@ __device__ __forceinline__ float ep_arith(uint32_t fam, float x, float v) {
 // output; (i, j) its row and column; n the row length used when a TENSOR
 // node's ld is 0. Nodes apply in order (the trailing activation is the last
 // node, as resolve_nodes appends it: src/exec/scalar.rs:28-53).
-template <bool BF16>
-__device__ uint16_t ep_cell(const EpArgs &ep, float x, size_t i, size_t j, size_t n) {
+template <bool BF16, class E>
+__device__ uint16_t ep_cell(const E &ep, float x, size_t i, size_t j, size_t n) {
     for (uint32_t t = 0; t < ep.n_nodes; t++) {
         const EpNode &nd = ep.nodes[t];
         const uint16_t *p = (const uint16_t *)nd.ptr;

@@ -22,6 +22,8 @@
 // multiplies, and step k+1 is dequantized into the other LDS buffer at the end
 // of step k, so each load has two steps of MFMA work to arrive behind. With
 // BM = 256 every Q4 weight is dequantized once per 256 output rows.
+#include <algorithm>
+
 #include "kernels.h"
 #include "tile_store.cuh"
 
@@ -338,7 +340,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const EpArgs &ep, 
     __syncthreads();
     const StoreArgs sa = {g.dst, g.dst_rs, g.dst_cs, g.m, g.n, g.alpha, g.read_dst && ep.n_nodes != 0};
     float *colv = (float *)(lds + BM * CS);      // [node][BN]
-    float *rowv = colv + SMG_MAX_EP_NODES * BN;  // [node][BM]
+    float *rowv = colv + EP_FUSED * BN;  // [node][BM]
     ep_load_vectors<BF16, BM, BN, BM * 2>(sa, ep, colv, rowv, row0, col0);
     __syncthreads();
     for (int u = t; u < BM * (BN / 8); u += BM * 2) {
@@ -347,7 +349,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const EpArgs &ep, 
     }
 }
 
-constexpr int EPI_LDS_HALFS(int bm) { return bm * (BN + 8) + SMG_MAX_EP_NODES * (BN + bm) * 2; }
+constexpr int EPI_LDS_HALFS(int bm) { return bm * (BN + 8) + EP_FUSED * (BN + bm) * 2; }
 
 template <int BM>
 struct Tile {
@@ -477,7 +479,41 @@ hipError_t launch_shape(const GemmArgs &g, const EpArgs &ep, bool vec_a, hipStre
     }
 }
 
+// An op-graph longer than a store's EP_FUSED nodes, as a pass over C: cell
+// (i, j) of src is the product rounded to T, stored without a graph, and
+// dst[i, j] = to16(graph(f32(src[i, j]))) in the node order of ep_cell (a
+// trailing activation rounded once) -- with add_dst, to16(f32(that) + alpha *
+// f32(old dst[i, j])), the store's add_dst step. src is dst unless add_dst.
+template <bool BF16>
+__global__ void __launch_bounds__(256) ep_tail(const uint16_t *src, long src_rs, long src_cs, uint16_t *dst,
+                                               long dst_rs, long dst_cs, uint32_t m, uint32_t n, float alpha,
+                                               uint32_t add_dst, EpLong ep) {
+    const size_t total = (size_t)m * n;
+    for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)gridDim.x * 256) {
+        const uint32_t i = (uint32_t)(idx / n), j = (uint32_t)(idx % n);
+        const uint16_t c = src[(size_t)i * src_rs + (size_t)j * src_cs];
+        uint16_t out = ep_cell<BF16>(ep, to_f32<BF16>(c), i, j, n);
+        uint16_t *dp = dst + (size_t)i * dst_rs + (size_t)j * dst_cs;
+        if (add_dst) out = from_f32<BF16>(to_f32<BF16>(out) + alpha * to_f32<BF16>(*dp));
+        *dp = out;
+    }
+}
+
 }  // namespace
+
+hipError_t launch_ep_tail(const uint16_t *src, long src_rs, long src_cs, uint16_t *dst, long dst_rs, long dst_cs,
+                          size_t m, size_t n, float alpha, bool add_dst, const EpLong &ep, bool bf16, hipStream_t s) {
+    if (m == 0 || n == 0 || ep.n_nodes == 0) return hipSuccess;
+    if (m > 0xFFFFFFFFu || n > 0xFFFFFFFFu) return hipErrorInvalidValue;
+    const size_t blocks = std::min<size_t>(((size_t)m * n + 255) / 256, (size_t)1 << 20);
+    if (bf16)
+        hipLaunchKernelGGL(ep_tail<true>, dim3((uint32_t)blocks), dim3(256), 0, s, src, src_rs, src_cs, dst, dst_rs,
+                           dst_cs, (uint32_t)m, (uint32_t)n, alpha, add_dst ? 1u : 0u, ep);
+    else
+        hipLaunchKernelGGL(ep_tail<false>, dim3((uint32_t)blocks), dim3(256), 0, s, src, src_rs, src_cs, dst, dst_rs,
+                           dst_cs, (uint32_t)m, (uint32_t)n, alpha, add_dst ? 1u : 0u, ep);
+    return hipGetLastError();
+}
 
 hipError_t launch_gemm(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,
                        const uint16_t *lhs, long lhs_cs, long lhs_rs, float beta,

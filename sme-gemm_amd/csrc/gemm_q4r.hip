@@ -384,7 +384,7 @@ template <bool AFFINE, bool SPLIT, int EPV = 0, bool BF16 = false>
 __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
     static_assert(!SPLIT || EPV == 0, "a split kernel's store is q4r_reduce's");
     __shared__ __align__(16) uint8_t ring[NSTAGE * STAGE_BYTES];
-    __shared__ __align__(16) float epv[EPV == 0 ? SMG_MAX_EP_NODES * (RBN + RBM) : 4];
+    __shared__ __align__(16) float epv[EPV == 0 ? EP_FUSED * (RBN + RBM) : 4];
 
     const uint32_t mtiles = (g.m + RBM - 1) / RBM;
     const int t = threadIdx.x, lane = t % 64;
@@ -494,7 +494,7 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
         wait_vm<0>();
         __syncthreads();
 
-        float *colv = epv, *rowv = epv + SMG_MAX_EP_NODES * RBN;
+        float *colv = epv, *rowv = epv + EP_FUSED * RBN;
         // the op-graph's vectors first: their global loads overlap the exchange
         if constexpr (!SPLIT && EPV == 0) ep_load_vectors<BF16, RBM, RBN, RNT>(g.st, ep, colv, rowv, row0, col0);
         EpCols cv;
@@ -599,11 +599,11 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
 constexpr int QR_BN = 256, QR_NT = 256, QR_BM = QR_NT / (QR_BN / 8);
 template <bool BF16>
 __global__ void __launch_bounds__(QR_NT) q4r_reduce(RArgs g, EpArgs ep) {
-    __shared__ __align__(16) float epv[SMG_MAX_EP_NODES * (QR_BN + QR_BM)];
+    __shared__ __align__(16) float epv[EP_FUSED * (QR_BN + QR_BM)];
     const uint32_t mtiles = (g.m + QR_BM - 1) / QR_BM;
     const uint32_t tile = xcd_tile(blockIdx.x, gridDim.x);
     const uint32_t row0 = (tile % mtiles) * QR_BM, col0 = (tile / mtiles) * QR_BN;
-    float *colv = epv, *rowv = epv + SMG_MAX_EP_NODES * QR_BN;
+    float *colv = epv, *rowv = epv + EP_FUSED * QR_BN;
     ep_load_vectors<BF16, QR_BM, QR_BN, QR_NT>(g.st, ep, colv, rowv, row0, col0);
     __syncthreads();
     const int t = threadIdx.x;

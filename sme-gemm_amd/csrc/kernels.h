@@ -67,6 +67,11 @@ hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint
 
 // MFMA GEMM over any weight kind (Q4 / Q2 / Q1 dequantized to f16/bf16 in LDS,
 // or dense), C[i,j] at dst[i*rs + j*cs] = ep(to16(beta * acc)).
+// A graph of more than EP_FUSED nodes over an m x n C whose cells hold the
+// product rounded to T (ep_tail, gemm_mfma.hip): src and dst may be the same
+// array; add_dst adds alpha * old dst after the graph.
+hipError_t launch_ep_tail(const uint16_t *src, long src_rs, long src_cs, uint16_t *dst, long dst_rs, long dst_cs,
+                          size_t m, size_t n, float alpha, bool add_dst, const EpLong &ep, bool bf16, hipStream_t s);
 hipError_t launch_gemm(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,
                        const uint16_t *lhs, long lhs_cs, long lhs_rs, float beta,
                        const EpArgs &ep, bool bf16, hipStream_t s, bool read_dst = false,

@@ -95,9 +95,14 @@ __global__ void __launch_bounds__(MF_WAVES * 64) q4_gemv_mfma(Q4GemvArgs g, EpAr
 // -- everything the loads need -- are what the dispatcher preloads into SGPRs
 // (this file is compiled with kernarg preloading), so a wave's first loads do
 // not wait on a kernel-argument fetch; the op-graph arguments that follow are
-// read only at the store. Each wave stages its own activations (q4_wave_loop),
-// so the one workgroup barrier is the partial-tile reduction's. Block 32, k a
-// multiple of 8 (16-byte activation rows), grids under 2 GiB; misc = m.
+// read only at the store, and only when the op-graph has nodes: misc = m |
+// n_nodes << 8 carries its length in a preloaded dword, so a plain call's
+// store reads no kernel argument (a scalar load of a line no earlier
+// instruction touched would otherwise stand between every workgroup's
+// reduction and its store). Each wave stages its own activations
+// (q4_wave_loop), so the one workgroup barrier is the partial-tile
+// reduction's. Block 32, k a multiple of 8 (16-byte activation rows), grids
+// under 2 GiB.
 // ---------------------------------------------------------------------------
 template <int MR, bool BF16, bool AFFINE>
 __global__ void __launch_bounds__(MF_WAVES * 64)
@@ -110,7 +115,7 @@ __global__ void __launch_bounds__(MF_WAVES * 64)
     const int t = threadIdx.x;
     const uint32_t tile = xcd_tile(blockIdx.x, tiles);
     const uint32_t col = tile * 16 + (t & 15);  // < n_pad
-    const uint32_t m = misc;
+    const uint32_t m = misc & 0xFF, n_nodes = misc >> 8;
     const uint32_t grid_rows = (nchunks + 3) & ~3u;  // the nibble and (block 32) scale grids' rows
     Q4WaveArgs g;
     g.nr = make_rsrc(nib, grid_rows * n_pad * 16u);
@@ -132,7 +137,8 @@ __global__ void __launch_bounds__(MF_WAVES * 64)
         const int cc = t / MR, r = t % MR;
         const float total = tile_total<MR>(red, cc, r);
         const uint32_t j = tile * 16 + cc;
-        if (r < (int)m && j < n) dst[(size_t)r * n + j] = finish<BF16>(ep, total, r, j, n);
+        if (r < (int)m && j < n)
+            dst[(size_t)r * n + j] = n_nodes == 0 ? from_f32<BF16>(total) : finish<BF16>(ep, total, r, j, n);
     }
 }
 
@@ -326,7 +332,7 @@ hipError_t launch_wave(const Q4GemvArgs &g, const EpArgs &ep, hipStream_t s) {
     }
     const uint32_t tiles = g.n_pad / 16;
     hipLaunchKernelGGL((q4_gemv_wave<MR, BF16, AFFINE>), dim3(tiles), dim3(MF_WAVES * 64), lds, s, g.nib, g.sc,
-                       g.lhs, g.dst, g.n_pad, g.nchunks, g.k, g.n, tiles, g.m, g.mn, ep);
+                       g.lhs, g.dst, g.n_pad, g.nchunks, g.k, g.n, tiles, g.m | (ep.n_nodes << 8), g.mn, ep);
     return hipGetLastError();
 }
 

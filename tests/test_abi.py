@@ -155,7 +155,14 @@ def test_c_boundary_refuses_operand_nodes_without_a_pointer(lib):
     assert check([smg.EpNode(0, 0, 1.0, None, 0), smg.EpNode(8, 3, 0.0, None, 0)]) == 0
     assert check([smg.EpNode(25, 0, 0.0, None, 0)]) == -1       # unknown op
     assert check([smg.EpNode(8, 25, 0.0, None, 0)]) == -1       # unknown activation
-    assert check([smg.EpNode(0, 0, 1.0, None, 0)] * 17) == -1   # too many nodes
+    # past the store's 16 nodes a graph runs as a pass over C, up to 64 nodes,
+    # each node checked alike
+    assert check([smg.EpNode(0, 0, 1.0, None, 0)] * 17) == 0
+    assert check([smg.EpNode(0, 0, 1.0, None, 0)] * 64) == 0
+    assert check([smg.EpNode(0, 0, 1.0, None, 0)] * 65) == -1   # too many nodes
+    assert check([smg.EpNode(0, 0, 1.0, None, 0)] * 40 + [smg.EpNode(4, 0, 0.0, None, 0)]) == -1
+    assert b"null operand" in lib.smg_last_error()
+    assert check([smg.EpNode(0, 0, 1.0, None, 0)] * 30 + [smg.EpNode(6, 0, 0.0, buf.ctypes.data, 7)]) == -1
     assert lib.smg_ep_check(None, 8) == 0                       # no epilogue
     d = smg.EpDesc16(1, None)
     assert lib.smg_ep_check(C.addressof(d), 8) == -1            # n_nodes without nodes
