@@ -263,34 +263,70 @@ template <int CTRL>
 __device__ __forceinline__ uint32_t dpp(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
 }
+// (The DPP moves zero their out-of-row lanes, bound_ctrl, which these row
+// permutations never read: the compiler then folds each move into the max or
+// add that consumes it.)
+template <int CTRL>
+__device__ __forceinline__ uint32_t dppz(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
 __device__ __forceinline__ uint32_t group_max_u32(uint32_t a, uint32_t gl) {
-    if (gl > 1) a = max(a, dpp<0xB1>(a));   // quad_perm [1,0,3,2]
-    if (gl > 2) a = max(a, dpp<0x4E>(a));   // quad_perm [2,3,0,1]
-    if (gl > 4) a = max(a, dpp<0x141>(a));  // row_half_mirror
-    if (gl > 8) a = max(a, dpp<0x140>(a));  // row_mirror
+    if (gl > 1) a = max(a, dppz<0xB1>(a));   // quad_perm [1,0,3,2]
+    if (gl > 2) a = max(a, dppz<0x4E>(a));   // quad_perm [2,3,0,1]
+    if (gl > 4) a = max(a, dppz<0x141>(a));  // row_half_mirror
+    if (gl > 8) a = max(a, dppz<0x140>(a));  // row_mirror
     if (gl > 16) a = max(a, (uint32_t)__shfl_xor((int)a, 16));
     if (gl > 32) a = max(a, (uint32_t)__shfl_xor((int)a, 32));
     return a;
 }
 __device__ __forceinline__ int32_t group_sum_i32(int32_t a, uint32_t gl) {
-    if (gl > 1) a += (int32_t)dpp<0xB1>((uint32_t)a);
-    if (gl > 2) a += (int32_t)dpp<0x4E>((uint32_t)a);
-    if (gl > 4) a += (int32_t)dpp<0x141>((uint32_t)a);
-    if (gl > 8) a += (int32_t)dpp<0x140>((uint32_t)a);
+    if (gl > 1) a += (int32_t)dppz<0xB1>((uint32_t)a);
+    if (gl > 2) a += (int32_t)dppz<0x4E>((uint32_t)a);
+    if (gl > 4) a += (int32_t)dppz<0x141>((uint32_t)a);
+    if (gl > 8) a += (int32_t)dppz<0x140>((uint32_t)a);
     if (gl > 16) a += __shfl_xor(a, 16);
     if (gl > 32) a += __shfl_xor(a, 32);
     return a;
 }
 
-// LDS: q [MR][kq + 16] i8, for one row later the fold's y [16 CG][nbq + 4]
-//      f32 (the products have read q by then) | s [MR][nbq] f32 |
-//      -sum(q) [MR][nbq] i32 | block sums [MR][16 CG][nbq + 4] i32 (for one
-//      row then the fold's x, f32) | scales [16 CG][nbq + 4] f16 | wave partials
-__host__ __device__ inline uint32_t tile_q_region(uint32_t kq, uint32_t nbq, uint32_t mr, uint32_t cg) {
-    const uint32_t q = mr * (kq + 16), y = mr == 1 ? 16 * cg * (nbq + 4) * 4 : 0;
-    return q > y ? q : y;
+// Four f16 activations (two dwords) quantized with the block's inv and packed
+// into four int8 bytes: f32(a) * inv with one rounding (v_fma_mix_f32: the f16
+// operand widened exactly, a -0 addend leaves the product as it is), ties to
+// even (v_rndne_f32), then v_cvt_i32_f32, whose NaN gives 0 as the reference's
+// quantize_row does. No clamp is needed: |a| <= amax, inv <= 127/amax * (1 +
+// 2^-24), so |a * inv| rounds to at most 127 (and inv = 0 when amax is 0, inf
+// or NaN, leaving 0 or NaN).
+__device__ __forceinline__ uint32_t quant4(uint32_t w0, uint32_t w1, float inv) {
+    float f[4];
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(f[0]) : "v"(w0), "v"(inv), "v"(-0.0f));
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(f[1]) : "v"(w0), "v"(inv), "v"(-0.0f));
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(f[2]) : "v"(w1), "v"(inv), "v"(-0.0f));
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(f[3]) : "v"(w1), "v"(inv), "v"(-0.0f));
+    uint32_t q[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float r = __builtin_rintf(f[e]);
+        asm("v_cvt_i32_f32 %0, %1" : "=v"(q[e]) : "v"(r));
+    }
+    const uint32_t lo = __builtin_amdgcn_perm(q[1], q[0], 0x0c0c0400u);  // {q0, q1, 0, 0} (low bytes)
+    const uint32_t hi = __builtin_amdgcn_perm(q[3], q[2], 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
-size_t tile_lds_bytes(uint32_t kq, uint32_t nbq, int mr, uint32_t cg) {
+
+// LDS: q [MR][kq + 16] i8, for one row later the fold's y and x, each [16
+//      CG][nbq + 4] f32 (the products have read q by then) | s [MR][nbq] f32 |
+//      -sum(q) [MR][nbq] i32 | block sums [MR][16 CG][nbq + 4] i32 (one row:
+//      [nbq][16 CG], a lane's four columns in one 16-byte store) | scales [16
+//      CG][nbq + 4] f16 | wave partials
+__host__ __device__ inline uint32_t tile_q_region(uint32_t kq, uint32_t nbq, uint32_t mr, uint32_t cg) {
+    const uint32_t q = mr * (kq + 16), xy = mr == 1 ? 2 * 16 * cg * (nbq + 4) * 4 : 0;
+    return q > xy ? q : xy;
+}
+// The one-row layout for blocks of 128 (fast, the usual decode call): q [kq
+// + 16] i8 | 64 zero bytes | s [nbq] f32 | -sum(q) [nbq] i32 | the fold's (x,
+// y) pairs [16 CG][nbq + 2] | wave partials.
+size_t tile_lds_bytes(uint32_t kq, uint32_t nbq, int mr, uint32_t cg, bool fast) {
+    if (fast) return (size_t)kq + 16 + 64 + (size_t)nbq * 8 + (size_t)16 * cg * (nbq + 2) * 8 + (size_t)WV * 8;
     return (size_t)tile_q_region(kq, nbq, (uint32_t)mr, cg) + (size_t)mr * nbq * 8 +
            (size_t)mr * 16 * cg * (nbq + 4) * 4 + (size_t)16 * cg * (nbq + 4) * 2 + (size_t)mr * WV * 8;
 }
@@ -302,11 +338,15 @@ size_t tile_lds_bytes(uint32_t kq, uint32_t nbq, int mr, uint32_t cg) {
 // it to 2*sum(q*b)).
 // A block's amax and sum(q) reduce over its lanes by DPP / shuffles, and
 // through the LDS words wmax / wsum ([MR][WV]) for blocks longer than 512.
-template <int KIND, int MR>
+// BSH: the block's log2 when fixed at compile time (7: blocks of 128, the
+// usual decode format), 0 for the runtime block_shift.
+template <int KIND, int MR, int BSH = 0>
 __device__ __forceinline__ void quant_pass(const uint4 (&ar)[MR], uint32_t p, int8_t *q, uint32_t qstride,
                                            float *s, int32_t *sum_out, uint32_t nbq, uint32_t kq,
                                            uint32_t block_shift, float *wmax, int32_t *wsum) {
+    typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    if constexpr (BSH > 0) block_shift = BSH;
     const uint32_t block = 1u << block_shift;
     const uint32_t gl = block / 8 < 64u ? block / 8 : 64u;  // lanes of a block in a wave
     const uint32_t wpb = block > 512u ? block / 512u : 1u;   // waves of a block
@@ -317,11 +357,13 @@ __device__ __forceinline__ void quant_pass(const uint4 (&ar)[MR], uint32_t p, in
     float am[MR];
 #pragma unroll
     for (int r = 0; r < MR; r++) {
-        const uint32_t w0 = ar[r].x & 0x7FFF7FFFu, w1 = ar[r].y & 0x7FFF7FFFu;
-        const uint32_t w2 = ar[r].z & 0x7FFF7FFFu, w3 = ar[r].w & 0x7FFF7FFFu;
-        const uint32_t lo = max(max(w0 & 0xFFFFu, w1 & 0xFFFFu), max(w2 & 0xFFFFu, w3 & 0xFFFFu));
-        const uint32_t hi = max(max(w0 >> 16, w1 >> 16), max(w2 >> 16, w3 >> 16));
-        am[r] = f16_to_f32((uint16_t)group_max_u32(max(lo, hi), gl));
+        const u16x2_t w0 = __builtin_bit_cast(u16x2_t, ar[r].x & 0x7FFF7FFFu);
+        const u16x2_t w1 = __builtin_bit_cast(u16x2_t, ar[r].y & 0x7FFF7FFFu);
+        const u16x2_t w2 = __builtin_bit_cast(u16x2_t, ar[r].z & 0x7FFF7FFFu);
+        const u16x2_t w3 = __builtin_bit_cast(u16x2_t, ar[r].w & 0x7FFF7FFFu);
+        const u16x2_t mx = __builtin_elementwise_max(__builtin_elementwise_max(w0, w1),
+                                                     __builtin_elementwise_max(w2, w3));
+        am[r] = f16_to_f32((uint16_t)group_max_u32(max((uint32_t)mx.x, (uint32_t)mx.y), gl));
     }
     if (wpb > 1) {  // blocks longer than a wave: combine the waves' maxima
         if (p > 0) __syncthreads();
@@ -340,20 +382,15 @@ __device__ __forceinline__ void quant_pass(const uint4 (&ar)[MR], uint32_t p, in
     int32_t qs[MR];
 #pragma unroll
     for (int r = 0; r < MR; r++) {
-        const uint32_t wd[4] = {ar[r].x, ar[r].y, ar[r].z, ar[r].w};
         const float inv = am[r] > 0.0f ? __fdiv_rn(127.0f, am[r]) : 0.0f;
-        uint32_t qw0 = 0, qw1 = 0;
-        int32_t sum = 0;
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float v = rintf(f16_to_f32((uint16_t)(wd[e / 2] >> (16 * (e % 2)))) * inv);
-            const int qi = (v != v) ? 0 : (int)fminf(fmaxf(v, -128.0f), 127.0f);
-            if (e < 4) qw0 |= ((uint32_t)qi & 0xFFu) << (8 * e);
-            else qw1 |= ((uint32_t)qi & 0xFFu) << (8 * (e - 4));
-            sum += qi;
-        }
+        const uint32_t qw0 = quant4(ar[r].x, ar[r].y, inv), qw1 = quant4(ar[r].z, ar[r].w, inv);
         if (d0 < kq) *(uint2 *)(q + r * qstride + d0) = make_uint2(qw0, qw1);
-        qs[r] = KIND == 1 ? group_sum_i32(sum, gl) : 0;
+        if constexpr (KIND == 1) {
+            const int32_t sum = __builtin_amdgcn_sdot4((int)qw1, 0x01010101, __builtin_amdgcn_sdot4((int)qw0, 0x01010101, 0, false), false);
+            qs[r] = group_sum_i32(sum, gl);
+        } else {
+            qs[r] = 0;
+        }
     }
     if (KIND == 1 && wpb > 1) {
         if (lane == 0)
@@ -416,7 +453,8 @@ __global__ void __launch_bounds__(T)
     constexpr int NSW = NG * (int)SPG;            // slabs per wave
     constexpr int QP = 2;                         // A passes held in registers (K <= 8192)
     constexpr int PQ = 4;                         // pre-quantized block entries per thread
-    const uint32_t m = misc & 0xFF, block_shift = (misc >> 8) & 0xFF, cg_shift = misc >> 16;
+    // SPB 2: blocks of 128 (the host launches SPB 2 only for them)
+    const uint32_t m = misc & 0xFF, block_shift = SPB == 2 ? 7u : (misc >> 8) & 0xFF, cg_shift = misc >> 16;
     const uint32_t block = 1u << block_shift;
     // the host's geometry (tile_geometry_cg): 8 / CG waves along K cover kq
     const uint32_t kq = (8u >> cg_shift) * NSW * LB_SLAB;
@@ -427,13 +465,25 @@ __global__ void __launch_bounds__(T)
     const uint32_t ncol = 16 * cg;
     const uint32_t qs_ = kq + 16;   // q row stride (bytes)
     const uint32_t bs = nbq + 4;    // block-sum / scale row stride (elements)
+    // FAST: one row, blocks of 128 (tile_lds_bytes' fast layout). Each wave's
+    // products put block b of its range in row b of the MFMA output (the B
+    // operand's column b holds q on that block's slabs, zeros elsewhere), so
+    // the lanes that hold a block's sums form the fold's factors right after
+    // the products, with the scales they loaded themselves.
+    constexpr bool FAST = MR == 1 && SPB == 2;
+    constexpr int NBW = SPB > 0 ? NSW / SPB : 1;  // blocks per wave (SPB > 0)
+    static_assert(!FAST || NBW <= 16, "a wave's blocks are rows of one product tile");
+    const uint32_t bs2 = nbq + 2;   // (x, y) pair row stride (FAST)
     int8_t *ql = (int8_t *)smem;                        // [MR][qs_]
+    const int8_t *zq = ql + qs_;                        // 64 zero bytes (FAST)
     float *yl = (float *)smem;                          // [ncol][bs] (one row), after the products
-    float *sa = (float *)(smem + tile_q_region(kq, nbq, MR, cg));  // [MR][nbq]
+    float *xl = yl + ncol * bs;                         // [ncol][bs] (one row), after the products
+    float *sa = (float *)(smem + (FAST ? qs_ + 64 : tile_q_region(kq, nbq, MR, cg)));  // [MR][nbq]
     int32_t *as = (int32_t *)(sa + MR * nbq);           // [MR][nbq]
+    float2 *xy = (float2 *)(as + MR * nbq);             // [ncol][bs2] (FAST)
     int32_t *sb = as + MR * nbq;                        // [MR][ncol][bs]
     uint16_t *scl = (uint16_t *)(sb + MR * ncol * bs);  // [ncol][bs]
-    float *wmax = (float *)(scl + ncol * bs);           // [MR][WV]
+    float *wmax = FAST ? (float *)(xy + ncol * bs2) : (float *)(scl + ncol * bs);  // [MR][WV]
     int32_t *wsum = (int32_t *)(wmax + MR * WV);        // [MR][WV]
 
     const int t = threadIdx.x;
@@ -475,12 +525,19 @@ __global__ void __launch_bounds__(T)
     // scale rows next (waited on before the first barrier), then the codes,
     // then the epilogue operands: vmcnt retires in issue order, so the codes
     // can still be in flight when the waits before them end
-    uint4 sreg;
+    uint4 sreg = {};
+    uint2 sreg4 = {};  // FAST: the scales of this lane's block and four columns
+    const uint32_t fb = kw * NBW + (uint32_t)c;  // FAST: this lane's block (c < NBW)
     {
         const rsrc_t sr = make_rsrc(sc, ((sc_rows + 3) & ~3u) * n_pad * 2u);
-        const uint32_t bb = t >> (cg_shift + 1), piece = t & (2 * cg - 1);  // 8 columns a piece
-        sreg = bload16(sr, (bb < nbq && bb < sc_rows) ? (uint32_t)cell_index(bb, wg_col0 + piece * 8, sc_rows, n_pad) * 2u
-                                                      : OOB);
+        if constexpr (FAST) {
+            sreg4 = bload8(sr, ((uint32_t)c < (uint32_t)NBW && fb < sc_rows)
+                                   ? (uint32_t)cell_index(fb, col0 + 4 * gq4, sc_rows, n_pad) * 2u : OOB);
+        } else {
+            const uint32_t bb = t >> (cg_shift + 1), piece = t & (2 * cg - 1);  // 8 columns a piece
+            sreg = bload16(sr, (bb < nbq && bb < sc_rows)
+                                   ? (uint32_t)cell_index(bb, wg_col0 + piece * 8, sc_rows, n_pad) * 2u : OOB);
+        }
     }
     uint4 wreg[NG];
     {
@@ -495,8 +552,8 @@ __global__ void __launch_bounds__(T)
     // and pinned to a register of its own: the compiler can otherwise build it
     // late with a 64-bit multiply-add whose unused high half is a register
     // one of those loads targets, and wait for that load
-    uint32_t dp_off = (c * ncol + gi * 16 + 4 * gq4) * bs;
-    asm volatile("" : "+v"(dp_off));
+    uint32_t dp_off = FAST ? 0u : (c * ncol + gi * 16 + 4 * gq4) * bs;
+    if constexpr (!FAST) asm volatile("" : "+v"(dp_off));
     const bool folder = (uint32_t)t < ncol * m;
     const int fc = t & (ncol - 1), frow = t >> (4 + cg_shift);
 
@@ -513,6 +570,10 @@ __global__ void __launch_bounds__(T)
         // the activation's kernel arguments are read here, not after the
         // fold, where their scalar load would sit on the kernel's last steps
         asm volatile("" : "+s"(act), "+s"(alpha));
+    } else if constexpr (EPV == 1) {
+        // n (past the preloaded arguments) likewise: read while the codes are
+        // in flight, not at the store
+        asm volatile("" : "+s"(n));
     }
 
     // -- 2. quantize A (quantize_row, src/kernels/lowbit/matmul.rs:354-371),
@@ -533,16 +594,19 @@ __global__ void __launch_bounds__(T)
 #pragma unroll
         for (int p = 0; p < QP; p++) {
             if ((uint32_t)p * QPASS >= kq) break;  // uniform
-            quant_pass<KIND, MR>(areg[p], p, ql, qs_, sa, as, nbq, kq, block_shift, wmax, wsum);
+            quant_pass<KIND, MR, SPB == 2 ? 7 : 0>(areg[p], p, ql, qs_, sa, as, nbq, kq, block_shift, wmax, wsum);
         }
     }
-    if ((uint32_t)t < 2 * cg * nbq) {  // transpose: scale of (block bb, column 8 piece + e)
+    if constexpr (FAST) {
+        if (t < 4) *(uint4 *)(ql + qs_ + 16 * t) = make_uint4(0, 0, 0, 0);  // the zero B operand
+    } else if ((uint32_t)t < 2 * cg * nbq) {  // transpose: scale of (block bb, column 8 piece + e)
         const uint32_t bb = t >> (cg_shift + 1), piece = t & (2 * cg - 1);
         const uint32_t sw[4] = {sreg.x, sreg.y, sreg.z, sreg.w};
 #pragma unroll
         for (int e = 0; e < 8; e++) scl[(8 * piece + e) * bs + bb] = (uint16_t)(sw[e / 2] >> (16 * (e % 2)));
     }
     __syncthreads();
+    const uint32_t nb_live = (k + block - 1) >> block_shift;
 
     // -- 3. exact block sums on the matrix cores: A = 16 columns x 64 depths
     //       of expanded codes, B = 64 depths x up to 16 rows of q
@@ -576,7 +640,51 @@ __global__ void __launch_bounds__(T)
         return __builtin_bit_cast(int4_t, *(const uint4 *)(ql + (c < MR ? c : 0) * qs_ + slab * LB_SLAB + 16 * gq4));
     };
     constexpr int PF = NSW < 8 ? NSW : 8;  // slabs whose q is read ahead at once
-    if constexpr (SPB > 0) {
+    if constexpr (FAST) {
+        // B column c is q on block c's slabs (slab i belongs to block i / 2)
+        // and zero elsewhere: one address select per slab
+        auto qloadf = [&](int i) {
+            const uint32_t slab = kw * NSW + i;
+            const int8_t *pa = (c == i / SPB) ? ql + slab * LB_SLAB + 16 * gq4 : zq + 16 * gq4;
+            return __builtin_bit_cast(int4_t, *(const uint4 *)pa);
+        };
+        int4_t acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};  // a block's first and second slab
+#pragma unroll
+        for (int i0 = 0; i0 < NSW; i0 += PF) {
+            int4_t qv[PF];
+#pragma unroll
+            for (int j = 0; j < PF; j++) qv[j] = qloadf(i0 + j);
+#pragma unroll
+            for (int j = 0; j < PF; j++) {
+                if ((i0 + j) % 2 == 0) acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(i0 + j), qv[j], acc0, 0, 0, 0);
+                else acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(i0 + j), qv[j], acc1, 0, 0, 0);
+            }
+        }
+        // lane (gq4, c < NBW): block fb's sums of columns 4 gq4 + v; its fold
+        // factors x = f32(sum) (Q1: 2 sum(q b) + (-sum(q))) and y =
+        // f32(scale) * s by v_fma_mix (the f16 scale widened exactly, one
+        // rounding, the -0 addend leaves the product as it is); blocks past K
+        // give x = y = 0
+        if ((uint32_t)c < (uint32_t)NBW) {
+            const float s_b = sa[fb];
+            const int32_t a_b = KIND == 1 ? as[fb] : 0;
+            const bool live = fb < nb_live;
+            float2 *xo = xy + (gi * 16 + 4 * gq4) * bs2 + fb;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int32_t sum = acc0[v] + acc1[v];
+                float x = (float)(KIND == 1 ? 2 * sum + a_b : sum), y;
+                const uint32_t cw = v < 2 ? sreg4.x : sreg4.y;
+                if (v % 2 == 0)
+                    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(y) : "v"(cw), "v"(s_b), "v"(-0.0f));
+                else
+                    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                        : "=v"(y) : "v"(cw), "v"(s_b), "v"(-0.0f));
+                if (!live) x = y = 0.0f;
+                xo[v * bs2] = make_float2(x, y);
+            }
+        }
+    } else if constexpr (SPB > 0) {
         // blocks of SPB slabs, whole inside this wave's range; independent
         // accumulators, written after the last product
         constexpr int NBW = NSW / SPB;
@@ -593,7 +701,15 @@ __global__ void __launch_bounds__(T)
                 acc[(i0 + j) / SPB] =
                     __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(i0 + j), qv[j], acc[(i0 + j) / SPB], 0, 0, 0);
         }
-        if (c < MR) {
+        if constexpr (MR == 1) {
+            // row 0's lanes (c = 0) store their four columns' sums of each
+            // block at once: [block][column]
+            if (c == 0) {
+                int32_t *o = sb + kw * NBW * ncol + gi * 16 + 4 * gq4;
+#pragma unroll
+                for (int b = 0; b < NBW; b++) *(int4_t *)(o + b * ncol) = acc[b];
+            }
+        } else if (c < MR) {
             // block kw * NBW + b < kq / block <= nbq (the waves hold whole
             // blocks); one base offset per column, held in a register of its
             // own, and the block as the stores' immediate offset
@@ -653,21 +769,45 @@ __global__ void __launch_bounds__(T)
     //       addend leaves every product as it is), then total = fmaf(x, y,
     //       total). Blocks past K add fmaf(0, 0, total) == total (total starts
     //       at +0 and never becomes -0, so its bits are unchanged).
-    const uint32_t nb_live = (k + block - 1) >> block_shift;
     float total = 0.0f;
-    if constexpr (MR == 1) {
+    if constexpr (FAST) {
+        // (x, y) of blocks 0 .. nb_live - 1 in order, two blocks a 16-byte
+        // load: whole groups of 16 blocks, then the last group's live pairs
+        // (a wave's range is an even number of blocks, so a pair that starts
+        // below nb_live was written)
+        if (folder) {
+            const float *xp = (const float *)(xy + fc * bs2);
+            auto group16 = [&](uint32_t b0, auto tail_tag) {
+                constexpr bool TAIL = decltype(tail_tag)::value;
+                float4_t v4[8];
+#pragma unroll
+                for (int h = 0; h < 8; h++) {
+                    const bool live = !TAIL || b0 + 2 * h < nb_live;
+                    v4[h] = *(const float4_t *)(xp + 2 * (live ? b0 + 2 * h : 0));
+                    if (TAIL && !live) v4[h] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
+                }
+#pragma unroll
+                for (int h = 0; h < 8; h++) {
+                    total = fmaf(v4[h][0], v4[h][1], total);
+                    total = fmaf(v4[h][2], v4[h][3], total);
+                }
+            };
+            const uint32_t nb16 = nb_live & ~15u;
+            for (uint32_t b0 = 0; b0 < nb16; b0 += 16) group16(b0, std::false_type{});
+            if (nb16 < nb_live) group16(nb16, std::true_type{});
+        }
+    } else if constexpr (MR == 1) {
         // one row: 16 * CG folding lanes, so every thread first computes a
-        // few blocks' x and y (x in place of the sum), and the folding lanes
-        // then only load them, 16 blocks per four LDS loads, and run the fmas
+        // few blocks' x and y, and the folding lanes then only load them, 16
+        // blocks per four LDS loads, and run the fmas
         const uint32_t nbf = (nb_live + 3) & ~3u;  // <= nbq; x = y = 0 past nb_live
         {
-            float *xl = (float *)sb;
             const uint32_t j = t & (ncol - 1), bstep = (uint32_t)T >> (4 + cg_shift);
             for (uint32_t b = (uint32_t)t >> (4 + cg_shift); b < nbf; b += bstep) {
                 const uint32_t e = j * bs + b;
                 float x = 0.0f, y = 0.0f;
                 if (b < nb_live) {
-                    const int32_t sum = sb[e];
+                    const int32_t sum = SPB > 0 ? sb[b * ncol + j] : sb[e];  // the products' layouts
                     x = (float)(KIND == 1 ? 2 * sum + as[b] : sum);
                     const uint32_t cw = scl[e];
                     asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(y) : "v"(cw), "v"(sa[b]), "v"(-0.0f));
@@ -678,7 +818,7 @@ __global__ void __launch_bounds__(T)
         }
         __syncthreads();
         if (folder) {
-            const float *xp = (const float *)sb + fc * bs;
+            const float *xp = xl + fc * bs;
             const float *yp = yl + fc * bs;
             auto group16 = [&](uint32_t b0, auto tail_tag) {
                 constexpr bool TAIL = decltype(tail_tag)::value;
@@ -770,7 +910,7 @@ __global__ void __launch_bounds__(T)
 
 template <int KIND, int MR, int NG, int SPB, int EPV>
 hipError_t launch_tile_v(const LtArgs &g, const EpArgs &ep, const EpPick &pk, hipStream_t s) {
-    const size_t lds = tile_lds_bytes(g.kq, g.nbq, MR, 1u << g.cg_shift);
+    const size_t lds = tile_lds_bytes(g.kq, g.nbq, MR, 1u << g.cg_shift, MR == 1 && SPB == 2);
     if (lds > 64 * 1024) {
         static bool attr = false;  // benign race: every setter writes the same value
         if (!attr) {
@@ -952,7 +1092,7 @@ TileGeo tile_geometry_cg(const WDev &w, size_t m, uint32_t cg_shift) {
     if (w.block > (size_t)ng * spg * LB_SLAB) return sg;
     const size_t nbq = (kq / w.block + 3) / 4 * 4;  // whole 16-byte runs of blocks
     const size_t cg = (size_t)1 << cg_shift;
-    if (2 * cg * nbq > (size_t)T || tile_lds_bytes((uint32_t)kq, (uint32_t)nbq, mr, (uint32_t)cg) > 96 * 1024)
+    if (2 * cg * nbq > (size_t)T || tile_lds_bytes((uint32_t)kq, (uint32_t)nbq, mr, (uint32_t)cg, mr == 1 && w.block == 128) > 96 * 1024)
         return sg;
     if (mr > 1 && (size_t)mr * nbq > (size_t)4 * T) return sg;  // pre-quantized entries per thread (PQ)
     sg.ok = true;
