@@ -96,6 +96,9 @@ __device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t off) {
 __device__ __forceinline__ uint2 bload8(rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
 }
+__device__ __forceinline__ uint2 bload8_nt(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 2));
+}
 
 // 8 consecutive 16-bit elements A[row][d..d+8) of a row-major [rows][k] array
 // at `r` (zero outside rows x k). vec: k % 8 == 0, so rows are 16-byte aligned

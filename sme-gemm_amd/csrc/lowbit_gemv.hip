@@ -23,6 +23,7 @@
 //   using sum(q*(2b-1)) = 2*sum(q*b) - sum(q)), B operand = 64 depths x up to 16
 //   rows of q. Sums go to LDS; then one lane per output folds them in block
 //   order -- the only sequential step, and it is one fma per block.
+#include <algorithm>
 #include <type_traits>
 
 #include "kernels.h"
@@ -438,28 +439,35 @@ __global__ void __launch_bounds__(T) lowbit_prequant(const uint16_t *lhs, uint32
 // trailing activation act (0: none, alpha its scalar), 3 mul_col(col_a),
 // add_col(col_b), then act. Each runs the graph's f32 steps in its order on
 // the f16-rounded sum, as the generic store does.
-// The first 14 argument dwords -- all that the first loads need -- arrive in
-// SGPRs with the wave (this file is compiled with kernarg preloading); the
-// rest derive from them: misc = m | block_shift << 8 | cg_shift << 16, src is
-// A (f16 [m][k], one row) or its pre-quantized rows (int8 [m][kq], several).
+// The first 14 argument dwords arrive in SGPRs with the wave (this file is
+// compiled with kernarg preloading): everything but col_a, alpha and the
+// interpreted graph, so no scalar load of an argument sits on the kernel's
+// path. The rest derive from them: misc = m | block_shift << 8 | cg_shift <<
+// 16 | act << 24; n_pad = n rounded up to 128 (every weight handle's grid);
+// the code groups per column, ceil(k / group depths); src is A (f16 [m][k],
+// one row) or its pre-quantized rows (int8 [m][kq], several), followed by
+// their block scales and negated sums (lowbit_prequant's layout).
 template <int KIND, int MR, int NG, int SPB, int EPV>
 __global__ void __launch_bounds__(T)
-    lowbit_tile(const uint8_t *codes, const uint16_t *sc, const void *src, uint16_t *dst, uint32_t n_pad, uint32_t k,
-                uint32_t tiles, uint32_t misc, uint32_t codebook, uint32_t ngroups, uint32_t n,
-                const uint16_t *col_a, const uint16_t *col_b, uint32_t act, float alpha, const float *qs,
-                const int32_t *qsum, EpArgs ep) {
+    lowbit_tile(const uint8_t *codes, const uint16_t *sc, const void *src, uint16_t *dst, const uint16_t *col_b,
+                uint32_t k, uint32_t misc, uint32_t n, uint32_t codebook, const uint16_t *col_a, float alpha,
+                EpArgs ep) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr uint32_t SPG = KIND == 2 ? 4 : 8;  // slabs per code group
     constexpr int NSW = NG * (int)SPG;            // slabs per wave
     constexpr int QP = 2;                         // A passes held in registers (K <= 8192)
     constexpr int PQ = 4;                         // pre-quantized block entries per thread
     // SPB 2: blocks of 128 (the host launches SPB 2 only for them)
-    const uint32_t m = misc & 0xFF, block_shift = SPB == 2 ? 7u : (misc >> 8) & 0xFF, cg_shift = misc >> 16;
+    const uint32_t m = misc & 0xFF, block_shift = SPB == 2 ? 7u : (misc >> 8) & 0xFF;
+    const uint32_t cg_shift = (misc >> 16) & 0xFF, act = misc >> 24;
+    const uint32_t n_pad = ((n ? n : 1u) + 127u) & ~127u;
+    const uint32_t tiles = n_pad >> (4 + cg_shift);
     const uint32_t block = 1u << block_shift;
     // the host's geometry (tile_geometry_cg): 8 / CG waves along K cover kq
     const uint32_t kq = (8u >> cg_shift) * NSW * LB_SLAB;
     const uint32_t nbq = ((kq >> block_shift) + 3) & ~3u;
     const uint32_t grp_depths = KIND == 2 ? Q2_GROUP : Q1_GROUP;
+    const uint32_t ngroups = (k + grp_depths - 1) / grp_depths;
     const uint32_t sc_rows = (ngroups * grp_depths + block - 1) >> block_shift;
     const uint32_t cg = 1u << cg_shift;           // 16-column groups in this workgroup
     const uint32_t ncol = 16 * cg;
@@ -507,13 +515,6 @@ __global__ void __launch_bounds__(T)
 #pragma unroll
         for (int r = 0; r < MR; r++)
             qreg[r] = bload16(qr, ((uint32_t)r < m && 16u * t < kq) ? r * kq + 16 * t : OOB);
-        const rsrc_t fr = make_rsrc(qs, m * nbq * 4u), ur = make_rsrc(qsum, m * nbq * 4u);
-#pragma unroll
-        for (int j = 0; j < PQ; j++) {
-            const uint32_t i = t + T * j;
-            pqs[j] = __uint_as_float(bload4(fr, i < m * nbq ? i * 4u : OOB));
-            pqsum[j] = (int32_t)bload4(ur, i < m * nbq ? i * 4u : OOB);
-        }
     } else {
 #pragma unroll
         for (int p = 0; p < QP; p++)
@@ -548,6 +549,23 @@ __global__ void __launch_bounds__(T)
             wreg[i] = bload16(cr, grp < ngroups ? ((uint32_t)cell_index(grp, col0 + c, ngroups, n_pad) * 4 + gq4) * 16 : OOB);
         }
     }
+    // every code load is issued before anything below: the scalar loads of
+    // the arguments past the preloaded ones (n, the epilogue's) must not be
+    // hoisted between them, where their wait would hold the later code loads
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (MR > 1) {
+        // the rows' block scales and sums: their pointers are arguments past
+        // the preloaded ones
+        const float *qs = (const float *)((const uint8_t *)src + ((m * kq + 255) & ~255u));
+        const int32_t *qsum = (const int32_t *)(qs + m * nbq);
+        const rsrc_t fr = make_rsrc(qs, m * nbq * 4u), ur = make_rsrc(qsum, m * nbq * 4u);
+#pragma unroll
+        for (int j = 0; j < PQ; j++) {
+            const uint32_t i = t + T * j;
+            pqs[j] = __uint_as_float(bload4(fr, i < m * nbq ? i * 4u : OOB));
+            pqsum[j] = (int32_t)bload4(ur, i < m * nbq ? i * 4u : OOB);
+        }
+    }
     // this lane's block-sum slot (step 3), computed before the epilogue loads
     // and pinned to a register of its own: the compiler can otherwise build it
     // late with a 64-bit multiply-add whose unused high half is a register
@@ -556,25 +574,6 @@ __global__ void __launch_bounds__(T)
     if constexpr (!FAST) asm volatile("" : "+v"(dp_off));
     const bool folder = (uint32_t)t < ncol * m;
     const int fc = t & (ncol - 1), frow = t >> (4 + cg_shift);
-
-    // the epilogue operands last: their addresses wait on the op-graph's
-    // kernel arguments, which must not hold up the codes
-    EpPre pre = {};
-    uint16_t opa = 0, opb = 0;
-    if constexpr (EPV == 0) {
-        if (folder && wg_col0 + fc < n) pre = ep_prefetch(ep, frow, wg_col0 + fc, n);
-    } else if constexpr (EPV >= 2) {
-        const uint32_t ob = folder && wg_col0 + fc < n ? (wg_col0 + fc) * 2u : OOB;
-        opb = bload2(make_rsrc(col_b, n * 2u), ob);
-        if constexpr (EPV == 3) opa = bload2(make_rsrc(col_a, n * 2u), ob);
-        // the activation's kernel arguments are read here, not after the
-        // fold, where their scalar load would sit on the kernel's last steps
-        asm volatile("" : "+s"(act), "+s"(alpha));
-    } else if constexpr (EPV == 1) {
-        // n (past the preloaded arguments) likewise: read while the codes are
-        // in flight, not at the store
-        asm volatile("" : "+s"(n));
-    }
 
     // -- 2. quantize A (quantize_row, src/kernels/lowbit/matmul.rs:354-371),
     //       or store the rows quantized beforehand
@@ -597,6 +596,19 @@ __global__ void __launch_bounds__(T)
             quant_pass<KIND, MR, SPB == 2 ? 7 : 0>(areg[p], p, ql, qs_, sa, as, nbq, kq, block_shift, wmax, wsum);
         }
     }
+    // the epilogue operands after the quantization: their addresses wait on
+    // scalar loads of kernel arguments, which must hold up neither the codes
+    // nor the quantization (the operands are used only at the store)
+    EpPre pre = {};
+    uint16_t opa = 0, opb = 0;
+    if constexpr (EPV == 0) {
+        if (folder && wg_col0 + fc < n) pre = ep_prefetch(ep, frow, wg_col0 + fc, n);
+    } else if constexpr (EPV >= 2) {
+        const uint32_t ob = folder && wg_col0 + fc < n ? (wg_col0 + fc) * 2u : OOB;
+        opb = bload2(make_rsrc(col_b, n * 2u), ob);
+        if constexpr (EPV == 3) opa = bload2(make_rsrc(col_a, n * 2u), ob);
+    }
+
     if constexpr (FAST) {
         if (t < 4) *(uint4 *)(ql + qs_ + 16 * t) = make_uint4(0, 0, 0, 0);  // the zero B operand
     } else if ((uint32_t)t < 2 * cg * nbq) {  // transpose: scale of (block bb, column 8 piece + e)
@@ -908,6 +920,231 @@ __global__ void __launch_bounds__(T)
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// One row, blocks of 128 (the usual decode call), persistent: one workgroup
+// per compute unit (grid G = min(tiles, CUs)), workgroup g taking tiles g, g
+// + G, ... (up to TPW of them). Two workgroups on one compute unit were
+// measured to serialize: the second one's activation loads queue behind the
+// first one's weight stream, so it quantizes ~1.2 us later. Here a compute
+// unit issues A first, then every tile's scales and codes, quantizes A once,
+// and multiplies its tiles as their codes land:
+//   1. loads: A (f16, one 4096-depth pass per thread), then per tile the
+//      lane's scales (its block, four columns) and code groups;
+//   2. quant_pass into LDS (shared by the tiles), one barrier;
+//   3. per tile, the products put block c of the wave's range in output row
+//      c (the B operand's column c holds q on that block's slabs, zero
+//      elsewhere), and the lanes holding a block's sums form its fold factors
+//      x = f32(sum) (Q1: 2 sum(q b) + (-sum(q))) and y = f32(scale) * s;
+//   4. one barrier, then one thread per (tile, column) folds its blocks in
+//      order (fmaf), runs the op-graph and stores.
+// misc = cg_shift | act << 8. LDS: q [kq + 16] i8 | 64 zero bytes | s [nbq]
+// f32 | -sum(q) [nbq] i32 | (x, y) [TPW][16 CG][nbq + 2] | wave partials.
+// ---------------------------------------------------------------------------
+size_t row_lds_bytes(uint32_t kq, uint32_t nbq, uint32_t cg, int tpw) {
+    return (size_t)kq + 16 + 64 + (size_t)nbq * 8 + (size_t)tpw * 16 * cg * (nbq + 2) * 8 + (size_t)WV * 8;
+}
+
+template <int KIND, int NG, int EPV, int TPW>
+__global__ void __launch_bounds__(T)
+    lowbit_row(const uint8_t *codes, const uint16_t *sc, const uint16_t *lhs, uint16_t *dst, const uint16_t *col_b,
+               uint32_t k, uint32_t misc, uint32_t n, uint32_t codebook, const uint16_t *col_a, float alpha,
+               EpArgs ep) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr uint32_t SPG = KIND == 2 ? 4 : 8;  // slabs per code group
+    constexpr int NSW = NG * (int)SPG;            // slabs per wave
+    constexpr int NBW = NSW / 2;                  // blocks of 128 per wave (rows of a product)
+    static_assert(NBW >= 1 && NBW <= 16, "a wave's blocks are rows of one product tile");
+    constexpr int QP = 2;                         // A passes held in registers (K <= 8192)
+    constexpr uint32_t BSH = 7, BLOCK = 128;
+    const uint32_t cg_shift = misc & 0xFF, act = misc >> 8;
+    const uint32_t n_pad = ((n ? n : 1u) + 127u) & ~127u;
+    const uint32_t tiles = n_pad >> (4 + cg_shift);
+    const uint32_t G = gridDim.x;
+    const uint32_t kq = (8u >> cg_shift) * NSW * LB_SLAB;
+    const uint32_t nbq = ((kq >> BSH) + 3) & ~3u;
+    const uint32_t grp_depths = KIND == 2 ? Q2_GROUP : Q1_GROUP;
+    const uint32_t ngroups = (k + grp_depths - 1) / grp_depths;
+    const uint32_t sc_rows = (ngroups * grp_depths + BLOCK - 1) >> BSH;
+    const uint32_t ncol = 16u << cg_shift;
+    const uint32_t qs_ = kq + 16;
+    const uint32_t bs2 = nbq + 2;
+    int8_t *ql = (int8_t *)smem;
+    const int8_t *zq = ql + qs_;
+    float *sa = (float *)(smem + qs_ + 64);
+    int32_t *as = (int32_t *)(sa + nbq);
+    float2 *xy = (float2 *)(as + nbq);  // [TPW][ncol][bs2]
+    float *wmax = (float *)(xy + TPW * ncol * bs2);
+    int32_t *wsum = (int32_t *)(wmax + WV);
+
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int gq4 = lane >> 4, c = lane & 15;
+    const uint32_t wpg_shift = 3 - cg_shift;
+    const uint32_t gi = (uint32_t)wave >> wpg_shift, kw = (uint32_t)wave & ((1u << wpg_shift) - 1);
+    const uint32_t fb = kw * NBW + (uint32_t)c;  // this lane's block (c < NBW)
+
+    // -- 1. loads: A, then each tile's scales and codes
+    uint4 areg[QP][1];
+    {
+        const rsrc_t ar = make_rsrc(lhs, k * 2u);
+        const bool vec = (k & 7) == 0;
+#pragma unroll
+        for (int p = 0; p < QP; p++)
+            areg[p][0] = (uint32_t)p * QPASS < kq ? load_row8(ar, 0, 1, k, p * QPASS + 8 * t, vec) : make_uint4(0, 0, 0, 0);
+    }
+    uint32_t tcol0[TPW];  // each tile's first column (tiles past the last: none)
+    bool tlive[TPW];
+    uint2 sreg4[TPW];
+    uint4 wreg[TPW][NG];
+    {
+        const rsrc_t sr = make_rsrc(sc, ((sc_rows + 3) & ~3u) * n_pad * 2u);
+        const rsrc_t cr = make_rsrc(codes, ((ngroups + 3) & ~3u) * n_pad * 64u);
+#pragma unroll
+        for (int j = 0; j < TPW; j++) {
+            const uint32_t li = blockIdx.x + j * G;
+            tlive[j] = li < tiles;
+            tcol0[j] = xcd_tile(tlive[j] ? li : 0, tiles) * ncol;
+            const uint32_t col0 = tcol0[j] + gi * 16;
+            sreg4[j] = bload8(sr, (tlive[j] && (uint32_t)c < (uint32_t)NBW && fb < sc_rows)
+                                      ? (uint32_t)cell_index(fb, col0 + 4 * gq4, sc_rows, n_pad) * 2u : OOB);
+#pragma unroll
+            for (int i = 0; i < NG; i++) {
+                const uint32_t grp = kw * NG + i;
+                wreg[j][i] = bload16(cr, tlive[j] && grp < ngroups
+                                             ? ((uint32_t)cell_index(grp, col0 + c, ngroups, n_pad) * 4 + gq4) * 16 : OOB);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // -- 2. quantize A once for every tile of this workgroup
+#pragma unroll
+    for (int p = 0; p < QP; p++) {
+        if ((uint32_t)p * QPASS >= kq) break;  // uniform
+        quant_pass<KIND, 1, BSH>(areg[p], p, ql, qs_, sa, as, nbq, kq, BSH, wmax, wsum);
+    }
+    // the epilogue operands of the (tile, column) this thread folds
+    const uint32_t fj = (uint32_t)t >> (4 + cg_shift), fc = (uint32_t)t & (ncol - 1);
+    const bool folder = fj < (uint32_t)TPW && blockIdx.x + fj * G < tiles;
+    const uint32_t fcol = (folder ? xcd_tile(blockIdx.x + fj * G, tiles) * ncol : 0) + fc;
+    EpPre pre = {};
+    uint16_t opa = 0, opb = 0;
+    if constexpr (EPV == 0) {
+        if (folder && fcol < n) pre = ep_prefetch(ep, 0, fcol, n);
+    } else if constexpr (EPV >= 2) {
+        const uint32_t ob = folder && fcol < n ? fcol * 2u : OOB;
+        opb = bload2(make_rsrc(col_b, n * 2u), ob);
+        if constexpr (EPV == 3) opa = bload2(make_rsrc(col_a, n * 2u), ob);
+    }
+    if (t < 4) *(uint4 *)(ql + qs_ + 16 * t) = make_uint4(0, 0, 0, 0);  // the zero B operand
+    __syncthreads();
+    const uint32_t nb_live = (k + BLOCK - 1) >> BSH;
+
+    // -- 3. per tile: exact block sums, block c of the wave in row c, then the
+    //       fold factors of the lanes (gq4, c < NBW)
+    const float s_b = (uint32_t)c < (uint32_t)NBW ? sa[fb] : 0.0f;
+    const int32_t a_b = KIND == 1 && (uint32_t)c < (uint32_t)NBW ? as[fb] : 0;
+    constexpr int PF = NSW < 8 ? NSW : 8;
+#pragma unroll
+    for (int j = 0; j < TPW; j++) {
+        if (!tlive[j]) break;  // uniform; later tiles are past the last too
+        auto expand = [&](int i) {
+            const uint4 wv = wreg[j][i / SPG];
+            const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+            int4_t wa;
+            if (KIND == 2) {
+                const uint32_t w = words[i % 4];
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    wa[e] = (int)__builtin_amdgcn_perm(codebook, codebook, (w >> (2 * e)) & 0x03030303u);
+            } else {
+                const uint32_t w = words[(i % 8) / 2], hs = 4 * (i % 2);
+#pragma unroll
+                for (int e = 0; e < 4; e++) wa[e] = (int)((w >> (hs + e)) & 0x01010101u);
+            }
+            return wa;
+        };
+        auto qloadf = [&](int i) {
+            const uint32_t slab = kw * NSW + i;
+            const int8_t *pa = (c == i / 2) ? ql + slab * LB_SLAB + 16 * gq4 : zq + 16 * gq4;
+            return __builtin_bit_cast(int4_t, *(const uint4 *)pa);
+        };
+        int4_t acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};  // a block's first and second slab
+#pragma unroll
+        for (int i0 = 0; i0 < NSW; i0 += PF) {
+            int4_t qv[PF];
+#pragma unroll
+            for (int i = 0; i < PF; i++) qv[i] = qloadf(i0 + i);
+#pragma unroll
+            for (int i = 0; i < PF; i++) {
+                if ((i0 + i) % 2 == 0) acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(i0 + i), qv[i], acc0, 0, 0, 0);
+                else acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(i0 + i), qv[i], acc1, 0, 0, 0);
+            }
+        }
+        if ((uint32_t)c < (uint32_t)NBW) {
+            const bool live = fb < nb_live;
+            float2 *xo = xy + ((uint32_t)j * ncol + gi * 16 + 4 * gq4) * bs2 + fb;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int32_t sum = acc0[v] + acc1[v];
+                float x = (float)(KIND == 1 ? 2 * sum + a_b : sum), y;
+                const uint32_t cw = v < 2 ? sreg4[j].x : sreg4[j].y;
+                if (v % 2 == 0)
+                    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(y) : "v"(cw), "v"(s_b), "v"(-0.0f));
+                else
+                    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                        : "=v"(y) : "v"(cw), "v"(s_b), "v"(-0.0f));
+                if (!live) x = y = 0.0f;
+                xo[v * bs2] = make_float2(x, y);
+            }
+        }
+    }
+    __syncthreads();
+
+    // -- 4. fold in block order (reference, matmul.rs:380-393), two blocks a
+    //       16-byte load; whole groups of 16 blocks, then the last group's live
+    //       pairs (a wave's range is an even number of blocks, so a pair that
+    //       starts below nb_live was written)
+    if (folder) {
+        float total = 0.0f;
+        const float *xp = (const float *)(xy + (fj * ncol + fc) * bs2);
+        auto group16 = [&](uint32_t b0, auto tail_tag) {
+            constexpr bool TAIL = decltype(tail_tag)::value;
+            float4_t v4[8];
+#pragma unroll
+            for (int h = 0; h < 8; h++) {
+                const bool live = !TAIL || b0 + 2 * h < nb_live;
+                v4[h] = *(const float4_t *)(xp + 2 * (live ? b0 + 2 * h : 0));
+                if (TAIL && !live) v4[h] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
+            }
+#pragma unroll
+            for (int h = 0; h < 8; h++) {
+                total = fmaf(v4[h][0], v4[h][1], total);
+                total = fmaf(v4[h][2], v4[h][3], total);
+            }
+        };
+        const uint32_t nb16 = nb_live & ~15u;
+        for (uint32_t b0 = 0; b0 < nb16; b0 += 16) group16(b0, std::false_type{});
+        if (nb16 < nb_live) group16(nb16, std::true_type{});
+        if (fcol < n) {
+            uint16_t out;
+            if constexpr (EPV == 0) {
+                out = finish_pre<false>(ep, pre, total, 0, fcol, n);
+            } else {
+                out = f32_to_f16(total);
+                if constexpr (EPV >= 2) {
+                    float x = f16_to_f32(out);
+                    if constexpr (EPV == 3) x = x * f16_to_f32(opa);
+                    x = x + f16_to_f32(opb);
+                    out = act == EP_ACT_NONE ? f32_to_f16(x) : act_round16<false>(act, x, alpha);
+                }
+            }
+            dst[fcol] = out;
+        }
+    }
+}
+
 template <int KIND, int MR, int NG, int SPB, int EPV>
 hipError_t launch_tile_v(const LtArgs &g, const EpArgs &ep, const EpPick &pk, hipStream_t s) {
     const size_t lds = tile_lds_bytes(g.kq, g.nbq, MR, 1u << g.cg_shift, MR == 1 && SPB == 2);
@@ -923,9 +1160,15 @@ hipError_t launch_tile_v(const LtArgs &g, const EpArgs &ep, const EpPick &pk, hi
     }
     const uint32_t tiles = g.n_pad / (16u << g.cg_shift);
     const void *src = MR > 1 ? (const void *)g.q : (const void *)g.lhs;
+    // the kernel derives these from its other arguments
+    const uint32_t grp = KIND == 2 ? Q2_GROUP : Q1_GROUP;
+    if (g.n_pad != (((g.n ? g.n : 1u) + 127u) & ~127u) || g.ngroups != (g.k + grp - 1) / grp || pk.act > 0xFF ||
+        (MR > 1 && ((const uint8_t *)g.qs != (const uint8_t *)g.q + ((g.m * g.kq + 255) & ~255u) ||
+                    g.qsum != (const int32_t *)(g.qs + g.m * g.nbq))))
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL((lowbit_tile<KIND, MR, NG, SPB, EPV>), dim3(tiles), dim3(T), lds, s, g.codes, g.sc, src,
-                       g.dst, g.n_pad, g.k, tiles, g.m | (g.block_shift << 8) | (g.cg_shift << 16), g.codebook,
-                       g.ngroups, g.n, pk.a, pk.b, pk.act, pk.alpha, g.qs, g.qsum, ep);
+                       g.dst, pk.b, g.k, g.m | (g.block_shift << 8) | (g.cg_shift << 16) | (pk.act << 24), g.n,
+                       g.codebook, pk.a, pk.alpha, ep);
     return hipGetLastError();
 }
 
@@ -959,6 +1202,59 @@ hipError_t launch_tile(const LtArgs &g, const EpArgs &ep, int mr, int ng, hipStr
     if (mr <= 2) return launch_tile_ng<KIND, 2>(g, ep, ng, s);
     if (mr <= 4) return launch_tile_ng<KIND, 4>(g, ep, ng, s);
     return launch_tile_ng<KIND, 8>(g, ep, ng, s);
+}
+
+
+// The persistent one-row kernel (lowbit_row): compiled stores only (the
+// interpreted graph, Q2 with 8 code groups a lane and more than 4 tiles per
+// compute unit take lowbit_tile); hipErrorNotSupported leaves those to it.
+template <int KIND, int NG, int EPV, int TPW>
+hipError_t launch_row_v(const LtArgs &g, const EpArgs &ep, const EpPick &pk, uint32_t grid, hipStream_t s) {
+    const size_t lds = row_lds_bytes(g.kq, g.nbq, 1u << g.cg_shift, TPW);
+    if (lds > 64 * 1024) {
+        static bool attr = false;  // benign race: every setter writes the same value
+        if (!attr) {
+            const hipError_t e = hipFuncSetAttribute((const void *)lowbit_row<KIND, NG, EPV, TPW>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+            if (e != hipSuccess) return e;
+            attr = true;
+        }
+    }
+    hipLaunchKernelGGL((lowbit_row<KIND, NG, EPV, TPW>), dim3(grid), dim3(T), lds, s, g.codes, g.sc, g.lhs, g.dst,
+                       pk.b, g.k, g.cg_shift | (pk.act << 8), g.n, g.codebook, pk.a, pk.alpha, ep);
+    return hipGetLastError();
+}
+template <int KIND, int NG, int EPV>
+hipError_t launch_row_t(const LtArgs &g, const EpArgs &ep, const EpPick &pk, uint32_t grid, int tpw, hipStream_t s) {
+    switch (tpw) {
+    case 1: return launch_row_v<KIND, NG, EPV, 1>(g, ep, pk, grid, s);
+    case 2: return launch_row_v<KIND, NG, EPV, 2>(g, ep, pk, grid, s);
+    case 3: return launch_row_v<KIND, NG, EPV, 3>(g, ep, pk, grid, s);
+    default: return launch_row_v<KIND, NG, EPV, 4>(g, ep, pk, grid, s);
+    }
+}
+template <int KIND, int NG>
+hipError_t launch_row_e(const LtArgs &g, const EpArgs &ep, uint32_t grid, int tpw, hipStream_t s) {
+    const EpPick pk = pick_ep(ep);
+    if (pk.v == 1) return launch_row_t<KIND, NG, 1>(g, ep, pk, grid, tpw, s);
+    if (pk.v == 2) return launch_row_t<KIND, NG, 2>(g, ep, pk, grid, tpw, s);
+    if (pk.v == 3) return launch_row_t<KIND, NG, 3>(g, ep, pk, grid, tpw, s);
+    return hipErrorNotSupported;
+}
+template <int KIND>
+hipError_t launch_row(const LtArgs &g, const EpArgs &ep, int ng, hipStream_t s) {
+    const uint32_t tiles = g.n_pad >> (4 + g.cg_shift);
+    const uint32_t grid = std::min<uint32_t>(tiles, (uint32_t)device_cus());
+    const int tpw = (int)((tiles + grid - 1) / grid);
+    const uint32_t grp = KIND == 2 ? Q2_GROUP : Q1_GROUP;
+    if (g.m != 1 || g.block_shift != 7 || tpw > 4 || grid == 0 || g.n_pad != (((g.n ? g.n : 1u) + 127u) & ~127u) ||
+        g.ngroups != (g.k + grp - 1) / grp || row_lds_bytes(g.kq, g.nbq, 1u << g.cg_shift, tpw) > 96 * 1024)
+        return hipErrorNotSupported;
+    if (pick_ep(ep).act > 0xFFFFFF) return hipErrorNotSupported;
+    if (ng <= 1) return launch_row_e<KIND, 1>(g, ep, grid, tpw, s);
+    if (ng <= 2) return launch_row_e<KIND, 2>(g, ep, grid, tpw, s);
+    if (ng <= 4) return launch_row_e<KIND, 4>(g, ep, grid, tpw, s);
+    return hipErrorNotSupported;
 }
 
 // One workgroup per (row, block): q for the block's depths (zero past k), the
@@ -1168,6 +1464,10 @@ hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint
                                    f.block_shift, (int8_t *)f.q, (float *)f.qs, (int32_t *)f.qsum);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
+        }
+        if (m == 1) {
+            const hipError_t e = w.kind == W_Q2 ? launch_row<2>(f, ep, sg.ng, s) : launch_row<1>(f, ep, sg.ng, s);
+            if (e != hipErrorNotSupported) return e;
         }
         if (w.kind == W_Q2) return launch_tile<2>(f, ep, mr, sg.ng, s);
         return launch_tile<1>(f, ep, mr, sg.ng, s);
