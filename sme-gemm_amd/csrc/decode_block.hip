@@ -136,10 +136,12 @@ __device__ __forceinline__ float glu_act(uint32_t act, float g) {
 struct BlkPre {
     float y, c, s;
 };
+// t: the thread's lane within the tile's store (threadIdx.x when a workgroup
+// stores one tile at a time).
 template <int STORE>
-__device__ __forceinline__ BlkPre blk_prefetch(const Q4GemvArgs &g, const BlkArgs &a, uint32_t tile) {
+__device__ __forceinline__ BlkPre blk_prefetch(const Q4GemvArgs &g, const BlkArgs &a, uint32_t tile,
+                                               uint32_t t = threadIdx.x) {
     BlkPre p{0.0f, 1.0f, 0.0f};
-    const uint32_t t = threadIdx.x;
     if constexpr (STORE == BS_RESID) {
         const uint32_t j = tile * 16 + t;
         if (t < 16 && j < g.n) p.y = a.x[j];
@@ -158,8 +160,7 @@ __device__ __forceinline__ BlkPre blk_prefetch(const Q4GemvArgs &g, const BlkArg
 // pre: blk_prefetch's loads for MR = 1 (MR > 1 reads the residual here).
 template <int MR, int STORE>
 __device__ __forceinline__ void blk_store(const Q4GemvArgs &g, const BlkArgs &a, uint32_t tile, const float *red,
-                                          const BlkPre &pre) {
-    const int t = threadIdx.x;
+                                          const BlkPre &pre, int t = (int)threadIdx.x) {
     if constexpr (STORE == BS_RESID) {
         // y += f32(f16(x @ W)): Linear::accumulate's add_f16 (src/convert.rs:37-49)
         if (t < 16 * MR) {
@@ -311,6 +312,176 @@ __global__ void __launch_bounds__(MF_WAVES * 64) blk_gemv_p(Q4GemvArgs g, BlkArg
     }
 }
 
+
+// The single-row GEMV with every weight step in flight (K <= 1024 NS, at most
+// TPW tiles a workgroup, one workgroup a compute unit): the weights of all
+// its tiles are issued at the start, behind the activation runs, and each
+// wave stages only the activations its own chunks multiply (wave w's step u
+// multiplies chunks s*128 + 4(w + 8(u%4)) + grp of segment s = u/4), so
+// nothing but the fused norm's sum of squares and the partial-tile reduction
+// waits on other waves. Two workgroups on one compute unit were measured to
+// serialize (the second one's loads queue behind the first one's weights),
+// and segment-by-segment loops wait on one segment's weights before the
+// next is issued; this form does neither. Step u of a tile reads chunk kc of
+// the blocked grid at a constant offset from the wave's first cell; a step
+// past K reads zeros (or the grid's padding, with its scale replaced by 0).
+template <bool NORM, int STORE, int TPW, int NS>
+__global__ void __launch_bounds__(MF_WAVES * 64) blk_gemv_w(Q4GemvArgs g, BlkArgs a) {
+    constexpr int NSEG = (NS + 3) / 4;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, c = lane & 15, grp = lane >> 4;
+    uint16_t *wlds = (uint16_t *)smem + wave * (NSEG * 512);  // this wave's runs [NSEG][4][128]
+    float *red = (float *)(smem + MF_WAVES * NSEG * 1024);    // [TPW][MF_WAVES][16]
+    const uint32_t ntiles = g.n_pad / 16, G = gridDim.x;
+    const uint32_t mag_lo = __builtin_amdgcn_readfirstlane(0x64006400u) | (uint32_t)(t >> 30);
+    const uint32_t mag_hi = __builtin_amdgcn_readfirstlane(0x54005400u) | (uint32_t)(t >> 30);
+
+    // -- 1. the wave's activation runs (lane (grp, c): 8 depths of run grp of
+    //       each segment), then every tile's weight steps
+    uint4 ah[NSEG];
+    float4 ax[NSEG][2], aw[NSEG][2];
+#pragma unroll
+    for (int sg = 0; sg < NSEG; sg++) {
+        const uint32_t da = (sg * 128u + 4u * (wave + MF_WAVES * grp)) * Q4_CHUNK + (uint32_t)c * 8u;
+        if constexpr (NORM) {
+            const rsrc_t xr = make_rsrc(a.nx, g.k * 4u), wr = make_rsrc(a.nw, g.k * 4u);
+            const uint32_t off = da < g.k ? da * 4u : OOB;
+            ax[sg][0] = bload16f(xr, off);
+            ax[sg][1] = bload16f(xr, da < g.k ? off + 16 : OOB);
+            aw[sg][0] = bload16f(wr, off);
+            aw[sg][1] = bload16f(wr, da < g.k ? off + 16 : OOB);
+        } else {
+            ah[sg] = bload16(make_rsrc(g.lhs, g.k * 2u), da < g.k ? da * 2u : OOB);
+        }
+    }
+    const uint32_t grid_rows = (g.nchunks + 3) & ~3u;
+    const rsrc_t nr = make_rsrc(g.nib, grid_rows * g.n_pad * 16u), sr = make_rsrc(g.sc, grid_rows * g.n_pad * 2u);
+    bool live[TPW];
+    uint32_t tile[TPW];
+    uint4 wq[TPW][NS];
+    uint16_t sv[TPW][NS];
+#pragma unroll
+    for (int j = 0; j < TPW; j++) {
+        const uint32_t li = blockIdx.x + j * G;
+        live[j] = li < ntiles;
+        tile[j] = xcd_tile(live[j] ? li : 0, ntiles);
+        const uint32_t col = tile[j] * 16 + c;
+        const uint32_t cell0 = wave * 4u * g.n_pad + grp * 16u + (col >> 4) * 64u + (col & 15);
+#pragma unroll
+        for (int u = 0; u < NS; u++) {
+            const uint32_t kc = (u / 4) * 128u + 4u * (wave + MF_WAVES * (u % 4)) + grp;
+            const uint32_t cell = cell0 + ((u / 4) * 32u + MF_WAVES * (u % 4)) * 4u * g.n_pad;
+            wq[j][u] = bload16_nt(nr, live[j] ? cell * 16u : OOB);
+            const uint16_t sl = bload2_nt(sr, live[j] ? cell * 2u : OOB);
+            sv[j][u] = kc < g.nchunks ? sl : (uint16_t)0;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // the stores' own loads (threads 16 j .. 16 j + 15 store tile j)
+    const int sj = t >> 4, st = t & 15;
+    BlkPre pre{0.0f, 1.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < TPW; j++)
+        if (sj == j && live[j]) pre = blk_prefetch<STORE>(g, a, tile[j], (uint32_t)st);
+
+    // -- 2. stage the wave's runs (with the fused norm: h = f16(x r w), r
+    //       from the whole row's sum of squares, nn.rs:127-144)
+    if constexpr (NORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int sg = 0; sg < NSEG; sg++) {
+            const float xs[8] = {ax[sg][0].x, ax[sg][0].y, ax[sg][0].z, ax[sg][0].w,
+                                 ax[sg][1].x, ax[sg][1].y, ax[sg][1].z, ax[sg][1].w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) ss = ss + xs[i] * xs[i];
+        }
+        const float r = rms_scale(ss, g.k, a.eps);
+#pragma unroll
+        for (int sg = 0; sg < NSEG; sg++) {
+            const float xs[8] = {ax[sg][0].x, ax[sg][0].y, ax[sg][0].z, ax[sg][0].w,
+                                 ax[sg][1].x, ax[sg][1].y, ax[sg][1].z, ax[sg][1].w};
+            const float ws[8] = {aw[sg][0].x, aw[sg][0].y, aw[sg][0].z, aw[sg][0].w,
+                                 aw[sg][1].x, aw[sg][1].y, aw[sg][1].z, aw[sg][1].w};
+            uint16_t h[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) h[i] = f32_to_f16((xs[i] - 0.0f) * r * ws[i] + 0.0f);
+            *(uint4 *)(wlds + sg * 512 + lane * 8) =
+                make_uint4(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+                           h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16));
+        }
+    } else {
+#pragma unroll
+        for (int sg = 0; sg < NSEG; sg++) *(uint4 *)(wlds + sg * 512 + lane * 8) = ah[sg];
+    }
+
+    // -- 3. dequant + MFMA, step by step as the weights land (every B lane
+    //       reads row 0: only output row 0 is used)
+    float4_t acc[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; j++) {
+        acc[j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+        if (!live[j]) continue;  // uniform
+#pragma unroll
+        for (int u = 0; u < NS; u++) {
+            uint4 ab[4];
+#pragma unroll
+            for (int w = 0; w < 4; w++) ab[w] = *(const uint4 *)(wlds + (u / 4) * 512 + (u % 4) * 128 + grp * 32 + w * 8);
+            const half2_t s2 = {__builtin_bit_cast(_Float16, sv[j][u]), __builtin_bit_cast(_Float16, sv[j][u])};
+            const uint32_t words[4] = {wq[j][u].x, wq[j][u].y, wq[j][u].z, wq[j][u].w};
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const uint4 wa = q4_deq8(words[w], s2, mag_lo, mag_hi);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wa),
+                                                                __builtin_bit_cast(half8_t, ab[w]), acc[j], 0, 0, 0);
+            }
+        }
+    }
+    // -- 4. the waves' partial tiles in fixed order, then each tile's store
+    if (c == 0) {
+#pragma unroll
+        for (int j = 0; j < TPW; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) red[(j * MF_WAVES + wave) * 16 + 4 * grp + v] = acc[j][v];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < TPW; j++)
+        if (sj == j && live[j]) blk_store<1, STORE>(g, a, tile[j], red + j * MF_WAVES * 16, pre, st);
+}
+
+template <bool NORM, int STORE, int TPW, int NS>
+hipError_t launch_blk_w(const Q4GemvArgs &g, const BlkArgs &a, uint32_t grid, hipStream_t s) {
+    constexpr size_t lds = (size_t)MF_WAVES * ((NS + 3) / 4) * 1024 + (size_t)TPW * MF_WAVES * 16 * 4;
+    hipLaunchKernelGGL((blk_gemv_w<NORM, STORE, TPW, NS>), dim3(grid), dim3(MF_WAVES * 64), lds, s, g, a);
+    return hipGetLastError();
+}
+
+// blk_gemv_w when it serves the call (one row, block 32, K within 16 steps a
+// lane -- 4 with the fused norm or two tiles a compute unit -- and at most
+// two tiles a compute unit): the qkv, out and down projections. Wider
+// projections (the 28672-column gate/up) keep blk_gemv_p's two-workgroup
+// ring: all seven tiles of a compute unit in flight at once measured 20.7
+// against 16.3 us there. hipErrorNotSupported otherwise.
+template <bool NORM, int STORE>
+hipError_t try_blk_w(const Q4GemvArgs &g, const BlkArgs &a, size_t m, hipStream_t s) {
+    const uint32_t ntiles = g.n_pad / 16;
+    const uint32_t grid = std::min<uint32_t>(ntiles, (uint32_t)device_cus());
+    const uint32_t tpw = grid ? (ntiles + grid - 1) / grid : 0;
+    const uint32_t ns = (g.nchunks + 31) / 32;  // steps a lane: 32 chunks a step across the workgroup
+    if (m != 1 || g.block_shift != 5 || (g.k & 7) != 0 || grid == 0 || tpw > 2 || ns > 16 ||
+        cell_grid_rows(g.nchunks) * (size_t)g.n_pad * 16 >= ((size_t)1 << 31) || ((NORM || tpw > 1) && ns > 4))
+        return hipErrorNotSupported;
+    if (tpw == 2) return launch_blk_w<NORM, STORE, 2, 4>(g, a, grid, s);
+    if (ns <= 4) return launch_blk_w<NORM, STORE, 1, 4>(g, a, grid, s);
+    if constexpr (NORM) {
+        return hipErrorNotSupported;
+    } else {
+        if (ns <= 8) return launch_blk_w<NORM, STORE, 1, 8>(g, a, grid, s);
+        if (ns <= 14) return launch_blk_w<NORM, STORE, 1, 14>(g, a, grid, s);
+        return launch_blk_w<NORM, STORE, 1, 16>(g, a, grid, s);
+    }
+}
+
 template <int MR, bool NORM, int STORE>
 hipError_t launch_blk(const Q4GemvArgs &g, const BlkArgs &a, hipStream_t s) {
     hipLaunchKernelGGL((blk_gemv<MR, NORM, STORE>), dim3(g.n_pad / 16), dim3(MF_WAVES * 64),
@@ -336,6 +507,10 @@ hipError_t launch_blk_p(const Q4GemvArgs &g, const BlkArgs &a, hipStream_t s) {
 // 28672 columns 15.7 vs 18.4 us, 4096-6144 columns 0.3-0.4 us slower).
 template <bool NORM, int STORE>
 hipError_t launch_blk_rows(const Q4GemvArgs &g, const BlkArgs &a, size_t m, hipStream_t s) {
+    {
+        const hipError_t e = try_blk_w<NORM, STORE>(g, a, m, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     const bool persistent = m == 1 && (g.nchunks + MF_SEG_CH - 1) / MF_SEG_CH <= (uint32_t)BP_MAX_SEG &&
                             g.n_pad / 16 >= 2u * BP_WG_PER_CU * (uint32_t)device_cus();
     if constexpr (NORM || STORE == BS_QKV) {
