@@ -922,30 +922,39 @@ __global__ void __launch_bounds__(T)
 
 
 // ---------------------------------------------------------------------------
-// One row, blocks of 128 (the usual decode call), persistent: one workgroup
-// per compute unit (grid G = min(tiles, CUs)), workgroup g taking tiles g, g
-// + G, ... (up to TPW of them). Two workgroups on one compute unit were
-// measured to serialize: the second one's activation loads queue behind the
-// first one's weight stream, so it quantizes ~1.2 us later. Here a compute
-// unit issues A first, then every tile's scales and codes, quantizes A once,
-// and multiplies its tiles as their codes land:
-//   1. loads: A (f16, one 4096-depth pass per thread), then per tile the
-//      lane's scales (its block, four columns) and code groups;
+// Up to 8 rows, blocks of 128 (the usual decode call), persistent: one
+// workgroup per compute unit (grid G = min(tiles, CUs)), workgroup g taking
+// tiles g, g + G, ... (up to TPW of them). Two workgroups on one compute unit
+// were measured to serialize: the second one's activation loads queue behind
+// the first one's weight stream, so it quantizes ~1.2 us later. Here a
+// compute unit issues A first, then every tile's scales and codes, quantizes
+// A once (every row: no separate quantization launch) and multiplies its
+// tiles as their codes land:
+//   1. loads: A (f16, one 4096-depth pass per thread and row), then per tile
+//      the scales and code groups;
 //   2. quant_pass into LDS (shared by the tiles), one barrier;
-//   3. per tile, the products put block c of the wave's range in output row
-//      c (the B operand's column c holds q on that block's slabs, zero
-//      elsewhere), and the lanes holding a block's sums form its fold factors
-//      x = f32(sum) (Q1: 2 sum(q b) + (-sum(q))) and y = f32(scale) * s;
-//   4. one barrier, then one thread per (tile, column) folds its blocks in
-//      order (fmaf), runs the op-graph and stores.
-// misc = cg_shift | act << 8. LDS: q [kq + 16] i8 | 64 zero bytes | s [nbq]
-// f32 | -sum(q) [nbq] i32 | (x, y) [TPW][16 CG][nbq + 2] | wave partials.
+//   3. per tile, exact block sums on v_mfma_i32_16x16x64_i8. One row: block
+//      c of the wave's range lands in output row c (the B operand's column c
+//      holds q on that block's slabs, zero elsewhere), so the lanes holding a
+//      block's sums form its fold factors x = f32(sum) (Q1: 2 sum(q b) +
+//      (-sum(q))) and y = f32(scale) * s with scales they loaded themselves.
+//      Several rows: B column c is row c; each block's sums accumulate over
+//      its two slabs and x goes to LDS, the scales through an LDS transpose;
+//   4. one barrier, then one thread per (tile, row, column) folds its blocks
+//      in order (fmaf), runs the op-graph and stores.
+// misc = cg_shift | act << 8 | m << 16. LDS (row_lds_bytes): q [MR][kq + 16]
+// i8 | 64 zero bytes | s [MR][nbq] f32 | -sum(q) [MR][nbq] i32 | one row: (x,
+// y) [TPW][16 CG][nbq + 2]; several: x [TPW][MR][16 CG][nbq + 4] f32 and
+// scales [TPW][16 CG][nbq + 4] f16 | wave partials.
 // ---------------------------------------------------------------------------
-size_t row_lds_bytes(uint32_t kq, uint32_t nbq, uint32_t cg, int tpw) {
-    return (size_t)kq + 16 + 64 + (size_t)nbq * 8 + (size_t)tpw * 16 * cg * (nbq + 2) * 8 + (size_t)WV * 8;
+size_t row_lds_bytes(uint32_t kq, uint32_t nbq, uint32_t cg, int tpw, int mr) {
+    const size_t head = (size_t)mr * (kq + 16) + 64 + (size_t)mr * nbq * 8;
+    const size_t body = mr == 1 ? (size_t)tpw * 16 * cg * (nbq + 2) * 8
+                                : (size_t)tpw * 16 * cg * (nbq + 4) * ((size_t)mr * 4 + 2);
+    return head + body + (size_t)mr * WV * 8;
 }
 
-template <int KIND, int NG, int EPV, int TPW>
+template <int KIND, int MR, int NG, int EPV, int TPW>
 __global__ void __launch_bounds__(T)
     lowbit_row(const uint8_t *codes, const uint16_t *sc, const uint16_t *lhs, uint16_t *dst, const uint16_t *col_b,
                uint32_t k, uint32_t misc, uint32_t n, uint32_t codebook, const uint16_t *col_a, float alpha,
@@ -953,11 +962,11 @@ __global__ void __launch_bounds__(T)
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr uint32_t SPG = KIND == 2 ? 4 : 8;  // slabs per code group
     constexpr int NSW = NG * (int)SPG;            // slabs per wave
-    constexpr int NBW = NSW / 2;                  // blocks of 128 per wave (rows of a product)
+    constexpr int NBW = NSW / 2;                  // blocks of 128 per wave
     static_assert(NBW >= 1 && NBW <= 16, "a wave's blocks are rows of one product tile");
     constexpr int QP = 2;                         // A passes held in registers (K <= 8192)
     constexpr uint32_t BSH = 7, BLOCK = 128;
-    const uint32_t cg_shift = misc & 0xFF, act = misc >> 8;
+    const uint32_t cg_shift = misc & 0xFF, act = (misc >> 8) & 0xFF, m = MR == 1 ? 1u : misc >> 16;
     const uint32_t n_pad = ((n ? n : 1u) + 127u) & ~127u;
     const uint32_t tiles = n_pad >> (4 + cg_shift);
     const uint32_t G = gridDim.x;
@@ -968,34 +977,40 @@ __global__ void __launch_bounds__(T)
     const uint32_t sc_rows = (ngroups * grp_depths + BLOCK - 1) >> BSH;
     const uint32_t ncol = 16u << cg_shift;
     const uint32_t qs_ = kq + 16;
-    const uint32_t bs2 = nbq + 2;
-    int8_t *ql = (int8_t *)smem;
-    const int8_t *zq = ql + qs_;
-    float *sa = (float *)(smem + qs_ + 64);
-    int32_t *as = (int32_t *)(sa + nbq);
-    float2 *xy = (float2 *)(as + nbq);  // [TPW][ncol][bs2]
-    float *wmax = (float *)(xy + TPW * ncol * bs2);
-    int32_t *wsum = (int32_t *)(wmax + WV);
+    const uint32_t bs = nbq + 4;   // several rows: x / scale row stride
+    const uint32_t bs2 = nbq + 2;  // one row: (x, y) pair row stride
+    int8_t *ql = (int8_t *)smem;                     // [MR][qs_]
+    const int8_t *zq = ql + MR * qs_;                // 64 zero bytes
+    float *sa = (float *)(smem + MR * qs_ + 64);     // [MR][nbq]
+    int32_t *as = (int32_t *)(sa + MR * nbq);        // [MR][nbq]
+    float2 *xy = (float2 *)(as + MR * nbq);          // one row: [TPW][ncol][bs2]
+    float *xs = (float *)(as + MR * nbq);            // several: [TPW][MR][ncol][bs]
+    uint16_t *scl = (uint16_t *)(xs + TPW * MR * ncol * bs);  // several: [TPW][ncol][bs]
+    float *wmax = MR == 1 ? (float *)(xy + TPW * ncol * bs2) : (float *)(scl + TPW * ncol * bs);
+    int32_t *wsum = (int32_t *)(wmax + MR * WV);
 
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int gq4 = lane >> 4, c = lane & 15;
     const uint32_t wpg_shift = 3 - cg_shift;
     const uint32_t gi = (uint32_t)wave >> wpg_shift, kw = (uint32_t)wave & ((1u << wpg_shift) - 1);
-    const uint32_t fb = kw * NBW + (uint32_t)c;  // this lane's block (c < NBW)
+    const uint32_t fb = kw * NBW + (uint32_t)c;  // one row: this lane's block (c < NBW)
 
     // -- 1. loads: A, then each tile's scales and codes
-    uint4 areg[QP][1];
+    uint4 areg[QP][MR];
     {
-        const rsrc_t ar = make_rsrc(lhs, k * 2u);
+        const rsrc_t ar = make_rsrc(lhs, m * k * 2u);
         const bool vec = (k & 7) == 0;
 #pragma unroll
         for (int p = 0; p < QP; p++)
-            areg[p][0] = (uint32_t)p * QPASS < kq ? load_row8(ar, 0, 1, k, p * QPASS + 8 * t, vec) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < MR; r++)
+                areg[p][r] = (uint32_t)p * QPASS < kq ? load_row8(ar, r, m, k, p * QPASS + 8 * t, vec)
+                                                      : make_uint4(0, 0, 0, 0);
     }
-    uint32_t tcol0[TPW];  // each tile's first column (tiles past the last: none)
     bool tlive[TPW];
-    uint2 sreg4[TPW];
+    uint2 sreg4[TPW];  // one row: the lane's block, four columns
+    uint4 sreg[TPW];   // several rows: block t / (2 CG), eight columns
     uint4 wreg[TPW][NG];
     {
         const rsrc_t sr = make_rsrc(sc, ((sc_rows + 3) & ~3u) * n_pad * 2u);
@@ -1004,10 +1019,16 @@ __global__ void __launch_bounds__(T)
         for (int j = 0; j < TPW; j++) {
             const uint32_t li = blockIdx.x + j * G;
             tlive[j] = li < tiles;
-            tcol0[j] = xcd_tile(tlive[j] ? li : 0, tiles) * ncol;
-            const uint32_t col0 = tcol0[j] + gi * 16;
-            sreg4[j] = bload8(sr, (tlive[j] && (uint32_t)c < (uint32_t)NBW && fb < sc_rows)
-                                      ? (uint32_t)cell_index(fb, col0 + 4 * gq4, sc_rows, n_pad) * 2u : OOB);
+            const uint32_t tcol0 = xcd_tile(tlive[j] ? li : 0, tiles) * ncol;
+            const uint32_t col0 = tcol0 + gi * 16;
+            if constexpr (MR == 1) {
+                sreg4[j] = bload8(sr, (tlive[j] && (uint32_t)c < (uint32_t)NBW && fb < sc_rows)
+                                          ? (uint32_t)cell_index(fb, col0 + 4 * gq4, sc_rows, n_pad) * 2u : OOB);
+            } else {
+                const uint32_t bb = t >> (cg_shift + 1), piece = t & (2 * (1u << cg_shift) - 1);
+                sreg[j] = bload16(sr, (tlive[j] && bb < nbq && bb < sc_rows)
+                                          ? (uint32_t)cell_index(bb, tcol0 + piece * 8, sc_rows, n_pad) * 2u : OOB);
+            }
 #pragma unroll
             for (int i = 0; i < NG; i++) {
                 const uint32_t grp = kw * NG + i;
@@ -1022,29 +1043,28 @@ __global__ void __launch_bounds__(T)
 #pragma unroll
     for (int p = 0; p < QP; p++) {
         if ((uint32_t)p * QPASS >= kq) break;  // uniform
-        quant_pass<KIND, 1, BSH>(areg[p], p, ql, qs_, sa, as, nbq, kq, BSH, wmax, wsum);
+        quant_pass<KIND, MR, BSH>(areg[p], p, ql, qs_, sa, as, nbq, kq, BSH, wmax, wsum);
     }
-    // the epilogue operands of the (tile, column) this thread folds
-    const uint32_t fj = (uint32_t)t >> (4 + cg_shift), fc = (uint32_t)t & (ncol - 1);
-    const bool folder = fj < (uint32_t)TPW && blockIdx.x + fj * G < tiles;
+    // the epilogue operands of the (tile, row, column) this thread folds
+    const uint32_t fj = (uint32_t)t / (MR * ncol), frow = ((uint32_t)t / ncol) % MR, fc = (uint32_t)t & (ncol - 1);
+    const bool folder = fj < (uint32_t)TPW && blockIdx.x + fj * G < tiles && frow < m;
     const uint32_t fcol = (folder ? xcd_tile(blockIdx.x + fj * G, tiles) * ncol : 0) + fc;
     EpPre pre = {};
     uint16_t opa = 0, opb = 0;
     if constexpr (EPV == 0) {
-        if (folder && fcol < n) pre = ep_prefetch(ep, 0, fcol, n);
+        if (folder && fcol < n) pre = ep_prefetch(ep, frow, fcol, n);
     } else if constexpr (EPV >= 2) {
         const uint32_t ob = folder && fcol < n ? fcol * 2u : OOB;
         opb = bload2(make_rsrc(col_b, n * 2u), ob);
         if constexpr (EPV == 3) opa = bload2(make_rsrc(col_a, n * 2u), ob);
     }
-    if (t < 4) *(uint4 *)(ql + qs_ + 16 * t) = make_uint4(0, 0, 0, 0);  // the zero B operand
+    if (t < 4) *(uint4 *)(ql + MR * qs_ + 16 * t) = make_uint4(0, 0, 0, 0);  // the zero B operand
     __syncthreads();
     const uint32_t nb_live = (k + BLOCK - 1) >> BSH;
 
-    // -- 3. per tile: exact block sums, block c of the wave in row c, then the
-    //       fold factors of the lanes (gq4, c < NBW)
-    const float s_b = (uint32_t)c < (uint32_t)NBW ? sa[fb] : 0.0f;
-    const int32_t a_b = KIND == 1 && (uint32_t)c < (uint32_t)NBW ? as[fb] : 0;
+    // -- 3. per tile: exact block sums, then the fold factors
+    const float s_b = MR == 1 && (uint32_t)c < (uint32_t)NBW ? sa[fb] : 0.0f;
+    const int32_t a_b = MR == 1 && KIND == 1 && (uint32_t)c < (uint32_t)NBW ? as[fb] : 0;
     constexpr int PF = NSW < 8 ? NSW : 8;
 #pragma unroll
     for (int j = 0; j < TPW; j++) {
@@ -1065,72 +1085,171 @@ __global__ void __launch_bounds__(T)
             }
             return wa;
         };
-        auto qloadf = [&](int i) {
-            const uint32_t slab = kw * NSW + i;
-            const int8_t *pa = (c == i / 2) ? ql + slab * LB_SLAB + 16 * gq4 : zq + 16 * gq4;
-            return __builtin_bit_cast(int4_t, *(const uint4 *)pa);
-        };
-        int4_t acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};  // a block's first and second slab
+        if constexpr (MR == 1) {
+            auto qloadf = [&](int i) {
+                const uint32_t slab = kw * NSW + i;
+                const int8_t *pa = (c == i / 2) ? ql + slab * LB_SLAB + 16 * gq4 : zq + 16 * gq4;
+                return __builtin_bit_cast(int4_t, *(const uint4 *)pa);
+            };
+            int4_t acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};  // a block's first and second slab
 #pragma unroll
-        for (int i0 = 0; i0 < NSW; i0 += PF) {
-            int4_t qv[PF];
+            for (int i0 = 0; i0 < NSW; i0 += PF) {
+                int4_t qv[PF];
 #pragma unroll
-            for (int i = 0; i < PF; i++) qv[i] = qloadf(i0 + i);
+                for (int i = 0; i < PF; i++) qv[i] = qloadf(i0 + i);
 #pragma unroll
-            for (int i = 0; i < PF; i++) {
-                if ((i0 + i) % 2 == 0) acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(i0 + i), qv[i], acc0, 0, 0, 0);
-                else acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(i0 + i), qv[i], acc1, 0, 0, 0);
+                for (int i = 0; i < PF; i++) {
+                    if ((i0 + i) % 2 == 0) acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(i0 + i), qv[i], acc0, 0, 0, 0);
+                    else acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(i0 + i), qv[i], acc1, 0, 0, 0);
+                }
             }
-        }
-        if ((uint32_t)c < (uint32_t)NBW) {
-            const bool live = fb < nb_live;
-            float2 *xo = xy + ((uint32_t)j * ncol + gi * 16 + 4 * gq4) * bs2 + fb;
+            if ((uint32_t)c < (uint32_t)NBW) {
+                const bool live = fb < nb_live;
+                float2 *xo = xy + ((uint32_t)j * ncol + gi * 16 + 4 * gq4) * bs2 + fb;
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int32_t sum = acc0[v] + acc1[v];
-                float x = (float)(KIND == 1 ? 2 * sum + a_b : sum), y;
-                const uint32_t cw = v < 2 ? sreg4[j].x : sreg4[j].y;
-                if (v % 2 == 0)
-                    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(y) : "v"(cw), "v"(s_b), "v"(-0.0f));
-                else
-                    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-                        : "=v"(y) : "v"(cw), "v"(s_b), "v"(-0.0f));
-                if (!live) x = y = 0.0f;
-                xo[v * bs2] = make_float2(x, y);
+                for (int v = 0; v < 4; v++) {
+                    const int32_t sum = acc0[v] + acc1[v];
+                    float x = (float)(KIND == 1 ? 2 * sum + a_b : sum), y;
+                    const uint32_t cw = v < 2 ? sreg4[j].x : sreg4[j].y;
+                    if (v % 2 == 0)
+                        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(y) : "v"(cw), "v"(s_b), "v"(-0.0f));
+                    else
+                        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                            : "=v"(y) : "v"(cw), "v"(s_b), "v"(-0.0f));
+                    if (!live) x = y = 0.0f;
+                    xo[v * bs2] = make_float2(x, y);
+                }
+            }
+        } else {
+            // B column c is row c (lanes c >= MR read row 0 again: their
+            // output rows are never stored); block b's sums in acc[b]
+            auto qload = [&](int i) {
+                const uint32_t slab = kw * NSW + i;
+                return __builtin_bit_cast(int4_t, *(const uint4 *)(ql + (c < MR ? c : 0) * qs_ + slab * LB_SLAB + 16 * gq4));
+            };
+            int4_t acc[NBW];
+#pragma unroll
+            for (int b = 0; b < NBW; b++) acc[b] = (int4_t){0, 0, 0, 0};
+#pragma unroll
+            for (int i0 = 0; i0 < NSW; i0 += PF) {
+                int4_t qv[PF];
+#pragma unroll
+                for (int i = 0; i < PF; i++) qv[i] = qload(i0 + i);
+#pragma unroll
+                for (int i = 0; i < PF; i++)
+                    acc[(i0 + i) / 2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(expand(i0 + i), qv[i], acc[(i0 + i) / 2], 0, 0, 0);
+            }
+            // x = f32(sum) (Q1: 2 sum + (-sum(q))) of row c, columns 4 gq4 + v,
+            // this wave's blocks, four blocks a 16-byte store
+            if (c < MR) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    float *xo = xs + (((uint32_t)j * MR + c) * ncol + gi * 16 + 4 * gq4 + v) * bs + kw * NBW;
+#pragma unroll
+                    for (int b4 = 0; b4 < NBW; b4 += 4) {
+                        float4_t x4;
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const int b = b4 + e;
+                            if (b < NBW) {
+                                const int32_t sum = acc[b][v];
+                                x4[e] = (float)(KIND == 1 ? 2 * sum + as[c * nbq + kw * NBW + b] : sum);
+                            } else {
+                                x4[e] = 0.0f;
+                            }
+                        }
+                        if (b4 + 4 <= NBW) *(float4_t *)(xo + b4) = x4;
+                        else
+#pragma unroll
+                            for (int e = 0; e < 4; e++)
+                                if (b4 + e < NBW) xo[b4 + e] = x4[e];
+                    }
+                }
+            }
+            // the tile's scales, transposed: scale of (block bb, column 8 piece + e)
+            if ((uint32_t)t < 2 * (1u << cg_shift) * nbq) {
+                const uint32_t bb = t >> (cg_shift + 1), piece = t & (2 * (1u << cg_shift) - 1);
+                const uint32_t sw[4] = {sreg[j].x, sreg[j].y, sreg[j].z, sreg[j].w};
+                uint16_t *sp = scl + (uint32_t)j * ncol * bs;
+#pragma unroll
+                for (int e = 0; e < 8; e++) sp[(8 * piece + e) * bs + bb] = (uint16_t)(sw[e / 2] >> (16 * (e % 2)));
             }
         }
     }
     __syncthreads();
 
-    // -- 4. fold in block order (reference, matmul.rs:380-393), two blocks a
-    //       16-byte load; whole groups of 16 blocks, then the last group's live
-    //       pairs (a wave's range is an even number of blocks, so a pair that
-    //       starts below nb_live was written)
+    // -- 4. fold in block order (reference, matmul.rs:380-393)
     if (folder) {
         float total = 0.0f;
-        const float *xp = (const float *)(xy + (fj * ncol + fc) * bs2);
-        auto group16 = [&](uint32_t b0, auto tail_tag) {
-            constexpr bool TAIL = decltype(tail_tag)::value;
-            float4_t v4[8];
+        if constexpr (MR == 1) {
+            // two blocks a 16-byte load: whole groups of 16 blocks, then the
+            // last group's live pairs (a wave's range is an even number of
+            // blocks, so a pair that starts below nb_live was written)
+            const float *xp = (const float *)(xy + (fj * ncol + fc) * bs2);
+            auto group16 = [&](uint32_t b0, auto tail_tag) {
+                constexpr bool TAIL = decltype(tail_tag)::value;
+                float4_t v4[8];
 #pragma unroll
-            for (int h = 0; h < 8; h++) {
-                const bool live = !TAIL || b0 + 2 * h < nb_live;
-                v4[h] = *(const float4_t *)(xp + 2 * (live ? b0 + 2 * h : 0));
-                if (TAIL && !live) v4[h] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
-            }
+                for (int h = 0; h < 8; h++) {
+                    const bool live = !TAIL || b0 + 2 * h < nb_live;
+                    v4[h] = *(const float4_t *)(xp + 2 * (live ? b0 + 2 * h : 0));
+                    if (TAIL && !live) v4[h] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
+                }
 #pragma unroll
-            for (int h = 0; h < 8; h++) {
-                total = fmaf(v4[h][0], v4[h][1], total);
-                total = fmaf(v4[h][2], v4[h][3], total);
-            }
-        };
-        const uint32_t nb16 = nb_live & ~15u;
-        for (uint32_t b0 = 0; b0 < nb16; b0 += 16) group16(b0, std::false_type{});
-        if (nb16 < nb_live) group16(nb16, std::true_type{});
+                for (int h = 0; h < 8; h++) {
+                    total = fmaf(v4[h][0], v4[h][1], total);
+                    total = fmaf(v4[h][2], v4[h][3], total);
+                }
+            };
+            const uint32_t nb16 = nb_live & ~15u;
+            for (uint32_t b0 = 0; b0 < nb16; b0 += 16) group16(b0, std::false_type{});
+            if (nb16 < nb_live) group16(nb16, std::true_type{});
+        } else {
+            // per block: x, and y = f32(scale) * s by v_fma_mix (the f16 scale
+            // widened exactly, one rounding); blocks past K add nothing
+            const float *xp = xs + ((fj * MR + frow) * ncol + fc) * bs;
+            const uint16_t *cp = scl + (fj * ncol + fc) * bs;
+            const float *ap = sa + frow * nbq;
+            auto group16 = [&](uint32_t b0, auto tail_tag) {
+                constexpr bool TAIL = decltype(tail_tag)::value;
+                float4_t x4[4], a4[4];
+                uint2 c4[4];
+#pragma unroll
+                for (int h = 0; h < 4; h++) {
+                    const uint32_t bh = !TAIL || b0 + 4 * h < nb_live ? b0 + 4 * h : 0;
+                    x4[h] = *(const float4_t *)(xp + bh);
+                    c4[h] = *(const uint2 *)(cp + bh);
+                    a4[h] = *(const float4_t *)(ap + bh);
+                }
+#pragma unroll
+                for (int h = 0; h < 4; h++) {
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const uint32_t cw = u < 2 ? c4[h].x : c4[h].y;
+                        float y, x = x4[h][u];
+                        if (u % 2 == 0)
+                            asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]"
+                                : "=v"(y) : "v"(cw), "v"(a4[h][u]), "v"(-0.0f));
+                        else
+                            asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+                                : "=v"(y) : "v"(cw), "v"(a4[h][u]), "v"(-0.0f));
+                        if constexpr (TAIL) {
+                            const bool live = b0 + 4 * h + u < nb_live;
+                            x = live ? x : 0.0f;
+                            y = live ? y : 0.0f;
+                        }
+                        total = fmaf(x, y, total);
+                    }
+                }
+            };
+            const uint32_t nb_full = nb_live & ~15u;
+            for (uint32_t b0 = 0; b0 < nb_full; b0 += 16) group16(b0, std::false_type{});
+            if (nb_full < nb_live) group16(nb_full, std::true_type{});
+        }
         if (fcol < n) {
             uint16_t out;
             if constexpr (EPV == 0) {
-                out = finish_pre<false>(ep, pre, total, 0, fcol, n);
+                out = finish_pre<false>(ep, pre, total, frow, fcol, n);
             } else {
                 out = f32_to_f16(total);
                 if constexpr (EPV >= 2) {
@@ -1140,7 +1259,7 @@ __global__ void __launch_bounds__(T)
                     out = act == EP_ACT_NONE ? f32_to_f16(x) : act_round16<false>(act, x, alpha);
                 }
             }
-            dst[fcol] = out;
+            dst[(size_t)frow * n + fcol] = out;
         }
     }
 }
@@ -1205,56 +1324,67 @@ hipError_t launch_tile(const LtArgs &g, const EpArgs &ep, int mr, int ng, hipStr
 }
 
 
-// The persistent one-row kernel (lowbit_row): compiled stores only (the
-// interpreted graph, Q2 with 8 code groups a lane and more than 4 tiles per
-// compute unit take lowbit_tile); hipErrorNotSupported leaves those to it.
-template <int KIND, int NG, int EPV, int TPW>
+// The persistent kernel (lowbit_row): up to 8 rows, blocks of 128, compiled
+// stores only (the interpreted graph, Q2 with 8 code groups a lane, more than
+// 4 tiles a compute unit and LDS past 150 KB take lowbit_tile);
+// hipErrorNotSupported leaves those to it.
+template <int KIND, int MR, int NG, int EPV, int TPW>
 hipError_t launch_row_v(const LtArgs &g, const EpArgs &ep, const EpPick &pk, uint32_t grid, hipStream_t s) {
-    const size_t lds = row_lds_bytes(g.kq, g.nbq, 1u << g.cg_shift, TPW);
+    const size_t lds = row_lds_bytes(g.kq, g.nbq, 1u << g.cg_shift, TPW, MR);
     if (lds > 64 * 1024) {
         static bool attr = false;  // benign race: every setter writes the same value
         if (!attr) {
-            const hipError_t e = hipFuncSetAttribute((const void *)lowbit_row<KIND, NG, EPV, TPW>,
+            const hipError_t e = hipFuncSetAttribute((const void *)lowbit_row<KIND, MR, NG, EPV, TPW>,
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
             if (e != hipSuccess) return e;
             attr = true;
         }
     }
-    hipLaunchKernelGGL((lowbit_row<KIND, NG, EPV, TPW>), dim3(grid), dim3(T), lds, s, g.codes, g.sc, g.lhs, g.dst,
-                       pk.b, g.k, g.cg_shift | (pk.act << 8), g.n, g.codebook, pk.a, pk.alpha, ep);
+    hipLaunchKernelGGL((lowbit_row<KIND, MR, NG, EPV, TPW>), dim3(grid), dim3(T), lds, s, g.codes, g.sc, g.lhs,
+                       g.dst, pk.b, g.k, g.cg_shift | (pk.act << 8) | (g.m << 16), g.n, g.codebook, pk.a, pk.alpha,
+                       ep);
     return hipGetLastError();
 }
-template <int KIND, int NG, int EPV>
+template <int KIND, int MR, int NG, int EPV>
 hipError_t launch_row_t(const LtArgs &g, const EpArgs &ep, const EpPick &pk, uint32_t grid, int tpw, hipStream_t s) {
     switch (tpw) {
-    case 1: return launch_row_v<KIND, NG, EPV, 1>(g, ep, pk, grid, s);
-    case 2: return launch_row_v<KIND, NG, EPV, 2>(g, ep, pk, grid, s);
-    case 3: return launch_row_v<KIND, NG, EPV, 3>(g, ep, pk, grid, s);
-    default: return launch_row_v<KIND, NG, EPV, 4>(g, ep, pk, grid, s);
+    case 1: return launch_row_v<KIND, MR, NG, EPV, 1>(g, ep, pk, grid, s);
+    case 2: return launch_row_v<KIND, MR, NG, EPV, 2>(g, ep, pk, grid, s);
+    case 3: return launch_row_v<KIND, MR, NG, EPV, 3>(g, ep, pk, grid, s);
+    default: return launch_row_v<KIND, MR, NG, EPV, 4>(g, ep, pk, grid, s);
     }
 }
-template <int KIND, int NG>
+template <int KIND, int MR, int NG>
 hipError_t launch_row_e(const LtArgs &g, const EpArgs &ep, uint32_t grid, int tpw, hipStream_t s) {
     const EpPick pk = pick_ep(ep);
-    if (pk.v == 1) return launch_row_t<KIND, NG, 1>(g, ep, pk, grid, tpw, s);
-    if (pk.v == 2) return launch_row_t<KIND, NG, 2>(g, ep, pk, grid, tpw, s);
-    if (pk.v == 3) return launch_row_t<KIND, NG, 3>(g, ep, pk, grid, tpw, s);
+    if (pk.act > 0xFF) return hipErrorNotSupported;
+    if (pk.v == 1) return launch_row_t<KIND, MR, NG, 1>(g, ep, pk, grid, tpw, s);
+    if (pk.v == 2) return launch_row_t<KIND, MR, NG, 2>(g, ep, pk, grid, tpw, s);
+    if (pk.v == 3) return launch_row_t<KIND, MR, NG, 3>(g, ep, pk, grid, tpw, s);
+    return hipErrorNotSupported;
+}
+template <int KIND, int MR>
+hipError_t launch_row_ng(const LtArgs &g, const EpArgs &ep, int ng, uint32_t grid, int tpw, hipStream_t s) {
+    if (ng <= 1) return launch_row_e<KIND, MR, 1>(g, ep, grid, tpw, s);
+    if (ng <= 2) return launch_row_e<KIND, MR, 2>(g, ep, grid, tpw, s);
+    if (ng <= 4) return launch_row_e<KIND, MR, 4>(g, ep, grid, tpw, s);
     return hipErrorNotSupported;
 }
 template <int KIND>
 hipError_t launch_row(const LtArgs &g, const EpArgs &ep, int ng, hipStream_t s) {
     const uint32_t tiles = g.n_pad >> (4 + g.cg_shift);
     const uint32_t grid = std::min<uint32_t>(tiles, (uint32_t)device_cus());
-    const int tpw = (int)((tiles + grid - 1) / grid);
+    const int tpw = grid ? (int)((tiles + grid - 1) / grid) : 0;
+    const int mr = g.m <= 1 ? 1 : g.m <= 2 ? 2 : g.m <= 4 ? 4 : 8;
     const uint32_t grp = KIND == 2 ? Q2_GROUP : Q1_GROUP;
-    if (g.m != 1 || g.block_shift != 7 || tpw > 4 || grid == 0 || g.n_pad != (((g.n ? g.n : 1u) + 127u) & ~127u) ||
-        g.ngroups != (g.k + grp - 1) / grp || row_lds_bytes(g.kq, g.nbq, 1u << g.cg_shift, tpw) > 96 * 1024)
+    if (g.m < 1 || g.m > 8 || g.block_shift != 7 || tpw < 1 || tpw > 4 ||
+        g.n_pad != (((g.n ? g.n : 1u) + 127u) & ~127u) || g.ngroups != (g.k + grp - 1) / grp ||
+        row_lds_bytes(g.kq, g.nbq, 1u << g.cg_shift, tpw, mr) > 150 * 1024)
         return hipErrorNotSupported;
-    if (pick_ep(ep).act > 0xFFFFFF) return hipErrorNotSupported;
-    if (ng <= 1) return launch_row_e<KIND, 1>(g, ep, grid, tpw, s);
-    if (ng <= 2) return launch_row_e<KIND, 2>(g, ep, grid, tpw, s);
-    if (ng <= 4) return launch_row_e<KIND, 4>(g, ep, grid, tpw, s);
-    return hipErrorNotSupported;
+    if (mr == 1) return launch_row_ng<KIND, 1>(g, ep, ng, grid, tpw, s);
+    if (mr == 2) return launch_row_ng<KIND, 2>(g, ep, ng, grid, tpw, s);
+    if (mr == 4) return launch_row_ng<KIND, 4>(g, ep, ng, grid, tpw, s);
+    return launch_row_ng<KIND, 8>(g, ep, ng, grid, tpw, s);
 }
 
 // One workgroup per (row, block): q for the block's depths (zero past k), the
@@ -1451,6 +1581,10 @@ hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint
         f.codes_bytes = (uint32_t)cb;
         f.cg_shift = sg.cg_shift;
         const int mr = m <= 2 ? (int)m : m <= 4 ? 4 : 8;
+        {
+            const hipError_t e = w.kind == W_Q2 ? launch_row<2>(f, ep, sg.ng, s) : launch_row<1>(f, ep, sg.ng, s);
+            if (e != hipErrorNotSupported) return e;
+        }
         if (m > 1) {
             f.q = (const int8_t *)scratch;
             f.qs = (const float *)((uint8_t *)scratch + (m * sg.kq + 255) / 256 * 256);
@@ -1464,10 +1598,6 @@ hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint
                                    f.block_shift, (int8_t *)f.q, (float *)f.qs, (int32_t *)f.qsum);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
-        }
-        if (m == 1) {
-            const hipError_t e = w.kind == W_Q2 ? launch_row<2>(f, ep, sg.ng, s) : launch_row<1>(f, ep, sg.ng, s);
-            if (e != hipErrorNotSupported) return e;
         }
         if (w.kind == W_Q2) return launch_tile<2>(f, ep, mr, sg.ng, s);
         return launch_tile<1>(f, ep, mr, sg.ng, s);
