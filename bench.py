@@ -28,7 +28,9 @@ times must match) and the average kernel duration inside it.
     and its fraction of 139.5 MB/token at 8 TB/s, over 4 block copies (558 MB,
     a 4-layer model's worth) so each step's weights come from HBM;
   - `floors`: a plain streaming read of each config's bytes over the same
-    rotation (the time a single launch reading that much needs on this box).
+    rotation (the time a single launch reading that much needs on this box),
+    and for config 1 the same read followed by a store of the GEMV's output
+    (`config1_with_store`: a launch that writes its result pays for it).
 `cpu_baseline` is the C restatement of the reference's portable path (oracle/)
 on this host: config 1 single-threaded (faithful mode, a bounded sample) and
 over `cores` threads (threaded mode, bit-identical); `extra.cpu` the other
@@ -179,19 +181,30 @@ def rotate(w, per_copy_bytes):
     return [w] + [w.clone() for _ in range(copies - 1)]
 
 
-def stream_floor(smg, torch, timer, nbytes, steps, warmup):
-    """A plain read of `nbytes` per call over a rotation past the MALL."""
+def stream_floor(smg, torch, timer, nbytes, steps, warmup, out_bytes=0):
+    """A plain read of `nbytes` per call over a rotation past the MALL (with
+    out_bytes, the same read that then stores that many bytes of output, as a
+    GEMV stores its result)."""
     per = (nbytes + 4095) // 4096 * 4096
     copies = max(1, -(-(2 * MALL_BYTES + 64 * 2**20) // per))
     buf = torch.zeros(per * copies // 4, dtype=torch.int32, device="cuda")
+    out = torch.empty(max(out_bytes, 2) // 2, dtype=torch.int16, device="cuda")
     base = buf.data_ptr()
     L = smg.lib()
-    calls = [(lambda i=i: L.smg_stream_read_dev(base + i * per, nbytes // 16 * 16,
-                                                torch.cuda.current_stream().cuda_stream))
-             for i in range(copies)]
+    if out_bytes:
+        calls = [(lambda i=i: L.smg_stream_read_store_dev(base + i * per, nbytes // 16 * 16, out.data_ptr(),
+                                                          out_bytes, torch.cuda.current_stream().cuda_stream))
+                 for i in range(copies)]
+    else:
+        calls = [(lambda i=i: L.smg_stream_read_dev(base + i * per, nbytes // 16 * 16,
+                                                    torch.cuda.current_stream().cuda_stream))
+                 for i in range(copies)]
     us = timer(calls, steps, warmup)
-    del buf
-    return {"bytes": nbytes, "us": us, "GBps": nbytes / (us * 1e-6) / 1e9}
+    del buf, out
+    r = {"bytes": nbytes, "us": us, "GBps": nbytes / (us * 1e-6) / 1e9}
+    if out_bytes:
+        r["out_bytes"] = out_bytes
+    return r
 
 
 def shader_clock_mhz(smg, torch):
@@ -277,12 +290,14 @@ def main():
     us1 = timer(calls, steps, warm, min_calls=0)  # exactly `steps` passes over the 64 copies
     us1_hot = timer(calls[:1], steps, warm, flush=False)
     achieved = bytes1 / (us1 * 1e-6) / 1e9
-    floors = {"config1": stream_floor(smg, torch, timer, bytes1, steps, warm)}
+    floors = {"config1": stream_floor(smg, torch, timer, bytes1, steps, warm),
+              "config1_with_store": stream_floor(smg, torch, timer, bytes1, steps, warm, out_bytes=2 * n)}
     extra = {"config1_q4_gemv": {
         "bytes": bytes1, "weight_copies": len(ws), "us_cold": us1, "us_hot_mall": us1_hot,
         "GBps_cold": achieved, "GBps_hot": bytes1 / (us1_hot * 1e-6) / 1e9,
         "frac_hbm_cold": achieved / HBM_PEAK_GBS,
         "vs_stream_floor": us1 / floors["config1"]["us"],
+        "vs_store_floor": us1 / floors["config1_with_store"]["us"],
         "launch_us": launch_us, "kernel_us_est": us1 - launch_us}}
     len_rot1 = len(ws)
     del ws, calls

@@ -493,6 +493,10 @@ int smg_layer_norm_f16(const float *x, const float *weight, const float *bias, s
  * memory, writing nothing: the time floor that a single launch reading that
  * many bytes meets on this device. */
 int smg_stream_read_dev(const void *p, size_t bytes, void *stream);
+/* The same pass, then `out_bytes` (a multiple of 2) of device memory at `out`
+ * written with 16-bit values, one per thread, as a GEMV writes its output:
+ * the floor of a launch that reads `bytes` and stores a result. */
+int smg_stream_read_store_dev(const void *p, size_t bytes, void *out, size_t out_bytes, void *stream);
 /* Spins one wave `iters` times and stores out[0] = shader-clock ticks
  * (clock64) and out[1] = 100 MHz wall-clock ticks over the spin (device
  * memory, 3 words): out[0] / out[1] * 100 MHz is the shader clock then. */

@@ -1646,7 +1646,7 @@ int smg_lowbit_matmul_dev(size_t m, const smg_weights *w, uint16_t *dst, const u
     if (rc) return rc;
     if ((rc = check_dev_ptrs("smg_lowbit_matmul_dev", w->device, stream, ep_p, {dst, lhs}))) return rc;
     const EpArgs &ea = ep_p.fused;
-    const size_t sb = lowbit_scratch_bytes(w->d, m);
+    const size_t sb = lowbit_scratch_bytes(w->d, m, &ea);
     void *scratch = nullptr;
     if (sb) {
         // several rows (or blocks past one in-kernel pass): the activations
@@ -1673,7 +1673,7 @@ int smg_lowbit_matmul_dev_noalloc(size_t m, const smg_weights *w, uint16_t *dst,
     if (rc) return rc;
     if ((rc = check_dev_ptrs("smg_lowbit_matmul_dev_noalloc", w->device, stream, ep_p, {dst, lhs}))) return rc;
     const EpArgs &ea = ep_p.fused;
-    const size_t sb = lowbit_scratch_bytes(w->d, m);
+    const size_t sb = lowbit_scratch_bytes(w->d, m, &ea);
     if (sb > SMG_NOALLOC_SCRATCH_BYTES)
         return fail(SMG_EINVAL, "smg_lowbit_matmul_dev_noalloc: the call needs more scratch than "
                                 "SMG_NOALLOC_SCRATCH_BYTES (fewer rows or a shorter K)");
@@ -2269,6 +2269,13 @@ int smg_stream_read_dev(const void *p, size_t bytes, void *stream) {
     if (!p || bytes % 16) return fail(SMG_EINVAL, "smg_stream_read_dev: a device pointer and a multiple of 16 bytes");
     hipError_t e = launch_stream_read(p, bytes, nullptr, (hipStream_t)stream);
     return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_stream_read_dev", e);
+}
+
+int smg_stream_read_store_dev(const void *p, size_t bytes, void *out, size_t out_bytes, void *stream) {
+    if (!p || bytes % 16 || (out_bytes && !out) || out_bytes % 2)
+        return fail(SMG_EINVAL, "smg_stream_read_store_dev: device pointers, bytes a multiple of 16, out_bytes of 2");
+    hipError_t e = launch_stream_read_store(p, bytes, (uint16_t *)out, out_bytes / 2, (hipStream_t)stream);
+    return e == hipSuccess ? SMG_OK : fail(SMG_EHIP, "smg_stream_read_store_dev", e);
 }
 
 int smg_clock_probe_dev(unsigned long long *out, unsigned iters, void *stream) {

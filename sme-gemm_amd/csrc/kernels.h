@@ -60,8 +60,11 @@ hipError_t launch_q4_gemv_chained(const WDev &w, size_t m, uint16_t *dst, const 
                                   const EpArgs &ep, const ChainArgs &ch, hipStream_t s);
 
 // Low-bit int8 path. scratch: device buffer of lowbit_scratch_bytes() bytes
-// (only used when the block is too large to quantize in-kernel).
-size_t lowbit_scratch_bytes(const WDev &w, size_t m);
+// (used when the activations are quantized before the product kernel: several
+// rows outside the persistent kernel, or blocks too large to quantize
+// in-kernel). ep: the call's fused op-graph, which decides whether the
+// persistent kernel serves (then 0); null sizes for the other kernels.
+size_t lowbit_scratch_bytes(const WDev &w, size_t m, const EpArgs *ep = nullptr);
 hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint16_t *lhs,
                               const EpArgs &ep, void *scratch, hipStream_t s);
 
@@ -182,6 +185,7 @@ hipError_t launch_add_f16(const uint16_t *h, size_t count, float *y, hipStream_t
 
 // Measurement probes (probes.hip).
 hipError_t launch_stream_read(const void *p, size_t bytes, unsigned *sink, hipStream_t s);
+hipError_t launch_stream_read_store(const void *p, size_t bytes, uint16_t *out, size_t nout, hipStream_t s);
 hipError_t launch_clock_probe(unsigned long long *out, unsigned iters, hipStream_t s);
 
 // Sets the calling thread's smg_last_error() text and returns code.

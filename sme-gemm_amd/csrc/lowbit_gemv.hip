@@ -1370,17 +1370,18 @@ hipError_t launch_row_ng(const LtArgs &g, const EpArgs &ep, int ng, uint32_t gri
     if (ng <= 4) return launch_row_e<KIND, MR, 4>(g, ep, grid, tpw, s);
     return hipErrorNotSupported;
 }
+// The persistent grid's shape for a call of tile_geometry sg: its workgroups
+// and tiles a workgroup, or tpw = 0 when lowbit_row does not serve the call.
+struct RowShape {
+    uint32_t grid;
+    int tpw;
+};
 template <int KIND>
-hipError_t launch_row(const LtArgs &g, const EpArgs &ep, int ng, hipStream_t s) {
-    const uint32_t tiles = g.n_pad >> (4 + g.cg_shift);
-    const uint32_t grid = std::min<uint32_t>(tiles, (uint32_t)device_cus());
-    const int tpw = grid ? (int)((tiles + grid - 1) / grid) : 0;
+hipError_t launch_row(const LtArgs &g, const EpArgs &ep, int ng, const RowShape &rs, hipStream_t s) {
+    const uint32_t grid = rs.grid;
+    const int tpw = rs.tpw;
     const int mr = g.m <= 1 ? 1 : g.m <= 2 ? 2 : g.m <= 4 ? 4 : 8;
-    const uint32_t grp = KIND == 2 ? Q2_GROUP : Q1_GROUP;
-    if (g.m < 1 || g.m > 8 || g.block_shift != 7 || tpw < 1 || tpw > 4 ||
-        g.n_pad != (((g.n ? g.n : 1u) + 127u) & ~127u) || g.ngroups != (g.k + grp - 1) / grp ||
-        row_lds_bytes(g.kq, g.nbq, 1u << g.cg_shift, tpw, mr) > 150 * 1024)
-        return hipErrorNotSupported;
+    if (tpw < 1) return hipErrorNotSupported;
     if (mr == 1) return launch_row_ng<KIND, 1>(g, ep, ng, grid, tpw, s);
     if (mr == 2) return launch_row_ng<KIND, 2>(g, ep, ng, grid, tpw, s);
     if (mr == 4) return launch_row_ng<KIND, 4>(g, ep, ng, grid, tpw, s);
@@ -1543,13 +1544,32 @@ TileGeo tile_geometry(const WDev &w, size_t m) {
     return none;
 }
 
+RowShape row_shape(const WDev &w, size_t m, const TileGeo &sg, const EpArgs &ep) {
+    RowShape r = {0, 0};
+    const uint32_t grp = w.kind == W_Q2 ? Q2_GROUP : Q1_GROUP;
+    if (!sg.ok || m < 1 || m > 8 || w.block != 128 || sg.ng > 4 ||
+        w.n_pad != (((w.n ? w.n : 1u) + 127u) & ~(size_t)127u) || w.nchunks != (w.k + grp - 1) / grp)
+        return r;
+    const EpPick pk = pick_ep(ep);
+    if (pk.v < 1 || pk.v > 3 || pk.act > 0xFF) return r;
+    const uint32_t tiles = (uint32_t)(w.n_pad >> (4 + sg.cg_shift));
+    const uint32_t grid = std::min<uint32_t>(tiles, (uint32_t)device_cus());
+    const int tpw = grid ? (int)((tiles + grid - 1) / grid) : 0;
+    const int mr = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+    if (tpw < 1 || tpw > 4 || row_lds_bytes(sg.kq, sg.nbq, 1u << sg.cg_shift, tpw, mr) > 150 * 1024) return r;
+    r.grid = grid;
+    r.tpw = tpw;
+    return r;
+}
+
 // Bytes of the pre-quantized rows (q [m][kq], then s and sum(q) [m][nbq]).
 size_t prequant_bytes(size_t m, size_t kq, size_t nbq) { return (m * kq + 255) / 256 * 256 + m * nbq * 8; }
 
 }  // namespace
 
-size_t lowbit_scratch_bytes(const WDev &w, size_t m) {
+size_t lowbit_scratch_bytes(const WDev &w, size_t m, const EpArgs *ep) {
     const TileGeo sg = tile_geometry(w, m);
+    if (sg.ok && ep && row_shape(w, m, sg, *ep).tpw > 0) return 0;  // lowbit_row quantizes in-kernel
     if (sg.ok) return m > 1 ? prequant_bytes(m, sg.kq, sg.nbq) : 0;
     const Geo ge = geometry(w, m);
     return (m * ge.kq + 255) / 256 * 256 + m * ge.nbq * 8;
@@ -1581,10 +1601,9 @@ hipError_t launch_lowbit_gemv(const WDev &w, size_t m, uint16_t *dst, const uint
         f.codes_bytes = (uint32_t)cb;
         f.cg_shift = sg.cg_shift;
         const int mr = m <= 2 ? (int)m : m <= 4 ? 4 : 8;
-        {
-            const hipError_t e = w.kind == W_Q2 ? launch_row<2>(f, ep, sg.ng, s) : launch_row<1>(f, ep, sg.ng, s);
-            if (e != hipErrorNotSupported) return e;
-        }
+        const RowShape rs = row_shape(w, m, sg, ep);
+        if (rs.tpw > 0)
+            return w.kind == W_Q2 ? launch_row<2>(f, ep, sg.ng, rs, s) : launch_row<1>(f, ep, sg.ng, rs, s);
         if (m > 1) {
             f.q = (const int8_t *)scratch;
             f.qs = (const float *)((uint8_t *)scratch + (m * sg.kq + 255) / 256 * 256);

@@ -20,6 +20,19 @@ __global__ void __launch_bounds__(256) stream_read(const uint4 *p, size_t n16, u
     if (acc == 0x9E3779B9u && sink) sink[0] = acc;
 }
 
+// stream_read, then threads 0 .. nout - 1 of the grid each store the low 16
+// bits of their fold to out[thread]: a read of the same bytes that also
+// writes a GEMV-sized output.
+__global__ void __launch_bounds__(256) stream_read_store(const uint4 *p, size_t n16, uint16_t *out, size_t nout) {
+    uint32_t acc = 0;
+    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (size_t i = tid; i < n16; i += (size_t)gridDim.x * blockDim.x) {
+        const uint4 v = p[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (tid < nout) out[tid] = (uint16_t)acc;
+}
+
 // Thread 0 of one workgroup spins `iters` times, reading the shader clock
 // (clock64) and the 100 MHz wall clock before and after.
 __global__ void clock_probe(unsigned long long *out, unsigned iters) {
@@ -40,6 +53,13 @@ hipError_t launch_stream_read(const void *p, size_t bytes, unsigned *sink, hipSt
     if (n16 == 0) return hipSuccess;
     const size_t blocks = std::min<size_t>((n16 + 255) / 256, 256 * 8);
     hipLaunchKernelGGL(stream_read, dim3((uint32_t)blocks), dim3(256), 0, s, (const uint4 *)p, n16, sink);
+    return hipGetLastError();
+}
+
+hipError_t launch_stream_read_store(const void *p, size_t bytes, uint16_t *out, size_t nout, hipStream_t s) {
+    const size_t n16 = bytes / 16;
+    const size_t blocks = std::max<size_t>(std::min<size_t>((n16 + 255) / 256, 256 * 8), (nout + 255) / 256);
+    hipLaunchKernelGGL(stream_read_store, dim3((uint32_t)blocks), dim3(256), 0, s, (const uint4 *)p, n16, out, nout);
     return hipGetLastError();
 }
 

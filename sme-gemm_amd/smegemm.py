@@ -147,6 +147,7 @@ def lib() -> C.CDLL:
     L.smg_rms_norm_f16.argtypes = [P, P, SZ, SZ, C.c_float, P]
     L.smg_layer_norm_f16.argtypes = [P, P, P, SZ, SZ, C.c_float, P]
     L.smg_stream_read_dev.argtypes = [P, SZ, P]
+    L.smg_stream_read_store_dev.argtypes = [P, SZ, P, SZ, P]
     L.smg_clock_probe_dev.argtypes = [P, C.c_uint, P]
     _lib = L
     return L

@@ -27,12 +27,15 @@ def _run(fn, torch, m, w, ad, n, ep_ptr, fill=0):
     return rc, cd.cpu().numpy().view(np.uint16)
 
 
+# blocks of 128 run on the persistent kernel, which quantizes in-kernel (no
+# scratch); blocks of 64 quantize several rows into the static array first
+@pytest.mark.parametrize("block", [128, 64])
 @pytest.mark.parametrize("kind", [2, 1])
-def test_noalloc_matches_the_allocating_entry_point(smg, orc, kind):
+def test_noalloc_matches_the_allocating_entry_point(smg, orc, kind, block):
     import torch
     dev_fn, noalloc_fn = _fns(smg)
-    rng = np.random.default_rng(70 + kind)
-    n, k, block = 2048, 4096, 128
+    rng = np.random.default_rng(70 + kind + block)
+    n, k = 2048, 4096
     nbk = k // block
     scales = orc.f32_to_f16(rng.uniform(0.01, 0.05, n * nbk).astype(np.float32))
     if kind == 2:
@@ -52,9 +55,9 @@ def test_noalloc_matches_the_allocating_entry_point(smg, orc, kind):
         rc0, want = _run(dev_fn, torch, m, w, ad, n, ep_ptr)
         rc1, got = _run(noalloc_fn, torch, m, w, ad, n, ep_ptr, fill=0x1234)
         assert rc0 == 0 and rc1 == 0, smg.last_error()
-        assert np.array_equal(got, want), f"kind {kind} m={m}"
+        assert np.array_equal(got, want), f"kind {kind} block {block} m={m}"
         ref = orc.matmul_lowbit_ep(kind, a, codes, scales, m, n, k, block, [(4, 0, 0.0, bias, 0)], 3)
-        assert np.array_equal(got, ref), f"kind {kind} m={m} vs oracle"
+        assert np.array_equal(got, ref), f"kind {kind} block {block} m={m} vs oracle"
 
 
 def test_noalloc_refuses_calls_past_its_scratch(smg, orc):
