@@ -1556,7 +1556,10 @@ RowShape row_shape(const WDev &w, size_t m, const TileGeo &sg, const EpArgs &ep)
     const uint32_t grid = std::min<uint32_t>(tiles, (uint32_t)device_cus());
     const int tpw = grid ? (int)((tiles + grid - 1) / grid) : 0;
     const int mr = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
-    if (tpw < 1 || tpw > 4 || row_lds_bytes(sg.kq, sg.nbq, 1u << sg.cg_shift, tpw, mr) > 150 * 1024) return r;
+    // one folding thread per (tile, row, column) of a workgroup
+    if (tpw < 1 || tpw > 4 || (size_t)tpw * mr * (16u << sg.cg_shift) > (size_t)T ||
+        row_lds_bytes(sg.kq, sg.nbq, 1u << sg.cg_shift, tpw, mr) > 150 * 1024)
+        return r;
     r.grid = grid;
     r.tpw = tpw;
     return r;

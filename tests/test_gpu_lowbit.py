@@ -422,3 +422,44 @@ def test_multi_row_calls_in_a_replayed_graph(smg, orc):
         for m, ad, cd, want in cases:  # eager work between replays
             smg.matmul_q2(ad, w, cd, m)
         torch.cuda.synchronize()
+
+
+# Shapes of the persistent kernel (lowbit_row: m <= 8, blocks of 128, the
+# compiled stores): 1-4 tiles a compute unit on a 256-CU device (N up to 53248
+# with 64-column tiles), K short of a block, ragged, over one pass (8192), and
+# grids of fewer tiles than compute units.
+ROW_CASES = [(1, 16, 128), (2, 48, 640), (3, 2064, 4096), (5, 4112, 1000), (8, 12304, 4096),
+             (1, 14336, 8192), (7, 20496, 384), (4, 53248, 128), (1, 53264, 256), (6, 33, 4100)]
+
+
+@pytest.mark.parametrize("graph", ["none", "add_silu", "mul_add_relu"])
+@pytest.mark.parametrize("case", range(len(ROW_CASES)))
+@pytest.mark.parametrize("kind", [2, 1])
+def test_persistent_row_kernel_shapes(smg, orc, kind, case, graph):
+    """Bit for bit against the oracle's portable path, every compiled store."""
+    m, n, k = ROW_CASES[case]
+    rng = np.random.default_rng(1000 * kind + 10 * case + len(graph))
+    a = orc.f32_to_f16(rng.standard_normal(m * k).astype(np.float32))
+    nbk = -(-k // 128)
+    scales = orc.f32_to_f16(rng.uniform(0.01, 0.05, n * nbk).astype(np.float32))
+    if kind == 2:
+        codes = rng.integers(0, 256, (k * n + 3) // 4, dtype=np.uint8)
+        w = smg.Q2Weights(codes, scales, n, k, smg.Q2Params(128))
+    else:
+        codes = rng.integers(0, 256, (k * n + 7) // 8, dtype=np.uint8)
+        w = smg.Q1Weights(codes, scales, smg.WeightLayout.OutIn, n, k, 128)
+    colv = orc.f32_to_f16(rng.uniform(0.5, 1.5, n).astype(np.float32))
+    bias = orc.f32_to_f16(rng.normal(0, 0.1, n).astype(np.float32))
+    ep, nodes, act = None, [], 0
+    if graph == "add_silu":
+        ep, nodes, act = smg.Epilogue().add_col(bias).silu(), [(4, 0, 0.0, bias, 0)], 3
+    elif graph == "mul_add_relu":
+        ep = smg.Epilogue().mul_col(colv).add_col(bias).relu()
+        nodes, act = [(5, 0, 0.0, colv, 0), (4, 0, 0.0, bias, 0)], 1
+    got = np.full(m * n, 0x1234, np.uint16)
+    if kind == 2:
+        (smg.matmul_q2_ep(a, w, got, m, ep) if ep else smg.matmul_q2(a, w, got, m))
+    else:
+        (smg.matmul_q1_ep(a, w, got, m, ep) if ep else smg.matmul_q1(a, w, got, m))
+    want = orc.matmul_lowbit_ep(kind, a, codes, scales, m, n, k, 128, nodes, act)
+    assert np.array_equal(got, want), (kind, m, n, k, graph)
