@@ -214,6 +214,25 @@ def test_linear_accumulate(smg, orc, m, n, k):
     _check_term(y.cpu().numpy(), y0, out, f16_tol(k))
 
 
+# One row on the all-steps-in-flight decode GEMV: one or two tiles a compute
+# unit (N up to 8192 on 256 CUs), 4, 8, 14 or 16 weight steps a lane (K up to
+# 16384), ragged N and K, and the shapes it hands to the other kernels
+# (two tiles with more than 4 steps, more than two tiles).
+@pytest.mark.parametrize("n,k", [(5000, 4096), (8192, 4096), (200, 5000), (1000, 10000), (96, 16384),
+                                 (333, 14336), (4100, 5000), (9000, 2048), (4096, 100)])
+def test_linear_accumulate_one_row_shapes(smg, orc, n, k):
+    """Linear::accumulate (src/linear.rs:425-432) for one row."""
+    import torch
+    a, quants, scales, _ = WL.q4_inputs(1, n, k, seed=n + k)
+    lin = smg.Linear(smg.Q4Weights(quants, scales, n, k))
+    y0 = np.random.default_rng(2).standard_normal(n).astype(np.float32)
+    y = _f32(y0)
+    lin.accumulate(_h16(a), y, 1)
+    torch.cuda.synchronize()
+    out = orc.f16_to_f32(orc.matmul_q4_ep(a, quants, scales, None, 1, n, k, 32))
+    _check_term(y.cpu().numpy(), y0, out, f16_tol(k))
+
+
 def _mlp_oracle(orc, x16, inp, m, d, ffn, gated, gelu=False, parts=None):
     gq, gs, _, _ = inp["gate"]
     dq, ds, _, _ = inp["down"]
