@@ -154,6 +154,79 @@ def test_attention_config5_shape(smg, orc):
     assert np.max(np.abs(out.cpu().numpy() - want)) <= 1e-4 * (1 + vmax)
 
 
+def test_attention_merge_repeats_and_replays(smg, orc):
+    """The split partials and their merge (two launches on the stream's own
+    scratch): calls of 1 to 65 splits (head dims 32 to 256, decode and causal
+    rows, up to 64 query heads a KV head) agree with the oracle, give the same
+    bits when repeated in another order, and a HIP graph that captured them
+    replays them bit for bit three times, with eager calls between the
+    replays."""
+    import torch
+    rng = np.random.default_rng(11)
+    cases = []
+    for heads, kv_heads, hd, length, rows in [(32, 8, 128, 4097, 1), (8, 2, 64, 300, 1), (2, 2, 256, 1000, 1),
+                                              (32, 8, 128, 700, 5), (4, 1, 128, 64, 1), (64, 1, 32, 3100, 3)]:
+        q = (rng.standard_normal(rows * heads * hd) * 4).astype(np.float32)
+        k = orc.f32_to_f16(rng.standard_normal(length * kv_heads * hd).astype(np.float32))
+        v = orc.f32_to_f16(rng.standard_normal(length * kv_heads * hd).astype(np.float32))
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+        out = torch.empty(rows * heads * hd, dtype=torch.float32, device="cuda")
+        cases.append(dict(shape=(heads, kv_heads, hd, length, rows), q=q, k=k, v=v, qd=_f32(q), kd=_h16(k),
+                          vd=_h16(v), scale=scale, out=out))
+
+    def call(c):
+        heads, kv_heads, hd, length, rows = c["shape"]
+        if rows == 1:
+            smg.attention_kv_f16(c["qd"], c["kd"], c["vd"], length, heads, kv_heads, hd, c["scale"], c["out"])
+        else:
+            smg.attention_kv_causal_f16(c["qd"], c["kd"], c["vd"], length - rows, rows, heads, kv_heads, hd,
+                                        c["scale"], c["out"])
+
+    for c in cases:
+        call(c)
+    torch.cuda.synchronize()
+    first = [c["out"].cpu().numpy().copy() for c in cases]
+    for c, got in zip(cases, first):
+        heads, kv_heads, hd, length, rows = c["shape"]
+        if rows == 1:
+            want = orc.attention_kv_f16(c["q"], c["k"], c["v"], length, heads, kv_heads, hd, np.float32(c["scale"]))
+        else:
+            want = orc.attention_kv_causal_f16(c["q"], c["k"], c["v"], length - rows, rows, heads, kv_heads, hd,
+                                               np.float32(c["scale"]))
+        vmax = float(np.max(np.abs(orc.f16_to_f32(c["v"]))))
+        assert np.max(np.abs(got - want)) <= 1e-4 * (1 + vmax), c["shape"]
+    for c in reversed(cases):
+        c["out"].zero_()
+        call(c)
+    torch.cuda.synchronize()
+    for c, got in zip(cases, first):
+        assert np.array_equal(c["out"].cpu().numpy(), got), ("repeat", c["shape"])
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for c in cases:  # the capture stream's own scratch and counters, before capture
+            call(c)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=side):
+            for c in cases:
+                call(c)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for c in cases:
+            c["out"].zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for c, got in zip(cases, first):
+            assert np.array_equal(c["out"].cpu().numpy(), got), ("replay", rep, c["shape"])
+        for c in cases:  # eager calls between replays
+            call(c)
+        torch.cuda.synchronize()
+        for c, got in zip(cases, first):
+            assert np.array_equal(c["out"].cpu().numpy(), got), ("eager after replay", rep, c["shape"])
+
+
 def test_kv_cache_api(smg, orc):
     """KvCache on the device (kv_attention.rs:342-578; the reference's
     kv_cache_matches_free_functions): rows pushed one at a time and in blocks
