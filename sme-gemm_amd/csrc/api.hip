@@ -945,10 +945,17 @@ int carve_scratch(int device, void *stream, size_t base, std::initializer_list<s
 // The attention partial sums one launch may hold: a causal block of rows is
 // attended in chunks of rows whose partials fit (row r of a chunk needs
 // attn_splits(its prefix) x heads x (hd + 2) floats).
+// A block of rows that runs the matrix-core form is one launch with no
+// partials.
 constexpr size_t ATT_PART_BYTES = 64u << 20;
 size_t causal_chunk_rows(size_t rows, size_t last_len, size_t heads, size_t hd) {
+    if (attn_rows_blocked(rows)) return rows;
     const size_t per_row = attn_partial_floats(1, last_len, heads, hd) * 4;
     return std::max<size_t>(1, std::min(rows, ATT_PART_BYTES / per_row));
+}
+size_t causal_part_bytes(size_t rows, size_t last_len, size_t heads, size_t hd) {
+    if (attn_rows_blocked(rows)) return 0;
+    return attn_partial_floats(causal_chunk_rows(rows, last_len, heads, hd), last_len, heads, hd) * 4;
 }
 
 // Causal attention of `rows` f16 query rows (q16 [rows][heads hd], already
@@ -960,7 +967,7 @@ hipError_t causal_attention(const uint16_t *q16, const uint16_t *k, const uint16
                             hipStream_t s) {
     const size_t qlen = heads * hd, last = start + rows;
     const size_t rc = causal_chunk_rows(rows, last, heads, hd);
-    const size_t po_floats = rc * attn_splits(last) * heads * hd;
+    const size_t po_floats = attn_rows_blocked(rows) ? 0 : rc * attn_splits(last) * heads * hd;
     for (size_t r0 = 0; r0 < rows; r0 += rc) {
         AttnArgs at = {};
         at.q = q16 + r0 * qlen;
@@ -998,11 +1005,10 @@ int attn_rows(smg_attn *a, smg_kv_cache *c, const uint16_t *x16, float *y, size_
     if ((rc = ensure_rope(a, c->cap, &rope, &rope_cap))) return rc;
     const size_t pos = c->len, ld = a->kv_heads * a->hd, qlen = a->heads * a->hd, half = a->hd / 2;
     const size_t nq = a->qkv->d.n, d_out = a->out->d.n;
-    const size_t crow = causal_chunk_rows(m, pos + m, a->heads, a->hd);
     uint8_t *bufs[5];
     if ((rc = carve_scratch(a->device, stream, base,
                             {m * nq * 2, m * qlen * 2, m * qlen * 2, m > 8 ? m * d_out * 2 : 0,
-                             attn_partial_floats(crow, pos + m, a->heads, a->hd) * 4},
+                             causal_part_bytes(m, pos + m, a->heads, a->hd)},
                             bufs)))
         return rc;
     uint16_t *qkv16 = (uint16_t *)bufs[0], *q16 = (uint16_t *)bufs[1], *att16 = (uint16_t *)bufs[2];
@@ -1812,9 +1818,9 @@ int smg_kv_cache_extend_dev(smg_kv_cache *c, const uint16_t *k, const uint16_t *
 static int causal_dev(int device, const float *q, const uint16_t *k, const uint16_t *v, size_t start, size_t rows,
                       size_t heads, size_t kv_heads, size_t hd, float scale, float *out, void *stream) {
     if (!q || !k || !v || !out) return fail(SMG_EINVAL, "null array");
-    const size_t qlen = heads * hd, crow = causal_chunk_rows(rows, start + rows, heads, hd);
+    const size_t qlen = heads * hd;
     uint8_t *bufs[2];
-    int rc = carve_scratch(device, stream, 0, {rows * qlen * 2, attn_partial_floats(crow, start + rows, heads, hd) * 4},
+    int rc = carve_scratch(device, stream, 0, {rows * qlen * 2, causal_part_bytes(rows, start + rows, heads, hd)},
                            bufs);
     if (rc) return rc;
     hipStream_t s = (hipStream_t)stream;

@@ -715,6 +715,180 @@ __global__ void __launch_bounds__(CM_T) attn_combine(const float *po, const floa
     }
 }
 
+// ---------------------------------------------------------------------------
+// Causal attention of a block of query rows on the matrix cores
+// ---------------------------------------------------------------------------
+// For blocks of at least AP_MIN_ROWS rows (attention_kv_causal_f16's blocked
+// path, src/kernels/kv_attention.rs:198-201 with csrc/attention_kv_sme.h: the
+// same arithmetic as the one-row call -- q * scale rounded to f16, f32 scores
+// from f16 products, f32 exp, probabilities rounded to f16, f32 sums of p * v
+// -- with both products on the matrix unit, so only the order of the sums
+// differs; the reference holds such rows to 1e-3 of the one-row call). A
+// workgroup takes one KV head, a chunk of up to 4 of its query heads (one a
+// wave) and AP_BR consecutive query positions, and walks the keys of its last
+// position in blocks of AP_KB: the block's keys and values go global ->
+// registers (the next block's while this one is multiplied) -> LDS, keys
+// row-major and values transposed; each wave then forms S^T = K Q^T for its
+// head (v_mfma_f32_16x16x32_f16: A = 16 keys x 32 depths read from LDS, B =
+// its 16 query rows, kept in registers), masks keys past each row's own
+// position, updates the rows' running max and sum (flash attention's
+// rescale), and adds O^T += V^T P^T (v_mfma_f32_16x16x16_f16: A = 16 depths x
+// 4 keys of the transposed values, B = the f16 probabilities, which S^T's
+// accumulator layout already holds as that operand: lane l has row l % 16 and
+// keys 4 (l / 16) .. + 3 of a 16-key tile). Every lane's accumulators belong to
+// its row l % 16, so the rescale and the final o / l need no exchange.
+constexpr int AP_T = 256, AP_KB = 64, AP_BR = 16;
+constexpr uint32_t AP_MIN_ROWS = 32;
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float xor_lanes(float v, int m) { return __shfl_xor(v, m, 64); }
+
+template <int HDM>
+__global__ void __launch_bounds__(AP_T) attn_rows_mfma(AttnArgs a) {
+    constexpr int KK = HDM / 32;  // 32-depth steps of the scores
+    constexpr int DT = HDM / 16;  // 16-depth tiles of the output
+    constexpr int LJ = HDM / 32;  // 16-byte loads a thread a block, of keys and of values
+    constexpr int KS = HDM + 8;   // key row stride in LDS (halfs)
+    constexpr int VS = AP_KB + 4; // transposed value row stride (halfs): conflict-free 8-byte reads
+    __shared__ __align__(16) uint16_t k_lds[AP_KB * KS];
+    __shared__ __align__(16) uint16_t v_lds[HDM * VS];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, r16 = lane & 15, g4 = lane >> 4;
+    // unit u: head chunk u % ny, position tile u / ny (consecutive units, which
+    // the dispatcher spreads over the XCDs, take one tile's head chunks, so the
+    // workgroups of one KV head share an XCD's L2 when ny is a multiple of 8)
+    const uint32_t ny = (a.heads / a.group) * a.hchunks, yc = blockIdx.x % ny;
+    const uint32_t p0 = (blockIdx.x / ny) * AP_BR;
+    const uint32_t kvh = yc / a.hchunks, hc0 = (yc % a.hchunks) * AT_HC;
+    const bool head_ok = hc0 + wave < a.group;  // uniform per wave
+    const uint32_t h = kvh * a.group + hc0 + wave;
+    const uint32_t pend = min(p0 + AP_BR, a.rows);
+    const uint32_t nkeys = a.len + pend - 1;  // the last position's prefix
+    const uint32_t nblk = (nkeys + AP_KB - 1) / AP_KB;
+    const uint32_t row = p0 + r16;  // this lane's query position (of the block)
+    const bool rok = head_ok && row < a.rows;
+    const uint32_t lim = a.len + row;  // its keys: 0 .. lim - 1
+
+    // the wave's 16 query rows of head h (B operand of the scores)
+    const rsrc_t qr = make_rsrc(a.q, a.rows * a.heads * a.hd * 2u);
+    uint4 qf[KK];
+#pragma unroll
+    for (int kk = 0; kk < KK; kk++) {
+        const uint32_t d = 32u * kk + 8u * g4;
+        qf[kk] = bload16(qr, rok && d < a.hd ? ((row * a.heads + h) * a.hd + d) * 2u : OOB);
+    }
+    // a block's keys and values: thread t loads key t % 64, depths 8 ((t / 64) + 4 j) .. + 8
+    const rsrc_t kr = make_rsrc(a.k, nkeys * a.ld * 2u), vr = make_rsrc(a.v, nkeys * a.ld * 2u);
+    // two blocks' keys and values in flight in registers (sets A and B)
+    uint4 ka_[LJ], va_[LJ], kb_[LJ], vb_[LJ];
+    auto load_blk = [&](uint32_t b, uint4 (&kreg)[LJ], uint4 (&vreg)[LJ]) __attribute__((always_inline)) {
+        const uint32_t key = b * AP_KB + (uint32_t)(t & 63);
+#pragma unroll
+        for (int j = 0; j < LJ; j++) {
+            const uint32_t d = (uint32_t)((t >> 6) + 4 * j) * 8u;
+            const uint32_t off = b < nblk && key < nkeys && d < a.hd ? (key * a.ld + kvh * a.hd + d) * 2u : OOB;
+            kreg[j] = bload16(kr, off);
+            vreg[j] = bload16(vr, off);
+        }
+    };
+    auto store_blk = [&](const uint4 (&kreg)[LJ], const uint4 (&vreg)[LJ]) __attribute__((always_inline)) {
+        const int key = t & 63;
+#pragma unroll
+        for (int j = 0; j < LJ; j++) {
+            const int d0 = ((t >> 6) + 4 * j) * 8;
+            *(uint4 *)(k_lds + key * KS + d0) = kreg[j];
+            const uint32_t w[4] = {vreg[j].x, vreg[j].y, vreg[j].z, vreg[j].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) v_lds[(d0 + e) * VS + key] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+        }
+    };
+
+    float m_run = -INFINITY, l_run = 0.0f;
+    float4_t o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) o[dt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    // block b: its registers to LDS, then block b + 2's loads into them (a
+    // block past the last loads nothing: every offset out of range)
+    auto block = [&](uint32_t b, uint4 (&kreg)[LJ], uint4 (&vreg)[LJ]) __attribute__((always_inline)) {
+        __syncthreads();  // the previous block's LDS readers are done
+        store_blk(kreg, vreg);
+        load_blk(b + 2, kreg, vreg);
+        __syncthreads();
+        if (!head_ok) return;
+        // S^T for the block's 4 key tiles
+        float4_t sc[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) {
+            sc[kt] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++) {
+                const uint4 ka = *(const uint4 *)(k_lds + (16 * kt + r16) * KS + 32 * kk + 8 * g4);
+                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, ka),
+                                                                __builtin_bit_cast(half8_t, qf[kk]), sc[kt], 0, 0, 0);
+            }
+        }
+        // causal mask, the block's row max and the running rescale
+        float mb = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const uint32_t key = b * AP_KB + 16u * kt + 4u * g4 + v;
+                if (!rok || key >= lim) sc[kt][v] = -INFINITY;
+                mb = fmaxf(mb, sc[kt][v]);
+            }
+        mb = fmaxf(mb, xor_lanes(mb, 16));
+        mb = fmaxf(mb, xor_lanes(mb, 32));
+        const float mn = fmaxf(m_run, mb);
+        // e^x as the hardware 2^(x log2 e) (v_exp_f32; the blocked form's
+        // rounding of p to f16 dominates its error)
+        const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f((m_run - mn) * 1.4426950408889634f);
+        float ps = 0.0f;
+        half4_t pf[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float p = sc[kt][v] == -INFINITY ? 0.0f
+                                                       : __builtin_amdgcn_exp2f((sc[kt][v] - mn) * 1.4426950408889634f);
+                ps = ps + p;
+                pf[kt][v] = (_Float16)p;
+            }
+        ps = ps + xor_lanes(ps, 16);
+        ps = ps + xor_lanes(ps, 32);
+        l_run = __builtin_fmaf(l_run, alpha, ps);
+        m_run = mn;
+        // O^T += V^T P^T
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            o[dt] = o[dt] * alpha;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++) {
+                const uint2 va = *(const uint2 *)(v_lds + (16 * dt + r16) * VS + 16 * kt + 4 * g4);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, va), pf[kt], o[dt], 0, 0,
+                                                              0);
+            }
+        }
+    };
+    load_blk(0, ka_, va_);
+    load_blk(1, kb_, vb_);
+    for (uint32_t b = 0; b < nblk; b += 2) {
+        block(b, ka_, va_);
+        if (b + 1 < nblk) block(b + 1, kb_, vb_);
+    }
+    if (!rok) return;
+    const size_t base = ((size_t)row * a.heads + h) * a.hd;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const uint32_t d = 16u * dt + 4u * g4 + v;
+            if (d >= a.hd) continue;
+            const float val = o[dt][v] / l_run;
+            if (a.f16_out) ((uint16_t *)a.out)[base + d] = f32_to_f16(val);
+            else ((float *)a.out)[base + d] = val;
+        }
+}
+
 // m rows of the qkv projection (an f16 GEMM output in the fused QKV store's
 // device column order: a 16-column tile holds depths 8q..8q+7 and
 // half+8q..half+8q+7 of one head, each RoPE pair in lanes c, c ^ 8) to the
@@ -863,6 +1037,8 @@ size_t attn_partial_floats(size_t rows, size_t last_len, size_t heads, size_t hd
     return std::max<size_t>(rows, 1) * attn_splits(last_len) * heads * (hd + 2);
 }
 
+bool attn_rows_blocked(size_t rows) { return rows >= AP_MIN_ROWS; }
+
 hipError_t launch_attention(const AttnArgs &a0, void *out, bool f16_out, hipStream_t s) {
     AttnArgs a = a0;
     if (a.rows == 0) a.rows = 1;
@@ -872,6 +1048,17 @@ hipError_t launch_attention(const AttnArgs &a0, void *out, bool f16_out, hipStre
     if (last * a.ld * 2 >= ((size_t)1 << 31)) return hipErrorInvalidValue;
     a.nsplit = (uint32_t)attn_splits(last);
     a.hchunks = (a.group + AT_HC - 1) / AT_HC;
+    if (attn_rows_blocked(a.rows)) {
+        // the matrix-core form: no partials, one launch
+        if ((size_t)a.rows * a.heads * a.hd * 2 >= ((size_t)1 << 31)) return hipErrorInvalidValue;
+        a.out = out;
+        a.f16_out = f16_out ? 1u : 0u;
+        const dim3 grid(((a.rows + AP_BR - 1) / AP_BR) * (a.heads / a.group) * a.hchunks);
+        if (a.hd <= 64) hipLaunchKernelGGL(attn_rows_mfma<64>, grid, dim3(AP_T), 0, s, a);
+        else if (a.hd <= 128) hipLaunchKernelGGL(attn_rows_mfma<128>, grid, dim3(AP_T), 0, s, a);
+        else hipLaunchKernelGGL(attn_rows_mfma<256>, grid, dim3(AP_T), 0, s, a);
+        return hipGetLastError();
+    }
     const dim3 grid(a.nsplit, (a.heads / a.group) * a.hchunks, a.rows);
     if (a.hd <= 64) hipLaunchKernelGGL(attn_split<8>, grid, dim3(AT_T), 0, s, a);
     else if (a.hd <= 128) hipLaunchKernelGGL(attn_split<16>, grid, dim3(AT_T), 0, s, a);

@@ -149,7 +149,13 @@ struct AttnArgs {
     uint32_t len, ld, hd, heads, group;  // len: row 0's keys; group = heads / kv_heads
     uint32_t nsplit, hchunks;            // set by launch_attention (nsplit: the last row's)
     uint32_t rows;                       // 0 is taken as 1
+    void *out;                           // set by launch_attention (the blocked form)
+    uint32_t f16_out;                    // set by launch_attention (the blocked form)
 };
+// Blocks of this many rows run the matrix-core causal attention (one launch,
+// no partials: po / pml unused); fewer rows run the split pass and merge,
+// each row the same bits as a one-row call.
+bool attn_rows_blocked(size_t rows);
 size_t attn_splits(size_t len);
 // Partial-sum bytes (po, then pml) launch_attention needs for `rows` rows whose
 // last attends to `last_len` keys.
