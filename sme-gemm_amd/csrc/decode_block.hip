@@ -826,16 +826,23 @@ __global__ void __launch_bounds__(AP_T) attn_rows_mfma(AttnArgs a) {
                                                                 __builtin_bit_cast(half8_t, qf[kk]), sc[kt], 0, 0, 0);
             }
         }
-        // causal mask, the block's row max and the running rescale
+        // causal mask (only in the blocks that reach past the first row's
+        // prefix, or for rows past the block), the block's row max and the
+        // running rescale
         float mb = -INFINITY;
+        if ((b + 1) * AP_KB > a.len + p0 || pend - p0 < (uint32_t)AP_BR) {
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const uint32_t key = b * AP_KB + 16u * kt + 4u * g4 + v;
+                    if (!rok || key >= lim) sc[kt][v] = -INFINITY;
+                }
+        }
 #pragma unroll
         for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const uint32_t key = b * AP_KB + 16u * kt + 4u * g4 + v;
-                if (!rok || key >= lim) sc[kt][v] = -INFINITY;
-                mb = fmaxf(mb, sc[kt][v]);
-            }
+            for (int v = 0; v < 4; v++) mb = fmaxf(mb, sc[kt][v]);
         mb = fmaxf(mb, xor_lanes(mb, 16));
         mb = fmaxf(mb, xor_lanes(mb, 32));
         const float mn = fmaxf(m_run, mb);
