@@ -547,7 +547,9 @@ def test_decode_parts_refuse_bad_calls(smg, orc):
 
 @pytest.mark.parametrize("heads,kv_heads,hd,start,rows", [(8, 2, 64, 0, 3), (8, 2, 64, 100, 40), (6, 6, 64, 5, 17),
                                                           (32, 8, 128, 4096, 80), (4, 1, 128, 63, 66),
-                                                          (6, 6, 64, 10, 31), (6, 6, 64, 10, 32)])
+                                                          (6, 6, 64, 10, 31), (6, 6, 64, 10, 32),
+                                                          (2, 2, 256, 10, 40), (16, 2, 64, 30, 48),
+                                                          (8, 8, 16, 0, 33)])
 def test_attention_causal_rows_match_one_row(smg, orc, heads, kv_heads, hd, start, rows):
     """attention_kv_causal_f16 (kv_attention.rs:140-240): query row i attends
     to keys 0 .. start + i. As the reference's kv_causal_rows_match_one_row
