@@ -846,17 +846,19 @@ __global__ void __launch_bounds__(AP_T) attn_rows_mfma(AttnArgs a) {
         mb = fmaxf(mb, xor_lanes(mb, 16));
         mb = fmaxf(mb, xor_lanes(mb, 32));
         const float mn = fmaxf(m_run, mb);
-        // e^x as the hardware 2^(x log2 e) (v_exp_f32; the blocked form's
-        // rounding of p to f16 dominates its error)
-        const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f((m_run - mn) * 1.4426950408889634f);
+        // e^(x - mn) as the hardware 2^(x log2 e - mn log2 e) (v_exp_f32;
+        // the blocked form's rounding of p to f16 dominates its error); a row
+        // with no key yet keeps p = 0 (2^-inf)
+        constexpr float LOG2E = 1.4426950408889634f;
+        const float nb2 = mn == -INFINITY ? 0.0f : -mn * LOG2E;
+        const float alpha = m_run == mn ? 1.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, LOG2E, nb2));
         float ps = 0.0f;
         half4_t pf[4];
 #pragma unroll
         for (int kt = 0; kt < 4; kt++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                const float p = sc[kt][v] == -INFINITY ? 0.0f
-                                                       : __builtin_amdgcn_exp2f((sc[kt][v] - mn) * 1.4426950408889634f);
+                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kt][v], LOG2E, nb2));
                 ps = ps + p;
                 pf[kt][v] = (_Float16)p;
             }
@@ -864,10 +866,11 @@ __global__ void __launch_bounds__(AP_T) attn_rows_mfma(AttnArgs a) {
         ps = ps + xor_lanes(ps, 32);
         l_run = __builtin_fmaf(l_run, alpha, ps);
         m_run = mn;
-        // O^T += V^T P^T
+        // O^T += V^T P^T (the rescale only when some row's max moved)
+        const bool moved = __builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0;
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) {
-            o[dt] = o[dt] * alpha;
+            if (moved) o[dt] = o[dt] * alpha;
 #pragma unroll
             for (int kt = 0; kt < 4; kt++) {
                 const uint2 va = *(const uint2 *)(v_lds + (16 * dt + r16) * VS + 16 * kt + 4 * g4);
