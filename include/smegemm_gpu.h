@@ -374,9 +374,13 @@ int smg_attention_kv_f16_dev(const float *q, const uint16_t *k, const uint16_t *
                              void *stream);
 /* attention_kv_causal_f16 (kv_attention.rs:140-240) on device arrays: q f32
  * [rows][heads*head_dim], k / v f16 [start + rows][kv_heads*head_dim]; query
- * row i attends to keys 0 .. start + i, each row as attention_kv_f16 over its
- * prefix (the portable path's one_row per row), into out f32
- * [rows][heads*head_dim]. Replaces attn_kv_causal_f16 / _sme_f16 (src/ffi.rs). */
+ * row i attends to keys 0 .. start + i, into out f32 [rows][heads*head_dim].
+ * Below 32 rows each row is attention_kv_f16 over its prefix bit for bit (the
+ * portable path's one_row per row); from 32 rows the call runs the blocked
+ * arithmetic of the reference's attn_kv_causal_sme_f16 (probabilities rounded
+ * to f16, sums in another order: within 1e-3 of the one-row call on the
+ * reference's test data), as kv_attention.rs:198-201 dispatches. Replaces
+ * attn_kv_causal_f16 / _sme_f16 (src/ffi.rs). */
 int smg_attention_kv_causal_f16_dev(const float *q, const uint16_t *k, const uint16_t *v, size_t start,
                                     size_t rows, size_t heads, size_t kv_heads, size_t head_dim, float scale,
                                     float *out, void *stream);
