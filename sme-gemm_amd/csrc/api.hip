@@ -1093,9 +1093,17 @@ int mlp_step(smg_mlp *m, const uint16_t *x16, const float *nx, const float *nw, 
             ea.cls[0] = ep_class(EP_OP_ACT);
         }
         uint16_t *dst = m->gated ? spare : sc.hid;
-        if ((e = run_q4_dev(m->up->device, m->up->d, rows, dst, x16, ea, false, s)) != hipSuccess) return q4_fail("up projection", e);
-        if (m->gated && (e = launch_glu(dst, rows, m->hidden, m->act, 1, sc.hid, s)) != hipSuccess)
-            return fail(SMG_EHIP, "glu", e);
+        const WDev &uw = m->up->d;
+        if (m->gated && q4r_supported(uw, rows, 1, (long)uw.k, x16, false) && !q4_gemv_rows(uw, rows, true) &&
+            q4r_split_bytes(uw, rows) == 0) {  // one gemm_q4r pass, glu at its store
+            if ((e = launch_q4r_glu(uw, rows, sc.hid, m->hidden, x16, m->act, s)) != hipSuccess)
+                return fail(SMG_EHIP, "gate/up projection", e);
+        } else {
+            if ((e = run_q4_dev(m->up->device, uw, rows, dst, x16, ea, false, s)) != hipSuccess)
+                return q4_fail("up projection", e);
+            if (m->gated && (e = launch_glu(dst, rows, m->hidden, m->act, 1, sc.hid, s)) != hipSuccess)
+                return fail(SMG_EHIP, "glu", e);
+        }
     }
     if (rows <= 8) {
         BlkArgs r = {};

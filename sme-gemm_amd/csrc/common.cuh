@@ -33,6 +33,11 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
 __device__ __forceinline__ uint16_t f32_to_f16(float x) {
     return __builtin_bit_cast(uint16_t, (_Float16)x);
 }
+// GatedLinear's activation on the gate (linear.rs:815-822), in f32.
+__device__ __forceinline__ float glu_act(uint32_t act, float g) {
+    if (act == EP_ACT_GELU) return 0.5f * g * (1.0f + tanhf(0.7978846f * (g + 0.044715f * g * g * g)));
+    return g / (1.0f + expf(-g));
+}
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return __uint_as_float((uint32_t)h << 16);
 }

@@ -124,12 +124,6 @@ struct SrcNormRow {
     }
 };
 
-// GatedLinear's activation on the gate (linear.rs:815-822), in f32.
-__device__ __forceinline__ float glu_act(uint32_t act, float g) {
-    if (act == EP_ACT_GELU) return 0.5f * g * (1.0f + tanhf(0.7978846f * (g + 0.044715f * g * g * g)));
-    return g / (1.0f + expf(-g));
-}
-
 // Loads a single-row tile store reads (the residual it adds to, the RoPE
 // angles), issued ahead of the next item's weight loads so the store does not
 // wait for those.

@@ -62,10 +62,12 @@ struct RArgs {
     // part[s][row][col] (row stride part_ld floats); q4r_reduce finishes them
     float *part;
     uint32_t nsplit, part_ld;
-    // the compiled store's operands (EPV 2, 3: EpPick's a, b, act, alpha)
+    // the compiled store's operands (EPV 2, 3: EpPick's a, b, act, alpha;
+    // EPV 4: act, and nh the gated store's output width)
     const uint16_t *col_a, *col_b;
     uint32_t act;
     float act_alpha;
+    uint32_t nh;
 };
 
 // LDS DMA: each lane's 16 (4) bytes from sbase + voff land at M0 + 16 (4) *
@@ -379,10 +381,12 @@ __device__ __forceinline__ void mma_step(const Half &cur, const Half &nxt, float
 
 // EPV: the store's op-graph, compiled for the common shapes (pick_ep): 0 any
 // graph (the interpreted store), 1 none, 2 [add_col] + act, 3 [mul_col,
-// add_col] + act. SPLIT kernels store partials only (EPV 0).
+// add_col] + act; 4 the gated store (ep_store_glu8, f16). SPLIT kernels store
+// partials only (EPV 0).
 template <bool AFFINE, bool SPLIT, int EPV = 0, bool BF16 = false>
 __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
     static_assert(!SPLIT || EPV == 0, "a split kernel's store is q4r_reduce's");
+    static_assert(EPV != 4 || !BF16, "the gated store is f16");
     __shared__ __align__(16) uint8_t ring[NSTAGE * STAGE_BYTES];
     __shared__ __align__(16) float epv[EPV == 0 ? EP_FUSED * (RBN + RBM) : 4];
 
@@ -498,7 +502,7 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
         // the op-graph's vectors first: their global loads overlap the exchange
         if constexpr (!SPLIT && EPV == 0) ep_load_vectors<BF16, RBM, RBN, RNT>(g.st, ep, colv, rowv, row0, col0);
         EpCols cv;
-        if constexpr (EPV >= 2) ep_cols_load<EPV>(g.col_a, g.col_b, col0 + (t % (RBN / 8)) * 8, g.n, cv);
+        if constexpr (EPV == 2 || EPV == 3) ep_cols_load<EPV>(g.col_a, g.col_b, col0 + (t % (RBN / 8)) * 8, g.n, cv);
 
         // The pair's partial tiles: each wave hands the other the half of its
         // f32 tile that the other finishes (wave w keeps row tiles 0-3, wave
@@ -582,6 +586,9 @@ __global__ void __launch_bounds__(RNT) gemm_q4r(RArgs g, EpArgs ep) {
         if constexpr (EPV == 0)
             ep_store_rows<BF16, RBM, RBN, RBM * (RBN / 8) / RNT>(g.st, ep, colv, rowv, stg, CS, t / (RBN / 8),
                                                                  RNT / (RBN / 8), (t % (RBN / 8)) * 8, row0, col0);
+        else if constexpr (EPV == 4)  // thread t: gate group t % 16, rows t / 16 + 32 j
+            ep_store_glu8<RBM * (RBN / 16) / RNT>(g.st, g.act, g.nh, stg, CS, t / (RBN / 16), RNT / (RBN / 16),
+                                                  (t % (RBN / 16)) * 16, row0, col0);
         else
             ep_store_rows_c<BF16, RBM * (RBN / 8) / RNT, EPV>(g.st, g.act, g.act_alpha, cv, stg, CS, t / (RBN / 8),
                                                               RNT / (RBN / 8), (t % (RBN / 8)) * 8, row0, col0);
@@ -751,6 +758,39 @@ hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long 
         hipLaunchKernelGGL(q4r_reduce<true>, dim3(rtiles), dim3(QR_NT), 0, s, g, ep);
     else
         hipLaunchKernelGGL(q4r_reduce<false>, dim3(rtiles), dim3(QR_NT), 0, s, g, ep);
+    return hipGetLastError();
+}
+
+// The gate/up GEMM of a GatedLinear with glu at the store: w holds 8 gate then
+// 8 up columns a group (n = 16 * ceil(nh / 8)); dst [m][nh] f16 gets
+// glu(gate) * up, the values glu_rows (tile8) computes from the f16 GEMM
+// output. One pass, no split: the caller takes it when q4r_nsplit is 1.
+hipError_t launch_q4r_glu(const WDev &w, size_t m, uint16_t *dst, size_t nh, const uint16_t *lhs, uint32_t act,
+                          hipStream_t s) {
+    if (w.n != 16 * ((nh + 7) / 8)) return hipErrorInvalidValue;
+    RArgs g = {};
+    g.lhs = lhs;
+    g.codes = w.codes;
+    g.sc = w.scales;
+    g.mn = w.mins;
+    g.st = {dst, (long)nh, 1, (uint32_t)m, (uint32_t)w.n, 0.0f, 0u};
+    g.beta = 1.0f;
+    g.lhs_rs = (long)w.k;
+    g.m = (uint32_t)m;
+    g.n = (uint32_t)w.n;
+    g.k = (uint32_t)w.k;
+    g.n_pad = (uint32_t)w.n_pad;
+    g.block_shift = (uint32_t)__builtin_ctzll(w.block);
+    g.nchunks = (uint32_t)w.nchunks;
+    g.sc_rows = (uint32_t)w.sc_rows;
+    g.act = act;
+    g.nh = (uint32_t)nh;
+    const uint32_t tiles = (uint32_t)(((m + RBM - 1) / RBM) * ((w.n + RBN - 1) / RBN));
+    const EpArgs ep = {};
+    if (w.mins)
+        hipLaunchKernelGGL((gemm_q4r<true, false, 4, false>), dim3(tiles), dim3(RNT), 0, s, g, ep);
+    else
+        hipLaunchKernelGGL((gemm_q4r<false, false, 4, false>), dim3(tiles), dim3(RNT), 0, s, g, ep);
     return hipGetLastError();
 }
 

@@ -316,4 +316,44 @@ __device__ __forceinline__ void ep_store_rows_c(const StoreArgs &g, uint32_t act
     }
 }
 
+// The gated store (f16 only): the tile's columns come in groups of 8 gate and
+// 8 up values (the device layout of a GatedLinear's gate/up weights), and the
+// store writes glu(gate) * up for each pair -- glu_rows' tile8 arithmetic on
+// the same rounded f16 values -- to column (col0 + cu) / 2 + e of g.dst, which
+// holds hidden = nh columns. cu: the gate group's column in the tile (a
+// multiple of 16).
+template <int R>
+__device__ __forceinline__ void ep_store_glu8(const StoreArgs &g, uint32_t act, uint32_t nh, const uint16_t *tile,
+                                              int cs, int rl0, int rstep, int cu, uint32_t row0, uint32_t col0) {
+    const uint32_t col = (col0 + cu) / 2;
+    if (col >= nh) return;
+    const uint32_t ne = nh - col < 8 ? nh - col : 8;
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        const uint32_t row = row0 + rl0 + rstep * j;
+        if (row >= g.m) continue;
+        const uint16_t *tr = tile + (rl0 + rstep * j) * cs + cu;
+        const uint4 gq = *(const uint4 *)tr, uq = *(const uint4 *)(tr + 8);
+        const uint32_t gw[4] = {gq.x, gq.y, gq.z, gq.w}, uw[4] = {uq.x, uq.y, uq.z, uq.w};
+        uint32_t w4[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            uint32_t h2 = 0;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const float gv = f16_to_f32((uint16_t)(gw[e] >> (16 * h)));
+                const float uv = f16_to_f32((uint16_t)(uw[e] >> (16 * h)));
+                h2 |= (uint32_t)f32_to_f16(glu_act(act, gv) * uv) << (16 * h);
+            }
+            w4[e] = h2;
+        }
+        uint16_t *dp = g.dst + (size_t)row * g.dst_rs + col;
+        if (ne == 8 && ((uintptr_t)dp & 15) == 0) {
+            *(uint4 *)dp = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+            continue;
+        }
+        for (uint32_t e = 0; e < ne; e++) dp[e] = (uint16_t)(w4[e / 2] >> (16 * (e % 2)));
+    }
+}
+
 }  // namespace smg

@@ -337,10 +337,13 @@ def _down_moved(orc, inp, hid, m, d, ffn):
 
 @pytest.mark.parametrize("gated,gelu,m,d,ffn", [(True, False, 1, 4096, 14336), (True, False, 3, 256, 320),
                                                 (True, True, 1, 256, 100), (False, True, 2, 256, 320),
-                                                (False, False, 1, 512, 1024), (True, False, 12, 256, 320)])
+                                                (False, False, 1, 512, 1024), (True, False, 12, 256, 320),
+                                                (True, False, 640, 256, 3204), (True, True, 520, 256, 3300)])
 def test_mlp_accumulate(smg, orc, gated, gelu, m, d, ffn):
     """Mlp::gated / Mlp::new accumulate (src/mlp.rs:113-149): the up GEMV with
-    its activation (or glu) at the store, then down adding into y."""
+    its activation (or glu) at the store, then down adding into y. The 640- and
+    520-row cases fill the device with one GEMM pass, which applies glu at its
+    store (hidden widths that are not whole groups of 8 included)."""
     import torch
     inp = WL.block_inputs(d, 2, 1, 64, ffn, 1, seed=ffn + m)
     gate = smg.Gate.Gelu if gelu else smg.Gate.Silu
