@@ -700,6 +700,21 @@ hipError_t run_q4_dev(int device, const WDev &w, size_t m, uint16_t *dst, const 
     return run_q4(w, m, dst, lhs, ea, bf16, s, part, sb);
 }
 
+// y [m][w.n] f32 += the f16 projection of lhs (the residual add after an out
+// or down projection): in the split-K reduce where run_q4 would split, else
+// the f16 result into tmp16, then add_f16_values.
+hipError_t q4_add_dev(int device, const WDev &w, size_t m, const uint16_t *lhs, uint16_t *tmp16, float *y,
+                      hipStream_t s) {
+    const size_t sb = q4_split_bytes(w, m, lhs, false);
+    if (sb) {
+        void *part = split_pool().get(device, s, sb);
+        if (!part) return hipErrorOutOfMemory;
+        return launch_q4r_resid(w, m, lhs, y, (float *)part, sb, s);
+    }
+    const hipError_t e = run_q4_dev(device, w, m, tmp16, lhs, EpArgs{}, false, s);
+    return e != hipSuccess ? e : launch_add_f16(tmp16, m * w.n, y, s);
+}
+
 // k == 0: every output is the epilogue applied to +0 (reference GEMM of an
 // empty sum); the GEMV and GEMM kernels handle it (zero chunks, zero steps).
 
@@ -1041,9 +1056,8 @@ int attn_rows(smg_attn *a, smg_kv_cache *c, const uint16_t *x16, float *y, size_
         if ((e = launch_blk_gemv(a->out->d, m, att16, r, BS_RESID, false, s)) != hipSuccess)
             return fail(SMG_EHIP, "out projection", e);
     } else {
-        if ((e = run_q4_dev(a->out->device, a->out->d, m, out16, att16, EpArgs{}, false, s)) != hipSuccess)
+        if ((e = q4_add_dev(a->out->device, a->out->d, m, att16, out16, y, s)) != hipSuccess)
             return q4_fail("out projection", e);
-        if ((e = launch_add_f16(out16, m * d_out, y, s)) != hipSuccess) return fail(SMG_EHIP, "residual add", e);
     }
     c->len = pos + m;
     return SMG_OK;
@@ -1112,9 +1126,8 @@ int mlp_step(smg_mlp *m, const uint16_t *x16, const float *nx, const float *nw, 
             return fail(SMG_EHIP, "down projection", e);
     } else {
         uint16_t *out16 = spare + rows * both;
-        if ((e = run_q4_dev(m->down->device, m->down->d, rows, out16, sc.hid, EpArgs{}, false, s)) != hipSuccess)
+        if ((e = q4_add_dev(m->down->device, m->down->d, rows, sc.hid, out16, y, s)) != hipSuccess)
             return q4_fail("down projection", e);
-        if ((e = launch_add_f16(out16, rows * d_out, y, s)) != hipSuccess) return fail(SMG_EHIP, "residual add", e);
     }
     return SMG_OK;
 }
@@ -1938,8 +1951,7 @@ int smg_q4_accumulate_dev(size_t m, const smg_weights *w, float *y, const uint16
     } else {
         DecodeScratch sc;
         if ((rc = decode_scratch(w->device, stream, 0, 0, 0, m * w->d.n, 0, &sc))) return rc;
-        e = run_q4_dev(w->device, w->d, m, sc.h16, x, EpArgs{}, false, s);
-        if (e == hipSuccess) e = launch_add_f16(sc.h16, m * w->d.n, y, s);
+        e = q4_add_dev(w->device, w->d, m, x, sc.h16, y, s);
     }
     return e == hipSuccess ? SMG_OK : q4_fail("smg_q4_accumulate_dev", e);
 }

@@ -62,6 +62,9 @@ struct RArgs {
     // part[s][row][col] (row stride part_ld floats); q4r_reduce finishes them
     float *part;
     uint32_t nsplit, part_ld;
+    // q4r_reduce with resid ([m][n] f32): resid += the rounded f16 result
+    // (the residual add), which is then not stored
+    float *resid;
     // the compiled store's operands (EPV 2, 3: EpPick's a, b, act, alpha;
     // EPV 4: act, and nh the gated store's output width)
     const uint16_t *col_a, *col_b;
@@ -645,6 +648,23 @@ __global__ void __launch_bounds__(QR_NT) q4r_reduce(RArgs g, EpArgs ep) {
         w4[2 + e] = (uint32_t)from_f32<BF16>(0.0f + g.beta * s1[2 * e]) |
                     ((uint32_t)from_f32<BF16>(0.0f + g.beta * s1[2 * e + 1]) << 16);
     }
+    if (g.resid) {  // f16 only (launch_q4r_resid)
+        const uint32_t row = row0 + rl, col = col0 + cl, ne = g.n - col < 8 ? g.n - col : 8;
+        float *yp = g.resid + (size_t)row * g.n + col;
+        if (ne == 8 && ((uintptr_t)yp & 15) == 0) {
+            float4_t y0 = *(const float4_t *)yp, y1 = *(const float4_t *)(yp + 4);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                y0[e] = y0[e] + f16_to_f32((uint16_t)(w4[e / 2] >> (16 * (e % 2))));
+                y1[e] = y1[e] + f16_to_f32((uint16_t)(w4[2 + e / 2] >> (16 * (e % 2))));
+            }
+            *(float4_t *)yp = y0;
+            *(float4_t *)(yp + 4) = y1;
+            return;
+        }
+        for (uint32_t e = 0; e < ne; e++) yp[e] = yp[e] + f16_to_f32((uint16_t)(w4[e / 2] >> (16 * (e % 2))));
+        return;
+    }
     ep_store8<BF16, QR_BM, QR_BN>(g.st, ep, colv, rowv, make_uint4(w4[0], w4[1], w4[2], w4[3]), rl, cl, row0,
                                    col0);
 }
@@ -694,9 +714,8 @@ size_t q4r_split_bytes(const WDev &w, size_t m) {
     return ns > 1 ? (size_t)ns * m * ((w.n + 7) / 8 * 8) * sizeof(float) : 0;
 }
 
-hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,
-                      const uint16_t *lhs, long lhs_rs, float beta, const EpArgs &ep, float *part,
-                      size_t part_bytes, bool bf16, hipStream_t s) {
+static RArgs q4r_args(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs, const uint16_t *lhs,
+                      long lhs_rs, float beta) {
     RArgs g = {};
     g.lhs = lhs;
     g.codes = w.codes;
@@ -712,6 +731,13 @@ hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long 
     g.block_shift = (uint32_t)__builtin_ctzll(w.block);
     g.nchunks = (uint32_t)w.nchunks;
     g.sc_rows = (uint32_t)w.sc_rows;
+    return g;
+}
+
+hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,
+                      const uint16_t *lhs, long lhs_rs, float beta, const EpArgs &ep, float *part,
+                      size_t part_bytes, bool bf16, hipStream_t s) {
+    RArgs g = q4r_args(w, m, dst, dst_cs, dst_rs, lhs, lhs_rs, beta);
     const uint32_t tiles = (uint32_t)(((m + RBM - 1) / RBM) * ((w.n + RBN - 1) / RBN));
     const size_t slice_bytes = m * ((w.n + 7) / 8 * 8) * sizeof(float);
     const uint32_t ns = part ? (uint32_t)std::min<size_t>(q4r_nsplit(w, m), part_bytes / slice_bytes) : 1;
@@ -768,21 +794,7 @@ hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long 
 hipError_t launch_q4r_glu(const WDev &w, size_t m, uint16_t *dst, size_t nh, const uint16_t *lhs, uint32_t act,
                           hipStream_t s) {
     if (w.n != 16 * ((nh + 7) / 8)) return hipErrorInvalidValue;
-    RArgs g = {};
-    g.lhs = lhs;
-    g.codes = w.codes;
-    g.sc = w.scales;
-    g.mn = w.mins;
-    g.st = {dst, (long)nh, 1, (uint32_t)m, (uint32_t)w.n, 0.0f, 0u};
-    g.beta = 1.0f;
-    g.lhs_rs = (long)w.k;
-    g.m = (uint32_t)m;
-    g.n = (uint32_t)w.n;
-    g.k = (uint32_t)w.k;
-    g.n_pad = (uint32_t)w.n_pad;
-    g.block_shift = (uint32_t)__builtin_ctzll(w.block);
-    g.nchunks = (uint32_t)w.nchunks;
-    g.sc_rows = (uint32_t)w.sc_rows;
+    RArgs g = q4r_args(w, m, dst, 1, (long)nh, lhs, (long)w.k, 1.0f);
     g.act = act;
     g.nh = (uint32_t)nh;
     const uint32_t tiles = (uint32_t)(((m + RBM - 1) / RBM) * ((w.n + RBN - 1) / RBN));
@@ -791,6 +803,32 @@ hipError_t launch_q4r_glu(const WDev &w, size_t m, uint16_t *dst, size_t nh, con
         hipLaunchKernelGGL((gemm_q4r<true, false, 4, false>), dim3(tiles), dim3(RNT), 0, s, g, ep);
     else
         hipLaunchKernelGGL((gemm_q4r<false, false, 4, false>), dim3(tiles), dim3(RNT), 0, s, g, ep);
+    return hipGetLastError();
+}
+
+// y [m][n] f32 += the f16 product of lhs [m][k] f16 and w, rounded as
+// launch_q4r stores it: the split-K GEMM, with the residual add in its reduce.
+// part: q4r_split_bytes(w, m) bytes, which must be nonzero (a split call).
+hipError_t launch_q4r_resid(const WDev &w, size_t m, const uint16_t *lhs, float *y, float *part, size_t part_bytes,
+                            hipStream_t s) {
+    const size_t slice_bytes = m * ((w.n + 7) / 8 * 8) * sizeof(float);
+    const uint32_t ns = part ? (uint32_t)std::min<size_t>(q4r_nsplit(w, m), part_bytes / slice_bytes) : 1;
+    if (ns <= 1) return hipErrorInvalidValue;
+    RArgs g = q4r_args(w, m, nullptr, 1, (long)w.n, lhs, (long)w.k, 1.0f);
+    g.part = part;
+    g.nsplit = ns;
+    g.part_ld = (uint32_t)((w.n + 7) / 8 * 8);
+    g.resid = y;
+    const uint32_t tiles = (uint32_t)(((m + RBM - 1) / RBM) * ((w.n + RBN - 1) / RBN));
+    const EpArgs ep = {};
+    if (w.mins)
+        hipLaunchKernelGGL((gemm_q4r<true, true>), dim3(tiles * ns), dim3(RNT), 0, s, g, ep);
+    else
+        hipLaunchKernelGGL((gemm_q4r<false, true>), dim3(tiles * ns), dim3(RNT), 0, s, g, ep);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t rtiles = (uint32_t)(((m + QR_BM - 1) / QR_BM) * ((w.n + QR_BN - 1) / QR_BN));
+    hipLaunchKernelGGL(q4r_reduce<false>, dim3(rtiles), dim3(QR_NT), 0, s, g, ep);
     return hipGetLastError();
 }
 

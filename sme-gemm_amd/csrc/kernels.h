@@ -104,6 +104,11 @@ hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long 
 // reduce), so callers take it where q4r_split_bytes(w, m) is 0.
 hipError_t launch_q4r_glu(const WDev &w, size_t m, uint16_t *dst, size_t nh, const uint16_t *lhs, uint32_t act,
                           hipStream_t s);
+// y [m][n] f32 += the f16-rounded product of lhs and w (launch_q4r's store
+// value, then the residual add), the add done in the split-K reduce: part
+// holds q4r_split_bytes(w, m) bytes, which must be nonzero.
+hipError_t launch_q4r_resid(const WDev &w, size_t m, const uint16_t *lhs, float *y, float *part, size_t part_bytes,
+                            hipStream_t s);
 
 // Compute units of the current device (cached per device).
 int device_cus();

@@ -273,7 +273,8 @@ def test_kv_cache_api(smg, orc):
 
 # ---- projections ----------------------------------------------------------------------
 
-@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (3, 200, 96), (8, 512, 1024), (12, 256, 512)])
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (3, 200, 96), (8, 512, 1024), (12, 256, 512),
+                                   (64, 4100, 4096), (200, 1000, 512)])
 def test_linear_accumulate(smg, orc, m, n, k):
     """Linear::accumulate (src/linear.rs:425-432): y += f32(f16(x @ W))."""
     import torch
@@ -285,6 +286,24 @@ def test_linear_accumulate(smg, orc, m, n, k):
     torch.cuda.synchronize()
     out = orc.f16_to_f32(orc.matmul_q4_ep(a, quants, scales, None, m, n, k, 32))
     _check_term(y.cpu().numpy(), y0, out, f16_tol(k))
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 4100, 4096), (33, 4096, 4096), (512, 4096, 4096), (200, 1000, 512)])
+def test_linear_accumulate_adds_forward(smg, m, n, k):
+    """Linear::accumulate (src/linear.rs:425-432) is y + f32(forward's f16
+    output), bit for bit: the split-K GEMM adds into y in its reduce, from the
+    value the split GEMM of forward stores."""
+    import torch
+    a, quants, scales, _ = WL.q4_inputs(m, n, k, seed=3 * m + n)
+    lin = smg.Linear(smg.Q4Weights(quants, scales, n, k))
+    y0 = np.random.default_rng(2).standard_normal(m * n).astype(np.float32)
+    y = _f32(y0)
+    out = torch.empty(m * n, dtype=torch.float16, device="cuda")
+    lin.forward(_h16(a), out, m)
+    lin.accumulate(_h16(a), y, m)
+    torch.cuda.synchronize()
+    want = y0 + out.float().cpu().numpy()
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
 # One row on the all-steps-in-flight decode GEMV: one or two tiles a compute
