@@ -793,16 +793,12 @@ hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long 
 // output. One pass, no split: the caller takes it when q4r_nsplit is 1.
 hipError_t launch_q4r_glu(const WDev &w, size_t m, uint16_t *dst, size_t nh, const uint16_t *lhs, uint32_t act,
                           hipStream_t s) {
-    if (w.n != 16 * ((nh + 7) / 8)) return hipErrorInvalidValue;
+    if (w.n != 16 * ((nh + 7) / 8) || w.mins) return hipErrorInvalidValue;  // a gated MLP's weights are Q4_0
     RArgs g = q4r_args(w, m, dst, 1, (long)nh, lhs, (long)w.k, 1.0f);
     g.act = act;
     g.nh = (uint32_t)nh;
     const uint32_t tiles = (uint32_t)(((m + RBM - 1) / RBM) * ((w.n + RBN - 1) / RBN));
-    const EpArgs ep = {};
-    if (w.mins)
-        hipLaunchKernelGGL((gemm_q4r<true, false, 4, false>), dim3(tiles), dim3(RNT), 0, s, g, ep);
-    else
-        hipLaunchKernelGGL((gemm_q4r<false, false, 4, false>), dim3(tiles), dim3(RNT), 0, s, g, ep);
+    hipLaunchKernelGGL((gemm_q4r<false, false, 4, false>), dim3(tiles), dim3(RNT), 0, s, g, EpArgs{});
     return hipGetLastError();
 }
 

@@ -97,8 +97,8 @@ size_t q4r_split_bytes(const WDev &w, size_t m);
 hipError_t launch_q4r(const WDev &w, size_t m, uint16_t *dst, long dst_cs, long dst_rs,
                       const uint16_t *lhs, long lhs_rs, float beta, const EpArgs &ep, float *part,
                       size_t part_bytes, bool bf16, hipStream_t s);
-// The gate/up projection of a GatedLinear (w: 8 gate then 8 up columns a
-// group, n = 16 * ceil(nh / 8)) with glu at the store: dst [m][nh] f16 holds
+// The gate/up projection of a GatedLinear (w: Q4_0, 8 gate then 8 up columns
+// a group, n = 16 * ceil(nh / 8)) with glu at the store: dst [m][nh] f16 holds
 // glu(gate) * up from the rounded f16 projections, as launch_glu (tile8) gives
 // from the GEMM's output. One kernel over all of K (split K has no gated
 // reduce), so callers take it where q4r_split_bytes(w, m) is 0.
