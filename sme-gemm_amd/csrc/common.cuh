@@ -30,7 +30,12 @@ typedef int int4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
+// The empty asm makes x an opaque f32 register value: without it hipcc folds
+// a producing multiply or FMA into the conversion (v_fma_mixlo_f16, one
+// rounding of the exact result to f16), where the reference rounds the f32
+// result and then that to f16.
 __device__ __forceinline__ uint16_t f32_to_f16(float x) {
+    __asm__("" : "+v"(x));
     return __builtin_bit_cast(uint16_t, (_Float16)x);
 }
 // GatedLinear's activation on the gate (linear.rs:815-822), in f32.
